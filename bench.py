@@ -1,0 +1,256 @@
+"""Benchmark of the MI355X speculative-verify hot path (one GPU).
+
+Default workload (BASELINE cfg3): one depth-3 verify step (B=1, 4 rows) of the
+27B-shaped 4-bit dense decoder at 4096-token context, random init, synthetic
+inputs resident in HBM: embedding -> 64 layers (fused norm+q|k|v, RoPE+KV write,
+ragged GQA attention, o_proj+residual, fused norm+gate/up+SwiGLU,
+down_proj+residual) -> norm+lm_head (fp32 logits) -> exact accept/reject.
+
+Prints one JSON line. ``value`` = verify rows/s = B*(K+1)/t_step. The
+``roofline`` object times the step's dominant kernel (the fused norm+gate/up
+quantized matmul, one launch per layer's weights, so no launch re-reads
+cached weights) with HIP events on the stream it runs on; ``cpu_baseline``
+times the float64 NumPy oracle on a bounded sample of the same step.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import subprocess
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+
+def _gate_up_bytes(M: int, N: int, K: int, gs: int) -> int:
+    w = N * K // 2
+    sb = 2 * N * (K // gs) * 2
+    return 2 * (w + sb) + M * K * 2 + K * 2 + M * N * 2
+
+
+def _qmv_bytes(M: int, N: int, K: int, gs: int) -> int:
+    return N * K // 2 + 2 * N * (K // gs) * 2 + M * K * 2 + M * N * 2
+
+
+def roofline_gate_up(model, M: int, reps: int = 5) -> dict:
+    """Average duration of the fused norm+gate/up launch over every layer's weights."""
+    import torch
+
+    from mtplx_amd import _lib
+
+    c = model.cfg
+    dev = model.device
+    st = _lib.stream_handle(dev)
+    x = torch.randn((M, c.hidden), device=dev).to(torch.bfloat16)
+    y = torch.empty((M, c.ffn), dtype=torch.bfloat16, device=dev)
+    eps = ctypes.c_float(c.rms_eps)
+
+    def launch(L):
+        _lib.call("mtp_qmv_affine4_rmsnorm_dual", x.data_ptr(), L.post_norm.data_ptr(), eps, L.gate.weight.data_ptr(),
+                  L.gate.scales.data_ptr(), L.gate.biases.data_ptr(), L.up.weight.data_ptr(), L.up.scales.data_ptr(),
+                  L.up.biases.data_ptr(), y.data_ptr(), M, c.ffn, c.hidden, c.group_size, None, 0, st)
+
+    for L in model.layers:
+        launch(L)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    n = 0
+    for _ in range(reps):
+        for L in model.layers:
+            launch(L)
+            n += 1
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / n
+    byts = _gate_up_bytes(M, c.ffn, c.hidden, c.group_size)
+    gbs = byts / us / 1e3
+    return {"bound": "hbm", "kernel": "qmm4_kernel<R=4,X_RMSNORM,E_DUAL_SWIGLU> (mtp_qmv_affine4_rmsnorm_dual)",
+            "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None, "algorithmic_bytes_per_launch": byts, "avg_launch_us": round(us, 3),
+            "launches_timed": n}
+
+
+def roofline_qmv_cfg1(reps: int = 64, nsets: int = 8) -> dict:
+    """BASELINE cfg1 qmv (x [4,5120] . W [17408,5120] 4-bit g64), 8 rotating weight
+    sets (400 MB > 256 MB MALL) so every launch streams from HBM."""
+    import torch
+
+    from mtplx_amd import _lib
+    from mtplx_amd.quant import QuantizedLinear
+
+    M, N, K, gs = 4, 17408, 5120, 64
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    sets = [QuantizedLinear.random(N, K, gs, generator=gen) for _ in range(nsets)]
+    x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    st = _lib.stream_handle()
+
+    def launch(q):
+        _lib.call("mtp_qmv_affine4", x.data_ptr(), q.weight.data_ptr(), q.scales.data_ptr(), q.biases.data_ptr(),
+                  y.data_ptr(), M, N, K, gs, None, 0, st)
+
+    for q in sets:
+        launch(q)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(reps):
+        launch(sets[i % nsets])
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / reps
+    byts = _qmv_bytes(M, N, K, gs)
+    gbs = byts / us / 1e3
+    return {"kernel": "qmm4_kernel<R=4,X_PLAIN,E_STORE> (mtp_qmv_affine4)", "achieved": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": byts}
+
+
+def cpu_baseline(layers: int, timeout_s: int = 300) -> dict | None:
+    """Float64 NumPy oracle on a bounded sample, single thread, in a child process."""
+    env = dict(os.environ, OMP_NUM_THREADS="1", OPENBLAS_NUM_THREADS="1", MKL_NUM_THREADS="1")
+    cmd = [sys.executable, "-c", f"import sys; sys.path.insert(0, {ROOT!r}); import bench; bench._cpu_child({layers})"]
+    try:
+        out = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        return None
+    for line in out.stdout.splitlines()[::-1]:
+        if line.startswith("{"):
+            return json.loads(line)
+    sys.stderr.write(out.stderr[-2000:])
+    return None
+
+
+def _cpu_child(layers: int) -> None:
+    """One decoder layer + 1/16 of the lm_head + the sampler on the oracle,
+    extrapolated to the full depth-3 verify step of the 27B shape."""
+    import numpy as np
+
+    from oracle import attention as A
+    from oracle import sampler as S
+    from oracle.moe import silu
+    from oracle.qmv import make_affine4_weights, qmm_affine4
+
+    rng = np.random.default_rng(0)
+    M, H, F, Hq, Hkv, D, V, ctx = 4, 5120, 17408, 40, 8, 128, 151936, 4096
+    lay = {n: make_affine4_weights(rng, o, i) for n, o, i in
+           [("qkv", (Hq + 2 * Hkv) * D, H), ("o", H, Hq * D), ("g", F, H), ("u", F, H), ("d", H, F)]}
+    lm = make_affine4_weights(rng, V // 16, H)
+    k = rng.standard_normal((1, Hkv, ctx, D)).astype(np.float32)
+    v = rng.standard_normal((1, Hkv, ctx, D)).astype(np.float32)
+    h = rng.standard_normal((M, H))
+    t0 = time.perf_counter()
+    xn = h / np.sqrt((h ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    qkv = qmm_affine4(xn, *lay["qkv"], 64)
+    q = qkv[:, : Hq * D].reshape(M, Hq, D).transpose(1, 0, 2)[None]
+    att = A.ragged_gqa_attention(q, k, v, [ctx - M])
+    h = h + qmm_affine4(att[0].transpose(1, 0, 2).reshape(M, Hq * D), *lay["o"], 64)
+    xn = h / np.sqrt((h ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    a = silu(qmm_affine4(xn, *lay["g"], 64)) * qmm_affine4(xn, *lay["u"], 64)
+    h = h + qmm_affine4(a, *lay["d"], 64)
+    t_layer = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    qmm_affine4(xn, *lm, 64)
+    t_lm = (time.perf_counter() - t0) * 16
+    logits = rng.normal(0, 3, (7, V))
+    t0 = time.perf_counter()
+    S.spec_accept(logits[:4], logits[4:], np.array([1, 2, 3]), rng.random(4), S.SamplerConfig())
+    t_acc = time.perf_counter() - t0
+    t_step = layers * t_layer + t_lm + t_acc
+    print(json.dumps({"value": round(M / t_step, 4), "unit": "verify rows/s", "cores": 1, "kind": "port",
+                      "sample": f"float64 NumPy oracle, 1 thread: 1 of {layers} decoder layers "
+                                f"({t_layer:.2f} s) + 1/16 of lm_head ({t_lm / 16:.2f} s) + accept "
+                                f"({t_acc:.3f} s), extrapolated to the full step ({t_step:.1f} s)",
+                      "host_cpu_count": os.cpu_count()}))
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the hot path is single-GPU); --gpus {args.gpus} is not supported",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from mtplx_amd import _lib
+    from mtplx_amd.sampling import SamplerConfig
+    from mtplx_amd.verify_step import DENSE_27B, VerifyModel
+
+    _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    cfg = DENSE_27B
+    B, K = 1, 3
+    L = K + 1
+    model = VerifyModel(cfg, device=dev, seed=0)
+    model.allocate_cache(B, args.ctx)
+    gen = torch.Generator(device=dev).manual_seed(123)
+    tokens = torch.randint(0, cfg.vocab, (B, L), device=dev, dtype=torch.int32, generator=gen)
+    q_start = torch.full((B,), args.ctx - L, dtype=torch.int32, device=dev)
+    draft_logits = (torch.randn((B, K, cfg.vocab), device=dev, generator=gen) * 3.0).contiguous()
+    uniforms = torch.rand((B, K + 1), device=dev, dtype=torch.float64, generator=gen)
+    sampler = SamplerConfig(0.6, 0.95, 20)
+
+    for _ in range(args.warmup):
+        model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        res = model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    assert int(res.status.max().item()) == 0, "non-finite logits in the verify step"
+    value = B * L / (ms / 1e3)
+
+    roof = roofline_gate_up(model, B * L)
+    roof["cfg1_qmv"] = roofline_qmv_cfg1()
+    del model
+    torch.cuda.empty_cache()
+    cpu = None if args.no_cpu_baseline else cpu_baseline(cfg.layers)
+
+    line = {
+        "metric": "verify tokens/s at MTP depth 3; qmv achieved HBM GB/s (% of peak)",
+        "value": round(value, 2),
+        "unit": "verify rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 activations x 4-bit affine weights, fp32 accumulate; fp64 sampler",
+        "data": "synthetic (random-init weights, random tokens/KV/draft logits, seeded)",
+        "config": {"workload": "cfg3: depth-3 verify step, 27B-shaped 4-bit dense decoder, batch 1, "
+                               f"{args.ctx}-token context, 4 verify rows + accept/reject",
+                   "layers": cfg.layers, "hidden": cfg.hidden, "ffn": cfg.ffn, "heads": f"{cfg.n_heads}/{cfg.n_kv_heads}",
+                   "head_dim": cfg.head_dim, "vocab": cfg.vocab, "group_size": cfg.group_size, "batch": B,
+                   "verify_rows": L, "context": args.ctx, "wall_s_timed": round(wall, 3)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

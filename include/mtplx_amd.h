@@ -1,0 +1,199 @@
+/*
+ * C ABI of the MI355X (gfx950) speculative-verify hot path.
+ *
+ * Conventions for every entry point:
+ *   - returns 0 on success, a negative MTP_ERR_* code otherwise; the message
+ *     is in mtp_last_error() (thread-local);
+ *   - all pointers are device pointers (hipMalloc / torch CUDA tensors) unless
+ *     stated; bf16 tensors are passed as raw 16-bit patterns (void*);
+ *   - work is enqueued on `stream` (a hipStream_t, NULL = default stream) and
+ *     is asynchronous; nothing allocates device memory: callers pass a
+ *     workspace sized by the matching *_workspace_bytes() query;
+ *   - workspaces hold self-resetting arrival counters: give each stream its
+ *     own workspace, zero-filled once when first allocated.
+ *
+ * Reference interfaces replaced are cited as file:line of youssofal/MTPLX.
+ */
+#ifndef MTPLX_AMD_H
+#define MTPLX_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MTP_OK = 0,
+  MTP_ERR_ARG = -1,
+  MTP_ERR_UNSUPPORTED = -2,
+  MTP_ERR_WORKSPACE = -3,
+  MTP_ERR_HIP = -4
+};
+
+const char* mtp_last_error(void);
+
+/* ---- 4-bit affine quantized verify matmul ------------------------------
+ * y[M,N] = x[M,K] @ dequant(w)^T, w uint32 [N,K/8] little-endian nibbles,
+ * scales/biases bf16 [N,K/group_size], group_size 64 or 128, 1 <= M <= 32,
+ * K % 64 == 0, x/w 16-byte aligned. fp32 accumulation, bf16 output.
+ * Replaces: mtplx/verify_qmv.py:194 multi3_qmv4_matmul, :1217
+ * stocklike_qmv4_matmul, mtplx/kernels/qmv4_matmul.py:185 qmv4_matmul,
+ * mtplx/verify_kernels.py:580 vk_qmm_m4_impl (-> _run_ksplit :531), and the
+ * M<=16 routes of mtplx/nax_verify.py:754 (nax_qmm_m4 :977, m6 :628, m16 :690).
+ * `dual` selects the two-matrix workspace size (mtp_qmv_affine4_dual). */
+size_t mtp_qmv_workspace_bytes(int M, int N, int K, int dual);
+int mtp_qmv_affine4(const void* x, const void* w, const void* scales, const void* biases, void* y, int M, int N,
+                    int K, int group_size, void* ws, size_t ws_bytes, void* stream);
+
+/* y = bf16(bf16(x @ W^T) + resid) — the residual add that follows o_proj and
+ * down_proj in the verify forward (mlx-lm decoder layer `h + r`).
+ * resid may alias y. */
+int mtp_qmv_affine4_residual(const void* x, const void* w, const void* scales, const void* biases,
+                             const void* resid, void* y, int M, int N, int K, int group_size, void* ws,
+                             size_t ws_bytes, void* stream);
+
+/* Gate/up pair sharing one read of x. swiglu=0: y0 = x@W0^T, y1 = x@W1^T
+ * (mtplx/verify_qmv.py:614 multi3_dual_qmv4_matmul, :833 parallel dual);
+ * swiglu=1: y0 = silu(x@W0^T) * (x@W1^T), y1 unused. */
+int mtp_qmv_affine4_dual(const void* x, const void* w0, const void* s0, const void* b0, const void* w1,
+                         const void* s1, const void* b1, void* y0, void* y1, int M, int N, int K, int group_size,
+                         int swiglu, void* ws, size_t ws_bytes, void* stream);
+
+/* y = (silu(gate) * up) @ W^T (+ resid if resid != NULL).
+ * Replaces mtplx/verify_qmv.py:1063 multi3_swiglu_down_qmv4_matmul. */
+int mtp_qmv_affine4_swiglu_in(const void* gate, const void* up, const void* w, const void* scales,
+                              const void* biases, const void* resid, void* y, int M, int N, int K, int group_size,
+                              void* ws, size_t ws_bytes, void* stream);
+
+/* y = rmsnorm(x; norm_w, eps) @ W^T, the norm fused into the matmul's
+ * activation staging (the layer's input_layernorm + q|k|v projection). */
+int mtp_qmv_affine4_rmsnorm_in(const void* x, const void* norm_w, float eps, const void* w, const void* scales,
+                               const void* biases, void* y, int M, int N, int K, int group_size, void* ws,
+                               size_t ws_bytes, void* stream);
+
+/* fp32 logits: y = float(bf16(rmsnorm(x) @ W^T)) (norm_w NULL = no norm);
+ * the lm_head of the verify rows feeding the sampler. */
+int mtp_qmv_affine4_rmsnorm_f32(const void* x, const void* norm_w, float eps, const void* w, const void* scales,
+                                const void* biases, float* y, int M, int N, int K, int group_size, void* ws,
+                                size_t ws_bytes, void* stream);
+
+/* y = silu(rmsnorm(x)@W0^T) * (rmsnorm(x)@W1^T): post-attention norm + gate/up. */
+int mtp_qmv_affine4_rmsnorm_dual(const void* x, const void* norm_w, float eps, const void* w0, const void* s0,
+                                 const void* b0, const void* w1, const void* s1, const void* b1, void* y, int M,
+                                 int N, int K, int group_size, void* ws, size_t ws_bytes, void* stream);
+
+/* ---- Ragged KV cache + attention -----------------------------------------
+ * Cache layout [B, Hkv, cap, D] bf16 (mtplx/ragged_kv_cache.py:71).
+ * Scatter: cache[b,h,write_start[b]+i,:] = new[b,h,i,:]
+ * (RaggedBatchKVCache.update_and_fetch, mtplx/ragged_kv_cache.py:201-277).
+ * Positions outside [0,cap) are skipped and flagged in *status (device int32,
+ * may be NULL). */
+int mtp_kv_scatter(void* k_cache, void* v_cache, const void* k_new, const void* v_new, const int32_t* write_start,
+                   int B, int Hkv, int cap, int q, int D, int32_t* status, void* stream);
+
+/* Rows with row_mask[b] != 0 take snap over positions [lo,hi) (zero past
+ * snap_cap) — RaggedBatchKVCache.restore_masked, mtplx/ragged_kv_cache.py:473-496. */
+int mtp_kv_restore_masked(void* cur, const void* snap, const uint8_t* row_mask, int B, int Hkv, int cap,
+                          int snap_cap, int D, int lo, int hi, void* stream);
+
+/* uint8 mask [B,1,q_len,key_len], mask[b,0,i,j] = j <= q_start[b]+i
+ * (mtplx/ragged_attention.py:42 ragged_causal_mask). */
+int mtp_ragged_causal_mask(uint8_t* out, const int32_t* q_start, int B, int q_len, int key_len, void* stream);
+
+/* out = softmax(q k^T * scale, ragged causal mask) v with GQA (D = 128,
+ * (Hq/Hkv)*L <= 32). q,out [B,Hq,L,D]; k,v [B,Hkv,cap,D]; q_start int32 [B]
+ * on the device; q_lens int32 [B] or NULL. split_keys <= 0 picks the default.
+ * Replaces the stock SDPA on the ragged lane (mtplx/attention_split.py:347 with
+ * the mask of mtplx/ragged_attention.py:42) and the packed-GQA verify kernel
+ * (mtplx/kernels/sdpa_gqa_packed.py:299 sdpa_gqa_packed_tail). */
+size_t mtp_attn_workspace_bytes(int B, int Hkv, int cap, int split_keys);
+int mtp_ragged_gqa_attn(const void* q, const void* k, const void* v, const int32_t* q_start, const int32_t* q_lens,
+                        void* out, int B, int Hq, int Hkv, int L, int D, int cap, float scale, int split_keys,
+                        void* ws, size_t ws_bytes, void* stream);
+/* Same, out written as [B, L, Hq, D] rows (the o_proj input layout). */
+int mtp_ragged_gqa_attn_rows(const void* q, const void* k, const void* v, const int32_t* q_start,
+                             const int32_t* q_lens, void* out, int B, int Hq, int Hkv, int L, int D, int cap,
+                             float scale, int split_keys, void* ws, size_t ws_bytes, void* stream);
+
+/* ---- Verify-step glue -------------------------------------------------------
+ * RoPE (rotate-half, fp32 angles) on fused q|k|v rows [B*L, (Hq+2Hkv)*D] at
+ * positions q_start[b]+i; q -> q_out [B,Hq,L,D], k/v written into the cache
+ * (the per-row RoPE offset of tests/test_ragged_kv_cache.py:62-100 followed by
+ * update_and_fetch). */
+int mtp_rope_qkv_to_cache(const void* qkv, const int32_t* q_start, const int32_t* q_lens, void* q_out,
+                          void* k_cache, void* v_cache, int B, int L, int Hq, int Hkv, int D, int cap,
+                          float rope_base, int32_t* status, void* stream);
+int mtp_rmsnorm(const void* x, const void* w, void* out, int M, int H, float eps, void* stream);
+/* out[m] = dequant(w[tokens[m]]) — 4-bit quantized embedding rows [V, H/8]. */
+int mtp_embed_affine4(const int32_t* tokens, const void* w, const void* scales, const void* biases, void* out,
+                      int M, int H, int V, int group_size, int32_t* status, void* stream);
+
+/* ---- Expert-sorted MoE -----------------------------------------------------
+ * Routing: per token top-k of fp32 router logits (value desc, id asc) and
+ * softmax weights renormalised over the k (Qwen-MoE norm_topk_prob). */
+int mtp_moe_route(const float* logits, int T, int E, int top_k, int32_t* ids, float* weights, void* stream);
+
+/* Stable counting sort of topk_ids int32 [T, top_k] (R = T*top_k <= 8192,
+ * E <= 4096): row_map = order // top_k, sorted_ids = flat[order],
+ * inv_order = argsort(order), expert_off int32 [E+1], active int32 [1+E] =
+ * (count, active expert ids ascending); active[0] = -1 flags an id outside
+ * [0, E). Replaces mtplx/moe_sorted_gather.py:221 sort_rows. */
+size_t mtp_moe_workspace_bytes(int T, int top_k, int E);
+int mtp_moe_sort(const int32_t* topk_ids, int T, int top_k, int E, uint32_t* row_map, uint32_t* sorted_ids,
+                 uint32_t* inv_order, int32_t* expert_off, int32_t* active, void* ws, size_t ws_bytes, void* stream);
+
+/* Gathered 4-bit matmul over expert-sorted rows: sorted row i (expert e with
+ * expert_off[e] <= i < expert_off[e+1]) computes x[row_map[i]] @ deq(W[e])^T
+ * (row_map NULL: x[i]). Weights [E, rows_per_expert, K/8]; xmode 0 = x,
+ * 1 = silu(x)*x2; emode 0 = store y [R, N], 3 = silu(x@W0^T)*(x@W1^T) with
+ * W1 the up rows (mtplx/moe_sorted_gather.py:241 gather_qmm_rows, :288
+ * swiglu_rows, :339 switch_linear; mlx gather_qmm(sorted_indices=True) at
+ * :170). max_rows_per_expert bounds any expert's row count (<= T). */
+int mtp_gather_qmv_affine4(const void* x, const void* x2, const uint32_t* row_map, const int32_t* expert_off,
+                           const int32_t* active, const void* w0, const void* s0, const void* b0, const void* w1,
+                           const void* s1, const void* b1, void* y, int max_rows_per_expert, int E, int N, int K,
+                           int group_size, int xmode, int emode, int rows_per_expert, void* ws, size_t ws_bytes,
+                           void* stream);
+
+/* out[t] = bf16(sum_j route_w[t,j] * y_sorted[inv_order[t*k+j]]) (+ shared[t])
+ * — unsort and weighted combine (mtplx/models/qwen4_exp.py:1544-1577). */
+int mtp_moe_combine(const void* y_sorted, const uint32_t* inv_order, const float* route_w, const void* shared,
+                    void* out, int T, int top_k, int H, void* stream);
+
+/* ---- Exact speculative accept / reject ------------------------------------
+ * target_logits fp32 [B*(K+1), V] (row K of each request = bonus row),
+ * draft_logits fp32 [B*K, V], draft_ids int32 [B,K], uniforms fp64 [B,K+1]
+ * consumed in stream order. Law: mtplx/sampling.py:131-391 (softmax with T,
+ * top-k value desc/id asc, top-p over full-vocab mass, min(1,p/q), residual
+ * max(p-q,0) renormalised, Generator.choice = cdf/searchsorted); loop order
+ * mtplx/generation.py:15560-15790, bonus :16085-16110. temperature <= 0 is the
+ * greedy lane (no uniforms). 1 <= top_k <= 64 on the GPU.
+ * Outputs: out_tokens int32 [B,K+1] (committed ids, -1 padded), n_accepted
+ * int32 [B], accept_probs fp64 [B,K] (-1 = not examined), status int32 [B]
+ * (1 = non-finite logits: mtplx/sampling.py:32 NonFiniteLogitsError). */
+size_t mtp_sampler_workspace_bytes(int rows, int V);
+int mtp_spec_accept(const float* target_logits, const float* draft_logits, const int32_t* draft_ids,
+                    const double* uniforms, int B, int K, int V, double temperature, int top_k, double top_p,
+                    int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
+                    size_t ws_bytes, void* stream);
+
+/* Per-row sparse law (ids ascending, fp64 probs, count) and optionally one
+ * draw per row with uniforms[r]: mtplx/sampling.py:259 distribution_from_logits
+ * + :342 sample_from_distribution; mtplx/fast_sampling.py:637
+ * sparse_distribution_from_mlx_logits. out_ids/out_probs are [rows, top_k]. */
+int mtp_sample_rows(const float* logits, int rows, int V, double temperature, int top_k, double top_p,
+                    const double* uniforms, int32_t* out_ids, double* out_probs, int32_t* out_count,
+                    int32_t* sampled, int32_t* status, void* ws, size_t ws_bytes, void* stream);
+
+/* Diagnostic with no counterpart in the reference: writes the 64x16 register
+ * image of one v_mfma_f32_32x32x16_bf16 on a known operand pattern (tests use
+ * it to pin the lane layout the kernels assume). */
+int mtp_probe_mfma_layout(float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MTPLX_AMD_H */

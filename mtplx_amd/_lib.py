@@ -1,0 +1,143 @@
+"""ctypes binding of ``libmtplx_amd.so`` (the C ABI in ``include/mtplx_amd.h``).
+
+The library is loaded after ``torch`` so that it binds to the HIP runtime
+torch already mapped (one runtime per process). There is no CPU fallback: if
+the library is missing or a call fails, :class:`MtpError` is raised.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmtplx_amd.so")
+
+_vp = C.c_void_p
+_i = C.c_int
+_f = C.c_float
+_d = C.c_double
+_sz = C.c_size_t
+
+# name -> (restype, argtypes); mirrors include/mtplx_amd.h.
+SIGNATURES = {
+    "mtp_last_error": (C.c_char_p, []),
+    "mtp_qmv_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "mtp_qmv_affine4": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "mtp_qmv_affine4_residual": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "mtp_qmv_affine4_dual": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "mtp_qmv_affine4_swiglu_in": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "mtp_qmv_affine4_rmsnorm_in": (_i, [_vp, _vp, _f, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "mtp_qmv_affine4_rmsnorm_f32": (_i, [_vp, _vp, _f, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "mtp_qmv_affine4_rmsnorm_dual": (_i, [_vp, _vp, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp,
+                                          _sz, _vp]),
+    "mtp_kv_scatter": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]),
+    "mtp_kv_restore_masked": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "mtp_ragged_causal_mask": (_i, [_vp, _vp, _i, _i, _i, _vp]),
+    "mtp_attn_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "mtp_ragged_gqa_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp]),
+    "mtp_ragged_gqa_attn_rows": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz,
+                                      _vp]),
+    "mtp_rope_qkv_to_cache": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _vp]),
+    "mtp_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
+    "mtp_embed_affine4": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp]),
+    "mtp_sampler_workspace_bytes": (_sz, [_i, _i]),
+    "mtp_spec_accept": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mtp_sample_rows": (_i, [_vp, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mtp_probe_mfma_layout": (_i, [_vp, _vp]),
+    "mtp_moe_workspace_bytes": (_sz, [_i, _i, _i]),
+    "mtp_moe_sort": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mtp_gather_qmv_affine4": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
+                                    _i, _i, _i, _i, _vp, _sz, _vp]),
+    "mtp_moe_route": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
+    "mtp_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+}
+
+
+class MtpError(RuntimeError):
+    """A C-ABI call failed (message from ``mtp_last_error``)."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed ({code}): {msg}")
+        self.code = code
+
+
+_LIB = None
+_LOCK = threading.Lock()
+
+
+def load():
+    """Load the library once (after torch) and bind every declared symbol."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    with _LOCK:
+        if _LIB is not None:
+            return _LIB
+        import torch  # noqa: F401  -- bind to the HIP runtime torch mapped
+
+        if not os.path.exists(LIB_PATH):
+            raise MtpError("load", -4, f"{LIB_PATH} is missing; run `python -m mtplx_amd.build`")
+        lib = C.CDLL(LIB_PATH, mode=C.RTLD_GLOBAL)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = lib
+        return lib
+
+
+def call(name: str, *args) -> int:
+    """Call ``name`` and raise :class:`MtpError` on a non-zero return."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.mtp_last_error().decode(errors="replace")
+        raise MtpError(name, rc, msg)
+    return rc
+
+
+def query(name: str, *args) -> int:
+    return int(getattr(load(), name)(*args))
+
+
+# ---------------------------------------------------------------------------
+# torch plumbing: pointers, streams, workspaces.
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device=None) -> int:
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class _Workspaces:
+    """One zero-initialised byte buffer per (device, stream, tag), grown on demand.
+
+    Kernels keep self-resetting arrival counters in their workspace, so a
+    buffer is zero-filled only when it is (re)allocated.
+    """
+
+    def __init__(self):
+        self._bufs: dict = {}
+
+    def get(self, nbytes: int, tag: str, device=None):
+        import torch
+
+        dev = torch.device("cuda", torch.cuda.current_device() if device is None else torch.device(device).index)
+        key = (dev.index, stream_handle(dev), tag)
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            size = max(int(nbytes), 256)
+            if buf is not None:
+                size = max(size, 2 * buf.numel())
+            buf = torch.zeros(size, dtype=torch.uint8, device=dev)
+            self._bufs[key] = buf
+        return buf
+
+
+WORKSPACES = _Workspaces()

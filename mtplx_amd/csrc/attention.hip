@@ -1,0 +1,419 @@
+// Ragged-batch GQA verify attention over a padded ragged KV cache, gfx950.
+//
+// Semantics (mtplx/ragged_attention.py:42-85 + MLX SDPA as called from
+// mtplx/attention_split.py:347): query row i of request b sits at absolute
+// position q_start[b] + i and attends keys j <= q_start[b] + i; GQA maps query
+// head hq to kv head hq / (Hq/Hkv); softmax in fp32; bf16 in/out.
+//
+// Design: a work unit is (request b, kv head h, key split s). The rep*L query
+// rows that share kv head h (e.g. 5 heads x 4 verify rows = 20) form the
+// 32-row side of v_mfma_f32_32x32x16_bf16, so one wave streams each K/V row of
+// the split exactly once:
+//   S^T = K Q^T        A = K rows (lane = key, 128 B contiguous per lane)
+//   O^T += V^T P^T     B = P^T straight from the S^T accumulators (no shuffle),
+//                      A = V^T read from a transposed LDS tile
+// Online softmax per query column; each column's 32 keys live in two lanes
+// (l, l^32), so the tile max is one shuffle. Splits write (m, l, O) partials
+// and a second kernel merges them in split order (deterministic). Offsets are
+// read on the GPU; units past a request's length exit at once.
+#include "common.hpp"
+
+namespace mtp {
+
+constexpr int kHD = 128;          // head dim
+constexpr int kTileKeys = 32;
+constexpr int kVtStride = 34;     // keys per LDS row (padded against bank conflicts)
+constexpr float kNegBig = -1.0e30f;
+
+struct AttnParams {
+  const uint16_t* q;         // [B, Hq, L, D]
+  const uint16_t* k;         // [B, Hkv, cap, D]
+  const uint16_t* v;
+  const int32_t* q_start;    // [B]
+  const int32_t* q_lens;     // [B] or null (all L)
+  uint16_t* out;             // [B, Hq, L, D]
+  float* part_o;             // [B*Hkv*S][32][D]
+  float* part_ml;            // [B*Hkv*S][32][2]
+  int B, Hq, Hkv, L, cap, S, split_keys;
+  int out_rows;              // 1: out is [B, L, Hq, D] (rows feed the o projection)
+  float scale_log2;          // softmax scale * log2(e)
+};
+
+__device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
+  return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+}
+
+__global__ __launch_bounds__(64) void attn_split_kernel(AttnParams p) {
+  __shared__ __align__(16) uint16_t vt[kHD * kVtStride];
+  const int lane = threadIdx.x;
+  const int c32 = lane & 31;
+  const int h2 = lane >> 5;
+  const int unit = blockIdx.x;
+  const int s = unit % p.S;
+  const int bh = unit / p.S;
+  const int h = bh % p.Hkv;
+  const int b = bh / p.Hkv;
+  const int rep = p.Hq / p.Hkv;
+  const int qs = p.q_start[b];
+  const int L = p.q_lens ? p.q_lens[b] : p.L;
+  const int kv_end = qs + L;  // keys [0, kv_end) are visible to some row
+  const int k0 = s * p.split_keys;
+  int k1 = k0 + p.split_keys;
+  if (k1 > kv_end) k1 = kv_end;
+  if (k1 > p.cap) k1 = p.cap;
+
+  float* po = p.part_o + (size_t)unit * 32 * kHD;
+  float* pml = p.part_ml + (size_t)unit * 64;
+  if (k0 >= k1) {
+    // Empty split: mark so the merge skips it.
+    if (lane < 32) {
+      pml[2 * lane] = kNegBig;
+      pml[2 * lane + 1] = 0.f;
+    }
+    return;
+  }
+
+  // Query column q = r*L + i (head h*rep + r, verify row i).
+  const int qcol = c32;
+  const int qr = qcol / p.L;
+  const int qi = qcol - qr * p.L;
+  const bool qvalid = (qr < rep) && (qi < L);
+  const int qbound = qs + qi;  // last key this column may see
+
+  // B operand Q^T: lane (q, h2) holds d = 64*h2 + 8*i + e for MFMA i.
+  bf16x8 qop[8];
+  {
+    const uint16_t* qrow = p.q + ((((size_t)b * p.Hq + h * rep + (qvalid ? qr : 0)) * p.L + (qvalid ? qi : 0)) * kHD);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint4 raw = qvalid ? *reinterpret_cast<const uint4*>(qrow + 64 * h2 + 8 * i) : make_uint4(0, 0, 0, 0);
+      qop[i] = __builtin_bit_cast(bf16x8, raw);
+    }
+  }
+
+  f32x16 o[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) o[t] = f32x16{};
+  float m_run = kNegBig;
+  float l_run = 0.f;
+
+  const uint16_t* kbase = p.k + ((size_t)b * p.Hkv + h) * (size_t)p.cap * kHD;
+  const uint16_t* vbase = p.v + ((size_t)b * p.Hkv + h) * (size_t)p.cap * kHD;
+
+  for (int kt = k0; kt < k1; kt += kTileKeys) {
+    const int key = kt + c32;
+    const bool kin = key < k1;
+    const uint16_t* krow = kbase + (size_t)(kin ? key : kt) * kHD + 64 * h2;
+    const uint16_t* vrow = vbase + (size_t)(kin ? key : kt) * kHD + 64 * h2;
+    uint4 kr[8], vr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      kr[i] = kin ? *reinterpret_cast<const uint4*>(krow + 8 * i) : make_uint4(0, 0, 0, 0);
+      vr[i] = kin ? *reinterpret_cast<const uint4*>(vrow + 8 * i) : make_uint4(0, 0, 0, 0);
+    }
+    // S^T[key][q]
+    f32x16 st = {};
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kr[i]), qop[i], st, 0, 0, 0);
+
+    // V^T tile into LDS: vt[d][key].
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t w4[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int d = 64 * h2 + 8 * i + 2 * t;
+        vt[d * kVtStride + c32] = (uint16_t)(w4[t] & 0xffff);
+        vt[(d + 1) * kVtStride + c32] = (uint16_t)(w4[t] >> 16);
+      }
+    }
+
+    // Scale, mask, tile max for column q (this lane's 16 keys + lane^32's).
+    float sv[16];
+    float tmax = kNegBig;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kk = kt + 8 * (r >> 2) + 4 * h2 + (r & 3);
+      const bool ok = qvalid && kk < k1 && kk <= qbound;
+      sv[r] = ok ? st[r] * p.scale_log2 : -INFINITY;
+      tmax = fmaxf(tmax, sv[r]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float corr = exp2f(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sv[r] = exp2f(sv[r] - m_new);
+      psum += sv[r];
+    }
+    l_run = l_run * corr + psum;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+
+    // P^T operands: MFMA j uses registers 8j..8j+7.
+    bf16x8 pop[2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      uint32_t pk[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) pk[t] = pack_bf2(sv[8 * jj + 2 * t], sv[8 * jj + 2 * t + 1]);
+      pop[jj] = __builtin_bit_cast(bf16x8, pk);
+    }
+    __syncthreads();
+    // O^T[d][q] += V^T[d][keys] P^T[keys][q]; slot e of lane (d, h2) in step j
+    // is key 16j + (e<4 ? 4*h2+e : 8+4*h2+e-4).
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint16_t* vd = vt + (32 * t + c32) * kVtStride;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        uint16_t e8[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          e8[e] = vd[16 * jj + 4 * h2 + e];
+          e8[4 + e] = vd[16 * jj + 8 + 4 * h2 + e];
+        }
+        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, e8), pop[jj], o[t], 0, 0, 0);
+      }
+    }
+  }
+
+  // Split partial: l over both halves of the column; O^T rows d, column q.
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (h2 == 0) {
+    pml[2 * qcol] = m_run;
+    pml[2 * qcol + 1] = l_tot;
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = 32 * t + 8 * (r >> 2) + 4 * h2 + (r & 3);
+      po[qcol * kHD + d] = o[t][r];
+    }
+}
+
+// grid: B*Hkv workgroups of 256 threads; merge splits in order.
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
+  const int bh = blockIdx.x;
+  const int h = bh % p.Hkv;
+  const int b = bh / p.Hkv;
+  const int rep = p.Hq / p.Hkv;
+  const int L = p.q_lens ? p.q_lens[b] : p.L;
+  const int kv_end = p.q_start[b] + L;
+  int ns = cdiv(kv_end < p.cap ? kv_end : p.cap, p.split_keys);
+  if (ns > p.S) ns = p.S;
+  const int rows = rep * p.L;
+  for (int idx = threadIdx.x; idx < rows * kHD; idx += blockDim.x) {
+    const int q = idx / kHD;
+    const int d = idx - q * kHD;
+    const int qr = q / p.L, qi = q - (q / p.L) * p.L;
+    float M = kNegBig;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, p.part_ml[((size_t)bh * p.S + s) * 64 + 2 * q]);
+    float lsum = 0.f, acc = 0.f;
+    for (int s = 0; s < ns; ++s) {
+      const size_t u = (size_t)bh * p.S + s;
+      const float w = exp2f(p.part_ml[u * 64 + 2 * q] - M);
+      lsum += p.part_ml[u * 64 + 2 * q + 1] * w;
+      acc += p.part_o[(u * 32 + q) * kHD + d] * w;
+    }
+    const float val = (qi < L && lsum > 0.f) ? acc / lsum : 0.f;
+    const size_t oi = p.out_rows ? ((((size_t)b * p.L + qi) * p.Hq + h * rep + qr) * kHD + d)
+                                 : ((((size_t)b * p.Hq + h * rep + qr) * p.L + qi) * kHD + d);
+    p.out[oi] = f2bf(val);
+  }
+}
+
+static int attn_plan(int cap, int split_keys_req, int* S, int* split_keys) {
+  int sk = split_keys_req > 0 ? split_keys_req : 512;
+  sk = ((sk + kTileKeys - 1) / kTileKeys) * kTileKeys;
+  *split_keys = sk;
+  *S = cdiv(cap, sk);
+  return MTP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// KV cache mechanics (mtplx/ragged_kv_cache.py:201-277, :473-496).
+
+// new [B, Hkv, q, D] -> cache[b, h, ws[b] + i, :]; 16 B per thread.
+__global__ void kv_scatter_kernel(uint16_t* kc, uint16_t* vc, const uint16_t* kn, const uint16_t* vn,
+                                  const int32_t* ws, int B, int Hkv, int cap, int q, int D, int32_t* status) {
+  const size_t n16 = (size_t)B * Hkv * q * D / 8;
+  for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n16; t += (size_t)gridDim.x * blockDim.x) {
+    const size_t e = t * 8;
+    const int d = (int)(e % D);
+    const size_t r = e / D;
+    const int i = (int)(r % q);
+    const size_t bh = r / q;
+    const int b = (int)(bh / Hkv);
+    const int pos = ws[b] + i;
+    if (pos < 0 || pos >= cap) {
+      if (status) atomicOr(status, 1);
+      continue;
+    }
+    const size_t dst = (bh * cap + pos) * D + d;
+    *reinterpret_cast<uint4*>(kc + dst) = *reinterpret_cast<const uint4*>(kn + e);
+    *reinterpret_cast<uint4*>(vc + dst) = *reinterpret_cast<const uint4*>(vn + e);
+  }
+}
+
+// Rows with mask[b] take the snapshot over positions [lo, hi) (snapshot zero
+// padded past its capacity); other rows untouched.
+__global__ void kv_restore_kernel(uint16_t* cur, const uint16_t* snap, const uint8_t* mask, int B, int Hkv,
+                                  int cap, int snap_cap, int D, int lo, int hi) {
+  const int span = hi - lo;
+  const size_t n16 = (size_t)B * Hkv * span * D / 8;
+  for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n16; t += (size_t)gridDim.x * blockDim.x) {
+    const size_t e = t * 8;
+    const int d = (int)(e % D);
+    const size_t r = e / D;
+    const int pos = lo + (int)(r % span);
+    const size_t bh = r / span;
+    const int b = (int)(bh / Hkv);
+    if (!mask[b]) continue;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (pos < snap_cap) val = *reinterpret_cast<const uint4*>(snap + (bh * snap_cap + pos) * D + d);
+    *reinterpret_cast<uint4*>(cur + (bh * cap + pos) * D + d) = val;
+  }
+}
+
+// bool mask [B, 1, q_len, key_len]: mask[b,0,i,j] = j <= q_start[b] + i.
+__global__ void ragged_mask_kernel(uint8_t* out, const int32_t* qs, int B, int q_len, int key_len) {
+  const size_t n = (size_t)B * q_len * key_len;
+  for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n; t += (size_t)gridDim.x * blockDim.x) {
+    const int j = (int)(t % key_len);
+    const size_t r = t / key_len;
+    const int i = (int)(r % q_len);
+    const int b = (int)(r / q_len);
+    out[t] = (j <= qs[b] + i) ? 1 : 0;
+  }
+}
+
+static int grid_for(size_t n, int block) {
+  size_t g = (n + block - 1) / block;
+  if (g > 65536) g = 65536;
+  if (g < 1) g = 1;
+  return (int)g;
+}
+
+}  // namespace mtp
+
+using namespace mtp;
+
+MTP_API size_t mtp_attn_workspace_bytes(int B, int Hkv, int cap, int split_keys) {
+  int S, sk;
+  attn_plan(cap, split_keys, &S, &sk);
+  const size_t units = (size_t)B * Hkv * S;
+  return units * 32 * kHD * sizeof(float) + units * 64 * sizeof(float);
+}
+
+static int attn_run(const void* q, const void* k, const void* v, const int32_t* q_start, const int32_t* q_lens,
+                    void* out, int out_rows, int B, int Hq, int Hkv, int L, int D, int cap, float scale,
+                    int split_keys, void* ws, size_t ws_bytes, void* stream, const char* who) {
+  if (!q || !k || !v || !q_start || !out || B < 1 || Hq < 1 || Hkv < 1 || L < 1 || cap < 1) {
+    set_error("%s: bad arguments", who);
+    return MTP_ERR_ARG;
+  }
+  if (D != kHD) {
+    set_error("%s: head_dim %d unsupported (128)", who, D);
+    return MTP_ERR_UNSUPPORTED;
+  }
+  if (Hq % Hkv) {
+    set_error("%s: Hq=%d not a multiple of Hkv=%d", who, Hq, Hkv);
+    return MTP_ERR_ARG;
+  }
+  if ((Hq / Hkv) * L > 32) {
+    set_error("%s: (Hq/Hkv)*L = %d query rows per kv head exceeds 32", who, (Hq / Hkv) * L);
+    return MTP_ERR_UNSUPPORTED;
+  }
+  AttnParams p = {};
+  p.q = (const uint16_t*)q;
+  p.k = (const uint16_t*)k;
+  p.v = (const uint16_t*)v;
+  p.q_start = q_start;
+  p.q_lens = q_lens;
+  p.out = (uint16_t*)out;
+  p.B = B;
+  p.Hq = Hq;
+  p.Hkv = Hkv;
+  p.L = L;
+  p.cap = cap;
+  p.out_rows = out_rows;
+  attn_plan(cap, split_keys, &p.S, &p.split_keys);
+  p.scale_log2 = scale * 1.4426950408889634f;
+  const size_t need = mtp_attn_workspace_bytes(B, Hkv, cap, split_keys);
+  if (!ws || ws_bytes < need) {
+    set_error("%s: workspace %zu B < required %zu B", who, ws_bytes, need);
+    return MTP_ERR_WORKSPACE;
+  }
+  const size_t units = (size_t)B * Hkv * p.S;
+  p.part_o = (float*)ws;
+  p.part_ml = p.part_o + units * 32 * kHD;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(attn_split_kernel, dim3((unsigned)units), dim3(64), 0, st, p);
+  int rc = launch_check(who);
+  if (rc) return rc;
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(B * Hkv), dim3(256), 0, st, p);
+  return launch_check(who);
+}
+
+MTP_API int mtp_ragged_gqa_attn(const void* q, const void* k, const void* v, const int32_t* q_start,
+                                const int32_t* q_lens, void* out, int B, int Hq, int Hkv, int L, int D, int cap,
+                                float scale, int split_keys, void* ws, size_t ws_bytes, void* stream) {
+  return attn_run(q, k, v, q_start, q_lens, out, 0, B, Hq, Hkv, L, D, cap, scale, split_keys, ws, ws_bytes, stream,
+                  "mtp_ragged_gqa_attn");
+}
+
+MTP_API int mtp_ragged_gqa_attn_rows(const void* q, const void* k, const void* v, const int32_t* q_start,
+                                     const int32_t* q_lens, void* out, int B, int Hq, int Hkv, int L, int D, int cap,
+                                     float scale, int split_keys, void* ws, size_t ws_bytes, void* stream) {
+  return attn_run(q, k, v, q_start, q_lens, out, 1, B, Hq, Hkv, L, D, cap, scale, split_keys, ws, ws_bytes, stream,
+                  "mtp_ragged_gqa_attn_rows");
+}
+
+MTP_API int mtp_kv_scatter(void* k_cache, void* v_cache, const void* k_new, const void* v_new,
+                           const int32_t* write_start, int B, int Hkv, int cap, int q, int D, int32_t* status,
+                           void* stream) {
+  if (!k_cache || !v_cache || !k_new || !v_new || !write_start || B < 1 || Hkv < 1 || cap < 1 || q < 1 ||
+      D < 8 || D % 8) {
+    set_error("mtp_kv_scatter: bad arguments (D must be a multiple of 8)");
+    return MTP_ERR_ARG;
+  }
+  const size_t n16 = (size_t)B * Hkv * q * D / 8;
+  hipLaunchKernelGGL(kv_scatter_kernel, dim3(grid_for(n16, 256)), dim3(256), 0, (hipStream_t)stream,
+                     (uint16_t*)k_cache, (uint16_t*)v_cache, (const uint16_t*)k_new, (const uint16_t*)v_new,
+                     write_start, B, Hkv, cap, q, D, status);
+  return launch_check("mtp_kv_scatter");
+}
+
+MTP_API int mtp_kv_restore_masked(void* cur, const void* snap, const uint8_t* row_mask, int B, int Hkv, int cap,
+                                  int snap_cap, int D, int lo, int hi, void* stream) {
+  if (!cur || !snap || !row_mask || B < 1 || Hkv < 1 || cap < 1 || snap_cap < 0 || D < 8 || D % 8 || lo < 0 ||
+      hi > cap || lo > hi) {
+    set_error("mtp_kv_restore_masked: bad arguments");
+    return MTP_ERR_ARG;
+  }
+  if (hi == lo) return MTP_OK;
+  const size_t n16 = (size_t)B * Hkv * (hi - lo) * D / 8;
+  hipLaunchKernelGGL(kv_restore_kernel, dim3(grid_for(n16, 256)), dim3(256), 0, (hipStream_t)stream,
+                     (uint16_t*)cur, (const uint16_t*)snap, row_mask, B, Hkv, cap, snap_cap, D, lo, hi);
+  return launch_check("mtp_kv_restore_masked");
+}
+
+MTP_API int mtp_ragged_causal_mask(uint8_t* out, const int32_t* q_start, int B, int q_len, int key_len,
+                                   void* stream) {
+  if (!out || !q_start || B < 1 || q_len < 1 || key_len < 1) {
+    set_error("mtp_ragged_causal_mask: bad arguments");
+    return MTP_ERR_ARG;
+  }
+  const size_t n = (size_t)B * q_len * key_len;
+  hipLaunchKernelGGL(ragged_mask_kernel, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t)stream, out, q_start, B,
+                     q_len, key_len);
+  return launch_check("mtp_ragged_causal_mask");
+}

@@ -1,0 +1,59 @@
+// Shared definitions for the gfx950 verify-path kernels and their C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#define MTP_API extern "C" __attribute__((visibility("default")))
+
+// Error codes returned by every entry point (0 = ok).
+enum {
+  MTP_OK = 0,
+  MTP_ERR_ARG = -1,          // bad shape / pointer / size argument
+  MTP_ERR_UNSUPPORTED = -2,  // valid but not implemented (e.g. group_size 32)
+  MTP_ERR_WORKSPACE = -3,    // workspace too small
+  MTP_ERR_HIP = -4,          // a HIP runtime call failed
+};
+
+namespace mtp {
+
+// Thread-local message for mtp_last_error().
+void set_error(const char* fmt, ...);
+
+inline int hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) {
+    set_error("%s: %s", what, hipGetErrorString(e));
+    return MTP_ERR_HIP;
+  }
+  return MTP_OK;
+}
+
+// Launch-status check used after every kernel launch.
+inline int launch_check(const char* what) {
+  return hip_check(hipGetLastError(), what);
+}
+
+typedef uint16_t bf16_t;  // raw bfloat16 bits at the ABI
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf2f(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+
+// float -> bf16 bits, round to nearest even, NaN kept quiet.
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+
+__host__ __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace mtp

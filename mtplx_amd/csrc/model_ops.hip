@@ -1,0 +1,151 @@
+// Glue around the verify matmuls for the synthetic dense/MoE verify step:
+// quantized embedding gather, RoPE on the fused q|k|v rows with per-request
+// offsets (writing K/V straight into the ragged cache), standalone RMSNorm.
+//
+// RoPE is the non-interleaved (rotate-half) form with fp32 angles
+// theta_i = pos * 2^(-(2i/D) * log2(base)), as MLX's fast rope computes it;
+// per-row positions come from q_start[b] + i on the GPU
+// (tests/test_ragged_kv_cache.py:62-100 gate 5, mtplx/ragged_kv_cache.py:201).
+#include "common.hpp"
+
+namespace mtp {
+
+// out[m, :] = dequant(W[tok[m], :]) in bf16; 4-bit affine rows [V, H/8].
+__global__ void embed_affine4_kernel(const int32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                                     uint16_t* out, int M, int H, int gs, int V, int32_t* status) {
+  const int m = blockIdx.y;
+  const int t = tok[m];
+  const bool ok = t >= 0 && t < V;
+  if (!ok && threadIdx.x == 0 && blockIdx.x == 0 && status) atomicOr(status, 1);
+  for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < H / 8; j += gridDim.x * blockDim.x) {
+    uint4 o = make_uint4(0, 0, 0, 0);
+    if (ok) {
+      const uint32_t word = w[(size_t)t * (H / 8) + j];
+      const int g = (8 * j) / gs;
+      const float sc = bf2f(s[(size_t)t * (H / gs) + g]);
+      const float bi = bf2f(b[(size_t)t * (H / gs) + g]);
+      uint16_t e[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) e[i] = f2bf((float)((word >> (4 * i)) & 0xF) * sc + bi);
+      o.x = e[0] | ((uint32_t)e[1] << 16);
+      o.y = e[2] | ((uint32_t)e[3] << 16);
+      o.z = e[4] | ((uint32_t)e[5] << 16);
+      o.w = e[6] | ((uint32_t)e[7] << 16);
+    }
+    *reinterpret_cast<uint4*>(out + (size_t)m * H + 8 * j) = o;
+  }
+}
+
+// qkv rows [M = B*L, (Hq + 2*Hkv) * D]; q_out [B, Hq, L, D]; cache [B, Hkv, cap, D].
+// One thread per (row, head, rotary pair) for q and k; v copied 8 elements per thread.
+__global__ void rope_qkv_kernel(const uint16_t* qkv, const int32_t* q_start, const int32_t* q_lens, uint16_t* q_out,
+                                uint16_t* kc, uint16_t* vc, int B, int L, int Hq, int Hkv, int D, int cap,
+                                float log2_base, int32_t* status) {
+  const int half = D / 2;
+  const int m = blockIdx.y;
+  const int b = m / L;
+  const int i = m - b * L;
+  const int len = q_lens ? q_lens[b] : L;
+  const int pos = q_start[b] + i;
+  const int width = (Hq + 2 * Hkv) * D;
+  const uint16_t* row = qkv + (size_t)m * width;
+  const int nrot = (Hq + Hkv) * half;
+  for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < nrot + Hkv * D / 8; t += gridDim.x * blockDim.x) {
+    if (t < nrot) {
+      const int head = t / half;
+      const int j = t - head * half;
+      const float inv_freq = exp2f(-((float)(2 * j) / (float)D) * log2_base);
+      const float theta = (float)pos * inv_freq;
+      float sn, cs;
+      sincosf(theta, &sn, &cs);
+      const uint16_t* src = row + head * D;
+      const float x1 = bf2f(src[j]), x2 = bf2f(src[j + half]);
+      const uint16_t o1 = f2bf(x1 * cs - x2 * sn);
+      const uint16_t o2 = f2bf(x1 * sn + x2 * cs);
+      if (head < Hq) {
+        uint16_t* dst = q_out + (((size_t)b * Hq + head) * L + i) * D;
+        dst[j] = o1;
+        dst[j + half] = o2;
+      } else if (i < len) {
+        if (pos < 0 || pos >= cap) {
+          if (status) atomicOr(status, 1);
+          continue;
+        }
+        uint16_t* dst = kc + (((size_t)b * Hkv + (head - Hq)) * cap + pos) * D;
+        dst[j] = o1;
+        dst[j + half] = o2;
+      }
+    } else if (i < len) {
+      const int e = (t - nrot) * 8;
+      const int head = e / D;
+      const int d = e - head * D;
+      if (pos < 0 || pos >= cap) {
+        if (status) atomicOr(status, 1);
+        continue;
+      }
+      *reinterpret_cast<uint4*>(vc + (((size_t)b * Hkv + head) * cap + pos) * D + d) =
+          *reinterpret_cast<const uint4*>(row + (Hq + Hkv) * D + e);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const uint16_t* w, uint16_t* out, int H,
+                                                      float eps) {
+  const int m = blockIdx.x;
+  const uint16_t* xr = x + (size_t)m * H;
+  __shared__ float red[4];
+  float ss = 0.f;
+  for (int k = threadIdx.x; k < H; k += 256) {
+    const float a = bf2f(xr[k]);
+    ss += a * a;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float inv = rsqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)H + eps);
+  for (int k = threadIdx.x; k < H; k += 256) out[(size_t)m * H + k] = f2bf(bf2f(xr[k]) * inv * bf2f(w[k]));
+}
+
+}  // namespace mtp
+
+using namespace mtp;
+
+MTP_API int mtp_embed_affine4(const int32_t* tokens, const void* w, const void* scales, const void* biases, void* out,
+                              int M, int H, int V, int group_size, int32_t* status, void* stream) {
+  if (!tokens || !w || !scales || !biases || !out || M < 1 || H < 8 || H % 8 || group_size < 8 ||
+      H % group_size || group_size % 8) {
+    set_error("mtp_embed_affine4: bad arguments");
+    return MTP_ERR_ARG;
+  }
+  dim3 grid(cdiv(H / 8, 256), M);
+  hipLaunchKernelGGL(embed_affine4_kernel, grid, dim3(256), 0, (hipStream_t)stream, tokens, (const uint32_t*)w,
+                     (const uint16_t*)scales, (const uint16_t*)biases, (uint16_t*)out, M, H, group_size, V, status);
+  return launch_check("mtp_embed_affine4");
+}
+
+MTP_API int mtp_rope_qkv_to_cache(const void* qkv, const int32_t* q_start, const int32_t* q_lens, void* q_out,
+                                  void* k_cache, void* v_cache, int B, int L, int Hq, int Hkv, int D, int cap,
+                                  float rope_base, int32_t* status, void* stream) {
+  if (!qkv || !q_start || !q_out || !k_cache || !v_cache || B < 1 || L < 1 || Hq < 1 || Hkv < 1 || D < 8 ||
+      D % 8 || cap < 1 || !(rope_base > 1.f)) {
+    set_error("mtp_rope_qkv_to_cache: bad arguments");
+    return MTP_ERR_ARG;
+  }
+  const int work = (Hq + Hkv) * (D / 2) + Hkv * D / 8;
+  dim3 grid(cdiv(work, 256), B * L);
+  hipLaunchKernelGGL(rope_qkv_kernel, grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t*)qkv, q_start, q_lens,
+                     (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, B, L, Hq, Hkv, D, cap,
+                     log2f(rope_base), status);
+  return launch_check("mtp_rope_qkv_to_cache");
+}
+
+MTP_API int mtp_rmsnorm(const void* x, const void* w, void* out, int M, int H, float eps, void* stream) {
+  if (!x || !w || !out || M < 1 || H < 1) {
+    set_error("mtp_rmsnorm: bad arguments");
+    return MTP_ERR_ARG;
+  }
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)x,
+                     (const uint16_t*)w, (uint16_t*)out, H, eps);
+  return launch_check("mtp_rmsnorm");
+}

@@ -1,0 +1,187 @@
+// Expert-sorted MoE dispatch around the gathered quantized matmul, gfx950.
+//
+//  * mtp_moe_route: per token, top-k of the router logits (value desc, id
+//    asc) and the softmax weights renormalised over the chosen k.
+//  * mtp_moe_sort: stable counting sort of the flattened top-k expert ids —
+//    the closed form of mtplx/moe_sorted_gather.py:221-238 sort_rows:
+//      order = stable_argsort(flat), inv_order = argsort(order),
+//      row_map = order // top_k, sorted = flat[order]
+//    plus expert row offsets and the compact list of experts that got rows
+//    (the gathered matmul launches one workgroup column per active expert).
+//  * mtp_moe_combine: unsort + route-weighted sum over top_k (+ shared
+//    expert), the caller's tail in mtplx/models/qwen4_exp.py:1544-1577.
+#include "common.hpp"
+
+namespace mtp {
+
+constexpr int kSortThreads = 1024;
+constexpr int kMaxSortRows = 8192;
+constexpr int kMaxExperts = 4096;
+
+__global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t* ids, int R, int top_k, int E,
+                                                                uint32_t* row_map, uint32_t* sorted_ids,
+                                                                uint32_t* inv_order, int32_t* expert_off,
+                                                                int32_t* active) {
+  __shared__ int s_ids[kMaxSortRows];
+  __shared__ int s_cnt[kMaxExperts + 1];
+  __shared__ int s_bad;
+  const int tid = threadIdx.x;
+  if (tid == 0) s_bad = 0;
+  for (int e = tid; e <= E; e += kSortThreads) s_cnt[e] = 0;
+  __syncthreads();
+  for (int i = tid; i < R; i += kSortThreads) {
+    const int e = ids[i];
+    s_ids[i] = e;
+    if (e < 0 || e >= E)
+      s_bad = 1;
+    else
+      atomicAdd(&s_cnt[e], 1);
+  }
+  __syncthreads();
+  if (s_bad) {
+    if (tid == 0) active[0] = -1;
+    return;
+  }
+  // Exclusive scan of counts (E <= 4096, one thread: small and fixed order).
+  if (tid == 0) {
+    int run = 0, na = 0;
+    for (int e = 0; e < E; ++e) {
+      const int c = s_cnt[e];
+      expert_off[e] = run;
+      if (c > 0) active[1 + na++] = e;
+      s_cnt[e] = run;
+      run += c;
+    }
+    expert_off[E] = run;
+    active[0] = na;
+  }
+  __syncthreads();
+  // Stable rank: earlier rows routed to the same expert.
+  for (int i = tid; i < R; i += kSortThreads) {
+    const int e = s_ids[i];
+    int rank = 0;
+    for (int j = 0; j < i; ++j) rank += (s_ids[j] == e);
+    const int pos = s_cnt[e] + rank;
+    row_map[pos] = (uint32_t)(i / top_k);
+    sorted_ids[pos] = (uint32_t)e;
+    inv_order[i] = (uint32_t)pos;
+  }
+}
+
+// One wave per token: top-k experts and renormalised softmax weights.
+__global__ __launch_bounds__(64) void moe_route_kernel(const float* logits, int E, int top_k, int32_t* ids,
+                                                       float* weights) {
+  const int t = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* row = logits + (size_t)t * E;
+  __shared__ float s_val[64];
+  __shared__ int s_id[64];
+  int taken_id = -1;
+  float taken_val = INFINITY;
+  for (int r = 0; r < top_k; ++r) {
+    // best below the previous winner in (value desc, id asc) order
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int e = lane; e < E; e += 64) {
+      const float v = row[e];
+      const bool below = (v < taken_val) || (v == taken_val && e > taken_id);
+      if (!below) continue;
+      if (v > bv || (v == bv && e < bi)) {
+        bv = v;
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (lane == 0) {
+      s_val[r] = bv;
+      s_id[r] = bi;
+    }
+    taken_val = bv;
+    taken_id = bi;
+  }
+  __syncthreads();
+  if (lane == 0) {
+    const float mx = s_val[0];
+    float sum = 0.f;
+    for (int r = 0; r < top_k; ++r) sum += __expf(s_val[r] - mx);
+    for (int r = 0; r < top_k; ++r) {
+      ids[(size_t)t * top_k + r] = s_id[r];
+      weights[(size_t)t * top_k + r] = __expf(s_val[r] - mx) / sum;
+    }
+  }
+}
+
+// out[t, :] = bf16( sum_j w[t,j] * y_sorted[inv_order[t*k + j], :] (+ shared[t, :]) )
+__global__ void moe_combine_kernel(const uint16_t* y_sorted, const uint32_t* inv_order, const float* w,
+                                   const uint16_t* shared, uint16_t* out, int T, int k, int H) {
+  const int t = blockIdx.y;
+  for (int h = blockIdx.x * blockDim.x + threadIdx.x; h < H; h += gridDim.x * blockDim.x) {
+    float acc = 0.f;
+    for (int j = 0; j < k; ++j) {
+      const uint32_t r = inv_order[(size_t)t * k + j];
+      acc += w[(size_t)t * k + j] * bf2f(y_sorted[(size_t)r * H + h]);
+    }
+    if (shared) acc = round_bf(acc) + bf2f(shared[(size_t)t * H + h]);
+    out[(size_t)t * H + h] = f2bf(acc);
+  }
+}
+
+}  // namespace mtp
+
+using namespace mtp;
+
+MTP_API size_t mtp_moe_workspace_bytes(int T, int top_k, int E) {
+  (void)T;
+  (void)top_k;
+  (void)E;
+  return 0;
+}
+
+MTP_API int mtp_moe_sort(const int32_t* topk_ids, int T, int top_k, int E, uint32_t* row_map, uint32_t* sorted_ids,
+                         uint32_t* inv_order, int32_t* expert_off, int32_t* active, void* ws, size_t ws_bytes,
+                         void* stream) {
+  (void)ws;
+  (void)ws_bytes;
+  const int R = T * top_k;
+  if (!topk_ids || !row_map || !sorted_ids || !inv_order || !expert_off || !active || T < 1 || top_k < 1 || E < 1) {
+    set_error("mtp_moe_sort: bad arguments");
+    return MTP_ERR_ARG;
+  }
+  if (R > kMaxSortRows || E > kMaxExperts) {
+    set_error("mtp_moe_sort: %d routed rows / %d experts exceed the single-workgroup sort (%d / %d)", R, E,
+              kMaxSortRows, kMaxExperts);
+    return MTP_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(kSortThreads), 0, (hipStream_t)stream, topk_ids, R, top_k, E,
+                     row_map, sorted_ids, inv_order, expert_off, active);
+  return launch_check("mtp_moe_sort");
+}
+
+MTP_API int mtp_moe_route(const float* logits, int T, int E, int top_k, int32_t* ids, float* weights, void* stream) {
+  if (!logits || !ids || !weights || T < 1 || E < 1 || top_k < 1 || top_k > 64 || top_k > E) {
+    set_error("mtp_moe_route: bad arguments (1 <= top_k <= min(64, E))");
+    return MTP_ERR_ARG;
+  }
+  hipLaunchKernelGGL(moe_route_kernel, dim3(T), dim3(64), 0, (hipStream_t)stream, logits, E, top_k, ids, weights);
+  return launch_check("mtp_moe_route");
+}
+
+MTP_API int mtp_moe_combine(const void* y_sorted, const uint32_t* inv_order, const float* route_w,
+                            const void* shared, void* out, int T, int top_k, int H, void* stream) {
+  if (!y_sorted || !inv_order || !route_w || !out || T < 1 || top_k < 1 || H < 1) {
+    set_error("mtp_moe_combine: bad arguments");
+    return MTP_ERR_ARG;
+  }
+  dim3 grid(cdiv(H, 256), T);
+  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t*)y_sorted,
+                     inv_order, route_w, (const uint16_t*)shared, (uint16_t*)out, T, top_k, H);
+  return launch_check("mtp_moe_combine");
+}

@@ -1,0 +1,60 @@
+"""Quantized linear layer in the reference's 4-bit affine format, on the GPU.
+
+Mirrors the attributes the reference's verify kernels read from MLX's
+``nn.QuantizedLinear`` (``mtplx/verify_qmv.py:19-34``, ``mtplx/nax_verify.py:754``):
+``weight`` uint32 ``[N, K/8]`` (held as int32), ``scales``/``biases`` bf16
+``[N, K/group_size]``, ``group_size``, ``bits``, ``mode`` and an optional
+``bias``. Calling the layer runs the HIP verify matmul; nothing runs on the CPU.
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+class QuantizedLinear:
+    def __init__(self, weight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                 group_size: int = 64, bits: int = 4, mode: str = "affine", bias: torch.Tensor | None = None):
+        if weight.dtype not in (torch.int32, torch.uint32):
+            raise TypeError("weight must be int32/uint32 packed words")
+        self.weight = weight.view(torch.int32) if weight.dtype == torch.uint32 else weight
+        self.scales = scales
+        self.biases = biases
+        self.group_size = int(group_size)
+        self.bits = int(bits)
+        self.mode = mode
+        self.bias = bias
+
+    @property
+    def in_features(self) -> int:
+        return int(self.weight.shape[-1]) * 32 // self.bits
+
+    @property
+    def out_features(self) -> int:
+        return int(self.weight.shape[-2])
+
+    def __contains__(self, name: str) -> bool:   # MLX-style `"bias" in module`
+        return getattr(self, name, None) is not None
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        from .verify_kernels import quantized_matmul
+
+        y = quantized_matmul(x, self.weight, self.scales, self.biases, group_size=self.group_size, bits=self.bits,
+                             mode=self.mode)
+        if self.bias is not None:
+            y = y + self.bias
+        return y
+
+    @classmethod
+    def random(cls, out_features: int, in_features: int, group_size: int = 64, *, generator=None,
+               device="cuda", scale_std: float = 0.02, bias_std: float = 0.01, experts: int | None = None):
+        """Synthetic layer (random init): nibbles U{0..15}, scales |N(0,scale_std)|,
+        biases N(0,bias_std), bf16 — the BASELINE weight recipe. ``experts``
+        adds a leading expert axis (MoE switch layers)."""
+        lead = () if experts is None else (experts,)
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, lead + (out_features, in_features // 8), dtype=torch.int32,
+                          device=device, generator=generator)
+        g = in_features // group_size
+        s = (torch.randn(lead + (out_features, g), device=device, generator=generator) * scale_std).abs()
+        b = torch.randn(lead + (out_features, g), device=device, generator=generator) * bias_std
+        return cls(w, s.to(torch.bfloat16), b.to(torch.bfloat16), group_size=group_size)

@@ -1,0 +1,258 @@
+"""One speculative verify step of a 4-bit decoder on gfx950 (random init).
+
+This is the forward the reference runs on ``[primary, d1..dK]``
+(``mtplx/generation.py:15027-15066`` → ``MTPLXRuntime.forward_ar``,
+``mtplx/runtime.py:161``) followed by the accept/reject of
+``mtplx/generation.py:15560-15790``, for a dense GQA decoder (the 27B shape:
+64 layers, hidden 5120, SwiGLU 17408, 40/8 heads of 128, RMSNorm, RoPE 1e6,
+vocab 151936, every linear 4-bit affine g64, bf16 KV cache) or its MoE variant.
+
+Per layer the kernels are:
+  1. ``mtp_qmv_affine4_rmsnorm_in``  input RMSNorm fused into the q|k|v matmul
+  2. ``mtp_rope_qkv_to_cache``       RoPE at per-request offsets, K/V into the cache
+  3. ``mtp_ragged_gqa_attn_rows``    ragged GQA attention (split-KV + merge)
+  4. ``mtp_qmv_affine4_residual``    o_proj + residual add
+  5. ``mtp_qmv_affine4_rmsnorm_dual`` post-attention RMSNorm + gate/up + SwiGLU
+  6. ``mtp_qmv_affine4_residual``    down_proj + residual add
+  (MoE layers replace 5-6 with route → expert sort → gathered SwiGLU →
+  gathered down → unsort/combine (+ shared expert).)
+then the final RMSNorm fused into the lm_head (fp32 logits) and
+``mtp_spec_accept`` on the verify rows.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _lib
+from .moe_sorted_gather import expert_sort, moe_combine
+from .quant import QuantizedLinear
+from .sampling import SamplerConfig, spec_accept
+
+
+@dataclass
+class DecoderConfig:
+    layers: int = 64
+    hidden: int = 5120
+    ffn: int = 17408
+    n_heads: int = 40
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    vocab: int = 151936
+    rope_theta: float = 1.0e6
+    rms_eps: float = 1.0e-6
+    group_size: int = 64
+    # MoE variant (n_experts > 0): routed experts top-k + one shared expert.
+    n_experts: int = 0
+    top_k: int = 0
+    expert_ffn: int = 0
+    shared_ffn: int = 0
+    router_zipf_s: float = 1.1
+
+    @property
+    def qkv_out(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+
+DENSE_27B = DecoderConfig()
+MOE_125B = DecoderConfig(layers=48, hidden=4096, ffn=0, n_heads=32, n_kv_heads=4, n_experts=256, top_k=8,
+                         expert_ffn=1536, shared_ffn=1536)
+
+
+def _norm_weight(n: int, gen, device) -> torch.Tensor:
+    return (1.0 + 0.1 * torch.randn(n, generator=gen, device=device)).to(torch.bfloat16)
+
+
+@dataclass
+class Layer:
+    in_norm: torch.Tensor
+    qkv: QuantizedLinear
+    o: QuantizedLinear
+    post_norm: torch.Tensor
+    gate: QuantizedLinear | None = None
+    up: QuantizedLinear | None = None
+    down: QuantizedLinear | None = None
+    # MoE
+    router_logits: torch.Tensor | None = None   # synthetic fp32 [T, E] (Zipf-skewed), per layer
+    expert_gate_up: QuantizedLinear | None = None   # [E, 2F, K/8] fused [gate | up]
+    expert_down: QuantizedLinear | None = None      # [E, H, F/8]
+    shared_gate: QuantizedLinear | None = None
+    shared_up: QuantizedLinear | None = None
+    shared_down: QuantizedLinear | None = None
+
+
+class VerifyModel:
+    """Random-init weights of ``cfg`` resident in HBM plus a ragged KV cache."""
+
+    def __init__(self, cfg: DecoderConfig, *, device="cuda", seed: int = 0):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        gen = torch.Generator(device=self.device).manual_seed(seed)
+        self.gen = gen
+        c = cfg
+        gs = c.group_size
+        self.embed = QuantizedLinear.random(c.vocab, c.hidden, gs, generator=gen, device=device)
+        self.layers: list[Layer] = []
+        for _ in range(c.layers):
+            L = Layer(in_norm=_norm_weight(c.hidden, gen, device),
+                      qkv=QuantizedLinear.random(c.qkv_out, c.hidden, gs, generator=gen, device=device),
+                      o=QuantizedLinear.random(c.hidden, c.n_heads * c.head_dim, gs, generator=gen, device=device),
+                      post_norm=_norm_weight(c.hidden, gen, device))
+            if c.n_experts:
+                L.expert_gate_up = QuantizedLinear.random(2 * c.expert_ffn, c.hidden, gs, generator=gen,
+                                                          device=device, experts=c.n_experts)
+                L.expert_down = QuantizedLinear.random(c.hidden, c.expert_ffn, gs, generator=gen, device=device,
+                                                       experts=c.n_experts)
+                L.shared_gate = QuantizedLinear.random(c.shared_ffn, c.hidden, gs, generator=gen, device=device)
+                L.shared_up = QuantizedLinear.random(c.shared_ffn, c.hidden, gs, generator=gen, device=device)
+                L.shared_down = QuantizedLinear.random(c.hidden, c.shared_ffn, gs, generator=gen, device=device)
+            else:
+                L.gate = QuantizedLinear.random(c.ffn, c.hidden, gs, generator=gen, device=device)
+                L.up = QuantizedLinear.random(c.ffn, c.hidden, gs, generator=gen, device=device)
+                L.down = QuantizedLinear.random(c.hidden, c.ffn, gs, generator=gen, device=device)
+            self.layers.append(L)
+        self.final_norm = _norm_weight(c.hidden, gen, device)
+        self.lm_head = QuantizedLinear.random(c.vocab, c.hidden, gs, generator=gen, device=device)
+        self.k_cache: list[torch.Tensor] = []
+        self.v_cache: list[torch.Tensor] = []
+        self.cap = 0
+
+    # -- cache ----------------------------------------------------------------
+    def allocate_cache(self, batch: int, capacity: int, *, fill_random: bool = True) -> None:
+        c = self.cfg
+        cap = ((capacity + 255) // 256) * 256
+        self.k_cache, self.v_cache = [], []
+        for _ in range(c.layers):
+            shape = (batch, c.n_kv_heads, cap, c.head_dim)
+            if fill_random:
+                k = torch.randn(shape, generator=self.gen, device=self.device).to(torch.bfloat16)
+                v = torch.randn(shape, generator=self.gen, device=self.device).to(torch.bfloat16)
+            else:
+                k = torch.zeros(shape, dtype=torch.bfloat16, device=self.device)
+                v = torch.zeros_like(k)
+            self.k_cache.append(k)
+            self.v_cache.append(v)
+        self.cap = cap
+        self.batch = batch
+
+    def synthetic_router_logits(self, tokens: int) -> None:
+        """Per-layer router logits skewed Zipf(s) over experts: logit_e = -s*log(rank_e)
+        with a per-layer random expert ranking plus N(0, 0.5) noise per token."""
+        c = self.cfg
+        for L in self.layers:
+            perm = torch.randperm(c.n_experts, generator=self.gen, device=self.device)
+            base = -c.router_zipf_s * torch.log(torch.arange(1, c.n_experts + 1, device=self.device,
+                                                             dtype=torch.float32))
+            lg = base[perm][None, :] + 0.5 * torch.randn((tokens, c.n_experts), generator=self.gen,
+                                                         device=self.device)
+            L.router_logits = lg.contiguous()
+
+    # -- forward --------------------------------------------------------------
+    def verify_logits(self, tokens: torch.Tensor, q_start: torch.Tensor, q_lens: torch.Tensor | None = None,
+                      *, logits_out: torch.Tensor | None = None) -> torch.Tensor:
+        """``tokens`` int32 ``[B, L]`` (GPU), ``q_start`` int32 ``[B]`` (GPU):
+        writes K/V of the L rows at ``q_start[b] + i`` and returns fp32 logits ``[B*L, V]``."""
+        c = self.cfg
+        B, Lq = (int(s) for s in tokens.shape)
+        M = B * Lq
+        dev = self.device
+        st = _lib.stream_handle(dev)
+        gs = c.group_size
+        H = c.hidden
+        call = _lib.call
+        eps = ctypes.c_float(c.rms_eps)
+        status = torch.zeros(1, dtype=torch.int32, device=dev)
+        h = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+        tok = tokens.reshape(-1).to(torch.int32).contiguous()
+        call("mtp_embed_affine4", tok.data_ptr(), self.embed.weight.data_ptr(), self.embed.scales.data_ptr(),
+             self.embed.biases.data_ptr(), h.data_ptr(), M, H, c.vocab, gs, status.data_ptr(), st)
+        qkv = torch.empty((M, c.qkv_out), dtype=torch.bfloat16, device=dev)
+        qh = torch.empty((B, c.n_heads, Lq, c.head_dim), dtype=torch.bfloat16, device=dev)
+        attn = torch.empty((M, c.n_heads * c.head_dim), dtype=torch.bfloat16, device=dev)
+        ffn = c.expert_ffn if c.n_experts else c.ffn
+        act = torch.empty((M, ffn), dtype=torch.bfloat16, device=dev)
+        nb = _lib.query("mtp_attn_workspace_bytes", B, c.n_kv_heads, self.cap, 0)
+        aws = _lib.WORKSPACES.get(nb, "attn", dev)
+        scale = 1.0 / math.sqrt(c.head_dim)
+        ql = None if q_lens is None else q_lens.to(torch.int32).contiguous()
+        for li, L in enumerate(self.layers):
+            call("mtp_qmv_affine4_rmsnorm_in", h.data_ptr(), L.in_norm.data_ptr(), eps, L.qkv.weight.data_ptr(),
+                 L.qkv.scales.data_ptr(), L.qkv.biases.data_ptr(), qkv.data_ptr(), M, c.qkv_out, H, gs, None, 0, st)
+            call("mtp_rope_qkv_to_cache", qkv.data_ptr(), q_start.data_ptr(), _lib.ptr(ql), qh.data_ptr(),
+                 self.k_cache[li].data_ptr(), self.v_cache[li].data_ptr(), B, Lq, c.n_heads, c.n_kv_heads,
+                 c.head_dim, self.cap, ctypes.c_float(c.rope_theta), status.data_ptr(), st)
+            call("mtp_ragged_gqa_attn_rows", qh.data_ptr(), self.k_cache[li].data_ptr(),
+                 self.v_cache[li].data_ptr(), q_start.data_ptr(), _lib.ptr(ql), attn.data_ptr(), B, c.n_heads,
+                 c.n_kv_heads, Lq, c.head_dim, self.cap, ctypes.c_float(scale), 0, aws.data_ptr(), aws.numel(), st)
+            call("mtp_qmv_affine4_residual", attn.data_ptr(), L.o.weight.data_ptr(), L.o.scales.data_ptr(),
+                 L.o.biases.data_ptr(), h.data_ptr(), h.data_ptr(), M, H, c.n_heads * c.head_dim, gs, None, 0, st)
+            if c.n_experts:
+                self._moe_block(L, h, M, st)
+            else:
+                call("mtp_qmv_affine4_rmsnorm_dual", h.data_ptr(), L.post_norm.data_ptr(), eps,
+                     L.gate.weight.data_ptr(), L.gate.scales.data_ptr(), L.gate.biases.data_ptr(),
+                     L.up.weight.data_ptr(), L.up.scales.data_ptr(), L.up.biases.data_ptr(), act.data_ptr(), M,
+                     c.ffn, H, gs, None, 0, st)
+                call("mtp_qmv_affine4_residual", act.data_ptr(), L.down.weight.data_ptr(), L.down.scales.data_ptr(),
+                     L.down.biases.data_ptr(), h.data_ptr(), h.data_ptr(), M, H, c.ffn, gs, None, 0, st)
+        logits = logits_out if logits_out is not None else torch.empty((M, c.vocab), dtype=torch.float32, device=dev)
+        call("mtp_qmv_affine4_rmsnorm_f32", h.data_ptr(), self.final_norm.data_ptr(), eps,
+             self.lm_head.weight.data_ptr(), self.lm_head.scales.data_ptr(), self.lm_head.biases.data_ptr(),
+             logits.data_ptr(), M, c.vocab, H, gs, None, 0, st)
+        self._status = status
+        return logits
+
+    def _moe_block(self, L: Layer, h: torch.Tensor, M: int, st: int) -> None:
+        """Routed experts (sorted chain, ``mtplx/models/qwen4_exp.py:1544-1577``) + shared expert."""
+        c = self.cfg
+        call = _lib.call
+        gs = c.group_size
+        eps = ctypes.c_float(c.rms_eps)
+        dev = h.device
+        H = c.hidden
+        xn = torch.empty_like(h)
+        call("mtp_rmsnorm", h.data_ptr(), L.post_norm.data_ptr(), xn.data_ptr(), M, H, c.rms_eps, st)
+        ids = torch.empty((M, c.top_k), dtype=torch.int32, device=dev)
+        wts = torch.empty((M, c.top_k), dtype=torch.float32, device=dev)
+        call("mtp_moe_route", L.router_logits[:M].data_ptr(), M, c.n_experts, c.top_k, ids.data_ptr(),
+             wts.data_ptr(), st)
+        es = expert_sort(ids, c.n_experts)
+        R = M * c.top_k
+        F = c.expert_ffn
+        hsorted = torch.empty((R, F), dtype=torch.bfloat16, device=dev)
+        gu = L.expert_gate_up
+        kw = int(gu.weight.shape[-1])
+        gk = int(gu.scales.shape[-1])
+        call("mtp_gather_qmv_affine4", xn.data_ptr(), None, es.row_map.data_ptr(), es.expert_off.data_ptr(),
+             es.active.data_ptr(), gu.weight.data_ptr(), gu.scales.data_ptr(), gu.biases.data_ptr(),
+             gu.weight.reshape(-1, kw)[F:].data_ptr(), gu.scales.reshape(-1, gk)[F:].data_ptr(),
+             gu.biases.reshape(-1, gk)[F:].data_ptr(), hsorted.data_ptr(), M, c.n_experts, F, H, gs, 0, 3, 2 * F,
+             None, 0, st)
+        ysorted = torch.empty((R, H), dtype=torch.bfloat16, device=dev)
+        dn = L.expert_down
+        call("mtp_gather_qmv_affine4", hsorted.data_ptr(), None, None, es.expert_off.data_ptr(),
+             es.active.data_ptr(), dn.weight.data_ptr(), dn.scales.data_ptr(), dn.biases.data_ptr(), None, None,
+             None, ysorted.data_ptr(), M, c.n_experts, H, F, gs, 0, 0, H, None, 0, st)
+        # shared expert on the normalised rows, then h += routed + shared
+        sh_act = torch.empty((M, c.shared_ffn), dtype=torch.bfloat16, device=dev)
+        call("mtp_qmv_affine4_dual", xn.data_ptr(), L.shared_gate.weight.data_ptr(), L.shared_gate.scales.data_ptr(),
+             L.shared_gate.biases.data_ptr(), L.shared_up.weight.data_ptr(), L.shared_up.scales.data_ptr(),
+             L.shared_up.biases.data_ptr(), sh_act.data_ptr(), None, M, c.shared_ffn, H, gs, 1, None, 0, st)
+        shared = torch.empty_like(h)
+        call("mtp_qmv_affine4_residual", sh_act.data_ptr(), L.shared_down.weight.data_ptr(),
+             L.shared_down.scales.data_ptr(), L.shared_down.biases.data_ptr(), h.data_ptr(), shared.data_ptr(), M, H,
+             c.shared_ffn, gs, None, 0, st)
+        out = moe_combine(ysorted, es, wts, shared)
+        h.copy_(out)
+
+    def verify_step(self, tokens: torch.Tensor, q_start: torch.Tensor, draft_logits: torch.Tensor,
+                    uniforms: torch.Tensor, sampler: SamplerConfig = SamplerConfig()):
+        """Forward the ``B x (K+1)`` verify rows, then accept/reject against the drafts
+        (``tokens[:, 1:]`` are the draft ids). Returns the device-side accept result."""
+        B, L = (int(s) for s in tokens.shape)
+        logits = self.verify_logits(tokens, q_start)
+        return spec_accept(logits.reshape(B, L, -1), draft_logits, tokens[:, 1:].contiguous(), uniforms, sampler)

@@ -1,0 +1,93 @@
+"""Float64 restatement of one verify forward of the synthetic 4-bit decoder.
+
+Follows the mlx-lm decoder layer the reference verifies with
+(``mtplx/runtime.py:161`` forward_ar → per layer: input RMSNorm, q|k|v, RoPE
+at the cache offset, ``update_and_fetch`` then SDPA with the ragged mask,
+o_proj + residual, post-attention RMSNorm, SwiGLU MLP + residual; final norm
+and lm_head). Values are rounded to bf16 wherever the GPU path stores a bf16
+tensor, so the comparison isolates arithmetic error, not storage format.
+
+Parity pins (tests/test_oracle_model.py): a zero-layer model reduces to
+norm + lm_head of the embedding; RoPE at position 0 is the identity and
+preserves norms; the attention and qmv pieces are pinned in their own files.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .attention import ragged_gqa_attention
+from .bf16 import round_to_bf16
+from .moe import moe_forward, silu
+from .qmv import dequantize_affine4, qmm_affine4
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = np.asarray(x, dtype=np.float64)
+    return x / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps) * np.asarray(w, dtype=np.float64)
+
+
+def rope_rotate_half(x: np.ndarray, pos: np.ndarray, base: float) -> np.ndarray:
+    """Non-interleaved RoPE: pairs (j, j + D/2), theta_j = pos * base^(-2j/D).
+    ``x`` [..., n, D] with ``pos`` broadcastable to [..., n]."""
+    D = x.shape[-1]
+    half = D // 2
+    inv = base ** (-(2.0 * np.arange(half)) / D)
+    ang = np.asarray(pos, dtype=np.float64)[..., None] * inv
+    c, s = np.cos(ang), np.sin(ang)
+    x1, x2 = x[..., :half], x[..., half:]
+    return np.concatenate([x1 * c - x2 * s, x1 * s + x2 * c], axis=-1)
+
+
+def verify_forward(params: dict, cfg, tokens: np.ndarray, q_start: np.ndarray, k_cache: list, v_cache: list,
+                   router: list | None = None) -> np.ndarray:
+    """Logits [B*L, V] (float64 of bf16 values). ``params`` holds numpy copies of
+    the GPU model (bf16 values as float64, weight triples for 4-bit layers).
+    ``k_cache``/``v_cache`` are per-layer float64 arrays [B, Hkv, cap, D],
+    updated in place at ``q_start[b] + i``."""
+    B, L = tokens.shape
+    M = B * L
+    gs = cfg.group_size
+    H, D, Hq, Hkv = cfg.hidden, cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    emb = params["embed"]
+    h = round_to_bf16(np.stack([dequantize_affine4(emb[0][t:t + 1], emb[1][t:t + 1], emb[2][t:t + 1], gs)[0]
+                                for t in tokens.reshape(-1)]))
+    pos = (np.asarray(q_start)[:, None] + np.arange(L)[None, :])  # [B, L]
+    for li, lay in enumerate(params["layers"]):
+        xn = round_to_bf16(rmsnorm(h, lay["in_norm"], cfg.rms_eps))
+        qkv = round_to_bf16(qmm_affine4(xn, *lay["qkv"], gs)).reshape(B, L, Hq + 2 * Hkv, D)
+        q = round_to_bf16(rope_rotate_half(qkv[:, :, :Hq].transpose(0, 2, 1, 3), pos[:, None, :], cfg.rope_theta))
+        k = round_to_bf16(rope_rotate_half(qkv[:, :, Hq:Hq + Hkv].transpose(0, 2, 1, 3), pos[:, None, :],
+                                           cfg.rope_theta))
+        v = qkv[:, :, Hq + Hkv:].transpose(0, 2, 1, 3)
+        for b in range(B):
+            k_cache[li][b, :, q_start[b]:q_start[b] + L] = k[b]
+            v_cache[li][b, :, q_start[b]:q_start[b] + L] = v[b]
+        att = round_to_bf16(ragged_gqa_attention(q, k_cache[li], v_cache[li], q_start))   # [B, Hq, L, D]
+        att = att.transpose(0, 2, 1, 3).reshape(M, Hq * D)
+        h = round_to_bf16(round_to_bf16(qmm_affine4(att, *lay["o"], gs)) + h)
+        xn = round_to_bf16(rmsnorm(h, lay["post_norm"], cfg.rms_eps))
+        if cfg.n_experts:
+            ids, wts = router[li]
+            routed = moe_forward(xn, ids, wts, lay["expert_gate_up"], lay["expert_down"], gs)
+            sg = round_to_bf16(qmm_affine4(xn, *lay["shared_gate"], gs))
+            su = round_to_bf16(qmm_affine4(xn, *lay["shared_up"], gs))
+            sa = round_to_bf16(round_to_bf16(silu(sg)) * su)
+            shared = round_to_bf16(round_to_bf16(qmm_affine4(sa, *lay["shared_down"], gs)) + h)
+            h = round_to_bf16(round_to_bf16(routed) + shared)
+        else:
+            g = round_to_bf16(qmm_affine4(xn, *lay["gate"], gs))
+            u = round_to_bf16(qmm_affine4(xn, *lay["up"], gs))
+            a = round_to_bf16(round_to_bf16(silu(g)) * u)
+            h = round_to_bf16(round_to_bf16(qmm_affine4(a, *lay["down"], gs)) + h)
+    xn = round_to_bf16(rmsnorm(h, params["final_norm"], cfg.rms_eps))
+    return round_to_bf16(qmm_affine4(xn, *params["lm_head"], gs))
+
+
+def route_topk(logits: np.ndarray, top_k: int):
+    """Top-k experts (value desc, id asc) and softmax weights over the chosen k."""
+    logits = np.asarray(logits, dtype=np.float64)
+    ids = np.stack([np.lexsort((np.arange(r.size), -r))[:top_k] for r in logits])
+    sel = np.take_along_axis(logits, ids, axis=1)
+    e = np.exp(sel - sel[:, :1])
+    return ids, e / e.sum(axis=1, keepdims=True)

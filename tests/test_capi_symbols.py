@@ -1,0 +1,53 @@
+"""CPU checks of the C ABI: the library loads and exports exactly what the
+header declares; size queries answer without a GPU."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mtplx_amd.h")
+LIB = os.path.join(ROOT, "mtplx_amd", "libmtplx_amd.so")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mtp_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail("libmtplx_amd.so is not built (run python -m mtplx_amd.build)")
+    return ctypes.CDLL(LIB)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = _declared()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_binding_matches_header():
+    from mtplx_amd._lib import SIGNATURES
+    assert sorted(SIGNATURES) == _declared()
+
+
+def test_size_queries_without_gpu(lib):
+    lib.mtp_sampler_workspace_bytes.restype = ctypes.c_size_t
+    lib.mtp_attn_workspace_bytes.restype = ctypes.c_size_t
+    lib.mtp_qmv_workspace_bytes.restype = ctypes.c_size_t
+    assert lib.mtp_sampler_workspace_bytes(7, 151936) == 7 * 38 * 536
+    assert lib.mtp_attn_workspace_bytes(8, 8, 32768, 0) == 8 * 8 * 64 * (32 * 128 + 64) * 4
+    assert lib.mtp_qmv_workspace_bytes(4, 17408, 5120, 0) == 0
+
+
+def test_error_path_reports_message(lib):
+    lib.mtp_last_error.restype = ctypes.c_char_p
+    rc = lib.mtp_qmv_affine4(None, None, None, None, None, 4, 8, 100, 64, None, 0, None)
+    assert rc == -1
+    assert b"K=" in lib.mtp_last_error() or b"M=" in lib.mtp_last_error()

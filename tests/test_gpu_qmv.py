@@ -1,0 +1,173 @@
+"""GPU parity: 4-bit affine verify matmul (all entry points) vs the float64 oracle.
+
+Bar (north star): bf16 outputs within rtol 1e-2 / atol 1e-2 of the oracle.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits, round_to_bf16
+from oracle.moe import silu
+from oracle.qmv import make_affine4_weights, qmm_affine4
+from tests.gpu_util import assert_close, bf16_values, bits, from_bits, randn_bf16, u32
+
+pytestmark = pytest.mark.gpu
+
+
+def _layer(rng, n, k, gs=64):
+    w, s, b = make_affine4_weights(rng, n, k, gs)
+    return (w, s, b), (u32(w), from_bits(s), from_bits(b))
+
+
+def _ws(lib, m, n, k, dual=0):
+    nb = lib.mtp_qmv_workspace_bytes(m, n, k, dual)
+    return torch.zeros(max(nb, 256), dtype=torch.uint8, device="cuda"), nb
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def test_mfma_32x32x16_output_layout(gpu):
+    out = torch.zeros(64 * 16, dtype=torch.float32, device="cuda")
+    from mtplx_amd import _lib
+    _lib.call("mtp_probe_mfma_layout", out.data_ptr(), _stream())
+    got = out.cpu().numpy().reshape(64, 16)
+    for lane in range(64):
+        for r in range(16):
+            i = 8 * (r // 4) + 4 * (lane // 32) + r % 4
+            j = lane % 32
+            want = float(i + 1) if i % 16 == j % 16 else 0.0
+            assert got[lane, r] == want, (lane, r, got[lane, r], want)
+
+
+SHAPES = [  # (M, N, K, gs)
+    (4, 17408, 5120, 64),     # BASELINE cfg1
+    (1, 1032, 2560, 64), (2, 2560, 6144, 64), (4, 1032, 2560, 128),
+    (6, 136, 1024, 64), (8, 256, 768, 128), (3, 100, 768, 64),
+    (16, 512, 1024, 64), (24, 300, 1280, 64), (32, 1024, 2048, 128), (5, 7168, 5120, 64),
+]
+
+
+@pytest.mark.parametrize("m,n,k,gs", SHAPES)
+def test_qmv_matches_oracle(gpu, m, n, k, gs):
+    from mtplx_amd import _lib
+    rng = np.random.default_rng(1000 + m * 7 + n)
+    (w, s, b), (tw, ts, tb) = _layer(rng, n, k, gs)
+    x = randn_bf16(rng, (m, k))
+    y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")   # poisoned
+    ws, nb = _ws(lib=_lib.load(), m=m, n=n, k=k)
+    _lib.call("mtp_qmv_affine4", x.data_ptr(), tw.data_ptr(), ts.data_ptr(), tb.data_ptr(), y.data_ptr(),
+              m, n, k, gs, ws.data_ptr(), nb, _stream())
+    torch.cuda.synchronize()
+    want = qmm_affine4(bits(x), w, s, b, gs)
+    got = bf16_values(y)
+    assert np.isfinite(got).all(), "unwritten (NaN-poisoned) outputs"
+    assert_close(got, want, what=f"qmv M={m} N={n} K={k}")
+    rel = np.abs(got - want).max() / (np.abs(want).max() + 1e-9)
+    assert rel < 4e-3, rel
+    # deterministic: a second launch is bitwise identical
+    y2 = torch.empty_like(y)
+    _lib.call("mtp_qmv_affine4", x.data_ptr(), tw.data_ptr(), ts.data_ptr(), tb.data_ptr(), y2.data_ptr(),
+              m, n, k, gs, ws.data_ptr(), nb, _stream())
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+
+
+def test_qmv_closed_form_zero_nibbles(gpu):
+    from mtplx_amd import _lib
+    rng = np.random.default_rng(5)
+    m, n, k = 4, 256, 1024
+    w = np.zeros((n, k // 8), np.uint32)
+    s = f32_to_bf16_bits(np.abs(rng.normal(0, 0.02, (n, k // 64))).astype(np.float32))
+    b = f32_to_bf16_bits(rng.normal(0, 0.01, (n, k // 64)).astype(np.float32))
+    x = randn_bf16(rng, (m, k))
+    y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    ws, nb = _ws(_lib.load(), m, n, k)
+    tw, ts, tb = u32(w), from_bits(s), from_bits(b)   # keep the buffers alive across the launch
+    _lib.call("mtp_qmv_affine4", x.data_ptr(), tw.data_ptr(), ts.data_ptr(), tb.data_ptr(),
+              y.data_ptr(), m, n, k, 64, ws.data_ptr(), nb, _stream())
+    xv = bf16_values(x)
+    want = xv.reshape(m, -1, 64).sum(axis=2) @ bf16_bits_to_f32(b).astype(np.float64).T
+    assert_close(bf16_values(y), want, what="q=0 closed form")
+
+
+def test_residual_dual_swiglu_and_rmsnorm_variants(gpu):
+    from mtplx_amd import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(11)
+    m, n, k = 4, 1536, 2048
+    (w0, s0, b0), (tw0, ts0, tb0) = _layer(rng, n, k)
+    (w1, s1, b1), (tw1, ts1, tb1) = _layer(rng, n, k)
+    x = randn_bf16(rng, (m, k))
+    xb = bits(x)
+    st = _stream()
+    ws = torch.zeros(1 << 24, dtype=torch.uint8, device="cuda")
+    W = ws.numel()
+    y0 = qmm_affine4(xb, w0, s0, b0, 64)
+    y1 = qmm_affine4(xb, w1, s1, b1, 64)
+
+    # residual
+    r = randn_bf16(rng, (m, n))
+    out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    _lib.call("mtp_qmv_affine4_residual", x.data_ptr(), tw0.data_ptr(), ts0.data_ptr(), tb0.data_ptr(), r.data_ptr(),
+              out.data_ptr(), m, n, k, 64, ws.data_ptr(), W, st)
+    assert_close(bf16_values(out), round_to_bf16(y0) + bf16_values(r), what="residual")
+
+    # dual (two outputs) and dual swiglu
+    o0 = torch.empty((m, n), dtype=torch.bfloat16, device="cuda"); o1 = torch.empty_like(o0)
+    _lib.call("mtp_qmv_affine4_dual", x.data_ptr(), tw0.data_ptr(), ts0.data_ptr(), tb0.data_ptr(), tw1.data_ptr(),
+              ts1.data_ptr(), tb1.data_ptr(), o0.data_ptr(), o1.data_ptr(), m, n, k, 64, 0, ws.data_ptr(), W, st)
+    assert_close(bf16_values(o0), y0, what="dual y0")
+    assert_close(bf16_values(o1), y1, what="dual y1")
+    h = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    _lib.call("mtp_qmv_affine4_dual", x.data_ptr(), tw0.data_ptr(), ts0.data_ptr(), tb0.data_ptr(), tw1.data_ptr(),
+              ts1.data_ptr(), tb1.data_ptr(), h.data_ptr(), None, m, n, k, 64, 1, ws.data_ptr(), W, st)
+    assert_close(bf16_values(h), silu(y0) * y1, what="dual swiglu")
+
+    # swiglu input -> down projection (+ residual)
+    (wd, sd, bd), (twd, tsd, tbd) = _layer(rng, k, n)
+    g = randn_bf16(rng, (m, n)); u = randn_bf16(rng, (m, n))
+    act = round_to_bf16(round_to_bf16(silu(bf16_values(g))) * bf16_values(u))
+    want = qmm_affine4(f32_to_bf16_bits(act.astype(np.float32)), wd, sd, bd, 64)
+    yd = torch.empty((m, k), dtype=torch.bfloat16, device="cuda")
+    _lib.call("mtp_qmv_affine4_swiglu_in", g.data_ptr(), u.data_ptr(), twd.data_ptr(), tsd.data_ptr(), tbd.data_ptr(),
+              None, yd.data_ptr(), m, k, n, 64, ws.data_ptr(), W, st)
+    assert_close(bf16_values(yd), want, what="swiglu-in")
+
+    # rmsnorm input (bf16 and fp32 outputs) and rmsnorm + dual swiglu
+    nw = randn_bf16(rng, (k,), 0.1)
+    xv = bf16_values(x)
+    xn = xv / np.sqrt((xv ** 2).mean(axis=1, keepdims=True) + 1e-6) * bf16_values(nw)[None]
+    xnb = f32_to_bf16_bits(xn.astype(np.float32))
+    yn = qmm_affine4(xnb, w0, s0, b0, 64)
+    o = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    _lib.call("mtp_qmv_affine4_rmsnorm_in", x.data_ptr(), nw.data_ptr(), ctypes.c_float(1e-6), tw0.data_ptr(),
+              ts0.data_ptr(), tb0.data_ptr(), o.data_ptr(), m, n, k, 64, ws.data_ptr(), W, st)
+    assert_close(bf16_values(o), yn, what="rmsnorm-in")
+    of = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    _lib.call("mtp_qmv_affine4_rmsnorm_f32", x.data_ptr(), nw.data_ptr(), ctypes.c_float(1e-6), tw0.data_ptr(),
+              ts0.data_ptr(), tb0.data_ptr(), of.data_ptr(), m, n, k, 64, ws.data_ptr(), W, st)
+    ofn = of.cpu().numpy().astype(np.float64)
+    assert_close(ofn, yn, what="rmsnorm-f32")
+    assert np.array_equal(round_to_bf16(ofn), ofn), "fp32 logits must carry bf16 values"
+    hd = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    _lib.call("mtp_qmv_affine4_rmsnorm_dual", x.data_ptr(), nw.data_ptr(), ctypes.c_float(1e-6), tw0.data_ptr(),
+              ts0.data_ptr(), tb0.data_ptr(), tw1.data_ptr(), ts1.data_ptr(), tb1.data_ptr(), hd.data_ptr(),
+              m, n, k, 64, ws.data_ptr(), W, st)
+    yn1 = qmm_affine4(xnb, w1, s1, b1, 64)
+    assert_close(bf16_values(hd), silu(yn) * yn1, what="rmsnorm-dual-swiglu")
+
+
+def test_bad_arguments_raise(gpu):
+    from mtplx_amd import _lib
+    x = torch.zeros((4, 100), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(_lib.MtpError):
+        _lib.call("mtp_qmv_affine4", x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
+                  4, 8, 100, 64, None, 0, _stream())
+    with pytest.raises(_lib.MtpError):   # group size 32 is not on the GPU path
+        _lib.call("mtp_qmv_affine4", x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
+                  4, 8, 256, 32, None, 0, _stream())
