@@ -51,7 +51,8 @@ def roofline_gate_up(model, M: int, reps: int = 5) -> dict:
     eps = ctypes.c_float(c.rms_eps)
 
     def launch(L):
-        _lib.call("mtp_qmv_affine4_rmsnorm_dual", x.data_ptr(), L.post_norm.data_ptr(), eps, L.gate.weight.data_ptr(),
+        _lib.call("mtp_qmv_affine4_rmsnorm_dual", x.data_ptr(), L.post_norm.data_ptr(), None, eps,
+                  L.gate.weight.data_ptr(),
                   L.gate.scales.data_ptr(), L.gate.biases.data_ptr(), L.up.weight.data_ptr(), L.up.scales.data_ptr(),
                   L.up.biases.data_ptr(), y.data_ptr(), M, c.ffn, c.hidden, c.group_size, None, 0, st)
 
@@ -178,6 +179,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="launch kernel by kernel instead of one HIP graph per step")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the hot path is single-GPU); --gpus {args.gpus} is not supported",
@@ -188,7 +190,7 @@ def main() -> int:
 
     from mtplx_amd import _lib
     from mtplx_amd.sampling import SamplerConfig
-    from mtplx_amd.verify_step import DENSE_27B, VerifyModel
+    from mtplx_amd.verify_step import DENSE_27B, CapturedVerifyStep, VerifyModel
 
     _lib.load()
     dev = torch.device("cuda", 0)
@@ -205,17 +207,26 @@ def main() -> int:
     uniforms = torch.rand((B, K + 1), device=dev, dtype=torch.float64, generator=gen)
     sampler = SamplerConfig(0.6, 0.95, 20)
 
-    for _ in range(args.warmup):
-        model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(args.steps):
-        res = model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)
-    e1.record()
-    torch.cuda.synchronize()
+    if args.eager:
+        def step():
+            return model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)
+        stream = torch.cuda.current_stream()
+    else:
+        cap = CapturedVerifyStep(model, tokens, q_start, draft_logits, uniforms, sampler)
+        step = cap.replay
+        stream = cap.stream
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            res = step()
+        e1.record(stream)
+        torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / args.steps
     assert int(res.status.max().item()) == 0, "non-finite logits in the verify step"
@@ -244,7 +255,8 @@ def main() -> int:
                                f"{args.ctx}-token context, 4 verify rows + accept/reject",
                    "layers": cfg.layers, "hidden": cfg.hidden, "ffn": cfg.ffn, "heads": f"{cfg.n_heads}/{cfg.n_kv_heads}",
                    "head_dim": cfg.head_dim, "vocab": cfg.vocab, "group_size": cfg.group_size, "batch": B,
-                   "verify_rows": L, "context": args.ctx, "wall_s_timed": round(wall, 3)},
+                   "verify_rows": L, "context": args.ctx, "wall_s_timed": round(wall, 3),
+                   "launch": "eager" if args.eager else "hip_graph"},
         "roofline": roof,
         "cpu_baseline": cpu,
     }

@@ -49,10 +49,12 @@ int mtp_qmv_affine4(const void* x, const void* w, const void* scales, const void
 
 /* y = bf16(bf16(x @ W^T) + resid) — the residual add that follows o_proj and
  * down_proj in the verify forward (mlx-lm decoder layer `h + r`).
- * resid may alias y. */
+ * resid may alias y. ss_out (NULL = skip) receives, for each 32-column block
+ * j and row m, ss_out[j*32 + m] = sum of squares of the stored y values: the
+ * statistic a following fused RMSNorm needs (pass it as that call's ss_in). */
 int mtp_qmv_affine4_residual(const void* x, const void* w, const void* scales, const void* biases,
-                             const void* resid, void* y, int M, int N, int K, int group_size, void* ws,
-                             size_t ws_bytes, void* stream);
+                             const void* resid, void* y, float* ss_out, int M, int N, int K, int group_size,
+                             void* ws, size_t ws_bytes, void* stream);
 
 /* Gate/up pair sharing one read of x. swiglu=0: y0 = x@W0^T, y1 = x@W1^T
  * (mtplx/verify_qmv.py:614 multi3_dual_qmv4_matmul, :833 parallel dual);
@@ -68,21 +70,65 @@ int mtp_qmv_affine4_swiglu_in(const void* gate, const void* up, const void* w, c
                               void* ws, size_t ws_bytes, void* stream);
 
 /* y = rmsnorm(x; norm_w, eps) @ W^T, the norm fused into the matmul's
- * activation staging (the layer's input_layernorm + q|k|v projection). */
-int mtp_qmv_affine4_rmsnorm_in(const void* x, const void* norm_w, float eps, const void* w, const void* scales,
+ * activation staging (the layer's input_layernorm + q|k|v projection).
+ * ss_in: the producer's ss_out for x (K/32 blocks), or NULL to compute the
+ * row statistics here. */
+int mtp_qmv_affine4_rmsnorm_in(const void* x, const void* norm_w, const float* ss_in, float eps, const void* w,
+                               const void* scales,
                                const void* biases, void* y, int M, int N, int K, int group_size, void* ws,
                                size_t ws_bytes, void* stream);
 
 /* fp32 logits: y = float(bf16(rmsnorm(x) @ W^T)) (norm_w NULL = no norm);
  * the lm_head of the verify rows feeding the sampler. */
-int mtp_qmv_affine4_rmsnorm_f32(const void* x, const void* norm_w, float eps, const void* w, const void* scales,
+int mtp_qmv_affine4_rmsnorm_f32(const void* x, const void* norm_w, const float* ss_in, float eps, const void* w,
+                                const void* scales,
                                 const void* biases, float* y, int M, int N, int K, int group_size, void* ws,
                                 size_t ws_bytes, void* stream);
 
 /* y = silu(rmsnorm(x)@W0^T) * (rmsnorm(x)@W1^T): post-attention norm + gate/up. */
-int mtp_qmv_affine4_rmsnorm_dual(const void* x, const void* norm_w, float eps, const void* w0, const void* s0,
+int mtp_qmv_affine4_rmsnorm_dual(const void* x, const void* norm_w, const float* ss_in, float eps, const void* w0,
+                                 const void* s0,
                                  const void* b0, const void* w1, const void* s1, const void* b1, void* y, int M,
                                  int N, int K, int group_size, void* ws, size_t ws_bytes, void* stream);
+
+/* ---- Tile-major packed weights + generic entry -----------------------------
+ * mtp_pack_affine4 rewrites one 4-bit affine matrix (MLX layout above) into
+ * the layout the streaming kernel reads with full-line loads: per 32-row tile
+ * and 256-column quad, 1152 words = 4 x 256 words of nibbles in wave-load
+ * order, then 32 rows x (4 scales, 4 biases) bf16; rows past N are zero.
+ * No reference counterpart: the reference reads MLX's layout directly
+ * (mtplx/verify_kernels.py:69-88); this is the MI355X memory layout of the
+ * same values, produced once at load time. */
+size_t mtp_pack_affine4_bytes(int N, int K);
+int mtp_pack_affine4(const void* w, const void* scales, const void* biases, void* out, int N, int K, int group_size,
+                     void* stream);
+
+/* Every verify-matmul variant through one argument block. xmode: 0 = x,
+ * 1 = silu(x)*x2 (x2 = up), 2 = rmsnorm(x; norm weight x2, eps, ss_in);
+ * emode: 0 = store (y0 bf16, or yf fp32 when set), 1 = + resid (ss_out
+ * optional), 2 = two outputs (w1 -> y1), 3 = silu(x@W0^T)*(x@W1^T).
+ * packed = 1: w0/w1 come from mtp_pack_affine4 (s0/b0/s1/b1 unused).
+ * ldx/ldy <= 0 mean K/N. */
+typedef struct mtp_qmv_args {
+  const void* x;
+  const void* x2;
+  const float* ss_in;
+  const void* w0;
+  const void* s0;
+  const void* b0;
+  const void* w1;
+  const void* s1;
+  const void* b1;
+  void* y0;
+  void* y1;
+  float* yf;
+  const void* resid;
+  float* ss_out;
+  float eps;
+  int M, N, K, group_size, ldx, ldy;
+  int xmode, emode, packed;
+} mtp_qmv_args;
+int mtp_qmv_affine4_ex(const mtp_qmv_args* args, void* stream);
 
 /* ---- Ragged KV cache + attention -----------------------------------------
  * Cache layout [B, Hkv, cap, D] bf16 (mtplx/ragged_kv_cache.py:71).

@@ -25,13 +25,13 @@ SIGNATURES = {
     "mtp_last_error": (C.c_char_p, []),
     "mtp_qmv_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "mtp_qmv_affine4": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
-    "mtp_qmv_affine4_residual": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "mtp_qmv_affine4_residual": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "mtp_qmv_affine4_dual": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "mtp_qmv_affine4_swiglu_in": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
-    "mtp_qmv_affine4_rmsnorm_in": (_i, [_vp, _vp, _f, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
-    "mtp_qmv_affine4_rmsnorm_f32": (_i, [_vp, _vp, _f, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
-    "mtp_qmv_affine4_rmsnorm_dual": (_i, [_vp, _vp, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp,
-                                          _sz, _vp]),
+    "mtp_qmv_affine4_rmsnorm_in": (_i, [_vp, _vp, _vp, _f, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "mtp_qmv_affine4_rmsnorm_f32": (_i, [_vp, _vp, _vp, _f, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "mtp_qmv_affine4_rmsnorm_dual": (_i, [_vp, _vp, _vp, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
+                                          _vp, _sz, _vp]),
     "mtp_kv_scatter": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]),
     "mtp_kv_restore_masked": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
     "mtp_ragged_causal_mask": (_i, [_vp, _vp, _i, _i, _i, _vp]),
@@ -52,7 +52,28 @@ SIGNATURES = {
                                     _i, _i, _i, _i, _vp, _sz, _vp]),
     "mtp_moe_route": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "mtp_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "mtp_pack_affine4_bytes": (_sz, [_i, _i]),
+    "mtp_pack_affine4": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "mtp_qmv_affine4_ex": (_i, [_vp, _vp]),
 }
+
+
+class QmvArgs(C.Structure):
+    """``mtp_qmv_args`` of include/mtplx_amd.h (same field order)."""
+
+    _fields_ = [(n, _vp) for n in ("x", "x2", "ss_in", "w0", "s0", "b0", "w1", "s1", "b1", "y0", "y1", "yf",
+                                   "resid", "ss_out")] + [("eps", _f)] + \
+               [(n, _i) for n in ("M", "N", "K", "group_size", "ldx", "ldy", "xmode", "emode", "packed")]
+
+
+def qmv_ex(stream, **fields) -> None:
+    """Call ``mtp_qmv_affine4_ex``; tensor fields may be torch tensors or None."""
+    a = QmvArgs()
+    for k, v in fields.items():
+        if hasattr(v, "data_ptr"):
+            v = v.data_ptr()
+        setattr(a, k, v)
+    call("mtp_qmv_affine4_ex", C.byref(a), stream)
 
 
 class MtpError(RuntimeError):

@@ -199,42 +199,82 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnParams p) {
     }
 }
 
-// grid: B*Hkv workgroups of 256 threads; merge splits in order.
-__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
-  const int bh = blockIdx.x;
+// grid: one 128-thread workgroup per (request, kv head, query column); thread
+// d merges column d over the splits in split order (deterministic).
+constexpr int kMaxSplits = 256;
+
+__global__ __launch_bounds__(128) void attn_merge_kernel(AttnParams p) {
+  __shared__ float s_w[kMaxSplits];
+  __shared__ float s_red[2];
+  const int rep = p.Hq / p.Hkv;
+  const int rows = rep * p.L;
+  const int q = blockIdx.x % rows;
+  const int bh = blockIdx.x / rows;
   const int h = bh % p.Hkv;
   const int b = bh / p.Hkv;
-  const int rep = p.Hq / p.Hkv;
+  const int d = threadIdx.x;
   const int L = p.q_lens ? p.q_lens[b] : p.L;
+  const int qr = q / p.L, qi = q - (q / p.L) * p.L;
   const int kv_end = p.q_start[b] + L;
   int ns = cdiv(kv_end < p.cap ? kv_end : p.cap, p.split_keys);
   if (ns > p.S) ns = p.S;
-  const int rows = rep * p.L;
-  for (int idx = threadIdx.x; idx < rows * kHD; idx += blockDim.x) {
-    const int q = idx / kHD;
-    const int d = idx - q * kHD;
-    const int qr = q / p.L, qi = q - (q / p.L) * p.L;
-    float M = kNegBig;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, p.part_ml[((size_t)bh * p.S + s) * 64 + 2 * q]);
-    float lsum = 0.f, acc = 0.f;
-    for (int s = 0; s < ns; ++s) {
-      const size_t u = (size_t)bh * p.S + s;
-      const float w = exp2f(p.part_ml[u * 64 + 2 * q] - M);
-      lsum += p.part_ml[u * 64 + 2 * q + 1] * w;
-      acc += p.part_o[(u * 32 + q) * kHD + d] * w;
-    }
-    const float val = (qi < L && lsum > 0.f) ? acc / lsum : 0.f;
-    const size_t oi = p.out_rows ? ((((size_t)b * p.L + qi) * p.Hq + h * rep + qr) * kHD + d)
-                                 : ((((size_t)b * p.Hq + h * rep + qr) * p.L + qi) * kHD + d);
-    p.out[oi] = f2bf(val);
+  const float* ml = p.part_ml + (size_t)bh * p.S * 64 + 2 * q;
+  // max over splits (fixed tree over lanes, one wave)
+  if (d < 64) {
+    float m = kNegBig;
+    for (int s = d; s < ns; s += 64) m = fmaxf(m, ml[(size_t)s * 64]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if (d == 0) s_red[0] = m;
   }
+  __syncthreads();
+  const float M = s_red[0];
+  for (int s = d; s < ns; s += 128) s_w[s] = exp2f(ml[(size_t)s * 64] - M);
+  __syncthreads();
+  if (d == 0) {
+    float lsum = 0.f;
+    for (int s = 0; s < ns; ++s) lsum += ml[(size_t)s * 64 + 1] * s_w[s];
+    s_red[1] = lsum;
+  }
+  const float* po = p.part_o + ((size_t)bh * p.S * 32 + q) * kHD + d;
+  float acc = 0.f;
+  int s = 0;
+  for (; s + 4 <= ns; s += 4) {
+    const float o0 = po[(size_t)(s + 0) * 32 * kHD], o1 = po[(size_t)(s + 1) * 32 * kHD];
+    const float o2 = po[(size_t)(s + 2) * 32 * kHD], o3 = po[(size_t)(s + 3) * 32 * kHD];
+    acc += o0 * s_w[s];
+    acc += o1 * s_w[s + 1];
+    acc += o2 * s_w[s + 2];
+    acc += o3 * s_w[s + 3];
+  }
+  for (; s < ns; ++s) acc += po[(size_t)s * 32 * kHD] * s_w[s];
+  __syncthreads();
+  const float lsum = s_red[1];
+  const float val = (qi < L && lsum > 0.f) ? acc / lsum : 0.f;
+  const size_t oi = p.out_rows ? ((((size_t)b * p.L + qi) * p.Hq + h * rep + qr) * kHD + d)
+                               : ((((size_t)b * p.Hq + h * rep + qr) * p.L + qi) * kHD + d);
+  p.out[oi] = f2bf(val);
 }
 
-static int attn_plan(int cap, int split_keys_req, int* S, int* split_keys) {
-  int sk = split_keys_req > 0 ? split_keys_req : 512;
+// Split length: ~2048 work units over the whole capacity (ragged rows leave
+// the units past their length empty), 64..4096 keys, a multiple of the tile.
+static int attn_plan(int B, int Hkv, int cap, int split_keys_req, int* S, int* split_keys) {
+  int sk = split_keys_req;
+  if (sk <= 0) {
+    const long long total = (long long)cap * B * Hkv;
+    sk = (int)((total + 2047) / 2048);
+    if (sk < 64) sk = 64;
+    if (sk > 4096) sk = 4096;
+  }
   sk = ((sk + kTileKeys - 1) / kTileKeys) * kTileKeys;
+  int s = cdiv(cap, sk);
+  if (s > kMaxSplits) {
+    s = kMaxSplits;
+    sk = ((cdiv(cap, s) + kTileKeys - 1) / kTileKeys) * kTileKeys;
+    s = cdiv(cap, sk);
+  }
   *split_keys = sk;
-  *S = cdiv(cap, sk);
+  *S = s;
   return MTP_OK;
 }
 
@@ -308,7 +348,7 @@ using namespace mtp;
 
 MTP_API size_t mtp_attn_workspace_bytes(int B, int Hkv, int cap, int split_keys) {
   int S, sk;
-  attn_plan(cap, split_keys, &S, &sk);
+  attn_plan(B, Hkv, cap, split_keys, &S, &sk);
   const size_t units = (size_t)B * Hkv * S;
   return units * 32 * kHD * sizeof(float) + units * 64 * sizeof(float);
 }
@@ -345,7 +385,7 @@ static int attn_run(const void* q, const void* k, const void* v, const int32_t* 
   p.L = L;
   p.cap = cap;
   p.out_rows = out_rows;
-  attn_plan(cap, split_keys, &p.S, &p.split_keys);
+  attn_plan(B, Hkv, cap, split_keys, &p.S, &p.split_keys);
   p.scale_log2 = scale * 1.4426950408889634f;
   const size_t need = mtp_attn_workspace_bytes(B, Hkv, cap, split_keys);
   if (!ws || ws_bytes < need) {
@@ -359,7 +399,7 @@ static int attn_run(const void* q, const void* k, const void* v, const int32_t* 
   hipLaunchKernelGGL(attn_split_kernel, dim3((unsigned)units), dim3(64), 0, st, p);
   int rc = launch_check(who);
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(B * Hkv), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(B * Hkv * (Hq / Hkv) * L), dim3(128), 0, st, p);
   return launch_check(who);
 }
 

@@ -59,6 +59,9 @@ struct QmmParams {
   uint16_t* y1;            // E_DUAL: second output
   float* yf;               // E_STORE: optional fp32 output (bf16-rounded values)
   const uint16_t* resid;   // E_RESID: [rows, ldy]
+  float* ss_out;           // E_RESID: per 32-column block, per row: sum of squares of y
+  const float* ss_in;      // X_RMSNORM: producer's ss_out ([ss_parts][32]); null = compute
+  int ss_parts;
   float* partial;          // [S, M, nvirt]
   uint32_t* counters;      // [n_blocks]
   // Expert-gathered mode (MoE): rows of expert e are [off[e], off[e+1]) of
@@ -71,36 +74,80 @@ struct QmmParams {
   int M, N, K, gs;
   int ldx, ldy;
   int S, gps, n_blocks, nvirt, chunk;
+  int packed;              // w0/w1 in the tile-major layout (scales/biases inside)
   float eps;
 };
 
 constexpr int kThreads = 256;
+constexpr int kPackQuadWords = 1152;   // tile-major pack: words per (32-row tile, 256-k quad)
 
 // Nibbles of one word -> bf16x8 operand (128+q exactly), element order
-// (n0, n4, n1, n5, n2, n6, n3, n7).
-__device__ __forceinline__ bf16x8 nibbles_to_bf16(uint32_t w) {
+// (n0, n4, n1, n5, n2, n6, n3, n7). The mask and the exponent pattern are
+// held in registers (gfx9 VOP3 encodings take no literal), so each output
+// dword is one v_and_or_b32 (plus a shift): 7 VALU per word instead of 11.
+struct NibConsts {
+  uint32_t mask, bias;
+};
+__device__ __forceinline__ NibConsts nib_consts() {
+  NibConsts c;
+  asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(c.mask));
+  asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(c.bias));
+  return c;
+}
+__device__ __forceinline__ bf16x8 nibbles_to_bf16(uint32_t w, NibConsts c) {
   uint32_t v[4];
-  v[0] = (w & 0x000F000Fu) | 0x43004300u;
-  v[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  v[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  v[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  v[0] = (w & c.mask) | c.bias;
+  v[1] = ((w >> 4) & c.mask) | c.bias;
+  v[2] = ((w >> 8) & c.mask) | c.bias;
+  v[3] = ((w >> 12) & c.mask) | c.bias;
   return __builtin_bit_cast(bf16x8, v);
 }
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
 
 // x value as the consumer sees it (after the fused producer), rounded to bf16
-// exactly as an unfused producer would have stored it.
+// exactly as an unfused producer would have stored it. ``b`` is the up half
+// (X_SWIGLU) or the norm weight (X_RMSNORM).
 template <int XM>
-__device__ __forceinline__ uint16_t produce(const QmmParams& p, uint16_t a, uint16_t b, float inv_rms,
-                                            int k) {
+__device__ __forceinline__ uint16_t produce(uint16_t a, uint16_t b, float inv_rms) {
   if (XM == X_PLAIN) return a;
   if (XM == X_SWIGLU) {
     float g = round_bf(silu_f(bf2f(a)));
     return f2bf(g * bf2f(b));
   }
   // X_RMSNORM: x * inv_rms * w in fp32, rounded once (a fused norm).
-  return f2bf(bf2f(a) * inv_rms * bf2f(p.x2[k]));
+  return f2bf(bf2f(a) * inv_rms * bf2f(b));
+}
+
+// One 16 B chunk of x (8 consecutive k) through the producer: returns it in
+// MFMA A order (bf16 pairs (t, t+4)) and adds its 8 values to ``sum``.
+template <int XM>
+__device__ __forceinline__ uint4 produce_chunk(uint4 raw, uint4 raw2, float inv_rms, float& sum) {
+  const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+  const uint32_t uv[4] = {raw2.x, raw2.y, raw2.z, raw2.w};
+  uint16_t e[8];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    e[2 * t] = produce<XM>((uint16_t)(wv[t] & 0xffff), (uint16_t)(uv[t] & 0xffff), inv_rms);
+    e[2 * t + 1] = produce<XM>((uint16_t)(wv[t] >> 16), (uint16_t)(uv[t] >> 16), inv_rms);
+  }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) sum += bf2f(e[t]);
+  uint4 o;
+  o.x = (uint32_t)e[0] | ((uint32_t)e[4] << 16);
+  o.y = (uint32_t)e[1] | ((uint32_t)e[5] << 16);
+  o.z = (uint32_t)e[2] | ((uint32_t)e[6] << 16);
+  o.w = (uint32_t)e[3] | ((uint32_t)e[7] << 16);
+  return o;
+}
+
+// Second producer input of the chunk at (row offset xo, column k): the up
+// half for SwiGLU, the norm weight for RMSNorm, nothing otherwise.
+template <int XM>
+__device__ __forceinline__ uint4 producer_aux(const QmmParams& p, size_t xo, int k) {
+  if (XM == X_SWIGLU) return *reinterpret_cast<const uint4*>(p.x2 + xo);
+  if (XM == X_RMSNORM) return *reinterpret_cast<const uint4*>(p.x2 + k);
+  return make_uint4(0, 0, 0, 0);
 }
 
 __device__ __forceinline__ size_t x_row(const QmmParams& p, int row0, int m) {
@@ -108,50 +155,65 @@ __device__ __forceinline__ size_t x_row(const QmmParams& p, int row0, int m) {
   return (size_t)(p.rowmap ? (int)p.rowmap[r] : r) * p.ldx;
 }
 
-// One workgroup = 4 waves over 32 output columns (one MFMA column tile) and
+// One workgroup = NW waves over 32 output columns (one MFMA column tile) and
 // the whole K range. K is split between the waves by "quads" (4 groups =
 // 256 k = one 128 B line per weight row): plain modes give wave w the quads
-// w, w+4, ...; dual modes give waves 0,1 matrix 0 and waves 2,3 matrix 1,
-// each pair splitting the quads two ways. Partials meet in LDS and are summed
-// in wave order — deterministic, no global atomics. x is staged in chunks of
-// p.chunk quads shared by all waves; weight loads run one quad ahead of the
-// MFMAs with no data-dependent branches, so the memory pipeline never drains.
+// w, w+NW, ...; dual modes give the first NW/2 waves matrix 0 and the rest
+// matrix 1, each half splitting the quads NW/2 ways. Partials meet in LDS and
+// are summed in wave order — deterministic, no global atomics. x is staged in
+// chunks of p.chunk quads shared by all waves; weight loads run two quads
+// ahead of the MFMAs with no data-dependent branches, so every wave keeps
+// 128 B per lane in flight.
 // Leaves the final values in fin[M][64] (cols 0..31 matrix 0, 32..63 matrix 1).
-template <int R, int XM, int EM, int GSH>
+template <int NW, int R, int XM, int EM, int GSH>
 __device__ __forceinline__ void qmm_body(const QmmParams& p, unsigned char* smem, int nb, int M, int row0,
                                          long long woff, long long soff) {
+  constexpr int NT = NW * 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int Q = p.K >> 8;            // quads
   const int CHQ = p.chunk;           // quads per staging chunk
   constexpr bool dual = (EM == E_DUAL || EM == E_DUAL_SWIGLU);
-  constexpr int KS = dual ? 2 : 4;   // waves sharing one column tile
-  const int kw = dual ? (wave & 1) : wave;
-  const int which = dual ? (wave >> 1) : 0;
+  constexpr int KS = dual ? NW / 2 : NW;   // waves sharing one column tile
+  const NibConsts nc = nib_consts();
+  const int kw = wave % KS;
+  const int which = dual ? (wave / KS) : 0;
 
   uint4* xa = reinterpret_cast<uint4*>(smem);                                 // [CHQ*4][4][2][M]
   float* xs = reinterpret_cast<float*>(smem + (size_t)CHQ * 4 * 8 * M * 16);  // [CHQ*4][32]
-  float* red = reinterpret_cast<float*>(smem);  // [4][32 m][32 c], reuses the staging area
+  float* red = reinterpret_cast<float*>(smem);  // [NW][32 m][32 c], reuses the staging area
   __shared__ float s_inv_rms[32];
 
-  // ---- RMSNorm statistics (full row, fp32, fixed order) ----
+  // ---- RMSNorm statistics (fp32, fixed order) ----
   if (XM == X_RMSNORM) {
-    for (int m = wave; m < M; m += 4) {
-      const uint16_t* xr = p.x + x_row(p, row0, m);
-      float ss = 0.f;
-      for (int k = lane * 8; k < p.K; k += 64 * 8) {
-        uint4 raw = *reinterpret_cast<const uint4*>(xr + k);
-        const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+    if (p.ss_in) {
+      // Partial sums of squares left by the producer's epilogue, one per
+      // 32-column block of the row: lane-strided sums then a fixed butterfly.
+      for (int m = wave; m < M; m += NW) {
+        float ss = 0.f;
+        for (int j = lane; j < p.ss_parts; j += 64) ss += p.ss_in[(size_t)j * 32 + row0 + m];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          float a = bf2f((uint16_t)(wv[t] & 0xffff)), b = bf2f((uint16_t)(wv[t] >> 16));
-          ss += a * a + b * b;
-        }
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        if (lane == 0) s_inv_rms[m] = rsqrtf(ss / (float)p.K + p.eps);
       }
+    } else {
+      for (int m = wave; m < M; m += NW) {
+        const uint16_t* xr = p.x + x_row(p, row0, m);
+        float ss = 0.f;
+        for (int k = lane * 8; k < p.K; k += 64 * 8) {
+          uint4 raw = *reinterpret_cast<const uint4*>(xr + k);
+          const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-      if (lane == 0) s_inv_rms[m] = rsqrtf(ss / (float)p.K + p.eps);
+          for (int t = 0; t < 4; ++t) {
+            float a = bf2f((uint16_t)(wv[t] & 0xffff)), b = bf2f((uint16_t)(wv[t] >> 16));
+            ss += a * a + b * b;
+          }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        if (lane == 0) s_inv_rms[m] = rsqrtf(ss / (float)p.K + p.eps);
+      }
     }
     __syncthreads();
   }
@@ -205,59 +267,42 @@ __device__ __forceinline__ void qmm_body(const QmmParams& p, unsigned char* smem
 
   const int nchunks = cdiv(Q, CHQ);
   int q = kw;
-  QuadRegs cur;
+  QuadRegs cur, n1;
   load_quad(q < Q ? q : Q - 1, cur);
+  load_quad(q + KS < Q ? q + KS : Q - 1, n1);
   for (int c = 0; c < nchunks; ++c) {
     const int cq0 = c * CHQ;
     const int cq1 = min(Q, cq0 + CHQ);
     // ---- stage x for quads [cq0, cq1) in MFMA A order + group sums ----
     __syncthreads();
     const int ng = 4 * (cq1 - cq0);
-    for (int pidx = tid; pidx < ng * M; pidx += kThreads) {
+    for (int pidx = tid; pidx < ng * M; pidx += NT) {
       const int gl = pidx / M;
       const int m = pidx - gl * M;
       const int kbase = 64 * (4 * cq0 + gl);
       const size_t xo = x_row(p, row0, m) + kbase;
-      const uint16_t* xr = p.x + xo;
-      const uint16_t* ur = (XM == X_SWIGLU) ? p.x2 + xo : nullptr;
       const float inv = (XM == X_RMSNORM) ? s_inv_rms[m] : 1.f;
-      float sum = 0.f;
+      uint4 raw[8], raw2[8];
 #pragma unroll
       for (int cc = 0; cc < 8; ++cc) {
-        uint4 raw = *reinterpret_cast<const uint4*>(xr + 8 * cc);
-        uint4 raw2 = make_uint4(0, 0, 0, 0);
-        if (XM == X_SWIGLU) raw2 = *reinterpret_cast<const uint4*>(ur + 8 * cc);
-        const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
-        const uint32_t uv[4] = {raw2.x, raw2.y, raw2.z, raw2.w};
-        uint16_t e[8];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          e[2 * t] = produce<XM>(p, (uint16_t)(wv[t] & 0xffff), (uint16_t)(uv[t] & 0xffff), inv,
-                                 kbase + 8 * cc + 2 * t);
-          e[2 * t + 1] = produce<XM>(p, (uint16_t)(wv[t] >> 16), (uint16_t)(uv[t] >> 16), inv,
-                                     kbase + 8 * cc + 2 * t + 1);
-        }
-#pragma unroll
-        for (int t = 0; t < 8; ++t) sum += bf2f(e[t]);
-        uint4 o;
-        o.x = (uint32_t)e[0] | ((uint32_t)e[4] << 16);
-        o.y = (uint32_t)e[1] | ((uint32_t)e[5] << 16);
-        o.z = (uint32_t)e[2] | ((uint32_t)e[6] << 16);
-        o.w = (uint32_t)e[3] | ((uint32_t)e[7] << 16);
-        // 8-element chunk cc covers k offset 8cc = 32*kq + 8*i within the group
-        xa[((gl * 4 + (cc & 3)) * 2 + (cc >> 2)) * M + m] = o;
+        raw[cc] = *reinterpret_cast<const uint4*>(p.x + xo + 8 * cc);
+        raw2[cc] = producer_aux<XM>(p, xo + 8 * cc, kbase + 8 * cc);
       }
+      float sum = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < 8; ++cc)   // chunk cc covers k offset 8cc = 32*kq + 8*i within the group
+        xa[((gl * 4 + (cc & 3)) * 2 + (cc >> 2)) * M + m] = produce_chunk<XM>(raw[cc], raw2[cc], inv, sum);
       xs[gl * 32 + m] = sum;
     }
-    for (int idx = tid; idx < ng * 32; idx += kThreads)
+    for (int idx = tid; idx < ng * 32; idx += NT)
       if ((idx & 31) >= M) xs[idx] = 0.f;
     __syncthreads();
 
     // ---- this wave's quads inside the chunk ----
     for (; q < cq1; q += KS) {
-      QuadRegs nxt;
-      const int qn = q + KS;
-      load_quad(qn < Q ? qn : Q - 1, nxt);
+      QuadRegs n2;
+      const int qn = q + 2 * KS;
+      load_quad(qn < Q ? qn : Q - 1, n2);
       const int gq = 4 * (q - cq0);
 #pragma unroll
       for (int u = 0; u < 4; u += 2) {
@@ -271,8 +316,8 @@ __device__ __forceinline__ void qmm_body(const QmmParams& p, unsigned char* smem
             a0 = __builtin_bit_cast(bf16x8, xa[(((gq + u) * 4 + i) * 2 + kq) * M + c32]);
             a1 = __builtin_bit_cast(bf16x8, xa[(((gq + u + 1) * 4 + i) * 2 + kq) * M + c32]);
           }
-          G0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, nibbles_to_bf16(w0[i]), G0, 0, 0, 0);
-          G1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, nibbles_to_bf16(w1[i]), G1, 0, 0, 0);
+          G0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, nibbles_to_bf16(w0[i], nc), G0, 0, 0, 0);
+          G1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, nibbles_to_bf16(w1[i], nc), G1, 0, 0, 0);
         }
         const float s0 = scale_of(cur.s, u), s1 = scale_of(cur.s, u + 1);
         const float cb0 = scale_of(cur.b, u) - 128.f * s0;
@@ -294,7 +339,8 @@ __device__ __forceinline__ void qmm_body(const QmmParams& p, unsigned char* smem
           acc[r] = fmaf(s1, G1[r], fmaf(cb1, x1, acc[r]));
         }
       }
-      cur = nxt;
+      cur = n1;
+      n1 = n2;
     }
   }
 
@@ -306,61 +352,80 @@ __device__ __forceinline__ void qmm_body(const QmmParams& p, unsigned char* smem
     if (m < M) red[(wave * 32 + m) * 32 + c32] = valid ? acc[r] : 0.f;
   }
   __syncthreads();
-  float* fin = red + 4 * 32 * 32;  // [M][64]
-  for (int idx = tid; idx < M * 64; idx += kThreads) {
+  float* fin = red + NW * 32 * 32;  // [M][64]
+  for (int idx = tid; idx < M * 64; idx += NT) {
     const int m = idx >> 6;
     const int c = idx & 63;
     const int mat = c >> 5;
     float v = 0.f;
     if (!dual && mat == 0) {
 #pragma unroll
-      for (int w = 0; w < 4; ++w) v += red[(w * 32 + m) * 32 + c];
+      for (int w = 0; w < NW; ++w) v += red[(w * 32 + m) * 32 + c];
     } else if (dual) {
-      v = red[((2 * mat) * 32 + m) * 32 + (c & 31)] + red[((2 * mat + 1) * 32 + m) * 32 + (c & 31)];
+#pragma unroll
+      for (int w = 0; w < KS; ++w) v += red[((mat * KS + w) * 32 + m) * 32 + (c & 31)];
     }
     fin[idx] = v;
   }
   __syncthreads();
 }
 
-// Epilogue from fin[m][64]: columns nb*32 + c, output rows row0 + m.
-template <int EM>
-__device__ __forceinline__ void qmm_epilogue(const QmmParams& p, const float* fin, int nb, int M, int row0) {
+// Epilogue from fin[m][64]: columns nb*32 + c, output rows row0 + m. The
+// residual mode also leaves, per output row, the sum of squares of this
+// block's 32 stored values (fixed order) for a following fused RMSNorm.
+template <int NW, int EM>
+__device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int nb, int M, int row0) {
+  constexpr int NT = NW * 64;
   const int tid = threadIdx.x;
-  for (int idx = tid; idx < M * 32; idx += kThreads) {
+  for (int idx = tid; idx < M * 32; idx += NT) {
     const int m = idx >> 5;
     const int c = idx & 31;
     const int nn = nb * 32 + c;
-    if (nn >= p.N) continue;
+    const bool in = nn < p.N;
     const size_t o = (size_t)(row0 + m) * p.ldy + nn;
     const float g = fin[m * 64 + c];
     if (EM == E_DUAL) {
-      p.y0[o] = f2bf(g);
-      p.y1[o] = f2bf(fin[m * 64 + 32 + c]);
+      if (in) {
+        p.y0[o] = f2bf(g);
+        p.y1[o] = f2bf(fin[m * 64 + 32 + c]);
+      }
     } else if (EM == E_DUAL_SWIGLU) {
       const float gs = round_bf(silu_f(round_bf(g)));
-      p.y0[o] = f2bf(gs * round_bf(fin[m * 64 + 32 + c]));
+      if (in) p.y0[o] = f2bf(gs * round_bf(fin[m * 64 + 32 + c]));
     } else {
       float v = g;
-      if (EM == E_RESID) v = round_bf(v) + bf2f(p.resid[o]);
-      if (EM == E_STORE && p.yf)
-        p.yf[o] = round_bf(v);
-      else
-        p.y0[o] = f2bf(v);
+      if (EM == E_RESID) {
+        v = round_bf(in ? round_bf(v) + bf2f(p.resid[o]) : 0.f);
+        fin[m * 64 + 32 + c] = v * v;  // column 32+c is free in non-dual modes
+      }
+      if (in) {
+        if (EM == E_STORE && p.yf)
+          p.yf[o] = round_bf(v);
+        else
+          p.y0[o] = f2bf(v);
+      }
+    }
+  }
+  if (EM == E_RESID && p.ss_out) {
+    __syncthreads();
+    if (tid < M) {
+      float ss = 0.f;
+      for (int c = 0; c < 32; ++c) ss += fin[tid * 64 + 32 + c];
+      p.ss_out[(size_t)nb * 32 + row0 + tid] = ss;
     }
   }
 }
 
-__device__ __forceinline__ float* fin_of(unsigned char* smem) {
-  return reinterpret_cast<float*>(smem) + 4 * 32 * 32;
+__device__ __forceinline__ float* fin_of(unsigned char* smem, int NW) {
+  return reinterpret_cast<float*>(smem) + NW * 32 * 32;
 }
 
-template <int R, int XM, int EM, int GSH>
-__global__ __launch_bounds__(kThreads) void qmm4_kernel(QmmParams p) {
+template <int NW, int R, int XM, int EM, int GSH>
+__global__ __launch_bounds__(NW * 64) void qmm4_kernel(QmmParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int nb = blockIdx.x;
-  qmm_body<R, XM, EM, GSH>(p, smem, nb, p.M, 0, 0, 0);
-  qmm_epilogue<EM>(p, fin_of(smem), nb, p.M, 0);
+  qmm_body<NW, R, XM, EM, GSH>(p, smem, nb, p.M, 0, 0, 0);
+  qmm_epilogue<NW, EM>(p, fin_of(smem, NW), nb, p.M, 0);
 }
 
 // Expert-gathered launch: grid (column tiles, row tiles, expert slots).
@@ -376,15 +441,528 @@ __global__ __launch_bounds__(kThreads) void gather_qmm4_kernel(QmmParams p) {
   const int r1 = p.expert_off[e + 1];
   if (r0 >= r1) return;
   const int M = min(32, r1 - r0);
-  qmm_body<R, XM, EM, GSH>(p, smem, nb, M, r0, (long long)e * p.w_estride, (long long)e * p.s_estride);
-  qmm_epilogue<EM>(p, fin_of(smem), nb, M, r0);
+  qmm_body<4, R, XM, EM, GSH>(p, smem, nb, M, r0, (long long)e * p.w_estride, (long long)e * p.s_estride);
+  qmm_epilogue<4, EM>(p, fin_of(smem, 4), nb, M, r0);
+}
+
+// ---------------------------------------------------------------------------
+// Persistent streaming form of the dense verify matmul.
+//
+// The grid holds at most as many workgroups as the GPU keeps resident; each
+// loops over 32-column tiles nb = blockIdx.x, + gridDim.x, ... Within a tile
+// the NW waves split K by quads as in qmm_body. The activations are staged
+// into LDS once per workgroup when all of K fits (chunk >= K/256 quads), and
+// every wave walks one flat sequence of (tile, quad) items with a two-quad
+// prefetch that runs across tile boundaries, so the weight stream does not
+// drain between tiles. Per tile: LDS reduction of the wave partials (wave
+// order, deterministic) and the shared epilogue.
+template <int NW, int R, int XM, int EM, int GSH>
+__global__ __launch_bounds__(NW * 64) void qmv_chunked_kernel(QmmParams p) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int NT = NW * 64;
+  constexpr bool dual = (EM == E_DUAL || EM == E_DUAL_SWIGLU);
+  constexpr int KS = dual ? NW / 2 : NW;
+  constexpr int XSW = 2 * R;  // group sums per staged group (rows 0..2R-1)
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kw = wave % KS;
+  const int which = dual ? (wave / KS) : 0;
+  const int M = p.M;
+  const int Q = p.K >> 8;
+  const int CHQ = p.chunk;
+  const bool resident = CHQ >= Q;
+  const NibConsts nc = nib_consts();
+  const int nchunks = cdiv(Q, CHQ);
+  const int G = gridDim.x;
+
+  uint4* xa = reinterpret_cast<uint4*>(smem);                                       // [CHQ*4][4][2][M]
+  float* xs = reinterpret_cast<float*>(smem + (size_t)CHQ * 4 * 8 * M * 16);        // [CHQ*4][XSW]
+  float* red = xs + CHQ * 4 * XSW;                                                  // [NW][M][32]
+  float* fin = red + NW * M * 32;                                                   // [M][64]
+  __shared__ float s_inv_rms[32];
+
+  // ---- RMSNorm statistics (once: every tile has the same rows) ----
+  if (XM == X_RMSNORM) {
+    for (int m = wave; m < M; m += NW) {
+      float ss = 0.f;
+      if (p.ss_in) {
+        for (int j = lane; j < p.ss_parts; j += 64) ss += p.ss_in[(size_t)j * 32 + m];
+      } else {
+        const uint16_t* xr = p.x + (size_t)m * p.ldx;
+#pragma unroll 4
+        for (int k = lane * 8; k < p.K; k += 64 * 8) {
+          uint4 raw = *reinterpret_cast<const uint4*>(xr + k);
+          const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            float a = bf2f((uint16_t)(wv[t] & 0xffff)), b = bf2f((uint16_t)(wv[t] >> 16));
+            ss += a * a + b * b;
+          }
+        }
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+      if (lane == 0) s_inv_rms[m] = rsqrtf(ss / (float)p.K + p.eps);
+    }
+    __syncthreads();
+  }
+
+  const int c32 = lane & 31;
+  const int kq = lane >> 5;
+  const uint32_t* W = which ? p.w1 : p.w0;
+  const uint16_t* Sc = which ? p.s1 : p.s0;
+  const uint16_t* Bi = which ? p.b1 : p.b0;
+  const int sgroups = p.K >> (6 + GSH);
+  const bool arow = c32 < M;
+
+  // This wave's items: tile j of this workgroup, quad q = kw + t*KS.
+  const int qw = (Q > kw) ? cdiv(Q - kw, KS) : 0;
+  const int ntiles = cdiv(p.n_blocks - (int)blockIdx.x, G);
+  const int nitems = ntiles * qw;
+
+  struct QuadRegs {
+    uint4 w[4];
+    uint32_t s[2], b[2];
+  };
+  auto load_item = [&](int i, QuadRegs& qr) {
+    int j = 0, q = kw < Q ? kw : Q - 1;
+    if (qw > 0) {
+      const int ii = i < nitems ? i : nitems - 1;
+      j = ii / qw;
+      q = kw + (ii - j * qw) * KS;
+    }
+    const int n = ((int)blockIdx.x + j * G) * 32 + c32;
+    const int nrow = n < p.N ? n : 0;
+    const uint32_t* wp = W + (size_t)nrow * (p.K >> 3) + kq * 4 + 32 * q;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) qr.w[u] = *reinterpret_cast<const uint4*>(wp + 8 * u);
+    const uint16_t* sr = Sc + (size_t)nrow * sgroups;
+    const uint16_t* br = Bi + (size_t)nrow * sgroups;
+    if (GSH == 0) {
+      const uint2 sv = *reinterpret_cast<const uint2*>(sr + 4 * q);
+      const uint2 bv = *reinterpret_cast<const uint2*>(br + 4 * q);
+      qr.s[0] = sv.x; qr.s[1] = sv.y;
+      qr.b[0] = bv.x; qr.b[1] = bv.y;
+    } else {
+      qr.s[0] = *reinterpret_cast<const uint32_t*>(sr + 2 * q);
+      qr.b[0] = *reinterpret_cast<const uint32_t*>(br + 2 * q);
+      qr.s[1] = qr.s[0];
+      qr.b[1] = qr.b[0];
+    }
+  };
+  auto scale_of = [&](const uint32_t* v, int u) -> float {
+    const uint32_t word = (GSH == 0) ? v[u >> 1] : v[0];
+    const int half = (GSH == 0) ? (u & 1) : (u >> 1);
+    return bf2f((uint16_t)(half ? (word >> 16) : (word & 0xffff)));
+  };
+
+  int item = 0;
+  QuadRegs cur, n1;
+  load_item(0, cur);
+  load_item(1, n1);
+
+  for (int j = 0; j < ntiles; ++j) {
+    const int nb = (int)blockIdx.x + j * G;
+    const bool valid = nb * 32 + c32 < p.N;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+
+    for (int c = 0; c < nchunks; ++c) {
+      const int cq0 = c * CHQ;
+      const int cq1 = min(Q, cq0 + CHQ);
+      if (!resident || j == 0) {
+        // ---- stage x for quads [cq0, cq1) in MFMA A order + group sums ----
+        __syncthreads();
+        const int ng = 4 * (cq1 - cq0);
+        for (int pidx = tid; pidx < ng * M; pidx += NT) {
+          const int gl = pidx / M;
+          const int m = pidx - gl * M;
+          const int kbase = 64 * (4 * cq0 + gl);
+          const size_t xo = (size_t)m * p.ldx + kbase;
+          const float inv = (XM == X_RMSNORM) ? s_inv_rms[m] : 1.f;
+          uint4 raw[8], raw2[8];
+#pragma unroll
+          for (int cc = 0; cc < 8; ++cc) {
+            raw[cc] = *reinterpret_cast<const uint4*>(p.x + xo + 8 * cc);
+            raw2[cc] = producer_aux<XM>(p, xo + 8 * cc, kbase + 8 * cc);
+          }
+          float sum = 0.f;
+#pragma unroll
+          for (int cc = 0; cc < 8; ++cc)
+            xa[((gl * 4 + (cc & 3)) * 2 + (cc >> 2)) * M + m] = produce_chunk<XM>(raw[cc], raw2[cc], inv, sum);
+          xs[gl * XSW + m] = sum;
+        }
+        for (int idx = tid; idx < ng * XSW; idx += NT)
+          if ((idx % XSW) >= M) xs[idx] = 0.f;
+        __syncthreads();
+      }
+
+      // ---- this wave's quads of tile j inside the chunk ----
+      int q = cq0 + ((kw - cq0) % KS + KS) % KS;
+      for (; q < cq1; q += KS) {
+        QuadRegs n2;
+        load_item(item + 2, n2);
+        const int gq = 4 * (q - cq0);
+#pragma unroll
+        for (int u = 0; u < 4; u += 2) {
+          f32x16 G0 = {}, G1 = {};
+          const uint32_t w0[4] = {cur.w[u].x, cur.w[u].y, cur.w[u].z, cur.w[u].w};
+          const uint32_t w1[4] = {cur.w[u + 1].x, cur.w[u + 1].y, cur.w[u + 1].z, cur.w[u + 1].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            bf16x8 a0 = {}, a1 = {};
+            if (arow) {
+              a0 = __builtin_bit_cast(bf16x8, xa[(((gq + u) * 4 + i) * 2 + kq) * M + c32]);
+              a1 = __builtin_bit_cast(bf16x8, xa[(((gq + u + 1) * 4 + i) * 2 + kq) * M + c32]);
+            }
+            G0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, nibbles_to_bf16(w0[i], nc), G0, 0, 0, 0);
+            G1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, nibbles_to_bf16(w1[i], nc), G1, 0, 0, 0);
+          }
+          const float s0 = scale_of(cur.s, u), s1 = scale_of(cur.s, u + 1);
+          const float cb0 = scale_of(cur.b, u) - 128.f * s0;
+          const float cb1 = scale_of(cur.b, u + 1) - 128.f * s1;
+          const float* xr0 = xs + (gq + u) * XSW + 4 * kq;
+          const float* xr1 = xs + (gq + u + 1) * XSW + 4 * kq;
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const int off = 8 * (r >> 2) + (r & 3);
+            acc[r] = fmaf(s0, G0[r], fmaf(cb0, xr0[off], acc[r]));
+            acc[r] = fmaf(s1, G1[r], fmaf(cb1, xr1[off], acc[r]));
+          }
+        }
+        cur = n1;
+        n1 = n2;
+        ++item;
+      }
+    }
+
+    // ---- reduce the K-split waves (wave order) and finish the tile ----
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int m = 8 * (r >> 2) + 4 * kq + (r & 3);
+      if (m < M) red[(wave * M + m) * 32 + c32] = valid ? acc[r] : 0.f;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < M * 64; idx += NT) {
+      const int m = idx >> 6;
+      const int cc = idx & 63;
+      const int mat = cc >> 5;
+      float v = 0.f;
+      if (!dual && mat == 0) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += red[(w * M + m) * 32 + cc];
+      } else if (dual) {
+#pragma unroll
+        for (int w = 0; w < KS; ++w) v += red[((mat * KS + w) * M + m) * 32 + (cc & 31)];
+      }
+      fin[idx] = v;
+    }
+    __syncthreads();
+    qmm_epilogue<NW, EM>(p, fin, nb, M, 0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Resident streaming kernel (the fast path): all of x is staged into LDS once
+// per workgroup, then every wave walks its flat (tile, quad) item list with a
+// three-deep register ring (A, B, C) advanced by unrolling — no register
+// copies and no data-dependent branches between a load and its use, so the
+// compiler's wait for quad i only covers loads issued before i (the two
+// quads behind it stay in flight). Lanes whose A-operand row is past M read
+// a zero block in LDS instead of branching.
+template <int NW, int R, int XM, int EM, int GSH, bool PK>
+__global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int NT = NW * 64;
+  constexpr bool dual = (EM == E_DUAL || EM == E_DUAL_SWIGLU);
+  constexpr int KS = dual ? NW / 2 : NW;
+  constexpr int XSW = 2 * R;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar loop control
+  const int kw = wave % KS;
+  const int which = dual ? (wave / KS) : 0;
+  const int M = p.M;
+  const int Q = p.K >> 8;
+  const int G = gridDim.x;
+  const NibConsts nc = nib_consts();
+
+  uint4* xa = reinterpret_cast<uint4*>(smem);                                  // [Q*4][4][2][M]
+  float* xs = reinterpret_cast<float*>(smem + (size_t)Q * 4 * 8 * M * 16);     // [Q*4][XSW]
+  float* red = xs + Q * 4 * XSW;                                               // [NW][M][32]
+  float* fin = red + NW * M * 32;                                              // [M][64]
+  uint4* zero16 = reinterpret_cast<uint4*>(fin + M * 64);                      // one 16 B zero block
+  __shared__ float s_inv_rms[32];
+
+  if (tid == 0) *zero16 = make_uint4(0, 0, 0, 0);
+  if (XM == X_RMSNORM) {
+    for (int m = wave; m < M; m += NW) {
+      float ss = 0.f;
+      if (p.ss_in) {
+        for (int j = lane; j < p.ss_parts; j += 64) ss += p.ss_in[(size_t)j * 32 + m];
+      } else {
+        const uint16_t* xr = p.x + (size_t)m * p.ldx;
+#pragma unroll 4
+        for (int k = lane * 8; k < p.K; k += 64 * 8) {
+          uint4 raw = *reinterpret_cast<const uint4*>(xr + k);
+          const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            float a = bf2f((uint16_t)(wv[t] & 0xffff)), b = bf2f((uint16_t)(wv[t] >> 16));
+            ss += a * a + b * b;
+          }
+        }
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+      if (lane == 0) s_inv_rms[m] = rsqrtf(ss / (float)p.K + p.eps);
+    }
+    __syncthreads();
+  }
+
+  const int c32 = lane & 31;
+  const int kq = lane >> 5;
+  const uint32_t* W = which ? p.w1 : p.w0;
+  const uint16_t* Sc = which ? p.s1 : p.s0;
+  const uint16_t* Bi = which ? p.b1 : p.b0;
+  const int sgroups = p.K >> (6 + GSH);
+  const int qw = (Q > kw) ? cdiv(Q - kw, KS) : 0;
+  const int ntiles = cdiv(p.n_blocks - (int)blockIdx.x, G);
+  const int nitems = ntiles * qw;
+
+  // A-operand addressing without branches: lanes past M read the zero block.
+  const bool arow = c32 < M;
+  const uint32_t xa_base = arow ? (uint32_t)((kq * M + c32) * 16) : (uint32_t)((unsigned char*)zero16 - smem);
+  const uint32_t xa_step = arow ? (uint32_t)(2 * M * 16) : 0u;   // per (group*4 + i)
+
+  struct QuadRegs {
+    uint4 w[4];
+    uint32_t s[2], b[2];
+  };
+  // Prefetch iterator: tile j_pf, quad counter t_pf (q = kw + t_pf*KS); the
+  // per-lane row pointers are recomputed only when the tile changes.
+  int j_pf = 0, t_pf = 0, left_pf = nitems;
+  const uint32_t* wrow = nullptr;
+  const uint16_t* srow = nullptr;
+  const uint16_t* brow = nullptr;
+  auto set_rows = [&](int j) {
+    const int nb = (int)blockIdx.x + j * G;
+    if (PK) {
+      // Tile-major packed weights: per (tile, quad) 1152 words — 4 x 256
+      // words of nibbles in load order, then 32 rows x (4 s, 4 b) bf16.
+      wrow = W + (size_t)nb * Q * kPackQuadWords + lane * 4;
+      srow = reinterpret_cast<const uint16_t*>(W + (size_t)nb * Q * kPackQuadWords + 1024 + c32 * 4);
+      brow = nullptr;
+    } else {
+      const int n = nb * 32 + c32;
+      const int nrow = n < p.N ? n : 0;
+      wrow = W + (size_t)nrow * (p.K >> 3) + kq * 4 + 32 * kw;
+      srow = Sc + (size_t)nrow * sgroups + (GSH == 0 ? 4 : 2) * kw;
+      brow = Bi + (size_t)nrow * sgroups + (GSH == 0 ? 4 : 2) * kw;
+    }
+  };
+  set_rows(0);
+  // Loads the iterator's current item, then advances it (past the end it
+  // keeps re-reading the last item, whose registers are never used).
+  auto load_next = [&](QuadRegs& qr) {
+    if (PK) {
+      const size_t qoff = (size_t)(kw + KS * t_pf) * kPackQuadWords;
+      const uint32_t* wp = wrow + qoff;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) qr.w[u] = *reinterpret_cast<const uint4*>(wp + 256 * u);
+      const uint4 sb = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(srow) + qoff);
+      qr.s[0] = sb.x; qr.s[1] = sb.y;
+      qr.b[0] = sb.z; qr.b[1] = sb.w;
+    } else {
+      const uint32_t* wp = wrow + 32 * KS * t_pf;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) qr.w[u] = *reinterpret_cast<const uint4*>(wp + 8 * u);
+      if (GSH == 0) {
+        const uint2 sv = *reinterpret_cast<const uint2*>(srow + 4 * KS * t_pf);
+        const uint2 bv = *reinterpret_cast<const uint2*>(brow + 4 * KS * t_pf);
+        qr.s[0] = sv.x; qr.s[1] = sv.y;
+        qr.b[0] = bv.x; qr.b[1] = bv.y;
+      } else {
+        qr.s[0] = *reinterpret_cast<const uint32_t*>(srow + 2 * KS * t_pf);
+        qr.b[0] = *reinterpret_cast<const uint32_t*>(brow + 2 * KS * t_pf);
+        qr.s[1] = qr.s[0];
+        qr.b[1] = qr.b[0];
+      }
+    }
+    if (left_pf > 1) {
+      --left_pf;
+      if (++t_pf == qw) {
+        t_pf = 0;
+        set_rows(++j_pf);
+      }
+    }
+  };
+
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+
+  auto compute = [&](const QuadRegs& cr, int t) {
+    const int gq = 4 * (kw + t * KS);
+#pragma unroll
+    for (int u = 0; u < 4; u += 2) {
+      f32x16 G0 = {}, G1 = {};
+      const uint32_t w0[4] = {cr.w[u].x, cr.w[u].y, cr.w[u].z, cr.w[u].w};
+      const uint32_t w1[4] = {cr.w[u + 1].x, cr.w[u + 1].y, cr.w[u + 1].z, cr.w[u + 1].w};
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const uint32_t a0off = xa_base + (uint32_t)((gq + u) * 4 + ii) * xa_step;
+        const uint32_t a1off = xa_base + (uint32_t)((gq + u + 1) * 4 + ii) * xa_step;
+        const bf16x8 a0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(smem + a0off));
+        const bf16x8 a1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(smem + a1off));
+        G0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, nibbles_to_bf16(w0[ii], nc), G0, 0, 0, 0);
+        G1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, nibbles_to_bf16(w1[ii], nc), G1, 0, 0, 0);
+      }
+      const uint32_t sw0 = (GSH == 0) ? cr.s[u >> 1] : cr.s[0];
+      const uint32_t bw0 = (GSH == 0) ? cr.b[u >> 1] : cr.b[0];
+      const float s0 = bf2f((uint16_t)((GSH == 0) ? (sw0 & 0xffff) : (u < 2 ? (sw0 & 0xffff) : (sw0 >> 16))));
+      const float s1 = bf2f((uint16_t)((GSH == 0) ? (sw0 >> 16) : (u < 2 ? (sw0 & 0xffff) : (sw0 >> 16))));
+      const float b0 = bf2f((uint16_t)((GSH == 0) ? (bw0 & 0xffff) : (u < 2 ? (bw0 & 0xffff) : (bw0 >> 16))));
+      const float b1 = bf2f((uint16_t)((GSH == 0) ? (bw0 >> 16) : (u < 2 ? (bw0 & 0xffff) : (bw0 >> 16))));
+      const float cb0 = b0 - 128.f * s0;
+      const float cb1 = b1 - 128.f * s1;
+      const float* xr0 = xs + (gq + u) * XSW + 4 * kq;
+      const float* xr1 = xs + (gq + u + 1) * XSW + 4 * kq;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int off = 8 * (r >> 2) + (r & 3);
+        acc[r] = fmaf(s0, G0[r], fmaf(cb0, xr0[off], acc[r]));
+        acc[r] = fmaf(s1, G1[r], fmaf(cb1, xr1[off], acc[r]));
+      }
+    }
+  };
+
+  // End of tile j: reduce the K-split waves in LDS (wave order), epilogue.
+  auto finish = [&](int j) {
+    const int nb = (int)blockIdx.x + j * G;
+    const bool valid = nb * 32 + c32 < p.N;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int m = 8 * (r >> 2) + 4 * kq + (r & 3);
+      if (m < M) red[(wave * M + m) * 32 + c32] = valid ? acc[r] : 0.f;
+      acc[r] = 0.f;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < M * 64; idx += NT) {
+      const int m = idx >> 6;
+      const int cc = idx & 63;
+      const int mat = cc >> 5;
+      float v = 0.f;
+      if (!dual && mat == 0) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += red[(w * M + m) * 32 + cc];
+      } else if (dual) {
+#pragma unroll
+        for (int w = 0; w < KS; ++w) v += red[((mat * KS + w) * M + m) * 32 + (cc & 31)];
+      }
+      fin[idx] = v;
+    }
+    __syncthreads();
+    qmm_epilogue<NW, EM>(p, fin, nb, M, 0);
+  };
+
+  QuadRegs A, B, C;
+  if (qw > 0) {
+    load_next(A);
+    load_next(B);
+  }
+  // ---- stage all of x once: MFMA A order + per-group sums ----
+  // Thread item = one 16 B chunk (8 values) of one row: consecutive threads
+  // read consecutive chunks (coalesced); the 8 chunks of a 64-group are 8
+  // adjacent lanes, whose sums meet in a fixed xor-shuffle tree.
+  {
+    const int cpr = p.K >> 3;                   // chunks per row
+    const int total = M * cpr;
+    constexpr int SU = 8;                       // chunks per thread in flight
+    // (row, chunk) of this thread's item, advanced by NT per item without
+    // dividing (one division at the start).
+    int m_it = tid / cpr, c_it = tid - (tid / cpr) * cpr;
+    for (int base = 0; base < total; base += NT * SU) {
+      uint4 raw[SU], raw2[SU];
+      int mu[SU], cu[SU];
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        mu[u] = m_it;
+        cu[u] = c_it;
+        c_it += NT;
+        while (c_it >= cpr) {
+          c_it -= cpr;
+          ++m_it;
+        }
+        raw[u] = raw2[u] = make_uint4(0, 0, 0, 0);
+        if (mu[u] < M) {
+          const size_t xo = (size_t)mu[u] * p.ldx + 8 * cu[u];
+          raw[u] = *reinterpret_cast<const uint4*>(p.x + xo);
+          raw2[u] = producer_aux<XM>(p, xo, 8 * cu[u]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        const bool ok = mu[u] < M;
+        const int m = ok ? mu[u] : 0;
+        const int gl = cu[u] >> 3, cc = cu[u] & 7;
+        float sum = 0.f;
+        const uint4 o = produce_chunk<XM>(raw[u], raw2[u], (XM == X_RMSNORM) ? s_inv_rms[m] : 1.f, sum);
+        if (ok) xa[((gl * 4 + (cc & 3)) * 2 + (cc >> 2)) * M + m] = o;
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        sum += __shfl_xor(sum, 4, 64);
+        if (ok && cc == 0) xs[gl * XSW + m] = sum;
+      }
+    }
+    for (int idx = tid; idx < 4 * Q * XSW; idx += NT)
+      if ((idx % XSW) >= M) xs[idx] = 0.f;
+  }
+  __syncthreads();  // staged x visible to every wave
+
+  // Every wave of the workgroup must reach each tile's barriers: waves with
+  // fewer quads per tile (qw smaller) still finish every tile.
+  if (qw == 0) {
+    for (int j = 0; j < ntiles; ++j) finish(j);
+    return;
+  }
+  // One exit, at the bottom: a break after each step would be merged by the
+  // control-flow structurizer into the latch, and the waitcnt analysis would
+  // then see the ring's newest loads as pending at the loop head and drain
+  // the whole ring there (vmcnt(0)) every iteration. Steps past the end are
+  // skipped by a uniform branch instead.
+  int i = 0, t = 0, j = 0;
+  auto step = [&](const QuadRegs& cur) {
+    if (i < nitems) {
+      compute(cur, t);
+      if (++t == qw) {
+        finish(j);
+        t = 0;
+        ++j;
+      }
+      ++i;
+    }
+  };
+  do {
+    load_next(C);
+    step(A);
+    load_next(A);
+    step(B);
+    load_next(B);
+    step(C);
+  } while (i < nitems);
 }
 
 // ---------------------------------------------------------------------------
 // Host side: split planning and dispatch.
 
 struct Plan {
-  int n_blocks, chunk;
+  int n_blocks, chunk, nw;
+  bool resident;
   size_t lds;
 };
 
@@ -393,11 +971,13 @@ static int env_int(const char* name, int dflt) {
   return (v && *v) ? atoi(v) : dflt;
 }
 
-// LDS: staged x per quad (4 groups x (8*M*16 B + 32 floats)); the K-split
-// reduction (16 KiB + fin) reuses the same area afterwards.
-static size_t lds_bytes(int chunk_q, int M) {
+static int r_of(int M) { return M <= 8 ? 4 : (M <= 16 ? 8 : 16); }
+
+// LDS of the gathered (chunked) kernel: staged x per quad (4 groups x
+// (8*M*16 B + 32 floats)); the K-split reduction reuses the same area.
+static size_t lds_bytes(int chunk_q, int M, int nw) {
   size_t stage = (size_t)chunk_q * 4 * (8 * M * 16 + 32 * 4);
-  size_t red = 4 * 32 * 32 * 4 + (size_t)M * 64 * 4;
+  size_t red = (size_t)nw * 32 * 32 * 4 + (size_t)M * 64 * 4;
   return stage > red ? stage : red;
 }
 
@@ -406,27 +986,98 @@ static int max_chunk_quads(int M) {
   return ch < 1 ? 1 : ch;
 }
 
+// LDS of the streaming kernels: staged x (+ 2R group sums per group), the
+// wave partials [NW][M][32], the finished tile [M][64] and a 16 B zero block.
+static size_t stream_lds(int chunk_q, int M, int nw) {
+  return (size_t)chunk_q * 4 * (8 * M * 16 + 2 * r_of(M) * 4) + (size_t)nw * M * 32 * 4 + (size_t)M * 64 * 4 + 16;
+}
+
+static constexpr size_t kLdsMax = 160 * 1024 - 256;   // gfx950: 160 KiB of LDS per CU
+
+static constexpr size_t kLdsBudget = 65536 - 256;
+
+// Waves per workgroup: 8 when the column tiles alone cannot give every CU
+// two workgroups (small N: q|k|v, o, down), else 4. All of K is staged once
+// per workgroup when it fits in LDS, else in chunks per tile.
 static Plan make_plan(int M, int N, int K) {
   Plan pl;
   pl.n_blocks = cdiv(N, 32);
   const int Q = K / 256;
-  int ch = max_chunk_quads(M);
+  const int nw_env = env_int("MTPLX_AMD_QMV_WAVES", 0);
+  pl.nw = (nw_env == 4 || nw_env == 8) ? nw_env : (pl.n_blocks < 512 ? 8 : 4);
   const int cap = env_int("MTPLX_AMD_QMV_CHUNK_QUADS", 0);
-  if (cap > 0 && cap < ch) ch = cap;
-  pl.chunk = ch < Q ? ch : Q;
-  pl.lds = lds_bytes(pl.chunk, M);
+  pl.resident = cap <= 0 && stream_lds(Q, M, pl.nw) <= kLdsMax;
+  if (pl.resident) {
+    pl.chunk = Q;
+  } else {
+    int ch = Q;
+    while (ch > 1 && stream_lds(ch, M, pl.nw) > kLdsBudget) --ch;
+    if (cap > 0 && cap < ch) ch = cap;
+    pl.chunk = ch;
+  }
+  pl.lds = stream_lds(pl.chunk, M, pl.nw);
   return pl;
+}
+
+static int device_cus() {
+  static thread_local int dev_cached = -1, cus = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev != dev_cached) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    dev_cached = dev;
+  }
+  return cus;
+}
+
+// Grid of the streaming kernel: every column tile once when they fit in the
+// resident workgroups, else as many workgroups as stay resident (each then
+// loops over several tiles).
+template <typename K>
+static int stream_grid(K kernel, int nt, size_t lds, int n_blocks) {
+  const int forced = env_int("MTPLX_AMD_QMV_GRID", 0);
+  if (forced > 0) return forced < n_blocks ? forced : n_blocks;
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, nt, lds) != hipSuccess || occ < 1) occ = 1;
+  const int resident = occ * device_cus();
+  return n_blocks < resident ? n_blocks : resident;
+}
+
+template <typename K>
+static void launch_one(K k, const Plan& pl, int nt, hipStream_t st, const QmmParams& q) {
+  if (pl.lds > 65536) hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl.lds);
+  hipLaunchKernelGGL(k, dim3(stream_grid(k, nt, pl.lds, pl.n_blocks)), dim3(nt), pl.lds, st, q);
+}
+
+template <int NW, int R, int XM, int EM, int GSH>
+static void launch_rk(const QmmParams& q, const Plan& pl, hipStream_t st) {
+  if (q.packed)
+    launch_one(qmv_stream_kernel<NW, R, XM, EM, 0, true>, pl, NW * 64, st, q);
+  else if (pl.resident)
+    launch_one(qmv_stream_kernel<NW, R, XM, EM, GSH, false>, pl, NW * 64, st, q);
+  else
+    launch_one(qmv_chunked_kernel<NW, R, XM, EM, GSH>, pl, NW * 64, st, q);
+}
+
+template <int NW, int XM, int EM, int GSH>
+static void launch_n(const QmmParams& p, const Plan& pl, hipStream_t st) {
+  QmmParams q = p;
+  q.n_blocks = pl.n_blocks;
+  if (p.M <= 8)
+    launch_rk<NW, 4, XM, EM, GSH>(q, pl, st);
+  else if (p.M <= 16)
+    launch_rk<NW, 8, XM, EM, GSH>(q, pl, st);
+  else
+    launch_rk<NW, 16, XM, EM, GSH>(q, pl, st);
 }
 
 template <int XM, int EM, int GSH>
 static void launch_r(const QmmParams& p, const Plan& pl, hipStream_t st) {
-  dim3 grid(pl.n_blocks), block(kThreads);
-  if (p.M <= 8)
-    hipLaunchKernelGGL((qmm4_kernel<4, XM, EM, GSH>), grid, block, pl.lds, st, p);
-  else if (p.M <= 16)
-    hipLaunchKernelGGL((qmm4_kernel<8, XM, EM, GSH>), grid, block, pl.lds, st, p);
+  if (pl.nw == 8)
+    launch_n<8, XM, EM, GSH>(p, pl, st);
   else
-    hipLaunchKernelGGL((qmm4_kernel<16, XM, EM, GSH>), grid, block, pl.lds, st, p);
+    launch_n<4, XM, EM, GSH>(p, pl, st);
 }
 
 template <int XM, int GSH>
@@ -465,18 +1116,20 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
     set_error("%s: group_size %d unsupported (64 or 128)", who, p.gs);
     return MTP_ERR_UNSUPPORTED;
   }
-  if (!p.x || !p.w0 || !p.s0 || !p.b0 || (!p.y0 && !p.yf)) {
+  if (!p.x || !p.w0 || (!p.packed && (!p.s0 || !p.b0)) || (!p.y0 && !p.yf)) {
     set_error("%s: null pointer argument", who);
     return MTP_ERR_ARG;
   }
-  if (p.ldx < p.K || p.ldx % 8 || !aligned16(p.x) || !aligned16(p.w0) || ((uintptr_t)p.s0 & 7) ||
-      ((uintptr_t)p.b0 & 7) || (p.x2 && xm == X_SWIGLU && !aligned16(p.x2))) {
+  if (p.ldx < p.K || p.ldx % 8 || !aligned16(p.x) || !aligned16(p.w0) ||
+      (!p.packed && (((uintptr_t)p.s0 & 7) || ((uintptr_t)p.b0 & 7))) ||
+      (p.x2 && xm == X_SWIGLU && !aligned16(p.x2))) {
     set_error("%s: x rows/weights must be 16-byte and scales/biases 8-byte aligned, ldx %% 8 == 0 (ldx=%d)", who,
               p.ldx);
     return MTP_ERR_ARG;
   }
   const bool dual = (em == E_DUAL || em == E_DUAL_SWIGLU);
-  if (dual && (!p.w1 || !p.s1 || !p.b1 || !aligned16(p.w1) || ((uintptr_t)p.s1 & 7) || ((uintptr_t)p.b1 & 7))) {
+  if (dual && (!p.w1 || !aligned16(p.w1) ||
+               (!p.packed && (!p.s1 || !p.b1 || ((uintptr_t)p.s1 & 7) || ((uintptr_t)p.b1 & 7))))) {
     set_error("%s: dual mode needs a second aligned weight triple", who);
     return MTP_ERR_ARG;
   }
@@ -499,6 +1152,11 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
   (void)ws;
   (void)ws_bytes;
   Plan pl = make_plan(p.M, p.N, p.K);
+  if (p.packed && !pl.resident) {
+    set_error("%s: packed weights need all of x in LDS (M=%d, K=%d too large); use the unpacked layout", who,
+              p.M, p.K);
+    return MTP_ERR_UNSUPPORTED;
+  }
   p.chunk = pl.chunk;
   if (p.gs == 64)
     launch_x<0>(xm, em, p, pl, st);
@@ -547,10 +1205,11 @@ MTP_API int mtp_qmv_affine4(const void* x, const void* w, const void* scales, co
 }
 
 MTP_API int mtp_qmv_affine4_residual(const void* x, const void* w, const void* scales, const void* biases,
-                                     const void* resid, void* y, int M, int N, int K, int group_size, void* ws,
-                                     size_t ws_bytes, void* stream) {
+                                     const void* resid, void* y, float* ss_out, int M, int N, int K, int group_size,
+                                     void* ws, size_t ws_bytes, void* stream) {
   QmmParams p = base_params(x, w, scales, biases, y, M, N, K, group_size);
   p.resid = (const uint16_t*)resid;
+  p.ss_out = ss_out;
   return qmm_dispatch(X_PLAIN, E_RESID, p, ws, ws_bytes, (hipStream_t)stream, "mtp_qmv_affine4_residual");
 }
 
@@ -576,33 +1235,39 @@ MTP_API int mtp_qmv_affine4_swiglu_in(const void* gate, const void* up, const vo
                       "mtp_qmv_affine4_swiglu_in");
 }
 
-MTP_API int mtp_qmv_affine4_rmsnorm_in(const void* x, const void* norm_w, float eps, const void* w,
+MTP_API int mtp_qmv_affine4_rmsnorm_in(const void* x, const void* norm_w, const float* ss_in, float eps, const void* w,
                                        const void* scales, const void* biases, void* y, int M, int N, int K,
                                        int group_size, void* ws, size_t ws_bytes, void* stream) {
   QmmParams p = base_params(x, w, scales, biases, y, M, N, K, group_size);
   p.x2 = (const uint16_t*)norm_w;
   p.eps = eps;
+  p.ss_in = ss_in;
+  p.ss_parts = cdiv(K, 32);
   return qmm_dispatch(X_RMSNORM, E_STORE, p, ws, ws_bytes, (hipStream_t)stream, "mtp_qmv_affine4_rmsnorm_in");
 }
 
-MTP_API int mtp_qmv_affine4_rmsnorm_f32(const void* x, const void* norm_w, float eps, const void* w,
+MTP_API int mtp_qmv_affine4_rmsnorm_f32(const void* x, const void* norm_w, const float* ss_in, float eps, const void* w,
                                         const void* scales, const void* biases, float* y, int M, int N, int K,
                                         int group_size, void* ws, size_t ws_bytes, void* stream) {
   QmmParams p = base_params(x, w, scales, biases, nullptr, M, N, K, group_size);
   p.x2 = (const uint16_t*)norm_w;
   p.eps = eps;
+  p.ss_in = ss_in;
+  p.ss_parts = cdiv(K, 32);
   p.yf = y;
   return qmm_dispatch(norm_w ? X_RMSNORM : X_PLAIN, E_STORE, p, ws, ws_bytes, (hipStream_t)stream,
                       "mtp_qmv_affine4_rmsnorm_f32");
 }
 
-MTP_API int mtp_qmv_affine4_rmsnorm_dual(const void* x, const void* norm_w, float eps, const void* w0,
+MTP_API int mtp_qmv_affine4_rmsnorm_dual(const void* x, const void* norm_w, const float* ss_in, float eps, const void* w0,
                                          const void* s0, const void* b0, const void* w1, const void* s1,
                                          const void* b1, void* y, int M, int N, int K, int group_size, void* ws,
                                          size_t ws_bytes, void* stream) {
   QmmParams p = base_params(x, w0, s0, b0, y, M, N, K, group_size);
   p.x2 = (const uint16_t*)norm_w;
   p.eps = eps;
+  p.ss_in = ss_in;
+  p.ss_parts = cdiv(K, 32);
   p.w1 = (const uint32_t*)w1;
   p.s1 = (const uint16_t*)s1;
   p.b1 = (const uint16_t*)b1;
@@ -691,8 +1356,15 @@ MTP_API int mtp_gather_qmv_affine4(const void* x, const void* x2, const uint32_t
   p.s_estride = (long long)rows_per_expert * (K / group_size);
   const int mrows = max_rows_per_expert < 32 ? max_rows_per_expert : 32;
   p.row_tiles = cdiv(max_rows_per_expert, 32);
-  Plan pl = make_plan(mrows, N, K);
+  Plan pl;
+  pl.n_blocks = cdiv(N, 32);
+  {
+    const int Q = K / 256;
+    const int ch = max_chunk_quads(mrows);
+    pl.chunk = ch < Q ? ch : Q;
+  }
   p.chunk = pl.chunk;
+  pl.lds = lds_bytes(pl.chunk, mrows, 4);
   dim3 grid(pl.n_blocks, p.row_tiles, E);
   hipStream_t st = (hipStream_t)stream;
 #define MTP_GATHER(RR, XMV, EMV)                                                                            \
@@ -713,4 +1385,121 @@ MTP_API int mtp_gather_qmv_affine4(const void* x, const void* x2, const uint32_t
   }
 #undef MTP_GATHER
   return launch_check(who);
+}
+
+// ---------------------------------------------------------------------------
+// Tile-major packing of a 4-bit affine matrix for the streaming kernel.
+// Per (32-row tile nb, 256-k quad q), 1152 words:
+//   words [256u + 4l, +4)  = row 32nb + l%32, words 32q + 8u + 4*(l/32) .. +3
+//                            (u = 0..3, lane l = 0..63: the order one wave
+//                            instruction reads, 1 KiB contiguous);
+//   words [1024 + 4c, +4)  = row 32nb + c: scales of groups 4q..4q+3 then
+//                            biases (bf16; group 128 repeats each value).
+// Rows past N are zero (their outputs are never stored).
+__global__ void pack_affine4_kernel(const uint32_t* w, const uint16_t* s, const uint16_t* b, uint32_t* out, int N,
+                                    int K, int gshift) {
+  const int Q = K >> 8;
+  const size_t units = (size_t)cdiv(N, 32) * Q * 288;   // 16 B units
+  for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < units; t += (size_t)gridDim.x * blockDim.x) {
+    const size_t tq = t / 288;
+    const int u16 = (int)(t - tq * 288);
+    const int nb = (int)(tq / Q);
+    const int q = (int)(tq - (size_t)nb * Q);
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (u16 < 256) {
+      const int u = u16 >> 6, l = u16 & 63;
+      const int row = nb * 32 + (l & 31);
+      if (row < N) v = *reinterpret_cast<const uint4*>(w + (size_t)row * (K >> 3) + 32 * q + 8 * u + 4 * (l >> 5));
+    } else {
+      const int c = u16 - 256;
+      const int row = nb * 32 + c;
+      if (row < N) {
+        const int sg = K >> (6 + gshift);
+        const uint16_t* sr = s + (size_t)row * sg;
+        const uint16_t* br = b + (size_t)row * sg;
+        uint16_t e[8];
+        for (int g = 0; g < 4; ++g) {
+          const int gi = (4 * q + g) >> gshift;
+          e[g] = sr[gi];
+          e[4 + g] = br[gi];
+        }
+        v.x = e[0] | ((uint32_t)e[1] << 16);
+        v.y = e[2] | ((uint32_t)e[3] << 16);
+        v.z = e[4] | ((uint32_t)e[5] << 16);
+        v.w = e[6] | ((uint32_t)e[7] << 16);
+      }
+    }
+    *reinterpret_cast<uint4*>(out + tq * kPackQuadWords + 4 * (size_t)u16) = v;
+  }
+}
+
+MTP_API size_t mtp_pack_affine4_bytes(int N, int K) {
+  if (N < 1 || K < 256 || K % 256) return 0;
+  return (size_t)cdiv(N, 32) * (K / 256) * kPackQuadWords * 4;
+}
+
+MTP_API int mtp_pack_affine4(const void* w, const void* scales, const void* biases, void* out, int N, int K,
+                             int group_size, void* stream) {
+  if (!w || !scales || !biases || !out || N < 1 || K < 256 || K % 256 || !aligned16(w) || !aligned16(out)) {
+    set_error("mtp_pack_affine4: bad arguments (K %% 256 == 0, 16-byte aligned w/out)");
+    return MTP_ERR_ARG;
+  }
+  if (group_size != 64 && group_size != 128) {
+    set_error("mtp_pack_affine4: group_size %d unsupported", group_size);
+    return MTP_ERR_UNSUPPORTED;
+  }
+  const size_t units = (size_t)cdiv(N, 32) * (K / 256) * 288;
+  size_t grid = (units + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  hipLaunchKernelGGL(pack_affine4_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+                     (const uint32_t*)w, (const uint16_t*)scales, (const uint16_t*)biases, (uint32_t*)out, N, K,
+                     group_size == 128 ? 1 : 0);
+  return launch_check("mtp_pack_affine4");
+}
+
+struct mtp_qmv_args {
+  const void* x;
+  const void* x2;
+  const float* ss_in;
+  const void* w0;
+  const void* s0;
+  const void* b0;
+  const void* w1;
+  const void* s1;
+  const void* b1;
+  void* y0;
+  void* y1;
+  float* yf;
+  const void* resid;
+  float* ss_out;
+  float eps;
+  int M, N, K, group_size, ldx, ldy;
+  int xmode, emode, packed;
+};
+
+MTP_API int mtp_qmv_affine4_ex(const mtp_qmv_args* a, void* stream) {
+  if (!a) {
+    set_error("mtp_qmv_affine4_ex: null argument block");
+    return MTP_ERR_ARG;
+  }
+  if (a->xmode < 0 || a->xmode > 2 || a->emode < 0 || a->emode > 3) {
+    set_error("mtp_qmv_affine4_ex: xmode %d / emode %d out of range", a->xmode, a->emode);
+    return MTP_ERR_ARG;
+  }
+  QmmParams p = base_params(a->x, a->w0, a->s0, a->b0, a->y0, a->M, a->N, a->K, a->group_size);
+  p.x2 = (const uint16_t*)a->x2;
+  p.ss_in = a->ss_in;
+  p.ss_parts = cdiv(a->K, 32);
+  p.w1 = (const uint32_t*)a->w1;
+  p.s1 = (const uint16_t*)a->s1;
+  p.b1 = (const uint16_t*)a->b1;
+  p.y1 = (uint16_t*)a->y1;
+  p.yf = a->yf;
+  p.resid = (const uint16_t*)a->resid;
+  p.ss_out = a->ss_out;
+  p.eps = a->eps;
+  p.packed = a->packed;
+  if (a->ldx > 0) p.ldx = a->ldx;
+  if (a->ldy > 0) p.ldy = a->ldy;
+  return qmm_dispatch(a->xmode, a->emode, p, nullptr, 0, (hipStream_t)stream, "mtp_qmv_affine4_ex");
 }

@@ -24,6 +24,24 @@ class QuantizedLinear:
         self.bits = int(bits)
         self.mode = mode
         self.bias = bias
+        self.packed: torch.Tensor | None = None
+
+    def pack(self) -> torch.Tensor:
+        """Tile-major copy of the weights for the streaming kernel (made once, cached)."""
+        if self.packed is None:
+            from . import _lib
+
+            if self.weight.dim() != 2 or self.bits != 4 or self.mode != "affine":
+                raise NotImplementedError("packing covers 2-D 4-bit affine layers")
+            n, k = self.out_features, self.in_features
+            nbytes = _lib.query("mtp_pack_affine4_bytes", n, k)
+            if nbytes == 0:
+                raise NotImplementedError(f"cannot pack N={n} K={k} (K must be a multiple of 256)")
+            out = torch.empty(nbytes // 4, dtype=torch.int32, device=self.weight.device)
+            _lib.call("mtp_pack_affine4", self.weight.data_ptr(), self.scales.data_ptr(), self.biases.data_ptr(),
+                      out.data_ptr(), n, k, self.group_size, _lib.stream_handle(self.weight.device))
+            self.packed = out
+        return self.packed
 
     @property
     def in_features(self) -> int:

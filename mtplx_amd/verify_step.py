@@ -117,6 +117,12 @@ class VerifyModel:
             self.layers.append(L)
         self.final_norm = _norm_weight(c.hidden, gen, device)
         self.lm_head = QuantizedLinear.random(c.vocab, c.hidden, gs, generator=gen, device=device)
+        # Tile-major copies for the streaming verify matmul (one pass at load time).
+        for L in self.layers:
+            for q in (L.qkv, L.o, L.gate, L.up, L.down, L.shared_gate, L.shared_up, L.shared_down):
+                if q is not None:
+                    q.pack()
+        self.lm_head.pack()
         self.k_cache: list[torch.Tensor] = []
         self.v_cache: list[torch.Tensor] = []
         self.cap = 0
@@ -175,34 +181,41 @@ class VerifyModel:
         attn = torch.empty((M, c.n_heads * c.head_dim), dtype=torch.bfloat16, device=dev)
         ffn = c.expert_ffn if c.n_experts else c.ffn
         act = torch.empty((M, ffn), dtype=torch.bfloat16, device=dev)
+        # Sum-of-squares statistics of h handed from each residual epilogue to the
+        # next fused RMSNorm (two buffers so a producer never overwrites what its
+        # consumer has not read yet). None for the embedding output.
+        ss_a = torch.empty(((H + 31) // 32) * 32, dtype=torch.float32, device=dev)
+        ss_b = torch.empty_like(ss_a)
+        ss_h = None
         nb = _lib.query("mtp_attn_workspace_bytes", B, c.n_kv_heads, self.cap, 0)
         aws = _lib.WORKSPACES.get(nb, "attn", dev)
         scale = 1.0 / math.sqrt(c.head_dim)
         ql = None if q_lens is None else q_lens.to(torch.int32).contiguous()
+        qmv = _lib.qmv_ex
         for li, L in enumerate(self.layers):
-            call("mtp_qmv_affine4_rmsnorm_in", h.data_ptr(), L.in_norm.data_ptr(), eps, L.qkv.weight.data_ptr(),
-                 L.qkv.scales.data_ptr(), L.qkv.biases.data_ptr(), qkv.data_ptr(), M, c.qkv_out, H, gs, None, 0, st)
+            qmv(st, x=h, x2=L.in_norm, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv.packed, y0=qkv, M=M, N=c.qkv_out, K=H,
+                group_size=gs, xmode=2, emode=0, packed=1)
             call("mtp_rope_qkv_to_cache", qkv.data_ptr(), q_start.data_ptr(), _lib.ptr(ql), qh.data_ptr(),
                  self.k_cache[li].data_ptr(), self.v_cache[li].data_ptr(), B, Lq, c.n_heads, c.n_kv_heads,
                  c.head_dim, self.cap, ctypes.c_float(c.rope_theta), status.data_ptr(), st)
             call("mtp_ragged_gqa_attn_rows", qh.data_ptr(), self.k_cache[li].data_ptr(),
                  self.v_cache[li].data_ptr(), q_start.data_ptr(), _lib.ptr(ql), attn.data_ptr(), B, c.n_heads,
                  c.n_kv_heads, Lq, c.head_dim, self.cap, ctypes.c_float(scale), 0, aws.data_ptr(), aws.numel(), st)
-            call("mtp_qmv_affine4_residual", attn.data_ptr(), L.o.weight.data_ptr(), L.o.scales.data_ptr(),
-                 L.o.biases.data_ptr(), h.data_ptr(), h.data_ptr(), M, H, c.n_heads * c.head_dim, gs, None, 0, st)
+            qmv(st, x=attn, w0=L.o.packed, resid=h, y0=h, ss_out=ss_a, M=M, N=H, K=c.n_heads * c.head_dim,
+                group_size=gs, xmode=0, emode=1, packed=1)
+            ss_h = ss_a
             if c.n_experts:
                 self._moe_block(L, h, M, st)
+                ss_h = None
             else:
-                call("mtp_qmv_affine4_rmsnorm_dual", h.data_ptr(), L.post_norm.data_ptr(), eps,
-                     L.gate.weight.data_ptr(), L.gate.scales.data_ptr(), L.gate.biases.data_ptr(),
-                     L.up.weight.data_ptr(), L.up.scales.data_ptr(), L.up.biases.data_ptr(), act.data_ptr(), M,
-                     c.ffn, H, gs, None, 0, st)
-                call("mtp_qmv_affine4_residual", act.data_ptr(), L.down.weight.data_ptr(), L.down.scales.data_ptr(),
-                     L.down.biases.data_ptr(), h.data_ptr(), h.data_ptr(), M, H, c.ffn, gs, None, 0, st)
+                qmv(st, x=h, x2=L.post_norm, ss_in=ss_h, eps=c.rms_eps, w0=L.gate.packed, w1=L.up.packed, y0=act,
+                    M=M, N=c.ffn, K=H, group_size=gs, xmode=2, emode=3, packed=1)
+                qmv(st, x=act, w0=L.down.packed, resid=h, y0=h, ss_out=ss_b, M=M, N=H, K=c.ffn, group_size=gs,
+                    xmode=0, emode=1, packed=1)
+                ss_h = ss_b
         logits = logits_out if logits_out is not None else torch.empty((M, c.vocab), dtype=torch.float32, device=dev)
-        call("mtp_qmv_affine4_rmsnorm_f32", h.data_ptr(), self.final_norm.data_ptr(), eps,
-             self.lm_head.weight.data_ptr(), self.lm_head.scales.data_ptr(), self.lm_head.biases.data_ptr(),
-             logits.data_ptr(), M, c.vocab, H, gs, None, 0, st)
+        qmv(st, x=h, x2=self.final_norm, ss_in=ss_h, eps=c.rms_eps, w0=self.lm_head.packed, yf=logits, M=M,
+            N=c.vocab, K=H, group_size=gs, xmode=2, emode=0, packed=1)
         self._status = status
         return logits
 
@@ -244,8 +257,8 @@ class VerifyModel:
              L.shared_up.biases.data_ptr(), sh_act.data_ptr(), None, M, c.shared_ffn, H, gs, 1, None, 0, st)
         shared = torch.empty_like(h)
         call("mtp_qmv_affine4_residual", sh_act.data_ptr(), L.shared_down.weight.data_ptr(),
-             L.shared_down.scales.data_ptr(), L.shared_down.biases.data_ptr(), h.data_ptr(), shared.data_ptr(), M, H,
-             c.shared_ffn, gs, None, 0, st)
+             L.shared_down.scales.data_ptr(), L.shared_down.biases.data_ptr(), h.data_ptr(), shared.data_ptr(), None,
+             M, H, c.shared_ffn, gs, None, 0, st)
         out = moe_combine(ysorted, es, wts, shared)
         h.copy_(out)
 
@@ -255,4 +268,37 @@ class VerifyModel:
         (``tokens[:, 1:]`` are the draft ids). Returns the device-side accept result."""
         B, L = (int(s) for s in tokens.shape)
         logits = self.verify_logits(tokens, q_start)
+        self.last_logits = logits
         return spec_accept(logits.reshape(B, L, -1), draft_logits, tokens[:, 1:].contiguous(), uniforms, sampler)
+
+
+class CapturedVerifyStep:
+    """The whole verify step (embedding → layers → lm_head → accept/reject)
+    recorded once as a HIP graph on a dedicated stream and replayed per step,
+    so the ~7 launches per layer cost no host round trips.
+
+    The graph reads its inputs from the tensors given at capture time: update
+    them in place (``tokens.copy_(...)`` etc.) between replays. Workspaces are
+    created by an eager warm-up on the same stream, so the capture itself
+    allocates nothing but the step's own activations (from the graph pool).
+    """
+
+    def __init__(self, model: VerifyModel, tokens: torch.Tensor, q_start: torch.Tensor,
+                 draft_logits: torch.Tensor, uniforms: torch.Tensor, sampler: SamplerConfig = SamplerConfig()):
+        self.model = model
+        self.inputs = (tokens, q_start, draft_logits, uniforms)
+        self.stream = torch.cuda.Stream(device=model.device)
+        self.graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize(model.device)
+        with torch.cuda.stream(self.stream):
+            model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)     # warm-up: workspaces
+        self.stream.synchronize()
+        with torch.cuda.graph(self.graph, stream=self.stream):
+            self.result = model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)
+        self.logits = model.last_logits          # graph-owned output buffer
+        torch.cuda.synchronize(model.device)
+
+    def replay(self):
+        """Enqueue one step on the current stream's device; returns the (static) accept result."""
+        self.graph.replay()
+        return self.result

@@ -42,7 +42,7 @@ def test_size_queries_without_gpu(lib):
     lib.mtp_attn_workspace_bytes.restype = ctypes.c_size_t
     lib.mtp_qmv_workspace_bytes.restype = ctypes.c_size_t
     assert lib.mtp_sampler_workspace_bytes(7, 151936) == 7 * 38 * 536
-    assert lib.mtp_attn_workspace_bytes(8, 8, 32768, 0) == 8 * 8 * 64 * (32 * 128 + 64) * 4
+    assert lib.mtp_attn_workspace_bytes(8, 8, 32768, 0) == 8 * 8 * 32 * (32 * 128 + 64) * 4
     assert lib.mtp_qmv_workspace_bytes(4, 17408, 5120, 0) == 0
 
 

@@ -73,7 +73,8 @@ def test_gathered_swiglu_down_and_combine(gpu):
     want_y = OM.gather_qmm_rows(bits(h.reshape(-1, F)), np.arange(T * k), sorted_ids, *dn, 64)
     assert_close(bf16_values(y), want_y, what="down rows")
     out = moe_combine(y, es, torch.from_numpy(sc).cuda())
-    want_out = (want_y[inv.astype(np.int64)].reshape(T, k, H) * sc[:, :, None]).sum(axis=1)
+    yv = bf16_values(y)     # the combine is checked on the stored (bf16) expert outputs
+    want_out = (yv[inv.astype(np.int64)].reshape(T, k, H) * sc[:, :, None]).sum(axis=1)
     assert_close(bf16_values(out), want_out, what="combine")
 
 

@@ -113,9 +113,14 @@ def test_residual_dual_swiglu_and_rmsnorm_variants(gpu):
     # residual
     r = randn_bf16(rng, (m, n))
     out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    ss = torch.full(((n // 32 + 1) * 32,), float("nan"), dtype=torch.float32, device="cuda")
     _lib.call("mtp_qmv_affine4_residual", x.data_ptr(), tw0.data_ptr(), ts0.data_ptr(), tb0.data_ptr(), r.data_ptr(),
-              out.data_ptr(), m, n, k, 64, ws.data_ptr(), W, st)
+              out.data_ptr(), ss.data_ptr(), m, n, k, 64, ws.data_ptr(), W, st)
     assert_close(bf16_values(out), round_to_bf16(y0) + bf16_values(r), what="residual")
+    ov = bf16_values(out)
+    ssn = ss.cpu().numpy()[: (n // 32) * 32].reshape(n // 32, 32)[:, :m]
+    assert np.allclose(ssn.sum(axis=0), (ov ** 2).sum(axis=1), rtol=1e-4), "row sums of squares"
+    assert np.allclose(ssn, (ov ** 2).reshape(m, n // 32, 32).sum(axis=2).T, rtol=1e-4), "per-block sums"
 
     # dual (two outputs) and dual swiglu
     o0 = torch.empty((m, n), dtype=torch.bfloat16, device="cuda"); o1 = torch.empty_like(o0)
@@ -145,21 +150,31 @@ def test_residual_dual_swiglu_and_rmsnorm_variants(gpu):
     xnb = f32_to_bf16_bits(xn.astype(np.float32))
     yn = qmm_affine4(xnb, w0, s0, b0, 64)
     o = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-    _lib.call("mtp_qmv_affine4_rmsnorm_in", x.data_ptr(), nw.data_ptr(), ctypes.c_float(1e-6), tw0.data_ptr(),
+    _lib.call("mtp_qmv_affine4_rmsnorm_in", x.data_ptr(), nw.data_ptr(), None, ctypes.c_float(1e-6), tw0.data_ptr(),
               ts0.data_ptr(), tb0.data_ptr(), o.data_ptr(), m, n, k, 64, ws.data_ptr(), W, st)
     assert_close(bf16_values(o), yn, what="rmsnorm-in")
     of = torch.empty((m, n), dtype=torch.float32, device="cuda")
-    _lib.call("mtp_qmv_affine4_rmsnorm_f32", x.data_ptr(), nw.data_ptr(), ctypes.c_float(1e-6), tw0.data_ptr(),
+    _lib.call("mtp_qmv_affine4_rmsnorm_f32", x.data_ptr(), nw.data_ptr(), None, ctypes.c_float(1e-6), tw0.data_ptr(),
               ts0.data_ptr(), tb0.data_ptr(), of.data_ptr(), m, n, k, 64, ws.data_ptr(), W, st)
     ofn = of.cpu().numpy().astype(np.float64)
     assert_close(ofn, yn, what="rmsnorm-f32")
     assert np.array_equal(round_to_bf16(ofn), ofn), "fp32 logits must carry bf16 values"
     hd = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-    _lib.call("mtp_qmv_affine4_rmsnorm_dual", x.data_ptr(), nw.data_ptr(), ctypes.c_float(1e-6), tw0.data_ptr(),
+    _lib.call("mtp_qmv_affine4_rmsnorm_dual", x.data_ptr(), nw.data_ptr(), None, ctypes.c_float(1e-6), tw0.data_ptr(),
               ts0.data_ptr(), tb0.data_ptr(), tw1.data_ptr(), ts1.data_ptr(), tb1.data_ptr(), hd.data_ptr(),
               m, n, k, 64, ws.data_ptr(), W, st)
     yn1 = qmm_affine4(xnb, w1, s1, b1, 64)
     assert_close(bf16_values(hd), silu(yn) * yn1, what="rmsnorm-dual-swiglu")
+
+    # statistics handed over from a residual producer give the same result
+    ssx = torch.empty((k // 32) * 32, dtype=torch.float32, device="cuda")
+    xsq = (xv ** 2).reshape(m, k // 32, 32).sum(axis=2).T                     # [k/32, m]
+    ssx_np = np.zeros((k // 32, 32), np.float32); ssx_np[:, :m] = xsq
+    ssx.copy_(torch.from_numpy(ssx_np.reshape(-1)))
+    o2 = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    _lib.call("mtp_qmv_affine4_rmsnorm_in", x.data_ptr(), nw.data_ptr(), ssx.data_ptr(), ctypes.c_float(1e-6),
+              tw0.data_ptr(), ts0.data_ptr(), tb0.data_ptr(), o2.data_ptr(), m, n, k, 64, ws.data_ptr(), W, st)
+    assert_close(bf16_values(o2), yn, what="rmsnorm-in with handed-over statistics")
 
 
 def test_bad_arguments_raise(gpu):
@@ -171,3 +186,78 @@ def test_bad_arguments_raise(gpu):
     with pytest.raises(_lib.MtpError):   # group size 32 is not on the GPU path
         _lib.call("mtp_qmv_affine4", x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
                   4, 8, 256, 32, None, 0, _stream())
+
+
+def _pack_reference(w, s, b, gs):
+    """NumPy restatement of the tile-major layout (include/mtplx_amd.h)."""
+    N, kw = w.shape
+    K = kw * 8
+    Q = K // 256
+    T = -(-N // 32)
+    out = np.zeros((T, Q, 1152), np.uint32)
+    sb = s.view(np.uint16); bb = b.view(np.uint16)
+    for nb in range(T):
+        for q in range(Q):
+            for u in range(4):
+                for l in range(64):
+                    row = nb * 32 + (l & 31)
+                    if row < N:
+                        out[nb, q, 256 * u + 4 * l: 256 * u + 4 * l + 4] = w[row, 32 * q + 8 * u + 4 * (l >> 5):][:4]
+            for c in range(32):
+                row = nb * 32 + c
+                if row < N:
+                    e = [sb[row, (4 * q + g) * 64 // gs] for g in range(4)] + [bb[row, (4 * q + g) * 64 // gs] for g in range(4)]
+                    e = np.array(e, np.uint16).view(np.uint32)
+                    out[nb, q, 1024 + 4 * c: 1024 + 4 * c + 4] = e
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("n,k,gs", [(70, 512, 64), (64, 768, 128)])
+def test_pack_layout_bit_exact(gpu, n, k, gs):
+    from mtplx_amd.quant import QuantizedLinear
+    rng = np.random.default_rng(n + k)
+    w, s, b = make_affine4_weights(rng, n, k, gs)
+    q = QuantizedLinear(u32(w), from_bits(s), from_bits(b), group_size=gs)
+    got = q.pack().cpu().numpy().view(np.uint32)
+    assert np.array_equal(got, _pack_reference(w, s, b, gs))
+
+
+@pytest.mark.parametrize("m,n,k,gs,xmode,emode", [
+    (4, 17408, 5120, 64, 0, 0), (4, 7168, 5120, 64, 2, 0), (4, 5120, 17408, 64, 0, 1),
+    (4, 1536, 2048, 64, 2, 3), (4, 300, 1024, 128, 0, 0), (8, 600, 1024, 64, 2, 3), (16, 256, 512, 64, 0, 1),
+    (4, 151936 // 8, 5120, 64, 2, 0)])
+def test_packed_path_bitwise_equals_unpacked(gpu, m, n, k, gs, xmode, emode):
+    """The tile-major path reads the same values in the same order as the MLX
+    layout path, so outputs must agree bit for bit (and hence with the oracle)."""
+    from mtplx_amd import _lib
+    from mtplx_amd.quant import QuantizedLinear
+    g = torch.Generator(device="cuda").manual_seed(m * 1000 + n)
+    q0 = QuantizedLinear.random(n, k, gs, generator=g)
+    q1 = QuantizedLinear.random(n, k, gs, generator=g)
+    x = torch.randn((m, k), device="cuda", generator=g).to(torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn(k, device="cuda", generator=g)).to(torch.bfloat16)
+    r = torch.randn((m, n), device="cuda", generator=g).to(torch.bfloat16)
+    st = _stream()
+    outs = []
+    for packed in (0, 1):
+        y0 = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+        y1 = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+        ss = torch.zeros(((n + 31) // 32) * 32, dtype=torch.float32, device="cuda")
+        kw = dict(x=x, x2=nw if xmode == 2 else None, eps=1e-6, M=m, N=n, K=k, group_size=gs, xmode=xmode,
+                  emode=emode, packed=packed, y0=y0, y1=y1 if emode == 2 else None,
+                  resid=r if emode == 1 else None, ss_out=ss if emode == 1 else None)
+        if packed:
+            kw.update(w0=q0.pack(), w1=q1.pack() if emode >= 2 else None)
+        else:
+            kw.update(w0=q0.weight, s0=q0.scales, b0=q0.biases, w1=q1.weight if emode >= 2 else None,
+                      s1=q1.scales if emode >= 2 else None, b1=q1.biases if emode >= 2 else None)
+        _lib.qmv_ex(st, **kw)
+        torch.cuda.synchronize()
+        outs.append((y0.clone(), ss.clone()))
+    assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
+    assert torch.equal(outs[0][1], outs[1][1])
+    assert not torch.isnan(outs[1][0].float()).any()
+    if xmode == 0 and emode == 0 and n * k <= 4_000_000:
+        want = qmm_affine4(bits(x), *(t.cpu().numpy().view(np.uint32) if i == 0 else bits(t)
+                                       for i, t in enumerate((q0.weight, q0.scales, q0.biases))), gs)
+        assert_close(bf16_values(outs[1][0]), want, what="packed vs oracle")
