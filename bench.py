@@ -16,7 +16,6 @@ times the float64 NumPy oracle on a bounded sample of the same step.
 from __future__ import annotations
 
 import argparse
-import ctypes
 import json
 import os
 import subprocess
@@ -48,13 +47,10 @@ def roofline_gate_up(model, M: int, reps: int = 5) -> dict:
     st = _lib.stream_handle(dev)
     x = torch.randn((M, c.hidden), device=dev).to(torch.bfloat16)
     y = torch.empty((M, c.ffn), dtype=torch.bfloat16, device=dev)
-    eps = ctypes.c_float(c.rms_eps)
 
-    def launch(L):
-        _lib.call("mtp_qmv_affine4_rmsnorm_dual", x.data_ptr(), L.post_norm.data_ptr(), None, eps,
-                  L.gate.weight.data_ptr(),
-                  L.gate.scales.data_ptr(), L.gate.biases.data_ptr(), L.up.weight.data_ptr(), L.up.scales.data_ptr(),
-                  L.up.biases.data_ptr(), y.data_ptr(), M, c.ffn, c.hidden, c.group_size, None, 0, st)
+    def launch(L):   # the same call the verify step makes (tile-major packed weights)
+        _lib.qmv_ex(st, x=x, x2=L.post_norm, eps=c.rms_eps, w0=L.gate.packed, w1=L.up.packed, y0=y, M=M, N=c.ffn,
+                    K=c.hidden, group_size=c.group_size, xmode=2, emode=3, packed=1)
 
     for L in model.layers:
         launch(L)
@@ -72,7 +68,8 @@ def roofline_gate_up(model, M: int, reps: int = 5) -> dict:
     us = e0.elapsed_time(e1) * 1000.0 / n
     byts = _gate_up_bytes(M, c.ffn, c.hidden, c.group_size)
     gbs = byts / us / 1e3
-    return {"bound": "hbm", "kernel": "qmm4_kernel<R=4,X_RMSNORM,E_DUAL_SWIGLU> (mtp_qmv_affine4_rmsnorm_dual)",
+    return {"bound": "hbm",
+            "kernel": "qmv_stream_kernel<NW=4,R=4,X_RMSNORM,E_DUAL_SWIGLU,packed> (mtp_qmv_affine4_ex)",
             "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": None, "algorithmic_bytes_per_launch": byts, "avg_launch_us": round(us, 3),
             "launches_timed": n}
@@ -89,13 +86,14 @@ def roofline_qmv_cfg1(reps: int = 64, nsets: int = 8) -> dict:
     M, N, K, gs = 4, 17408, 5120, 64
     gen = torch.Generator(device="cuda").manual_seed(1)
     sets = [QuantizedLinear.random(N, K, gs, generator=gen) for _ in range(nsets)]
+    for q in sets:
+        q.pack()
     x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     st = _lib.stream_handle()
 
     def launch(q):
-        _lib.call("mtp_qmv_affine4", x.data_ptr(), q.weight.data_ptr(), q.scales.data_ptr(), q.biases.data_ptr(),
-                  y.data_ptr(), M, N, K, gs, None, 0, st)
+        _lib.qmv_ex(st, x=x, w0=q.packed, y0=y, M=M, N=N, K=K, group_size=gs, xmode=0, emode=0, packed=1)
 
     for q in sets:
         launch(q)
@@ -110,7 +108,8 @@ def roofline_qmv_cfg1(reps: int = 64, nsets: int = 8) -> dict:
     us = e0.elapsed_time(e1) * 1000.0 / reps
     byts = _qmv_bytes(M, N, K, gs)
     gbs = byts / us / 1e3
-    return {"kernel": "qmm4_kernel<R=4,X_PLAIN,E_STORE> (mtp_qmv_affine4)", "achieved": round(gbs, 1),
+    return {"kernel": "qmv_stream_kernel<NW=4,R=4,X_PLAIN,E_STORE,packed> (mtp_qmv_affine4_ex)",
+            "achieved": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4), "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": byts}
 
 
