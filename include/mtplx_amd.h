@@ -108,7 +108,12 @@ int mtp_pack_affine4(const void* w, const void* scales, const void* biases, void
  * emode: 0 = store (y0 bf16, or yf fp32 when set), 1 = + resid (ss_out
  * optional), 2 = two outputs (w1 -> y1), 3 = silu(x@W0^T)*(x@W1^T).
  * packed = 1: w0/w1 come from mtp_pack_affine4 (s0/b0/s1/b1 unused).
- * ldx/ldy <= 0 mean K/N. */
+ * ldx/ldy <= 0 mean K/N.
+ * ws/ws_bytes: with packed weights, a workspace of mtp_qmv_workspace_bytes
+ * (256-byte aligned, zeroed once before first use and then left to the
+ * library) selects the stream-K kernel, which spreads (tile, 256-k) items
+ * evenly over all CUs; calls sharing one workspace must be stream-ordered.
+ * Without it the per-tile kernel runs. */
 typedef struct mtp_qmv_args {
   const void* x;
   const void* x2;
@@ -127,6 +132,8 @@ typedef struct mtp_qmv_args {
   float eps;
   int M, N, K, group_size, ldx, ldy;
   int xmode, emode, packed;
+  void* ws;
+  size_t ws_bytes;
 } mtp_qmv_args;
 int mtp_qmv_affine4_ex(const mtp_qmv_args* args, void* stream);
 

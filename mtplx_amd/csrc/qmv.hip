@@ -5,9 +5,8 @@
 // Weight format is the reference's (mtplx/verify_kernels.py:69-88, :372):
 // uint32 [N, K/8] with little-endian nibbles, bf16 scales/biases [N, K/gs].
 //
-// Design (MI355X-first, not a translation of the Metal split-K kernel):
-//  * At M = 4 a VALU dot product cannot keep up with 8 TB/s of nibbles
-//    (4 MACs + unpack per nibble exceeds the 64 lane-ops/clk/CU budget), so
+// Design (MI355X-first, not a translation of the Metal kernels):
+//  * At M <= 32 a VALU dot product cannot keep up with 8 TB/s of nibbles, so
 //    the contraction runs on the matrix cores even for skinny M:
 //    v_mfma_f32_32x32x16_bf16 with A = activations (rows m, zero-padded to 32)
 //    and B = nibbles.
@@ -16,17 +15,14 @@
 //    therefore yields G = sum x*(128+q) per 64-wide group, and the group is
 //    finished on the VALU as s*G + (b - 128*s)*sum(x) with sum(x) per group
 //    precomputed while staging x. Dequantised weights are never rounded.
-//  * One lane streams 16 B of a weight row per 64-group (two lanes per row,
-//    32 rows per wave, 128 rows per 256-thread workgroup): each wave load is
-//    32 contiguous 32 B row segments.
-//  * K is split across workgroups so every launch has ~1k workgroups; split
-//    partials go to a fp32 workspace and the last workgroup of a column block
-//    (an integer arrival counter, reset by that workgroup) sums them in split
-//    order — deterministic, no float atomics. Splits of one column block are
-//    mapped onto the same XCD so the partials meet in one L2.
+//  * A workgroup owns one 32-column tile; its waves split K by quads (256 k)
+//    and meet in LDS in wave order (deterministic). Weights stream either in
+//    the reference layout or in the tile-major packed layout (1 KB contiguous
+//    per wave load); the packed layout also has a stream-K kernel
+//    (qmv_sk.hip) that balances (tile, quad) items over all CUs.
 //  * Activations are staged once per workgroup into LDS in the MFMA A-operand
 //    order, with optional fused producers: SwiGLU (silu(gate)*up) or RMSNorm.
-#include "common.hpp"
+#include "qmv_common.hpp"
 
 #include <stdarg.h>
 #include <stdio.h>
@@ -41,118 +37,6 @@ void set_error(const char* fmt, ...) {
   va_start(ap, fmt);
   vsnprintf(g_err, sizeof(g_err), fmt, ap);
   va_end(ap);
-}
-
-enum XMode { X_PLAIN = 0, X_SWIGLU = 1, X_RMSNORM = 2 };
-enum EMode { E_STORE = 0, E_RESID = 1, E_DUAL = 2, E_DUAL_SWIGLU = 3 };
-
-struct QmmParams {
-  const uint16_t* x;       // activations [rows, ldx] (X_SWIGLU: gate)
-  const uint16_t* x2;      // X_SWIGLU: up [rows, ldx]; X_RMSNORM: norm weight [K]
-  const uint32_t* w0;
-  const uint16_t* s0;
-  const uint16_t* b0;
-  const uint32_t* w1;      // second matrix (E_DUAL*), same shape
-  const uint16_t* s1;
-  const uint16_t* b1;
-  uint16_t* y0;            // [rows, ldy]
-  uint16_t* y1;            // E_DUAL: second output
-  float* yf;               // E_STORE: optional fp32 output (bf16-rounded values)
-  const uint16_t* resid;   // E_RESID: [rows, ldy]
-  float* ss_out;           // E_RESID: per 32-column block, per row: sum of squares of y
-  const float* ss_in;      // X_RMSNORM: producer's ss_out ([ss_parts][32]); null = compute
-  int ss_parts;
-  float* partial;          // [S, M, nvirt]
-  uint32_t* counters;      // [n_blocks]
-  // Expert-gathered mode (MoE): rows of expert e are [off[e], off[e+1]) of
-  // the sorted row space; x row of sorted row i is rowmap[i] (null: i).
-  const uint32_t* rowmap;
-  const int32_t* expert_off;  // [E+1]
-  const int32_t* active;      // [1 + E]: count, then active expert ids
-  long long w_estride, s_estride;  // per-expert strides (uint32 words / bf16 elems)
-  int row_tiles;              // 32-row tiles per expert in the grid
-  int M, N, K, gs;
-  int ldx, ldy;
-  int S, gps, n_blocks, nvirt, chunk;
-  int packed;              // w0/w1 in the tile-major layout (scales/biases inside)
-  float eps;
-};
-
-constexpr int kThreads = 256;
-constexpr int kPackQuadWords = 1152;   // tile-major pack: words per (32-row tile, 256-k quad)
-
-// Nibbles of one word -> bf16x8 operand (128+q exactly), element order
-// (n0, n4, n1, n5, n2, n6, n3, n7). The mask and the exponent pattern are
-// held in registers (gfx9 VOP3 encodings take no literal), so each output
-// dword is one v_and_or_b32 (plus a shift): 7 VALU per word instead of 11.
-struct NibConsts {
-  uint32_t mask, bias;
-};
-__device__ __forceinline__ NibConsts nib_consts() {
-  NibConsts c;
-  asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(c.mask));
-  asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(c.bias));
-  return c;
-}
-__device__ __forceinline__ bf16x8 nibbles_to_bf16(uint32_t w, NibConsts c) {
-  uint32_t v[4];
-  v[0] = (w & c.mask) | c.bias;
-  v[1] = ((w >> 4) & c.mask) | c.bias;
-  v[2] = ((w >> 8) & c.mask) | c.bias;
-  v[3] = ((w >> 12) & c.mask) | c.bias;
-  return __builtin_bit_cast(bf16x8, v);
-}
-
-__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
-
-// x value as the consumer sees it (after the fused producer), rounded to bf16
-// exactly as an unfused producer would have stored it. ``b`` is the up half
-// (X_SWIGLU) or the norm weight (X_RMSNORM).
-template <int XM>
-__device__ __forceinline__ uint16_t produce(uint16_t a, uint16_t b, float inv_rms) {
-  if (XM == X_PLAIN) return a;
-  if (XM == X_SWIGLU) {
-    float g = round_bf(silu_f(bf2f(a)));
-    return f2bf(g * bf2f(b));
-  }
-  // X_RMSNORM: x * inv_rms * w in fp32, rounded once (a fused norm).
-  return f2bf(bf2f(a) * inv_rms * bf2f(b));
-}
-
-// One 16 B chunk of x (8 consecutive k) through the producer: returns it in
-// MFMA A order (bf16 pairs (t, t+4)) and adds its 8 values to ``sum``.
-template <int XM>
-__device__ __forceinline__ uint4 produce_chunk(uint4 raw, uint4 raw2, float inv_rms, float& sum) {
-  const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
-  const uint32_t uv[4] = {raw2.x, raw2.y, raw2.z, raw2.w};
-  uint16_t e[8];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    e[2 * t] = produce<XM>((uint16_t)(wv[t] & 0xffff), (uint16_t)(uv[t] & 0xffff), inv_rms);
-    e[2 * t + 1] = produce<XM>((uint16_t)(wv[t] >> 16), (uint16_t)(uv[t] >> 16), inv_rms);
-  }
-#pragma unroll
-  for (int t = 0; t < 8; ++t) sum += bf2f(e[t]);
-  uint4 o;
-  o.x = (uint32_t)e[0] | ((uint32_t)e[4] << 16);
-  o.y = (uint32_t)e[1] | ((uint32_t)e[5] << 16);
-  o.z = (uint32_t)e[2] | ((uint32_t)e[6] << 16);
-  o.w = (uint32_t)e[3] | ((uint32_t)e[7] << 16);
-  return o;
-}
-
-// Second producer input of the chunk at (row offset xo, column k): the up
-// half for SwiGLU, the norm weight for RMSNorm, nothing otherwise.
-template <int XM>
-__device__ __forceinline__ uint4 producer_aux(const QmmParams& p, size_t xo, int k) {
-  if (XM == X_SWIGLU) return *reinterpret_cast<const uint4*>(p.x2 + xo);
-  if (XM == X_RMSNORM) return *reinterpret_cast<const uint4*>(p.x2 + k);
-  return make_uint4(0, 0, 0, 0);
-}
-
-__device__ __forceinline__ size_t x_row(const QmmParams& p, int row0, int m) {
-  const int r = row0 + m;
-  return (size_t)(p.rowmap ? (int)p.rowmap[r] : r) * p.ldx;
 }
 
 // One workgroup = NW waves over 32 output columns (one MFMA column tile) and
@@ -291,7 +175,7 @@ __device__ __forceinline__ void qmm_body(const QmmParams& p, unsigned char* smem
       float sum = 0.f;
 #pragma unroll
       for (int cc = 0; cc < 8; ++cc)   // chunk cc covers k offset 8cc = 32*kq + 8*i within the group
-        xa[((gl * 4 + (cc & 3)) * 2 + (cc >> 2)) * M + m] = produce_chunk<XM>(raw[cc], raw2[cc], inv, sum);
+        xa[((gl * 4 + (cc & 3)) * 2 + (cc >> 2)) * M + m] = produce_chunk<XM, false>(raw[cc], raw2[cc], inv, sum);
       xs[gl * 32 + m] = sum;
     }
     for (int idx = tid; idx < ng * 32; idx += NT)
@@ -373,59 +257,8 @@ __device__ __forceinline__ void qmm_body(const QmmParams& p, unsigned char* smem
 // Epilogue from fin[m][64]: columns nb*32 + c, output rows row0 + m. The
 // residual mode also leaves, per output row, the sum of squares of this
 // block's 32 stored values (fixed order) for a following fused RMSNorm.
-template <int NW, int EM>
-__device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int nb, int M, int row0) {
-  constexpr int NT = NW * 64;
-  const int tid = threadIdx.x;
-  for (int idx = tid; idx < M * 32; idx += NT) {
-    const int m = idx >> 5;
-    const int c = idx & 31;
-    const int nn = nb * 32 + c;
-    const bool in = nn < p.N;
-    const size_t o = (size_t)(row0 + m) * p.ldy + nn;
-    const float g = fin[m * 64 + c];
-    if (EM == E_DUAL) {
-      if (in) {
-        p.y0[o] = f2bf(g);
-        p.y1[o] = f2bf(fin[m * 64 + 32 + c]);
-      }
-    } else if (EM == E_DUAL_SWIGLU) {
-      const float gs = round_bf(silu_f(round_bf(g)));
-      if (in) p.y0[o] = f2bf(gs * round_bf(fin[m * 64 + 32 + c]));
-    } else {
-      float v = g;
-      if (EM == E_RESID) {
-        v = round_bf(in ? round_bf(v) + bf2f(p.resid[o]) : 0.f);
-        fin[m * 64 + 32 + c] = v * v;  // column 32+c is free in non-dual modes
-      }
-      if (in) {
-        if (EM == E_STORE && p.yf)
-          p.yf[o] = round_bf(v);
-        else
-          p.y0[o] = f2bf(v);
-      }
-    }
-  }
-  if (EM == E_RESID && p.ss_out) {
-    __syncthreads();
-    if (tid < M) {
-      float ss = 0.f;
-      for (int c = 0; c < 32; ++c) ss += fin[tid * 64 + 32 + c];
-      p.ss_out[(size_t)nb * 32 + row0 + tid] = ss;
-    }
-  }
-}
-
 __device__ __forceinline__ float* fin_of(unsigned char* smem, int NW) {
   return reinterpret_cast<float*>(smem) + NW * 32 * 32;
-}
-
-template <int NW, int R, int XM, int EM, int GSH>
-__global__ __launch_bounds__(NW * 64) void qmm4_kernel(QmmParams p) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int nb = blockIdx.x;
-  qmm_body<NW, R, XM, EM, GSH>(p, smem, nb, p.M, 0, 0, 0);
-  qmm_epilogue<NW, EM>(p, fin_of(smem, NW), nb, p.M, 0);
 }
 
 // Expert-gathered launch: grid (column tiles, row tiles, expert slots).
@@ -591,7 +424,7 @@ __global__ __launch_bounds__(NW * 64) void qmv_chunked_kernel(QmmParams p) {
           float sum = 0.f;
 #pragma unroll
           for (int cc = 0; cc < 8; ++cc)
-            xa[((gl * 4 + (cc & 3)) * 2 + (cc >> 2)) * M + m] = produce_chunk<XM>(raw[cc], raw2[cc], inv, sum);
+            xa[((gl * 4 + (cc & 3)) * 2 + (cc >> 2)) * M + m] = produce_chunk<XM, false>(raw[cc], raw2[cc], inv, sum);
           xs[gl * XSW + m] = sum;
         }
         for (int idx = tid; idx < ng * XSW; idx += NT)
@@ -690,38 +523,13 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   const int G = gridDim.x;
   const NibConsts nc = nib_consts();
 
-  uint4* xa = reinterpret_cast<uint4*>(smem);                                  // [Q*4][4][2][M]
-  float* xs = reinterpret_cast<float*>(smem + (size_t)Q * 4 * 8 * M * 16);     // [Q*4][XSW]
+  uint4* xa = reinterpret_cast<uint4*>(smem);                                  // staged x, xa_index()
+  const int rstride = xa_row_stride(4 * Q);
+  float* xs = reinterpret_cast<float*>(smem + xa_bytes(4 * Q, M));             // [Q*4][XSW]
   float* red = xs + Q * 4 * XSW;                                               // [NW][M][32]
   float* fin = red + NW * M * 32;                                              // [M][64]
-  uint4* zero16 = reinterpret_cast<uint4*>(fin + M * 64);                      // one 16 B zero block
+  uint16_t* nwt = reinterpret_cast<uint16_t*>(fin + M * 64);                   // X_RMSNORM: norm weight [K]
   __shared__ float s_inv_rms[32];
-
-  if (tid == 0) *zero16 = make_uint4(0, 0, 0, 0);
-  if (XM == X_RMSNORM) {
-    for (int m = wave; m < M; m += NW) {
-      float ss = 0.f;
-      if (p.ss_in) {
-        for (int j = lane; j < p.ss_parts; j += 64) ss += p.ss_in[(size_t)j * 32 + m];
-      } else {
-        const uint16_t* xr = p.x + (size_t)m * p.ldx;
-#pragma unroll 4
-        for (int k = lane * 8; k < p.K; k += 64 * 8) {
-          uint4 raw = *reinterpret_cast<const uint4*>(xr + k);
-          const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            float a = bf2f((uint16_t)(wv[t] & 0xffff)), b = bf2f((uint16_t)(wv[t] >> 16));
-            ss += a * a + b * b;
-          }
-        }
-      }
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-      if (lane == 0) s_inv_rms[m] = rsqrtf(ss / (float)p.K + p.eps);
-    }
-    __syncthreads();
-  }
 
   const int c32 = lane & 31;
   const int kq = lane >> 5;
@@ -733,10 +541,10 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   const int ntiles = cdiv(p.n_blocks - (int)blockIdx.x, G);
   const int nitems = ntiles * qw;
 
-  // A-operand addressing without branches: lanes past M read the zero block.
-  const bool arow = c32 < M;
-  const uint32_t xa_base = arow ? (uint32_t)((kq * M + c32) * 16) : (uint32_t)((unsigned char*)zero16 - smem);
-  const uint32_t xa_step = arow ? (uint32_t)(2 * M * 16) : 0u;   // per (group*4 + i)
+  // A operands: lanes of rows >= M repeat row c32 % M (their output rows
+  // are never stored), so every lane reads its quad at immediate offsets.
+  const uint32_t a_lane = (uint32_t)xa_index(kq, c32 % M, M, rstride, 0, 0) * 16;
+  const uint32_t x_lane = (uint32_t)((unsigned char*)xs - smem) + 16 * kq;
 
   struct QuadRegs {
     uint4 w[4];
@@ -759,9 +567,10 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
     } else {
       const int n = nb * 32 + c32;
       const int nrow = n < p.N ? n : 0;
-      wrow = W + (size_t)nrow * (p.K >> 3) + kq * 4 + 32 * kw;
-      srow = Sc + (size_t)nrow * sgroups + (GSH == 0 ? 4 : 2) * kw;
-      brow = Bi + (size_t)nrow * sgroups + (GSH == 0 ? 4 : 2) * kw;
+      const int kw0 = qw > 0 ? kw : 0;   // waves without quads read a valid block
+      wrow = W + (size_t)nrow * (p.K >> 3) + kq * 4 + 32 * kw0;
+      srow = Sc + (size_t)nrow * sgroups + (GSH == 0 ? 4 : 2) * kw0;
+      brow = Bi + (size_t)nrow * sgroups + (GSH == 0 ? 4 : 2) * kw0;
     }
   };
   set_rows(0);
@@ -769,7 +578,7 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   // keeps re-reading the last item, whose registers are never used).
   auto load_next = [&](QuadRegs& qr) {
     if (PK) {
-      const size_t qoff = (size_t)(kw + KS * t_pf) * kPackQuadWords;
+      const size_t qoff = (size_t)(qw > 0 ? kw + KS * t_pf : 0) * kPackQuadWords;
       const uint32_t* wp = wrow + qoff;
 #pragma unroll
       for (int u = 0; u < 4; ++u) qr.w[u] = *reinterpret_cast<const uint4*>(wp + 256 * u);
@@ -807,38 +616,19 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
 
   auto compute = [&](const QuadRegs& cr, int t) {
     const int gq = 4 * (kw + t * KS);
-#pragma unroll
-    for (int u = 0; u < 4; u += 2) {
-      f32x16 G0 = {}, G1 = {};
-      const uint32_t w0[4] = {cr.w[u].x, cr.w[u].y, cr.w[u].z, cr.w[u].w};
-      const uint32_t w1[4] = {cr.w[u + 1].x, cr.w[u + 1].y, cr.w[u + 1].z, cr.w[u + 1].w};
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        const uint32_t a0off = xa_base + (uint32_t)((gq + u) * 4 + ii) * xa_step;
-        const uint32_t a1off = xa_base + (uint32_t)((gq + u + 1) * 4 + ii) * xa_step;
-        const bf16x8 a0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(smem + a0off));
-        const bf16x8 a1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(smem + a1off));
-        G0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, nibbles_to_bf16(w0[ii], nc), G0, 0, 0, 0);
-        G1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, nibbles_to_bf16(w1[ii], nc), G1, 0, 0, 0);
-      }
-      const uint32_t sw0 = (GSH == 0) ? cr.s[u >> 1] : cr.s[0];
-      const uint32_t bw0 = (GSH == 0) ? cr.b[u >> 1] : cr.b[0];
-      const float s0 = bf2f((uint16_t)((GSH == 0) ? (sw0 & 0xffff) : (u < 2 ? (sw0 & 0xffff) : (sw0 >> 16))));
-      const float s1 = bf2f((uint16_t)((GSH == 0) ? (sw0 >> 16) : (u < 2 ? (sw0 & 0xffff) : (sw0 >> 16))));
-      const float b0 = bf2f((uint16_t)((GSH == 0) ? (bw0 & 0xffff) : (u < 2 ? (bw0 & 0xffff) : (bw0 >> 16))));
-      const float b1 = bf2f((uint16_t)((GSH == 0) ? (bw0 >> 16) : (u < 2 ? (bw0 & 0xffff) : (bw0 >> 16))));
-      const float cb0 = b0 - 128.f * s0;
-      const float cb1 = b1 - 128.f * s1;
-      const float* xr0 = xs + (gq + u) * XSW + 4 * kq;
-      const float* xr1 = xs + (gq + u + 1) * XSW + 4 * kq;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int off = 8 * (r >> 2) + (r & 3);
-        acc[r] = fmaf(s0, G0[r], fmaf(cb0, xr0[off], acc[r]));
-        acc[r] = fmaf(s1, G1[r], fmaf(cb1, xr1[off], acc[r]));
-      }
-    }
+    float sv[4], cb[4];
+    quad_scales<GSH>(cr.s, cr.b, sv, cb);
+    quad_mma<R>(smem, a_lane + (uint32_t)gq * 64, x_lane + (uint32_t)gq * (XSW * 4), cr.w, sv, cb, nc, acc);
   };
+
+  // Residual of this thread's first epilogue element, fetched now so the
+  // epilogue does not wait for it.
+  float pre_resid = 0.f;
+  const bool use_pre = (EM == E_RESID) && (R == 4) && ntiles > 0;
+  if (use_pre && tid < M * 32) {
+    const int col = (int)blockIdx.x * 32 + (tid & 31);
+    if (col < p.N) pre_resid = bf2f(p.resid[(size_t)(tid >> 5) * p.ldy + col]);
+  }
 
   // End of tile j: reduce the K-split waves in LDS (wave order), epilogue.
   auto finish = [&](int j) {
@@ -867,61 +657,31 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
       fin[idx] = v;
     }
     __syncthreads();
-    qmm_epilogue<NW, EM>(p, fin, nb, M, 0);
+    qmm_epilogue<NW, EM>(p, fin, nb, M, 0, (use_pre && j == 0) ? &pre_resid : nullptr);
   };
 
+  // Prologue: the norm statistics, x (and the norm weights) straight into
+  // LDS, then all three ring slots, issued back to back. The wait below is
+  // for everything but the ring loads (they are the newest), so staging x
+  // overlaps the weights' first round trip.
+  float ssv[kMaxSsLoads];
+  if (XM == X_RMSNORM && p.ss_in && wave < M) ss_prefetch(p, wave, lane, ssv);
+  stage_x_issue<XM, NW>(p, xa, rstride, nwt, M, Q, 0, Q, wave, lane);
+  asm volatile("" ::: "memory");
   QuadRegs A, B, C;
-  if (qw > 0) {
-    load_next(A);
-    load_next(B);
-  }
-  // ---- stage all of x once: MFMA A order + per-group sums ----
-  // Thread item = one 16 B chunk (8 values) of one row: consecutive threads
-  // read consecutive chunks (coalesced); the 8 chunks of a 64-group are 8
-  // adjacent lanes, whose sums meet in a fixed xor-shuffle tree.
-  {
-    const int cpr = p.K >> 3;                   // chunks per row
-    const int total = M * cpr;
-    constexpr int SU = 8;                       // chunks per thread in flight
-    // (row, chunk) of this thread's item, advanced by NT per item without
-    // dividing (one division at the start).
-    int m_it = tid / cpr, c_it = tid - (tid / cpr) * cpr;
-    for (int base = 0; base < total; base += NT * SU) {
-      uint4 raw[SU], raw2[SU];
-      int mu[SU], cu[SU];
-#pragma unroll
-      for (int u = 0; u < SU; ++u) {
-        mu[u] = m_it;
-        cu[u] = c_it;
-        c_it += NT;
-        while (c_it >= cpr) {
-          c_it -= cpr;
-          ++m_it;
-        }
-        raw[u] = raw2[u] = make_uint4(0, 0, 0, 0);
-        if (mu[u] < M) {
-          const size_t xo = (size_t)mu[u] * p.ldx + 8 * cu[u];
-          raw[u] = *reinterpret_cast<const uint4*>(p.x + xo);
-          raw2[u] = producer_aux<XM>(p, xo, 8 * cu[u]);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < SU; ++u) {
-        const bool ok = mu[u] < M;
-        const int m = ok ? mu[u] : 0;
-        const int gl = cu[u] >> 3, cc = cu[u] & 7;
-        float sum = 0.f;
-        const uint4 o = produce_chunk<XM>(raw[u], raw2[u], (XM == X_RMSNORM) ? s_inv_rms[m] : 1.f, sum);
-        if (ok) xa[((gl * 4 + (cc & 3)) * 2 + (cc >> 2)) * M + m] = o;
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        sum += __shfl_xor(sum, 4, 64);
-        if (ok && cc == 0) xs[gl * XSW + m] = sum;
-      }
+  load_next(A);   // waves without items reload a valid block; never used
+  load_next(B);
+  load_next(C);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * (PK ? 5 : 6)));
+  if (XM == X_RMSNORM) {
+    for (int m = wave; m < M; m += NW) {
+      const float v = (p.ss_in && m == wave) ? ss_reduce(p, ssv, lane) : row_inv_rms(p, m, lane);
+      if (lane == 0) s_inv_rms[m] = v;
     }
-    for (int idx = tid; idx < 4 * Q * XSW; idx += NT)
-      if ((idx % XSW) >= M) xs[idx] = 0.f;
   }
+  __syncthreads();
+  stage_x_finish<XM, NW, XSW, PK>(p, xa, rstride, xs, nwt, s_inv_rms, M, Q, 0, Q, tid);
   __syncthreads();  // staged x visible to every wave
 
   // Every wave of the workgroup must reach each tile's barriers: waves with
@@ -948,12 +708,12 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
     }
   };
   do {
-    load_next(C);
     step(A);
     load_next(A);
     step(B);
     load_next(B);
     step(C);
+    load_next(C);
   } while (i < nitems);
 }
 
@@ -989,7 +749,8 @@ static int max_chunk_quads(int M) {
 // LDS of the streaming kernels: staged x (+ 2R group sums per group), the
 // wave partials [NW][M][32], the finished tile [M][64] and a 16 B zero block.
 static size_t stream_lds(int chunk_q, int M, int nw) {
-  return (size_t)chunk_q * 4 * (8 * M * 16 + 2 * r_of(M) * 4) + (size_t)nw * M * 32 * 4 + (size_t)M * 64 * 4 + 16;
+  return xa_bytes(4 * chunk_q, M) + (size_t)chunk_q * 4 * 2 * r_of(M) * 4 + (size_t)nw * M * 32 * 4 +
+         (size_t)M * 64 * 4;
 }
 
 static constexpr size_t kLdsMax = 160 * 1024 - 256;   // gfx950: 160 KiB of LDS per CU
@@ -999,14 +760,14 @@ static constexpr size_t kLdsBudget = 65536 - 256;
 // Waves per workgroup: 8 when the column tiles alone cannot give every CU
 // two workgroups (small N: q|k|v, o, down), else 4. All of K is staged once
 // per workgroup when it fits in LDS, else in chunks per tile.
-static Plan make_plan(int M, int N, int K) {
+static Plan make_plan(int M, int N, int K, bool norm = false) {
   Plan pl;
   pl.n_blocks = cdiv(N, 32);
   const int Q = K / 256;
   const int nw_env = env_int("MTPLX_AMD_QMV_WAVES", 0);
   pl.nw = (nw_env == 4 || nw_env == 8) ? nw_env : (pl.n_blocks < 512 ? 8 : 4);
   const int cap = env_int("MTPLX_AMD_QMV_CHUNK_QUADS", 0);
-  pl.resident = cap <= 0 && stream_lds(Q, M, pl.nw) <= kLdsMax;
+  pl.resident = cap <= 0 && stream_lds(Q, M, pl.nw) + (norm ? (size_t)K * 2 : 0) <= kLdsMax;
   if (pl.resident) {
     pl.chunk = Q;
   } else {
@@ -1015,11 +776,11 @@ static Plan make_plan(int M, int N, int K) {
     if (cap > 0 && cap < ch) ch = cap;
     pl.chunk = ch;
   }
-  pl.lds = stream_lds(pl.chunk, M, pl.nw);
+  pl.lds = stream_lds(pl.chunk, M, pl.nw) + (norm ? (size_t)K * 2 : 0);
   return pl;
 }
 
-static int device_cus() {
+int device_cus() {
   static thread_local int dev_cached = -1, cus = 0;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 256;
@@ -1149,9 +910,18 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
     set_error("%s: ldy=%d < N=%d", who, p.ldy, p.N);
     return MTP_ERR_ARG;
   }
-  (void)ws;
-  (void)ws_bytes;
-  Plan pl = make_plan(p.M, p.N, p.K);
+  if (p.packed && ws) {
+    // Stream-K over all CUs when the caller gave it a workspace; shapes whose
+    // staged x does not fit its LDS plan use the per-tile kernel below.
+    const int rc = qmv_sk_launch(xm, em, p, ws, ws_bytes, st);
+    if (rc == MTP_OK) return launch_check(who);
+    if (rc == MTP_ERR_WORKSPACE) {
+      set_error("%s: workspace of %zu B (256-B aligned) needed, got %zu B", who,
+                qmv_sk_workspace_bytes(p.M, p.N, p.K, em >= E_DUAL), ws_bytes);
+      return rc;
+    }
+  }
+  Plan pl = make_plan(p.M, p.N, p.K, xm == X_RMSNORM);
   if (p.packed && !pl.resident) {
     set_error("%s: packed weights need all of x in LDS (M=%d, K=%d too large); use the unpacked layout", who,
               p.M, p.K);
@@ -1190,12 +960,9 @@ using namespace mtp;
 MTP_API const char* mtp_last_error(void) { return g_err; }
 
 MTP_API size_t mtp_qmv_workspace_bytes(int M, int N, int K, int dual) {
-  // The current kernels reduce their K split inside the workgroup.
-  (void)M;
-  (void)N;
-  (void)K;
-  (void)dual;
-  return 0;
+  // Only the stream-K kernel (packed weights) uses it: arrival counters plus
+  // fp32 partials of the column tiles shared by two workgroups.
+  return qmv_sk_workspace_bytes(M, N, K, dual);
 }
 
 MTP_API int mtp_qmv_affine4(const void* x, const void* w, const void* scales, const void* biases, void* y,
@@ -1396,6 +1163,16 @@ MTP_API int mtp_gather_qmv_affine4(const void* x, const void* x2, const uint32_t
 //   words [1024 + 4c, +4)  = row 32nb + c: scales of groups 4q..4q+3 then
 //                            biases (bf16; group 128 repeats each value).
 // Rows past N are zero (their outputs are never stored).
+// Nibble k of a word moves to position (k >> 1) + 4 (k & 1): the operand
+// conversion (w >> 4i) & 0x000F000F then yields bf16 pairs (k0,k1), (k2,k3),
+// (k4,k5), (k6,k7) - natural k order, so packed weights take x as it is.
+__device__ __forceinline__ uint32_t nibbles_natural(uint32_t w) {
+  uint32_t o = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) o |= ((w >> (4 * k)) & 0xFu) << (4 * ((k >> 1) + 4 * (k & 1)));
+  return o;
+}
+
 __global__ void pack_affine4_kernel(const uint32_t* w, const uint16_t* s, const uint16_t* b, uint32_t* out, int N,
                                     int K, int gshift) {
   const int Q = K >> 8;
@@ -1409,7 +1186,10 @@ __global__ void pack_affine4_kernel(const uint32_t* w, const uint16_t* s, const 
     if (u16 < 256) {
       const int u = u16 >> 6, l = u16 & 63;
       const int row = nb * 32 + (l & 31);
-      if (row < N) v = *reinterpret_cast<const uint4*>(w + (size_t)row * (K >> 3) + 32 * q + 8 * u + 4 * (l >> 5));
+      if (row < N) {
+        v = *reinterpret_cast<const uint4*>(w + (size_t)row * (K >> 3) + 32 * q + 8 * u + 4 * (l >> 5));
+        v = make_uint4(nibbles_natural(v.x), nibbles_natural(v.y), nibbles_natural(v.z), nibbles_natural(v.w));
+      }
     } else {
       const int c = u16 - 256;
       const int row = nb * 32 + c;
@@ -1475,6 +1255,8 @@ struct mtp_qmv_args {
   float eps;
   int M, N, K, group_size, ldx, ldy;
   int xmode, emode, packed;
+  void* ws;
+  size_t ws_bytes;
 };
 
 MTP_API int mtp_qmv_affine4_ex(const mtp_qmv_args* a, void* stream) {
@@ -1501,5 +1283,5 @@ MTP_API int mtp_qmv_affine4_ex(const mtp_qmv_args* a, void* stream) {
   p.packed = a->packed;
   if (a->ldx > 0) p.ldx = a->ldx;
   if (a->ldy > 0) p.ldy = a->ldy;
-  return qmm_dispatch(a->xmode, a->emode, p, nullptr, 0, (hipStream_t)stream, "mtp_qmv_affine4_ex");
+  return qmm_dispatch(a->xmode, a->emode, p, a->ws, a->ws_bytes, (hipStream_t)stream, "mtp_qmv_affine4_ex");
 }

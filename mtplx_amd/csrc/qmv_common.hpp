@@ -1,0 +1,412 @@
+// Shared pieces of the 4-bit verify matmul kernels (qmv.hip, qmv_sk.hip):
+// launch parameters, the nibble -> bf16 operand conversion, the fused x
+// producers and the output epilogues.
+#pragma once
+
+#include "common.hpp"
+
+namespace mtp {
+
+enum XMode { X_PLAIN = 0, X_SWIGLU = 1, X_RMSNORM = 2 };
+enum EMode { E_STORE = 0, E_RESID = 1, E_DUAL = 2, E_DUAL_SWIGLU = 3 };
+
+struct QmmParams {
+  const uint16_t* x;       // activations [rows, ldx] (X_SWIGLU: gate)
+  const uint16_t* x2;      // X_SWIGLU: up [rows, ldx]; X_RMSNORM: norm weight [K]
+  const uint32_t* w0;
+  const uint16_t* s0;
+  const uint16_t* b0;
+  const uint32_t* w1;      // second matrix (E_DUAL*), same shape
+  const uint16_t* s1;
+  const uint16_t* b1;
+  uint16_t* y0;            // [rows, ldy]
+  uint16_t* y1;            // E_DUAL: second output
+  float* yf;               // E_STORE: optional fp32 output (bf16-rounded values)
+  const uint16_t* resid;   // E_RESID: [rows, ldy]
+  float* ss_out;           // E_RESID: per 32-column block, per row: sum of squares of y
+  const float* ss_in;      // X_RMSNORM: producer's ss_out ([ss_parts][32]); null = compute
+  int ss_parts;
+  float* partial;          // [S, M, nvirt]
+  uint32_t* counters;      // [n_blocks]
+  // Expert-gathered mode (MoE): rows of expert e are [off[e], off[e+1]) of
+  // the sorted row space; x row of sorted row i is rowmap[i] (null: i).
+  const uint32_t* rowmap;
+  const int32_t* expert_off;  // [E+1]
+  const int32_t* active;      // [1 + E]: count, then active expert ids
+  long long w_estride, s_estride;  // per-expert strides (uint32 words / bf16 elems)
+  int row_tiles;              // 32-row tiles per expert in the grid
+  int M, N, K, gs;
+  int ldx, ldy;
+  int S, gps, n_blocks, nvirt, chunk;
+  int packed;              // w0/w1 in the tile-major layout (scales/biases inside)
+  float eps;
+};
+
+constexpr int kThreads = 256;
+constexpr int kPackQuadWords = 1152;   // tile-major pack: words per (32-row tile, 256-k quad)
+
+// Nibbles of one word -> bf16x8 operand (128+q exactly), element order
+// (n0, n4, n1, n5, n2, n6, n3, n7). The mask and the exponent pattern are
+// held in registers (gfx9 VOP3 encodings take no literal), so each output
+// dword is one v_and_or_b32 (plus a shift): 7 VALU per word instead of 11.
+struct NibConsts {
+  uint32_t mask, bias;
+};
+__device__ __forceinline__ NibConsts nib_consts() {
+  NibConsts c;
+  asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(c.mask));
+  asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(c.bias));
+  return c;
+}
+__device__ __forceinline__ bf16x8 nibbles_to_bf16(uint32_t w, NibConsts c) {
+  uint32_t v[4];
+  v[0] = (w & c.mask) | c.bias;
+  v[1] = ((w >> 4) & c.mask) | c.bias;
+  v[2] = ((w >> 8) & c.mask) | c.bias;
+  v[3] = ((w >> 12) & c.mask) | c.bias;
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
+
+// x value as the consumer sees it (after the fused producer), rounded to bf16
+// exactly as an unfused producer would have stored it. ``b`` is the up half
+// (X_SWIGLU) or the norm weight (X_RMSNORM).
+template <int XM>
+__device__ __forceinline__ uint16_t produce(uint16_t a, uint16_t b, float inv_rms) {
+  if (XM == X_PLAIN) return a;
+  if (XM == X_SWIGLU) {
+    float g = round_bf(silu_f(bf2f(a)));
+    return f2bf(g * bf2f(b));
+  }
+  // X_RMSNORM: x * inv_rms * w in fp32, rounded once (a fused norm).
+  return f2bf(bf2f(a) * inv_rms * bf2f(b));
+}
+
+// Sum over each aligned group of 8 lanes, result in all 8 (DPP, no LDS).
+__device__ __forceinline__ float sum8_lanes(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+  return v;
+}
+
+// One 16 B chunk of x (8 consecutive k) through the producer, returned in
+// the A-operand element order of the weights' nibble order: NAT = natural
+// (tile-major packed weights), else bf16 pairs (t, t+4) (reference layout).
+// Adds its 8 (bf16-rounded) values to ``sum``.
+template <int XM, bool NAT>
+__device__ __forceinline__ uint4 produce_chunk(uint4 raw, uint4 raw2, float inv_rms, float& sum) {
+  uint4 o;
+  if (XM == X_PLAIN) {
+    if (NAT) {
+      o = raw;
+    } else {   // element t of the chunk is half (t & 1) of word t >> 1
+      o.x = __builtin_amdgcn_perm(raw.z, raw.x, 0x05040100u);   // (e0, e4)
+      o.y = __builtin_amdgcn_perm(raw.z, raw.x, 0x07060302u);   // (e1, e5)
+      o.z = __builtin_amdgcn_perm(raw.w, raw.y, 0x05040100u);   // (e2, e6)
+      o.w = __builtin_amdgcn_perm(raw.w, raw.y, 0x07060302u);   // (e3, e7)
+    }
+  } else {
+    const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+    const uint32_t uv[4] = {raw2.x, raw2.y, raw2.z, raw2.w};
+    float v[8];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float a0 = __uint_as_float(wv[t] << 16), a1 = __uint_as_float(wv[t] & 0xffff0000u);
+      const float b0 = __uint_as_float(uv[t] << 16), b1 = __uint_as_float(uv[t] & 0xffff0000u);
+      if (XM == X_SWIGLU) {
+        v[2 * t] = round_bf(silu_f(a0)) * b0;
+        v[2 * t + 1] = round_bf(silu_f(a1)) * b1;
+      } else {   // X_RMSNORM: x * inv_rms * w in fp32, rounded once (a fused norm)
+        v[2 * t] = a0 * inv_rms * b0;
+        v[2 * t + 1] = a1 * inv_rms * b1;
+      }
+    }
+    if (NAT) {
+      o.x = f2bf2(v[0], v[1]);
+      o.y = f2bf2(v[2], v[3]);
+      o.z = f2bf2(v[4], v[5]);
+      o.w = f2bf2(v[6], v[7]);
+    } else {
+      o.x = f2bf2(v[0], v[4]);
+      o.y = f2bf2(v[1], v[5]);
+      o.z = f2bf2(v[2], v[6]);
+      o.w = f2bf2(v[3], v[7]);
+    }
+  }
+  const uint32_t ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) sum += __uint_as_float(ov[t] << 16) + __uint_as_float(ov[t] & 0xffff0000u);
+  return o;
+}
+
+// Staged-x layout shared by the streaming kernels. Rows (kq, m), 2M of them:
+// row kq*M + m holds, for every staged 64-group g, the chunks ii = 0..3 of
+// k = 64g + 32kq + 8ii (MFMA step ii of half kq), so one lane's 16 A operands
+// of a quad are 256 contiguous bytes read at immediate offsets. Rows are
+// padded by 16 B against LDS bank conflicts. Group sums: xs[g][2R] fp32.
+__device__ __forceinline__ int xa_row_stride(int ngroups) { return ngroups * 4 + 1; }   // in uint4
+__device__ __forceinline__ int xa_index(int kq, int m, int M, int rstride, int g, int ii) {
+  return (kq * M + m) * rstride + g * 4 + ii;
+}
+__host__ __device__ __forceinline__ size_t xa_bytes(int ngroups, int M) {
+  return (size_t)2 * M * (ngroups * 4 + 1) * 16;
+}
+
+typedef const __attribute__((address_space(1))) void* gptr_t;
+typedef __attribute__((address_space(3))) void* lptr_t;
+
+// Staging, phase 1: direct-to-LDS loads (no registers) of the raw x chunks of
+// the k-quads kq0, kq0+1, ... (mod Q), nslot of them, into their staged
+// positions; X_RMSNORM also copies the norm weights [K] to ``nwt``. One wave
+// instruction fills 64 consecutive chunks (1 KB) of one staged row.
+template <int XM, int NW>
+__device__ __forceinline__ void stage_x_issue(const QmmParams& p, uint4* xa, int rstride, uint16_t* nwt, int M, int Q,
+                                              int kq0, int nslot, int wave, int lane) {
+  const int rowchunks = 16 * nslot;
+  const int nblk = (rowchunks + 63) >> 6;
+  const int ntask = 2 * M * nblk;
+  for (int task = wave; task < ntask; task += NW) {
+    const int row = task / nblk;
+    const int blk = task - row * nblk;
+    const int kq = row >= M ? 1 : 0;
+    const int m = row - kq * M;
+    const int c = blk * 64 + lane;
+    if (c < rowchunks) {
+      const int gl = c >> 2, ii = c & 3;
+      int qd = kq0 + (gl >> 2);
+      if (qd >= Q) qd -= Q;
+      const int k = 64 * (4 * qd + (gl & 3)) + 32 * kq + 8 * ii;
+      __builtin_amdgcn_global_load_lds((gptr_t)(p.x + (size_t)m * p.ldx + k),
+                                       (lptr_t)(xa + (size_t)row * rstride + blk * 64), 16, 0, 0);
+    }
+  }
+  if (XM == X_RMSNORM) {
+    const int nch = p.K >> 3;
+    for (int b = wave; b * 64 < nch; b += NW) {
+      const int c = b * 64 + lane;
+      if (c < nch) __builtin_amdgcn_global_load_lds((gptr_t)(p.x2 + 8 * c), (lptr_t)(nwt + b * 512), 16, 0, 0);
+    }
+  }
+}
+
+// Staging, phase 2 (after the loads have landed and a barrier): the fused
+// producer, the A-operand element order and the per-group sums, in place.
+// One thread owns one (row, 64-group): its 8 chunks are independent LDS reads
+// and its sum needs no cross-lane step. X_SWIGLU reads its up half from
+// global memory.
+template <int XM, int NW, int XSW, bool NAT>
+__device__ __forceinline__ void stage_x_finish(const QmmParams& p, uint4* xa, int rstride, float* xs,
+                                               const uint16_t* nwt, const float* inv_rms, int M, int Q, int kq0,
+                                               int nslot, int tid) {
+  constexpr int NT = NW * 64;
+  const int ng = 4 * nslot;   // staged groups
+  for (int it = tid; it < M * ng; it += NT) {
+    const int m = it / ng;
+    const int gl = it - m * ng;
+    int qd = kq0 + (gl >> 2);
+    if (qd >= Q) qd -= Q;
+    const int kb = 64 * (4 * qd + (gl & 3));
+    const float inv = (XM == X_RMSNORM) ? inv_rms[m] : 1.f;
+    float sum = 0.f;
+    constexpr int B = (XM == X_PLAIN) ? 4 : 2;   // chunks read ahead (register budget)
+#pragma unroll
+    for (int cb = 0; cb < 8; cb += B) {   // chunk cc = 4 kq + ii covers k = kb + 8 cc
+      uint4 c[B], aux[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int cc = cb + u;
+        c[u] = xa[xa_index(cc >> 2, m, M, rstride, gl, cc & 3)];
+        aux[u] = make_uint4(0, 0, 0, 0);
+        if (XM == X_RMSNORM) aux[u] = *reinterpret_cast<const uint4*>(nwt + kb + 8 * cc);
+        if (XM == X_SWIGLU) aux[u] = *reinterpret_cast<const uint4*>(p.x2 + (size_t)m * p.ldx + kb + 8 * cc);
+      }
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int cc = cb + u;
+        const uint4 o = produce_chunk<XM, NAT>(c[u], aux[u], inv, sum);
+        if (!(XM == X_PLAIN && NAT)) xa[xa_index(cc >> 2, m, M, rstride, gl, cc & 3)] = o;
+      }
+    }
+    xs[gl * XSW + m] = sum;
+  }
+  for (int idx = tid; idx < nslot * 4 * XSW; idx += NT)
+    if ((idx % XSW) >= M) xs[idx] = 0.f;
+}
+
+// s_waitcnt immediate for "at most vm vector-memory ops outstanding" (gfx9
+// encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at 15:14).
+__host__ __device__ constexpr int vmcnt_imm(int vm) { return (vm & 0xF) | (0x7 << 4) | (0xF << 8) | ((vm >> 4) << 14); }
+
+// Row m's sum-of-squares partials, fetched into registers early (up to
+// 64 * kMaxSsLoads partials, i.e. K <= 24576), reduced later.
+constexpr int kMaxSsLoads = 12;
+__device__ __forceinline__ void ss_prefetch(const QmmParams& p, int m, int lane, float (&v)[kMaxSsLoads]) {
+#pragma unroll
+  for (int i = 0; i < kMaxSsLoads; ++i) {
+    const int j = lane + 64 * i;
+    v[i] = (j < p.ss_parts) ? p.ss_in[(size_t)j * 32 + m] : 0.f;
+  }
+}
+__device__ __forceinline__ float ss_reduce(const QmmParams& p, const float (&v)[kMaxSsLoads], int lane) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxSsLoads; ++i) ss += v[i];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  (void)lane;
+  return rsqrtf(ss / (float)p.K + p.eps);
+}
+
+// 1/rms of row m from the producer's sum-of-squares partials ([parts][32]),
+// or from x itself when there are none; call with the whole wave.
+__device__ __forceinline__ float row_inv_rms(const QmmParams& p, int m, int lane) {
+  float ss = 0.f;
+  if (p.ss_in) {
+    for (int j = lane; j < p.ss_parts; j += 64) ss += p.ss_in[(size_t)j * 32 + m];
+  } else {
+    const uint16_t* xr = p.x + (size_t)m * p.ldx;
+#pragma unroll 4
+    for (int k = lane * 8; k < p.K; k += 64 * 8) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(xr + k);
+      const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float a = __uint_as_float(wv[t] << 16), b = __uint_as_float(wv[t] & 0xffff0000u);
+        ss += a * a + b * b;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  return rsqrtf(ss / (float)p.K + p.eps);
+}
+
+// Scales and bias corrections of the 4 groups of a quad from its packed
+// bf16 words (GSH = 1: one scale per two groups, group size 128).
+template <int GSH>
+__device__ __forceinline__ void quad_scales(const uint32_t (&sw)[2], const uint32_t (&bw)[2], float (&s)[4],
+                                            float (&cb)[4]) {
+  float b[4];
+  if (GSH == 0) {
+    s[0] = __uint_as_float(sw[0] << 16), s[1] = __uint_as_float(sw[0] & 0xffff0000u);
+    s[2] = __uint_as_float(sw[1] << 16), s[3] = __uint_as_float(sw[1] & 0xffff0000u);
+    b[0] = __uint_as_float(bw[0] << 16), b[1] = __uint_as_float(bw[0] & 0xffff0000u);
+    b[2] = __uint_as_float(bw[1] << 16), b[3] = __uint_as_float(bw[1] & 0xffff0000u);
+  } else {
+    s[0] = s[1] = __uint_as_float(sw[0] << 16);
+    s[2] = s[3] = __uint_as_float(sw[0] & 0xffff0000u);
+    b[0] = b[1] = __uint_as_float(bw[0] << 16);
+    b[2] = b[3] = __uint_as_float(bw[0] & 0xffff0000u);
+  }
+#pragma unroll
+  for (int g = 0; g < 4; ++g) cb[g] = fmaf(-128.f, s[g], b[g]);
+}
+
+// One quad (4 groups of 64 k, 32 columns) into the R accumulator rows of
+// this lane: t += s*G + (b - 128 s)*sum(x) per group, G = sum x*(128+q) on
+// the MFMA. ``a_off``: byte offset of this lane's first A chunk of the quad;
+// ``x_off``: byte offset of xs[g0][4*kq] (both relative to ``lds``).
+template <int R>
+__device__ __forceinline__ void quad_mma(const unsigned char* lds, uint32_t a_off, uint32_t x_off,
+                                         const uint4 (&w)[4], const float (&s)[4], const float (&cb)[4],
+                                         NibConsts nc, float (&t)[R]) {
+  constexpr int XSW = 2 * R;
+#pragma unroll
+  for (int u = 0; u < 4; u += 2) {
+    f32x16 G0 = {}, G1 = {};
+    const uint32_t w0[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+    const uint32_t w1[4] = {w[u + 1].x, w[u + 1].y, w[u + 1].z, w[u + 1].w};
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(lds + a_off + (u * 4 + ii) * 16);
+      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(lds + a_off + ((u + 1) * 4 + ii) * 16);
+      G0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, nibbles_to_bf16(w0[ii], nc), G0, 0, 0, 0);
+      G1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, nibbles_to_bf16(w1[ii], nc), G1, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < R / 4; ++j) {
+      const float4 x0 = *reinterpret_cast<const float4*>(lds + x_off + (u * XSW + 8 * j) * 4);
+      const float4 x1 = *reinterpret_cast<const float4*>(lds + x_off + ((u + 1) * XSW + 8 * j) * 4);
+      const float xv0[4] = {x0.x, x0.y, x0.z, x0.w};
+      const float xv1[4] = {x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int r = 4 * j + r4;
+        t[r] = fmaf(s[u], G0[r], fmaf(cb[u], xv0[r4], t[r]));
+        t[r] = fmaf(s[u + 1], G1[r], fmaf(cb[u + 1], xv1[r4], t[r]));
+      }
+    }
+  }
+}
+
+// Second producer input of the chunk at (row offset xo, column k): the up
+// half for SwiGLU, the norm weight for RMSNorm, nothing otherwise.
+template <int XM>
+__device__ __forceinline__ uint4 producer_aux(const QmmParams& p, size_t xo, int k) {
+  if (XM == X_SWIGLU) return *reinterpret_cast<const uint4*>(p.x2 + xo);
+  if (XM == X_RMSNORM) return *reinterpret_cast<const uint4*>(p.x2 + k);
+  return make_uint4(0, 0, 0, 0);
+}
+
+__device__ __forceinline__ size_t x_row(const QmmParams& p, int row0, int m) {
+  const int r = row0 + m;
+  return (size_t)(p.rowmap ? (int)p.rowmap[r] : r) * p.ldx;
+}
+
+// ``pre``: this thread's residual value for its first output element, loaded
+// at kernel start (E_RESID with M*32 <= threads), or null.
+template <int NW, int EM>
+__device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int nb, int M, int row0,
+                                             const float* pre = nullptr) {
+  constexpr int NT = NW * 64;
+  const int tid = threadIdx.x;
+  for (int idx = tid; idx < M * 32; idx += NT) {
+    const int m = idx >> 5;
+    const int c = idx & 31;
+    const int nn = nb * 32 + c;
+    const bool in = nn < p.N;
+    const size_t o = (size_t)(row0 + m) * p.ldy + nn;
+    const float g = fin[m * 64 + c];
+    if (EM == E_DUAL) {
+      if (in) {
+        p.y0[o] = f2bf(g);
+        p.y1[o] = f2bf(fin[m * 64 + 32 + c]);
+      }
+    } else if (EM == E_DUAL_SWIGLU) {
+      const float gs = round_bf(silu_f(round_bf(g)));
+      if (in) p.y0[o] = f2bf(gs * round_bf(fin[m * 64 + 32 + c]));
+    } else {
+      float v = g;
+      if (EM == E_RESID) {
+        const float rv = (pre && idx == tid) ? *pre : (in ? bf2f(p.resid[o]) : 0.f);
+        v = round_bf(in ? round_bf(v) + rv : 0.f);
+        fin[m * 64 + 32 + c] = v * v;  // column 32+c is free in non-dual modes
+      }
+      if (in) {
+        if (EM == E_STORE && p.yf)
+          p.yf[o] = round_bf(v);
+        else
+          p.y0[o] = f2bf(v);
+      }
+    }
+  }
+  if (EM == E_RESID && p.ss_out) {
+    __syncthreads();
+    if (tid < M) {
+      float ss = 0.f;
+      for (int c = 0; c < 32; ++c) ss += fin[tid * 64 + 32 + c];
+      p.ss_out[(size_t)nb * 32 + row0 + tid] = ss;
+    }
+  }
+}
+
+// Stream-K launch over tile-major packed weights (qmv_sk.hip). Returns
+// MTP_ERR_UNSUPPORTED when the shape does not fit its LDS plan (the caller
+// then uses the per-tile kernel).
+int qmv_sk_launch(int xm, int em, const QmmParams& p, void* ws, size_t ws_bytes, hipStream_t st);
+size_t qmv_sk_workspace_bytes(int M, int N, int K, int dual);
+int device_cus();
+
+}  // namespace mtp

@@ -191,7 +191,10 @@ class VerifyModel:
         aws = _lib.WORKSPACES.get(nb, "attn", dev)
         scale = 1.0 / math.sqrt(c.head_dim)
         ql = None if q_lens is None else q_lens.to(torch.int32).contiguous()
+        # Per-tile streaming kernel (no workspace): at these widths it beats the
+        # stream-K variant, whose shared tiles cost a fix-up at the end.
         qmv = _lib.qmv_ex
+
         for li, L in enumerate(self.layers):
             qmv(st, x=h, x2=L.in_norm, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv.packed, y0=qkv, M=M, N=c.qkv_out, K=H,
                 group_size=gs, xmode=2, emode=0, packed=1)

@@ -43,7 +43,11 @@ def test_size_queries_without_gpu(lib):
     lib.mtp_qmv_workspace_bytes.restype = ctypes.c_size_t
     assert lib.mtp_sampler_workspace_bytes(7, 151936) == 7 * 38 * 536
     assert lib.mtp_attn_workspace_bytes(8, 8, 32768, 0) == 8 * 8 * 32 * (32 * 128 + 64) * 4
-    assert lib.mtp_qmv_workspace_bytes(4, 17408, 5120, 0) == 0
+    # stream-K: two fp32 [8][64] partials per workgroup (one workgroup per CU,
+    # 256 when no device is visible, as here), then one arrival counter per
+    # 32-column tile (256-B aligned).
+    counters = (17408 // 32 * 4 + 255) // 256 * 256
+    assert lib.mtp_qmv_workspace_bytes(4, 17408, 5120, 0) == 2 * 256 * 8 * 64 * 4 + counters
 
 
 def test_error_path_reports_message(lib):

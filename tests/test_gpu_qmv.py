@@ -188,6 +188,16 @@ def test_bad_arguments_raise(gpu):
                   4, 8, 256, 32, None, 0, _stream())
 
 
+def _nibbles_natural(words):
+    """Nibble k of each word moved to position (k >> 1) + 4 (k & 1)."""
+    words = np.asarray(words, dtype=np.uint32)
+    out = np.zeros_like(words)
+    for k in range(8):
+        pos = (k >> 1) + 4 * (k & 1)
+        out |= ((words >> np.uint32(4 * k)) & np.uint32(0xF)) << np.uint32(4 * pos)
+    return out
+
+
 def _pack_reference(w, s, b, gs):
     """NumPy restatement of the tile-major layout (include/mtplx_amd.h)."""
     N, kw = w.shape
@@ -202,7 +212,8 @@ def _pack_reference(w, s, b, gs):
                 for l in range(64):
                     row = nb * 32 + (l & 31)
                     if row < N:
-                        out[nb, q, 256 * u + 4 * l: 256 * u + 4 * l + 4] = w[row, 32 * q + 8 * u + 4 * (l >> 5):][:4]
+                        out[nb, q, 256 * u + 4 * l: 256 * u + 4 * l + 4] = \
+                            _nibbles_natural(w[row, 32 * q + 8 * u + 4 * (l >> 5):][:4])
             for c in range(32):
                 row = nb * 32 + c
                 if row < N:
@@ -226,9 +237,10 @@ def test_pack_layout_bit_exact(gpu, n, k, gs):
     (4, 17408, 5120, 64, 0, 0), (4, 7168, 5120, 64, 2, 0), (4, 5120, 17408, 64, 0, 1),
     (4, 1536, 2048, 64, 2, 3), (4, 300, 1024, 128, 0, 0), (8, 600, 1024, 64, 2, 3), (16, 256, 512, 64, 0, 1),
     (4, 151936 // 8, 5120, 64, 2, 0)])
-def test_packed_path_bitwise_equals_unpacked(gpu, m, n, k, gs, xmode, emode):
-    """The tile-major path reads the same values in the same order as the MLX
-    layout path, so outputs must agree bit for bit (and hence with the oracle)."""
+def test_packed_path_matches_unpacked(gpu, m, n, k, gs, xmode, emode):
+    """The tile-major path computes the same sums as the reference-layout path
+    with the 8 k of each MFMA operand in another order, so outputs agree to
+    one bf16 ulp (and both meet the oracle bar)."""
     from mtplx_amd import _lib
     from mtplx_amd.quant import QuantizedLinear
     g = torch.Generator(device="cuda").manual_seed(m * 1000 + n)
@@ -254,8 +266,11 @@ def test_packed_path_bitwise_equals_unpacked(gpu, m, n, k, gs, xmode, emode):
         _lib.qmv_ex(st, **kw)
         torch.cuda.synchronize()
         outs.append((y0.clone(), ss.clone()))
-    assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
-    assert torch.equal(outs[0][1], outs[1][1])
+    a, b = bf16_values(outs[1][0]), bf16_values(outs[0][0])
+    tol = np.maximum(np.abs(a), np.abs(b)) * 2.0 ** -7 + 1e-4 * np.abs(b).max()
+    assert (np.abs(a - b) <= tol).all(), np.abs(a - b).max()
+    if emode == 1:
+        assert torch.allclose(outs[0][1], outs[1][1], rtol=1e-3, atol=1e-3)
     assert not torch.isnan(outs[1][0].float()).any()
     if xmode == 0 and emode == 0 and n * k <= 4_000_000:
         want = qmm_affine4(bits(x), *(t.cpu().numpy().view(np.uint32) if i == 0 else bits(t)
