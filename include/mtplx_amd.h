@@ -170,6 +170,26 @@ int mtp_ragged_gqa_attn_rows(const void* q, const void* k, const void* v, const 
                              const int32_t* q_lens, void* out, int B, int Hq, int Hkv, int L, int D, int cap,
                              float scale, int split_keys, void* ws, size_t ws_bytes, void* stream);
 
+/* Operand-major KV blocks, the verify step's own cache (head dim 128). Per
+ * (request, kv head), 32-key blocks of 4096 bf16 in which each attention MFMA
+ * operand of a wave is one 1 KB contiguous load:
+ *   K[key][d] at block*4096 + ((i*2 + h2)*32 + key%32)*8 + d%8,
+ *       i = (d/8)%8, h2 = d/64;
+ *   V[key][d] at block*4096 + ((t*2 + jj)*64 + h2*32 + d%32)*8 + e,
+ *       t = d/32, jj = (key%32)/16, r = key%16, h2 = (r%8)/4,
+ *       e = r < 8 ? r%4 : 4 + r%4.
+ * Same results as mtp_ragged_gqa_attn_rows / mtp_rope_qkv_to_cache on the
+ * same values; cap must be a multiple of 32. No reference counterpart: the
+ * reference cache (mtplx/ragged_kv_cache.py:71) is [B, Hkv, cap, D]; this is
+ * the MI355X layout of the same values for the fused verify step. */
+size_t mtp_attn_vt_workspace_bytes(int B, int Hkv, int cap);
+int mtp_ragged_gqa_attn_rows_vt(const void* q, const void* k_blk, const void* v_blk, const int32_t* q_start,
+                                const int32_t* q_lens, void* out, int B, int Hq, int Hkv, int L, int D, int cap,
+                                float scale, void* ws, size_t ws_bytes, void* stream);
+int mtp_rope_qkv_to_cache_vt(const void* qkv, const int32_t* q_start, const int32_t* q_lens, void* q_out,
+                             void* k_cache, void* v_cache, int B, int L, int Hq, int Hkv, int D, int cap,
+                             float rope_base, int32_t* status, void* stream);
+
 /* ---- Verify-step glue -------------------------------------------------------
  * RoPE (rotate-half, fp32 angles) on fused q|k|v rows [B*L, (Hq+2Hkv)*D] at
  * positions q_start[b]+i; q -> q_out [B,Hq,L,D], k/v written into the cache

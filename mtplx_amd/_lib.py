@@ -55,6 +55,9 @@ SIGNATURES = {
     "mtp_pack_affine4_bytes": (_sz, [_i, _i]),
     "mtp_pack_affine4": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mtp_qmv_affine4_ex": (_i, [_vp, _vp]),
+    "mtp_attn_vt_workspace_bytes": (_sz, [_i, _i, _i]),
+    "mtp_ragged_gqa_attn_rows_vt": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
+    "mtp_rope_qkv_to_cache_vt": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _vp]),
 }
 
 

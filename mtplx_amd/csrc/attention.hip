@@ -18,6 +18,8 @@
 // read on the GPU; units past a request's length exit at once.
 #include "common.hpp"
 
+#include <stdlib.h>
+
 namespace mtp {
 
 constexpr int kHD = 128;          // head dim
@@ -197,6 +199,201 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnParams p) {
       const int d = 32 * t + 8 * (r >> 2) + 4 * h2 + (r & 3);
       po[qcol * kHD + d] = o[t][r];
     }
+}
+
+// ---------------------------------------------------------------------------
+// Operand-major KV blocks (the verify step's own cache, kblk_index /
+// vblk_index in common.hpp): every K and V^T MFMA operand of a wave is one
+// 1 KB contiguous load, and V needs no LDS transpose.
+constexpr int kVtWaves = 4;   // waves per workgroup; each takes TPW 32-key tiles
+
+// Unit = (request, kv head, 128*TPW-key split): four waves take 32*TPW keys
+// each and merge in LDS (wave order), so the split partials are 4x fewer than
+// with one wave per split.
+template <int TPW>
+__global__ __launch_bounds__(kVtWaves * 64) void attn_vt_kernel(AttnParams p) {
+  constexpr int kVtWaveKeys = TPW * kTileKeys;
+  constexpr int kVtUnitKeys = kVtWaves * kVtWaveKeys;
+  constexpr int kOS = kHD + 4;   // padded row: lanes of one store hit distinct banks
+  __shared__ float s_o[kVtWaves][32 * kOS];
+  __shared__ float s_m[kVtWaves][32], s_l[kVtWaves][32];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c32 = lane & 31;
+  const int h2 = lane >> 5;
+  const int unit = blockIdx.x;
+  const int s = unit % p.S;
+  const int bh = unit / p.S;
+  const int h = bh % p.Hkv;
+  const int b = bh / p.Hkv;
+  const int rep = p.Hq / p.Hkv;
+  const int qs = p.q_start[b];
+  const int L = p.q_lens ? p.q_lens[b] : p.L;
+  int kv_end = qs + L;
+  if (kv_end > p.cap) kv_end = p.cap;
+  const int k0u = s * kVtUnitKeys;
+  float* po = p.part_o + (size_t)unit * 32 * kHD;
+  float* pml = p.part_ml + (size_t)unit * 64;
+  if (k0u >= kv_end) {
+    if (tid < 32) {
+      pml[2 * tid] = kNegBig;
+      pml[2 * tid + 1] = 0.f;
+    }
+    return;
+  }
+  const int k0 = k0u + wave * kVtWaveKeys;
+  const int k1 = (k0 + kVtWaveKeys < kv_end) ? k0 + kVtWaveKeys : kv_end;
+
+  const int qcol = c32;
+  const int qr = qcol / p.L;
+  const int qi = qcol - qr * p.L;
+  const bool qvalid = (qr < rep) && (qi < L);
+  const int qbound = qs + qi;
+  bf16x8 qop[8];
+  {
+    const uint16_t* qrow = p.q + ((((size_t)b * p.Hq + h * rep + (qvalid ? qr : 0)) * p.L + (qvalid ? qi : 0)) * kHD);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint4 raw = qvalid ? *reinterpret_cast<const uint4*>(qrow + 64 * h2 + 8 * i) : make_uint4(0, 0, 0, 0);
+      qop[i] = __builtin_bit_cast(bf16x8, raw);
+    }
+  }
+  f32x16 o[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) o[t] = f32x16{};
+  float m_run = kNegBig;
+  float l_run = 0.f;
+  const uint16_t* kbase = p.k + ((size_t)b * p.Hkv + h) * (size_t)p.cap * kHD;
+  const uint16_t* vbase = p.v + ((size_t)b * p.Hkv + h) * (size_t)p.cap * kHD;
+
+  // All tiles of this wave are loaded before any compute (one round trip).
+  uint4 kr[TPW][8], vr[TPW][8];
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) {
+    const int kt = k0 + tt * kTileKeys;
+    const bool kin = kt + c32 < k1;
+    const size_t blk = (size_t)((kt < k1 ? kt : k0) >> 5) * 4096 + (size_t)lane * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      kr[tt][i] = kin ? *reinterpret_cast<const uint4*>(kbase + blk + i * 512) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+        vr[tt][2 * t + jj] = *reinterpret_cast<const uint4*>(vbase + blk + (t * 2 + jj) * 512);
+  }
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) {
+    const int kt = k0 + tt * kTileKeys;
+    if (kt >= k1) break;   // wave-uniform
+    f32x16 st = {};
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kr[tt][i]), qop[i], st, 0, 0, 0);
+    float sv[16];
+    float tmax = kNegBig;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kk = kt + 8 * (r >> 2) + 4 * h2 + (r & 3);
+      const bool ok = qvalid && kk < k1 && kk <= qbound;
+      sv[r] = ok ? st[r] * p.scale_log2 : -INFINITY;
+      tmax = fmaxf(tmax, sv[r]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float corr = exp2f(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sv[r] = exp2f(sv[r] - m_new);
+      psum += sv[r];
+    }
+    l_run = l_run * corr + psum;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+    if (kt + kTileKeys > k1) {   // keys past the end: zero V so stale cache bits cannot leak in
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int kbase_e = kt + 16 * jj + 4 * h2;   // slot e<4: kbase_e+e, e>=4: kbase_e+8+e-4
+        uint32_t msk[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int e0 = 2 * w, e1 = 2 * w + 1;
+          const int key0 = kbase_e + (e0 < 4 ? e0 : 8 + e0 - 4);
+          const int key1 = kbase_e + (e1 < 4 ? e1 : 8 + e1 - 4);
+          msk[w] = (key0 < k1 ? 0x0000ffffu : 0u) | (key1 < k1 ? 0xffff0000u : 0u);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          uint4& c = vr[tt][2 * t + jj];
+          c.x &= msk[0];
+          c.y &= msk[1];
+          c.z &= msk[2];
+          c.w &= msk[3];
+        }
+      }
+    }
+    bf16x8 pop[2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      uint32_t pk[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) pk[t] = f2bf2(sv[8 * jj + 2 * t], sv[8 * jj + 2 * t + 1]);
+      pop[jj] = __builtin_bit_cast(bf16x8, pk);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vr[tt][2 * t + jj]), pop[jj],
+                                                        o[t], 0, 0, 0);
+  }
+
+  // Merge the four waves in LDS, wave order (deterministic).
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (h2 == 0) {
+    s_m[wave][c32] = m_run;
+    s_l[wave][c32] = l_tot;
+  }
+  __syncthreads();
+  float mq = s_m[0][c32];
+#pragma unroll
+  for (int w = 1; w < kVtWaves; ++w) mq = fmaxf(mq, s_m[w][c32]);
+  const float sc = exp2f(m_run - mq);
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)   // registers 4j..4j+3 are 4 consecutive d
+      *reinterpret_cast<float4*>(&s_o[wave][qcol * kOS + 32 * t + 8 * j + 4 * h2]) =
+          make_float4(o[t][4 * j] * sc, o[t][4 * j + 1] * sc, o[t][4 * j + 2] * sc, o[t][4 * j + 3] * sc);
+  __syncthreads();
+  for (int idx = 4 * tid; idx < 32 * kHD; idx += 4 * kVtWaves * 64) {
+    const int so = (idx / kHD) * kOS + (idx % kHD);
+    float4 v = *reinterpret_cast<const float4*>(&s_o[0][so]);
+#pragma unroll
+    for (int w = 1; w < kVtWaves; ++w) {
+      const float4 a = *reinterpret_cast<const float4*>(&s_o[w][so]);
+      v.x += a.x;
+      v.y += a.y;
+      v.z += a.z;
+      v.w += a.w;
+    }
+    *reinterpret_cast<float4*>(po + idx) = v;
+  }
+  if (tid < 32) {
+    float M = s_m[0][tid];
+#pragma unroll
+    for (int w = 1; w < kVtWaves; ++w) M = fmaxf(M, s_m[w][tid]);
+    float lsum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kVtWaves; ++w) lsum += s_l[w][tid] * exp2f(s_m[w][tid] - M);
+    pml[2 * tid] = M;
+    pml[2 * tid + 1] = lsum;
+  }
 }
 
 // grid: one 128-thread workgroup per (request, kv head, query column); thread
@@ -415,6 +612,77 @@ MTP_API int mtp_ragged_gqa_attn_rows(const void* q, const void* k, const void* v
                                      float scale, int split_keys, void* ws, size_t ws_bytes, void* stream) {
   return attn_run(q, k, v, q_start, q_lens, out, 1, B, Hq, Hkv, L, D, cap, scale, split_keys, ws, ws_bytes, stream,
                   "mtp_ragged_gqa_attn_rows");
+}
+
+// Tiles per wave: one (more workgroups, shorter chains) while that keeps the
+// partials to merge within kMaxSplits per (request, kv head), else two.
+static int attn_vt_plan(int cap, int* S, int* tpw) {
+  const char* env = getenv("MTPLX_AMD_ATTN_TPW");
+  *tpw = (env && atoi(env) == 2) || cdiv(cap, kVtWaves * kTileKeys) > kMaxSplits ? 2 : 1;
+  *S = cdiv(cap, kVtWaves * kTileKeys * *tpw);
+  return (*S <= kMaxSplits) ? MTP_OK : MTP_ERR_UNSUPPORTED;
+}
+
+MTP_API size_t mtp_attn_vt_workspace_bytes(int B, int Hkv, int cap) {
+  int S = 0, tpw = 1;
+  if (B < 1 || Hkv < 1 || cap < 1 || attn_vt_plan(cap, &S, &tpw) != MTP_OK) return 0;
+  const size_t units = (size_t)B * Hkv * S;
+  return units * 32 * kHD * sizeof(float) + units * 64 * sizeof(float);
+}
+
+MTP_API int mtp_ragged_gqa_attn_rows_vt(const void* q, const void* k, const void* v_vt, const int32_t* q_start,
+                                        const int32_t* q_lens, void* out, int B, int Hq, int Hkv, int L, int D,
+                                        int cap, float scale, void* ws, size_t ws_bytes, void* stream) {
+  const char* who = "mtp_ragged_gqa_attn_rows_vt";
+  if (!q || !k || !v_vt || !q_start || !out || B < 1 || Hq < 1 || Hkv < 1 || L < 1 || cap < 32 || cap % 32) {
+    set_error("%s: bad arguments (cap must be a positive multiple of 32)", who);
+    return MTP_ERR_ARG;
+  }
+  if (D != kHD) {
+    set_error("%s: head_dim %d unsupported (128)", who, D);
+    return MTP_ERR_UNSUPPORTED;
+  }
+  if (Hq % Hkv || (Hq / Hkv) * L > 32) {
+    set_error("%s: need Hq %% Hkv == 0 and (Hq/Hkv)*L <= 32 (Hq=%d Hkv=%d L=%d)", who, Hq, Hkv, L);
+    return MTP_ERR_UNSUPPORTED;
+  }
+  AttnParams p{};
+  p.q = (const uint16_t*)q;
+  p.k = (const uint16_t*)k;
+  p.v = (const uint16_t*)v_vt;
+  p.q_start = q_start;
+  p.q_lens = q_lens;
+  p.out = (uint16_t*)out;
+  p.B = B;
+  p.Hq = Hq;
+  p.Hkv = Hkv;
+  p.L = L;
+  p.cap = cap;
+  p.out_rows = 1;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  int tpw = 1;
+  if (attn_vt_plan(cap, &p.S, &tpw) != MTP_OK) {
+    set_error("%s: capacity %d needs more than %d splits", who, cap, kMaxSplits);
+    return MTP_ERR_UNSUPPORTED;
+  }
+  p.split_keys = kVtWaves * kTileKeys * tpw;
+  const size_t need = mtp_attn_vt_workspace_bytes(B, Hkv, cap);
+  if (!ws || ws_bytes < need) {
+    set_error("%s: workspace %zu < %zu", who, ws_bytes, need);
+    return MTP_ERR_WORKSPACE;
+  }
+  const size_t units = (size_t)B * Hkv * p.S;
+  p.part_o = (float*)ws;
+  p.part_ml = (float*)ws + units * 32 * kHD;
+  if (tpw == 1)
+    hipLaunchKernelGGL(attn_vt_kernel<1>, dim3((unsigned)units), dim3(kVtWaves * 64), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(attn_vt_kernel<2>, dim3((unsigned)units), dim3(kVtWaves * 64), 0, (hipStream_t)stream, p);
+  int rc = launch_check(who);
+  if (rc) return rc;
+  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * Hkv * (Hq / Hkv) * L)), dim3(128), 0,
+                     (hipStream_t)stream, p);
+  return launch_check(who);
 }
 
 MTP_API int mtp_kv_scatter(void* k_cache, void* v_cache, const void* k_new, const void* v_new,

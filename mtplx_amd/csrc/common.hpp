@@ -60,4 +60,23 @@ __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 
 __host__ __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// MFMA operand-major KV cache layout (the verify step's own cache, head dim
+// 128): per (request, kv head), 32-key blocks of 4096 elements in which every
+// attention MFMA operand of a wave is 64 lanes x 16 contiguous bytes.
+//   K block: operand i (0..7) of lane (key kk, half h2) = d 64 h2 + 8 i .. +7,
+//            at ((i*2 + h2)*32 + kk)*8.
+//   V block: operand (t, jj) of lane (d = 32t + c, half h2) = keys
+//            16 jj + {4h2 + e (e<4), 8 + 4h2 + e-4 (e>=4)}, at
+//            ((t*2 + jj)*64 + h2*32 + c)*8 + e.
+__host__ __device__ __forceinline__ size_t kblk_index(int key, int d) {
+  const int c = d >> 3, i = c & 7, h2 = c >> 3;
+  return (size_t)(key >> 5) * 4096 + ((size_t)(i * 2 + h2) * 32 + (key & 31)) * 8 + (d & 7);
+}
+__host__ __device__ __forceinline__ size_t vblk_index(int key, int d) {
+  const int kk = key & 31, jj = kk >> 4, r = kk & 15;
+  const int h2 = (r & 7) >> 2, e = (r < 8) ? (r & 3) : 4 + (r & 3);
+  const int t = d >> 5, c = d & 31;
+  return (size_t)(key >> 5) * 4096 + ((size_t)(t * 2 + jj) * 64 + h2 * 32 + c) * 8 + e;
+}
+
 }  // namespace mtp

@@ -40,7 +40,7 @@ __global__ void embed_affine4_kernel(const int32_t* tok, const uint32_t* w, cons
 // One thread per (row, head, rotary pair) for q and k; v copied 8 elements per thread.
 __global__ void rope_qkv_kernel(const uint16_t* qkv, const int32_t* q_start, const int32_t* q_lens, uint16_t* q_out,
                                 uint16_t* kc, uint16_t* vc, int B, int L, int Hq, int Hkv, int D, int cap,
-                                float log2_base, int32_t* status) {
+                                float log2_base, int32_t* status, int kv_blocked) {
   const int half = D / 2;
   const int m = blockIdx.y;
   const int b = m / L;
@@ -71,9 +71,15 @@ __global__ void rope_qkv_kernel(const uint16_t* qkv, const int32_t* q_start, con
           if (status) atomicOr(status, 1);
           continue;
         }
-        uint16_t* dst = kc + (((size_t)b * Hkv + (head - Hq)) * cap + pos) * D;
-        dst[j] = o1;
-        dst[j + half] = o2;
+        if (kv_blocked) {
+          uint16_t* kh = kc + ((size_t)b * Hkv + (head - Hq)) * cap * D;
+          kh[kblk_index(pos, j)] = o1;
+          kh[kblk_index(pos, j + half)] = o2;
+        } else {
+          uint16_t* dst = kc + (((size_t)b * Hkv + (head - Hq)) * cap + pos) * D;
+          dst[j] = o1;
+          dst[j + half] = o2;
+        }
       }
     } else if (i < len) {
       const int e = (t - nrot) * 8;
@@ -83,8 +89,18 @@ __global__ void rope_qkv_kernel(const uint16_t* qkv, const int32_t* q_start, con
         if (status) atomicOr(status, 1);
         continue;
       }
-      *reinterpret_cast<uint4*>(vc + (((size_t)b * Hkv + head) * cap + pos) * D + d) =
-          *reinterpret_cast<const uint4*>(row + (Hq + Hkv) * D + e);
+      const uint4 val = *reinterpret_cast<const uint4*>(row + (Hq + Hkv) * D + e);
+      if (kv_blocked) {   // operand-major blocks: the 8 values go to 8 d positions of their key block
+        uint16_t* vh = vc + ((size_t)b * Hkv + head) * cap * D;
+        const uint32_t w4[4] = {val.x, val.y, val.z, val.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          vh[vblk_index(pos, d + 2 * t)] = (uint16_t)(w4[t] & 0xffff);
+          vh[vblk_index(pos, d + 2 * t + 1)] = (uint16_t)(w4[t] >> 16);
+        }
+      } else {
+        *reinterpret_cast<uint4*>(vc + (((size_t)b * Hkv + head) * cap + pos) * D + d) = val;
+      }
     }
   }
 }
@@ -124,20 +140,34 @@ MTP_API int mtp_embed_affine4(const int32_t* tokens, const void* w, const void* 
   return launch_check("mtp_embed_affine4");
 }
 
-MTP_API int mtp_rope_qkv_to_cache(const void* qkv, const int32_t* q_start, const int32_t* q_lens, void* q_out,
-                                  void* k_cache, void* v_cache, int B, int L, int Hq, int Hkv, int D, int cap,
-                                  float rope_base, int32_t* status, void* stream) {
+static int rope_run(const void* qkv, const int32_t* q_start, const int32_t* q_lens, void* q_out, void* k_cache,
+                    void* v_cache, int B, int L, int Hq, int Hkv, int D, int cap, float rope_base, int32_t* status,
+                    void* stream, int kv_blocked, const char* who) {
   if (!qkv || !q_start || !q_out || !k_cache || !v_cache || B < 1 || L < 1 || Hq < 1 || Hkv < 1 || D < 8 ||
-      D % 8 || cap < 1 || !(rope_base > 1.f)) {
-    set_error("mtp_rope_qkv_to_cache: bad arguments");
+      D % 8 || cap < 1 || !(rope_base > 1.f) || (kv_blocked && (cap % 32 || D != 128))) {
+    set_error("%s: bad arguments", who);
     return MTP_ERR_ARG;
   }
   const int work = (Hq + Hkv) * (D / 2) + Hkv * D / 8;
   dim3 grid(cdiv(work, 256), B * L);
   hipLaunchKernelGGL(rope_qkv_kernel, grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t*)qkv, q_start, q_lens,
                      (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, B, L, Hq, Hkv, D, cap,
-                     log2f(rope_base), status);
-  return launch_check("mtp_rope_qkv_to_cache");
+                     log2f(rope_base), status, kv_blocked);
+  return launch_check(who);
+}
+
+MTP_API int mtp_rope_qkv_to_cache(const void* qkv, const int32_t* q_start, const int32_t* q_lens, void* q_out,
+                                  void* k_cache, void* v_cache, int B, int L, int Hq, int Hkv, int D, int cap,
+                                  float rope_base, int32_t* status, void* stream) {
+  return rope_run(qkv, q_start, q_lens, q_out, k_cache, v_cache, B, L, Hq, Hkv, D, cap, rope_base, status, stream, 0,
+                  "mtp_rope_qkv_to_cache");
+}
+
+MTP_API int mtp_rope_qkv_to_cache_vt(const void* qkv, const int32_t* q_start, const int32_t* q_lens, void* q_out,
+                                     void* k_cache, void* v_cache, int B, int L, int Hq, int Hkv, int D, int cap,
+                                     float rope_base, int32_t* status, void* stream) {
+  return rope_run(qkv, q_start, q_lens, q_out, k_cache, v_cache, B, L, Hq, Hkv, D, cap, rope_base, status, stream, 1,
+                  "mtp_rope_qkv_to_cache_vt");
 }
 
 MTP_API int mtp_rmsnorm(const void* x, const void* w, void* out, int M, int H, float eps, void* stream) {

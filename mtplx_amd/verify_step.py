@@ -85,6 +85,39 @@ class Layer:
     shared_down: QuantizedLinear | None = None
 
 
+def kv_block_offsets(kind: str) -> list[int]:
+    """Offset inside a 4096-element block of (key % 32, d) = index key%32*128 + d,
+    for the operand-major K ("k") or V ("v") cache blocks (head dim 128)."""
+    offs = []
+    for kk in range(32):
+        for d in range(128):
+            if kind == "k":
+                c = d // 8
+                offs.append(((c % 8) * 2 + c // 8) * 256 + kk * 8 + d % 8)
+            else:
+                jj, r = kk // 16, kk % 16
+                h2 = (r % 8) // 4
+                e = r % 4 if r < 8 else 4 + r % 4
+                offs.append(((d // 32) * 2 + jj) * 512 + (h2 * 32 + d % 32) * 8 + e)
+    return offs
+
+
+def kv_to_blocks(std: torch.Tensor, kind: str) -> torch.Tensor:
+    """[B, Hkv, cap, 128] -> operand-major blocks (same shape and storage size)."""
+    B, H, cap, D = std.shape
+    src = std.reshape(B, H, cap // 32, 4096)
+    out = torch.empty_like(src)
+    out[..., torch.tensor(kv_block_offsets(kind), device=std.device)] = src
+    return out.reshape(B, H, cap, D)
+
+
+def kv_from_blocks(blk: torch.Tensor, kind: str) -> torch.Tensor:
+    """Inverse of :func:`kv_to_blocks`."""
+    B, H, cap, D = blk.shape
+    src = blk.reshape(B, H, cap // 32, 4096)
+    return src.index_select(3, torch.tensor(kv_block_offsets(kind), device=blk.device)).reshape(B, H, cap, D)
+
+
 class VerifyModel:
     """Random-init weights of ``cfg`` resident in HBM plus a ragged KV cache."""
 
@@ -145,6 +178,14 @@ class VerifyModel:
         self.cap = cap
         self.batch = batch
 
+    # K and V caches are kept in the operand-major 32-key block layout
+    # (include/mtplx_amd.h); these give the reference [B, Hkv, cap, D] view.
+    def k_cache_standard(self, li: int) -> torch.Tensor:
+        return kv_from_blocks(self.k_cache[li], "k")
+
+    def v_cache_standard(self, li: int) -> torch.Tensor:
+        return kv_from_blocks(self.v_cache[li], "v")
+
     def synthetic_router_logits(self, tokens: int) -> None:
         """Per-layer router logits skewed Zipf(s) over experts: logit_e = -s*log(rank_e)
         with a per-layer random expert ranking plus N(0, 0.5) noise per token."""
@@ -187,7 +228,7 @@ class VerifyModel:
         ss_a = torch.empty(((H + 31) // 32) * 32, dtype=torch.float32, device=dev)
         ss_b = torch.empty_like(ss_a)
         ss_h = None
-        nb = _lib.query("mtp_attn_workspace_bytes", B, c.n_kv_heads, self.cap, 0)
+        nb = _lib.query("mtp_attn_vt_workspace_bytes", B, c.n_kv_heads, self.cap)
         aws = _lib.WORKSPACES.get(nb, "attn", dev)
         scale = 1.0 / math.sqrt(c.head_dim)
         ql = None if q_lens is None else q_lens.to(torch.int32).contiguous()
@@ -198,12 +239,12 @@ class VerifyModel:
         for li, L in enumerate(self.layers):
             qmv(st, x=h, x2=L.in_norm, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv.packed, y0=qkv, M=M, N=c.qkv_out, K=H,
                 group_size=gs, xmode=2, emode=0, packed=1)
-            call("mtp_rope_qkv_to_cache", qkv.data_ptr(), q_start.data_ptr(), _lib.ptr(ql), qh.data_ptr(),
+            call("mtp_rope_qkv_to_cache_vt", qkv.data_ptr(), q_start.data_ptr(), _lib.ptr(ql), qh.data_ptr(),
                  self.k_cache[li].data_ptr(), self.v_cache[li].data_ptr(), B, Lq, c.n_heads, c.n_kv_heads,
                  c.head_dim, self.cap, ctypes.c_float(c.rope_theta), status.data_ptr(), st)
-            call("mtp_ragged_gqa_attn_rows", qh.data_ptr(), self.k_cache[li].data_ptr(),
+            call("mtp_ragged_gqa_attn_rows_vt", qh.data_ptr(), self.k_cache[li].data_ptr(),
                  self.v_cache[li].data_ptr(), q_start.data_ptr(), _lib.ptr(ql), attn.data_ptr(), B, c.n_heads,
-                 c.n_kv_heads, Lq, c.head_dim, self.cap, ctypes.c_float(scale), 0, aws.data_ptr(), aws.numel(), st)
+                 c.n_kv_heads, Lq, c.head_dim, self.cap, ctypes.c_float(scale), aws.data_ptr(), aws.numel(), st)
             qmv(st, x=attn, w0=L.o.packed, resid=h, y0=h, ss_out=ss_a, M=M, N=H, K=c.n_heads * c.head_dim,
                 group_size=gs, xmode=0, emode=1, packed=1)
             ss_h = ss_a

@@ -125,3 +125,71 @@ def test_kv_scatter_restore_and_mask_bit_exact(gpu):
     _lib.call("mtp_ragged_causal_mask", m.data_ptr(), qs.data_ptr(), B, 4, 20, _st())
     torch.cuda.synchronize()
     assert np.array_equal(m.cpu().numpy().astype(bool), A.ragged_causal_mask([0, 5, 9], 4, 20))
+
+
+from mtplx_amd.verify_step import kv_to_blocks
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,cap,starts,lens", [
+    (1, 40, 8, 4, 4096, [4092], None),                     # cfg3 verify shape
+    (3, 40, 8, 4, 736, [17, 300, 700], None),
+    (2, 32, 4, 4, 1312, [1000, 5], [4, 2]),
+    (2, 16, 2, 2, 128, [33, 90], None),
+    (1, 8, 8, 1, 64, [40], None),
+])
+def test_blocked_v_attention_matches_oracle(gpu, B, Hq, Hkv, L, cap, starts, lens):
+    """The verify step's attention over the operand-major K/V block cache:
+    oracle within the bf16 bar, and within one bf16 ulp of the reference-layout
+    kernel."""
+    rng = np.random.default_rng(B * 1000 + cap + L)
+    q = randn_bf16(rng, (B, Hq, L, 128)); k = randn_bf16(rng, (B, Hkv, cap, 128)); v = randn_bf16(rng, (B, Hkv, cap, 128))
+    qs = torch.tensor(starts, dtype=torch.int32, device="cuda")
+    ql = None if lens is None else torch.tensor(lens, dtype=torch.int32, device="cuda")
+    # stale bits past every request's keys must not leak in: poison them in the blocked copy
+    vt_std = v.clone()
+    for b, s in enumerate(starts):
+        end = s + (L if lens is None else lens[b])
+        vt_std[b, :, end:] = float("nan")
+    kb = kv_to_blocks(k, "k")
+    vt = kv_to_blocks(vt_std, "v")
+    out = torch.full((B, L, Hq, 128), float("nan"), dtype=torch.bfloat16, device="cuda")
+    nb = _lib.query("mtp_attn_vt_workspace_bytes", B, Hkv, cap)
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    _lib.call("mtp_ragged_gqa_attn_rows_vt", q.data_ptr(), kb.data_ptr(), vt.data_ptr(), qs.data_ptr(),
+              None if ql is None else ql.data_ptr(), out.data_ptr(), B, Hq, Hkv, L, 128, cap,
+              1.0 / math.sqrt(128), ws.data_ptr(), nb, _st())
+    torch.cuda.synchronize()
+    got = bf16_values(out.permute(0, 2, 1, 3).contiguous())
+    qlen = [L] * B if lens is None else lens
+    for b in range(B):
+        want = A.ragged_gqa_attention(bits(q[b:b + 1]), bits(k[b:b + 1]), bits(v[b:b + 1]), [starts[b]])
+        assert_close(got[b:b + 1, :, :qlen[b]], want[:, :, :qlen[b]], what=f"blocked-V attention b={b}")
+    ref = bf16_values(_attn(q, k, v, starts, q_lens=lens).float().to(torch.bfloat16))
+    for b in range(B):
+        a, r = got[b, :, :qlen[b]], ref[b, :, :qlen[b]]
+        tol = np.maximum(np.abs(a), np.abs(r)) * 2.0 ** -7 + 1e-3
+        assert (np.abs(a - r) <= tol).all(), np.abs(a - r).max()
+
+
+def test_blocked_v_rope_writer(gpu):
+    """mtp_rope_qkv_to_cache_vt writes the same q, K and V values as the
+    reference-layout writer, K and V in the operand-major block layout."""
+    rng = np.random.default_rng(9)
+    B, L, Hq, Hkv, D, cap = 2, 4, 8, 2, 128, 256
+    qkv = randn_bf16(rng, (B * L, (Hq + 2 * Hkv) * D))
+    qs = torch.tensor([30, 250], dtype=torch.int32, device="cuda")
+    outs = []
+    for fn in ("mtp_rope_qkv_to_cache", "mtp_rope_qkv_to_cache_vt"):
+        qo = torch.zeros((B, Hq, L, D), dtype=torch.bfloat16, device="cuda")
+        kc = torch.zeros((B, Hkv, cap, D), dtype=torch.bfloat16, device="cuda")
+        vc = torch.zeros_like(kc)
+        st = torch.zeros(1, dtype=torch.int32, device="cuda")
+        _lib.call(fn, qkv.data_ptr(), qs.data_ptr(), None, qo.data_ptr(), kc.data_ptr(), vc.data_ptr(), B, L, Hq, Hkv,
+                  D, cap, 1e6, st.data_ptr(), _st())
+        torch.cuda.synchronize()
+        outs.append((qo, kc, vc, int(st.item())))
+    (q0, k0, v0, s0), (q1, k1, v1, s1) = outs
+    assert torch.equal(q0.view(torch.int16), q1.view(torch.int16))
+    assert torch.equal(kv_to_blocks(k0, "k").view(torch.int16), k1.view(torch.int16))
+    assert torch.equal(kv_to_blocks(v0, "v").view(torch.int16), v1.view(torch.int16))
+    assert s0 == 0 and s1 == 0

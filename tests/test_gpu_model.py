@@ -21,8 +21,8 @@ def _run(cfg, B, L, starts, seed, moe_tokens=None):
     if cfg.n_experts:
         model.synthetic_router_logits(B * L)
         router = [route_topk(Lr.router_logits.cpu().numpy(), cfg.top_k) for Lr in model.layers]
-    kc = [k.float().cpu().numpy().astype(np.float64) for k in model.k_cache]
-    vc = [v.float().cpu().numpy().astype(np.float64) for v in model.v_cache]
+    kc = [model.k_cache_standard(li).float().cpu().numpy().astype(np.float64) for li in range(cfg.layers)]
+    vc = [model.v_cache_standard(li).float().cpu().numpy().astype(np.float64) for li in range(cfg.layers)]
     gen = torch.Generator(device="cuda").manual_seed(seed + 1)
     tokens = torch.randint(0, cfg.vocab, (B, L), device="cuda", dtype=torch.int32, generator=gen)
     qs = torch.tensor(starts, dtype=torch.int32, device="cuda")
@@ -39,7 +39,7 @@ def test_dense_verify_step_matches_oracle(gpu):
     assert_close(logits.cpu().numpy().astype(np.float64), want, rtol=3e-2, atol=3e-2, what="dense logits")
     # the K/V rows the step wrote are the oracle's (RoPE'd k, raw v) within bf16 tolerance
     for li in range(cfg.layers):
-        got_k = model.k_cache[li].float().cpu().numpy()
+        got_k = model.k_cache_standard(li).float().cpu().numpy()
         for b, s in enumerate([37, 200]):
             assert_close(got_k[b, :, s:s + 4], kc[li][b, :, s:s + 4], rtol=2e-2, atol=2e-2, what="k rows")
     # accept/reject on the GPU logits is token-exact against the oracle law
