@@ -113,7 +113,23 @@ int mtp_pack_affine4(const void* w, const void* scales, const void* biases, void
  * (256-byte aligned, zeroed once before first use and then left to the
  * library) selects the stream-K kernel, which spreads (tile, 256-k) items
  * evenly over all CUs; calls sharing one workspace must be stream-ordered.
- * Without it the per-tile kernel runs. */
+ * Without it the per-tile kernel runs.
+ * emode 4 = q|k|v projection with RoPE and the cache write fused into the
+ * epilogue (the work of mtp_rope_qkv_to_cache / _vt below, same rounding):
+ * rope points at the outputs; y0 is unused; packed weights whose rows are in
+ * RoPE tile order - packed row 32t + c of head h = t / (D/32), sub-block
+ * sb = t % (D/32) is original row h*D + 16 sb + c % 16 + (c / 16) * D/2 -
+ * so each 32-column tile holds 16 rotate-half pairs. M <= 8, M = B * L. */
+typedef struct mtp_rope_out {
+  const int32_t* q_start; /* [B] first position of each request's rows */
+  const int32_t* q_lens;  /* [B] rows written to the cache, or NULL (= L) */
+  void* q_out;            /* [B, Hq, L, D] bf16 */
+  void* k_cache;          /* blocked = 1: operand-major blocks (below); 0: [B, Hkv, cap, D] */
+  void* v_cache;
+  int32_t* status;        /* bit 0 set when a position falls outside [0, cap); may be NULL */
+  int L, Hq, Hkv, D, cap, blocked;
+  float rope_base;
+} mtp_rope_out;
 typedef struct mtp_qmv_args {
   const void* x;
   const void* x2;
@@ -134,6 +150,7 @@ typedef struct mtp_qmv_args {
   int xmode, emode, packed;
   void* ws;
   size_t ws_bytes;
+  const mtp_rope_out* rope; /* emode 4 only */
 } mtp_qmv_args;
 int mtp_qmv_affine4_ex(const mtp_qmv_args* args, void* stream);
 

@@ -61,22 +61,38 @@ SIGNATURES = {
 }
 
 
+class RopeOut(C.Structure):
+    """``mtp_rope_out`` of include/mtplx_amd.h (same field order)."""
+
+    _fields_ = [(n, _vp) for n in ("q_start", "q_lens", "q_out", "k_cache", "v_cache", "status")] + \
+               [(n, _i) for n in ("L", "Hq", "Hkv", "D", "cap", "blocked")] + [("rope_base", _f)]
+
+
 class QmvArgs(C.Structure):
     """``mtp_qmv_args`` of include/mtplx_amd.h (same field order)."""
 
     _fields_ = [(n, _vp) for n in ("x", "x2", "ss_in", "w0", "s0", "b0", "w1", "s1", "b1", "y0", "y1", "yf",
                                    "resid", "ss_out")] + [("eps", _f)] + \
                [(n, _i) for n in ("M", "N", "K", "group_size", "ldx", "ldy", "xmode", "emode", "packed")] + \
-               [("ws", _vp), ("ws_bytes", C.c_size_t)]
+               [("ws", _vp), ("ws_bytes", C.c_size_t), ("rope", C.POINTER(RopeOut))]
 
 
-def qmv_ex(stream, **fields) -> None:
-    """Call ``mtp_qmv_affine4_ex``; tensor fields may be torch tensors or None."""
-    a = QmvArgs()
+def _fill(struct, fields: dict):
     for k, v in fields.items():
         if hasattr(v, "data_ptr"):
             v = v.data_ptr()
-        setattr(a, k, v)
+        setattr(struct, k, v)
+    return struct
+
+
+def qmv_ex(stream, rope: dict | None = None, **fields) -> None:
+    """Call ``mtp_qmv_affine4_ex``; tensor fields may be torch tensors or None.
+    ``rope``: fields of ``mtp_rope_out`` (emode 4)."""
+    a = _fill(QmvArgs(), fields)
+    r = None
+    if rope is not None:
+        r = _fill(RopeOut(), rope)
+        a.rope = C.pointer(r)
     call("mtp_qmv_affine4_ex", C.byref(a), stream)
 
 

@@ -60,6 +60,26 @@ __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 
 __host__ __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// Rotate-half RoPE of the pair (d, d + D/2) at position pos, fp32 angle
+// theta = pos * 2^(-(2d/D) * log2(base)); outputs rounded to bf16. Shared by
+// the standalone RoPE kernel and the fused q|k|v matmul epilogue so both
+// round identically.
+__device__ __forceinline__ void rope_angle(int pos, int d, int D, float log2_base, float& sn, float& cs) {
+  const float inv_freq = exp2f(-((float)(2 * d) / (float)D) * log2_base);
+  const float theta = (float)pos * inv_freq;
+  sincosf(theta, &sn, &cs);
+}
+__device__ __forceinline__ void rope_apply(float x1, float x2, float sn, float cs, uint16_t& o1, uint16_t& o2) {
+  o1 = f2bf(x1 * cs - x2 * sn);
+  o2 = f2bf(x1 * sn + x2 * cs);
+}
+__device__ __forceinline__ void rope_pair(float x1, float x2, int pos, int d, int D, float log2_base, uint16_t& o1,
+                                          uint16_t& o2) {
+  float sn, cs;
+  rope_angle(pos, d, D, log2_base, sn, cs);
+  rope_apply(x1, x2, sn, cs, o1, o2);
+}
+
 // MFMA operand-major KV cache layout (the verify step's own cache, head dim
 // 128): per (request, kv head), 32-key blocks of 4096 elements in which every
 // attention MFMA operand of a wave is 64 lanes x 16 contiguous bytes.

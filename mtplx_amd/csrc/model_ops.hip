@@ -54,14 +54,9 @@ __global__ void rope_qkv_kernel(const uint16_t* qkv, const int32_t* q_start, con
     if (t < nrot) {
       const int head = t / half;
       const int j = t - head * half;
-      const float inv_freq = exp2f(-((float)(2 * j) / (float)D) * log2_base);
-      const float theta = (float)pos * inv_freq;
-      float sn, cs;
-      sincosf(theta, &sn, &cs);
       const uint16_t* src = row + head * D;
-      const float x1 = bf2f(src[j]), x2 = bf2f(src[j + half]);
-      const uint16_t o1 = f2bf(x1 * cs - x2 * sn);
-      const uint16_t o2 = f2bf(x1 * sn + x2 * cs);
+      uint16_t o1, o2;
+      rope_pair(bf2f(src[j]), bf2f(src[j + half]), pos, j, D, log2_base, o1, o2);
       if (head < Hq) {
         uint16_t* dst = q_out + (((size_t)b * Hq + head) * L + i) * D;
         dst[j] = o1;

@@ -501,11 +501,11 @@ __global__ __launch_bounds__(NW * 64) void qmv_chunked_kernel(QmmParams p) {
 // ---------------------------------------------------------------------------
 // Resident streaming kernel (the fast path): all of x is staged into LDS once
 // per workgroup, then every wave walks its flat (tile, quad) item list with a
-// three-deep register ring (A, B, C) advanced by unrolling — no register
-// copies and no data-dependent branches between a load and its use, so the
-// compiler's wait for quad i only covers loads issued before i (the two
-// quads behind it stay in flight). Lanes whose A-operand row is past M read
-// a zero block in LDS instead of branching.
+// register ring of NR quads advanced by unrolling — no register copies and
+// no data-dependent branches between a load and its use, so the compiler's
+// wait for quad i only covers loads issued before i (the NR-1 quads behind it
+// stay in flight). Lanes whose A-operand row is past M read a zero block in
+// LDS instead of branching.
 template <int NW, int R, int XM, int EM, int GSH, bool PK>
 __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -513,6 +513,7 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   constexpr bool dual = (EM == E_DUAL || EM == E_DUAL_SWIGLU);
   constexpr int KS = dual ? NW / 2 : NW;
   constexpr int XSW = 2 * R;
+  constexpr int NR = 3;   // ring depth (deeper rings measured slower)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar loop control
@@ -528,7 +529,6 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   float* xs = reinterpret_cast<float*>(smem + xa_bytes(4 * Q, M));             // [Q*4][XSW]
   float* red = xs + Q * 4 * XSW;                                               // [NW][M][32]
   float* fin = red + NW * M * 32;                                              // [M][64]
-  uint16_t* nwt = reinterpret_cast<uint16_t*>(fin + M * 64);                   // X_RMSNORM: norm weight [K]
   __shared__ float s_inv_rms[32];
 
   const int c32 = lane & 31;
@@ -629,6 +629,16 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
     const int col = (int)blockIdx.x * 32 + (tid & 31);
     if (col < p.N) pre_resid = bf2f(p.resid[(size_t)(tid >> 5) * p.ldy + col]);
   }
+  // E_ROPE_QKV: the request offsets of this thread's first epilogue element
+  // are fetched now; its rotation is computed after staging.
+  RopeRow rope_pre = {};
+  const bool use_rpre = (EM == E_ROPE_QKV) && ntiles > 0 && tid < M * 16;
+  int rq_start = 0, rq_len = 0;
+  if (use_rpre) {
+    const int b = (tid >> 4) / p.rope_L;
+    rq_start = p.q_start[b];
+    rq_len = p.q_lens ? p.q_lens[b] : p.rope_L;
+  }
 
   // End of tile j: reduce the K-split waves in LDS (wave order), epilogue.
   auto finish = [&](int j) {
@@ -657,23 +667,25 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
       fin[idx] = v;
     }
     __syncthreads();
-    qmm_epilogue<NW, EM>(p, fin, nb, M, 0, (use_pre && j == 0) ? &pre_resid : nullptr);
+    qmm_epilogue<NW, EM>(p, fin, nb, M, 0, (use_pre && j == 0) ? &pre_resid : nullptr,
+                         (use_rpre && j == 0) ? &rope_pre : nullptr);
   };
 
-  // Prologue: the norm statistics, x (and the norm weights) straight into
-  // LDS, then all three ring slots, issued back to back. The wait below is
-  // for everything but the ring loads (they are the newest), so staging x
-  // overlaps the weights' first round trip.
+  // Prologue: the norm statistics, x straight into LDS, the norm weights
+  // into registers, then all three ring slots, issued back to back. The
+  // wait below is for everything but the ring loads (they are the newest),
+  // so staging x overlaps the weights' first round trip.
   float ssv[kMaxSsLoads];
   if (XM == X_RMSNORM && p.ss_in && wave < M) ss_prefetch(p, wave, lane, ssv);
-  stage_x_issue<XM, NW>(p, xa, rstride, nwt, M, Q, 0, Q, wave, lane);
+  stage_x_issue<NW>(p, xa, rstride, M, Q, 0, Q, wave, lane);
+  uint4 wpre[kNormPre];
+  if (XM == X_RMSNORM) norm_w_prefetch<NW>(p, wpre, Q, 0, Q, tid);
   asm volatile("" ::: "memory");
-  QuadRegs A, B, C;
-  load_next(A);   // waves without items reload a valid block; never used
-  load_next(B);
-  load_next(C);
+  QuadRegs ring[NR];
+#pragma unroll
+  for (int u = 0; u < NR; ++u) load_next(ring[u]);   // waves without items reload a valid block; never used
   asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * (PK ? 5 : 6)));
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(NR * (PK ? 5 : 6)));
   if (XM == X_RMSNORM) {
     for (int m = wave; m < M; m += NW) {
       const float v = (p.ss_in && m == wave) ? ss_reduce(p, ssv, lane) : row_inv_rms(p, m, lane);
@@ -681,8 +693,13 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
     }
   }
   __syncthreads();
-  stage_x_finish<XM, NW, XSW, PK>(p, xa, rstride, xs, nwt, s_inv_rms, M, Q, 0, Q, tid);
+  stage_x_finish<XM, NW, XSW, PK>(p, xa, rstride, xs, wpre, s_inv_rms, M, Q, 0, Q, tid);
   __syncthreads();  // staged x visible to every wave
+  if (use_rpre) {
+    const int head = (int)blockIdx.x / (p.rope_D >> 5);
+    const int d = 16 * ((int)blockIdx.x - head * (p.rope_D >> 5)) + (tid & 15);
+    rope_pre = rope_row(p, tid >> 4, d, rq_start, rq_len);
+  }
 
   // Every wave of the workgroup must reach each tile's barriers: waves with
   // fewer quads per tile (qw smaller) still finish every tile.
@@ -708,12 +725,11 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
     }
   };
   do {
-    step(A);
-    load_next(A);
-    step(B);
-    load_next(B);
-    step(C);
-    load_next(C);
+#pragma unroll
+    for (int u = 0; u < NR; ++u) {
+      step(ring[u]);
+      load_next(ring[u]);
+    }
   } while (i < nitems);
 }
 
@@ -760,14 +776,14 @@ static constexpr size_t kLdsBudget = 65536 - 256;
 // Waves per workgroup: 8 when the column tiles alone cannot give every CU
 // two workgroups (small N: q|k|v, o, down), else 4. All of K is staged once
 // per workgroup when it fits in LDS, else in chunks per tile.
-static Plan make_plan(int M, int N, int K, bool norm = false) {
+static Plan make_plan(int M, int N, int K) {
   Plan pl;
   pl.n_blocks = cdiv(N, 32);
   const int Q = K / 256;
   const int nw_env = env_int("MTPLX_AMD_QMV_WAVES", 0);
   pl.nw = (nw_env == 4 || nw_env == 8) ? nw_env : (pl.n_blocks < 512 ? 8 : 4);
   const int cap = env_int("MTPLX_AMD_QMV_CHUNK_QUADS", 0);
-  pl.resident = cap <= 0 && stream_lds(Q, M, pl.nw) + (norm ? (size_t)K * 2 : 0) <= kLdsMax;
+  pl.resident = cap <= 0 && stream_lds(Q, M, pl.nw) <= kLdsMax;
   if (pl.resident) {
     pl.chunk = Q;
   } else {
@@ -776,7 +792,7 @@ static Plan make_plan(int M, int N, int K, bool norm = false) {
     if (cap > 0 && cap < ch) ch = cap;
     pl.chunk = ch;
   }
-  pl.lds = stream_lds(pl.chunk, M, pl.nw) + (norm ? (size_t)K * 2 : 0);
+  pl.lds = stream_lds(pl.chunk, M, pl.nw);
   return pl;
 }
 
@@ -807,7 +823,8 @@ static int stream_grid(K kernel, int nt, size_t lds, int n_blocks) {
 
 template <typename K>
 static void launch_one(K k, const Plan& pl, int nt, hipStream_t st, const QmmParams& q) {
-  if (pl.lds > 65536) hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl.lds);
+  // A failure here surfaces as a launch error, which the caller checks.
+  if (pl.lds > 65536) (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl.lds);
   hipLaunchKernelGGL(k, dim3(stream_grid(k, nt, pl.lds, pl.n_blocks)), dim3(nt), pl.lds, st, q);
 }
 
@@ -860,6 +877,15 @@ static void launch_x(int xm, int em, const QmmParams& p, const Plan& pl, hipStre
   }
 }
 
+// q|k|v with the RoPE epilogue: packed weights, R = 4 (M <= 8) only.
+template <int XM>
+static void launch_rope(const QmmParams& q, const Plan& pl, hipStream_t st) {
+  if (pl.nw == 8)
+    launch_one(qmv_stream_kernel<8, 4, XM, E_ROPE_QKV, 0, true>, pl, 8 * 64, st, q);
+  else
+    launch_one(qmv_stream_kernel<4, 4, XM, E_ROPE_QKV, 0, true>, pl, 4 * 64, st, q);
+}
+
 static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 // Shared validation + dispatch for every qmm entry point.
@@ -877,7 +903,7 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
     set_error("%s: group_size %d unsupported (64 or 128)", who, p.gs);
     return MTP_ERR_UNSUPPORTED;
   }
-  if (!p.x || !p.w0 || (!p.packed && (!p.s0 || !p.b0)) || (!p.y0 && !p.yf)) {
+  if (!p.x || !p.w0 || (!p.packed && (!p.s0 || !p.b0)) || (!p.y0 && !p.yf && em != E_ROPE_QKV)) {
     set_error("%s: null pointer argument", who);
     return MTP_ERR_ARG;
   }
@@ -910,6 +936,30 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
     set_error("%s: ldy=%d < N=%d", who, p.ldy, p.N);
     return MTP_ERR_ARG;
   }
+  if (em == E_ROPE_QKV) {
+    const int D = p.rope_D;
+    if (!p.packed || p.M > 8 || (xm != X_PLAIN && xm != X_RMSNORM) || !p.q_start || !p.q_out || !p.k_cache ||
+        !p.v_cache || D < 32 || D % 32 || p.rope_L < 1 || p.M % p.rope_L || p.rope_Hq < 1 || p.rope_Hkv < 1 ||
+        p.N != (p.rope_Hq + 2 * p.rope_Hkv) * D || p.rope_cap < 1 || !(p.rope_log2_base > 0.f) ||
+        (p.rope_blocked && (p.rope_cap % 32 || D != 128))) {
+      set_error("%s: RoPE epilogue needs packed weights in RoPE tile order, M<=8 (a multiple of L), plain or "
+                "RMSNorm x, N=(Hq+2Hkv)*D with D%%32==0, base>1, non-null q_start/q_out/caches "
+                "(blocked caches: D=128, cap%%32==0)", who);
+      return MTP_ERR_ARG;
+    }
+    Plan pl = make_plan(p.M, p.N, p.K);
+    if (!pl.resident) {
+      set_error("%s: packed weights need all of x in LDS (M=%d, K=%d too large)", who, p.M, p.K);
+      return MTP_ERR_UNSUPPORTED;
+    }
+    p.chunk = pl.chunk;
+    p.n_blocks = pl.n_blocks;
+    if (xm == X_RMSNORM)
+      launch_rope<X_RMSNORM>(p, pl, st);
+    else
+      launch_rope<X_PLAIN>(p, pl, st);
+    return launch_check(who);
+  }
   if (p.packed && ws) {
     // Stream-K over all CUs when the caller gave it a workspace; shapes whose
     // staged x does not fit its LDS plan use the per-tile kernel below.
@@ -921,7 +971,7 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
       return rc;
     }
   }
-  Plan pl = make_plan(p.M, p.N, p.K, xm == X_RMSNORM);
+  Plan pl = make_plan(p.M, p.N, p.K);
   if (p.packed && !pl.resident) {
     set_error("%s: packed weights need all of x in LDS (M=%d, K=%d too large); use the unpacked layout", who,
               p.M, p.K);
@@ -1237,6 +1287,17 @@ MTP_API int mtp_pack_affine4(const void* w, const void* scales, const void* bias
   return launch_check("mtp_pack_affine4");
 }
 
+struct mtp_rope_out {
+  const int32_t* q_start;
+  const int32_t* q_lens;
+  void* q_out;
+  void* k_cache;
+  void* v_cache;
+  int32_t* status;
+  int L, Hq, Hkv, D, cap, blocked;
+  float rope_base;
+};
+
 struct mtp_qmv_args {
   const void* x;
   const void* x2;
@@ -1257,6 +1318,7 @@ struct mtp_qmv_args {
   int xmode, emode, packed;
   void* ws;
   size_t ws_bytes;
+  const mtp_rope_out* rope;
 };
 
 MTP_API int mtp_qmv_affine4_ex(const mtp_qmv_args* a, void* stream) {
@@ -1264,7 +1326,7 @@ MTP_API int mtp_qmv_affine4_ex(const mtp_qmv_args* a, void* stream) {
     set_error("mtp_qmv_affine4_ex: null argument block");
     return MTP_ERR_ARG;
   }
-  if (a->xmode < 0 || a->xmode > 2 || a->emode < 0 || a->emode > 3) {
+  if (a->xmode < 0 || a->xmode > 2 || a->emode < 0 || a->emode > 4 || (a->emode == E_ROPE_QKV && !a->rope)) {
     set_error("mtp_qmv_affine4_ex: xmode %d / emode %d out of range", a->xmode, a->emode);
     return MTP_ERR_ARG;
   }
@@ -1283,5 +1345,21 @@ MTP_API int mtp_qmv_affine4_ex(const mtp_qmv_args* a, void* stream) {
   p.packed = a->packed;
   if (a->ldx > 0) p.ldx = a->ldx;
   if (a->ldy > 0) p.ldy = a->ldy;
+  if (a->emode == E_ROPE_QKV) {
+    const mtp_rope_out* r = a->rope;
+    p.q_start = r->q_start;
+    p.q_lens = r->q_lens;
+    p.q_out = (uint16_t*)r->q_out;
+    p.k_cache = (uint16_t*)r->k_cache;
+    p.v_cache = (uint16_t*)r->v_cache;
+    p.status = r->status;
+    p.rope_L = r->L;
+    p.rope_Hq = r->Hq;
+    p.rope_Hkv = r->Hkv;
+    p.rope_D = r->D;
+    p.rope_cap = r->cap;
+    p.rope_blocked = r->blocked;
+    p.rope_log2_base = r->rope_base > 1.f ? log2f(r->rope_base) : 0.f;
+  }
   return qmm_dispatch(a->xmode, a->emode, p, a->ws, a->ws_bytes, (hipStream_t)stream, "mtp_qmv_affine4_ex");
 }

@@ -8,7 +8,7 @@
 namespace mtp {
 
 enum XMode { X_PLAIN = 0, X_SWIGLU = 1, X_RMSNORM = 2 };
-enum EMode { E_STORE = 0, E_RESID = 1, E_DUAL = 2, E_DUAL_SWIGLU = 3 };
+enum EMode { E_STORE = 0, E_RESID = 1, E_DUAL = 2, E_DUAL_SWIGLU = 3, E_ROPE_QKV = 4 };
 
 struct QmmParams {
   const uint16_t* x;       // activations [rows, ldx] (X_SWIGLU: gate)
@@ -40,6 +40,16 @@ struct QmmParams {
   int S, gps, n_blocks, nvirt, chunk;
   int packed;              // w0/w1 in the tile-major layout (scales/biases inside)
   float eps;
+  // E_ROPE_QKV: the q|k|v rows go through RoPE straight to q_out [B, Hq, L, D]
+  // and the K/V cache; row r is request r / rope_L, position q_start + r % rope_L.
+  const int32_t* q_start;
+  const int32_t* q_lens;
+  uint16_t* q_out;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int32_t* status;
+  int rope_L, rope_Hq, rope_Hkv, rope_D, rope_cap, rope_blocked;
+  float rope_log2_base;
 };
 
 constexpr int kThreads = 256;
@@ -135,9 +145,13 @@ __device__ __forceinline__ uint4 produce_chunk(uint4 raw, uint4 raw2, float inv_
       o.w = f2bf2(v[3], v[7]);
     }
   }
-  const uint32_t ov[4] = {o.x, o.y, o.z, o.w};
-#pragma unroll
-  for (int t = 0; t < 4; ++t) sum += __uint_as_float(ov[t] << 16) + __uint_as_float(ov[t] & 0xffff0000u);
+  // Sum of the 8 bf16 values: one bf16 dot product with (1, 1) per pair.
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t one2 = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
+  sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, o.x), one2, sum, false);
+  sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, o.y), one2, sum, false);
+  sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, o.z), one2, sum, false);
+  sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, o.w), one2, sum, false);
   return o;
 }
 
@@ -159,11 +173,11 @@ typedef __attribute__((address_space(3))) void* lptr_t;
 
 // Staging, phase 1: direct-to-LDS loads (no registers) of the raw x chunks of
 // the k-quads kq0, kq0+1, ... (mod Q), nslot of them, into their staged
-// positions; X_RMSNORM also copies the norm weights [K] to ``nwt``. One wave
-// instruction fills 64 consecutive chunks (1 KB) of one staged row.
-template <int XM, int NW>
-__device__ __forceinline__ void stage_x_issue(const QmmParams& p, uint4* xa, int rstride, uint16_t* nwt, int M, int Q,
-                                              int kq0, int nslot, int wave, int lane) {
+// positions. One wave instruction fills 64 consecutive chunks (1 KB) of one
+// staged row.
+template <int NW>
+__device__ __forceinline__ void stage_x_issue(const QmmParams& p, uint4* xa, int rstride, int M, int Q, int kq0,
+                                              int nslot, int wave, int lane) {
   const int rowchunks = 16 * nslot;
   const int nblk = (rowchunks + 63) >> 6;
   const int ntask = 2 * M * nblk;
@@ -182,54 +196,101 @@ __device__ __forceinline__ void stage_x_issue(const QmmParams& p, uint4* xa, int
                                        (lptr_t)(xa + (size_t)row * rstride + blk * 64), 16, 0, 0);
     }
   }
-  if (XM == X_RMSNORM) {
-    const int nch = p.K >> 3;
-    for (int b = wave; b * 64 < nch; b += NW) {
-      const int c = b * 64 + lane;
-      if (c < nch) __builtin_amdgcn_global_load_lds((gptr_t)(p.x2 + 8 * c), (lptr_t)(nwt + b * 512), 16, 0, 0);
-    }
+}
+
+// X_RMSNORM staging works on items (staged 64-group gl, chunk cc), item it =
+// 8 gl + cc, thread tid taking it = tid + j * NT. The norm-weight chunks of a
+// thread's first kNormPre items are loaded into registers with the x loads;
+// later items (K > 8 * kNormPre * NT) load theirs when used.
+constexpr int kNormPre = 3;
+__device__ __forceinline__ int norm_item_k(int it, int Q, int kq0) {
+  const int gl = it >> 3;
+  int qd = kq0 + (gl >> 2);
+  if (qd >= Q) qd -= Q;
+  return 64 * (4 * qd + (gl & 3)) + 8 * (it & 7);
+}
+template <int NW>
+__device__ __forceinline__ void norm_w_prefetch(const QmmParams& p, uint4 (&wpre)[kNormPre], int Q, int kq0,
+                                                int nslot, int tid) {
+  const int nit = 32 * nslot;
+#pragma unroll
+  for (int j = 0; j < kNormPre; ++j) {
+    const int it = tid + j * NW * 64;
+    wpre[j] = make_uint4(0, 0, 0, 0);
+    if (it < nit) wpre[j] = *reinterpret_cast<const uint4*>(p.x2 + norm_item_k(it, Q, kq0));
   }
 }
 
 // Staging, phase 2 (after the loads have landed and a barrier): the fused
 // producer, the A-operand element order and the per-group sums, in place.
-// One thread owns one (row, 64-group): its 8 chunks are independent LDS reads
-// and its sum needs no cross-lane step. X_SWIGLU reads its up half from
-// global memory.
+// X_RMSNORM: one thread per (64-group, chunk) for all rows, so each norm
+// weight chunk is loaded and unpacked once; the 8 threads of a group are 8
+// consecutive lanes and add their row sums by DPP. Other modes: one thread
+// per (row, 64-group), whose 8 chunks are independent LDS reads and whose sum
+// needs no cross-lane step; X_SWIGLU reads its up half from global memory.
 template <int XM, int NW, int XSW, bool NAT>
 __device__ __forceinline__ void stage_x_finish(const QmmParams& p, uint4* xa, int rstride, float* xs,
-                                               const uint16_t* nwt, const float* inv_rms, int M, int Q, int kq0,
-                                               int nslot, int tid) {
+                                               const uint4 (&wpre)[kNormPre], const float* inv_rms, int M, int Q,
+                                               int kq0, int nslot, int tid) {
   constexpr int NT = NW * 64;
   const int ng = 4 * nslot;   // staged groups
-  for (int it = tid; it < M * ng; it += NT) {
-    const int m = it / ng;
-    const int gl = it - m * ng;
-    int qd = kq0 + (gl >> 2);
-    if (qd >= Q) qd -= Q;
-    const int kb = 64 * (4 * qd + (gl & 3));
-    const float inv = (XM == X_RMSNORM) ? inv_rms[m] : 1.f;
-    float sum = 0.f;
-    constexpr int B = (XM == X_PLAIN) ? 4 : 2;   // chunks read ahead (register budget)
+  if (XM == X_RMSNORM) {
+    const int nit = ng * 8;   // a multiple of 32: whole groups are in or out
+    auto item = [&](int it, const uint4& wch) {
+      const int gl = it >> 3, cc = it & 7;
+      for (int m0 = 0; m0 < M; m0 += 4) {
+        uint4 c[4];
 #pragma unroll
-    for (int cb = 0; cb < 8; cb += B) {   // chunk cc = 4 kq + ii covers k = kb + 8 cc
-      uint4 c[B], aux[B];
+        for (int u = 0; u < 4; ++u)
+          if (m0 + u < M) c[u] = xa[xa_index(cc >> 2, m0 + u, M, rstride, gl, cc & 3)];
 #pragma unroll
-      for (int u = 0; u < B; ++u) {
-        const int cc = cb + u;
-        c[u] = xa[xa_index(cc >> 2, m, M, rstride, gl, cc & 3)];
-        aux[u] = make_uint4(0, 0, 0, 0);
-        if (XM == X_RMSNORM) aux[u] = *reinterpret_cast<const uint4*>(nwt + kb + 8 * cc);
-        if (XM == X_SWIGLU) aux[u] = *reinterpret_cast<const uint4*>(p.x2 + (size_t)m * p.ldx + kb + 8 * cc);
+        for (int u = 0; u < 4; ++u) {
+          if (m0 + u < M) {
+            float sum = 0.f;
+            xa[xa_index(cc >> 2, m0 + u, M, rstride, gl, cc & 3)] =
+                produce_chunk<XM, NAT>(c[u], wch, inv_rms[m0 + u], sum);
+            sum = sum8_lanes(sum);
+            if (cc == 0) xs[gl * XSW + m0 + u] = sum;
+          }
+        }
       }
+    };
+    // Trip counts are wave-uniform (base is a multiple of 64).
 #pragma unroll
-      for (int u = 0; u < B; ++u) {
-        const int cc = cb + u;
-        const uint4 o = produce_chunk<XM, NAT>(c[u], aux[u], inv, sum);
-        if (!(XM == X_PLAIN && NAT)) xa[xa_index(cc >> 2, m, M, rstride, gl, cc & 3)] = o;
-      }
+    for (int j = 0; j < kNormPre; ++j) {
+      const int it = tid + j * NT;
+      if ((it & ~63) < nit && it < nit) item(it, wpre[j]);
     }
-    xs[gl * XSW + m] = sum;
+    for (int it = tid + kNormPre * NT; (it & ~63) < nit; it += NT)
+      if (it < nit) item(it, *reinterpret_cast<const uint4*>(p.x2 + norm_item_k(it, Q, kq0)));
+  } else {
+    for (int it = tid; it < M * ng; it += NT) {
+      const int m = it / ng;
+      const int gl = it - m * ng;
+      int qd = kq0 + (gl >> 2);
+      if (qd >= Q) qd -= Q;
+      const int kb = 64 * (4 * qd + (gl & 3));
+      float sum = 0.f;
+      constexpr int B = (XM == X_PLAIN) ? 4 : 2;   // chunks read ahead (register budget)
+#pragma unroll
+      for (int cb = 0; cb < 8; cb += B) {   // chunk cc = 4 kq + ii covers k = kb + 8 cc
+        uint4 c[B], aux[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          const int cc = cb + u;
+          c[u] = xa[xa_index(cc >> 2, m, M, rstride, gl, cc & 3)];
+          aux[u] = make_uint4(0, 0, 0, 0);
+          if (XM == X_SWIGLU) aux[u] = *reinterpret_cast<const uint4*>(p.x2 + (size_t)m * p.ldx + kb + 8 * cc);
+        }
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          const int cc = cb + u;
+          const uint4 o = produce_chunk<XM, NAT>(c[u], aux[u], 1.f, sum);
+          if (!(XM == X_PLAIN && NAT)) xa[xa_index(cc >> 2, m, M, rstride, gl, cc & 3)] = o;
+        }
+      }
+      xs[gl * XSW + m] = sum;
+    }
   }
   for (int idx = tid; idx < nslot * 4 * XSW; idx += NT)
     if ((idx % XSW) >= M) xs[idx] = 0.f;
@@ -355,13 +416,74 @@ __device__ __forceinline__ size_t x_row(const QmmParams& p, int row0, int m) {
   return (size_t)(p.rowmap ? (int)p.rowmap[r] : r) * p.ldx;
 }
 
+// E_ROPE_QKV per-thread state of one epilogue element (row, pair): its
+// position, the request's row count and the rotation.
+struct RopeRow {
+  int b, li, pos, len;
+  float sn, cs;
+};
+// From the request's first position and row count (q_start[b], q_lens[b]).
+__device__ __forceinline__ RopeRow rope_row(const QmmParams& p, int r, int d, int start, int len) {
+  RopeRow q;
+  q.b = r / p.rope_L;
+  q.li = r - q.b * p.rope_L;
+  q.pos = start + q.li;
+  q.len = len;
+  rope_angle(q.pos, d, p.rope_D, p.rope_log2_base, q.sn, q.cs);
+  return q;
+}
+__device__ __forceinline__ RopeRow rope_row(const QmmParams& p, int r, int d) {
+  const int b = r / p.rope_L;
+  return rope_row(p, r, d, p.q_start[b], p.q_lens ? p.q_lens[b] : p.rope_L);
+}
+
 // ``pre``: this thread's residual value for its first output element, loaded
-// at kernel start (E_RESID with M*32 <= threads), or null.
+// at kernel start (E_RESID with M*32 <= threads), or null. ``rpre``: the same
+// for E_ROPE_QKV (position and rotation of element idx == tid), or null.
 template <int NW, int EM>
 __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int nb, int M, int row0,
-                                             const float* pre = nullptr) {
+                                             const float* pre = nullptr, const RopeRow* rpre = nullptr) {
   constexpr int NT = NW * 64;
   const int tid = threadIdx.x;
+  if (EM == E_ROPE_QKV) {
+    // Packed column order: tile nb is head nb / (D/32), sub-block sb; local
+    // column c < 16 holds d = 16 sb + c, c >= 16 holds d + D/2, so every
+    // rotate-half pair sits in one tile. Values are rounded to bf16 first,
+    // exactly as a stored q|k|v row would be.
+    const int D = p.rope_D, half = D >> 1;
+    const int head = nb / (D >> 5);
+    const int d = 16 * (nb - head * (D >> 5));
+    for (int idx = tid; idx < M * 16; idx += NT) {
+      const int m = idx >> 4, i = idx & 15;
+      const RopeRow rr = (rpre && idx == tid) ? *rpre : rope_row(p, row0 + m, d + i);
+      const int b = rr.b, li = rr.li, pos = rr.pos, len = rr.len;
+      const float x1 = round_bf(fin[m * 64 + i]), x2 = round_bf(fin[m * 64 + 16 + i]);
+      uint16_t o1 = f2bf(x1), o2 = f2bf(x2);
+      const bool kv = head >= p.rope_Hq;
+      if (head < p.rope_Hq + p.rope_Hkv) rope_apply(x1, x2, rr.sn, rr.cs, o1, o2);
+      if (!kv) {
+        uint16_t* dst = p.q_out + (((size_t)b * p.rope_Hq + head) * p.rope_L + li) * D;
+        dst[d + i] = o1;
+        dst[d + i + half] = o2;
+      } else if (li < len) {
+        if (pos < 0 || pos >= p.rope_cap) {
+          if (p.status) atomicOr(p.status, 1);
+          continue;
+        }
+        const bool is_k = head < p.rope_Hq + p.rope_Hkv;
+        const int kvh = head - p.rope_Hq - (is_k ? 0 : p.rope_Hkv);
+        uint16_t* base = (is_k ? p.k_cache : p.v_cache) + ((size_t)b * p.rope_Hkv + kvh) * p.rope_cap * D;
+        if (p.rope_blocked) {
+          base[is_k ? kblk_index(pos, d + i) : vblk_index(pos, d + i)] = o1;
+          base[is_k ? kblk_index(pos, d + i + half) : vblk_index(pos, d + i + half)] = o2;
+        } else {
+          base[(size_t)pos * D + d + i] = o1;
+          base[(size_t)pos * D + d + i + half] = o2;
+        }
+      }
+    }
+    return;
+  }
   for (int idx = tid; idx < M * 32; idx += NT) {
     const int m = idx >> 5;
     const int c = idx & 31;

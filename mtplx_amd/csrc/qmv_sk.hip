@@ -80,7 +80,6 @@ __global__ __launch_bounds__(NW * 64) void qmv_sk_kernel(QmmParams p) {
   float* xs = reinterpret_cast<float*>(smem + xa_bytes(4 * nslot, M));          // [nslot*4][XSW]
   float* red = xs + nslot * 4 * XSW;                                            // [nseg][NW][NMAT][M][32]
   float* fin = red + p.chunk * NW * NMAT * M * 32;                              // [M][64]
-  uint16_t* nwt = reinterpret_cast<uint16_t*>(fin + M * 64);                    // X_RMSNORM: norm weight [K]
   __shared__ float s_inv_rms[32];
   __shared__ int s_last;
 
@@ -149,7 +148,9 @@ __global__ __launch_bounds__(NW * 64) void qmv_sk_kernel(QmmParams p) {
   // everything but the ring loads, so staging overlaps their round trip.
   float ssv[kMaxSsLoads];
   if (XM == X_RMSNORM && p.ss_in && wave < M) ss_prefetch(p, wave, lane, ssv);
-  stage_x_issue<XM, NW>(p, xa, rstride, nwt, M, Q, kq0, nslot, wave, lane);
+  stage_x_issue<NW>(p, xa, rstride, M, Q, kq0, nslot, wave, lane);
+  uint4 wpre[kNormPre];
+  if (XM == X_RMSNORM) norm_w_prefetch<NW>(p, wpre, Q, kq0, nslot, tid);
   asm volatile("" ::: "memory");
   Item A, B, C;
   load_next(A);   // waves without items reload a valid block; never used
@@ -162,7 +163,7 @@ __global__ __launch_bounds__(NW * 64) void qmv_sk_kernel(QmmParams p) {
     if (lane == 0) s_inv_rms[wave] = v;
   }
   __syncthreads();
-  stage_x_finish<XM, NW, XSW, true>(p, xa, rstride, xs, nwt, s_inv_rms, M, Q, kq0, nslot, tid);
+  stage_x_finish<XM, NW, XSW, true>(p, xa, rstride, xs, wpre, s_inv_rms, M, Q, kq0, nslot, tid);
   __syncthreads();
 
   // A operands: lanes of rows >= M repeat row c32 % M (their output rows
@@ -345,7 +346,8 @@ size_t qmv_sk_workspace_bytes(int M, int N, int K, int dual) {
 template <int R, int XM, int EM>
 static void sk_launch_one(const QmmParams& q, int G, size_t lds, hipStream_t st) {
   auto k = qmv_sk_kernel<kSkWaves, R, XM, EM>;
-  if (lds > 65536) hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  // A failure here surfaces as a launch error, which the caller checks.
+  if (lds > 65536) (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   hipLaunchKernelGGL(k, dim3(G), dim3(kSkWaves * 64), lds, st, q);
 }
 
@@ -376,7 +378,7 @@ int qmv_sk_launch(int xm, int em, const QmmParams& p, void* ws, size_t ws_bytes,
   // M keeps the per-tile kernel, whose staged x is shared by fewer items.
   if (p.M > 8 || !p.packed) return MTP_ERR_UNSUPPORTED;
   const int nseg = sk_max_segments(per, Q * (dual ? 2 : 1));
-  const size_t lds = sk_lds_bytes(nslot, nseg, p.M, 4, dual ? 2 : 1) + (xm == X_RMSNORM ? (size_t)p.K * 2 : 0);
+  const size_t lds = sk_lds_bytes(nslot, nseg, p.M, 4, dual ? 2 : 1);
   if (lds > 160 * 1024 - 256) return MTP_ERR_UNSUPPORTED;
   const size_t coff = sk_counter_offset(device_cus());   // G <= CUs
   if (!ws || ws_bytes < coff + (size_t)n_blocks * 4 || ((uintptr_t)ws & 255)) return MTP_ERR_WORKSPACE;

@@ -26,22 +26,32 @@ class QuantizedLinear:
         self.bias = bias
         self.packed: torch.Tensor | None = None
 
-    def pack(self) -> torch.Tensor:
-        """Tile-major copy of the weights for the streaming kernel (made once, cached)."""
-        if self.packed is None:
-            from . import _lib
+    def pack(self, row_order: torch.Tensor | None = None) -> torch.Tensor:
+        """Tile-major copy of the weights for the streaming kernel. Without
+        ``row_order`` it is made once and cached; with it, packed row i is
+        original row ``row_order[i]`` (e.g. :func:`rope_row_order`)."""
+        if row_order is None and self.packed is not None:
+            return self.packed
+        from . import _lib
 
-            if self.weight.dim() != 2 or self.bits != 4 or self.mode != "affine":
-                raise NotImplementedError("packing covers 2-D 4-bit affine layers")
-            n, k = self.out_features, self.in_features
-            nbytes = _lib.query("mtp_pack_affine4_bytes", n, k)
-            if nbytes == 0:
-                raise NotImplementedError(f"cannot pack N={n} K={k} (K must be a multiple of 256)")
-            out = torch.empty(nbytes // 4, dtype=torch.int32, device=self.weight.device)
-            _lib.call("mtp_pack_affine4", self.weight.data_ptr(), self.scales.data_ptr(), self.biases.data_ptr(),
-                      out.data_ptr(), n, k, self.group_size, _lib.stream_handle(self.weight.device))
+        if self.weight.dim() != 2 or self.bits != 4 or self.mode != "affine":
+            raise NotImplementedError("packing covers 2-D 4-bit affine layers")
+        n, k = self.out_features, self.in_features
+        nbytes = _lib.query("mtp_pack_affine4_bytes", n, k)
+        if nbytes == 0:
+            raise NotImplementedError(f"cannot pack N={n} K={k} (K must be a multiple of 256)")
+        w, s, b = self.weight, self.scales, self.biases
+        if row_order is not None:
+            idx = row_order.to(device=w.device, dtype=torch.long)
+            if idx.numel() != n:
+                raise ValueError(f"row_order has {idx.numel()} entries, layer has {n} rows")
+            w, s, b = w[idx].contiguous(), s[idx].contiguous(), b[idx].contiguous()
+        out = torch.empty(nbytes // 4, dtype=torch.int32, device=w.device)
+        _lib.call("mtp_pack_affine4", w.data_ptr(), s.data_ptr(), b.data_ptr(), out.data_ptr(), n, k,
+                  self.group_size, _lib.stream_handle(w.device))
+        if row_order is None:
             self.packed = out
-        return self.packed
+        return out
 
     @property
     def in_features(self) -> int:
@@ -76,3 +86,17 @@ class QuantizedLinear:
         s = (torch.randn(lead + (out_features, g), device=device, generator=generator) * scale_std).abs()
         b = torch.randn(lead + (out_features, g), device=device, generator=generator) * bias_std
         return cls(w, s.to(torch.bfloat16), b.to(torch.bfloat16), group_size=group_size)
+
+
+def rope_row_order(n_heads: int, head_dim: int) -> torch.Tensor:
+    """Row order of a q|k|v projection for the fused RoPE epilogue (emode 4 of
+    ``mtp_qmv_affine4_ex``): packed tile t = head t // (D/32), sub-block
+    sb = t % (D/32); its column c is dimension 16 sb + c % 16 + (c // 16) * D/2,
+    so the rotate-half pairs (d, d + D/2) of a head share one 32-column tile."""
+    if head_dim % 32:
+        raise ValueError("head_dim must be a multiple of 32")
+    tph = head_dim // 32
+    t = torch.arange(n_heads * tph).repeat_interleave(32)
+    c = torch.arange(32).repeat(n_heads * tph)
+    head, sb = t // tph, t % tph
+    return head * head_dim + 16 * sb + c % 16 + (c // 16) * (head_dim // 2)

@@ -8,9 +8,12 @@ This is the forward the reference runs on ``[primary, d1..dK]``
 vocab 151936, every linear 4-bit affine g64, bf16 KV cache) or its MoE variant.
 
 Per layer the kernels are:
-  1. ``mtp_qmv_affine4_rmsnorm_in``  input RMSNorm fused into the q|k|v matmul
-  2. ``mtp_rope_qkv_to_cache``       RoPE at per-request offsets, K/V into the cache
-  3. ``mtp_ragged_gqa_attn_rows``    ragged GQA attention (split-KV + merge)
+  1. ``mtp_qmv_affine4_ex`` emode 4  input RMSNorm fused into the q|k|v matmul,
+                                     whose epilogue applies RoPE at per-request
+                                     offsets and writes K/V into the cache
+                                     (M > 8: the q|k|v matmul, then
+                                     ``mtp_rope_qkv_to_cache_vt``)
+  3. ``mtp_ragged_gqa_attn_rows_vt`` ragged GQA attention (split-KV + merge)
   4. ``mtp_qmv_affine4_residual``    o_proj + residual add
   5. ``mtp_qmv_affine4_rmsnorm_dual`` post-attention RMSNorm + gate/up + SwiGLU
   6. ``mtp_qmv_affine4_residual``    down_proj + residual add
@@ -30,7 +33,7 @@ import torch
 
 from . import _lib
 from .moe_sorted_gather import expert_sort, moe_combine
-from .quant import QuantizedLinear
+from .quant import QuantizedLinear, rope_row_order
 from .sampling import SamplerConfig, spec_accept
 
 
@@ -83,6 +86,7 @@ class Layer:
     shared_gate: QuantizedLinear | None = None
     shared_up: QuantizedLinear | None = None
     shared_down: QuantizedLinear | None = None
+    qkv_rope: torch.Tensor | None = None   # q|k|v packed in RoPE tile order (fused RoPE epilogue)
 
 
 def kv_block_offsets(kind: str) -> list[int]:
@@ -150,11 +154,14 @@ class VerifyModel:
             self.layers.append(L)
         self.final_norm = _norm_weight(c.hidden, gen, device)
         self.lm_head = QuantizedLinear.random(c.vocab, c.hidden, gs, generator=gen, device=device)
-        # Tile-major copies for the streaming verify matmul (one pass at load time).
+        # Tile-major copies for the streaming verify matmul (one pass at load
+        # time); q|k|v also in RoPE tile order for the fused RoPE epilogue.
+        rope_order = rope_row_order(c.n_heads + 2 * c.n_kv_heads, c.head_dim)
         for L in self.layers:
             for q in (L.qkv, L.o, L.gate, L.up, L.down, L.shared_gate, L.shared_up, L.shared_down):
                 if q is not None:
                     q.pack()
+            L.qkv_rope = L.qkv.pack(rope_order)
         self.lm_head.pack()
         self.k_cache: list[torch.Tensor] = []
         self.v_cache: list[torch.Tensor] = []
@@ -236,12 +243,21 @@ class VerifyModel:
         # stream-K variant, whose shared tiles cost a fix-up at the end.
         qmv = _lib.qmv_ex
 
+        fused_rope = M <= 8   # the RoPE epilogue covers up to 8 rows
+
         for li, L in enumerate(self.layers):
-            qmv(st, x=h, x2=L.in_norm, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv.packed, y0=qkv, M=M, N=c.qkv_out, K=H,
-                group_size=gs, xmode=2, emode=0, packed=1)
-            call("mtp_rope_qkv_to_cache_vt", qkv.data_ptr(), q_start.data_ptr(), _lib.ptr(ql), qh.data_ptr(),
-                 self.k_cache[li].data_ptr(), self.v_cache[li].data_ptr(), B, Lq, c.n_heads, c.n_kv_heads,
-                 c.head_dim, self.cap, ctypes.c_float(c.rope_theta), status.data_ptr(), st)
+            if fused_rope:
+                rope = dict(q_start=q_start, q_lens=ql, q_out=qh, k_cache=self.k_cache[li], v_cache=self.v_cache[li],
+                            status=status, L=Lq, Hq=c.n_heads, Hkv=c.n_kv_heads, D=c.head_dim, cap=self.cap,
+                            blocked=1, rope_base=c.rope_theta)
+                qmv(st, rope=rope, x=h, x2=L.in_norm, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv_rope, M=M,
+                    N=c.qkv_out, K=H, group_size=gs, xmode=2, emode=4, packed=1)
+            else:
+                qmv(st, x=h, x2=L.in_norm, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv.packed, y0=qkv, M=M, N=c.qkv_out,
+                    K=H, group_size=gs, xmode=2, emode=0, packed=1)
+                call("mtp_rope_qkv_to_cache_vt", qkv.data_ptr(), q_start.data_ptr(), _lib.ptr(ql), qh.data_ptr(),
+                     self.k_cache[li].data_ptr(), self.v_cache[li].data_ptr(), B, Lq, c.n_heads, c.n_kv_heads,
+                     c.head_dim, self.cap, ctypes.c_float(c.rope_theta), status.data_ptr(), st)
             call("mtp_ragged_gqa_attn_rows_vt", qh.data_ptr(), self.k_cache[li].data_ptr(),
                  self.v_cache[li].data_ptr(), q_start.data_ptr(), _lib.ptr(ql), attn.data_ptr(), B, c.n_heads,
                  c.n_kv_heads, Lq, c.head_dim, self.cap, ctypes.c_float(scale), aws.data_ptr(), aws.numel(), st)
