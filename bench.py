@@ -37,34 +37,46 @@ def _qmv_bytes(M: int, N: int, K: int, gs: int) -> int:
 
 
 def roofline_gate_up(model, M: int, reps: int = 5) -> dict:
-    """Average duration of the fused norm+gate/up launch over every layer's weights."""
+    """Average duration of the fused norm+gate/up launch over every layer's
+    weights: the verify step's own call (packed weights, norm statistics from
+    the residual epilogue, the shared workspace), one launch per layer captured
+    in a HIP graph and replayed, timed with events on the capture stream."""
     import torch
 
     from mtplx_amd import _lib
 
     c = model.cfg
     dev = model.device
-    st = _lib.stream_handle(dev)
     x = torch.randn((M, c.hidden), device=dev).to(torch.bfloat16)
+    xf = x.float()
+    ss = torch.zeros(((c.hidden + 31) // 32) * 32, dtype=torch.float32, device=dev)
+    ss.view(-1, 32)[:, :M] = (xf * xf).view(M, -1, 32).sum(dim=2).t()
     y = torch.empty((M, c.ffn), dtype=torch.bfloat16, device=dev)
+    nb = _lib.query("mtp_qmv_workspace_bytes", M, c.ffn, c.hidden, 1)
+    ws = _lib.WORKSPACES.get(nb, "qmv", dev)
 
-    def launch(L):   # the same call the verify step makes (tile-major packed weights)
-        _lib.qmv_ex(st, x=x, x2=L.post_norm, eps=c.rms_eps, w0=L.gate.packed, w1=L.up.packed, y0=y, M=M, N=c.ffn,
-                    K=c.hidden, group_size=c.group_size, xmode=2, emode=3, packed=1)
+    def launch(L):
+        _lib.qmv_ex(_lib.stream_handle(dev), x=x, x2=L.post_norm, ss_in=ss, eps=c.rms_eps, w0=L.gate.packed,
+                    w1=L.up.packed, y0=y, M=M, N=c.ffn, K=c.hidden, group_size=c.group_size, xmode=2, emode=3,
+                    packed=1, ws=ws, ws_bytes=ws.numel())
 
     for L in model.layers:
         launch(L)
     torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for L in model.layers:
+            launch(L)
+    graph.replay()
+    torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
-    n = 0
     for _ in range(reps):
-        for L in model.layers:
-            launch(L)
-            n += 1
+        graph.replay()
     e1.record()
     torch.cuda.synchronize()
+    n = reps * len(model.layers)
     us = e0.elapsed_time(e1) * 1000.0 / n
     byts = _gate_up_bytes(M, c.ffn, c.hidden, c.group_size)
     gbs = byts / us / 1e3

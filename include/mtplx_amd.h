@@ -111,9 +111,12 @@ int mtp_pack_affine4(const void* w, const void* scales, const void* biases, void
  * ldx/ldy <= 0 mean K/N.
  * ws/ws_bytes: with packed weights, a workspace of mtp_qmv_workspace_bytes
  * (256-byte aligned, zeroed once before first use and then left to the
- * library) selects the stream-K kernel, which spreads (tile, 256-k) items
- * evenly over all CUs; calls sharing one workspace must be stream-ordered.
- * Without it the per-tile kernel runs.
+ * library; calls sharing one workspace must be stream-ordered). schedule 0:
+ * the per-tile kernel, which with a workspace splits the leftover tiles of
+ * its last round by K over all CUs (tiles mod CUs must divide the CU count;
+ * the parts are summed in a fixed order); schedule 1: the stream-K kernel,
+ * which spreads (tile, 256-k) items evenly over all CUs. Without a
+ * workspace the per-tile kernel runs unsplit.
  * emode 4 = q|k|v projection with RoPE and the cache write fused into the
  * epilogue (the work of mtp_rope_qkv_to_cache / _vt below, same rounding):
  * rope points at the outputs; y0 is unused; packed weights whose rows are in
@@ -151,6 +154,7 @@ typedef struct mtp_qmv_args {
   void* ws;
   size_t ws_bytes;
   const mtp_rope_out* rope; /* emode 4 only */
+  int schedule;             /* 0 = per-tile, 1 = stream-K (see ws above) */
 } mtp_qmv_args;
 int mtp_qmv_affine4_ex(const mtp_qmv_args* args, void* stream);
 

@@ -74,7 +74,7 @@ class QmvArgs(C.Structure):
     _fields_ = [(n, _vp) for n in ("x", "x2", "ss_in", "w0", "s0", "b0", "w1", "s1", "b1", "y0", "y1", "yf",
                                    "resid", "ss_out")] + [("eps", _f)] + \
                [(n, _i) for n in ("M", "N", "K", "group_size", "ldx", "ldy", "xmode", "emode", "packed")] + \
-               [("ws", _vp), ("ws_bytes", C.c_size_t), ("rope", C.POINTER(RopeOut))]
+               [("ws", _vp), ("ws_bytes", C.c_size_t), ("rope", C.POINTER(RopeOut)), ("schedule", _i)]
 
 
 def _fill(struct, fields: dict):

@@ -523,6 +523,18 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   const int Q = p.K >> 8;
   const int G = gridDim.x;
   const NibConsts nc = nib_consts();
+  // Tail split (packed weights only): workgroups from p.tail_first on each
+  // take quads [q_lo, q_lo + q_n) of a leftover tile, one of tail_split
+  // parts; the part that arrives last sums the parts in order and finishes.
+  const bool tail = PK && p.tail_split > 1 && (int)blockIdx.x >= p.tail_first;
+  int tile0 = (int)blockIdx.x, part = 0, q_lo = 0, q_n = Q;
+  if (tail) {
+    const int e = (int)blockIdx.x - p.tail_first;
+    tile0 = p.tail_first + e / p.tail_split;
+    part = e - (e / p.tail_split) * p.tail_split;
+    q_lo = (part * Q) / p.tail_split;
+    q_n = ((part + 1) * Q) / p.tail_split - q_lo;
+  }
 
   uint4* xa = reinterpret_cast<uint4*>(smem);                                  // staged x, xa_index()
   const int rstride = xa_row_stride(4 * Q);
@@ -530,6 +542,7 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   float* red = xs + Q * 4 * XSW;                                               // [NW][M][32]
   float* fin = red + NW * M * 32;                                              // [M][64]
   __shared__ float s_inv_rms[32];
+  __shared__ int s_last;
 
   const int c32 = lane & 31;
   const int kq = lane >> 5;
@@ -537,8 +550,8 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   const uint16_t* Sc = which ? p.s1 : p.s0;
   const uint16_t* Bi = which ? p.b1 : p.b0;
   const int sgroups = p.K >> (6 + GSH);
-  const int qw = (Q > kw) ? cdiv(Q - kw, KS) : 0;
-  const int ntiles = cdiv(p.n_blocks - (int)blockIdx.x, G);
+  const int qw = (q_n > kw) ? cdiv(q_n - kw, KS) : 0;
+  const int ntiles = (PK && p.tail_split > 1) ? 1 : cdiv(p.n_blocks - (int)blockIdx.x, G);
   const int nitems = ntiles * qw;
 
   // A operands: lanes of rows >= M repeat row c32 % M (their output rows
@@ -557,7 +570,7 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   const uint16_t* srow = nullptr;
   const uint16_t* brow = nullptr;
   auto set_rows = [&](int j) {
-    const int nb = (int)blockIdx.x + j * G;
+    const int nb = tile0 + j * G;
     if (PK) {
       // Tile-major packed weights: per (tile, quad) 1152 words — 4 x 256
       // words of nibbles in load order, then 32 rows x (4 s, 4 b) bf16.
@@ -578,7 +591,7 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   // keeps re-reading the last item, whose registers are never used).
   auto load_next = [&](QuadRegs& qr) {
     if (PK) {
-      const size_t qoff = (size_t)(qw > 0 ? kw + KS * t_pf : 0) * kPackQuadWords;
+      const size_t qoff = (size_t)(q_lo + (qw > 0 ? kw + KS * t_pf : 0)) * kPackQuadWords;
       const uint32_t* wp = wrow + qoff;
 #pragma unroll
       for (int u = 0; u < 4; ++u) qr.w[u] = *reinterpret_cast<const uint4*>(wp + 256 * u);
@@ -626,7 +639,7 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   float pre_resid = 0.f;
   const bool use_pre = (EM == E_RESID) && (R == 4) && ntiles > 0;
   if (use_pre && tid < M * 32) {
-    const int col = (int)blockIdx.x * 32 + (tid & 31);
+    const int col = tile0 * 32 + (tid & 31);
     if (col < p.N) pre_resid = bf2f(p.resid[(size_t)(tid >> 5) * p.ldy + col]);
   }
   // E_ROPE_QKV: the request offsets of this thread's first epilogue element
@@ -642,7 +655,7 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
 
   // End of tile j: reduce the K-split waves in LDS (wave order), epilogue.
   auto finish = [&](int j) {
-    const int nb = (int)blockIdx.x + j * G;
+    const int nb = tile0 + j * G;
     const bool valid = nb * 32 + c32 < p.N;
     __syncthreads();
 #pragma unroll
@@ -667,6 +680,35 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
       fin[idx] = v;
     }
     __syncthreads();
+    if (tail) {
+      // This part's sums to the workspace (device-coherent stores), then
+      // arrive; the last arrival adds the parts in part order and finishes.
+      const int e = (int)blockIdx.x - p.tail_first;
+      for (int idx = tid; idx < M * 64; idx += NT)
+        __hip_atomic_store(p.partial + (size_t)e * (M * 64) + idx, fin[idx], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      const int ti = tile0 - p.tail_first;
+      if (tid == 0) {
+        const unsigned old =
+            __hip_atomic_fetch_add(p.counters + ti, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (old == (unsigned)(p.tail_split - 1)) ? 1 : 0;
+      }
+      __syncthreads();
+      if (!s_last) return;
+      const float* p0 = p.partial + (size_t)ti * p.tail_split * (M * 64);
+      for (int idx = tid; idx < M * 64; idx += NT) {
+        float v = 0.f;
+        for (int q = 0; q < p.tail_split; ++q)
+          v += __hip_atomic_load(p0 + (size_t)q * (M * 64) + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        fin[idx] = v;
+      }
+      __syncthreads();
+      qmm_epilogue<NW, EM>(p, fin, nb, M, 0);
+      if (tid == 0) __hip_atomic_store(p.counters + ti, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
     qmm_epilogue<NW, EM>(p, fin, nb, M, 0, (use_pre && j == 0) ? &pre_resid : nullptr,
                          (use_rpre && j == 0) ? &rope_pre : nullptr);
   };
@@ -677,9 +719,9 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   // so staging x overlaps the weights' first round trip.
   float ssv[kMaxSsLoads];
   if (XM == X_RMSNORM && p.ss_in && wave < M) ss_prefetch(p, wave, lane, ssv);
-  stage_x_issue<NW>(p, xa, rstride, M, Q, 0, Q, wave, lane);
+  stage_x_issue<NW>(p, xa, rstride, M, Q, q_lo, q_n, wave, lane);
   uint4 wpre[kNormPre];
-  if (XM == X_RMSNORM) norm_w_prefetch<NW>(p, wpre, Q, 0, Q, tid);
+  if (XM == X_RMSNORM) norm_w_prefetch<NW>(p, wpre, Q, q_lo, q_n, tid);
   asm volatile("" ::: "memory");
   QuadRegs ring[NR];
 #pragma unroll
@@ -693,11 +735,11 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
     }
   }
   __syncthreads();
-  stage_x_finish<XM, NW, XSW, PK>(p, xa, rstride, xs, wpre, s_inv_rms, M, Q, 0, Q, tid);
+  stage_x_finish<XM, NW, XSW, PK>(p, xa, rstride, xs, wpre, s_inv_rms, M, Q, q_lo, q_n, tid);
   __syncthreads();  // staged x visible to every wave
   if (use_rpre) {
-    const int head = (int)blockIdx.x / (p.rope_D >> 5);
-    const int d = 16 * ((int)blockIdx.x - head * (p.rope_D >> 5)) + (tid & 15);
+    const int head = tile0 / (p.rope_D >> 5);
+    const int d = 16 * (tile0 - head * (p.rope_D >> 5)) + (tid & 15);
     rope_pre = rope_row(p, tid >> 4, d, rq_start, rq_len);
   }
 
@@ -828,8 +870,37 @@ static void launch_one(K k, const Plan& pl, int nt, hipStream_t st, const QmmPar
   hipLaunchKernelGGL(k, dim3(stream_grid(k, nt, pl.lds, pl.n_blocks)), dim3(nt), pl.lds, st, q);
 }
 
+// Tail split of the per-tile kernel: when T tiles leave E = T mod CUs
+// leftover tiles and E divides the CU count, the T - E full tiles run as
+// usual and every leftover tile is split by K into S = CUs / E parts, so the
+// last round puts exactly one part on every CU instead of a whole tile on E
+// of them. All T - E + CUs workgroups must be resident at once.
+template <typename K>
+static bool tail_launch(K kernel, const Plan& pl, int nt, hipStream_t st, QmmParams q) {
+  const int cus = device_cus();
+  const int T = pl.n_blocks;
+  const int Q = q.K >> 8;
+  if (T <= cus) return false;
+  const int E = T % cus;
+  if (E == 0 || cus % E) return false;
+  const int S = cus / E;
+  if (S < 2 || S > Q) return false;
+  if (pl.lds > 65536) (void)hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                (int)pl.lds);
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, nt, pl.lds) != hipSuccess) return false;
+  const int grid = T - E + cus;
+  if (grid > occ * cus) return false;
+  q.tail_first = T - E;
+  q.tail_split = S;
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(nt), pl.lds, st, q);
+  return true;
+}
+
 template <int NW, int R, int XM, int EM, int GSH>
 static void launch_rk(const QmmParams& q, const Plan& pl, hipStream_t st) {
+  if (q.packed && R == 4 && q.tail_ok && tail_launch(qmv_stream_kernel<NW, R, XM, EM, 0, true>, pl, NW * 64, st, q))
+    return;
   if (q.packed)
     launch_one(qmv_stream_kernel<NW, R, XM, EM, 0, true>, pl, NW * 64, st, q);
   else if (pl.resident)
@@ -890,7 +961,7 @@ static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 // Shared validation + dispatch for every qmm entry point.
 static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, hipStream_t st,
-                        const char* who) {
+                        const char* who, int schedule = 0) {
   if (p.M < 1 || p.M > 32 || p.N < 1 || p.K < 256) {
     set_error("%s: need 1<=M<=32, N>=1, K>=256 (got M=%d N=%d K=%d)", who, p.M, p.N, p.K);
     return MTP_ERR_ARG;
@@ -961,14 +1032,22 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
     return launch_check(who);
   }
   if (p.packed && ws) {
-    // Stream-K over all CUs when the caller gave it a workspace; shapes whose
-    // staged x does not fit its LDS plan use the per-tile kernel below.
-    const int rc = qmv_sk_launch(xm, em, p, ws, ws_bytes, st);
-    if (rc == MTP_OK) return launch_check(who);
-    if (rc == MTP_ERR_WORKSPACE) {
-      set_error("%s: workspace of %zu B (256-B aligned) needed, got %zu B", who,
-                qmv_sk_workspace_bytes(p.M, p.N, p.K, em >= E_DUAL), ws_bytes);
-      return rc;
+    const size_t need = qmv_sk_workspace_bytes(p.M, p.N, p.K, em >= E_DUAL);
+    if (ws_bytes < need || ((uintptr_t)ws & 255)) {
+      set_error("%s: workspace of %zu B (256-B aligned) needed, got %zu B", who, need, ws_bytes);
+      return MTP_ERR_WORKSPACE;
+    }
+    if (schedule == 1) {
+      // Stream-K over all CUs; shapes whose staged x does not fit its LDS
+      // plan use the per-tile kernel below.
+      const int rc = qmv_sk_launch(xm, em, p, ws, ws_bytes, st);
+      if (rc == MTP_OK) return launch_check(who);
+      if (rc != MTP_ERR_UNSUPPORTED) return rc;
+    } else if (em != E_ROPE_QKV) {
+      // Per-tile kernel with its leftover tiles split over all CUs.
+      p.tail_ok = 1;
+      p.partial = reinterpret_cast<float*>(ws);
+      p.counters = reinterpret_cast<uint32_t*>(reinterpret_cast<unsigned char*>(ws) + sk_counter_offset(device_cus()));
     }
   }
   Plan pl = make_plan(p.M, p.N, p.K);
@@ -1319,6 +1398,7 @@ struct mtp_qmv_args {
   void* ws;
   size_t ws_bytes;
   const mtp_rope_out* rope;
+  int schedule;
 };
 
 MTP_API int mtp_qmv_affine4_ex(const mtp_qmv_args* a, void* stream) {
@@ -1361,5 +1441,6 @@ MTP_API int mtp_qmv_affine4_ex(const mtp_qmv_args* a, void* stream) {
     p.rope_blocked = r->blocked;
     p.rope_log2_base = r->rope_base > 1.f ? log2f(r->rope_base) : 0.f;
   }
-  return qmm_dispatch(a->xmode, a->emode, p, a->ws, a->ws_bytes, (hipStream_t)stream, "mtp_qmv_affine4_ex");
+  return qmm_dispatch(a->xmode, a->emode, p, a->ws, a->ws_bytes, (hipStream_t)stream, "mtp_qmv_affine4_ex",
+                      a->schedule);
 }

@@ -39,6 +39,8 @@ struct QmmParams {
   int ldx, ldy;
   int S, gps, n_blocks, nvirt, chunk;
   int packed;              // w0/w1 in the tile-major layout (scales/biases inside)
+  int tail_first, tail_split;   // tail split of the per-tile kernel (tail_split > 1)
+  int tail_ok;                  // a workspace (partial, counters) is available for it
   float eps;
   // E_ROPE_QKV: the q|k|v rows go through RoPE straight to q_out [B, Hq, L, D]
   // and the K/V cache; row r is request r / rope_L, position q_start + r % rope_L.
@@ -529,6 +531,7 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int
 // then uses the per-tile kernel).
 int qmv_sk_launch(int xm, int em, const QmmParams& p, void* ws, size_t ws_bytes, hipStream_t st);
 size_t qmv_sk_workspace_bytes(int M, int N, int K, int dual);
+size_t sk_counter_offset(int G);   // workspace: fp32 partials first, then arrival counters
 int device_cus();
 
 }  // namespace mtp

@@ -49,9 +49,11 @@ int sk_max_segments(int per, int QT) { return (per + QT - 2) / QT + 1; }
 // shapes can share one buffer: fp32 partials [2 G][8 rows][64] first, then
 // one arrival counter per 32-column tile.
 constexpr int kSkMaxRows = 8;
-size_t sk_counter_offset(int G) { return (size_t)2 * G * kSkMaxRows * 64 * sizeof(float); }
 
 }  // namespace
+
+// Shared with the per-tile kernel's tail split (qmv.hip).
+size_t sk_counter_offset(int G) { return (size_t)2 * G * kSkMaxRows * 64 * sizeof(float); }
 
 template <int NW, int R, int XM, int EM>
 __global__ __launch_bounds__(NW * 64) void qmv_sk_kernel(QmmParams p) {

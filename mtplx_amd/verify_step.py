@@ -239,9 +239,13 @@ class VerifyModel:
         aws = _lib.WORKSPACES.get(nb, "attn", dev)
         scale = 1.0 / math.sqrt(c.head_dim)
         ql = None if q_lens is None else q_lens.to(torch.int32).contiguous()
-        # Per-tile streaming kernel (no workspace): at these widths it beats the
-        # stream-K variant, whose shared tiles cost a fix-up at the end.
-        qmv = _lib.qmv_ex
+        # Per-tile streaming kernel with a workspace: its leftover tiles (e.g.
+        # the last 32 of gate/up's 544 on 256 CUs) are split by K over all CUs.
+        qmv_nb = max(_lib.query("mtp_qmv_workspace_bytes", M, n, 1, 1) for n in (c.qkv_out, H, ffn, c.vocab))
+        qws = _lib.WORKSPACES.get(qmv_nb, "qmv", dev)
+
+        def qmv(stream, **kw):
+            _lib.qmv_ex(stream, ws=qws, ws_bytes=qws.numel(), **kw)
 
         fused_rope = M <= 8   # the RoPE epilogue covers up to 8 rows
 

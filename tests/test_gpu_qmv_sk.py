@@ -36,7 +36,7 @@ def _run(q0, q1, x, nw, r, xmode, emode, M, N, K, ws):
               packed=1, y0=y0, resid=r if emode == 1 else None, ss_out=ss if emode == 1 else None,
               w0=q0.pack(), w1=q1.pack() if emode >= 2 else None)
     if ws is not None:
-        kw.update(ws=ws, ws_bytes=ws.numel())
+        kw.update(ws=ws, ws_bytes=ws.numel(), schedule=1)
     _lib.qmv_ex(_stream(), **kw)
     torch.cuda.synchronize()
     return y0, ss
@@ -133,5 +133,5 @@ def test_stream_k_rejects_small_workspace(gpu):
     ws = torch.zeros(256, dtype=torch.uint8, device="cuda")
     with pytest.raises(_lib.MtpError) as e:
         _lib.qmv_ex(_stream(), x=x, w0=q.pack(), y0=y, M=4, N=1024, K=1024, group_size=64, packed=1, ws=ws,
-                    ws_bytes=ws.numel())
+                    ws_bytes=ws.numel(), schedule=1)
     assert e.value.code == -3
