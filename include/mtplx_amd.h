@@ -104,7 +104,9 @@ int mtp_pack_affine4(const void* w, const void* scales, const void* biases, void
                      void* stream);
 
 /* Every verify-matmul variant through one argument block. xmode: 0 = x,
- * 1 = silu(x)*x2 (x2 = up), 2 = rmsnorm(x; norm weight x2, eps, ss_in);
+ * 1 = silu(x)*x2 (x2 = up), 2 = rmsnorm(x; norm weight x2, eps, ss_in),
+ * 3 = x with its per-32-column row sums in x_sums ([K/32][32] fp32, as the
+ * y_sums output below writes them; packed weights only);
  * emode: 0 = store (y0 bf16, or yf fp32 when set), 1 = + resid (ss_out
  * optional), 2 = two outputs (w1 -> y1), 3 = silu(x@W0^T)*(x@W1^T).
  * packed = 1: w0/w1 come from mtp_pack_affine4 (s0/b0/s1/b1 unused).
@@ -155,6 +157,11 @@ typedef struct mtp_qmv_args {
   size_t ws_bytes;
   const mtp_rope_out* rope; /* emode 4 only */
   int schedule;             /* 0 = per-tile, 1 = stream-K (see ws above) */
+  /* xmode 3 input sums; y_sums (emode 0, 1, 3, optional): the per-32-column
+   * row sums of the stored y0 values as [N/32][32] fp32, in column order -
+   * the x_sums of a following xmode 3 call on y0. */
+  const float* x_sums;
+  float* y_sums;
 } mtp_qmv_args;
 int mtp_qmv_affine4_ex(const mtp_qmv_args* args, void* stream);
 

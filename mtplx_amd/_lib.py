@@ -74,7 +74,8 @@ class QmvArgs(C.Structure):
     _fields_ = [(n, _vp) for n in ("x", "x2", "ss_in", "w0", "s0", "b0", "w1", "s1", "b1", "y0", "y1", "yf",
                                    "resid", "ss_out")] + [("eps", _f)] + \
                [(n, _i) for n in ("M", "N", "K", "group_size", "ldx", "ldy", "xmode", "emode", "packed")] + \
-               [("ws", _vp), ("ws_bytes", C.c_size_t), ("rope", C.POINTER(RopeOut)), ("schedule", _i)]
+               [("ws", _vp), ("ws_bytes", C.c_size_t), ("rope", C.POINTER(RopeOut)), ("schedule", _i)] + \
+               [(n, _vp) for n in ("x_sums", "y_sums")]
 
 
 def _fill(struct, fields: dict):

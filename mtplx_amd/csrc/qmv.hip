@@ -722,6 +722,8 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   stage_x_issue<NW>(p, xa, rstride, M, Q, q_lo, q_n, wave, lane);
   uint4 wpre[kNormPre];
   if (XM == X_RMSNORM) norm_w_prefetch<NW>(p, wpre, Q, q_lo, q_n, tid);
+  float2 xsv[kSumPre];
+  if (XM == X_PRE) xsum_prefetch<NW, XSW>(p, xsv, M, Q, q_lo, q_n, tid);
   asm volatile("" ::: "memory");
   QuadRegs ring[NR];
 #pragma unroll
@@ -735,7 +737,10 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
     }
   }
   __syncthreads();
-  stage_x_finish<XM, NW, XSW, PK>(p, xa, rstride, xs, wpre, s_inv_rms, M, Q, q_lo, q_n, tid);
+  if (XM == X_PRE)
+    xsum_finish<NW, XSW>(p, xs, xsv, M, Q, q_lo, q_n, tid);
+  else
+    stage_x_finish<XM, NW, XSW, PK>(p, xa, rstride, xs, wpre, s_inv_rms, M, Q, q_lo, q_n, tid);
   __syncthreads();  // staged x visible to every wave
   if (use_rpre) {
     const int head = tile0 / (p.rope_D >> 5);
@@ -901,12 +906,16 @@ template <int NW, int R, int XM, int EM, int GSH>
 static void launch_rk(const QmmParams& q, const Plan& pl, hipStream_t st) {
   if (q.packed && R == 4 && q.tail_ok && tail_launch(qmv_stream_kernel<NW, R, XM, EM, 0, true>, pl, NW * 64, st, q))
     return;
-  if (q.packed)
+  if constexpr (XM == X_PRE) {   // packed weights only (checked by the caller)
     launch_one(qmv_stream_kernel<NW, R, XM, EM, 0, true>, pl, NW * 64, st, q);
-  else if (pl.resident)
-    launch_one(qmv_stream_kernel<NW, R, XM, EM, GSH, false>, pl, NW * 64, st, q);
-  else
-    launch_one(qmv_chunked_kernel<NW, R, XM, EM, GSH>, pl, NW * 64, st, q);
+  } else {
+    if (q.packed)
+      launch_one(qmv_stream_kernel<NW, R, XM, EM, 0, true>, pl, NW * 64, st, q);
+    else if (pl.resident)
+      launch_one(qmv_stream_kernel<NW, R, XM, EM, GSH, false>, pl, NW * 64, st, q);
+    else
+      launch_one(qmv_chunked_kernel<NW, R, XM, EM, GSH>, pl, NW * 64, st, q);
+  }
 }
 
 template <int NW, int XM, int EM, int GSH>
@@ -944,6 +953,7 @@ static void launch_x(int xm, int em, const QmmParams& p, const Plan& pl, hipStre
   switch (xm) {
     case X_PLAIN: launch_e<X_PLAIN, GSH>(em, p, pl, st); break;
     case X_SWIGLU: launch_e<X_SWIGLU, GSH>(em, p, pl, st); break;
+    case X_PRE: launch_e<X_PRE, GSH>(em, p, pl, st); break;
     default: launch_e<X_RMSNORM, GSH>(em, p, pl, st); break;
   }
 }
@@ -999,8 +1009,12 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
     set_error("%s: residual mode needs a residual input", who);
     return MTP_ERR_ARG;
   }
-  if (xm != X_PLAIN && !p.x2) {
+  if ((xm == X_SWIGLU || xm == X_RMSNORM) && !p.x2) {
     set_error("%s: fused producer needs its second input", who);
+    return MTP_ERR_ARG;
+  }
+  if (xm == X_PRE && (!p.x_sums || !p.packed)) {
+    set_error("%s: xmode 3 needs the input's 32-column sums and packed weights", who);
     return MTP_ERR_ARG;
   }
   if (p.ldy < p.N) {
@@ -1399,6 +1413,8 @@ struct mtp_qmv_args {
   size_t ws_bytes;
   const mtp_rope_out* rope;
   int schedule;
+  const float* x_sums;
+  float* y_sums;
 };
 
 MTP_API int mtp_qmv_affine4_ex(const mtp_qmv_args* a, void* stream) {
@@ -1406,7 +1422,7 @@ MTP_API int mtp_qmv_affine4_ex(const mtp_qmv_args* a, void* stream) {
     set_error("mtp_qmv_affine4_ex: null argument block");
     return MTP_ERR_ARG;
   }
-  if (a->xmode < 0 || a->xmode > 2 || a->emode < 0 || a->emode > 4 || (a->emode == E_ROPE_QKV && !a->rope)) {
+  if (a->xmode < 0 || a->xmode > 3 || a->emode < 0 || a->emode > 4 || (a->emode == E_ROPE_QKV && !a->rope)) {
     set_error("mtp_qmv_affine4_ex: xmode %d / emode %d out of range", a->xmode, a->emode);
     return MTP_ERR_ARG;
   }
@@ -1425,6 +1441,8 @@ MTP_API int mtp_qmv_affine4_ex(const mtp_qmv_args* a, void* stream) {
   p.packed = a->packed;
   if (a->ldx > 0) p.ldx = a->ldx;
   if (a->ldy > 0) p.ldy = a->ldy;
+  p.x_sums = a->x_sums;
+  p.y_sums = a->y_sums;
   if (a->emode == E_ROPE_QKV) {
     const mtp_rope_out* r = a->rope;
     p.q_start = r->q_start;

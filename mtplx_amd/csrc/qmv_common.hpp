@@ -7,7 +7,9 @@
 
 namespace mtp {
 
-enum XMode { X_PLAIN = 0, X_SWIGLU = 1, X_RMSNORM = 2 };
+// X_PRE: x comes with its per-32-column row sums (written by the producing
+// epilogue), so staging is the copy alone.
+enum XMode { X_PLAIN = 0, X_SWIGLU = 1, X_RMSNORM = 2, X_PRE = 3 };
 enum EMode { E_STORE = 0, E_RESID = 1, E_DUAL = 2, E_DUAL_SWIGLU = 3, E_ROPE_QKV = 4 };
 
 struct QmmParams {
@@ -41,6 +43,11 @@ struct QmmParams {
   int packed;              // w0/w1 in the tile-major layout (scales/biases inside)
   int tail_first, tail_split;   // tail split of the per-tile kernel (tail_split > 1)
   int tail_ok;                  // a workspace (partial, counters) is available for it
+  // X_PRE input: per 32-column block, per row, sum of x ([K/32][32]).
+  const float* x_sums;
+  // Output for a following X_PRE matmul: the per-32-column row sums of the
+  // stored y0 values, layout [N/32][32] (E_STORE, E_RESID, E_DUAL_SWIGLU).
+  float* y_sums;
   float eps;
   // E_ROPE_QKV: the q|k|v rows go through RoPE straight to q_out [B, Hq, L, D]
   // and the K/V cache; row r is request r / rope_L, position q_start + r % rope_L.
@@ -220,6 +227,43 @@ __device__ __forceinline__ void norm_w_prefetch(const QmmParams& p, uint4 (&wpre
     const int it = tid + j * NW * 64;
     wpre[j] = make_uint4(0, 0, 0, 0);
     if (it < nit) wpre[j] = *reinterpret_cast<const uint4*>(p.x2 + norm_item_k(it, Q, kq0));
+  }
+}
+
+// X_PRE: the group sums xs[gl][r] (r < XSW) of the staged groups come from
+// the producer's 32-column sums; a thread's first kSumPre items are fetched
+// with the x loads. Item it = gl * XSW + r.
+constexpr int kSumPre = 3;
+__device__ __forceinline__ float2 xsum_item(const QmmParams& p, int it, int XSW, int M, int Q, int kq0) {
+  const int gl = it / XSW, r = it - gl * XSW;
+  if (r >= M) return make_float2(0.f, 0.f);
+  int qd = kq0 + (gl >> 2);
+  if (qd >= Q) qd -= Q;
+  const int g = 4 * qd + (gl & 3);
+  return make_float2(p.x_sums[(size_t)(2 * g) * 32 + r], p.x_sums[(size_t)(2 * g + 1) * 32 + r]);
+}
+template <int NW, int XSW>
+__device__ __forceinline__ void xsum_prefetch(const QmmParams& p, float2 (&sv)[kSumPre], int M, int Q, int kq0,
+                                              int nslot, int tid) {
+  const int nit = 4 * nslot * XSW;
+#pragma unroll
+  for (int j = 0; j < kSumPre; ++j) {
+    const int it = tid + j * NW * 64;
+    sv[j] = it < nit ? xsum_item(p, it, XSW, M, Q, kq0) : make_float2(0.f, 0.f);
+  }
+}
+template <int NW, int XSW>
+__device__ __forceinline__ void xsum_finish(const QmmParams& p, float* xs, const float2 (&sv)[kSumPre], int M, int Q,
+                                            int kq0, int nslot, int tid) {
+  const int nit = 4 * nslot * XSW;
+#pragma unroll
+  for (int j = 0; j < kSumPre; ++j) {
+    const int it = tid + j * NW * 64;
+    if (it < nit) xs[it] = sv[j].x + sv[j].y;
+  }
+  for (int it = tid + kSumPre * NW * 64; it < nit; it += NW * 64) {
+    const float2 v = xsum_item(p, it, XSW, M, Q, kq0);
+    xs[it] = v.x + v.y;
   }
 }
 
@@ -500,13 +544,18 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int
       }
     } else if (EM == E_DUAL_SWIGLU) {
       const float gs = round_bf(silu_f(round_bf(g)));
-      if (in) p.y0[o] = f2bf(gs * round_bf(fin[m * 64 + 32 + c]));
+      const float a = in ? round_bf(gs * round_bf(fin[m * 64 + 32 + c])) : 0.f;
+      if (in) p.y0[o] = f2bf(a);
+      fin[m * 64 + c] = a;   // this thread's own slot: the row sums below
     } else {
       float v = g;
       if (EM == E_RESID) {
         const float rv = (pre && idx == tid) ? *pre : (in ? bf2f(p.resid[o]) : 0.f);
         v = round_bf(in ? round_bf(v) + rv : 0.f);
         fin[m * 64 + 32 + c] = v * v;  // column 32+c is free in non-dual modes
+        fin[m * 64 + c] = v;           // this thread's own slot: the row sums below
+      } else {
+        fin[m * 64 + c] = in ? round_bf(v) : 0.f;
       }
       if (in) {
         if (EM == E_STORE && p.yf)
@@ -516,12 +565,20 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int
       }
     }
   }
-  if (EM == E_RESID && p.ss_out) {
+  const bool ss = EM == E_RESID && p.ss_out;
+  const bool xsum = EM != E_DUAL && p.y_sums;
+  if (ss || xsum) {
     __syncthreads();
-    if (tid < M) {
-      float ss = 0.f;
-      for (int c = 0; c < 32; ++c) ss += fin[tid * 64 + 32 + c];
-      p.ss_out[(size_t)nb * 32 + row0 + tid] = ss;
+    if (ss && tid < M) {
+      float a = 0.f;
+      for (int c = 0; c < 32; ++c) a += fin[tid * 64 + 32 + c];
+      p.ss_out[(size_t)nb * 32 + row0 + tid] = a;
+    }
+    if (xsum && tid >= 64 && tid < 64 + M) {   // another wave, in parallel
+      const int m = tid - 64;
+      float a = 0.f;
+      for (int c = 0; c < 32; ++c) a += fin[m * 64 + c];
+      p.y_sums[(size_t)nb * 32 + row0 + m] = a;
     }
   }
 }

@@ -378,7 +378,7 @@ int qmv_sk_launch(int xm, int em, const QmmParams& p, void* ws, size_t ws_bytes,
   const int nslot = per < Q ? per : Q;
   // Verify widths (M <= 8 rows: one 4-register accumulator row block); wider
   // M keeps the per-tile kernel, whose staged x is shared by fewer items.
-  if (p.M > 8 || !p.packed) return MTP_ERR_UNSUPPORTED;
+  if (p.M > 8 || !p.packed || xm == X_PRE) return MTP_ERR_UNSUPPORTED;
   const int nseg = sk_max_segments(per, Q * (dual ? 2 : 1));
   const size_t lds = sk_lds_bytes(nslot, nseg, p.M, 4, dual ? 2 : 1);
   if (lds > 160 * 1024 - 256) return MTP_ERR_UNSUPPORTED;

@@ -235,6 +235,9 @@ class VerifyModel:
         ss_a = torch.empty(((H + 31) // 32) * 32, dtype=torch.float32, device=dev)
         ss_b = torch.empty_like(ss_a)
         ss_h = None
+        # gate/up also writes the 32-column row sums of its SwiGLU output, so
+        # down_proj stages its x without a pass over it (xmode 3).
+        act_sums = torch.empty(((ffn + 31) // 32) * 32, dtype=torch.float32, device=dev)
         nb = _lib.query("mtp_attn_vt_workspace_bytes", B, c.n_kv_heads, self.cap)
         aws = _lib.WORKSPACES.get(nb, "attn", dev)
         scale = 1.0 / math.sqrt(c.head_dim)
@@ -250,15 +253,16 @@ class VerifyModel:
         fused_rope = M <= 8   # the RoPE epilogue covers up to 8 rows
 
         for li, L in enumerate(self.layers):
+            xin = dict(x=h, x2=L.in_norm, xmode=2)   # input RMSNorm fused into the staging
             if fused_rope:
                 rope = dict(q_start=q_start, q_lens=ql, q_out=qh, k_cache=self.k_cache[li], v_cache=self.v_cache[li],
                             status=status, L=Lq, Hq=c.n_heads, Hkv=c.n_kv_heads, D=c.head_dim, cap=self.cap,
                             blocked=1, rope_base=c.rope_theta)
-                qmv(st, rope=rope, x=h, x2=L.in_norm, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv_rope, M=M,
-                    N=c.qkv_out, K=H, group_size=gs, xmode=2, emode=4, packed=1)
+                qmv(st, rope=rope, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv_rope, M=M, N=c.qkv_out, K=H, group_size=gs,
+                    emode=4, packed=1, **xin)
             else:
-                qmv(st, x=h, x2=L.in_norm, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv.packed, y0=qkv, M=M, N=c.qkv_out,
-                    K=H, group_size=gs, xmode=2, emode=0, packed=1)
+                qmv(st, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv.packed, y0=qkv, M=M, N=c.qkv_out, K=H, group_size=gs,
+                    emode=0, packed=1, **xin)
                 call("mtp_rope_qkv_to_cache_vt", qkv.data_ptr(), q_start.data_ptr(), _lib.ptr(ql), qh.data_ptr(),
                      self.k_cache[li].data_ptr(), self.v_cache[li].data_ptr(), B, Lq, c.n_heads, c.n_kv_heads,
                      c.head_dim, self.cap, ctypes.c_float(c.rope_theta), status.data_ptr(), st)
@@ -273,9 +277,9 @@ class VerifyModel:
                 ss_h = None
             else:
                 qmv(st, x=h, x2=L.post_norm, ss_in=ss_h, eps=c.rms_eps, w0=L.gate.packed, w1=L.up.packed, y0=act,
-                    M=M, N=c.ffn, K=H, group_size=gs, xmode=2, emode=3, packed=1)
-                qmv(st, x=act, w0=L.down.packed, resid=h, y0=h, ss_out=ss_b, M=M, N=H, K=c.ffn, group_size=gs,
-                    xmode=0, emode=1, packed=1)
+                    y_sums=act_sums, M=M, N=c.ffn, K=H, group_size=gs, xmode=2, emode=3, packed=1)
+                qmv(st, x=act, x_sums=act_sums, w0=L.down.packed, resid=h, y0=h, ss_out=ss_b, M=M, N=H, K=c.ffn,
+                    group_size=gs, xmode=3, emode=1, packed=1)
                 ss_h = ss_b
         logits = logits_out if logits_out is not None else torch.empty((M, c.vocab), dtype=torch.float32, device=dev)
         qmv(st, x=h, x2=self.final_norm, ss_in=ss_h, eps=c.rms_eps, w0=self.lm_head.packed, yf=logits, M=M,
