@@ -18,6 +18,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import subprocess
 import sys
 import time
@@ -43,8 +44,6 @@ def roofline_gate_up(model, M: int, reps: int = 5) -> dict:
     in a HIP graph and replayed, timed with events on the capture stream."""
     import torch
 
-    from mtplx_amd import _lib
-
     c = model.cfg
     dev = model.device
     x = torch.randn((M, c.hidden), device=dev).to(torch.bfloat16)
@@ -52,13 +51,8 @@ def roofline_gate_up(model, M: int, reps: int = 5) -> dict:
     ss = torch.zeros(((c.hidden + 31) // 32) * 32, dtype=torch.float32, device=dev)
     ss.view(-1, 32)[:, :M] = (xf * xf).view(M, -1, 32).sum(dim=2).t()
     y = torch.empty((M, c.ffn), dtype=torch.bfloat16, device=dev)
-    nb = _lib.query("mtp_qmv_workspace_bytes", M, c.ffn, c.hidden, 1)
-    ws = _lib.WORKSPACES.get(nb, "qmv", dev)
-
-    def launch(L):
-        _lib.qmv_ex(_lib.stream_handle(dev), x=x, x2=L.post_norm, ss_in=ss, eps=c.rms_eps, w0=L.gate.packed,
-                    w1=L.up.packed, y0=y, M=M, N=c.ffn, K=c.hidden, group_size=c.group_size, xmode=2, emode=3,
-                    packed=1, ws=ws, ws_bytes=ws.numel())
+    ysum = torch.empty(((c.ffn + 31) // 32) * 32, dtype=torch.float32, device=dev)
+    launch = _gate_up_launcher(model, M, x, ss, y, ysum)
 
     for L in model.layers:
         launch(L)
@@ -81,10 +75,71 @@ def roofline_gate_up(model, M: int, reps: int = 5) -> dict:
     byts = _gate_up_bytes(M, c.ffn, c.hidden, c.group_size)
     gbs = byts / us / 1e3
     return {"bound": "hbm",
-            "kernel": "qmv_stream_kernel<NW=4,R=4,X_RMSNORM,E_DUAL_SWIGLU,packed> (mtp_qmv_affine4_ex)",
+            "kernel": "qmv_stream_kernel<NW=4,R=4,X_RMSNORM,E_DUAL_SWIGLU,packed> (mtp_qmv_affine4_ex, tail split)",
             "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None, "algorithmic_bytes_per_launch": byts, "avg_launch_us": round(us, 3),
+            "traffic": measured_traffic(), "algorithmic_bytes_per_launch": byts, "avg_launch_us": round(us, 3),
             "launches_timed": n}
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gate_up_cfg3_traffic.md")
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per launch of the roofline kernel, from the committed
+    rocprofv3 FETCH_SIZE + WRITE_SIZE summary (each scaled by the copy-kernel
+    calibration stated there), or None when absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                m = re.match(r"\s*traffic_bytes_per_launch:\s*(\d+)", line)
+                if m:
+                    return int(m.group(1))
+    except OSError:
+        pass
+    return None
+
+
+def profile_roofline(model, M: int) -> None:
+    """The counter workload: the roofline kernel over every layer twice, eager
+    (one dispatch each), then a 256 MiB device copy whose FETCH_SIZE /
+    WRITE_SIZE readings calibrate the counters (256 MiB read + written)."""
+    import torch
+
+    c = model.cfg
+    dev = model.device
+    x = torch.randn((M, c.hidden), device=dev).to(torch.bfloat16)
+    xf = x.float()
+    ss = torch.zeros(((c.hidden + 31) // 32) * 32, dtype=torch.float32, device=dev)
+    ss.view(-1, 32)[:, :M] = (xf * xf).view(M, -1, 32).sum(dim=2).t()
+    y = torch.empty((M, c.ffn), dtype=torch.bfloat16, device=dev)
+    ysum = torch.empty(((c.ffn + 31) // 32) * 32, dtype=torch.float32, device=dev)
+    launch = _gate_up_launcher(model, M, x, ss, y, ysum)
+    for _ in range(2):
+        for L in model.layers:
+            launch(L)
+    src = torch.ones(64 << 20, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("roofline counter workload done", flush=True)
+
+
+def _gate_up_launcher(model, M, x, ss, y, ysum):
+    """The verify step's own gate/up call (packed weights, norm statistics
+    handed over, SwiGLU output sums for down_proj, the shared workspace)."""
+    from mtplx_amd import _lib
+
+    c = model.cfg
+    dev = model.device
+    nb = _lib.query("mtp_qmv_workspace_bytes", M, c.ffn, c.hidden, 1)
+    ws = _lib.WORKSPACES.get(nb, "qmv", dev)
+
+    def launch(L):
+        _lib.qmv_ex(_lib.stream_handle(dev), x=x, x2=L.post_norm, ss_in=ss, eps=c.rms_eps, w0=L.gate.packed,
+                    w1=L.up.packed, y0=y, y_sums=ysum, M=M, N=c.ffn, K=c.hidden, group_size=c.group_size, xmode=2,
+                    emode=3, packed=1, ws=ws, ws_bytes=ws.numel())
+    return launch
 
 
 def roofline_qmv_cfg1(reps: int = 64, nsets: int = 8) -> dict:
@@ -191,6 +246,9 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch kernel by kernel instead of one HIP graph per step")
+    ap.add_argument("--profile-roofline", action="store_true",
+                    help="only launch the roofline kernel (2 passes over the layers, eager) and a 256 MiB copy, "
+                         "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the hot path is single-GPU); --gpus {args.gpus} is not supported",
@@ -210,6 +268,9 @@ def main() -> int:
     B, K = 1, 3
     L = K + 1
     model = VerifyModel(cfg, device=dev, seed=0)
+    if args.profile_roofline:
+        profile_roofline(model, B * L)
+        return 0
     model.allocate_cache(B, args.ctx)
     gen = torch.Generator(device=dev).manual_seed(123)
     tokens = torch.randint(0, cfg.vocab, (B, L), device=dev, dtype=torch.int32, generator=gen)
