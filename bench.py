@@ -75,7 +75,8 @@ def roofline_gate_up(model, M: int, reps: int = 5) -> dict:
     byts = _gate_up_bytes(M, c.ffn, c.hidden, c.group_size)
     gbs = byts / us / 1e3
     return {"bound": "hbm",
-            "kernel": "qmv_stream_kernel<NW=4,R=4,X_RMSNORM,E_DUAL_SWIGLU,packed> (mtp_qmv_affine4_ex, tail split)",
+            "kernel": "qmv_stream_kernel<NW=4,R=4,X_RMSNORM,E_DUAL_SWIGLU,packed,MF> (mtp_qmv_affine4_ex, packed layout 2, "
+                      "tail split)",
             "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(), "algorithmic_bytes_per_launch": byts, "avg_launch_us": round(us, 3),
             "launches_timed": n}
@@ -136,9 +137,11 @@ def _gate_up_launcher(model, M, x, ss, y, ysum):
     ws = _lib.WORKSPACES.get(nb, "qmv", dev)
 
     def launch(L):
-        _lib.qmv_ex(_lib.stream_handle(dev), x=x, x2=L.post_norm, ss_in=ss, eps=c.rms_eps, w0=L.gate.packed,
-                    w1=L.up.packed, y0=y, y_sums=ysum, M=M, N=c.ffn, K=c.hidden, group_size=c.group_size, xmode=2,
-                    emode=3, packed=1, ws=ws, ws_bytes=ws.numel())
+        lay = 2 if M <= 4 else 1   # as the verify step chooses
+        _lib.qmv_ex(_lib.stream_handle(dev), x=x, x2=L.post_norm, ss_in=ss, eps=c.rms_eps,
+                    w0=L.gate.packed_mf16 if lay == 2 else L.gate.packed,
+                    w1=L.up.packed_mf16 if lay == 2 else L.up.packed, y0=y, y_sums=ysum, M=M, N=c.ffn, K=c.hidden,
+                    group_size=c.group_size, xmode=2, emode=3, packed=lay, ws=ws, ws_bytes=ws.numel())
     return launch
 
 

@@ -54,6 +54,7 @@ SIGNATURES = {
     "mtp_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mtp_pack_affine4_bytes": (_sz, [_i, _i]),
     "mtp_pack_affine4": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "mtp_pack_affine4_mf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mtp_qmv_affine4_ex": (_i, [_vp, _vp]),
     "mtp_attn_vt_workspace_bytes": (_sz, [_i, _i, _i]),
     "mtp_ragged_gqa_attn_rows_vt": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),

@@ -506,7 +506,11 @@ __global__ __launch_bounds__(NW * 64) void qmv_chunked_kernel(QmmParams p) {
 // wait for quad i only covers loads issued before i (the NR-1 quads behind it
 // stay in flight). Lanes whose A-operand row is past M read a zero block in
 // LDS instead of branching.
-template <int NW, int R, int XM, int EM, int GSH, bool PK>
+//
+// MF (packed layout 2, M <= 4): the quads run on v_mfma_f32_16x16x32_bf16
+// (quad_mma16): half the MFMA cycles of the 32x32x16 form for these 4 rows
+// and a quarter of the group-finish FMAs. Staging and epilogues are shared.
+template <int NW, int R, int XM, int EM, int GSH, bool PK, bool MF = false>
 __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NT = NW * 64;
@@ -562,6 +566,7 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   struct QuadRegs {
     uint4 w[4];
     uint32_t s[2], b[2];
+    uint32_t s1[MF ? 2 : 1], b1[MF ? 2 : 1];   // MF: the lane's second column (16 + l%16)
   };
   // Prefetch iterator: tile j_pf, quad counter t_pf (q = kw + t_pf*KS); the
   // per-lane row pointers are recomputed only when the tile changes.
@@ -575,7 +580,7 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
       // Tile-major packed weights: per (tile, quad) 1152 words — 4 x 256
       // words of nibbles in load order, then 32 rows x (4 s, 4 b) bf16.
       wrow = W + (size_t)nb * Q * kPackQuadWords + lane * 4;
-      srow = reinterpret_cast<const uint16_t*>(W + (size_t)nb * Q * kPackQuadWords + 1024 + c32 * 4);
+      srow = reinterpret_cast<const uint16_t*>(W + (size_t)nb * Q * kPackQuadWords + 1024 + (MF ? (lane & 15) : c32) * 4);
       brow = nullptr;
     } else {
       const int n = nb * 32 + c32;
@@ -598,6 +603,11 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
       const uint4 sb = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(srow) + qoff);
       qr.s[0] = sb.x; qr.s[1] = sb.y;
       qr.b[0] = sb.z; qr.b[1] = sb.w;
+      if (MF) {
+        const uint4 sb1 = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(srow) + qoff + 64);
+        qr.s1[0] = sb1.x; qr.s1[MF ? 1 : 0] = sb1.y;
+        qr.b1[0] = sb1.z; qr.b1[MF ? 1 : 0] = sb1.w;
+      }
     } else {
       const uint32_t* wp = wrow + 32 * KS * t_pf;
 #pragma unroll
@@ -626,12 +636,26 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  // MF: A row 4m holds x row m, read by lanes with (l%16) = 4m (the other
+  // lanes of each four read a valid row too; their outputs are unused).
+  const int mf_arow = ((lane & 15) >> 2) < M ? ((lane & 15) >> 2) : 0;
+  const uint32_t mf_a0 = (uint32_t)xa_index(0, mf_arow, M, rstride, 0, lane >> 4) * 16;
+  const uint32_t mf_a1 = (uint32_t)xa_index(1, mf_arow, M, rstride, 0, lane >> 4) * 16;
+  const uint32_t mf_x = (uint32_t)((unsigned char*)xs - smem) + 4 * ((lane >> 4) < M ? (lane >> 4) : 0);
 
   auto compute = [&](const QuadRegs& cr, int t) {
     const int gq = 4 * (kw + t * KS);
     float sv[4], cb[4];
     quad_scales<GSH>(cr.s, cr.b, sv, cb);
-    quad_mma<R>(smem, a_lane + (uint32_t)gq * 64, x_lane + (uint32_t)gq * (XSW * 4), cr.w, sv, cb, nc, acc);
+    if constexpr (MF) {
+      float sv1[4], cb1[4];
+      const uint32_t s1w[2] = {cr.s1[0], cr.s1[MF ? 1 : 0]}, b1w[2] = {cr.b1[0], cr.b1[MF ? 1 : 0]};
+      quad_scales<0>(s1w, b1w, sv1, cb1);
+      quad_mma16(smem, mf_a0 + (uint32_t)gq * 64, mf_a1 + (uint32_t)gq * 64, mf_x + (uint32_t)gq * (XSW * 4), XSW,
+                 cr.w, sv, cb, sv1, cb1, nc, acc[0], acc[1]);
+    } else {
+      quad_mma<R>(smem, a_lane + (uint32_t)gq * 64, x_lane + (uint32_t)gq * (XSW * 4), cr.w, sv, cb, nc, acc);
+    }
   };
 
   // Residual of this thread's first epilogue element, fetched now so the
@@ -658,11 +682,21 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
     const int nb = tile0 + j * G;
     const bool valid = nb * 32 + c32 < p.N;
     __syncthreads();
+    if constexpr (MF) {   // lane l: row l/16, columns l%16 and 16 + l%16
+      const int m = lane >> 4, c = lane & 15;
+      if (m < M) {
+        red[(wave * M + m) * 32 + c] = (nb * 32 + c < p.N) ? acc[0] : 0.f;
+        red[(wave * M + m) * 32 + 16 + c] = (nb * 32 + 16 + c < p.N) ? acc[1] : 0.f;
+      }
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int m = 8 * (r >> 2) + 4 * kq + (r & 3);
-      if (m < M) red[(wave * M + m) * 32 + c32] = valid ? acc[r] : 0.f;
-      acc[r] = 0.f;
+      for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int m = 8 * (r >> 2) + 4 * kq + (r & 3);
+        if (m < M) red[(wave * M + m) * 32 + c32] = valid ? acc[r] : 0.f;
+        acc[r] = 0.f;
+      }
     }
     __syncthreads();
     for (int idx = tid; idx < M * 64; idx += NT) {
@@ -904,6 +938,13 @@ static bool tail_launch(K kernel, const Plan& pl, int nt, hipStream_t st, QmmPar
 
 template <int NW, int R, int XM, int EM, int GSH>
 static void launch_rk(const QmmParams& q, const Plan& pl, hipStream_t st) {
+  if constexpr (R == 4) {
+    if (q.packed == 2) {   // 16x16x32 layout, M <= 4 (checked by the caller)
+      if (!(q.tail_ok && tail_launch(qmv_stream_kernel<NW, 4, XM, EM, 0, true, true>, pl, NW * 64, st, q)))
+        launch_one(qmv_stream_kernel<NW, 4, XM, EM, 0, true, true>, pl, NW * 64, st, q);
+      return;
+    }
+  }
   if (q.packed && R == 4 && q.tail_ok && tail_launch(qmv_stream_kernel<NW, R, XM, EM, 0, true>, pl, NW * 64, st, q))
     return;
   if constexpr (XM == X_PRE) {   // packed weights only (checked by the caller)
@@ -961,10 +1002,16 @@ static void launch_x(int xm, int em, const QmmParams& p, const Plan& pl, hipStre
 // q|k|v with the RoPE epilogue: packed weights, R = 4 (M <= 8) only.
 template <int XM>
 static void launch_rope(const QmmParams& q, const Plan& pl, hipStream_t st) {
-  if (pl.nw == 8)
+  if (q.packed == 2) {
+    if (pl.nw == 8)
+      launch_one(qmv_stream_kernel<8, 4, XM, E_ROPE_QKV, 0, true, true>, pl, 8 * 64, st, q);
+    else
+      launch_one(qmv_stream_kernel<4, 4, XM, E_ROPE_QKV, 0, true, true>, pl, 4 * 64, st, q);
+  } else if (pl.nw == 8) {
     launch_one(qmv_stream_kernel<8, 4, XM, E_ROPE_QKV, 0, true>, pl, 8 * 64, st, q);
-  else
+  } else {
     launch_one(qmv_stream_kernel<4, 4, XM, E_ROPE_QKV, 0, true>, pl, 4 * 64, st, q);
+  }
 }
 
 static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
@@ -1021,6 +1068,14 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
     set_error("%s: ldy=%d < N=%d", who, p.ldy, p.N);
     return MTP_ERR_ARG;
   }
+  if (p.packed < 0 || p.packed > 2) {
+    set_error("%s: packed=%d (0 = MLX layout, 1, 2 = packed layouts)", who, p.packed);
+    return MTP_ERR_ARG;
+  }
+  if (p.packed == 2 && p.M > 4) {
+    set_error("%s: packed layout 2 (16x16x32) serves M <= 4 only (M=%d)", who, p.M);
+    return MTP_ERR_UNSUPPORTED;
+  }
   if (em == E_ROPE_QKV) {
     const int D = p.rope_D;
     if (!p.packed || p.M > 8 || (xm != X_PLAIN && xm != X_RMSNORM) || !p.q_start || !p.q_out || !p.k_cache ||
@@ -1051,7 +1106,7 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
       set_error("%s: workspace of %zu B (256-B aligned) needed, got %zu B", who, need, ws_bytes);
       return MTP_ERR_WORKSPACE;
     }
-    if (schedule == 1) {
+    if (schedule == 1 && p.packed == 1) {
       // Stream-K over all CUs; shapes whose staged x does not fit its LDS
       // plan use the per-tile kernel below.
       const int rc = qmv_sk_launch(xm, em, p, ws, ws_bytes, st);
@@ -1316,8 +1371,11 @@ __device__ __forceinline__ uint32_t nibbles_natural(uint32_t w) {
   return o;
 }
 
+// layout 1: the 32x32x16 order - load u, lane l: words [32q + 8u + 4(l/32), +4)
+// of row 32t + l%32. layout 2 (16x16x32, quad_mma16): load u = group u, lane l:
+// word jj = 2 kk + h is word 8u + 4kk + l/16 of row 32t + 16h + l%16.
 __global__ void pack_affine4_kernel(const uint32_t* w, const uint16_t* s, const uint16_t* b, uint32_t* out, int N,
-                                    int K, int gshift) {
+                                    int K, int gshift, int layout) {
   const int Q = K >> 8;
   const size_t units = (size_t)cdiv(N, 32) * Q * 288;   // 16 B units
   for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < units; t += (size_t)gridDim.x * blockDim.x) {
@@ -1326,7 +1384,16 @@ __global__ void pack_affine4_kernel(const uint32_t* w, const uint16_t* s, const 
     const int nb = (int)(tq / Q);
     const int q = (int)(tq - (size_t)nb * Q);
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (u16 < 256) {
+    if (u16 < 256 && layout == 2) {
+      const int u = u16 >> 6, l = u16 & 63;
+      uint32_t wv[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int row = nb * 32 + 16 * (jj & 1) + (l & 15);
+        wv[jj] = row < N ? nibbles_natural(w[(size_t)row * (K >> 3) + 32 * q + 8 * u + 4 * (jj >> 1) + (l >> 4)]) : 0u;
+      }
+      v = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+    } else if (u16 < 256) {
       const int u = u16 >> 6, l = u16 & 63;
       const int row = nb * 32 + (l & 31);
       if (row < N) {
@@ -1361,14 +1428,14 @@ MTP_API size_t mtp_pack_affine4_bytes(int N, int K) {
   return (size_t)cdiv(N, 32) * (K / 256) * kPackQuadWords * 4;
 }
 
-MTP_API int mtp_pack_affine4(const void* w, const void* scales, const void* biases, void* out, int N, int K,
-                             int group_size, void* stream) {
+static int pack_run(const void* w, const void* scales, const void* biases, void* out, int N, int K, int group_size,
+                    int layout, void* stream, const char* who) {
   if (!w || !scales || !biases || !out || N < 1 || K < 256 || K % 256 || !aligned16(w) || !aligned16(out)) {
-    set_error("mtp_pack_affine4: bad arguments (K %% 256 == 0, 16-byte aligned w/out)");
+    set_error("%s: bad arguments (K %% 256 == 0, 16-byte aligned w/out)", who);
     return MTP_ERR_ARG;
   }
   if (group_size != 64 && group_size != 128) {
-    set_error("mtp_pack_affine4: group_size %d unsupported", group_size);
+    set_error("%s: group_size %d unsupported", who, group_size);
     return MTP_ERR_UNSUPPORTED;
   }
   const size_t units = (size_t)cdiv(N, 32) * (K / 256) * 288;
@@ -1376,8 +1443,18 @@ MTP_API int mtp_pack_affine4(const void* w, const void* scales, const void* bias
   if (grid > 65536) grid = 65536;
   hipLaunchKernelGGL(pack_affine4_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
                      (const uint32_t*)w, (const uint16_t*)scales, (const uint16_t*)biases, (uint32_t*)out, N, K,
-                     group_size == 128 ? 1 : 0);
-  return launch_check("mtp_pack_affine4");
+                     group_size == 128 ? 1 : 0, layout);
+  return launch_check(who);
+}
+
+MTP_API int mtp_pack_affine4(const void* w, const void* scales, const void* biases, void* out, int N, int K,
+                             int group_size, void* stream) {
+  return pack_run(w, scales, biases, out, N, K, group_size, 1, stream, "mtp_pack_affine4");
+}
+
+MTP_API int mtp_pack_affine4_mf16(const void* w, const void* scales, const void* biases, void* out, int N, int K,
+                                  int group_size, void* stream) {
+  return pack_run(w, scales, biases, out, N, K, group_size, 2, stream, "mtp_pack_affine4_mf16");
 }
 
 struct mtp_rope_out {

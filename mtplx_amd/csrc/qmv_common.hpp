@@ -448,6 +448,32 @@ __device__ __forceinline__ void quad_mma(const unsigned char* lds, uint32_t a_of
   }
 }
 
+// One quad on v_mfma_f32_16x16x32_bf16 for M <= 4 (packed layout 2). x row m
+// sits at A row 4m, so lane l's output register 0 is (row l/16, column
+// l%16 [+16]): one accumulator per column half, two FMAs per group each.
+// ``w[g]``: group g's words (2g, h=0), (2g, h=1), (2g+1, h=0), (2g+1, h=1);
+// ``a0``/``a1``: byte offsets of the lane's A chunk of the group's first and
+// second 32-k step; ``x_off``: byte offset of xs[g0][l/16].
+__device__ __forceinline__ void quad_mma16(const unsigned char* lds, uint32_t a0, uint32_t a1, uint32_t x_off,
+                                           int xsw, const uint4 (&w)[4], const float (&s0)[4], const float (&cb0)[4],
+                                           const float (&s1)[4], const float (&cb1)[4], NibConsts nc, float& t0,
+                                           float& t1) {
+  typedef float f32x4_t __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const bf16x8 A0 = *reinterpret_cast<const bf16x8*>(lds + a0 + g * 64);
+    const bf16x8 A1 = *reinterpret_cast<const bf16x8*>(lds + a1 + g * 64);
+    f32x4_t G0 = {}, G1 = {};
+    G0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, nibbles_to_bf16(w[g].x, nc), G0, 0, 0, 0);
+    G1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, nibbles_to_bf16(w[g].y, nc), G1, 0, 0, 0);
+    G0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, nibbles_to_bf16(w[g].z, nc), G0, 0, 0, 0);
+    G1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, nibbles_to_bf16(w[g].w, nc), G1, 0, 0, 0);
+    const float xv = *reinterpret_cast<const float*>(lds + x_off + g * xsw * 4);
+    t0 = fmaf(s0[g], G0[0], fmaf(cb0[g], xv, t0));
+    t1 = fmaf(s1[g], G1[0], fmaf(cb1[g], xv, t1));
+  }
+}
+
 // Second producer input of the chunk at (row offset xo, column k): the up
 // half for SwiGLU, the norm weight for RMSNorm, nothing otherwise.
 template <int XM>

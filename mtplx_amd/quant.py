@@ -24,14 +24,21 @@ class QuantizedLinear:
         self.bits = int(bits)
         self.mode = mode
         self.bias = bias
-        self.packed: torch.Tensor | None = None
+        self.packed: torch.Tensor | None = None         # layout 1 (any M)
+        self.packed_mf16: torch.Tensor | None = None    # layout 2 (M <= 4)
 
-    def pack(self, row_order: torch.Tensor | None = None) -> torch.Tensor:
-        """Tile-major copy of the weights for the streaming kernel. Without
-        ``row_order`` it is made once and cached; with it, packed row i is
-        original row ``row_order[i]`` (e.g. :func:`rope_row_order`)."""
-        if row_order is None and self.packed is not None:
+    def pack(self, row_order: torch.Tensor | None = None, layout: int = 1) -> torch.Tensor:
+        """Tile-major copy of the weights for the streaming kernel. ``layout``
+        1 serves any M (``packed=1``); 2 is the 16x16x32-MFMA order for M <= 4
+        (``packed=2``). Without ``row_order`` each layout is made once and
+        cached; with it, packed row i is original row ``row_order[i]`` (e.g.
+        :func:`rope_row_order`)."""
+        if row_order is None and layout == 1 and self.packed is not None:
             return self.packed
+        if row_order is None and layout == 2 and self.packed_mf16 is not None:
+            return self.packed_mf16
+        if layout not in (1, 2):
+            raise ValueError(f"layout {layout} (1 or 2)")
         from . import _lib
 
         if self.weight.dim() != 2 or self.bits != 4 or self.mode != "affine":
@@ -47,10 +54,13 @@ class QuantizedLinear:
                 raise ValueError(f"row_order has {idx.numel()} entries, layer has {n} rows")
             w, s, b = w[idx].contiguous(), s[idx].contiguous(), b[idx].contiguous()
         out = torch.empty(nbytes // 4, dtype=torch.int32, device=w.device)
-        _lib.call("mtp_pack_affine4", w.data_ptr(), s.data_ptr(), b.data_ptr(), out.data_ptr(), n, k,
-                  self.group_size, _lib.stream_handle(w.device))
+        _lib.call("mtp_pack_affine4" if layout == 1 else "mtp_pack_affine4_mf16", w.data_ptr(), s.data_ptr(),
+                  b.data_ptr(), out.data_ptr(), n, k, self.group_size, _lib.stream_handle(w.device))
         if row_order is None:
-            self.packed = out
+            if layout == 1:
+                self.packed = out
+            else:
+                self.packed_mf16 = out
         return out
 
     @property

@@ -86,7 +86,8 @@ class Layer:
     shared_gate: QuantizedLinear | None = None
     shared_up: QuantizedLinear | None = None
     shared_down: QuantizedLinear | None = None
-    qkv_rope: torch.Tensor | None = None   # q|k|v packed in RoPE tile order (fused RoPE epilogue)
+    qkv_rope: torch.Tensor | None = None    # q|k|v packed in RoPE tile order (fused RoPE epilogue), layout 1
+    qkv_rope2: torch.Tensor | None = None   # the same in layout 2
 
 
 def kv_block_offsets(kind: str) -> list[int]:
@@ -155,14 +156,18 @@ class VerifyModel:
         self.final_norm = _norm_weight(c.hidden, gen, device)
         self.lm_head = QuantizedLinear.random(c.vocab, c.hidden, gs, generator=gen, device=device)
         # Tile-major copies for the streaming verify matmul (one pass at load
-        # time); q|k|v also in RoPE tile order for the fused RoPE epilogue.
+        # time), in layout 1 (any M) and layout 2 (M <= 4, 16x16x32 MFMA);
+        # q|k|v also in RoPE tile order for the fused RoPE epilogue.
         rope_order = rope_row_order(c.n_heads + 2 * c.n_kv_heads, c.head_dim)
         for L in self.layers:
             for q in (L.qkv, L.o, L.gate, L.up, L.down, L.shared_gate, L.shared_up, L.shared_down):
                 if q is not None:
                     q.pack()
+                    q.pack(layout=2)
             L.qkv_rope = L.qkv.pack(rope_order)
+            L.qkv_rope2 = L.qkv.pack(rope_order, layout=2)
         self.lm_head.pack()
+        self.lm_head.pack(layout=2)
         self.k_cache: list[torch.Tensor] = []
         self.v_cache: list[torch.Tensor] = []
         self.cap = 0
@@ -251,6 +256,10 @@ class VerifyModel:
             _lib.qmv_ex(stream, ws=qws, ws_bytes=qws.numel(), **kw)
 
         fused_rope = M <= 8   # the RoPE epilogue covers up to 8 rows
+        lay = 2 if M <= 4 else 1   # layout 2: the 16x16x32 MFMA form for up to 4 rows
+
+        def W(q):
+            return q.packed_mf16 if lay == 2 else q.packed
 
         for li, L in enumerate(self.layers):
             xin = dict(x=h, x2=L.in_norm, xmode=2)   # input RMSNorm fused into the staging
@@ -258,32 +267,32 @@ class VerifyModel:
                 rope = dict(q_start=q_start, q_lens=ql, q_out=qh, k_cache=self.k_cache[li], v_cache=self.v_cache[li],
                             status=status, L=Lq, Hq=c.n_heads, Hkv=c.n_kv_heads, D=c.head_dim, cap=self.cap,
                             blocked=1, rope_base=c.rope_theta)
-                qmv(st, rope=rope, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv_rope, M=M, N=c.qkv_out, K=H, group_size=gs,
-                    emode=4, packed=1, **xin)
+                qmv(st, rope=rope, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv_rope2 if lay == 2 else L.qkv_rope, M=M,
+                    N=c.qkv_out, K=H, group_size=gs, emode=4, packed=lay, **xin)
             else:
-                qmv(st, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv.packed, y0=qkv, M=M, N=c.qkv_out, K=H, group_size=gs,
-                    emode=0, packed=1, **xin)
+                qmv(st, ss_in=ss_h, eps=c.rms_eps, w0=W(L.qkv), y0=qkv, M=M, N=c.qkv_out, K=H, group_size=gs,
+                    emode=0, packed=lay, **xin)
                 call("mtp_rope_qkv_to_cache_vt", qkv.data_ptr(), q_start.data_ptr(), _lib.ptr(ql), qh.data_ptr(),
                      self.k_cache[li].data_ptr(), self.v_cache[li].data_ptr(), B, Lq, c.n_heads, c.n_kv_heads,
                      c.head_dim, self.cap, ctypes.c_float(c.rope_theta), status.data_ptr(), st)
             call("mtp_ragged_gqa_attn_rows_vt", qh.data_ptr(), self.k_cache[li].data_ptr(),
                  self.v_cache[li].data_ptr(), q_start.data_ptr(), _lib.ptr(ql), attn.data_ptr(), B, c.n_heads,
                  c.n_kv_heads, Lq, c.head_dim, self.cap, ctypes.c_float(scale), aws.data_ptr(), aws.numel(), st)
-            qmv(st, x=attn, w0=L.o.packed, resid=h, y0=h, ss_out=ss_a, M=M, N=H, K=c.n_heads * c.head_dim,
-                group_size=gs, xmode=0, emode=1, packed=1)
+            qmv(st, x=attn, w0=W(L.o), resid=h, y0=h, ss_out=ss_a, M=M, N=H, K=c.n_heads * c.head_dim,
+                group_size=gs, xmode=0, emode=1, packed=lay)
             ss_h = ss_a
             if c.n_experts:
                 self._moe_block(L, h, M, st)
                 ss_h = None
             else:
-                qmv(st, x=h, x2=L.post_norm, ss_in=ss_h, eps=c.rms_eps, w0=L.gate.packed, w1=L.up.packed, y0=act,
-                    y_sums=act_sums, M=M, N=c.ffn, K=H, group_size=gs, xmode=2, emode=3, packed=1)
-                qmv(st, x=act, x_sums=act_sums, w0=L.down.packed, resid=h, y0=h, ss_out=ss_b, M=M, N=H, K=c.ffn,
-                    group_size=gs, xmode=3, emode=1, packed=1)
+                qmv(st, x=h, x2=L.post_norm, ss_in=ss_h, eps=c.rms_eps, w0=W(L.gate), w1=W(L.up), y0=act,
+                    y_sums=act_sums, M=M, N=c.ffn, K=H, group_size=gs, xmode=2, emode=3, packed=lay)
+                qmv(st, x=act, x_sums=act_sums, w0=W(L.down), resid=h, y0=h, ss_out=ss_b, M=M, N=H, K=c.ffn,
+                    group_size=gs, xmode=3, emode=1, packed=lay)
                 ss_h = ss_b
         logits = logits_out if logits_out is not None else torch.empty((M, c.vocab), dtype=torch.float32, device=dev)
-        qmv(st, x=h, x2=self.final_norm, ss_in=ss_h, eps=c.rms_eps, w0=self.lm_head.packed, yf=logits, M=M,
-            N=c.vocab, K=H, group_size=gs, xmode=2, emode=0, packed=1)
+        qmv(st, x=h, x2=self.final_norm, ss_in=ss_h, eps=c.rms_eps, w0=W(self.lm_head), yf=logits, M=M,
+            N=c.vocab, K=H, group_size=gs, xmode=2, emode=0, packed=lay)
         self._status = status
         return logits
 
