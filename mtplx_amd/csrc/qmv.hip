@@ -763,7 +763,7 @@ __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
 #pragma unroll
   for (int u = 0; u < NR; ++u) load_next(ring[u]);   // waves without items reload a valid block; never used
   asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(NR * (PK ? 5 : 6)));
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(NR * ((PK && !MF) ? 5 : 6)));   // loads per ring slot
   if (XM == X_RMSNORM) {
     for (int m = wave; m < M; m += NW) {
       const float v = (p.ss_in && m == wave) ? ss_reduce(p, ssv, lane) : row_inv_rms(p, m, lane);

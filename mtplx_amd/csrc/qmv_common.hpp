@@ -230,13 +230,13 @@ __device__ __forceinline__ void norm_w_prefetch(const QmmParams& p, uint4 (&wpre
   }
 }
 
-// X_PRE: the group sums xs[gl][r] (r < XSW) of the staged groups come from
-// the producer's 32-column sums; a thread's first kSumPre items are fetched
-// with the x loads. Item it = gl * XSW + r.
+// X_PRE: the group sums xs[gl][r] of the staged groups come from the
+// producer's 32-column sums. Items are the (gl, r < M) pairs, it = gl * M + r;
+// a thread's first kSumPre items are fetched with the x loads. Rows M..XSW-1
+// are zeroed separately.
 constexpr int kSumPre = 3;
-__device__ __forceinline__ float2 xsum_item(const QmmParams& p, int it, int XSW, int M, int Q, int kq0) {
-  const int gl = it / XSW, r = it - gl * XSW;
-  if (r >= M) return make_float2(0.f, 0.f);
+__device__ __forceinline__ float2 xsum_item(const QmmParams& p, int it, int M, int Q, int kq0) {
+  const int gl = it / M, r = it - gl * M;
   int qd = kq0 + (gl >> 2);
   if (qd >= Q) qd -= Q;
   const int g = 4 * qd + (gl & 3);
@@ -245,26 +245,29 @@ __device__ __forceinline__ float2 xsum_item(const QmmParams& p, int it, int XSW,
 template <int NW, int XSW>
 __device__ __forceinline__ void xsum_prefetch(const QmmParams& p, float2 (&sv)[kSumPre], int M, int Q, int kq0,
                                               int nslot, int tid) {
-  const int nit = 4 * nslot * XSW;
+  const int nit = 4 * nslot * M;
 #pragma unroll
   for (int j = 0; j < kSumPre; ++j) {
     const int it = tid + j * NW * 64;
-    sv[j] = it < nit ? xsum_item(p, it, XSW, M, Q, kq0) : make_float2(0.f, 0.f);
+    sv[j] = it < nit ? xsum_item(p, it, M, Q, kq0) : make_float2(0.f, 0.f);
   }
 }
 template <int NW, int XSW>
 __device__ __forceinline__ void xsum_finish(const QmmParams& p, float* xs, const float2 (&sv)[kSumPre], int M, int Q,
                                             int kq0, int nslot, int tid) {
-  const int nit = 4 * nslot * XSW;
+  const int nit = 4 * nslot * M;
+  auto put = [&](int it, float2 v) {
+    const int gl = it / M;
+    xs[gl * XSW + (it - gl * M)] = v.x + v.y;
+  };
 #pragma unroll
   for (int j = 0; j < kSumPre; ++j) {
     const int it = tid + j * NW * 64;
-    if (it < nit) xs[it] = sv[j].x + sv[j].y;
+    if (it < nit) put(it, sv[j]);
   }
-  for (int it = tid + kSumPre * NW * 64; it < nit; it += NW * 64) {
-    const float2 v = xsum_item(p, it, XSW, M, Q, kq0);
-    xs[it] = v.x + v.y;
-  }
+  for (int it = tid + kSumPre * NW * 64; it < nit; it += NW * 64) put(it, xsum_item(p, it, M, Q, kq0));
+  for (int idx = tid; idx < nslot * 4 * XSW; idx += NW * 64)
+    if ((idx % XSW) >= M) xs[idx] = 0.f;
 }
 
 // Staging, phase 2 (after the loads have landed and a barrier): the fused
