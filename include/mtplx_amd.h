@@ -173,6 +173,40 @@ typedef struct mtp_qmv_args {
 } mtp_qmv_args;
 int mtp_qmv_affine4_ex(const mtp_qmv_args* args, void* stream);
 
+/* Fused dense decoder layer of the verify step (no single counterpart in the
+ * reference: it runs, as one persistent kernel with grid barriers, the
+ * q|k|v + RoPE (mtplx/verify_qmv.py:1217 for the linears), ragged attention
+ * (mtplx/ragged_attention.py:42-85), o_proj + residual, RMSNorm + gate/up +
+ * SwiGLU and down_proj + residual that mtp_qmv_affine4_ex and
+ * mtp_ragged_gqa_attn_rows_vt run as six kernels). One workgroup per CU.
+ *   qkv:     xmode 2, emode 4 (rope: blocked caches, D = 128), x = h
+ *   o:       xmode 0, emode 1, x = attn_out, resid = h, y0 = h1 (!= h), ss_out
+ *   gate_up: xmode 2, emode 3, x = h1, ss_in = o's ss_out, y_sums, ws (tail split)
+ *   down:    xmode 3, emode 1, x = gate_up's y0, x_sums = its y_sums, resid = h1,
+ *            y0 = any buffer but h1 and act (h itself is fine)
+ * All four matmuls in packed layout 2 (M <= 4, group 64). Attention reads
+ * q_out and the caches of qkv.rope, writes attn_out [B*L, Hq*D] (rows),
+ * scale = softmax scale, attn_ws sized by mtp_attn_vt_workspace_bytes. A
+ * buffer written by a phase may not be read by an earlier phase of the same
+ * call (checked: MTP_ERR_ARG). sync: mtp_verify_layer_sync_bytes() bytes,
+ * 256-byte aligned, zero-filled once, one per stream; its 32-bit word 640 is
+ * set to 1 if a grid-barrier wait gave up (the call's results are then
+ * invalid), which the caller checks after the call. */
+typedef struct mtp_verify_layer_args {
+  mtp_qmv_args qkv;
+  mtp_qmv_args o;
+  mtp_qmv_args gate_up;
+  mtp_qmv_args down;
+  void* attn_out;
+  float attn_scale;
+  void* attn_ws;
+  size_t attn_ws_bytes;
+  void* sync;
+  size_t sync_bytes;
+} mtp_verify_layer_args;
+size_t mtp_verify_layer_sync_bytes(void);
+int mtp_verify_layer(const mtp_verify_layer_args* args, void* stream);
+
 /* ---- Ragged KV cache + attention -----------------------------------------
  * Cache layout [B, Hkv, cap, D] bf16 (mtplx/ragged_kv_cache.py:71).
  * Scatter: cache[b,h,write_start[b]+i,:] = new[b,h,i,:]

@@ -1,0 +1,332 @@
+// Operand-major ragged GQA attention for the verify step: the split and
+// merge bodies, shared by the standalone kernels (attention.hip) and the
+// fused verify layer (layer.hip).
+#pragma once
+
+#include "common.hpp"
+
+#include <stdlib.h>
+
+namespace mtp {
+
+constexpr int kHD = 128;          // head dim
+constexpr int kTileKeys = 32;
+constexpr int kVtStride = 34;     // keys per LDS row (padded against bank conflicts)
+constexpr float kNegBig = -1.0e30f;
+
+struct AttnParams {
+  const uint16_t* q;         // [B, Hq, L, D]
+  const uint16_t* k;         // [B, Hkv, cap, D]
+  const uint16_t* v;
+  const int32_t* q_start;    // [B]
+  const int32_t* q_lens;     // [B] or null (all L)
+  uint16_t* out;             // [B, Hq, L, D]
+  float* part_o;             // [B*Hkv*S][32][D]
+  float* part_ml;            // [B*Hkv*S][32][2]
+  int B, Hq, Hkv, L, cap, S, split_keys;
+  int out_rows;              // 1: out is [B, L, Hq, D] (rows feed the o projection)
+  float scale_log2;          // softmax scale * log2(e)
+};
+
+__device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
+  return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+}
+
+constexpr int kMaxSplits = 256;
+
+// Operand-major KV blocks (the verify step's own cache, kblk_index /
+// vblk_index in common.hpp): every K and V^T MFMA operand of a wave is one
+// 1 KB contiguous load, and V needs no LDS transpose.
+constexpr int kVtWaves = 4;   // waves per workgroup; each takes TPW 32-key tiles
+
+// Unit = (request, kv head, 128*TPW-key split): four waves take 32*TPW keys
+// each and merge in LDS (wave order), so the split partials are 4x fewer than
+// with one wave per split.
+//
+// The body runs one unit with the workgroup's first kVtWaves waves; waves
+// past those (a persistent kernel's larger workgroup) only meet its
+// barriers. ``lds`` holds attn_vt_lds_bytes(). WT: device-coherent partial
+// stores (read on another XCD later in the same kernel).
+constexpr int kVtOS = kHD + 4;   // padded row: lanes of one store hit distinct banks
+constexpr size_t attn_vt_lds_bytes() { return (size_t)kVtWaves * (32 * kVtOS + 64) * sizeof(float); }
+
+template <int TPW, bool WT>
+__device__ __forceinline__ void attn_vt_body(const AttnParams& p, const int unit, unsigned char* lds) {
+  constexpr int kVtWaveKeys = TPW * kTileKeys;
+  constexpr int kVtUnitKeys = kVtWaves * kVtWaveKeys;
+  constexpr int kOS = kVtOS;
+  float* s_o = reinterpret_cast<float*>(lds);   // [kVtWaves][32 * kOS]
+  float* s_m = s_o + kVtWaves * 32 * kOS;       // [kVtWaves][32]
+  float* s_l = s_m + kVtWaves * 32;             // [kVtWaves][32]
+  const int tid = threadIdx.x;
+  const bool act = tid < kVtWaves * 64;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c32 = lane & 31;
+  const int h2 = lane >> 5;
+  const int s = unit % p.S;
+  const int bh = unit / p.S;
+  const int h = bh % p.Hkv;
+  const int b = bh / p.Hkv;
+  const int rep = p.Hq / p.Hkv;
+  const int qs = p.q_start[b];
+  const int L = p.q_lens ? p.q_lens[b] : p.L;
+  int kv_end = qs + L;
+  if (kv_end > p.cap) kv_end = p.cap;
+  const int k0u = s * kVtUnitKeys;
+  float* po = p.part_o + (size_t)unit * 32 * kHD;
+  float* pml = p.part_ml + (size_t)unit * 64;
+  if (k0u >= kv_end) {
+    if (tid < 32) {
+      st_f32<WT>(pml + 2 * tid, kNegBig);
+      st_f32<WT>(pml + 2 * tid + 1, 0.f);
+    }
+    return;   // uniform over the workgroup
+  }
+  const int k0 = k0u + wave * kVtWaveKeys;
+  const int k1 = (k0 + kVtWaveKeys < kv_end) ? k0 + kVtWaveKeys : kv_end;
+
+  const int qcol = c32;
+  const int qr = qcol / p.L;
+  const int qi = qcol - qr * p.L;
+  const bool qvalid = (qr < rep) && (qi < L);
+  const int qbound = qs + qi;
+  f32x16 o[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) o[t] = f32x16{};
+  float m_run = kNegBig;
+  float l_run = 0.f;
+  if (act) {
+    bf16x8 qop[8];
+    {
+      const uint16_t* qrow = p.q + ((((size_t)b * p.Hq + h * rep + (qvalid ? qr : 0)) * p.L + (qvalid ? qi : 0)) * kHD);
+  #pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint4 raw = qvalid ? *reinterpret_cast<const uint4*>(qrow + 64 * h2 + 8 * i) : make_uint4(0, 0, 0, 0);
+        qop[i] = __builtin_bit_cast(bf16x8, raw);
+      }
+    }
+    const uint16_t* kbase = p.k + ((size_t)b * p.Hkv + h) * (size_t)p.cap * kHD;
+    const uint16_t* vbase = p.v + ((size_t)b * p.Hkv + h) * (size_t)p.cap * kHD;
+
+    // All tiles of this wave are loaded before any compute (one round trip).
+    uint4 kr[TPW][8], vr[TPW][8];
+  #pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+      const int kt = k0 + tt * kTileKeys;
+      const bool kin = kt + c32 < k1;
+      const size_t blk = (size_t)((kt < k1 ? kt : k0) >> 5) * 4096 + (size_t)lane * 8;
+  #pragma unroll
+      for (int i = 0; i < 8; ++i)
+        kr[tt][i] = kin ? *reinterpret_cast<const uint4*>(kbase + blk + i * 512) : make_uint4(0, 0, 0, 0);
+  #pragma unroll
+      for (int t = 0; t < 4; ++t)
+  #pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+          vr[tt][2 * t + jj] = *reinterpret_cast<const uint4*>(vbase + blk + (t * 2 + jj) * 512);
+    }
+  #pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+      const int kt = k0 + tt * kTileKeys;
+      if (kt >= k1) break;   // wave-uniform
+      f32x16 st = {};
+  #pragma unroll
+      for (int i = 0; i < 8; ++i)
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kr[tt][i]), qop[i], st, 0, 0, 0);
+      float sv[16];
+      float tmax = kNegBig;
+  #pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kk = kt + 8 * (r >> 2) + 4 * h2 + (r & 3);
+        const bool ok = qvalid && kk < k1 && kk <= qbound;
+        sv[r] = ok ? st[r] * p.scale_log2 : -INFINITY;
+        tmax = fmaxf(tmax, sv[r]);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float m_new = fmaxf(m_run, tmax);
+      const float corr = exp2f(m_run - m_new);
+      m_run = m_new;
+      float psum = 0.f;
+  #pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sv[r] = exp2f(sv[r] - m_new);
+        psum += sv[r];
+      }
+      l_run = l_run * corr + psum;
+  #pragma unroll
+      for (int t = 0; t < 4; ++t)
+  #pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+      if (kt + kTileKeys > k1) {   // keys past the end: zero V so stale cache bits cannot leak in
+  #pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const int kbase_e = kt + 16 * jj + 4 * h2;   // slot e<4: kbase_e+e, e>=4: kbase_e+8+e-4
+          uint32_t msk[4];
+  #pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const int e0 = 2 * w, e1 = 2 * w + 1;
+            const int key0 = kbase_e + (e0 < 4 ? e0 : 8 + e0 - 4);
+            const int key1 = kbase_e + (e1 < 4 ? e1 : 8 + e1 - 4);
+            msk[w] = (key0 < k1 ? 0x0000ffffu : 0u) | (key1 < k1 ? 0xffff0000u : 0u);
+          }
+  #pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            uint4& c = vr[tt][2 * t + jj];
+            c.x &= msk[0];
+            c.y &= msk[1];
+            c.z &= msk[2];
+            c.w &= msk[3];
+          }
+        }
+      }
+      bf16x8 pop[2];
+  #pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        uint32_t pk[4];
+  #pragma unroll
+        for (int t = 0; t < 4; ++t) pk[t] = f2bf2(sv[8 * jj + 2 * t], sv[8 * jj + 2 * t + 1]);
+        pop[jj] = __builtin_bit_cast(bf16x8, pk);
+      }
+  #pragma unroll
+      for (int t = 0; t < 4; ++t)
+  #pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vr[tt][2 * t + jj]), pop[jj],
+                                                          o[t], 0, 0, 0);
+    }
+  }
+
+  // Merge the four waves in LDS, wave order (deterministic).
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (act && h2 == 0) {
+    s_m[wave * 32 + c32] = m_run;
+    s_l[wave * 32 + c32] = l_tot;
+  }
+  __syncthreads();
+  if (act) {
+    float mq = s_m[c32];
+#pragma unroll
+    for (int w = 1; w < kVtWaves; ++w) mq = fmaxf(mq, s_m[w * 32 + c32]);
+    const float sc = exp2f(m_run - mq);
+    float* so_w = s_o + wave * 32 * kOS;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)   // registers 4j..4j+3 are 4 consecutive d
+        *reinterpret_cast<float4*>(&so_w[qcol * kOS + 32 * t + 8 * j + 4 * h2]) =
+            make_float4(o[t][4 * j] * sc, o[t][4 * j + 1] * sc, o[t][4 * j + 2] * sc, o[t][4 * j + 3] * sc);
+  }
+  __syncthreads();
+  if (!act) return;
+  for (int idx = 4 * tid; idx < 32 * kHD; idx += 4 * kVtWaves * 64) {
+    const int so = (idx / kHD) * kOS + (idx % kHD);
+    float4 v = *reinterpret_cast<const float4*>(&s_o[so]);
+#pragma unroll
+    for (int w = 1; w < kVtWaves; ++w) {
+      const float4 a = *reinterpret_cast<const float4*>(&s_o[w * 32 * kOS + so]);
+      v.x += a.x;
+      v.y += a.y;
+      v.z += a.z;
+      v.w += a.w;
+    }
+    if constexpr (WT) {
+      st_f32<WT>(po + idx, v.x);
+      st_f32<WT>(po + idx + 1, v.y);
+      st_f32<WT>(po + idx + 2, v.z);
+      st_f32<WT>(po + idx + 3, v.w);
+    } else {
+      *reinterpret_cast<float4*>(po + idx) = v;
+    }
+  }
+  if (tid < 32) {
+    float M = s_m[tid];
+#pragma unroll
+    for (int w = 1; w < kVtWaves; ++w) M = fmaxf(M, s_m[w * 32 + tid]);
+    float lsum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kVtWaves; ++w) lsum += s_l[w * 32 + tid] * exp2f(s_m[w * 32 + tid] - M);
+    st_f32<WT>(pml + 2 * tid, M);
+    st_f32<WT>(pml + 2 * tid + 1, lsum);
+  }
+}
+
+
+
+// Merge item = (request, kv head, query column), 128 threads each: thread d
+// merges column d over the splits in split order (deterministic). A
+// workgroup of IPW*128 threads takes items item0 .. item0+IPW-1 (those below
+// nitems); ``lds`` holds attn_merge_lds_bytes(IPW).
+constexpr size_t attn_merge_lds_bytes(int ipw) { return (size_t)ipw * (kMaxSplits + 2) * sizeof(float); }
+
+template <int IPW, bool WT>
+__device__ __forceinline__ void attn_merge_body(const AttnParams& p, const int item0, const int nitems,
+                                                unsigned char* lds) {
+  const int sub = threadIdx.x >> 7;
+  const int item = item0 + sub;
+  const bool valid = sub < IPW && item < nitems;
+  float* s_w = reinterpret_cast<float*>(lds) + (valid ? sub : 0) * (kMaxSplits + 2);
+  float* s_red = s_w + kMaxSplits;
+  const int rep = p.Hq / p.Hkv;
+  const int rows = rep * p.L;
+  const int q = (valid ? item : 0) % rows;
+  const int bh = (valid ? item : 0) / rows;
+  const int h = bh % p.Hkv;
+  const int b = bh / p.Hkv;
+  const int d = threadIdx.x & 127;
+  const int L = p.q_lens ? p.q_lens[b] : p.L;
+  const int qr = q / p.L, qi = q - (q / p.L) * p.L;
+  const int kv_end = p.q_start[b] + L;
+  int ns = cdiv(kv_end < p.cap ? kv_end : p.cap, p.split_keys);
+  if (ns > p.S) ns = p.S;
+  const float* ml = p.part_ml + (size_t)bh * p.S * 64 + 2 * q;
+  // max over splits (fixed tree over lanes, one wave)
+  if (valid && d < 64) {
+    float m = kNegBig;
+    for (int s = d; s < ns; s += 64) m = fmaxf(m, ml[(size_t)s * 64]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if (d == 0) s_red[0] = m;
+  }
+  __syncthreads();
+  const float M = s_red[0];
+  if (valid)
+    for (int s = d; s < ns; s += 128) s_w[s] = exp2f(ml[(size_t)s * 64] - M);
+  __syncthreads();
+  if (valid && d == 0) {
+    float lsum = 0.f;
+    for (int s = 0; s < ns; ++s) lsum += ml[(size_t)s * 64 + 1] * s_w[s];
+    s_red[1] = lsum;
+  }
+  const float* po = p.part_o + ((size_t)bh * p.S * 32 + q) * kHD + d;
+  float acc = 0.f;
+  int s = 0;
+  if (!valid) s = ns;
+  for (; s + 4 <= ns; s += 4) {
+    const float o0 = po[(size_t)(s + 0) * 32 * kHD], o1 = po[(size_t)(s + 1) * 32 * kHD];
+    const float o2 = po[(size_t)(s + 2) * 32 * kHD], o3 = po[(size_t)(s + 3) * 32 * kHD];
+    acc += o0 * s_w[s];
+    acc += o1 * s_w[s + 1];
+    acc += o2 * s_w[s + 2];
+    acc += o3 * s_w[s + 3];
+  }
+  for (; s < ns; ++s) acc += po[(size_t)s * 32 * kHD] * s_w[s];
+  __syncthreads();
+  if (!valid) return;
+  const float lsum = s_red[1];
+  const float val = (qi < L && lsum > 0.f) ? acc / lsum : 0.f;
+  const size_t oi = p.out_rows ? ((((size_t)b * p.L + qi) * p.Hq + h * rep + qr) * kHD + d)
+                               : ((((size_t)b * p.Hq + h * rep + qr) * p.L + qi) * kHD + d);
+  st_u16<WT>(p.out + oi, f2bf(val));
+}
+
+
+// Tiles per wave: one (more workgroups, shorter chains) while that keeps the
+// partials to merge within kMaxSplits per (request, kv head), else two.
+inline int attn_vt_plan(int cap, int* S, int* tpw) {
+  const char* env = getenv("MTPLX_AMD_ATTN_TPW");
+  *tpw = (env && atoi(env) == 2) || cdiv(cap, kVtWaves * kTileKeys) > kMaxSplits ? 2 : 1;
+  *S = cdiv(cap, kVtWaves * kTileKeys * *tpw);
+  return (*S <= kMaxSplits) ? MTP_OK : MTP_ERR_UNSUPPORTED;
+}
+
+}  // namespace mtp

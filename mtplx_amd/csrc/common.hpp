@@ -99,4 +99,22 @@ __host__ __device__ __forceinline__ size_t vblk_index(int key, int d) {
   return (size_t)(key >> 5) * 4096 + ((size_t)(t * 2 + jj) * 64 + h2 * 32 + c) * 8 + e;
 }
 
+// Global stores of kernel outputs. WT: device-coherent stores (written
+// through to memory, no fence needed), for outputs that another XCD reads
+// later in the same kernel.
+template <bool WT>
+__device__ __forceinline__ void st_u16(uint16_t* a, uint16_t v) {
+  if constexpr (WT)
+    __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *a = v;
+}
+template <bool WT>
+__device__ __forceinline__ void st_f32(float* a, float v) {
+  if constexpr (WT)
+    __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *a = v;
+}
+
 }  // namespace mtp

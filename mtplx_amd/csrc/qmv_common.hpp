@@ -515,7 +515,7 @@ __device__ __forceinline__ RopeRow rope_row(const QmmParams& p, int r, int d) {
 // ``pre``: this thread's residual value for its first output element, loaded
 // at kernel start (E_RESID with M*32 <= threads), or null. ``rpre``: the same
 // for E_ROPE_QKV (position and rotation of element idx == tid), or null.
-template <int NW, int EM>
+template <int NW, int EM, bool WT = false>
 __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int nb, int M, int row0,
                                              const float* pre = nullptr, const RopeRow* rpre = nullptr) {
   constexpr int NT = NW * 64;
@@ -538,8 +538,8 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int
       if (head < p.rope_Hq + p.rope_Hkv) rope_apply(x1, x2, rr.sn, rr.cs, o1, o2);
       if (!kv) {
         uint16_t* dst = p.q_out + (((size_t)b * p.rope_Hq + head) * p.rope_L + li) * D;
-        dst[d + i] = o1;
-        dst[d + i + half] = o2;
+        st_u16<WT>(dst + d + i, o1);
+        st_u16<WT>(dst + d + i + half, o2);
       } else if (li < len) {
         if (pos < 0 || pos >= p.rope_cap) {
           if (p.status) atomicOr(p.status, 1);
@@ -549,11 +549,11 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int
         const int kvh = head - p.rope_Hq - (is_k ? 0 : p.rope_Hkv);
         uint16_t* base = (is_k ? p.k_cache : p.v_cache) + ((size_t)b * p.rope_Hkv + kvh) * p.rope_cap * D;
         if (p.rope_blocked) {
-          base[is_k ? kblk_index(pos, d + i) : vblk_index(pos, d + i)] = o1;
-          base[is_k ? kblk_index(pos, d + i + half) : vblk_index(pos, d + i + half)] = o2;
+          st_u16<WT>(base + (is_k ? kblk_index(pos, d + i) : vblk_index(pos, d + i)), o1);
+          st_u16<WT>(base + (is_k ? kblk_index(pos, d + i + half) : vblk_index(pos, d + i + half)), o2);
         } else {
-          base[(size_t)pos * D + d + i] = o1;
-          base[(size_t)pos * D + d + i + half] = o2;
+          st_u16<WT>(base + (size_t)pos * D + d + i, o1);
+          st_u16<WT>(base + (size_t)pos * D + d + i + half, o2);
         }
       }
     }
@@ -568,13 +568,13 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int
     const float g = fin[m * 64 + c];
     if (EM == E_DUAL) {
       if (in) {
-        p.y0[o] = f2bf(g);
-        p.y1[o] = f2bf(fin[m * 64 + 32 + c]);
+        st_u16<WT>(p.y0 + o, f2bf(g));
+        st_u16<WT>(p.y1 + o, f2bf(fin[m * 64 + 32 + c]));
       }
     } else if (EM == E_DUAL_SWIGLU) {
       const float gs = round_bf(silu_f(round_bf(g)));
       const float a = in ? round_bf(gs * round_bf(fin[m * 64 + 32 + c])) : 0.f;
-      if (in) p.y0[o] = f2bf(a);
+      if (in) st_u16<WT>(p.y0 + o, f2bf(a));
       fin[m * 64 + c] = a;   // this thread's own slot: the row sums below
     } else {
       float v = g;
@@ -588,9 +588,9 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int
       }
       if (in) {
         if (EM == E_STORE && p.yf)
-          p.yf[o] = round_bf(v);
+          st_f32<WT>(p.yf + o, round_bf(v));
         else
-          p.y0[o] = f2bf(v);
+          st_u16<WT>(p.y0 + o, f2bf(v));
       }
     }
   }
@@ -601,13 +601,13 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int
     if (ss && tid < M) {
       float a = 0.f;
       for (int c = 0; c < 32; ++c) a += fin[tid * 64 + 32 + c];
-      p.ss_out[(size_t)nb * 32 + row0 + tid] = a;
+      st_f32<WT>(p.ss_out + (size_t)nb * 32 + row0 + tid, a);
     }
     if (xsum && tid >= 64 && tid < 64 + M) {   // another wave, in parallel
       const int m = tid - 64;
       float a = 0.f;
       for (int c = 0; c < 32; ++c) a += fin[m * 64 + c];
-      p.y_sums[(size_t)nb * 32 + row0 + m] = a;
+      st_f32<WT>(p.y_sums + (size_t)nb * 32 + row0 + m, a);
     }
   }
 }

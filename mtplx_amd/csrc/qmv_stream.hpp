@@ -1,0 +1,360 @@
+// The resident streaming matmul body for the verify shapes (packed weights,
+// all of x in LDS), shared by the standalone kernel (qmv.hip) and the fused
+// verify layer (layer.hip).
+#pragma once
+
+#include "qmv_common.hpp"
+
+#include <type_traits>
+
+namespace mtp {
+
+// ---------------------------------------------------------------------------
+// Resident streaming kernel (the fast path): all of x is staged into LDS once
+// per workgroup, then every wave walks its flat (tile, quad) item list with a
+// register ring of NR quads advanced by unrolling — no register copies and
+// no data-dependent branches between a load and its use, so the compiler's
+// wait for quad i only covers loads issued before i (the NR-1 quads behind it
+// stay in flight). Lanes whose A-operand row is past M read a zero block in
+// LDS instead of branching.
+//
+// MF (packed layout 2, M <= 4): the quads run on v_mfma_f32_16x16x32_bf16
+// (quad_mma16): half the MFMA cycles of the 32x32x16 form for these 4 rows
+// and a quarter of the group-finish FMAs. Staging and epilogues are shared.
+//
+// The body takes its block index vb and grid size vg as arguments so a
+// persistent kernel can run it as one phase of several. ``pre`` is called
+// once by every thread after the weight ring's first loads are issued and
+// before anything produced by an earlier phase is read (x, its norm
+// statistics and sums): a grid barrier there overlaps the weights' first
+// round trip with the previous phase's tail. With it the epilogue's global
+// stores are device-coherent (WT), so the next phase may read them from
+// another XCD after the barrier.
+struct NoHook {
+  __device__ void operator()() const {}
+};
+
+template <int NW, int R, int XM, int EM, int GSH, bool PK, bool MF = false, typename Hook = NoHook>
+__device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb, const int vg, Hook&& pre) {
+  constexpr bool kPhase = !std::is_same<std::decay_t<Hook>, NoHook>::value;
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int NT = NW * 64;
+  constexpr bool dual = (EM == E_DUAL || EM == E_DUAL_SWIGLU);
+  constexpr int KS = dual ? NW / 2 : NW;
+  constexpr int XSW = 2 * R;
+  constexpr int NR = 3;   // ring depth (deeper rings measured slower)
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar loop control
+  const int kw = wave % KS;
+  const int which = dual ? (wave / KS) : 0;
+  const int M = p.M;
+  const int Q = p.K >> 8;
+  const int G = vg;
+  const NibConsts nc = nib_consts();
+  // Tail split (packed weights only): workgroups from p.tail_first on each
+  // take quads [q_lo, q_lo + q_n) of a leftover tile, one of tail_split
+  // parts; the part that arrives last sums the parts in order and finishes.
+  const bool tail = PK && p.tail_split > 1 && vb >= p.tail_first;
+  int tile0 = vb, part = 0, q_lo = 0, q_n = Q;
+  if (tail) {
+    const int e = vb - p.tail_first;
+    tile0 = p.tail_first + e / p.tail_split;
+    part = e - (e / p.tail_split) * p.tail_split;
+    q_lo = (part * Q) / p.tail_split;
+    q_n = ((part + 1) * Q) / p.tail_split - q_lo;
+  }
+  // A phase's grid can exceed its work (a persistent kernel keeps every CU):
+  // workgroups without a tile only meet the barrier.
+  if (tail ? vb - p.tail_first >= (p.n_blocks - p.tail_first) * p.tail_split : vb >= p.n_blocks) {
+    if constexpr (kPhase) pre();
+    return;
+  }
+
+  uint4* xa = reinterpret_cast<uint4*>(smem);                                  // staged x, xa_index()
+  const int rstride = xa_row_stride(4 * Q);
+  float* xs = reinterpret_cast<float*>(smem + xa_bytes(4 * Q, M));             // [Q*4][XSW]
+  float* red = xs + Q * 4 * XSW;                                               // [NW][M][32]
+  float* fin = red + NW * M * 32;                                              // [M][64]
+  __shared__ float s_inv_rms[32];
+  __shared__ int s_last;
+
+  const int c32 = lane & 31;
+  const int kq = lane >> 5;
+  const uint32_t* W = which ? p.w1 : p.w0;
+  const uint16_t* Sc = which ? p.s1 : p.s0;
+  const uint16_t* Bi = which ? p.b1 : p.b0;
+  const int sgroups = p.K >> (6 + GSH);
+  const int qw = (q_n > kw) ? cdiv(q_n - kw, KS) : 0;
+  const int ntiles = (PK && p.tail_split > 1) ? 1 : cdiv(p.n_blocks - vb, G);
+  const int nitems = ntiles * qw;
+
+  // A operands: lanes of rows >= M repeat row c32 % M (their output rows
+  // are never stored), so every lane reads its quad at immediate offsets.
+  const uint32_t a_lane = (uint32_t)xa_index(kq, c32 % M, M, rstride, 0, 0) * 16;
+  const uint32_t x_lane = (uint32_t)((unsigned char*)xs - smem) + 16 * kq;
+
+  struct QuadRegs {
+    uint4 w[4];
+    uint32_t s[2], b[2];
+    uint32_t s1[MF ? 2 : 1], b1[MF ? 2 : 1];   // MF: the lane's second column (16 + l%16)
+  };
+  // Prefetch iterator: tile j_pf, quad counter t_pf (q = kw + t_pf*KS); the
+  // per-lane row pointers are recomputed only when the tile changes.
+  int j_pf = 0, t_pf = 0, left_pf = nitems;
+  const uint32_t* wrow = nullptr;
+  const uint16_t* srow = nullptr;
+  const uint16_t* brow = nullptr;
+  auto set_rows = [&](int j) {
+    const int nb = tile0 + j * G;
+    if (PK) {
+      // Tile-major packed weights: per (tile, quad) 1152 words — 4 x 256
+      // words of nibbles in load order, then 32 rows x (4 s, 4 b) bf16.
+      wrow = W + (size_t)nb * Q * kPackQuadWords + lane * 4;
+      srow = reinterpret_cast<const uint16_t*>(W + (size_t)nb * Q * kPackQuadWords + 1024 + (MF ? (lane & 15) : c32) * 4);
+      brow = nullptr;
+    } else {
+      const int n = nb * 32 + c32;
+      const int nrow = n < p.N ? n : 0;
+      const int kw0 = qw > 0 ? kw : 0;   // waves without quads read a valid block
+      wrow = W + (size_t)nrow * (p.K >> 3) + kq * 4 + 32 * kw0;
+      srow = Sc + (size_t)nrow * sgroups + (GSH == 0 ? 4 : 2) * kw0;
+      brow = Bi + (size_t)nrow * sgroups + (GSH == 0 ? 4 : 2) * kw0;
+    }
+  };
+  set_rows(0);
+  // Loads the iterator's current item, then advances it (past the end it
+  // keeps re-reading the last item, whose registers are never used).
+  auto load_next = [&](QuadRegs& qr) {
+    if (PK) {
+      const size_t qoff = (size_t)(q_lo + (qw > 0 ? kw + KS * t_pf : 0)) * kPackQuadWords;
+      const uint32_t* wp = wrow + qoff;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) qr.w[u] = *reinterpret_cast<const uint4*>(wp + 256 * u);
+      const uint4 sb = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(srow) + qoff);
+      qr.s[0] = sb.x; qr.s[1] = sb.y;
+      qr.b[0] = sb.z; qr.b[1] = sb.w;
+      if (MF) {
+        const uint4 sb1 = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(srow) + qoff + 64);
+        qr.s1[0] = sb1.x; qr.s1[MF ? 1 : 0] = sb1.y;
+        qr.b1[0] = sb1.z; qr.b1[MF ? 1 : 0] = sb1.w;
+      }
+    } else {
+      const uint32_t* wp = wrow + 32 * KS * t_pf;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) qr.w[u] = *reinterpret_cast<const uint4*>(wp + 8 * u);
+      if (GSH == 0) {
+        const uint2 sv = *reinterpret_cast<const uint2*>(srow + 4 * KS * t_pf);
+        const uint2 bv = *reinterpret_cast<const uint2*>(brow + 4 * KS * t_pf);
+        qr.s[0] = sv.x; qr.s[1] = sv.y;
+        qr.b[0] = bv.x; qr.b[1] = bv.y;
+      } else {
+        qr.s[0] = *reinterpret_cast<const uint32_t*>(srow + 2 * KS * t_pf);
+        qr.b[0] = *reinterpret_cast<const uint32_t*>(brow + 2 * KS * t_pf);
+        qr.s[1] = qr.s[0];
+        qr.b[1] = qr.b[0];
+      }
+    }
+    if (left_pf > 1) {
+      --left_pf;
+      if (++t_pf == qw) {
+        t_pf = 0;
+        set_rows(++j_pf);
+      }
+    }
+  };
+
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  // MF: A row 4m holds x row m, read by lanes with (l%16) = 4m (the other
+  // lanes of each four read a valid row too; their outputs are unused).
+  const int mf_arow = ((lane & 15) >> 2) < M ? ((lane & 15) >> 2) : 0;
+  const uint32_t mf_a0 = (uint32_t)xa_index(0, mf_arow, M, rstride, 0, lane >> 4) * 16;
+  const uint32_t mf_a1 = (uint32_t)xa_index(1, mf_arow, M, rstride, 0, lane >> 4) * 16;
+  const uint32_t mf_x = (uint32_t)((unsigned char*)xs - smem) + 4 * ((lane >> 4) < M ? (lane >> 4) : 0);
+
+  auto compute = [&](const QuadRegs& cr, int t) {
+    const int gq = 4 * (kw + t * KS);
+    float sv[4], cb[4];
+    quad_scales<GSH>(cr.s, cr.b, sv, cb);
+    if constexpr (MF) {
+      float sv1[4], cb1[4];
+      const uint32_t s1w[2] = {cr.s1[0], cr.s1[MF ? 1 : 0]}, b1w[2] = {cr.b1[0], cr.b1[MF ? 1 : 0]};
+      quad_scales<0>(s1w, b1w, sv1, cb1);
+      quad_mma16(smem, mf_a0 + (uint32_t)gq * 64, mf_a1 + (uint32_t)gq * 64, mf_x + (uint32_t)gq * (XSW * 4), XSW,
+                 cr.w, sv, cb, sv1, cb1, nc, acc[0], acc[1]);
+    } else {
+      quad_mma<R>(smem, a_lane + (uint32_t)gq * 64, x_lane + (uint32_t)gq * (XSW * 4), cr.w, sv, cb, nc, acc);
+    }
+  };
+
+  // Residual of this thread's first epilogue element, fetched now so the
+  // epilogue does not wait for it.
+  float pre_resid = 0.f;
+  const bool use_pre = (EM == E_RESID) && (R == 4) && ntiles > 0;
+  if (use_pre && tid < M * 32) {
+    const int col = tile0 * 32 + (tid & 31);
+    if (col < p.N) pre_resid = bf2f(p.resid[(size_t)(tid >> 5) * p.ldy + col]);
+  }
+  // E_ROPE_QKV: the request offsets of this thread's first epilogue element
+  // are fetched now; its rotation is computed after staging.
+  RopeRow rope_pre = {};
+  const bool use_rpre = (EM == E_ROPE_QKV) && ntiles > 0 && tid < M * 16;
+  int rq_start = 0, rq_len = 0;
+  if (use_rpre) {
+    const int b = (tid >> 4) / p.rope_L;
+    rq_start = p.q_start[b];
+    rq_len = p.q_lens ? p.q_lens[b] : p.rope_L;
+  }
+
+  // End of tile j: reduce the K-split waves in LDS (wave order), epilogue.
+  auto finish = [&](int j) {
+    const int nb = tile0 + j * G;
+    const bool valid = nb * 32 + c32 < p.N;
+    __syncthreads();
+    if constexpr (MF) {   // lane l: row l/16, columns l%16 and 16 + l%16
+      const int m = lane >> 4, c = lane & 15;
+      if (m < M) {
+        red[(wave * M + m) * 32 + c] = (nb * 32 + c < p.N) ? acc[0] : 0.f;
+        red[(wave * M + m) * 32 + 16 + c] = (nb * 32 + 16 + c < p.N) ? acc[1] : 0.f;
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int m = 8 * (r >> 2) + 4 * kq + (r & 3);
+        if (m < M) red[(wave * M + m) * 32 + c32] = valid ? acc[r] : 0.f;
+        acc[r] = 0.f;
+      }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < M * 64; idx += NT) {
+      const int m = idx >> 6;
+      const int cc = idx & 63;
+      const int mat = cc >> 5;
+      float v = 0.f;
+      if (!dual && mat == 0) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += red[(w * M + m) * 32 + cc];
+      } else if (dual) {
+#pragma unroll
+        for (int w = 0; w < KS; ++w) v += red[((mat * KS + w) * M + m) * 32 + (cc & 31)];
+      }
+      fin[idx] = v;
+    }
+    __syncthreads();
+    if (tail) {
+      // This part's sums to the workspace (device-coherent stores), then
+      // arrive; the last arrival adds the parts in part order and finishes.
+      const int e = vb - p.tail_first;
+      for (int idx = tid; idx < M * 64; idx += NT)
+        __hip_atomic_store(p.partial + (size_t)e * (M * 64) + idx, fin[idx], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      const int ti = tile0 - p.tail_first;
+      if (tid == 0) {
+        const unsigned old =
+            __hip_atomic_fetch_add(p.counters + ti, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (old == (unsigned)(p.tail_split - 1)) ? 1 : 0;
+      }
+      __syncthreads();
+      if (!s_last) return;
+      const float* p0 = p.partial + (size_t)ti * p.tail_split * (M * 64);
+      for (int idx = tid; idx < M * 64; idx += NT) {
+        float v = 0.f;
+        for (int q = 0; q < p.tail_split; ++q)
+          v += __hip_atomic_load(p0 + (size_t)q * (M * 64) + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        fin[idx] = v;
+      }
+      __syncthreads();
+      qmm_epilogue<NW, EM, kPhase>(p, fin, nb, M, 0);
+      if (tid == 0) __hip_atomic_store(p.counters + ti, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    qmm_epilogue<NW, EM, kPhase>(p, fin, nb, M, 0, (use_pre && j == 0) ? &pre_resid : nullptr,
+                         (use_rpre && j == 0) ? &rope_pre : nullptr);
+  };
+
+  // Prologue: the norm statistics, x straight into LDS, the norm weights
+  // into registers, then all three ring slots, issued back to back. The
+  // wait below is for everything but the ring loads (they are the newest),
+  // so staging x overlaps the weights' first round trip.
+  // As a phase (kPhase), the ring loads come first and ``pre`` runs before
+  // the staging loads, which then wait with everything else.
+  QuadRegs ring[NR];
+  if constexpr (kPhase) {
+#pragma unroll
+    for (int u = 0; u < NR; ++u) load_next(ring[u]);
+    asm volatile("" ::: "memory");
+    pre();
+  }
+  float ssv[kMaxSsLoads];
+  if (XM == X_RMSNORM && p.ss_in && wave < M) ss_prefetch(p, wave, lane, ssv);
+  stage_x_issue<NW>(p, xa, rstride, M, Q, q_lo, q_n, wave, lane);
+  uint4 wpre[kNormPre];
+  if (XM == X_RMSNORM) norm_w_prefetch<NW>(p, wpre, Q, q_lo, q_n, tid);
+  float2 xsv[kSumPre];
+  if (XM == X_PRE) xsum_prefetch<NW, XSW>(p, xsv, M, Q, q_lo, q_n, tid);
+  asm volatile("" ::: "memory");
+  if constexpr (kPhase) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  } else {
+#pragma unroll
+    for (int u = 0; u < NR; ++u) load_next(ring[u]);   // waves without items reload a valid block; never used
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(NR * ((PK && !MF) ? 5 : 6)));   // loads per ring slot
+  }
+  if (XM == X_RMSNORM) {
+    for (int m = wave; m < M; m += NW) {
+      const float v = (p.ss_in && m == wave) ? ss_reduce(p, ssv, lane) : row_inv_rms(p, m, lane);
+      if (lane == 0) s_inv_rms[m] = v;
+    }
+  }
+  __syncthreads();
+  if (XM == X_PRE)
+    xsum_finish<NW, XSW>(p, xs, xsv, M, Q, q_lo, q_n, tid);
+  else
+    stage_x_finish<XM, NW, XSW, PK>(p, xa, rstride, xs, wpre, s_inv_rms, M, Q, q_lo, q_n, tid);
+  __syncthreads();  // staged x visible to every wave
+  if (use_rpre) {
+    const int head = tile0 / (p.rope_D >> 5);
+    const int d = 16 * (tile0 - head * (p.rope_D >> 5)) + (tid & 15);
+    rope_pre = rope_row(p, tid >> 4, d, rq_start, rq_len);
+  }
+
+  // Every wave of the workgroup must reach each tile's barriers: waves with
+  // fewer quads per tile (qw smaller) still finish every tile.
+  if (qw == 0) {
+    for (int j = 0; j < ntiles; ++j) finish(j);
+    return;
+  }
+  // One exit, at the bottom: a break after each step would be merged by the
+  // control-flow structurizer into the latch, and the waitcnt analysis would
+  // then see the ring's newest loads as pending at the loop head and drain
+  // the whole ring there (vmcnt(0)) every iteration. Steps past the end are
+  // skipped by a uniform branch instead.
+  int i = 0, t = 0, j = 0;
+  auto step = [&](const QuadRegs& cur) {
+    if (i < nitems) {
+      compute(cur, t);
+      if (++t == qw) {
+        finish(j);
+        t = 0;
+        ++j;
+      }
+      ++i;
+    }
+  };
+  do {
+#pragma unroll
+    for (int u = 0; u < NR; ++u) {
+      step(ring[u]);
+      load_next(ring[u]);
+    }
+  } while (i < nitems);
+}
+
+}  // namespace mtp

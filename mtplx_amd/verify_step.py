@@ -27,6 +27,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 from dataclasses import dataclass, field
 
 import torch
@@ -171,6 +172,20 @@ class VerifyModel:
         self.k_cache: list[torch.Tensor] = []
         self.v_cache: list[torch.Tensor] = []
         self.cap = 0
+        # One persistent kernel per dense layer for up to 4 rows
+        # (mtp_verify_layer) instead of six kernels; off unless
+        # MTPLX_AMD_FUSED_LAYER=1: its grid barriers (~3 us each under load)
+        # still cost more than the kernel boundaries they replace.
+        self.fused_layer = os.environ.get("MTPLX_AMD_FUSED_LAYER", "0") == "1"
+        self._layer_sync = None
+
+    def layer_sync_error(self) -> bool:
+        """True if a fused layer's grid barrier gave up waiting (that step's
+        results are invalid). Synchronises with the device."""
+        if self._layer_sync is None:
+            return False
+        words = self._layer_sync[: 4 * (_lib.LAYER_SYNC_ERROR_WORD + 1)].view(torch.int32)
+        return bool(words[_lib.LAYER_SYNC_ERROR_WORD].item())
 
     # -- cache ----------------------------------------------------------------
     def allocate_cache(self, batch: int, capacity: int, *, fill_random: bool = True) -> None:
@@ -261,7 +276,32 @@ class VerifyModel:
         def W(q):
             return q.packed_mf16 if lay == 2 else q.packed
 
+        # Dense layers with up to 4 rows run as one persistent kernel each
+        # (mtp_verify_layer): h -> h1 = h + o(attn) -> h = h1 + down(act).
+        fused = self.fused_layer and lay == 2 and not c.n_experts and c.head_dim == 128
+        if fused:
+            h1 = torch.empty_like(h)
+            sync = _lib.WORKSPACES.get(_lib.query("mtp_verify_layer_sync_bytes"), "layer_sync", dev)
+            self._layer_sync = sync
         for li, L in enumerate(self.layers):
+            if fused:
+                rope = dict(q_start=q_start, q_lens=ql, q_out=qh, k_cache=self.k_cache[li], v_cache=self.v_cache[li],
+                            status=status, L=Lq, Hq=c.n_heads, Hkv=c.n_kv_heads, D=c.head_dim, cap=self.cap,
+                            blocked=1, rope_base=c.rope_theta)
+                _lib.verify_layer(
+                    st, rope=rope,
+                    qkv=dict(x=h, x2=L.in_norm, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv_rope2, M=M, N=c.qkv_out, K=H,
+                             group_size=gs, xmode=2, emode=4, packed=2),
+                    o=dict(x=attn, w0=L.o.packed_mf16, resid=h, y0=h1, ss_out=ss_a, M=M, N=H,
+                           K=c.n_heads * c.head_dim, group_size=gs, xmode=0, emode=1, packed=2),
+                    gate_up=dict(x=h1, x2=L.post_norm, ss_in=ss_a, eps=c.rms_eps, w0=L.gate.packed_mf16,
+                                 w1=L.up.packed_mf16, y0=act, y_sums=act_sums, M=M, N=c.ffn, K=H, group_size=gs,
+                                 xmode=2, emode=3, packed=2, ws=qws, ws_bytes=qws.numel()),
+                    down=dict(x=act, x_sums=act_sums, w0=L.down.packed_mf16, resid=h1, y0=h, ss_out=ss_b, M=M, N=H,
+                              K=c.ffn, group_size=gs, xmode=3, emode=1, packed=2),
+                    attn_out=attn, attn_scale=scale, attn_ws=aws, sync=sync)
+                ss_h = ss_b
+                continue
             xin = dict(x=h, x2=L.in_norm, xmode=2)   # input RMSNorm fused into the staging
             if fused_rope:
                 rope = dict(q_start=q_start, q_lens=ql, q_out=qh, k_cache=self.k_cache[li], v_cache=self.v_cache[li],
