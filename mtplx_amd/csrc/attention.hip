@@ -186,9 +186,9 @@ __global__ __launch_bounds__(kVtWaves * 64) void attn_vt_kernel(AttnParams p) {
   attn_vt_body<TPW, false>(p, (int)blockIdx.x, lds);
 }
 
-__global__ __launch_bounds__(128) void attn_merge_kernel(AttnParams p) {
-  __shared__ __align__(16) unsigned char lds[attn_merge_lds_bytes(1)];
-  attn_merge_body<1, false>(p, (int)blockIdx.x, (int)gridDim.x, lds);
+__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(AttnParams p) {
+  __shared__ __align__(16) unsigned char lds[attn_merge_lds_bytes()];
+  attn_merge_body<false>(p, (int)blockIdx.x, lds);
 }
 
 // Split length: ~2048 work units over the whole capacity (ragged rows leave
@@ -334,7 +334,7 @@ static int attn_run(const void* q, const void* k, const void* v, const int32_t* 
   hipLaunchKernelGGL(attn_split_kernel, dim3((unsigned)units), dim3(64), 0, st, p);
   int rc = launch_check(who);
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(B * Hkv * (Hq / Hkv) * L), dim3(128), 0, st, p);
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(B * Hkv * (Hq / Hkv) * L), dim3(kMergeThreads), 0, st, p);
   return launch_check(who);
 }
 
@@ -409,7 +409,7 @@ MTP_API int mtp_ragged_gqa_attn_rows_vt(const void* q, const void* k, const void
     hipLaunchKernelGGL(attn_vt_kernel<2>, dim3((unsigned)units), dim3(kVtWaves * 64), 0, (hipStream_t)stream, p);
   int rc = launch_check(who);
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * Hkv * (Hq / Hkv) * L)), dim3(128), 0,
+  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * Hkv * (Hq / Hkv) * L)), dim3(kMergeThreads), 0,
                      (hipStream_t)stream, p);
   return launch_check(who);
 }

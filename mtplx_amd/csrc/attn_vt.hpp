@@ -252,27 +252,30 @@ __device__ __forceinline__ void attn_vt_body(const AttnParams& p, const int unit
 
 
 
-// Merge item = (request, kv head, query column), 128 threads each: thread d
-// merges column d over the splits in split order (deterministic). A
-// workgroup of IPW*128 threads takes items item0 .. item0+IPW-1 (those below
-// nitems); ``lds`` holds attn_merge_lds_bytes(IPW).
-constexpr size_t attn_merge_lds_bytes(int ipw) { return (size_t)ipw * (kMaxSplits + 2) * sizeof(float); }
+// Merge item = (request, kv head, query column), one per workgroup of
+// kMergeGroups x 128 threads: thread (g, d) sums column d over group g's
+// contiguous share of the splits, issuing all of its loads together (one
+// round trip instead of one per four splits); the groups then add in group
+// order, so the result is deterministic. ``lds`` holds attn_merge_lds_bytes().
+constexpr int kMergeGroups = 4;
+constexpr int kMergeThreads = kMergeGroups * 128;
+constexpr size_t attn_merge_lds_bytes() { return (size_t)(2 * kMaxSplits + 2 + kMergeGroups * 128) * sizeof(float); }
+static_assert(kMaxSplits <= kMergeThreads, "one split per thread in the weight pass");
 
-template <int IPW, bool WT>
-__device__ __forceinline__ void attn_merge_body(const AttnParams& p, const int item0, const int nitems,
-                                                unsigned char* lds) {
-  const int sub = threadIdx.x >> 7;
-  const int item = item0 + sub;
-  const bool valid = sub < IPW && item < nitems;
-  float* s_w = reinterpret_cast<float*>(lds) + (valid ? sub : 0) * (kMaxSplits + 2);
-  float* s_red = s_w + kMaxSplits;
+template <bool WT>
+__device__ __forceinline__ void attn_merge_body(const AttnParams& p, const int item, unsigned char* lds) {
+  float* s_w = reinterpret_cast<float*>(lds);   // [kMaxSplits] split weights
+  float* s_l = s_w + kMaxSplits;                // [kMaxSplits] weighted l of each split
+  float* s_red = s_l + kMaxSplits;              // max, l sum
+  float* s_acc = s_red + 2;                     // [kMergeGroups][128]
+  const int tid = threadIdx.x;
+  const int g = tid >> 7, d = tid & 127;
   const int rep = p.Hq / p.Hkv;
   const int rows = rep * p.L;
-  const int q = (valid ? item : 0) % rows;
-  const int bh = (valid ? item : 0) / rows;
+  const int q = item % rows;
+  const int bh = item / rows;
   const int h = bh % p.Hkv;
   const int b = bh / p.Hkv;
-  const int d = threadIdx.x & 127;
   const int L = p.q_lens ? p.q_lens[b] : p.L;
   const int qr = q / p.L, qi = q - (q / p.L) * p.L;
   const int kv_end = p.q_start[b] + L;
@@ -280,45 +283,54 @@ __device__ __forceinline__ void attn_merge_body(const AttnParams& p, const int i
   if (ns > p.S) ns = p.S;
   const float* ml = p.part_ml + (size_t)bh * p.S * 64 + 2 * q;
   // max over splits (fixed tree over lanes, one wave)
-  if (valid && d < 64) {
+  if (tid < 64) {
     float m = kNegBig;
-    for (int s = d; s < ns; s += 64) m = fmaxf(m, ml[(size_t)s * 64]);
+    for (int s = tid; s < ns; s += 64) m = fmaxf(m, ml[(size_t)s * 64]);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    if (d == 0) s_red[0] = m;
+    if (tid == 0) s_red[0] = m;
   }
   __syncthreads();
   const float M = s_red[0];
-  if (valid)
-    for (int s = d; s < ns; s += 128) s_w[s] = exp2f(ml[(size_t)s * 64] - M);
-  __syncthreads();
-  if (valid && d == 0) {
-    float lsum = 0.f;
-    for (int s = 0; s < ns; ++s) lsum += ml[(size_t)s * 64 + 1] * s_w[s];
-    s_red[1] = lsum;
+  // Split weights (one pass: ns <= kMaxSplits <= kMergeThreads), then the l
+  // sum as a fixed lane-strided tree over wave 0 (deterministic).
+  for (int s = tid; s < ns; s += kMergeThreads) {
+    const float2 mlv = *reinterpret_cast<const float2*>(ml + (size_t)s * 64);
+    const float w = exp2f(mlv.x - M);
+    s_w[s] = w;
+    s_l[s] = mlv.y * w;
   }
+  __syncthreads();
+  if (tid < 64) {
+    float l = 0.f;
+    for (int s = tid; s < ns; s += 64) l += s_l[s];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
+    if (tid == 0) s_red[1] = l;
+  }
+  const int s0 = (g * ns) / kMergeGroups, s1 = ((g + 1) * ns) / kMergeGroups;
   const float* po = p.part_o + ((size_t)bh * p.S * 32 + q) * kHD + d;
   float acc = 0.f;
-  int s = 0;
-  if (!valid) s = ns;
-  for (; s + 4 <= ns; s += 4) {
-    const float o0 = po[(size_t)(s + 0) * 32 * kHD], o1 = po[(size_t)(s + 1) * 32 * kHD];
-    const float o2 = po[(size_t)(s + 2) * 32 * kHD], o3 = po[(size_t)(s + 3) * 32 * kHD];
-    acc += o0 * s_w[s];
-    acc += o1 * s_w[s + 1];
-    acc += o2 * s_w[s + 2];
-    acc += o3 * s_w[s + 3];
+  for (int c = s0; c < s1; c += 16) {
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = (c + i < s1) ? po[(size_t)(c + i) * 32 * kHD] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (c + i < s1) acc += v[i] * s_w[c + i];
   }
-  for (; s < ns; ++s) acc += po[(size_t)s * 32 * kHD] * s_w[s];
+  s_acc[g * 128 + d] = acc;
   __syncthreads();
-  if (!valid) return;
+  if (g != 0) return;
+  float tot = s_acc[d];
+#pragma unroll
+  for (int k = 1; k < kMergeGroups; ++k) tot += s_acc[k * 128 + d];
   const float lsum = s_red[1];
-  const float val = (qi < L && lsum > 0.f) ? acc / lsum : 0.f;
+  const float val = (qi < L && lsum > 0.f) ? tot / lsum : 0.f;
   const size_t oi = p.out_rows ? ((((size_t)b * p.L + qi) * p.Hq + h * rep + qr) * kHD + d)
                                : ((((size_t)b * p.Hq + h * rep + qr) * p.L + qi) * kHD + d);
   st_u16<WT>(p.out + oi, f2bf(val));
 }
-
 
 // Tiles per wave: one (more workgroups, shorter chains) while that keeps the
 // partials to merge within kMaxSplits per (request, kv head), else two.

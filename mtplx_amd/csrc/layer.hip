@@ -29,7 +29,7 @@
 namespace mtp {
 
 constexpr int kLayerWaves = 8;
-constexpr int kMergePerWg = 4;          // merge items per workgroup (128 threads each)
+static_assert(kLayerWaves * 64 == kMergeThreads, "a merge item takes the whole workgroup");
 constexpr unsigned kSpinLimit = 1u << 16;   // barrier polls before giving up (~0.1 s)
 
 // Barrier state words, each on its own 256-byte line: [0] generation,
@@ -101,8 +101,7 @@ __global__ __launch_bounds__(kLayerWaves * 64) void verify_layer_kernel(LayerPar
       attn_vt_body<2, true>(P.attn, u, smem);
   }
   barrier();
-  for (int it = kMergePerWg * vb; it < P.merge_items; it += kMergePerWg * vg)
-    attn_merge_body<kMergePerWg, true>(P.attn, it, P.merge_items, smem);
+  for (int it = vb; it < P.merge_items; it += vg) attn_merge_body<true>(P.attn, it, smem);
   // 4. o_proj + residual; 5. gate/up (+ its leftover tiles split by K);
   // 6. down_proj + residual. Each issues its first weight loads, then waits.
   qmv_stream_body<kLayerWaves, 4, X_PLAIN, E_RESID, 0, true, true>(P.o, vb, vg, barrier);
@@ -247,7 +246,7 @@ MTP_API int mtp_verify_layer(const mtp_verify_layer_args* a, void* stream) {
   P.bar = (uint32_t*)a->sync;
   // LDS: the largest phase (all of x of each matmul, attention's merge area).
   size_t lds = attn_vt_lds_bytes();
-  if (attn_merge_lds_bytes(kMergePerWg) > lds) lds = attn_merge_lds_bytes(kMergePerWg);
+  if (attn_merge_lds_bytes() > lds) lds = attn_merge_lds_bytes();
   const QmmParams* mm[4] = {&P.qkv, &P.o, &P.gu, &P.down};
   for (const QmmParams* q : mm) {
     const size_t l = stream_lds_bytes(q->K >> 8, M, kLayerWaves);
