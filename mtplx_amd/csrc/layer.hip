@@ -91,7 +91,7 @@ __global__ __launch_bounds__(kLayerWaves * 64) void verify_layer_kernel(LayerPar
   auto barrier = [&]() { grid_barrier(P.bar); };
   auto none = []() {};
   // 1. fused RMSNorm + q|k|v + RoPE, q to q_out, K/V into the cache.
-  qmv_stream_body<kLayerWaves, 4, X_RMSNORM, E_ROPE_QKV, 0, true, true>(P.qkv, vb, vg, none);
+  qmv_stream_body<kLayerWaves, 4, X_RMSNORM, E_ROPE_QKV, 0, true, true, 1>(P.qkv, vb, vg, none);
   // 2. attention splits, then 3. their merge.
   barrier();
   for (int u = vb; u < P.attn_units; u += vg) {
@@ -104,10 +104,10 @@ __global__ __launch_bounds__(kLayerWaves * 64) void verify_layer_kernel(LayerPar
   for (int it = vb; it < P.merge_items; it += vg) attn_merge_body<true>(P.attn, it, smem);
   // 4. o_proj + residual; 5. gate/up (+ its leftover tiles split by K);
   // 6. down_proj + residual. Each issues its first weight loads, then waits.
-  qmv_stream_body<kLayerWaves, 4, X_PLAIN, E_RESID, 0, true, true>(P.o, vb, vg, barrier);
-  qmv_stream_body<kLayerWaves, 4, X_RMSNORM, E_DUAL_SWIGLU, 0, true, true>(P.gu, vb, vg, barrier);
-  if (P.has_tail) qmv_stream_body<kLayerWaves, 4, X_RMSNORM, E_DUAL_SWIGLU, 0, true, true>(P.gu_tail, vb, vg, none);
-  qmv_stream_body<kLayerWaves, 4, X_PRE, E_RESID, 0, true, true>(P.down, vb, vg, barrier);
+  qmv_stream_body<kLayerWaves, 4, X_PLAIN, E_RESID, 0, true, true, 1>(P.o, vb, vg, barrier);
+  qmv_stream_body<kLayerWaves, 4, X_RMSNORM, E_DUAL_SWIGLU, 0, true, true, 2>(P.gu, vb, vg, barrier);
+  if (P.has_tail) qmv_stream_body<kLayerWaves, 4, X_RMSNORM, E_DUAL_SWIGLU, 0, true, true, 2>(P.gu_tail, vb, vg, none);
+  qmv_stream_body<kLayerWaves, 4, X_PRE, E_RESID, 0, true, true, 2>(P.down, vb, vg, barrier);
 }
 
 static bool disjoint(const void* a, const void* b) { return a != b; }

@@ -499,10 +499,11 @@ __global__ __launch_bounds__(NW * 64) void qmv_chunked_kernel(QmmParams p) {
   }
 }
 
-template <int NW, int R, int XM, int EM, int GSH, bool PK, bool MF = false>
+template <int NW, int R, int XM, int EM, int GSH, bool PK, bool MF = false, int NRT = 3>
 __global__ __launch_bounds__(NW * 64) void qmv_stream_kernel(QmmParams p) {
-  qmv_stream_body<NW, R, XM, EM, GSH, PK, MF>(p, (int)blockIdx.x, (int)gridDim.x, NoHook{});
+  qmv_stream_body<NW, R, XM, EM, GSH, PK, MF, NRT>(p, (int)blockIdx.x, (int)gridDim.x, NoHook{});
 }
+
 
 // ---------------------------------------------------------------------------
 // Host side: split planning and dispatch.
@@ -626,12 +627,28 @@ static bool tail_launch(K kernel, const Plan& pl, int nt, hipStream_t st, QmmPar
   return true;
 }
 
+// Ring depth of the layout-2 kernels: one slot when a wave takes at most
+// three quads of a tile, else two (graph-timed: o 9.5 -> 8.5 us, q|k|v
+// 11.2 -> 9.8 us, gate/up 24.5 -> 21.9 us against three slots).
+static bool mf_short_ring(const QmmParams& q, int nw, int em) {
+  const int ks = (em == E_DUAL || em == E_DUAL_SWIGLU) ? nw / 2 : nw;
+  return cdiv(q.K >> 8, ks) <= 3;
+}
+
+template <int NW, int XM, int EM, int NRT>
+static void launch_mf(const QmmParams& q, const Plan& pl, hipStream_t st) {
+  if (!(q.tail_ok && tail_launch(qmv_stream_kernel<NW, 4, XM, EM, 0, true, true, NRT>, pl, NW * 64, st, q)))
+    launch_one(qmv_stream_kernel<NW, 4, XM, EM, 0, true, true, NRT>, pl, NW * 64, st, q);
+}
+
 template <int NW, int R, int XM, int EM, int GSH>
 static void launch_rk(const QmmParams& q, const Plan& pl, hipStream_t st) {
   if constexpr (R == 4) {
     if (q.packed == 2) {   // 16x16x32 layout, M <= 4 (checked by the caller)
-      if (!(q.tail_ok && tail_launch(qmv_stream_kernel<NW, 4, XM, EM, 0, true, true>, pl, NW * 64, st, q)))
-        launch_one(qmv_stream_kernel<NW, 4, XM, EM, 0, true, true>, pl, NW * 64, st, q);
+      if (mf_short_ring(q, NW, EM))
+        launch_mf<NW, XM, EM, 1>(q, pl, st);
+      else
+        launch_mf<NW, XM, EM, 2>(q, pl, st);
       return;
     }
   }
@@ -693,10 +710,15 @@ static void launch_x(int xm, int em, const QmmParams& p, const Plan& pl, hipStre
 template <int XM>
 static void launch_rope(const QmmParams& q, const Plan& pl, hipStream_t st) {
   if (q.packed == 2) {
-    if (pl.nw == 8)
-      launch_one(qmv_stream_kernel<8, 4, XM, E_ROPE_QKV, 0, true, true>, pl, 8 * 64, st, q);
+    const bool sh = mf_short_ring(q, pl.nw, E_ROPE_QKV);
+    if (pl.nw == 8 && sh)
+      launch_one(qmv_stream_kernel<8, 4, XM, E_ROPE_QKV, 0, true, true, 1>, pl, 8 * 64, st, q);
+    else if (pl.nw == 8)
+      launch_one(qmv_stream_kernel<8, 4, XM, E_ROPE_QKV, 0, true, true, 2>, pl, 8 * 64, st, q);
+    else if (sh)
+      launch_one(qmv_stream_kernel<4, 4, XM, E_ROPE_QKV, 0, true, true, 1>, pl, 4 * 64, st, q);
     else
-      launch_one(qmv_stream_kernel<4, 4, XM, E_ROPE_QKV, 0, true, true>, pl, 4 * 64, st, q);
+      launch_one(qmv_stream_kernel<4, 4, XM, E_ROPE_QKV, 0, true, true, 2>, pl, 4 * 64, st, q);
   } else if (pl.nw == 8) {
     launch_one(qmv_stream_kernel<8, 4, XM, E_ROPE_QKV, 0, true>, pl, 8 * 64, st, q);
   } else {

@@ -34,7 +34,11 @@ struct NoHook {
   __device__ void operator()() const {}
 };
 
-template <int NW, int R, int XM, int EM, int GSH, bool PK, bool MF = false, typename Hook = NoHook>
+//
+// NRT: depth of the weight ring. Its first fill is a burst of every wave's
+// loads at once, which x staging waits behind, so the best depth follows the
+// quads a wave takes per tile: 1 for <= 3 (q|k|v, o at K = 5120), 2 beyond.
+template <int NW, int R, int XM, int EM, int GSH, bool PK, bool MF = false, int NRT = 3, typename Hook = NoHook>
 __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb, const int vg, Hook&& pre) {
   constexpr bool kPhase = !std::is_same<std::decay_t<Hook>, NoHook>::value;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -42,7 +46,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   constexpr bool dual = (EM == E_DUAL || EM == E_DUAL_SWIGLU);
   constexpr int KS = dual ? NW / 2 : NW;
   constexpr int XSW = 2 * R;
-  constexpr int NR = 3;   // ring depth (deeper rings measured slower)
+  constexpr int NR = NRT;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar loop control
