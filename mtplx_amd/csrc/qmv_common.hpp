@@ -164,17 +164,19 @@ __device__ __forceinline__ uint4 produce_chunk(uint4 raw, uint4 raw2, float inv_
   return o;
 }
 
-// Staged-x layout shared by the streaming kernels. Rows (kq, m), 2M of them:
-// row kq*M + m holds, for every staged 64-group g, the chunks ii = 0..3 of
-// k = 64g + 32kq + 8ii (MFMA step ii of half kq), so one lane's 16 A operands
-// of a quad are 256 contiguous bytes read at immediate offsets. Rows are
-// padded by 16 B against LDS bank conflicts. Group sums: xs[g][2R] fp32.
-__device__ __forceinline__ int xa_row_stride(int ngroups) { return ngroups * 4 + 1; }   // in uint4
+// Staged-x layout shared by the streaming kernels: row m holds the staged
+// k range in natural order, 16-byte chunk c = k / 8 (group g = c / 8, half
+// kq = (c / 4) % 2, MFMA step ii = c % 4), so staging copies 1 KB contiguous
+// runs and a lane's A operands of a quad sit at immediate offsets (64-byte
+// runs 128 bytes apart). Rows are padded by 16 B against LDS bank conflicts.
+// Group sums: xs[g][2R] fp32.
+__device__ __forceinline__ int xa_row_stride(int ngroups) { return ngroups * 8 + 1; }   // in uint4
 __device__ __forceinline__ int xa_index(int kq, int m, int M, int rstride, int g, int ii) {
-  return (kq * M + m) * rstride + g * 4 + ii;
+  (void)M;
+  return m * rstride + g * 8 + kq * 4 + ii;
 }
 __host__ __device__ __forceinline__ size_t xa_bytes(int ngroups, int M) {
-  return (size_t)2 * M * (ngroups * 4 + 1) * 16;
+  return (size_t)M * (ngroups * 8 + 1) * 16;
 }
 
 typedef const __attribute__((address_space(1))) void* gptr_t;
@@ -182,27 +184,24 @@ typedef __attribute__((address_space(3))) void* lptr_t;
 
 // Staging, phase 1: direct-to-LDS loads (no registers) of the raw x chunks of
 // the k-quads kq0, kq0+1, ... (mod Q), nslot of them, into their staged
-// positions. One wave instruction fills 64 consecutive chunks (1 KB) of one
-// staged row.
+// positions. One wave instruction copies 64 consecutive chunks (1 KB) of one
+// row of x.
 template <int NW>
 __device__ __forceinline__ void stage_x_issue(const QmmParams& p, uint4* xa, int rstride, int M, int Q, int kq0,
                                               int nslot, int wave, int lane) {
-  const int rowchunks = 16 * nslot;
+  const int rowchunks = 32 * nslot;
   const int nblk = (rowchunks + 63) >> 6;
-  const int ntask = 2 * M * nblk;
+  const int ntask = M * nblk;
   for (int task = wave; task < ntask; task += NW) {
-    const int row = task / nblk;
-    const int blk = task - row * nblk;
-    const int kq = row >= M ? 1 : 0;
-    const int m = row - kq * M;
+    const int m = task / nblk;
+    const int blk = task - m * nblk;
     const int c = blk * 64 + lane;
     if (c < rowchunks) {
-      const int gl = c >> 2, ii = c & 3;
-      int qd = kq0 + (gl >> 2);
+      int qd = kq0 + (c >> 5);
       if (qd >= Q) qd -= Q;
-      const int k = 64 * (4 * qd + (gl & 3)) + 32 * kq + 8 * ii;
+      const int k = 256 * qd + 8 * (c & 31);
       __builtin_amdgcn_global_load_lds((gptr_t)(p.x + (size_t)m * p.ldx + k),
-                                       (lptr_t)(xa + (size_t)row * rstride + blk * 64), 16, 0, 0);
+                                       (lptr_t)(xa + (size_t)m * rstride + blk * 64), 16, 0, 0);
     }
   }
 }
@@ -430,8 +429,8 @@ __device__ __forceinline__ void quad_mma(const unsigned char* lds, uint32_t a_of
     const uint32_t w1[4] = {w[u + 1].x, w[u + 1].y, w[u + 1].z, w[u + 1].w};
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) {
-      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(lds + a_off + (u * 4 + ii) * 16);
-      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(lds + a_off + ((u + 1) * 4 + ii) * 16);
+      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(lds + a_off + (u * 8 + ii) * 16);
+      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(lds + a_off + ((u + 1) * 8 + ii) * 16);
       G0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, nibbles_to_bf16(w0[ii], nc), G0, 0, 0, 0);
       G1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, nibbles_to_bf16(w1[ii], nc), G1, 0, 0, 0);
     }
@@ -464,8 +463,8 @@ __device__ __forceinline__ void quad_mma16(const unsigned char* lds, uint32_t a0
   typedef float f32x4_t __attribute__((ext_vector_type(4)));
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    const bf16x8 A0 = *reinterpret_cast<const bf16x8*>(lds + a0 + g * 64);
-    const bf16x8 A1 = *reinterpret_cast<const bf16x8*>(lds + a1 + g * 64);
+    const bf16x8 A0 = *reinterpret_cast<const bf16x8*>(lds + a0 + g * 128);
+    const bf16x8 A1 = *reinterpret_cast<const bf16x8*>(lds + a1 + g * 128);
     f32x4_t G0 = {}, G1 = {};
     G0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, nibbles_to_bf16(w[g].x, nc), G0, 0, 0, 0);
     G1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, nibbles_to_bf16(w[g].y, nc), G1, 0, 0, 0);

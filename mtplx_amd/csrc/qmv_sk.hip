@@ -184,7 +184,7 @@ __global__ __launch_bounds__(NW * 64) void qmv_sk_kernel(QmmParams p) {
     float t[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) t[r] = 0.f;
-    quad_mma<R>(smem, a_lane + (uint32_t)gq * 64, x_lane + (uint32_t)gq * (XSW * 4), cr.w, sv, cb, nc, t);
+    quad_mma<R>(smem, a_lane + (uint32_t)gq * 128, x_lane + (uint32_t)gq * (XSW * 4), cr.w, sv, cb, nc, t);
     if (dual && cr.mat) {
 #pragma unroll
       for (int r = 0; r < R; ++r) acc1[r] += t[r];

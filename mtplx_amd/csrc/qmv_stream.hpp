@@ -186,10 +186,10 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
       float sv1[4], cb1[4];
       const uint32_t s1w[2] = {cr.s1[0], cr.s1[MF ? 1 : 0]}, b1w[2] = {cr.b1[0], cr.b1[MF ? 1 : 0]};
       quad_scales<0>(s1w, b1w, sv1, cb1);
-      quad_mma16(smem, mf_a0 + (uint32_t)gq * 64, mf_a1 + (uint32_t)gq * 64, mf_x + (uint32_t)gq * (XSW * 4), XSW,
+      quad_mma16(smem, mf_a0 + (uint32_t)gq * 128, mf_a1 + (uint32_t)gq * 128, mf_x + (uint32_t)gq * (XSW * 4), XSW,
                  cr.w, sv, cb, sv1, cb1, nc, acc[0], acc[1]);
     } else {
-      quad_mma<R>(smem, a_lane + (uint32_t)gq * 64, x_lane + (uint32_t)gq * (XSW * 4), cr.w, sv, cb, nc, acc);
+      quad_mma<R>(smem, a_lane + (uint32_t)gq * 128, x_lane + (uint32_t)gq * (XSW * 4), cr.w, sv, cb, nc, acc);
     }
   };
 
