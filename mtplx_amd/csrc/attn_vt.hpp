@@ -282,6 +282,13 @@ __device__ __forceinline__ void attn_merge_body(const AttnParams& p, const int i
   int ns = cdiv(kv_end < p.cap ? kv_end : p.cap, p.split_keys);
   if (ns > p.S) ns = p.S;
   const float* ml = p.part_ml + (size_t)bh * p.S * 64 + 2 * q;
+  // This thread's partial-O loads go out first: they do not depend on the
+  // split weights, so the max / weight pass below overlaps their round trip.
+  const int s0 = (g * ns) / kMergeGroups, s1 = ((g + 1) * ns) / kMergeGroups;
+  const float* po = p.part_o + ((size_t)bh * p.S * 32 + q) * kHD + d;
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = (s0 + i < s1) ? po[(size_t)(s0 + i) * 32 * kHD] : 0.f;
   // max over splits (fixed tree over lanes, one wave)
   if (tid < 64) {
     float m = kNegBig;
@@ -308,11 +315,11 @@ __device__ __forceinline__ void attn_merge_body(const AttnParams& p, const int i
     for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
     if (tid == 0) s_red[1] = l;
   }
-  const int s0 = (g * ns) / kMergeGroups, s1 = ((g + 1) * ns) / kMergeGroups;
-  const float* po = p.part_o + ((size_t)bh * p.S * 32 + q) * kHD + d;
   float acc = 0.f;
-  for (int c = s0; c < s1; c += 16) {
-    float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (s0 + i < s1) acc += v[i] * s_w[s0 + i];
+  for (int c = s0 + 16; c < s1; c += 16) {   // more than 64 splits
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = (c + i < s1) ? po[(size_t)(c + i) * 32 * kHD] : 0.f;
 #pragma unroll
