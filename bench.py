@@ -24,6 +24,7 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 ROOT = os.path.dirname(os.path.abspath(__file__))
 
 
@@ -183,6 +184,68 @@ def roofline_qmv_cfg1(reps: int = 64, nsets: int = 8) -> dict:
             "frac": round(gbs / HBM_PEAK_GBS, 4), "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": byts}
 
 
+def mfma_qmv(M: int, reps: int = 64, nsets: int = 8) -> dict:
+    """The M >= 16 path (cfg4's ragged batches reach 64 rows, run as 32-row
+    launches): x [M,5120] . W [17408,5120] 4-bit g64, packed layout 1 with
+    R = M/2 accumulator rows, 8 rotating weight sets. All of x does not fit in
+    one workgroup's LDS at these M, so the kernel splits K (each workgroup
+    stages one part of x for a group of tiles; parts meet in the workspace).
+    Reported against the dense bf16 MFMA peak (2.5 PFLOP/s) and against HBM."""
+    import torch
+
+    from mtplx_amd import _lib
+    from mtplx_amd.quant import QuantizedLinear
+
+    N, K, gs = 17408, 5120, 64
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    sets = [QuantizedLinear.random(N, K, gs, generator=gen) for _ in range(nsets)]
+    for q in sets:
+        q.pack()
+    x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    ws = _lib.WORKSPACES.get(_lib.query("mtp_qmv_workspace_bytes", M, N, K, 0), "bench_mfma")
+    st = _lib.stream_handle()
+
+    def launch(q):
+        _lib.qmv_ex(st, x=x, w0=q.packed, y0=y, M=M, N=N, K=K, group_size=gs, xmode=0, emode=0, packed=1, ws=ws,
+                    ws_bytes=ws.numel())
+
+    for q in sets:
+        launch(q)
+    torch.cuda.synchronize()
+    # Graph replays: the launches' host-side set-up is not timed.
+    gs_stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(gs_stream):
+        st = _lib.stream_handle()
+        for q in sets:
+            launch(q)
+        gs_stream.synchronize()
+        with torch.cuda.graph(graph, stream=gs_stream):
+            for q in sets:
+                launch(q)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    rounds = max(1, reps // nsets)
+    with torch.cuda.stream(gs_stream):   # replay() and the events on one stream
+        graph.replay()
+        gs_stream.synchronize()
+        e0.record()
+        for _ in range(rounds):
+            graph.replay()
+        e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / (rounds * nsets)
+    flops = 2.0 * M * N * K
+    tfs = flops / us / 1e6
+    byts = _qmv_bytes(M, N, K, gs)
+    return {"kernel": f"qmv_stream_kernel<NW=4,R={4 if M <= 8 else (8 if M <= 16 else 16)},X_PLAIN,E_STORE,packed> "
+                      "(mtp_qmv_affine4_ex, full K split)",
+            "rows": M, "avg_launch_us": round(us, 3), "achieved_tflops": round(tfs, 1),
+            "frac_mfma_bf16": round(tfs / MFMA_BF16_PEAK_TFLOPS, 4), "achieved_gbs": round(byts / us / 1e3, 1),
+            "frac_hbm": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
 def cpu_baseline(layers: int, timeout_s: int = 300) -> dict | None:
     """Float64 NumPy oracle on a bounded sample, single thread, in a child process."""
     env = dict(os.environ, OMP_NUM_THREADS="1", OPENBLAS_NUM_THREADS="1", MKL_NUM_THREADS="1")
@@ -309,6 +372,8 @@ def main() -> int:
 
     roof = roofline_gate_up(model, B * L)
     roof["cfg1_qmv"] = roofline_qmv_cfg1()
+    roof["m16_qmv"] = mfma_qmv(16)
+    roof["m32_qmv"] = mfma_qmv(32)
     del model
     torch.cuda.empty_cache()
     cpu = None if args.no_cpu_baseline else cpu_baseline(cfg.layers)

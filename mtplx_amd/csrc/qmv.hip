@@ -512,6 +512,7 @@ struct Plan {
   int n_blocks, chunk, nw;
   bool resident;
   size_t lds;
+  int split = 0, xq = 0;   // full K split: parts, quads of x each part stages
 };
 
 static int env_int(const char* name, int dflt) {
@@ -568,6 +569,23 @@ static Plan make_plan(int M, int N, int K) {
   return pl;
 }
 
+// Full K split (packed weights, x too large for LDS): the fewest parts whose
+// share of x fits, its fp32 partials [tiles][parts][M][64], then one arrival
+// counter per tile.
+static int full_split_parts(int M, int K, int nw) {
+  const int Q = K >> 8;
+  for (int S = 2; S <= Q; ++S)
+    if (stream_lds(cdiv(Q, S), M, nw) <= kLdsMax) return S;
+  return 0;
+}
+static size_t full_split_partial_bytes(int M, int N, int K, int nw) {
+  const size_t b = (size_t)cdiv(N, 32) * full_split_parts(M, K, nw) * M * 64 * sizeof(float);
+  return (b + 255) / 256 * 256;
+}
+static size_t full_split_ws_bytes(int M, int N, int K, int nw) {
+  return full_split_partial_bytes(M, N, K, nw) + ((size_t)cdiv(N, 32) * 4 + 255) / 256 * 256;
+}
+
 int device_cus() {
   static thread_local int dev_cached = -1, cus = 0;
   int dev = 0;
@@ -610,6 +628,23 @@ static bool tail_launch(K kernel, const Plan& pl, int nt, hipStream_t st, QmmPar
   const int cus = device_cus();
   const int T = pl.n_blocks;
   const int Q = q.K >> 8;
+  if (pl.split > 1) {
+    // Full K split: as many tile groups as the resident workgroups allow
+    // (each group of pl.split workgroups covers the same tiles).
+    if (pl.lds > 65536) (void)hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                  (int)pl.lds);
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, nt, pl.lds) != hipSuccess || occ < 1) occ = 1;
+    int groups = occ * cus / pl.split;
+    if (groups > T) groups = T;
+    if (groups < 1) groups = 1;
+    q.tail_first = 0;
+    q.tail_split = pl.split;
+    q.full_split = 1;
+    q.xq = pl.xq;
+    hipLaunchKernelGGL(kernel, dim3(groups * pl.split), dim3(nt), pl.lds, st, q);
+    return true;
+  }
   if (T <= cus) return false;
   const int E = T % cus;
   if (E == 0 || cus % E) return false;
@@ -652,7 +687,8 @@ static void launch_rk(const QmmParams& q, const Plan& pl, hipStream_t st) {
       return;
     }
   }
-  if (q.packed && R == 4 && q.tail_ok && tail_launch(qmv_stream_kernel<NW, R, XM, EM, 0, true>, pl, NW * 64, st, q))
+  if (q.packed && (R == 4 || pl.split > 1) && q.tail_ok &&
+      tail_launch(qmv_stream_kernel<NW, R, XM, EM, 0, true>, pl, NW * 64, st, q))
     return;
   if constexpr (XM == X_PRE) {   // packed weights only (checked by the caller)
     launch_one(qmv_stream_kernel<NW, R, XM, EM, 0, true>, pl, NW * 64, st, q);
@@ -842,9 +878,23 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
   }
   Plan pl = make_plan(p.M, p.N, p.K);
   if (p.packed && !pl.resident) {
-    set_error("%s: packed weights need all of x in LDS (M=%d, K=%d too large); use the unpacked layout", who,
-              p.M, p.K);
-    return MTP_ERR_UNSUPPORTED;
+    // All of x does not fit in LDS (M >= 16 at large K): split K into parts
+    // whose share of x does, one part per workgroup over a group of tiles;
+    // the parts meet through the workspace.
+    const int S = full_split_parts(p.M, p.K, pl.nw);
+    const size_t need = full_split_ws_bytes(p.M, p.N, p.K, pl.nw);
+    if (S < 2 || !ws || ws_bytes < need || ((uintptr_t)ws & 255)) {
+      set_error("%s: packed weights with x too large for LDS (M=%d, K=%d) need a 256-B aligned workspace of %zu B "
+                "(mtp_qmv_workspace_bytes)", who, p.M, p.K, need);
+      return ws ? MTP_ERR_WORKSPACE : MTP_ERR_UNSUPPORTED;
+    }
+    pl.split = S;
+    pl.xq = cdiv(p.K >> 8, S);
+    pl.lds = stream_lds(pl.xq, p.M, pl.nw);
+    p.tail_ok = 1;
+    p.partial = reinterpret_cast<float*>(ws);
+    p.counters = reinterpret_cast<uint32_t*>(reinterpret_cast<unsigned char*>(ws) +
+                                             full_split_partial_bytes(p.M, p.N, p.K, pl.nw));
   }
   p.chunk = pl.chunk;
   if (p.gs == 64)
@@ -882,9 +932,18 @@ using namespace mtp;
 MTP_API const char* mtp_last_error(void) { return g_err; }
 
 MTP_API size_t mtp_qmv_workspace_bytes(int M, int N, int K, int dual) {
-  // Only the stream-K kernel (packed weights) uses it: arrival counters plus
-  // fp32 partials of the column tiles shared by two workgroups.
-  return qmv_sk_workspace_bytes(M, N, K, dual);
+  // Packed weights only: the tail split and stream-K (fp32 partials of the
+  // tiles shared by several workgroups, then arrival counters) and, when all
+  // of x does not fit in LDS, the full K split.
+  size_t b = qmv_sk_workspace_bytes(M, N, K, dual);
+  if (M >= 1 && N >= 1 && K >= 256 && K % 256 == 0 && M <= 32) {
+    const Plan pl = make_plan(M, N, K);
+    if (!pl.resident && full_split_parts(M, K, pl.nw) >= 2) {
+      const size_t f = full_split_ws_bytes(M, N, K, pl.nw);
+      if (f > b) b = f;
+    }
+  }
+  return b;
 }
 
 MTP_API int mtp_qmv_affine4(const void* x, const void* w, const void* scales, const void* biases, void* y,

@@ -42,6 +42,10 @@ struct QmmParams {
   int S, gps, n_blocks, nvirt, chunk;
   int packed;              // w0/w1 in the tile-major layout (scales/biases inside)
   int tail_first, tail_split;   // tail split of the per-tile kernel (tail_split > 1)
+  // Full K split (tail_first 0): workgroup vb takes part vb % tail_split of
+  // the tiles vb / tail_split + j * (grid / tail_split), staging only that
+  // part's xq quads of x (used when all of x does not fit in LDS).
+  int full_split, xq;
   int tail_ok;                  // a workspace (partial, counters) is available for it
   // X_PRE input: per 32-column block, per row, sum of x ([K/32][32]).
   const float* x_sums;

@@ -34,6 +34,32 @@ struct NoHook {
   __device__ void operator()() const {}
 };
 
+// Adds the S parts of one tile's fp32 sums [S][M*64] (device-coherent loads)
+// into fin, in part order. A thread's elements of one part are loaded
+// together (at most 8: M*64 <= 8 * threads), so the sum costs S round trips.
+template <int NT>
+__device__ __forceinline__ void sum_parts(const float* p0, int S, int n, float* fin, int tid) {
+  static_assert(NT * 8 >= 32 * 64, "at most 8 elements per thread");
+  float a[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) a[k] = 0.f;
+  for (int q = 0; q < S; ++q) {
+    float l[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int idx = tid + k * NT;
+      l[k] = idx < n ? __hip_atomic_load(p0 + (size_t)q * n + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) a[k] += l[k];
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int idx = tid + k * NT;
+    if (idx < n) fin[idx] = a[k];
+  }
+}
+
 //
 // NRT: depth of the weight ring. Its first fill is a burst of every wave's
 // loads at once, which x staging waits behind, so the best depth follows the
@@ -54,12 +80,15 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   const int which = dual ? (wave / KS) : 0;
   const int M = p.M;
   const int Q = p.K >> 8;
-  const int G = vg;
   const NibConsts nc = nib_consts();
   // Tail split (packed weights only): workgroups from p.tail_first on each
   // take quads [q_lo, q_lo + q_n) of a leftover tile, one of tail_split
   // parts; the part that arrives last sums the parts in order and finishes.
   const bool tail = PK && p.tail_split > 1 && vb >= p.tail_first;
+  const bool full = tail && p.full_split;
+  // Tile stride between a workgroup's tiles: the grid, or the number of tile
+  // groups in the full split.
+  const int G = full ? vg / p.tail_split : vg;
   int tile0 = vb, part = 0, q_lo = 0, q_n = Q;
   if (tail) {
     const int e = vb - p.tail_first;
@@ -75,10 +104,12 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
     return;
   }
 
+  // LDS holds QX quads of x: all of K, or one part's share (full split).
+  const int QX = p.xq > 0 ? p.xq : Q;
   uint4* xa = reinterpret_cast<uint4*>(smem);                                  // staged x, xa_index()
-  const int rstride = xa_row_stride(4 * Q);
-  float* xs = reinterpret_cast<float*>(smem + xa_bytes(4 * Q, M));             // [Q*4][XSW]
-  float* red = xs + Q * 4 * XSW;                                               // [NW][M][32]
+  const int rstride = xa_row_stride(4 * QX);
+  float* xs = reinterpret_cast<float*>(smem + xa_bytes(4 * QX, M));            // [QX*4][XSW]
+  float* red = xs + QX * 4 * XSW;                                              // [NW][M][32]
   float* fin = red + NW * M * 32;                                              // [M][64]
   __shared__ float s_inv_rms[32];
   __shared__ int s_last;
@@ -90,7 +121,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   const uint16_t* Bi = which ? p.b1 : p.b0;
   const int sgroups = p.K >> (6 + GSH);
   const int qw = (q_n > kw) ? cdiv(q_n - kw, KS) : 0;
-  const int ntiles = (PK && p.tail_split > 1) ? 1 : cdiv(p.n_blocks - vb, G);
+  const int ntiles = full ? cdiv(p.n_blocks - tile0, G) : ((PK && p.tail_split > 1) ? 1 : cdiv(p.n_blocks - vb, G));
   const int nitems = ntiles * qw;
 
   // A operands: lanes of rows >= M repeat row c32 % M (their output rows
@@ -252,13 +283,14 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
     if (tail) {
       // This part's sums to the workspace (device-coherent stores), then
       // arrive; the last arrival adds the parts in part order and finishes.
-      const int e = vb - p.tail_first;
+      const int e = (nb - p.tail_first) * p.tail_split + part;   // this tile's part slot
       for (int idx = tid; idx < M * 64; idx += NT)
         __hip_atomic_store(p.partial + (size_t)e * (M * 64) + idx, fin[idx], __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
+      if (full) return;   // arrives for all its tiles at the end (arrive_all)
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      const int ti = tile0 - p.tail_first;
+      const int ti = nb - p.tail_first;
       if (tid == 0) {
         const unsigned old =
             __hip_atomic_fetch_add(p.counters + ti, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -266,13 +298,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
       }
       __syncthreads();
       if (!s_last) return;
-      const float* p0 = p.partial + (size_t)ti * p.tail_split * (M * 64);
-      for (int idx = tid; idx < M * 64; idx += NT) {
-        float v = 0.f;
-        for (int q = 0; q < p.tail_split; ++q)
-          v += __hip_atomic_load(p0 + (size_t)q * (M * 64) + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        fin[idx] = v;
-      }
+      sum_parts<NT>(p.partial + (size_t)ti * p.tail_split * (M * 64), p.tail_split, M * 64, fin, tid);
       __syncthreads();
       qmm_epilogue<NW, EM, kPhase>(p, fin, nb, M, 0);
       if (tid == 0) __hip_atomic_store(p.counters + ti, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -280,6 +306,36 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
     }
     qmm_epilogue<NW, EM, kPhase>(p, fin, nb, M, 0, (use_pre && j == 0) ? &pre_resid : nullptr,
                          (use_rpre && j == 0) ? &rope_pre : nullptr);
+  };
+
+  // Full split: after the last tile, wait once for all the part stores, then
+  // arrive at every tile's counter; for the tiles where this part came last,
+  // add the parts in part order and run the epilogue.
+  __shared__ unsigned char s_lastv[64];
+  auto arrive_all = [&]() {
+    if (!full) return;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int j0 = 0; j0 < ntiles; j0 += 64) {
+      const int jn = ntiles - j0 < 64 ? ntiles - j0 : 64;
+      if (tid < jn) {
+        const int nb = tile0 + (j0 + tid) * G;
+        const unsigned old =
+            __hip_atomic_fetch_add(p.counters + nb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_lastv[tid] = (old == (unsigned)(p.tail_split - 1)) ? 1 : 0;
+      }
+      __syncthreads();
+      for (int jj = 0; jj < jn; ++jj) {
+        if (!s_lastv[jj]) continue;   // the same LDS value for every thread
+        const int nb = tile0 + (j0 + jj) * G;
+        sum_parts<NT>(p.partial + (size_t)nb * p.tail_split * (M * 64), p.tail_split, M * 64, fin, tid);
+        __syncthreads();
+        qmm_epilogue<NW, EM, kPhase>(p, fin, nb, M, 0);
+        if (tid == 0) __hip_atomic_store(p.counters + nb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();   // fin is reused by the next tile
+      }
+      __syncthreads();   // s_lastv is rewritten by the next round
+    }
   };
 
   // Prologue: the norm statistics, x straight into LDS, the norm weights
@@ -333,6 +389,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   // fewer quads per tile (qw smaller) still finish every tile.
   if (qw == 0) {
     for (int j = 0; j < ntiles; ++j) finish(j);
+    arrive_all();
     return;
   }
   // One exit, at the bottom: a break after each step would be merged by the
@@ -359,6 +416,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
       load_next(ring[u]);
     }
   } while (i < nitems);
+  arrive_all();
 }
 
 }  // namespace mtp
