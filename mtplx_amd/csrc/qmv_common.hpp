@@ -348,6 +348,18 @@ __device__ __forceinline__ void stage_x_finish(const QmmParams& p, uint4* xa, in
     if ((idx % XSW) >= M) xs[idx] = 0.f;
 }
 
+// Workgroup barrier for LDS data only. __syncthreads() also releases every
+// global store, which compiles to s_waitcnt vmcnt(0): since loads and stores
+// share that counter, it would drain a weight ring in flight at every tile
+// boundary. This waits for the wave's LDS operations (lgkmcnt(0)) and meets;
+// callers whose global stores must be visible wait for them explicitly.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0); vmcnt and expcnt left at their maxima
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // s_waitcnt immediate for "at most vm vector-memory ops outstanding" (gfx9
 // encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at 15:14).
 __host__ __device__ constexpr int vmcnt_imm(int vm) { return (vm & 0xF) | (0x7 << 4) | (0xF << 8) | ((vm >> 4) << 14); }
@@ -600,7 +612,7 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int
   const bool ss = EM == E_RESID && p.ss_out;
   const bool xsum = EM != E_DUAL && p.y_sums;
   if (ss || xsum) {
-    __syncthreads();
+    lds_barrier();
     if (ss && tid < M) {
       float a = 0.f;
       for (int c = 0; c < 32; ++c) a += fin[tid * 64 + 32 + c];

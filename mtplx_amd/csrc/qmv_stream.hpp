@@ -247,7 +247,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   auto finish = [&](int j) {
     const int nb = tile0 + j * G;
     const bool valid = nb * 32 + c32 < p.N;
-    __syncthreads();
+    lds_barrier();
     if constexpr (MF) {   // lane l: row l/16, columns l%16 and 16 + l%16
       const int m = lane >> 4, c = lane & 15;
       if (m < M) {
@@ -264,7 +264,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
         acc[r] = 0.f;
       }
     }
-    __syncthreads();
+    lds_barrier();
     for (int idx = tid; idx < M * 64; idx += NT) {
       const int m = idx >> 6;
       const int cc = idx & 63;
@@ -279,7 +279,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
       }
       fin[idx] = v;
     }
-    __syncthreads();
+    lds_barrier();
     if (tail) {
       // This part's sums to the workspace (device-coherent stores), then
       // arrive; the last arrival adds the parts in part order and finishes.
@@ -289,17 +289,17 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
                            __HIP_MEMORY_SCOPE_AGENT);
       if (full) return;   // arrives for all its tiles at the end (arrive_all)
       __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
+      lds_barrier();
       const int ti = nb - p.tail_first;
       if (tid == 0) {
         const unsigned old =
             __hip_atomic_fetch_add(p.counters + ti, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = (old == (unsigned)(p.tail_split - 1)) ? 1 : 0;
       }
-      __syncthreads();
+      lds_barrier();
       if (!s_last) return;
       sum_parts<NT>(p.partial + (size_t)ti * p.tail_split * (M * 64), p.tail_split, M * 64, fin, tid);
-      __syncthreads();
+      lds_barrier();
       qmm_epilogue<NW, EM, kPhase>(p, fin, nb, M, 0);
       if (tid == 0) __hip_atomic_store(p.counters + ti, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
@@ -315,7 +315,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   auto arrive_all = [&]() {
     if (!full) return;
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    lds_barrier();
     for (int j0 = 0; j0 < ntiles; j0 += 64) {
       const int jn = ntiles - j0 < 64 ? ntiles - j0 : 64;
       if (tid < jn) {
@@ -324,17 +324,17 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
             __hip_atomic_fetch_add(p.counters + nb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_lastv[tid] = (old == (unsigned)(p.tail_split - 1)) ? 1 : 0;
       }
-      __syncthreads();
+      lds_barrier();
       for (int jj = 0; jj < jn; ++jj) {
         if (!s_lastv[jj]) continue;   // the same LDS value for every thread
         const int nb = tile0 + (j0 + jj) * G;
         sum_parts<NT>(p.partial + (size_t)nb * p.tail_split * (M * 64), p.tail_split, M * 64, fin, tid);
-        __syncthreads();
+        lds_barrier();
         qmm_epilogue<NW, EM, kPhase>(p, fin, nb, M, 0);
         if (tid == 0) __hip_atomic_store(p.counters + nb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();   // fin is reused by the next tile
+        lds_barrier();   // fin is reused by the next tile
       }
-      __syncthreads();   // s_lastv is rewritten by the next round
+      lds_barrier();   // s_lastv is rewritten by the next round
     }
   };
 
@@ -373,12 +373,12 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
       if (lane == 0) s_inv_rms[m] = v;
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (XM == X_PRE)
     xsum_finish<NW, XSW>(p, xs, xsv, M, Q, q_lo, q_n, tid);
   else
     stage_x_finish<XM, NW, XSW, PK>(p, xa, rstride, xs, wpre, s_inv_rms, M, Q, q_lo, q_n, tid);
-  __syncthreads();  // staged x visible to every wave
+  lds_barrier();  // staged x visible to every wave
   if (use_rpre) {
     const int head = tile0 / (p.rope_D >> 5);
     const int d = 16 * (tile0 - head * (p.rope_D >> 5)) + (tid & 15);
