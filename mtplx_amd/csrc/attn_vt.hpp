@@ -257,16 +257,18 @@ __device__ __forceinline__ void attn_vt_body(const AttnParams& p, const int unit
 // contiguous share of the splits, issuing all of its loads together (one
 // round trip instead of one per four splits); the groups then add in group
 // order, so the result is deterministic. ``lds`` holds attn_merge_lds_bytes().
+// Wave 0 writes the weights and the l sum before the body's first barrier:
+// a caller that runs several items in one workgroup puts a barrier between
+// them.
 constexpr int kMergeGroups = 4;
 constexpr int kMergeThreads = kMergeGroups * 128;
-constexpr size_t attn_merge_lds_bytes() { return (size_t)(2 * kMaxSplits + 2 + kMergeGroups * 128) * sizeof(float); }
-static_assert(kMaxSplits <= kMergeThreads, "one split per thread in the weight pass");
+constexpr size_t attn_merge_lds_bytes() { return (size_t)(kMaxSplits + 2 + kMergeGroups * 128) * sizeof(float); }
+static_assert(kMaxSplits % 64 == 0, "wave 0 holds kMaxSplits / 64 splits per lane");
 
 template <bool WT>
 __device__ __forceinline__ void attn_merge_body(const AttnParams& p, const int item, unsigned char* lds) {
   float* s_w = reinterpret_cast<float*>(lds);   // [kMaxSplits] split weights
-  float* s_l = s_w + kMaxSplits;                // [kMaxSplits] weighted l of each split
-  float* s_red = s_l + kMaxSplits;              // max, l sum
+  float* s_red = s_w + kMaxSplits;              // [1]: the l sum
   float* s_acc = s_red + 2;                     // [kMergeGroups][128]
   const int tid = threadIdx.x;
   const int g = tid >> 7, d = tid & 127;
@@ -289,32 +291,36 @@ __device__ __forceinline__ void attn_merge_body(const AttnParams& p, const int i
   float v[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) v[i] = (s0 + i < s1) ? po[(size_t)(s0 + i) * 32 * kHD] : 0.f;
-  // max over splits (fixed tree over lanes, one wave)
+  // Wave 0: each split's (max, l) loaded once into registers (lane s % 64),
+  // the max as a fixed tree over lanes, the split weights to LDS, and the
+  // l sum as a lane-strided fixed tree (deterministic).
   if (tid < 64) {
+    constexpr int kPerLane = kMaxSplits / 64;
+    float2 mlv[kPerLane];
     float m = kNegBig;
-    for (int s = tid; s < ns; s += 64) m = fmaxf(m, ml[(size_t)s * 64]);
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      const int s = tid + 64 * j;
+      mlv[j] = s < ns ? *reinterpret_cast<const float2*>(ml + (size_t)s * 64) : make_float2(kNegBig, 0.f);
+      m = fmaxf(m, mlv[j].x);
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    if (tid == 0) s_red[0] = m;
-  }
-  __syncthreads();
-  const float M = s_red[0];
-  // Split weights (one pass: ns <= kMaxSplits <= kMergeThreads), then the l
-  // sum as a fixed lane-strided tree over wave 0 (deterministic).
-  for (int s = tid; s < ns; s += kMergeThreads) {
-    const float2 mlv = *reinterpret_cast<const float2*>(ml + (size_t)s * 64);
-    const float w = exp2f(mlv.x - M);
-    s_w[s] = w;
-    s_l[s] = mlv.y * w;
-  }
-  __syncthreads();
-  if (tid < 64) {
     float l = 0.f;
-    for (int s = tid; s < ns; s += 64) l += s_l[s];
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      const int s = tid + 64 * j;
+      if (s < ns) {
+        const float w = exp2f(mlv[j].x - m);
+        s_w[s] = w;
+        l += __fmul_rn(mlv[j].y, w);   // the weighted l rounded before the sum
+      }
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
     if (tid == 0) s_red[1] = l;
   }
+  __syncthreads();
   float acc = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i)

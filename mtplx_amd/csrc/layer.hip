@@ -99,9 +99,13 @@ __global__ __launch_bounds__(kLayerWaves * 64) void verify_layer_kernel(LayerPar
       attn_vt_body<1, true>(P.attn, u, smem);
     else
       attn_vt_body<2, true>(P.attn, u, smem);
+    __syncthreads();   // the next unit rewrites the LDS merge area
   }
   barrier();
-  for (int it = vb; it < P.merge_items; it += vg) attn_merge_body<true>(P.attn, it, smem);
+  for (int it = vb; it < P.merge_items; it += vg) {
+    attn_merge_body<true>(P.attn, it, smem);
+    __syncthreads();   // the next item's weights and l sum go to the same LDS
+  }
   // 4. o_proj + residual; 5. gate/up (+ its leftover tiles split by K);
   // 6. down_proj + residual. Each issues its first weight loads, then waits.
   qmv_stream_body<kLayerWaves, 4, X_PLAIN, E_RESID, 0, true, true, 1>(P.o, vb, vg, barrier);
