@@ -119,12 +119,32 @@ def profile_roofline(model, M: int) -> None:
     for _ in range(2):
         for L in model.layers:
             launch(L)
+    _calibration_copy(dev)
+    print("roofline counter workload done", flush=True)
+
+
+def _calibration_copy(dev) -> None:
+    """A 256 MiB device-to-device copy, twice: reads and writes exactly
+    268,435,456 B, so its FETCH_SIZE / WRITE_SIZE readings scale the counters."""
+    import torch
+
     src = torch.ones(64 << 20, dtype=torch.int32, device=dev)
     dst = torch.empty_like(src)
     for _ in range(2):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print("roofline counter workload done", flush=True)
+
+
+def profile_step(model, tokens, q_start, draft_logits, uniforms, sampler) -> None:
+    """The counter workload for every kernel of the step: one eager verify
+    step (one dispatch per kernel and layer, each layer on its own weights),
+    then the calibration copy."""
+    import torch
+
+    model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)
+    torch.cuda.synchronize()
+    _calibration_copy(model.device)
+    print("step counter workload done", flush=True)
 
 
 def _gate_up_launcher(model, M, x, ss, y, ysum):
@@ -320,6 +340,8 @@ def main() -> int:
     ap.add_argument("--profile-roofline", action="store_true",
                     help="only launch the roofline kernel (2 passes over the layers, eager) and a 256 MiB copy, "
                          "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--profile-step", action="store_true",
+                    help="only run one eager verify step and a 256 MiB copy, for rocprofv3 --pmc over every kernel")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the hot path is single-GPU); --gpus {args.gpus} is not supported",
@@ -349,6 +371,9 @@ def main() -> int:
     draft_logits = (torch.randn((B, K, cfg.vocab), device=dev, generator=gen) * 3.0).contiguous()
     uniforms = torch.rand((B, K + 1), device=dev, dtype=torch.float64, generator=gen)
     sampler = SamplerConfig(0.6, 0.95, 20)
+    if args.profile_step:
+        profile_step(model, tokens, q_start, draft_logits, uniforms, sampler)
+        return 0
 
     if args.eager:
         def step():
