@@ -121,12 +121,10 @@ int mtp_pack_affine4_mf16(const void* w, const void* scales, const void* biases,
  * ldx/ldy <= 0 mean K/N.
  * ws/ws_bytes: with packed weights, a workspace of mtp_qmv_workspace_bytes
  * (256-byte aligned, zeroed once before first use and then left to the
- * library; calls sharing one workspace must be stream-ordered). schedule 0:
- * the per-tile kernel, which with a workspace splits the leftover tiles of
- * its last round by K over all CUs (tiles mod CUs must divide the CU count;
- * the parts are summed in a fixed order); schedule 1: the stream-K kernel,
- * which spreads (tile, 256-k) items evenly over all CUs. Without a
- * workspace the per-tile kernel runs unsplit.
+ * library; calls sharing one workspace must be stream-ordered). The per-tile
+ * kernel then splits the leftover tiles of its last round by K over all CUs
+ * (tiles mod CUs must divide the CU count; the parts are summed in a fixed
+ * order). Without a workspace it runs unsplit. schedule must be 0.
  * emode 4 = q|k|v projection with RoPE and the cache write fused into the
  * epilogue (the work of mtp_rope_qkv_to_cache / _vt below, same rounding):
  * rope points at the outputs; y0 is unused; packed weights whose rows are in
@@ -164,7 +162,7 @@ typedef struct mtp_qmv_args {
   void* ws;
   size_t ws_bytes;
   const mtp_rope_out* rope; /* emode 4 only */
-  int schedule;             /* 0 = per-tile, 1 = stream-K (see ws above) */
+  int schedule;             /* must be 0 (the per-tile kernel) */
   /* xmode 3 input sums; y_sums (emode 0, 1, 3, optional): the per-32-column
    * row sums of the stored y0 values as [N/32][32] fp32, in column order -
    * the x_sums of a following xmode 3 call on y0. */
@@ -172,40 +170,6 @@ typedef struct mtp_qmv_args {
   float* y_sums;
 } mtp_qmv_args;
 int mtp_qmv_affine4_ex(const mtp_qmv_args* args, void* stream);
-
-/* Fused dense decoder layer of the verify step (no single counterpart in the
- * reference: it runs, as one persistent kernel with grid barriers, the
- * q|k|v + RoPE (mtplx/verify_qmv.py:1217 for the linears), ragged attention
- * (mtplx/ragged_attention.py:42-85), o_proj + residual, RMSNorm + gate/up +
- * SwiGLU and down_proj + residual that mtp_qmv_affine4_ex and
- * mtp_ragged_gqa_attn_rows_vt run as six kernels). One workgroup per CU.
- *   qkv:     xmode 2, emode 4 (rope: blocked caches, D = 128), x = h
- *   o:       xmode 0, emode 1, x = attn_out, resid = h, y0 = h1 (!= h), ss_out
- *   gate_up: xmode 2, emode 3, x = h1, ss_in = o's ss_out, y_sums, ws (tail split)
- *   down:    xmode 3, emode 1, x = gate_up's y0, x_sums = its y_sums, resid = h1,
- *            y0 = any buffer but h1 and act (h itself is fine)
- * All four matmuls in packed layout 2 (M <= 4, group 64). Attention reads
- * q_out and the caches of qkv.rope, writes attn_out [B*L, Hq*D] (rows),
- * scale = softmax scale, attn_ws sized by mtp_attn_vt_workspace_bytes. A
- * buffer written by a phase may not be read by an earlier phase of the same
- * call (checked: MTP_ERR_ARG). sync: mtp_verify_layer_sync_bytes() bytes,
- * 256-byte aligned, zero-filled once, one per stream; its 32-bit word 640 is
- * set to 1 if a grid-barrier wait gave up (the call's results are then
- * invalid), which the caller checks after the call. */
-typedef struct mtp_verify_layer_args {
-  mtp_qmv_args qkv;
-  mtp_qmv_args o;
-  mtp_qmv_args gate_up;
-  mtp_qmv_args down;
-  void* attn_out;
-  float attn_scale;
-  void* attn_ws;
-  size_t attn_ws_bytes;
-  void* sync;
-  size_t sync_bytes;
-} mtp_verify_layer_args;
-size_t mtp_verify_layer_sync_bytes(void);
-int mtp_verify_layer(const mtp_verify_layer_args* args, void* stream);
 
 /* ---- Ragged KV cache + attention -----------------------------------------
  * Cache layout [B, Hkv, cap, D] bf16 (mtplx/ragged_kv_cache.py:71).
@@ -274,9 +238,12 @@ int mtp_embed_affine4(const int32_t* tokens, const void* w, const void* scales, 
                       int M, int H, int V, int group_size, int32_t* status, void* stream);
 
 /* ---- Expert-sorted MoE -----------------------------------------------------
- * Routing: per token top-k of fp32 router logits (value desc, id asc) and
- * softmax weights renormalised over the k (Qwen-MoE norm_topk_prob). */
-int mtp_moe_route(const float* logits, int T, int E, int top_k, int32_t* ids, float* weights, void* stream);
+ * Routing: per token top-k of fp32 router logits[t * ld + e] (+ skew[e] when
+ * skew != NULL; ld <= 0 means E) in (value desc, id asc) order, and softmax
+ * weights renormalised over the k: softmax over all experts, top-k of the
+ * probabilities, norm_topk_prob (mtplx/models/qwen4_exp.py:1430-1437). */
+int mtp_moe_route(const float* logits, int ld, const float* skew, int T, int E, int top_k, int32_t* ids,
+                  float* weights, void* stream);
 
 /* Stable counting sort of topk_ids int32 [T, top_k] (R = T*top_k <= 8192,
  * E <= 4096): row_map = order // top_k, sorted_ids = flat[order],
@@ -300,10 +267,21 @@ int mtp_gather_qmv_affine4(const void* x, const void* x2, const uint32_t* row_ma
                            int group_size, int xmode, int emode, int rows_per_expert, void* ws, size_t ws_bytes,
                            void* stream);
 
-/* out[t] = bf16(sum_j route_w[t,j] * y_sorted[inv_order[t*k+j]]) (+ shared[t])
- * — unsort and weighted combine (mtplx/models/qwen4_exp.py:1544-1577). */
+/* Expert offsets int32 [E+1] and the active list [1+E] (as mtp_moe_sort
+ * writes them) from ids already sorted ascending, the sorted_indices of the
+ * reference entry points (mtplx/moe_sorted_gather.py:241 gather_qmm_rows,
+ * :288 swiglu_rows, :339 switch_linear); active[0] = -1 flags an id outside
+ * [0, E) or a descent. */
+int mtp_moe_segments(const int32_t* sorted_ids, int R, int E, int32_t* expert_off, int32_t* active, void* stream);
+
+/* The sparse block's tail (mtplx/models/qwen4_exp.py:1438-1445, unsort of
+ * :1544-1577): routed = bf16(sum_j route_w[t,j] * y_sorted[inv_order[t*k+j]]);
+ * sh = bf16(sigmoid(shared_gate[t * gate_ld]) * shared[t]) (shared_gate NULL:
+ * shared[t]; shared NULL: no shared expert); out[t] = bf16(resid[t] +
+ * bf16(routed + sh)) (resid NULL: the block output alone). resid may alias out. */
 int mtp_moe_combine(const void* y_sorted, const uint32_t* inv_order, const float* route_w, const void* shared,
-                    void* out, int T, int top_k, int H, void* stream);
+                    const float* shared_gate, int gate_ld, const void* resid, void* out, int T, int top_k, int H,
+                    void* stream);
 
 /* ---- Exact speculative accept / reject ------------------------------------
  * target_logits fp32 [B*(K+1), V] (row K of each request = bonus row),
@@ -312,11 +290,15 @@ int mtp_moe_combine(const void* y_sorted, const uint32_t* inv_order, const float
  * top-k value desc/id asc, top-p over full-vocab mass, min(1,p/q), residual
  * max(p-q,0) renormalised, Generator.choice = cdf/searchsorted); loop order
  * mtplx/generation.py:15560-15790, bonus :16085-16110. temperature <= 0 is the
- * greedy lane (no uniforms). 1 <= top_k <= 64 on the GPU.
+ * greedy lane (no uniforms). Any top_k >= 0 (0 or >= V: no top-k bound) and
+ * top_p (outside (0, 1): no nucleus); supports wider than 64 ids take the
+ * wide-law kernels. Penalties are applied to the logits beforehand
+ * (mtp_apply_logit_deltas).
  * Outputs: out_tokens int32 [B,K+1] (committed ids, -1 padded), n_accepted
  * int32 [B], accept_probs fp64 [B,K] (-1 = not examined), status int32 [B]
- * (1 = non-finite logits: mtplx/sampling.py:32 NonFiniteLogitsError). */
-size_t mtp_sampler_workspace_bytes(int rows, int V);
+ * (1 = non-finite logits: mtplx/sampling.py:32 NonFiniteLogitsError).
+ * Workspace: mtp_sampler_workspace_bytes(B*(2K+1), V, top_k). */
+size_t mtp_sampler_workspace_bytes(int rows, int V, int top_k);
 int mtp_spec_accept(const float* target_logits, const float* draft_logits, const int32_t* draft_ids,
                     const double* uniforms, int B, int K, int V, double temperature, int top_k, double top_p,
                     int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
@@ -325,10 +307,23 @@ int mtp_spec_accept(const float* target_logits, const float* draft_logits, const
 /* Per-row sparse law (ids ascending, fp64 probs, count) and optionally one
  * draw per row with uniforms[r]: mtplx/sampling.py:259 distribution_from_logits
  * + :342 sample_from_distribution; mtplx/fast_sampling.py:637
- * sparse_distribution_from_mlx_logits. out_ids/out_probs are [rows, top_k]. */
+ * sparse_distribution_from_mlx_logits. out_ids/out_probs are [rows, ld_out],
+ * ld_out >= the support bound (1 when greedy, else min(top_k, V) or V for
+ * top_k = 0); slots past a row's count hold -1 / 0. Workspace:
+ * mtp_sampler_workspace_bytes(rows, V, top_k). */
 int mtp_sample_rows(const float* logits, int rows, int V, double temperature, int top_k, double top_p,
-                    const double* uniforms, int32_t* out_ids, double* out_probs, int32_t* out_count,
+                    const double* uniforms, int32_t* out_ids, double* out_probs, int ld_out, int32_t* out_count,
                     int32_t* sampled, int32_t* status, void* ws, size_t ws_bytes, void* stream);
+
+/* Sparse additive penalties on raw logits, in place, before temperature:
+ * logits[row_ids[i] * ld + token_ids[i]] += -deltas[i] in fp32, the device twin
+ * mtplx/fast_sampling.py:42-81 apply_penalties_mlx of mtplx/sampling.py:212
+ * apply_penalties (delta = frequency * count + presence * (count > 0), or an
+ * overlay value, computed by the caller and cast to fp32). (row, token) pairs
+ * must be unique within a call; an index outside [0, rows) x [0, V) sets
+ * *status (may be NULL) and is skipped. */
+int mtp_apply_logit_deltas(float* logits, long long ld, int rows, int V, const int32_t* row_ids,
+                           const int32_t* token_ids, const float* deltas, int n, int32_t* status, void* stream);
 
 /* Diagnostic with no counterpart in the reference: writes the 64x16 register
  * image of one v_mfma_f32_32x32x16_bf16 on a known operand pattern (tests use

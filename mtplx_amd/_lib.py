@@ -42,16 +42,18 @@ SIGNATURES = {
     "mtp_rope_qkv_to_cache": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _vp]),
     "mtp_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
     "mtp_embed_affine4": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp]),
-    "mtp_sampler_workspace_bytes": (_sz, [_i, _i]),
+    "mtp_sampler_workspace_bytes": (_sz, [_i, _i, _i]),
     "mtp_spec_accept": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
-    "mtp_sample_rows": (_i, [_vp, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mtp_sample_rows": (_i, [_vp, _i, _i, _d, _i, _d, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mtp_apply_logit_deltas": (_i, [_vp, C.c_longlong, _i, _i, _vp, _vp, _vp, _i, _vp, _vp]),
     "mtp_probe_mfma_layout": (_i, [_vp, _vp]),
     "mtp_moe_workspace_bytes": (_sz, [_i, _i, _i]),
     "mtp_moe_sort": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "mtp_gather_qmv_affine4": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
                                     _i, _i, _i, _i, _vp, _sz, _vp]),
-    "mtp_moe_route": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
-    "mtp_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "mtp_moe_route": (_i, [_vp, _i, _vp, _i, _i, _i, _vp, _vp, _vp]),
+    "mtp_moe_segments": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
+    "mtp_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp]),
     "mtp_pack_affine4_bytes": (_sz, [_i, _i]),
     "mtp_pack_affine4": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mtp_pack_affine4_mf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
@@ -59,8 +61,6 @@ SIGNATURES = {
     "mtp_attn_vt_workspace_bytes": (_sz, [_i, _i, _i]),
     "mtp_ragged_gqa_attn_rows_vt": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
     "mtp_rope_qkv_to_cache_vt": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _vp]),
-    "mtp_verify_layer_sync_bytes": (_sz, []),
-    "mtp_verify_layer": (_i, [_vp, _vp]),
 }
 
 
@@ -98,38 +98,6 @@ def qmv_ex(stream, rope: dict | None = None, **fields) -> None:
         r = _fill(RopeOut(), rope)
         a.rope = C.pointer(r)
     call("mtp_qmv_affine4_ex", C.byref(a), stream)
-
-
-class VerifyLayerArgs(C.Structure):
-    """``mtp_verify_layer_args`` of include/mtplx_amd.h (same field order)."""
-
-    _fields_ = [("qkv", QmvArgs), ("o", QmvArgs), ("gate_up", QmvArgs), ("down", QmvArgs), ("attn_out", _vp),
-                ("attn_scale", _f), ("attn_ws", _vp), ("attn_ws_bytes", C.c_size_t), ("sync", _vp),
-                ("sync_bytes", C.c_size_t)]
-
-
-# 32-bit word of the fused layer's sync buffer that a timed-out barrier sets.
-LAYER_SYNC_ERROR_WORD = 640
-
-
-def verify_layer(stream, *, qkv: dict, rope: dict, o: dict, gate_up: dict, down: dict, attn_out, attn_scale: float,
-                 attn_ws, sync) -> None:
-    """Call ``mtp_verify_layer``: the four matmul phases as ``mtp_qmv_args``
-    field dicts (``rope`` for q|k|v), attention output, workspace and sync buffer."""
-    a = VerifyLayerArgs()
-    _fill(a.qkv, qkv)
-    r = _fill(RopeOut(), rope)
-    a.qkv.rope = C.pointer(r)
-    _fill(a.o, o)
-    _fill(a.gate_up, gate_up)
-    _fill(a.down, down)
-    a.attn_out = attn_out.data_ptr()
-    a.attn_scale = attn_scale
-    a.attn_ws = attn_ws.data_ptr()
-    a.attn_ws_bytes = attn_ws.numel() * attn_ws.element_size()
-    a.sync = sync.data_ptr()
-    a.sync_bytes = sync.numel() * sync.element_size()
-    call("mtp_verify_layer", C.byref(a), stream)
 
 
 class MtpError(RuntimeError):

@@ -1,6 +1,5 @@
 // Operand-major ragged GQA attention for the verify step: the split and
-// merge bodies, shared by the standalone kernels (attention.hip) and the
-// fused verify layer (layer.hip).
+// merge bodies of the standalone kernels (attention.hip).
 #pragma once
 
 #include "common.hpp"

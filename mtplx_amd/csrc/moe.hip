@@ -1,15 +1,20 @@
 // Expert-sorted MoE dispatch around the gathered quantized matmul, gfx950.
 //
-//  * mtp_moe_route: per token, top-k of the router logits (value desc, id
-//    asc) and the softmax weights renormalised over the chosen k.
+//  * mtp_moe_route: per token, top-k of the router logits plus an optional
+//    per-expert skew (value desc, id asc) and the softmax weights
+//    renormalised over the chosen k (softmax over all experts, top-k of the
+//    probabilities, renormalised: mtplx/models/qwen4_exp.py:1430-1437).
 //  * mtp_moe_sort: stable counting sort of the flattened top-k expert ids —
 //    the closed form of mtplx/moe_sorted_gather.py:221-238 sort_rows:
 //      order = stable_argsort(flat), inv_order = argsort(order),
 //      row_map = order // top_k, sorted = flat[order]
 //    plus expert row offsets and the compact list of experts that got rows
 //    (the gathered matmul launches one workgroup column per active expert).
-//  * mtp_moe_combine: unsort + route-weighted sum over top_k (+ shared
-//    expert), the caller's tail in mtplx/models/qwen4_exp.py:1544-1577.
+//  * mtp_moe_segments: expert offsets and the active list from ids already
+//    in sorted order (the reference entry points take sorted indices).
+//  * mtp_moe_combine: unsort + route-weighted sum over top_k, plus the
+//    sigmoid-gated shared expert and the residual: the block tail of
+//    mtplx/models/qwen4_exp.py:1438-1445 and :1544-1577.
 #include "common.hpp"
 
 namespace mtp {
@@ -69,11 +74,11 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t* i
 }
 
 // One wave per token: top-k experts and renormalised softmax weights.
-__global__ __launch_bounds__(64) void moe_route_kernel(const float* logits, int E, int top_k, int32_t* ids,
-                                                       float* weights) {
+__global__ __launch_bounds__(64) void moe_route_kernel(const float* logits, long long ld, const float* skew, int E,
+                                                       int top_k, int32_t* ids, float* weights) {
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
-  const float* row = logits + (size_t)t * E;
+  const float* row = logits + (size_t)t * ld;
   __shared__ float s_val[64];
   __shared__ int s_id[64];
   int taken_id = -1;
@@ -83,7 +88,7 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* logits, int 
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     for (int e = lane; e < E; e += 64) {
-      const float v = row[e];
+      const float v = skew ? row[e] + skew[e] : row[e];
       const bool below = (v < taken_val) || (v == taken_val && e > taken_id);
       if (!below) continue;
       if (v > bv || (v == bv && e < bi)) {
@@ -119,18 +124,63 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* logits, int 
   }
 }
 
-// out[t, :] = bf16( sum_j w[t,j] * y_sorted[inv_order[t*k + j], :] (+ shared[t, :]) )
+// routed = bf16(sum_j w[t,j] * y_sorted[inv_order[t*k + j], :]);
+// sh = bf16(sigmoid(gate[t]) * shared[t, :]) (no gate: shared itself);
+// out[t, :] = bf16(resid[t, :] + bf16(routed + sh)) (no resid: the block output).
+// Each stored tensor of the reference chain is rounded where it stores it.
 __global__ void moe_combine_kernel(const uint16_t* y_sorted, const uint32_t* inv_order, const float* w,
-                                   const uint16_t* shared, uint16_t* out, int T, int k, int H) {
+                                   const uint16_t* shared, const float* gate, long long gate_ld,
+                                   const uint16_t* resid, uint16_t* out, int T, int k, int H) {
   const int t = blockIdx.y;
+  const float sg = gate ? 1.0f / (1.0f + __expf(-gate[(size_t)t * gate_ld])) : 1.0f;
   for (int h = blockIdx.x * blockDim.x + threadIdx.x; h < H; h += gridDim.x * blockDim.x) {
     float acc = 0.f;
     for (int j = 0; j < k; ++j) {
       const uint32_t r = inv_order[(size_t)t * k + j];
       acc += w[(size_t)t * k + j] * bf2f(y_sorted[(size_t)r * H + h]);
     }
-    if (shared) acc = round_bf(acc) + bf2f(shared[(size_t)t * H + h]);
-    out[(size_t)t * H + h] = f2bf(acc);
+    float v = round_bf(acc);
+    if (shared) {
+      const float sh = bf2f(shared[(size_t)t * H + h]);
+      v = round_bf(v + (gate ? round_bf(sg * sh) : sh));
+    }
+    if (resid) v = bf2f(resid[(size_t)t * H + h]) + v;
+    out[(size_t)t * H + h] = f2bf(v);
+  }
+}
+
+// Offsets of each expert's rows in ids already sorted ascending, and the
+// active list; active[0] = -1 flags an id outside [0, E) or a descent.
+__global__ __launch_bounds__(kSortThreads) void moe_segments_kernel(const int32_t* sorted_ids, int R, int E,
+                                                                    int32_t* expert_off, int32_t* active) {
+  __shared__ int s_bad;
+  const int tid = threadIdx.x;
+  if (tid == 0) s_bad = 0;
+  __syncthreads();
+  for (int i = tid; i < R; i += kSortThreads) {
+    const int e = sorted_ids[i];
+    if (e < 0 || e >= E || (i > 0 && sorted_ids[i - 1] > e)) s_bad = 1;
+  }
+  __syncthreads();
+  if (s_bad) {
+    if (tid == 0) active[0] = -1;
+    return;
+  }
+  // off[e] = first i with sorted_ids[i] >= e (binary search per expert).
+  for (int e = tid; e <= E; e += kSortThreads) {
+    int lo = 0, hi = R;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (sorted_ids[mid] < e) lo = mid + 1; else hi = mid;
+    }
+    expert_off[e] = lo;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int na = 0;
+    for (int e = 0; e < E; ++e)
+      if (expert_off[e + 1] > expert_off[e]) active[1 + na++] = e;
+    active[0] = na;
   }
 }
 
@@ -165,23 +215,40 @@ MTP_API int mtp_moe_sort(const int32_t* topk_ids, int T, int top_k, int E, uint3
   return launch_check("mtp_moe_sort");
 }
 
-MTP_API int mtp_moe_route(const float* logits, int T, int E, int top_k, int32_t* ids, float* weights, void* stream) {
-  if (!logits || !ids || !weights || T < 1 || E < 1 || top_k < 1 || top_k > 64 || top_k > E) {
-    set_error("mtp_moe_route: bad arguments (1 <= top_k <= min(64, E))");
+MTP_API int mtp_moe_route(const float* logits, int ld, const float* skew, int T, int E, int top_k, int32_t* ids,
+                          float* weights, void* stream) {
+  if (ld <= 0) ld = E;
+  if (!logits || !ids || !weights || T < 1 || E < 1 || ld < E || top_k < 1 || top_k > 64 || top_k > E) {
+    set_error("mtp_moe_route: bad arguments (1 <= top_k <= min(64, E), ld >= E)");
     return MTP_ERR_ARG;
   }
-  hipLaunchKernelGGL(moe_route_kernel, dim3(T), dim3(64), 0, (hipStream_t)stream, logits, E, top_k, ids, weights);
+  hipLaunchKernelGGL(moe_route_kernel, dim3(T), dim3(64), 0, (hipStream_t)stream, logits, (long long)ld, skew, E,
+                     top_k, ids, weights);
   return launch_check("mtp_moe_route");
 }
 
+MTP_API int mtp_moe_segments(const int32_t* sorted_ids, int R, int E, int32_t* expert_off, int32_t* active,
+                             void* stream) {
+  if (!sorted_ids || !expert_off || !active || R < 1 || E < 1) {
+    set_error("mtp_moe_segments: bad arguments");
+    return MTP_ERR_ARG;
+  }
+  hipLaunchKernelGGL(moe_segments_kernel, dim3(1), dim3(kSortThreads), 0, (hipStream_t)stream, sorted_ids, R, E,
+                     expert_off, active);
+  return launch_check("mtp_moe_segments");
+}
+
 MTP_API int mtp_moe_combine(const void* y_sorted, const uint32_t* inv_order, const float* route_w,
-                            const void* shared, void* out, int T, int top_k, int H, void* stream) {
-  if (!y_sorted || !inv_order || !route_w || !out || T < 1 || top_k < 1 || H < 1) {
+                            const void* shared, const float* shared_gate, int gate_ld, const void* resid, void* out,
+                            int T, int top_k, int H, void* stream) {
+  if (!y_sorted || !inv_order || !route_w || !out || T < 1 || top_k < 1 || H < 1 ||
+      (shared_gate && (!shared || gate_ld < 1))) {
     set_error("mtp_moe_combine: bad arguments");
     return MTP_ERR_ARG;
   }
   dim3 grid(cdiv(H, 256), T);
   hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t*)y_sorted,
-                     inv_order, route_w, (const uint16_t*)shared, (uint16_t*)out, T, top_k, H);
+                     inv_order, route_w, (const uint16_t*)shared, shared_gate, (long long)gate_ld,
+                     (const uint16_t*)resid, (uint16_t*)out, T, top_k, H);
   return launch_check("mtp_moe_combine");
 }

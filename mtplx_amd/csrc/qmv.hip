@@ -18,8 +18,7 @@
 //  * A workgroup owns one 32-column tile; its waves split K by quads (256 k)
 //    and meet in LDS in wave order (deterministic). Weights stream either in
 //    the reference layout or in the tile-major packed layout (1 KB contiguous
-//    per wave load); the packed layout also has a stream-K kernel
-//    (qmv_sk.hip) that balances (tile, quad) items over all CUs.
+//    per wave load).
 //  * Activations are staged once per workgroup into LDS in the MFMA A-operand
 //    order, with optional fused producers: SwiGLU (silu(gate)*up) or RMSNorm.
 #include "qmv_args.hpp"
@@ -857,24 +856,20 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
       launch_rope<X_PLAIN>(p, pl, st);
     return launch_check(who);
   }
+  if (schedule != 0) {
+    set_error("%s: schedule %d unsupported (0 = the per-tile kernel)", who, schedule);
+    return MTP_ERR_UNSUPPORTED;
+  }
   if (p.packed && ws) {
-    const size_t need = qmv_sk_workspace_bytes(p.M, p.N, p.K, em >= E_DUAL);
+    const size_t need = tail_workspace_bytes(p.M, p.N);
     if (ws_bytes < need || ((uintptr_t)ws & 255)) {
       set_error("%s: workspace of %zu B (256-B aligned) needed, got %zu B", who, need, ws_bytes);
       return MTP_ERR_WORKSPACE;
     }
-    if (schedule == 1 && p.packed == 1) {
-      // Stream-K over all CUs; shapes whose staged x does not fit its LDS
-      // plan use the per-tile kernel below.
-      const int rc = qmv_sk_launch(xm, em, p, ws, ws_bytes, st);
-      if (rc == MTP_OK) return launch_check(who);
-      if (rc != MTP_ERR_UNSUPPORTED) return rc;
-    } else if (em != E_ROPE_QKV) {
-      // Per-tile kernel with its leftover tiles split over all CUs.
-      p.tail_ok = 1;
-      p.partial = reinterpret_cast<float*>(ws);
-      p.counters = reinterpret_cast<uint32_t*>(reinterpret_cast<unsigned char*>(ws) + sk_counter_offset(device_cus()));
-    }
+    // Per-tile kernel with its leftover tiles split over all CUs.
+    p.tail_ok = 1;
+    p.partial = reinterpret_cast<float*>(ws);
+    p.counters = reinterpret_cast<uint32_t*>(reinterpret_cast<unsigned char*>(ws) + tail_counter_offset(device_cus()));
   }
   Plan pl = make_plan(p.M, p.N, p.K);
   if (p.packed && !pl.resident) {
@@ -932,10 +927,11 @@ using namespace mtp;
 MTP_API const char* mtp_last_error(void) { return g_err; }
 
 MTP_API size_t mtp_qmv_workspace_bytes(int M, int N, int K, int dual) {
-  // Packed weights only: the tail split and stream-K (fp32 partials of the
-  // tiles shared by several workgroups, then arrival counters) and, when all
-  // of x does not fit in LDS, the full K split.
-  size_t b = qmv_sk_workspace_bytes(M, N, K, dual);
+  // Packed weights only: the tail split (fp32 partials of the tiles shared by
+  // several workgroups, then arrival counters) and, when all of x does not
+  // fit in LDS, the full K split.
+  (void)dual;
+  size_t b = tail_workspace_bytes(M, N);
   if (M >= 1 && N >= 1 && K >= 256 && K % 256 == 0 && M <= 32) {
     const Plan pl = make_plan(M, N, K);
     if (!pl.resident && full_split_parts(M, K, pl.nw) >= 2) {

@@ -1,5 +1,5 @@
 // Argument blocks of the streaming-matmul C ABI (the same layout as
-// include/mtplx_amd.h), shared by qmv.hip and layer.hip.
+// include/mtplx_amd.h), read by qmv.hip.
 #pragma once
 
 #include "qmv_common.hpp"

@@ -1,4 +1,4 @@
-// Shared pieces of the 4-bit verify matmul kernels (qmv.hip, qmv_sk.hip):
+// Shared pieces of the 4-bit verify matmul kernels (qmv.hip, qmm_mfma.hip):
 // launch parameters, the nibble -> bf16 operand conversion, the fused x
 // producers and the output epilogues.
 #pragma once
@@ -627,12 +627,15 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int
   }
 }
 
-// Stream-K launch over tile-major packed weights (qmv_sk.hip). Returns
-// MTP_ERR_UNSUPPORTED when the shape does not fit its LDS plan (the caller
-// then uses the per-tile kernel).
-int qmv_sk_launch(int xm, int em, const QmmParams& p, void* ws, size_t ws_bytes, hipStream_t st);
-size_t qmv_sk_workspace_bytes(int M, int N, int K, int dual);
-size_t sk_counter_offset(int G);   // workspace: fp32 partials first, then arrival counters
 int device_cus();
+
+// Tail-split workspace: fp32 partials of up to 8 rows x 64 values for two
+// parts per CU, then one self-resetting arrival counter per 32-column tile.
+constexpr int kTailMaxRows = 8;
+inline size_t tail_counter_offset(int cus) { return (size_t)2 * cus * kTailMaxRows * 64 * sizeof(float); }
+inline size_t tail_workspace_bytes(int M, int N) {
+  if (M < 1 || N < 1) return 0;
+  return tail_counter_offset(device_cus()) + ((size_t)cdiv(N, 32) * 4 + 255) / 256 * 256;
+}
 
 }  // namespace mtp

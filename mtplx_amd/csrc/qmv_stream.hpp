@@ -1,6 +1,6 @@
 // The resident streaming matmul body for the verify shapes (packed weights,
-// all of x in LDS), shared by the standalone kernel (qmv.hip) and the fused
-// verify layer (layer.hip).
+// all of x in LDS), run by the standalone kernel (qmv.hip); written as a body
+// with a pre-read hook so a persistent kernel can run it as one phase.
 #pragma once
 
 #include "qmv_common.hpp"

@@ -26,6 +26,16 @@
 //     with the per-candidate work spread over lanes; wave 0 then runs the
 //     accept loop. (Vocabularies over 64 chunks use accept_finish, one wave
 //     per request building the laws in turn.)
+// Laws whose support may exceed 64 ids (top_k = 0 or > 64: pure nucleus, or
+// no truncation at all) take the wide path: one 1024-thread workgroup per row
+// finds the support's cut by a radix descent over the logits' order-preserving
+// bits (four 8-bit passes of per-digit counts and probability mass, the mass
+// in 2^-62 fixed point so integer atomics keep it exact and order-free),
+// resolves the cut inside the final tie group by id, and writes the support in
+// id order with a block scan. The accept loop and draws then run over those
+// laws with binary-searched lookups and block-wide scans.
+// Penalties (presence/frequency, steering overlays) are sparse fp32 deltas
+// added to the raw logits before any of this (mtp_apply_logit_deltas).
 // Deterministic: fixed reduction trees, no float atomics.
 #include "common.hpp"
 
@@ -783,10 +793,12 @@ static size_t accept_laws_lds(int K, int nwv) {
 }
 
 // One wave per row: sparse law of the row (ids ascending) and optionally a draw.
+// out_ids / out_probs rows are ld_out apart; slots past the support hold -1 / 0.
 __global__ __launch_bounds__(64) void row_laws(const ChunkPart* __restrict__ parts, int n_chunks, int ksel,
                                                int greedy, double temp, double top_p,
                                                const double* __restrict__ uniforms, int32_t* __restrict__ out_ids,
-                                               double* __restrict__ out_probs, int32_t* __restrict__ out_count,
+                                               double* __restrict__ out_probs, int ld_out,
+                                               int32_t* __restrict__ out_count,
                                                int32_t* __restrict__ sampled, int32_t* __restrict__ status) {
   const int r = blockIdx.x;
   __shared__ RowLaw s_p;
@@ -803,9 +815,9 @@ __global__ __launch_bounds__(64) void row_laws(const ChunkPart* __restrict__ par
     if (out_count) out_count[r] = s_p.n;
   }
   if (out_ids)
-    for (int i = lane; i < ksel; i += 64) {
-      out_ids[(size_t)r * ksel + i] = i < s_p.n ? s_p.ids[i] : -1;
-      out_probs[(size_t)r * ksel + i] = i < s_p.n ? s_p.probs[i] : 0.0;
+    for (int i = lane; i < ld_out; i += 64) {
+      out_ids[(size_t)r * ld_out + i] = i < s_p.n ? s_p.ids[i] : -1;
+      out_probs[(size_t)r * ld_out + i] = i < s_p.n ? s_p.probs[i] : 0.0;
     }
   if (sampled) {
     const int tok = s_p.nonfinite ? -1 : law_choice_wave(s_p.ids, s_p.probs, s_p.n, uniforms[r]);
@@ -813,33 +825,489 @@ __global__ __launch_bounds__(64) void row_laws(const ChunkPart* __restrict__ par
   }
 }
 
-static int sampler_plan(int V, int top_k, double temperature, int* ksel, int* greedy, int* n_chunks,
-                        const char* who) {
+// k_eff: the top-k bound of mtplx/sampling.py:176 (0 < top_k < V, else no
+// bound = V). Laws with k_eff <= 64 take the narrow path (ksel = k_eff keys
+// per chunk); wider ones the wide path (ksel = 1: the argmax only).
+struct SamplerPlan {
+  int ksel, greedy, n_chunks, k_eff, wide;
+};
+
+static int sampler_plan(int V, int top_k, double temperature, SamplerPlan* pl, const char* who) {
   if (V < 1) {
     set_error("%s: vocabulary size %d < 1", who, V);
     return MTP_ERR_ARG;
   }
-  *greedy = !(temperature > 0.0);
-  if (*greedy) {
-    *ksel = 1;
-  } else {
-    if (top_k < 1 || top_k > kMaxTopK) {
-      set_error("%s: top_k=%d unsupported on the GPU law (1..%d)", who, top_k, kMaxTopK);
-      return MTP_ERR_UNSUPPORTED;
-    }
-    *ksel = top_k < V ? top_k : V;
+  if (top_k < 0) {
+    set_error("%s: top_k=%d < 0", who, top_k);
+    return MTP_ERR_ARG;
   }
-  *n_chunks = cdiv(V, kChunk);
+  pl->greedy = !(temperature > 0.0);
+  pl->k_eff = (top_k > 0 && top_k < V) ? top_k : V;
+  pl->wide = !pl->greedy && pl->k_eff > kMaxTopK;
+  pl->ksel = pl->greedy ? 1 : (pl->wide ? 1 : pl->k_eff);
+  pl->n_chunks = cdiv(V, kChunk);
   return MTP_OK;
+}
+
+
+// ---------------------------------------------------------------------------
+// Wide laws (support bound above 64 ids). Per-row storage in the workspace:
+// a 16-byte header {n, nonfinite}, ids int32 [V], then probs fp64 [V].
+constexpr int kWideThreads = 1024;
+constexpr int kWideWaves = kWideThreads / 64;
+constexpr double kFix62 = 4611686018427387904.0;   // 2^62: fixed-point probability mass
+
+struct WideHdr {
+  int n;
+  int nonfinite;
+  int pad[2];
+};
+
+__host__ __device__ inline size_t wide_ids_off() { return 16; }
+__host__ __device__ inline size_t wide_probs_off(int V) { return (16 + 4 * (size_t)V + 15) & ~(size_t)15; }
+__host__ __device__ inline size_t wide_row_bytes(int V) { return (wide_probs_off(V) + 8 * (size_t)V + 255) & ~(size_t)255; }
+
+struct WideLaw {
+  const int* ids;
+  const double* probs;
+  int n;
+  int nonfinite;
+};
+
+__device__ __forceinline__ WideLaw wide_law(const unsigned char* base, size_t row_bytes, int V, int row) {
+  const unsigned char* r = base + (size_t)row * row_bytes;
+  const WideHdr* h = reinterpret_cast<const WideHdr*>(r);
+  WideLaw L;
+  L.ids = reinterpret_cast<const int*>(r + wide_ids_off());
+  L.probs = reinterpret_cast<const double*>(r + wide_probs_off(V));
+  L.n = h->n;
+  L.nonfinite = h->nonfinite;
+  return L;
+}
+
+__device__ __forceinline__ float ordered_value(uint32_t o) {
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
+// Exclusive block scan of a 0/1 flag; *total receives the block's count.
+// s_w: [kWideWaves + 1] LDS words. All threads must call it.
+__device__ __forceinline__ int block_scan_flag(bool f, uint32_t* s_w, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t m = __ballot(f);
+  const int in_wave = __popcll(m & ((1ull << lane) - 1ull));
+  if (lane == 0) s_w[wave] = (uint32_t)__popcll(m);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t run = 0;
+    for (int w = 0; w < kWideWaves; ++w) {
+      const uint32_t t = s_w[w];
+      s_w[w] = run;
+      run += t;
+    }
+    s_w[kWideWaves] = run;
+  }
+  __syncthreads();
+  const int r = (int)s_w[wave] + in_wave;
+  *total = (int)s_w[kWideWaves];
+  __syncthreads();
+  return r;
+}
+
+// Deterministic block sum of a[0..n): each thread adds its strided elements
+// in order, then the fixed wave tree, then the waves in order. Uniform result.
+__device__ double block_sum_f64(const double* a, int n, double* s_d) {
+  double v = 0.0;
+  for (int i = threadIdx.x; i < n; i += kWideThreads) v += a[i];
+  v = wave_sum_f64(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) s_d[wave] = v;
+  __syncthreads();
+  double t = 0.0;
+  for (int w = 0; w < kWideWaves; ++w) t += s_d[w];
+  __syncthreads();
+  return t;
+}
+
+// Inclusive prefix of tile element x within the block (fixed order): wave
+// Hillis-Steele scan, then the waves' totals in order. *tile_tot: the tile's
+// sum (waves in order).
+__device__ double block_incl_scan_f64(double x, double* s_d, double* tile_tot) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int o = 1; o < 64; o <<= 1) {
+    const double y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) s_d[wave] = x;
+  __syncthreads();
+  double before = 0.0, tot = 0.0;
+  for (int w = 0; w < kWideWaves; ++w) {
+    if (w == wave) before = tot;
+    tot += s_d[w];
+  }
+  __syncthreads();
+  *tile_tot = tot;
+  return before + x;
+}
+
+// Generator.choice(ids, p) given its uniform, for n up to the vocabulary:
+// cdf = cumsum(p) (a fixed-order block scan), idx = #{cdf / cdf[n-1] <= u},
+// at most n - 1. Two passes recompute the same cdf (the first only for its
+// last value). Uniform result.
+__device__ int block_choice(const int* ids, const double* p, int n, double u, double* s_d, double* s_last,
+                            uint32_t* s_w) {
+  double carry = 0.0;
+  for (int base = 0; base < n; base += kWideThreads) {
+    const int i = base + threadIdx.x;
+    double tt;
+    const double c = carry + block_incl_scan_f64(i < n ? p[i] : 0.0, s_d, &tt);
+    if (i == n - 1) *s_last = c;
+    carry += tt;
+  }
+  __syncthreads();
+  const double last = *s_last;
+  carry = 0.0;
+  int count = 0;
+  for (int base = 0; base < n; base += kWideThreads) {
+    const int i = base + threadIdx.x;
+    double tt;
+    const double c = carry + block_incl_scan_f64(i < n ? p[i] : 0.0, s_d, &tt);
+    carry += tt;
+    int t;
+    block_scan_flag(i < n && c / last <= u, s_w, &t);
+    count += t;
+  }
+  const int idx = count > n - 1 ? n - 1 : count;
+  return ids[idx];
+}
+
+// Probability of tok under a law with ids ascending (0 if absent).
+__device__ __forceinline__ double wide_prob(const WideLaw& L, int tok) {
+  int lo = 0, hi = L.n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (L.ids[mid] < tok) lo = mid + 1; else hi = mid;
+  }
+  return (lo < L.n && L.ids[lo] == tok) ? L.probs[lo] : 0.0;
+}
+
+// One workgroup per row: the sparse law p = renorm(topk(k_eff) ∩ nucleus(top_p))
+// of the full-vocabulary softmax of logits/T (the narrow path's formula for
+// each probability), ids ascending. Rows below nrows1 come from logits.
+__global__ __launch_bounds__(kWideThreads) void wide_law_kernel(const float* __restrict__ logits,
+                                                                const float* __restrict__ logits2, int nrows1,
+                                                                long long ld, int V,
+                                                                const ChunkPart* __restrict__ parts, int n_chunks,
+                                                                double temp, int k_eff, double top_p,
+                                                                unsigned char* __restrict__ lawbuf, size_t row_bytes) {
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const float* lr = row < nrows1 ? logits + (size_t)row * ld : logits2 + (size_t)(row - nrows1) * ld;
+  const ChunkPart* pp = parts + (size_t)row * n_chunks;
+  unsigned char* rb = lawbuf + (size_t)row * row_bytes;
+  WideHdr* hdr = reinterpret_cast<WideHdr*>(rb);
+  int* ids = reinterpret_cast<int*>(rb + wide_ids_off());
+  double* probs = reinterpret_cast<double*>(rb + wide_probs_off(V));
+
+  __shared__ uint32_t h_cnt[256];
+  __shared__ unsigned long long h_mass[256];
+  __shared__ double s_M, s_S;
+  __shared__ int s_nf, s_all, s_argmax;
+  __shared__ uint32_t s_prefix, s_cabove, s_w[kWideWaves + 1];
+  __shared__ unsigned long long s_mabove;
+  __shared__ double s_d[kWideWaves];
+
+  if (tid == 0) {   // fp64 max / sum-exp combine in fixed chunk order (as build_law)
+    double M = -INFINITY;
+    int nf = 0;
+    uint64_t best = 0ull;
+    for (int c = 0; c < n_chunks; ++c) {
+      M = fmax(M, pp[c].m);
+      nf |= pp[c].nonfinite;
+      best = pp[c].keys[0] > best ? pp[c].keys[0] : best;
+    }
+    double S = 0.0;
+    for (int c = 0; c < n_chunks; ++c)
+      if (pp[c].m > -INFINITY) S += pp[c].s * exp(pp[c].m - M);
+    s_M = M;
+    s_S = S;
+    s_nf = nf || !(isfinite(S) && S > 0.0);
+    s_argmax = key_id(best);
+    s_prefix = 0u;
+    s_cabove = 0u;
+    s_mabove = 0ull;
+    s_all = 0;
+  }
+  __syncthreads();
+  if (s_nf) {
+    if (tid == 0) {
+      hdr->n = 0;
+      hdr->nonfinite = 1;
+    }
+    return;
+  }
+  const double M = s_M, S = s_S;
+  const bool nuc = top_p > 0.0 && top_p < 1.0;
+  const unsigned long long TP = nuc ? (unsigned long long)(top_p * kFix62) : ~0ull;
+
+  // Radix descent: after pass j the top 8(j+1) bits of the cut's key are
+  // fixed, with the count and mass of everything ordered before its bin.
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    if (tid < 256) {
+      h_cnt[tid] = 0u;
+      h_mass[tid] = 0ull;
+    }
+    __syncthreads();
+    const uint32_t prefix = s_prefix;
+    for (int id = tid; id < V; id += kWideThreads) {
+      const float l = lr[id];
+      const uint32_t key = ordered_bits(l);
+      if (pass == 0 || (key >> (shift + 8)) == prefix) {
+        const int dgt = (key >> shift) & 255;
+        atomicAdd(&h_cnt[dgt], 1u);
+        const double pv = exp((double)l / temp - M) / S;
+        const unsigned long long P = (unsigned long long)(pv * kFix62);
+        if (P) atomicAdd(&h_mass[dgt], P);
+      }
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t ca = s_cabove;
+      unsigned long long ma = s_mabove;
+      int sel = -1;
+      for (int dgt = 255; dgt >= 0; --dgt) {
+        const uint32_t c = h_cnt[dgt];
+        if (!c) continue;
+        const uint32_t ac = ca + c;
+        const unsigned long long am = ma + h_mass[dgt];
+        // The position after this bin is excluded (top-k full or nucleus
+        // mass reached): the cut lies in this bin.
+        if ((int)ac >= k_eff || (nuc && am >= TP)) {
+          sel = dgt;
+          break;
+        }
+        ca = ac;
+        ma = am;
+      }
+      if (sel < 0) {
+        s_all = 1;   // only in pass 0: every id is inside the cut
+      } else {
+        s_prefix = (prefix << 8) | (uint32_t)sel;
+        s_cabove = ca;
+        s_mabove = ma;
+      }
+    }
+    __syncthreads();
+    if (s_all) break;
+  }
+
+  // Inside the tie group (every logit equal to the cut's): members in id
+  // order, each of the same fixed-point mass Pt; the first is included.
+  const uint32_t tau = s_prefix;
+  int t_cut = 0x7fffffff;
+  if (!s_all) {
+    const double pt = exp((double)ordered_value(tau) / temp - M) / S;
+    const unsigned long long Pt = (unsigned long long)(pt * kFix62);
+    const long long t_k = (long long)k_eff - (long long)s_cabove;
+    long long t_n = 0x7fffffff;
+    if (nuc && Pt) t_n = (long long)((TP - s_mabove + Pt - 1ull) / Pt);
+    const long long t = t_k < t_n ? t_k : t_n;
+    t_cut = (int)(t < 0x7fffffff ? t : 0x7fffffff);
+  }
+
+  // Support in id order: key above the cut, or a tie member before t_cut; p > 0.
+  int out = 0, grank = 0;
+  for (int base = 0; base < V; base += kWideThreads) {
+    const int id = base + tid;
+    const bool valid = id < V;
+    const float l = valid ? lr[id] : -INFINITY;
+    const uint32_t key = ordered_bits(l);
+    const double pv = valid ? exp((double)l / temp - M) / S : 0.0;
+    const bool isg = !s_all && valid && key == tau;
+    int gtot;
+    const int gr = grank + block_scan_flag(isg, s_w, &gtot);
+    grank += gtot;
+    const bool keep = valid && pv > 0.0 && (s_all || key > tau || (isg && gr < t_cut));
+    int ktot;
+    const int pos = out + block_scan_flag(keep, s_w, &ktot);
+    if (keep) {
+      ids[pos] = id;
+      probs[pos] = pv;
+    }
+    out += ktot;
+  }
+  __syncthreads();
+  if (out == 0) {   // empty filter -> argmax one-hot (mtplx/sampling.py:197-199)
+    if (tid == 0) {
+      ids[0] = s_argmax;
+      probs[0] = 1.0;
+      hdr->n = 1;
+      hdr->nonfinite = 0;
+    }
+    return;
+  }
+  // filtered / total, then the SparseDistribution renormalisation.
+  const double t1 = block_sum_f64(probs, out, s_d);
+  for (int i = tid; i < out; i += kWideThreads) probs[i] = probs[i] / t1;
+  __syncthreads();
+  const double t2 = block_sum_f64(probs, out, s_d);
+  for (int i = tid; i < out; i += kWideThreads) probs[i] = probs[i] / t2;
+  if (tid == 0) {
+    hdr->n = out;
+    hdr->nonfinite = 0;
+  }
+}
+
+// The accept loop of one request over wide laws: target rows b*(K+1)+d,
+// draft rows B*(K+1) + b*K + d; scratch: this request's residual ids/probs.
+__global__ __launch_bounds__(kWideThreads) void wide_accept_kernel(
+    const unsigned char* __restrict__ lawbuf, size_t row_bytes, int V, int B, int K,
+    const int32_t* __restrict__ draft_ids, const double* __restrict__ uniforms, int32_t* __restrict__ out_tokens,
+    int32_t* __restrict__ n_accepted, double* __restrict__ accept_probs, int32_t* __restrict__ status,
+    unsigned char* __restrict__ scratch) {
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  __shared__ double s_d[kWideWaves];
+  __shared__ double s_last, s_p, s_q;
+  __shared__ uint32_t s_w[kWideWaves + 1];
+  int* rid = reinterpret_cast<int*>(scratch + (size_t)b * wide_row_bytes(V) + wide_ids_off());
+  double* rp = reinterpret_cast<double*>(scratch + (size_t)b * wide_row_bytes(V) + wide_probs_off(V));
+  int32_t* ot = out_tokens + (size_t)b * (K + 1);
+  for (int d = tid; d <= K; d += kWideThreads) ot[d] = -1;
+  for (int d = tid; d < K; d += kWideThreads) accept_probs[(size_t)b * K + d] = -1.0;
+  const double* u = uniforms + (size_t)b * (K + 1);
+  int ui = 0, nacc = 0, bad = 0;
+  for (int d = 0; d <= K; ++d) {
+    const WideLaw P = wide_law(lawbuf, row_bytes, V, b * (K + 1) + d);
+    const WideLaw Q = d < K ? wide_law(lawbuf, row_bytes, V, B * (K + 1) + b * K + d) : P;
+    if (P.nonfinite || Q.nonfinite) {
+      bad = 1;
+      break;
+    }
+    if (d == K) {   // all drafts accepted: bonus from row K
+      const int tok = block_choice(P.ids, P.probs, P.n, u[ui++], s_d, &s_last, s_w);
+      if (tid == 0) ot[K] = tok;
+      nacc = K;
+      break;
+    }
+    const int tok = draft_ids[(size_t)b * K + d];
+    if (tid == 0) {
+      s_p = wide_prob(P, tok);
+      s_q = wide_prob(Q, tok);
+    }
+    __syncthreads();
+    const double p = s_p, q = s_q;
+    __syncthreads();
+    const double a = (q <= 0.0) ? (p > 0.0 ? 1.0 : 0.0) : fmin(1.0, p / q);
+    const bool acc = u[ui++] <= a;
+    if (tid == 0) accept_probs[(size_t)b * K + d] = a;
+    if (acc) {
+      if (tid == 0) ot[d] = tok;
+      continue;
+    }
+    // Residual max(p - q, 0) over the union of supports, ids ascending: only
+    // P's ids can be positive, in P's order.
+    int n = 0;
+    for (int base = 0; base < P.n; base += kWideThreads) {
+      const int i = base + tid;
+      double r = 0.0;
+      int id = 0;
+      if (i < P.n) {
+        id = P.ids[i];
+        r = fmax(P.probs[i] - wide_prob(Q, id), 0.0);
+      }
+      const bool keep = i < P.n && r > 0.0 && isfinite(r);
+      int tot;
+      const int pos = n + block_scan_flag(keep, s_w, &tot);
+      if (keep) {
+        rid[pos] = id;
+        rp[pos] = r;
+      }
+      n += tot;
+    }
+    __syncthreads();
+    int corr;
+    const double t1 = n ? block_sum_f64(rp, n, s_d) : 0.0;
+    if (n == 0 || !(isfinite(t1) && t1 > 0.0)) {
+      corr = block_choice(P.ids, P.probs, P.n, u[ui++], s_d, &s_last, s_w);
+    } else {
+      for (int i = tid; i < n; i += kWideThreads) rp[i] = rp[i] / t1;
+      __syncthreads();
+      const double t2 = block_sum_f64(rp, n, s_d);
+      for (int i = tid; i < n; i += kWideThreads) rp[i] = rp[i] / t2;
+      __syncthreads();
+      corr = block_choice(rid, rp, n, u[ui++], s_d, &s_last, s_w);
+    }
+    if (tid == 0) ot[d] = corr;
+    nacc = d;
+    break;
+  }
+  if (tid == 0) {
+    status[b] = bad;
+    n_accepted[b] = nacc;
+  }
+}
+
+// Per-row output of wide laws (and one draw per row).
+__global__ __launch_bounds__(kWideThreads) void wide_rows_kernel(const unsigned char* __restrict__ lawbuf,
+                                                                 size_t row_bytes, int V,
+                                                                 const double* __restrict__ uniforms,
+                                                                 int32_t* __restrict__ out_ids,
+                                                                 double* __restrict__ out_probs, int ld_out,
+                                                                 int32_t* __restrict__ out_count,
+                                                                 int32_t* __restrict__ sampled,
+                                                                 int32_t* __restrict__ status) {
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x;
+  __shared__ double s_d[kWideWaves];
+  __shared__ double s_last;
+  __shared__ uint32_t s_w[kWideWaves + 1];
+  const WideLaw L = wide_law(lawbuf, row_bytes, V, r);
+  if (tid == 0) {
+    status[r] = L.nonfinite ? 1 : 0;
+    if (out_count) out_count[r] = L.n;
+  }
+  if (out_ids)
+    for (int i = tid; i < ld_out; i += kWideThreads) {
+      out_ids[(size_t)r * ld_out + i] = i < L.n ? L.ids[i] : -1;
+      out_probs[(size_t)r * ld_out + i] = i < L.n ? L.probs[i] : 0.0;
+    }
+  if (sampled) {
+    const int tok = L.nonfinite ? -1 : block_choice(L.ids, L.probs, L.n, uniforms[r], s_d, &s_last, s_w);
+    if (tid == 0) sampled[r] = tok;
+  }
+}
+
+// logits[rows[i] * ld + ids[i]] += -deltas[i] in fp32 ((row, id) pairs unique).
+__global__ void logit_deltas_kernel(float* logits, long long ld, const int32_t* rows, const int32_t* ids,
+                                    const float* deltas, int n, int R, int V, int32_t* status) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int r = rows[i], id = ids[i];
+  if (r < 0 || r >= R || id < 0 || id >= V) {
+    if (status) atomicOr(status, 1);
+    return;
+  }
+  float* x = logits + (size_t)r * ld + id;
+  *x = *x + (-deltas[i]);
 }
 
 }  // namespace mtp
 
 using namespace mtp;
 
-MTP_API size_t mtp_sampler_workspace_bytes(int rows, int V) {
-  if (rows < 1 || V < 1) return 0;
-  return (size_t)rows * cdiv(V, kChunk) * sizeof(ChunkPart);
+// Workspace: chunk partials [rows][n_chunks]; on the wide path followed (at
+// a 256-byte boundary) by rows wide laws and rows residual scratch areas.
+static size_t parts_bytes(int rows, int V) {
+  return ((size_t)rows * cdiv(V, kChunk) * sizeof(ChunkPart) + 255) & ~(size_t)255;
+}
+
+MTP_API size_t mtp_sampler_workspace_bytes(int rows, int V, int top_k) {
+  if (rows < 1 || V < 1 || top_k < 0) return 0;
+  const int k_eff = (top_k > 0 && top_k < V) ? top_k : V;
+  size_t n = parts_bytes(rows, V);
+  if (k_eff > kMaxTopK) n += 2 * (size_t)rows * wide_row_bytes(V);
+  return n;
 }
 
 MTP_API int mtp_spec_accept(const float* target_logits, const float* draft_logits, const int32_t* draft_ids,
@@ -847,28 +1315,38 @@ MTP_API int mtp_spec_accept(const float* target_logits, const float* draft_logit
                             double top_p, int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status,
                             void* ws, size_t ws_bytes, void* stream) {
   const char* who = "mtp_spec_accept";
-  int ksel, greedy, n_chunks;
-  int rc = sampler_plan(V, top_k, temperature, &ksel, &greedy, &n_chunks, who);
+  SamplerPlan pl;
+  int rc = sampler_plan(V, top_k, temperature, &pl, who);
   if (rc) return rc;
   if (B < 1 || K < 1 || !target_logits || !draft_logits || !draft_ids || !uniforms || !out_tokens ||
       !n_accepted || !accept_probs || !status) {
     set_error("%s: need B>=1, K>=1 and non-null buffers", who);
     return MTP_ERR_ARG;
   }
-  const size_t need = mtp_sampler_workspace_bytes(B * (2 * K + 1), V);
+  const int rows = B * (2 * K + 1);
+  const size_t need = mtp_sampler_workspace_bytes(rows, V, pl.greedy ? 1 : top_k);
   if (!ws || ws_bytes < need) {
     set_error("%s: workspace %zu B < required %zu B", who, ws_bytes, need);
     return MTP_ERR_WORKSPACE;
   }
   hipStream_t st = (hipStream_t)stream;
+  const int n_chunks = pl.n_chunks;
   ChunkPart* tparts = reinterpret_cast<ChunkPart*>(ws);
   ChunkPart* dparts = tparts + (size_t)B * (K + 1) * n_chunks;
-  const double temp = greedy ? 1.0 : temperature;
+  const double temp = pl.greedy ? 1.0 : temperature;
   // target rows then draft rows, one launch (dparts follows tparts)
-  hipLaunchKernelGGL(vocab_partials, dim3(n_chunks, B * (2 * K + 1)), dim3(kSampThreads), 0, st, target_logits,
-                     draft_logits, B * (K + 1), (long long)V, V, n_chunks, temp, ksel, greedy, tparts);
+  hipLaunchKernelGGL(vocab_partials, dim3(n_chunks, rows), dim3(kSampThreads), 0, st, target_logits,
+                     draft_logits, B * (K + 1), (long long)V, V, n_chunks, temp, pl.ksel, pl.greedy, tparts);
   if ((rc = launch_check(who))) return rc;
-  if (n_chunks <= 64) {
+  if (pl.wide) {
+    unsigned char* lawbuf = reinterpret_cast<unsigned char*>(ws) + parts_bytes(rows, V);
+    const size_t rb = wide_row_bytes(V);
+    hipLaunchKernelGGL(wide_law_kernel, dim3(rows), dim3(kWideThreads), 0, st, target_logits, draft_logits,
+                       B * (K + 1), (long long)V, V, tparts, n_chunks, temp, pl.k_eff, top_p, lawbuf, rb);
+    if ((rc = launch_check(who))) return rc;
+    hipLaunchKernelGGL(wide_accept_kernel, dim3(B), dim3(kWideThreads), 0, st, lawbuf, rb, V, B, K, draft_ids,
+                       uniforms, out_tokens, n_accepted, accept_probs, status, lawbuf + (size_t)rows * rb);
+  } else if (n_chunks <= 64) {
     const int nwv = 2 * K + 1 < 16 ? 2 * K + 1 : 16;
     const size_t lds = accept_laws_lds(K, nwv);
     if (lds > 160 * 1024) {
@@ -879,37 +1357,67 @@ MTP_API int mtp_spec_accept(const float* target_logits, const float* draft_logit
     if (lds > 65536) (void)hipFuncSetAttribute((const void*)accept_laws, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)lds);
     hipLaunchKernelGGL(accept_laws, dim3(B), dim3(nwv * 64), lds, st, tparts, dparts, n_chunks, draft_ids, uniforms,
-                       K, ksel, greedy, temp, top_p, out_tokens, n_accepted, accept_probs, status);
+                       K, pl.ksel, pl.greedy, temp, top_p, out_tokens, n_accepted, accept_probs, status);
   } else {
     hipLaunchKernelGGL(accept_finish, dim3(B), dim3(64), 0, st, tparts, dparts, n_chunks, draft_ids, uniforms, K,
-                       ksel, greedy, temp, top_p, out_tokens, n_accepted, accept_probs, status);
+                       pl.ksel, pl.greedy, temp, top_p, out_tokens, n_accepted, accept_probs, status);
   }
   return launch_check(who);
 }
 
 MTP_API int mtp_sample_rows(const float* logits, int rows, int V, double temperature, int top_k, double top_p,
-                            const double* uniforms, int32_t* out_ids, double* out_probs, int32_t* out_count,
-                            int32_t* sampled, int32_t* status, void* ws, size_t ws_bytes, void* stream) {
+                            const double* uniforms, int32_t* out_ids, double* out_probs, int ld_out,
+                            int32_t* out_count, int32_t* sampled, int32_t* status, void* ws, size_t ws_bytes,
+                            void* stream) {
   const char* who = "mtp_sample_rows";
-  int ksel, greedy, n_chunks;
-  int rc = sampler_plan(V, top_k, temperature, &ksel, &greedy, &n_chunks, who);
+  SamplerPlan pl;
+  int rc = sampler_plan(V, top_k, temperature, &pl, who);
   if (rc) return rc;
   if (rows < 1 || !logits || !status || (sampled && !uniforms) || (out_ids && !out_probs)) {
     set_error("%s: need rows>=1, logits, status, and uniforms when sampling", who);
     return MTP_ERR_ARG;
   }
-  const size_t need = mtp_sampler_workspace_bytes(rows, V);
+  const int bound = pl.greedy ? 1 : pl.k_eff;   // the support never exceeds this
+  if (out_ids && ld_out < bound) {
+    set_error("%s: ld_out %d < the support bound %d", who, ld_out, bound);
+    return MTP_ERR_ARG;
+  }
+  const size_t need = mtp_sampler_workspace_bytes(rows, V, pl.greedy ? 1 : top_k);
   if (!ws || ws_bytes < need) {
     set_error("%s: workspace %zu B < required %zu B", who, ws_bytes, need);
     return MTP_ERR_WORKSPACE;
   }
   hipStream_t st = (hipStream_t)stream;
   ChunkPart* parts = reinterpret_cast<ChunkPart*>(ws);
-  const double temp = greedy ? 1.0 : temperature;
-  hipLaunchKernelGGL(vocab_partials, dim3(n_chunks, rows), dim3(kSampThreads), 0, st, logits, logits, rows,
-                     (long long)V, V, n_chunks, temp, ksel, greedy, parts);
+  const double temp = pl.greedy ? 1.0 : temperature;
+  hipLaunchKernelGGL(vocab_partials, dim3(pl.n_chunks, rows), dim3(kSampThreads), 0, st, logits, logits, rows,
+                     (long long)V, V, pl.n_chunks, temp, pl.ksel, pl.greedy, parts);
   if ((rc = launch_check(who))) return rc;
-  hipLaunchKernelGGL(row_laws, dim3(rows), dim3(64), 0, st, parts, n_chunks, ksel, greedy, temp, top_p,
-                     uniforms, out_ids, out_probs, out_count, sampled, status);
+  if (pl.wide) {
+    unsigned char* lawbuf = reinterpret_cast<unsigned char*>(ws) + parts_bytes(rows, V);
+    const size_t rb = wide_row_bytes(V);
+    hipLaunchKernelGGL(wide_law_kernel, dim3(rows), dim3(kWideThreads), 0, st, logits, logits, rows, (long long)V,
+                       V, parts, pl.n_chunks, temp, pl.k_eff, top_p, lawbuf, rb);
+    if ((rc = launch_check(who))) return rc;
+    hipLaunchKernelGGL(wide_rows_kernel, dim3(rows), dim3(kWideThreads), 0, st, lawbuf, rb, V, uniforms, out_ids,
+                       out_probs, ld_out, out_count, sampled, status);
+  } else {
+    hipLaunchKernelGGL(row_laws, dim3(rows), dim3(64), 0, st, parts, pl.n_chunks, pl.ksel, pl.greedy, temp, top_p,
+                       uniforms, out_ids, out_probs, ld_out, out_count, sampled, status);
+  }
+  return launch_check(who);
+}
+
+MTP_API int mtp_apply_logit_deltas(float* logits, long long ld, int rows, int V, const int32_t* row_ids,
+                                   const int32_t* token_ids, const float* deltas, int n, int32_t* status,
+                                   void* stream) {
+  const char* who = "mtp_apply_logit_deltas";
+  if (n == 0) return MTP_OK;
+  if (!logits || !row_ids || !token_ids || !deltas || n < 0 || rows < 1 || V < 1 || ld < V) {
+    set_error("%s: bad arguments", who);
+    return MTP_ERR_ARG;
+  }
+  hipLaunchKernelGGL(logit_deltas_kernel, dim3(cdiv(n, 256)), dim3(256), 0, (hipStream_t)stream, logits, ld, row_ids,
+                     token_ids, deltas, n, rows, V, status);
   return launch_check(who);
 }

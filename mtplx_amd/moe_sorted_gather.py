@@ -85,6 +85,33 @@ def expert_sort(indices: torch.Tensor, n_experts: int) -> ExpertSort:
     return ExpertSort(row_map, sorted_ids, inv, off, active, top_k, n_experts)
 
 
+_expert_sort = expert_sort   # for functions whose ``expert_sort`` keyword shadows the name
+
+
+def segments(sorted_ids: torch.Tensor, n_experts: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(expert_off int32 [E+1], active int32 [1+E])`` from ids already in
+    ascending order (``mtp_moe_segments``)."""
+    ids = sorted_ids.reshape(-1).to(torch.int32).contiguous()
+    dev = ids.device
+    off = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+    active = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+    _lib.call("mtp_moe_segments", ids.data_ptr(), int(ids.numel()), int(n_experts), off.data_ptr(), active.data_ptr(),
+              _lib.stream_handle(dev))
+    return off, active
+
+
+def _sorted_rows(rhs_indices: torch.Tensor, n_experts: int, top_k: int = 1) -> ExpertSort:
+    """An :class:`ExpertSort` view of rows whose expert ids are already sorted
+    (the ``sorted_indices=True`` contract); raises on unsorted or out-of-range ids."""
+    ids = rhs_indices.reshape(-1).to(torch.int32).contiguous()
+    off, active = segments(ids, n_experts)
+    if int(active[0].item()) < 0:
+        raise ValueError(f"sorted indices must ascend within [0, {n_experts})")
+    R = int(ids.numel())
+    ar = torch.arange(R, dtype=torch.int32, device=ids.device)
+    return ExpertSort(ar, ids, ar, off, active, top_k, n_experts)
+
+
 def sort_rows(x: torch.Tensor, indices: torch.Tensor, n_experts: int | None = None):
     """``(tokens [n,1,K], row_map, sorted_indices, inv_order)`` exactly as
     ``mtplx/moe_sorted_gather.py:221-238`` (stable sort of the flattened ids)."""
@@ -107,92 +134,162 @@ def _gather(x, x2, es: ExpertSort, rowmap, w, scales, biases, w1, s1, b1, n_out,
     return y
 
 
-def gather_qmm_rows(tokens: torch.Tensor, es: ExpertSort, w: torch.Tensor, scales: torch.Tensor,
-                    biases: torch.Tensor, *, group_size: int, bits: int = 4, mode: str = "affine") -> torch.Tensor:
-    """``gather_qmm(tokens[row_map], w, ..., sorted_indices=True)`` with rows read
-    in place through the map (``mtplx/moe_sorted_gather.py:241``). ``w`` is
-    ``[E, N, K/8]``; returns ``[R, 1, N]`` in sorted order."""
-    if bits != 4 or mode != "affine":
-        raise NotImplementedError("gfx950 gather path is 4-bit affine")
-    x = tokens.reshape(-1, tokens.shape[-1]).contiguous()
-    N = int(w.shape[-2])
-    T = x.shape[0]
-    y = _gather(x, None, es, es.row_map, w, scales, biases, None, None, None, N, 0, 0, N, group_size, T)
-    return y.reshape(-1, 1, N)
+def _check_quant(bits, mode):
+    if int(bits) != 4 or mode != "affine":
+        raise NotImplementedError(f"gfx950 gather path is 4-bit affine (got bits={bits}, mode={mode!r})")
 
 
-def swiglu_rows(tokens: torch.Tensor, es: ExpertSort, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
-                *, group_size: int, bits: int = 4, mode: str = "affine") -> torch.Tensor:
-    """``silu(gate) * up`` of the fused ``[gate | up]`` sorted gather
-    (``mtplx/moe_sorted_gather.py:288``); ``w`` is ``[E, 2F, K/8]``. Returns ``[R, 1, F]``."""
-    if bits != 4 or mode != "affine":
-        raise NotImplementedError("gfx950 gather path is 4-bit affine")
+def gather_qmm_rows(tokens: torch.Tensor, row_map: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                    biases: torch.Tensor, rhs_indices: torch.Tensor, *, group_size: int, bits: int,
+                    mode: str = "affine", expert_sort: ExpertSort | None = None) -> torch.Tensor:
+    """``gather_qmm(tokens[row_map], w, ..., rhs_indices, sorted_indices=True)``
+    with each token row read in place through ``row_map``
+    (``mtplx/moe_sorted_gather.py:241``). ``w`` is ``[E, N, K/8]``,
+    ``rhs_indices`` ascending; returns ``[R, 1, N]`` in sorted order.
+    ``expert_sort``: the :func:`expert_sort` that produced the rows, which
+    saves the segment pass."""
+    _check_quant(bits, mode)
     x = tokens.reshape(-1, tokens.shape[-1]).contiguous()
+    E, N = int(w.shape[0]), int(w.shape[-2])
+    es = expert_sort if expert_sort is not None else _sorted_rows(rhs_indices, E)
+    rm = row_map.reshape(-1).to(torch.int32).contiguous()
+    R = int(rm.numel())
+    y = _gather(x, None, es, rm, w, scales, biases, None, None, None, N, 0, 0, N, int(group_size), R)
+    return y.reshape(R, 1, N)
+
+
+def swiglu_rows(tokens: torch.Tensor, row_map: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                biases: torch.Tensor, rhs_indices: torch.Tensor, *, group_size: int, bits: int,
+                mode: str = "affine", expert_sort: ExpertSort | None = None) -> torch.Tensor:
+    """``nn.silu(gate) * up`` of the fused ``[gate | up]`` sorted gather
+    (``mtplx/moe_sorted_gather.py:288``); ``w`` is ``[E, 2F, K/8]``. One kernel:
+    the gate and up halves of a column tile are computed together and only
+    the product is stored. Returns ``[R, 1, F]``."""
+    _check_quant(bits, mode)
+    x = tokens.reshape(-1, tokens.shape[-1]).contiguous()
+    E = int(w.shape[0])
     F = int(w.shape[-2]) // 2
     kw = int(w.shape[-1])
     gs_k = int(scales.shape[-1])
+    es = expert_sort if expert_sort is not None else _sorted_rows(rhs_indices, E)
+    rm = row_map.reshape(-1).to(torch.int32).contiguous()
+    R = int(rm.numel())
     w_up = w.reshape(-1, kw)[F:]            # up rows start F rows into expert 0; same per-expert stride
     s_up = scales.reshape(-1, gs_k)[F:]
     b_up = biases.reshape(-1, gs_k)[F:]
-    y = _gather(x, None, es, es.row_map, w, scales, biases, w_up, s_up, b_up, F, 0, 3, 2 * F, group_size, x.shape[0])
-    return y.reshape(-1, 1, F)
+    y = _gather(x, None, es, rm, w, scales, biases, w_up, s_up, b_up, F, 0, 3, 2 * F, int(group_size), R)
+    return y.reshape(R, 1, F)
 
 
-def switch_linear(module: Any, x: torch.Tensor, es: ExpertSort, *, sorted_indices: bool = True,
-                  swiglu_up: torch.Tensor | None = None) -> torch.Tensor:
-    """Expert linear over rows already in sorted order (``mtplx/moe_sorted_gather.py:339``):
-    ``y[i] = x[i] @ W[e_i]^T``; with ``swiglu_up`` the input is ``silu(x) * up``."""
-    if not sorted_indices:
-        raise NotImplementedError("unsorted switch_linear: sort with expert_sort first")
+def switch_linear(module: Any, x: torch.Tensor, indices: torch.Tensor, *, sorted_indices: bool,
+                  expert_sort: ExpertSort | None = None) -> torch.Tensor:
+    """``module(x, indices, sorted_indices=...)`` for a quantized switch linear
+    (``mtplx/moe_sorted_gather.py:339``): row ``i`` of ``x`` times expert
+    ``indices[i]``'s weights; ``module`` exposes ``weight [E, N, K/8]``,
+    ``scales``, ``biases``, ``group_size``, ``bits``, ``mode``. Unsorted indices
+    are sorted on the GPU and the result returned in the caller's order."""
+    _check_quant(getattr(module, "bits", 4), getattr(module, "mode", "affine"))
+    E, N = int(module.weight.shape[0]), int(module.weight.shape[-2])
+    lead = x.shape[:-1]
     x2 = x.reshape(-1, x.shape[-1]).contiguous()
-    N = int(module.weight.shape[-2])
-    up = None if swiglu_up is None else swiglu_up.reshape(x2.shape).contiguous()
-    T = max(1, x2.shape[0] // max(es.top_k, 1))
-    y = _gather(x2, up, es, None, module.weight, module.scales, module.biases, None, None, None, N,
-                1 if up is not None else 0, 0, N, module.group_size, T)
-    return y.reshape(*x.shape[:-1], N)
+    ids = indices.reshape(-1)
+    if int(ids.numel()) != int(x2.shape[0]):
+        raise ValueError(f"switch_linear: {x2.shape[0]} rows but {ids.numel()} expert indices")
+    if sorted_indices:
+        es = expert_sort if expert_sort is not None else _sorted_rows(ids, E)
+        y = _gather(x2, None, es, None, module.weight, module.scales, module.biases, None, None, None, N, 0, 0, N,
+                    int(module.group_size), int(x2.shape[0]))
+        return y.reshape(*lead, N)
+    es = _expert_sort(ids.reshape(-1, 1), E)
+    y = _gather(x2, None, es, es.row_map, module.weight, module.scales, module.biases, None, None, None, N, 0, 0, N,
+                int(module.group_size), int(x2.shape[0]))
+    return y[es.inv_order.long()].reshape(*lead, N)
 
 
 def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor | None = None,
                lhs_indices: torch.Tensor | None = None, rhs_indices: torch.Tensor | None = None,
                transpose: bool = True, group_size: int | None = None, bits: int | None = None,
                mode: str = "affine", *, sorted_indices: bool = False) -> torch.Tensor:
-    """``y[i] = x[lhs_indices[i]] @ dequant(w[rhs_indices[i]]).T`` (the
-    ``mx.gather_qmm`` contract, ``mtplx/moe_sorted_gather.py:170``), 2-D rows."""
+    """``y[b] = x[lhs[b]] @ dequant(w[rhs[b]]).T`` (the ``mx.gather_qmm``
+    contract, ``mtplx/moe_sorted_gather.py:170``) for single-row operands:
+    ``x`` is ``[..., 1, K]`` (or ``[n, K]`` rows); without ``lhs_indices`` the
+    batch axes of ``x`` broadcast against ``rhs_indices`` (mlx-lm's SwitchGLU
+    call, ``x [T,1,1,K]`` with ``indices [T,k]`` gives ``[T,k,1,N]``)."""
     if not transpose or biases is None:
         raise NotImplementedError("gfx950 gather_qmm supports transpose=True affine weights")
-    E = int(w.shape[0])
-    rhs = rhs_indices.reshape(-1, 1).to(torch.int32)
-    es = expert_sort(rhs, E)
-    x2 = x.reshape(-1, x.shape[-1]).contiguous()
-    lhs = torch.arange(rhs.shape[0], device=x.device, dtype=torch.int32) if lhs_indices is None \
-        else lhs_indices.reshape(-1).to(torch.int32)
-    rowmap = lhs[es.row_map.long()].contiguous()     # x row of sorted row i
-    N = int(w.shape[-2])
-    y_sorted = _gather(x2, None, es, rowmap, w, scales, biases, None, None, None, N, 0, 0, N,
-                       int(group_size or 64), int(rhs.shape[0]))
-    return y_sorted[es.inv_order.long()]
+    _check_quant(4 if bits is None else bits, mode)
+    E, N, K = int(w.shape[0]), int(w.shape[-2]), int(x.shape[-1])
+    if rhs_indices is None:
+        raise ValueError("gather_qmm needs rhs_indices")
+    if x.dim() >= 2 and x.shape[-2] == 1:
+        xb = x.reshape(*x.shape[:-2], K)          # batch of single rows
+        out_tail = (1, N)
+    else:
+        xb = x.reshape(-1, K)
+        out_tail = (N,)
+    rows = xb.reshape(-1, K).contiguous()
+    if lhs_indices is None:
+        batch = torch.broadcast_shapes(tuple(xb.shape[:-1]), tuple(rhs_indices.shape))
+        lhs = torch.arange(rows.shape[0], device=x.device, dtype=torch.int32).reshape(xb.shape[:-1])
+        lhs = lhs.broadcast_to(batch).reshape(-1)
+        rhs = rhs_indices.broadcast_to(batch).reshape(-1)
+    else:
+        batch = tuple(torch.broadcast_shapes(tuple(lhs_indices.shape), tuple(rhs_indices.shape)))
+        lhs = lhs_indices.broadcast_to(batch).reshape(-1)
+        rhs = rhs_indices.broadcast_to(batch).reshape(-1)
+    lhs = lhs.to(torch.int32).contiguous()
+    rhs = rhs.to(torch.int32).contiguous()
+    R = int(rhs.numel())
+    gs = int(group_size or 64)
+    if sorted_indices:
+        es = _sorted_rows(rhs, E)
+        y = _gather(rows, None, es, lhs, w, scales, biases, None, None, None, N, 0, 0, N, gs, R)
+    else:
+        es = expert_sort(rhs.reshape(-1, 1), E)
+        rowmap = lhs[es.row_map.long()].contiguous()     # x row of sorted row i
+        y = _gather(rows, None, es, rowmap, w, scales, biases, None, None, None, N, 0, 0, N, gs, R)
+        y = y[es.inv_order.long()]
+    return y.reshape(*batch, *out_tail)
 
 
-def moe_combine(y_sorted: torch.Tensor, es: ExpertSort, route_weights: torch.Tensor,
-                shared: torch.Tensor | None = None) -> torch.Tensor:
-    """Unsort + route-weighted sum over top_k (+ shared expert)
-    (``mtplx/models/qwen4_exp.py:1544-1577``)."""
+def moe_combine(y_sorted: torch.Tensor, inv_order, route_weights: torch.Tensor, shared: torch.Tensor | None = None,
+                *, shared_gate: torch.Tensor | None = None, resid: torch.Tensor | None = None,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """The sparse block's tail (``mtplx/models/qwen4_exp.py:1438-1445``, the
+    unsort of ``:1544-1577``): ``bf16(sum_j w[t,j] * y_sorted[inv_order[t*k+j]])``
+    plus ``sigmoid(shared_gate[t]) * shared[t]`` (``shared_gate``: fp32 ``[T]``
+    or a strided column), plus ``resid`` when given. ``inv_order`` is the
+    tensor or an :class:`ExpertSort`."""
+    if isinstance(inv_order, ExpertSort):
+        inv, top_k = inv_order.inv_order, inv_order.top_k
+    else:
+        inv, top_k = inv_order, int(route_weights.shape[-1])
     H = int(y_sorted.shape[-1])
-    R = int(es.inv_order.numel())
-    T = R // es.top_k
-    out = torch.empty((T, H), dtype=torch.bfloat16, device=y_sorted.device)
+    R = int(inv.numel())
+    T = R // top_k
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.bfloat16, device=y_sorted.device)
     w = route_weights.to(torch.float32).contiguous()
-    _lib.call("mtp_moe_combine", y_sorted.contiguous().data_ptr(), es.inv_order.data_ptr(), w.data_ptr(),
-              _lib.ptr(shared), out.data_ptr(), T, es.top_k, H, _lib.stream_handle(y_sorted.device))
+    gate_ld = 1
+    if shared_gate is not None:
+        gate_ld = int(shared_gate.stride(0)) if shared_gate.dim() > 0 else 1
+    _lib.call("mtp_moe_combine", y_sorted.contiguous().data_ptr(), inv.to(torch.int32).contiguous().data_ptr(),
+              w.data_ptr(), _lib.ptr(shared), _lib.ptr(shared_gate), gate_ld, _lib.ptr(resid), out.data_ptr(), T,
+              top_k, H, _lib.stream_handle(y_sorted.device))
     return out
 
 
-def route(router_logits: torch.Tensor, top_k: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """Top-k experts per token (value desc, id asc) and renormalised softmax weights."""
-    T, E = (int(s) for s in router_logits.shape)
-    lg = router_logits.to(torch.float32).contiguous()
+def route(router_logits: torch.Tensor, top_k: int, skew: torch.Tensor | None = None,
+          n_experts: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Top-k experts per token of ``router_logits[:, :E]`` (+ ``skew``) in
+    (value desc, id asc) order and the renormalised softmax weights."""
+    T = int(router_logits.shape[0])
+    E = int(n_experts) if n_experts is not None else int(router_logits.shape[1])
+    lg = router_logits if router_logits.dtype == torch.float32 and router_logits.stride(1) == 1 else \
+        router_logits.to(torch.float32).contiguous()
     ids = torch.empty((T, top_k), dtype=torch.int32, device=lg.device)
     wts = torch.empty((T, top_k), dtype=torch.float32, device=lg.device)
-    _lib.call("mtp_moe_route", lg.data_ptr(), T, E, top_k, ids.data_ptr(), wts.data_ptr(), _lib.stream_handle(lg.device))
+    sk = None if skew is None else skew.to(torch.float32).contiguous()
+    _lib.call("mtp_moe_route", lg.data_ptr(), int(lg.stride(0)), _lib.ptr(sk), T, E, top_k, ids.data_ptr(),
+              wts.data_ptr(), _lib.stream_handle(lg.device))
     return ids, wts

@@ -11,6 +11,15 @@ Differences, on purpose: writes are in place (a HIP scatter into the
 preallocated buffer) rather than a functional copy, so a snapshot is an owned
 copy taken before the write; ``restore_masked`` can be limited to a position
 range (the rows' speculative window) instead of rewriting whole buffers.
+The reference's arrays are immutable, so every buffer this cache did not
+allocate itself — given to the constructor, adopted by ``extend`` or
+``from_scalar_cache``, set through ``state`` — or handed out through
+``state`` is copied before the next in-place write (copy on write): a write
+never changes another cache, the source scalar cache or a captured state.
+The bookkeeping bodies (capacity bound and frozen capacity in
+``update_and_fetch``, ``reserve``, ``freeze_capacity``, ``trim``, ``filter``,
+``extend``, ``state``/``meta_state``) restate the reference's methods step
+by step; they are the protocol a drop-in must keep.
 """
 
 from __future__ import annotations
@@ -47,8 +56,8 @@ class RaggedKVSnapshot:
 class RaggedBatchKVCache:
     def __init__(self, *, batch_size: int | None = None, step: int = 256, keys: torch.Tensor | None = None,
                  values: torch.Tensor | None = None, offsets: Any | None = None) -> None:
-        self.keys = keys
-        self.values = values
+        self._keys = keys
+        self._values = values
         self.step = int(step)
         if offsets is not None:
             self.offsets = _as_int32_vector(offsets, batch_size=batch_size)
@@ -61,6 +70,39 @@ class RaggedBatchKVCache:
         self._capacity_bound: int | None = None
         self._frozen_capacity: int | None = None
         self._status = None
+        # True while keys/values may be referenced outside this cache.
+        self._shared = keys is not None
+
+    # Buffers assigned from outside (``cache.keys = t``, as the reference's
+    # own tests do) may be referenced elsewhere: they are marked shared.
+    @property
+    def keys(self):
+        return self._keys
+
+    @keys.setter
+    def keys(self, value) -> None:
+        self._keys = value
+        self._shared = value is not None
+
+    @property
+    def values(self):
+        return self._values
+
+    @values.setter
+    def values(self, value) -> None:
+        self._values = value
+        self._shared = value is not None
+
+    def _set_buffers(self, k, v, *, shared: bool) -> None:
+        self._keys, self._values = k, v
+        self._shared = shared and k is not None
+
+    def _own_buffers(self) -> None:
+        """Copy buffers that may be referenced elsewhere before writing in place."""
+        if self._shared and self._keys is not None:
+            self._keys = self._keys.clone()
+            self._values = self._values.clone()
+        self._shared = False
 
     # -- construction ---------------------------------------------------------
     @classmethod
@@ -103,7 +145,7 @@ class RaggedBatchKVCache:
         if self.keys is not None:
             nk[:, :, :cur].copy_(self.keys)
             nv[:, :, :cur].copy_(self.values)
-        self.keys, self.values = nk, nv
+        self._set_buffers(nk, nv, shared=False)
 
     def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor, *, write_start: Any | None = None,
                          new_offsets: Any | None = None):
@@ -121,6 +163,7 @@ class RaggedBatchKVCache:
         else:
             required = int(start.max().item()) + q   # legacy single device read, as the reference
         self._grow_to(required, keys, values)
+        self._own_buffers()
         if self._status is None or self._status.device != keys.device:
             self._status = torch.zeros(1, dtype=torch.int32, device=keys.device)
         _lib.call("mtp_kv_scatter", self.keys.data_ptr(), self.values.data_ptr(), keys.contiguous().data_ptr(),
@@ -180,15 +223,22 @@ class RaggedBatchKVCache:
 
     @property
     def state(self):
+        """``(keys, values, offsets)``. The tensors are handed out as they are;
+        the cache copies its buffers before its next in-place write, so what
+        the caller holds keeps this moment's contents (the reference's
+        immutable-array semantics)."""
+        if self.keys is not None:
+            self._shared = True
         return (self.keys, self.values, self.offsets)
 
     @state.setter
     def state(self, value) -> None:
         if value is None:
-            self.keys = self.values = self.offsets = None
+            self._set_buffers(None, None, shared=False)
+            self.offsets = None
             return
         k, v, off = value
-        self.keys, self.values = k, v
+        self._set_buffers(k, v, shared=True)
         self.offsets = None if off is None else _as_int32_vector(off)
 
     @property
@@ -203,8 +253,8 @@ class RaggedBatchKVCache:
     def filter(self, batch_indices: Any) -> None:
         idx = _as_int32_vector(batch_indices, device=self.keys.device if self.keys is not None else None).long()
         if self.keys is not None:
-            self.keys = self.keys[idx].contiguous()
-            self.values = self.values[idx].contiguous()
+            # advanced indexing: new buffers
+            self._set_buffers(self.keys[idx].contiguous(), self.values[idx].contiguous(), shared=False)
         if self.offsets is not None:
             self.offsets = self.offsets[idx].to(torch.int32).contiguous()
 
@@ -212,14 +262,14 @@ class RaggedBatchKVCache:
         if other.keys is None:
             return
         if self.keys is None:
-            self.keys, self.values = other.keys, other.values
-            self.offsets = None if other.offsets is None else other.offsets.to(torch.int32)
+            self._set_buffers(other.keys, other.values, shared=True)
+            self.offsets = None if other.offsets is None else other.offsets.to(torch.int32).clone()
+            other._shared = True
             return
         cap = max(int(self.keys.shape[2]), int(other.keys.shape[2]))
         ak, av = _pad_seq_to(self.keys, cap), _pad_seq_to(self.values, cap)
         bk, bv = _pad_seq_to(other.keys, cap), _pad_seq_to(other.values, cap)
-        self.keys = torch.cat([ak, bk], dim=0)
-        self.values = torch.cat([av, bv], dim=0)
+        self._set_buffers(torch.cat([ak, bk], dim=0), torch.cat([av, bv], dim=0), shared=False)
         self.offsets = torch.cat([self.offsets, other.offsets]).to(torch.int32)
 
     def snapshot(self) -> RaggedKVSnapshot:
@@ -228,8 +278,8 @@ class RaggedBatchKVCache:
                                 None if self.offsets is None else self.offsets.clone(), int(self.step))
 
     def restore(self, snap: RaggedKVSnapshot) -> None:
-        self.keys = None if snap.keys is None else snap.keys.clone()
-        self.values = None if snap.values is None else snap.values.clone()
+        self._set_buffers(None if snap.keys is None else snap.keys.clone(),
+                          None if snap.values is None else snap.values.clone(), shared=False)
         self.offsets = None if snap.offsets is None else snap.offsets.clone()
         self.step = int(snap.step)
 
@@ -249,6 +299,7 @@ class RaggedBatchKVCache:
             self._grow_to(int(snap.keys.shape[2]), self.keys, self.values)
             cap = int(self.keys.shape[2])
         lo, hi = (0, cap) if positions is None else (max(0, int(positions[0])), min(cap, int(positions[1])))
+        self._own_buffers()
         m8 = mask.to(torch.uint8).contiguous()
         B, H, _, D = (int(s) for s in self.keys.shape)
         st = _lib.stream_handle(self.keys.device)

@@ -17,8 +17,10 @@ Per layer the kernels are:
   4. ``mtp_qmv_affine4_residual``    o_proj + residual add
   5. ``mtp_qmv_affine4_rmsnorm_dual`` post-attention RMSNorm + gate/up + SwiGLU
   6. ``mtp_qmv_affine4_residual``    down_proj + residual add
-  (MoE layers replace 5-6 with route → expert sort → gathered SwiGLU →
-  gathered down → unsort/combine (+ shared expert).)
+  (MoE layers replace 5-6 with RMSNorm → router projection (its last row
+  is the shared-expert gate) → top-k route → expert sort → gathered SwiGLU →
+  gathered down, the shared expert's SwiGLU MLP, and one combine: residual +
+  routed + sigmoid(gate) * shared, ``mtplx/models/qwen4_exp.py:1416-1445``.)
 then the final RMSNorm fused into the lm_head (fp32 logits) and
 ``mtp_spec_accept`` on the verify rows.
 """
@@ -27,8 +29,7 @@ from __future__ import annotations
 
 import ctypes
 import math
-import os
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 
 import torch
 
@@ -81,7 +82,8 @@ class Layer:
     up: QuantizedLinear | None = None
     down: QuantizedLinear | None = None
     # MoE
-    router_logits: torch.Tensor | None = None   # synthetic fp32 [T, E] (Zipf-skewed), per layer
+    router: QuantizedLinear | None = None       # [E + 1, H]: E router rows, then the shared-expert gate row
+    router_skew: torch.Tensor | None = None     # fp32 [E]: synthetic Zipf popularity added to the router logits
     expert_gate_up: QuantizedLinear | None = None   # [E, 2F, K/8] fused [gate | up]
     expert_down: QuantizedLinear | None = None      # [E, H, F/8]
     shared_gate: QuantizedLinear | None = None
@@ -142,6 +144,13 @@ class VerifyModel:
                       o=QuantizedLinear.random(c.hidden, c.n_heads * c.head_dim, gs, generator=gen, device=device),
                       post_norm=_norm_weight(c.hidden, gen, device))
             if c.n_experts:
+                # Small router weights (logits ~ +-1) so the Zipf skew sets the
+                # experts' popularity; rank r (a per-layer permutation) gets
+                # -s * log(r).
+                L.router = QuantizedLinear.random(c.n_experts + 1, c.hidden, gs, generator=gen, device=device,
+                                                  scale_std=0.002, bias_std=0.001)
+                rank = torch.randperm(c.n_experts, generator=gen, device=device).to(torch.float32) + 1.0
+                L.router_skew = (-c.router_zipf_s * torch.log(rank)).contiguous()
                 L.expert_gate_up = QuantizedLinear.random(2 * c.expert_ffn, c.hidden, gs, generator=gen,
                                                           device=device, experts=c.n_experts)
                 L.expert_down = QuantizedLinear.random(c.hidden, c.expert_ffn, gs, generator=gen, device=device,
@@ -161,7 +170,7 @@ class VerifyModel:
         # q|k|v also in RoPE tile order for the fused RoPE epilogue.
         rope_order = rope_row_order(c.n_heads + 2 * c.n_kv_heads, c.head_dim)
         for L in self.layers:
-            for q in (L.qkv, L.o, L.gate, L.up, L.down, L.shared_gate, L.shared_up, L.shared_down):
+            for q in (L.qkv, L.o, L.gate, L.up, L.down, L.router, L.shared_gate, L.shared_up, L.shared_down):
                 if q is not None:
                     q.pack()
                     q.pack(layout=2)
@@ -172,20 +181,7 @@ class VerifyModel:
         self.k_cache: list[torch.Tensor] = []
         self.v_cache: list[torch.Tensor] = []
         self.cap = 0
-        # One persistent kernel per dense layer for up to 4 rows
-        # (mtp_verify_layer) instead of six kernels; off unless
-        # MTPLX_AMD_FUSED_LAYER=1: its grid barriers (~3 us each under load)
-        # still cost more than the kernel boundaries they replace.
-        self.fused_layer = os.environ.get("MTPLX_AMD_FUSED_LAYER", "0") == "1"
-        self._layer_sync = None
-
-    def layer_sync_error(self) -> bool:
-        """True if a fused layer's grid barrier gave up waiting (that step's
-        results are invalid). Synchronises with the device."""
-        if self._layer_sync is None:
-            return False
-        words = self._layer_sync[: 4 * (_lib.LAYER_SYNC_ERROR_WORD + 1)].view(torch.int32)
-        return bool(words[_lib.LAYER_SYNC_ERROR_WORD].item())
+        self._status: torch.Tensor | None = None
 
     # -- cache ----------------------------------------------------------------
     def allocate_cache(self, batch: int, capacity: int, *, fill_random: bool = True) -> None:
@@ -213,23 +209,27 @@ class VerifyModel:
     def v_cache_standard(self, li: int) -> torch.Tensor:
         return kv_from_blocks(self.v_cache[li], "v")
 
-    def synthetic_router_logits(self, tokens: int) -> None:
-        """Per-layer router logits skewed Zipf(s) over experts: logit_e = -s*log(rank_e)
-        with a per-layer random expert ranking plus N(0, 0.5) noise per token."""
-        c = self.cfg
-        for L in self.layers:
-            perm = torch.randperm(c.n_experts, generator=self.gen, device=self.device)
-            base = -c.router_zipf_s * torch.log(torch.arange(1, c.n_experts + 1, device=self.device,
-                                                             dtype=torch.float32))
-            lg = base[perm][None, :] + 0.5 * torch.randn((tokens, c.n_experts), generator=self.gen,
-                                                         device=self.device)
-            L.router_logits = lg.contiguous()
+    def status(self) -> torch.Tensor | None:
+        """The last forward's device status word (int32 [1]): bit 0 is set when
+        a token id was outside the vocabulary (its embedding row reads as zero)
+        or a K/V write fell outside the cache capacity (skipped; attention then
+        stops at the capacity). Nonzero means that forward's logits are invalid."""
+        return self._status
+
+    def check_status(self) -> None:
+        """Raise :class:`MtpError` if the last forward flagged its status word
+        (synchronises with the device)."""
+        if self._status is not None and int(self._status.item()) != 0:
+            raise _lib.MtpError("verify_logits", -1, "token id outside the vocabulary or a K/V position outside "
+                                "the cache capacity (status word set)")
 
     # -- forward --------------------------------------------------------------
     def verify_logits(self, tokens: torch.Tensor, q_start: torch.Tensor, q_lens: torch.Tensor | None = None,
-                      *, logits_out: torch.Tensor | None = None) -> torch.Tensor:
+                      *, logits_out: torch.Tensor | None = None, check: bool = False) -> torch.Tensor:
         """``tokens`` int32 ``[B, L]`` (GPU), ``q_start`` int32 ``[B]`` (GPU):
-        writes K/V of the L rows at ``q_start[b] + i`` and returns fp32 logits ``[B*L, V]``."""
+        writes K/V of the L rows at ``q_start[b] + i`` and returns fp32 logits ``[B*L, V]``.
+        The device status word (:meth:`status`) flags invalid tokens or
+        positions; ``check=True`` synchronises and raises on it."""
         c = self.cfg
         B, Lq = (int(s) for s in tokens.shape)
         M = B * Lq
@@ -276,32 +276,7 @@ class VerifyModel:
         def W(q):
             return q.packed_mf16 if lay == 2 else q.packed
 
-        # Dense layers with up to 4 rows run as one persistent kernel each
-        # (mtp_verify_layer): h -> h1 = h + o(attn) -> h = h1 + down(act).
-        fused = self.fused_layer and lay == 2 and not c.n_experts and c.head_dim == 128
-        if fused:
-            h1 = torch.empty_like(h)
-            sync = _lib.WORKSPACES.get(_lib.query("mtp_verify_layer_sync_bytes"), "layer_sync", dev)
-            self._layer_sync = sync
         for li, L in enumerate(self.layers):
-            if fused:
-                rope = dict(q_start=q_start, q_lens=ql, q_out=qh, k_cache=self.k_cache[li], v_cache=self.v_cache[li],
-                            status=status, L=Lq, Hq=c.n_heads, Hkv=c.n_kv_heads, D=c.head_dim, cap=self.cap,
-                            blocked=1, rope_base=c.rope_theta)
-                _lib.verify_layer(
-                    st, rope=rope,
-                    qkv=dict(x=h, x2=L.in_norm, ss_in=ss_h, eps=c.rms_eps, w0=L.qkv_rope2, M=M, N=c.qkv_out, K=H,
-                             group_size=gs, xmode=2, emode=4, packed=2),
-                    o=dict(x=attn, w0=L.o.packed_mf16, resid=h, y0=h1, ss_out=ss_a, M=M, N=H,
-                           K=c.n_heads * c.head_dim, group_size=gs, xmode=0, emode=1, packed=2),
-                    gate_up=dict(x=h1, x2=L.post_norm, ss_in=ss_a, eps=c.rms_eps, w0=L.gate.packed_mf16,
-                                 w1=L.up.packed_mf16, y0=act, y_sums=act_sums, M=M, N=c.ffn, K=H, group_size=gs,
-                                 xmode=2, emode=3, packed=2, ws=qws, ws_bytes=qws.numel()),
-                    down=dict(x=act, x_sums=act_sums, w0=L.down.packed_mf16, resid=h1, y0=h, ss_out=ss_b, M=M, N=H,
-                              K=c.ffn, group_size=gs, xmode=3, emode=1, packed=2),
-                    attn_out=attn, attn_scale=scale, attn_ws=aws, sync=sync)
-                ss_h = ss_b
-                continue
             xin = dict(x=h, x2=L.in_norm, xmode=2)   # input RMSNorm fused into the staging
             if fused_rope:
                 rope = dict(q_start=q_start, q_lens=ql, q_out=qh, k_cache=self.k_cache[li], v_cache=self.v_cache[li],
@@ -322,7 +297,7 @@ class VerifyModel:
                 group_size=gs, xmode=0, emode=1, packed=lay)
             ss_h = ss_a
             if c.n_experts:
-                self._moe_block(L, h, M, st)
+                self._moe_block(L, h, M, st, qmv, lay)
                 ss_h = None
             else:
                 qmv(st, x=h, x2=L.post_norm, ss_in=ss_h, eps=c.rms_eps, w0=W(L.gate), w1=W(L.up), y0=act,
@@ -334,23 +309,33 @@ class VerifyModel:
         qmv(st, x=h, x2=self.final_norm, ss_in=ss_h, eps=c.rms_eps, w0=W(self.lm_head), yf=logits, M=M,
             N=c.vocab, K=H, group_size=gs, xmode=2, emode=0, packed=lay)
         self._status = status
+        if check:
+            self.check_status()
         return logits
 
-    def _moe_block(self, L: Layer, h: torch.Tensor, M: int, st: int) -> None:
-        """Routed experts (sorted chain, ``mtplx/models/qwen4_exp.py:1544-1577``) + shared expert."""
+    def _moe_block(self, L: Layer, h: torch.Tensor, M: int, st: int, qmv, lay: int) -> None:
+        """The sparse block on the post-attention norm of ``h``, added to ``h``
+        in place: routed experts through the sorted chain
+        (``mtplx/models/qwen4_exp.py:1544-1577``) plus the sigmoid-gated shared
+        expert (``:1438-1445``)."""
         c = self.cfg
         call = _lib.call
         gs = c.group_size
-        eps = ctypes.c_float(c.rms_eps)
         dev = h.device
         H = c.hidden
+        E = c.n_experts
         xn = torch.empty_like(h)
         call("mtp_rmsnorm", h.data_ptr(), L.post_norm.data_ptr(), xn.data_ptr(), M, H, c.rms_eps, st)
+        # Router logits (bf16-rounded, fp32 storage) [M, E+1]; column E is the
+        # shared-expert gate's pre-activation.
+        rl = torch.empty((M, E + 1), dtype=torch.float32, device=dev)
+        Wr = L.router.packed_mf16 if lay == 2 else L.router.packed
+        qmv(st, x=xn, w0=Wr, yf=rl, M=M, N=E + 1, K=H, group_size=gs, xmode=0, emode=0, packed=lay)
         ids = torch.empty((M, c.top_k), dtype=torch.int32, device=dev)
         wts = torch.empty((M, c.top_k), dtype=torch.float32, device=dev)
-        call("mtp_moe_route", L.router_logits[:M].data_ptr(), M, c.n_experts, c.top_k, ids.data_ptr(),
+        call("mtp_moe_route", rl.data_ptr(), E + 1, L.router_skew.data_ptr(), M, E, c.top_k, ids.data_ptr(),
              wts.data_ptr(), st)
-        es = expert_sort(ids, c.n_experts)
+        es = expert_sort(ids, E)
         R = M * c.top_k
         F = c.expert_ffn
         hsorted = torch.empty((R, F), dtype=torch.bfloat16, device=dev)
@@ -367,17 +352,18 @@ class VerifyModel:
         call("mtp_gather_qmv_affine4", hsorted.data_ptr(), None, None, es.expert_off.data_ptr(),
              es.active.data_ptr(), dn.weight.data_ptr(), dn.scales.data_ptr(), dn.biases.data_ptr(), None, None,
              None, ysorted.data_ptr(), M, c.n_experts, H, F, gs, 0, 0, H, None, 0, st)
-        # shared expert on the normalised rows, then h += routed + shared
+        # Shared expert (SwiGLU MLP) on the normalised rows, then one combine:
+        # h = h + bf16(routed + bf16(sigmoid(gate) * shared)).
+        def W(q):
+            return q.packed_mf16 if lay == 2 else q.packed
+
         sh_act = torch.empty((M, c.shared_ffn), dtype=torch.bfloat16, device=dev)
-        call("mtp_qmv_affine4_dual", xn.data_ptr(), L.shared_gate.weight.data_ptr(), L.shared_gate.scales.data_ptr(),
-             L.shared_gate.biases.data_ptr(), L.shared_up.weight.data_ptr(), L.shared_up.scales.data_ptr(),
-             L.shared_up.biases.data_ptr(), sh_act.data_ptr(), None, M, c.shared_ffn, H, gs, 1, None, 0, st)
+        qmv(st, x=xn, w0=W(L.shared_gate), w1=W(L.shared_up), y0=sh_act, M=M, N=c.shared_ffn, K=H, group_size=gs,
+            xmode=0, emode=3, packed=lay)
         shared = torch.empty_like(h)
-        call("mtp_qmv_affine4_residual", sh_act.data_ptr(), L.shared_down.weight.data_ptr(),
-             L.shared_down.scales.data_ptr(), L.shared_down.biases.data_ptr(), h.data_ptr(), shared.data_ptr(), None,
-             M, H, c.shared_ffn, gs, None, 0, st)
-        out = moe_combine(ysorted, es, wts, shared)
-        h.copy_(out)
+        qmv(st, x=sh_act, w0=W(L.shared_down), y0=shared, M=M, N=H, K=c.shared_ffn, group_size=gs, xmode=0,
+            emode=0, packed=lay)
+        moe_combine(ysorted, es, wts, shared, shared_gate=rl[:, E], resid=h, out=h)
 
     def verify_step(self, tokens: torch.Tensor, q_start: torch.Tensor, draft_logits: torch.Tensor,
                     uniforms: torch.Tensor, sampler: SamplerConfig = SamplerConfig()):

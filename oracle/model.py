@@ -7,9 +7,22 @@ o_proj + residual, post-attention RMSNorm, SwiGLU MLP + residual; final norm
 and lm_head). Values are rounded to bf16 wherever the GPU path stores a bf16
 tensor, so the comparison isolates arithmetic error, not storage format.
 
-Parity pins (tests/test_oracle_model.py): a zero-layer model reduces to
-norm + lm_head of the embedding; RoPE at position 0 is the identity and
-preserves norms; the attention and qmv pieces are pinned in their own files.
+The MoE layer follows the reference's verify call of the sparse block
+(``mtplx/models/qwen4_exp.py:1416-1445`` ``_verify_call``, routed chain
+``:1544-1577``): router logits (bf16, a quantized projection whose last row
+is the shared-expert gate) plus the synthetic per-expert Zipf skew pick the
+top-k experts (value desc, id asc) with softmax weights renormalised over the
+k; routed rows go through the sorted SwiGLU chain; the shared expert is
+``sigmoid(gate) * shared_mlp(x)``; the block output ``routed + shared`` is
+added to the residual stream.
+
+Parity pins (tests/test_oracle_model.py): a zero-layer model equals a
+closed form of norm + lm_head over the embedding rows; a layer whose o and
+down projections are zero leaves the residual stream unchanged, so its
+logits equal the zero-layer ones; one dense and one MoE layer equal an
+independent scalar-loop restatement of the decoder layer; RoPE at position 0
+is the identity and preserves norms; the attention and qmv pieces are pinned
+in their own files.
 """
 
 from __future__ import annotations
@@ -40,11 +53,12 @@ def rope_rotate_half(x: np.ndarray, pos: np.ndarray, base: float) -> np.ndarray:
 
 
 def verify_forward(params: dict, cfg, tokens: np.ndarray, q_start: np.ndarray, k_cache: list, v_cache: list,
-                   router: list | None = None) -> np.ndarray:
+                   routes: list | None = None) -> np.ndarray:
     """Logits [B*L, V] (float64 of bf16 values). ``params`` holds numpy copies of
     the GPU model (bf16 values as float64, weight triples for 4-bit layers).
     ``k_cache``/``v_cache`` are per-layer float64 arrays [B, Hkv, cap, D],
-    updated in place at ``q_start[b] + i``."""
+    updated in place at ``q_start[b] + i``. ``routes``, if a list, receives
+    each MoE layer's ``(ids, weights)``."""
     B, L = tokens.shape
     M = B * L
     gs = cfg.group_size
@@ -68,13 +82,20 @@ def verify_forward(params: dict, cfg, tokens: np.ndarray, q_start: np.ndarray, k
         h = round_to_bf16(round_to_bf16(qmm_affine4(att, *lay["o"], gs)) + h)
         xn = round_to_bf16(rmsnorm(h, lay["post_norm"], cfg.rms_eps))
         if cfg.n_experts:
-            ids, wts = router[li]
-            routed = moe_forward(xn, ids, wts, lay["expert_gate_up"], lay["expert_down"], gs)
+            E = cfg.n_experts
+            rl = round_to_bf16(qmm_affine4(xn, *lay["router"], gs))          # [M, E + 1]
+            logits = (rl[:, :E].astype(np.float32) + np.asarray(lay["router_skew"], np.float32)[None, :])
+            ids, wts = route_topk(logits.astype(np.float64), cfg.top_k)
+            if routes is not None:
+                routes.append((ids, wts))
+            routed = round_to_bf16(moe_forward(xn, ids, wts, lay["expert_gate_up"], lay["expert_down"], gs))
             sg = round_to_bf16(qmm_affine4(xn, *lay["shared_gate"], gs))
             su = round_to_bf16(qmm_affine4(xn, *lay["shared_up"], gs))
             sa = round_to_bf16(round_to_bf16(silu(sg)) * su)
-            shared = round_to_bf16(round_to_bf16(qmm_affine4(sa, *lay["shared_down"], gs)) + h)
-            h = round_to_bf16(round_to_bf16(routed) + shared)
+            sd = round_to_bf16(qmm_affine4(sa, *lay["shared_down"], gs))
+            gate = 1.0 / (1.0 + np.exp(-rl[:, E]))
+            shared = round_to_bf16(gate[:, None] * sd)
+            h = round_to_bf16(h + round_to_bf16(routed + shared))
         else:
             g = round_to_bf16(qmm_affine4(xn, *lay["gate"], gs))
             u = round_to_bf16(qmm_affine4(xn, *lay["up"], gs))

@@ -6,8 +6,12 @@ for the per-depth accept, ``:16085-16110`` for the all-accept bonus), with
 NumPy's weighted ``Generator.choice`` written out as the cdf/searchsorted rule
 the reference documents (``mtplx/qwen4_draft_device_chain.py:294-305``).
 
+Penalties: the host law (``apply_penalties``, fp64) and the runtime's
+device twin (``apply_penalties_f32``, fp32 deltas), which the GPU path
+follows.
+
 Parity pins (tests/test_oracle_sampler.py): the reference's own known-answer
-tests (``tests/test_sampling.py:22-103``) re-expressed; ``choice`` checked
+tests (``tests/test_sampling.py:22-103``) re-expressed; penalty closed forms; ``choice`` checked
 against ``numpy.random.Generator.choice`` draw for draw; the output-marginal
 law (``mtplx/sampling.py:372-391``) and exhaustive enumeration of draft paths
 on a tiny vocabulary (the method of ``tests/test_block_verify_exact_law.py``).
@@ -31,6 +35,51 @@ class SamplerConfig:
     temperature: float = 0.6
     top_p: float = 0.95
     top_k: int = 20
+
+
+PENALTY_MIN, PENALTY_MAX = -2.0, 2.0
+
+
+def apply_penalties(logits: np.ndarray, token_counts, presence: float = 0.0, frequency: float = 0.0,
+                    overlay=None) -> np.ndarray:
+    """Host law ``mtplx/sampling.py:212-256``: in fp64, ``l[j] -= frequency *
+    count[j] + presence * (count[j] > 0)`` (penalties clamped to [-2, 2]),
+    then ``l[j] -= overlay[j]``; a no-op (same array) when nothing is active."""
+    pres = float(np.clip(presence, PENALTY_MIN, PENALTY_MAX))
+    freq = float(np.clip(frequency, PENALTY_MIN, PENALTY_MAX))
+    counts_on = bool(token_counts) and (pres != 0.0 or freq != 0.0)
+    if not counts_on and not overlay:
+        return logits
+    out = np.array(logits, dtype=np.float64, copy=True)
+    if counts_on:
+        ids = np.fromiter(token_counts.keys(), dtype=np.int64, count=len(token_counts))
+        c = np.fromiter(token_counts.values(), dtype=np.float64, count=len(token_counts))
+        out[ids] -= freq * c + pres * (c > 0)
+    if overlay:
+        ids = np.fromiter(overlay.keys(), dtype=np.int64, count=len(overlay))
+        out[ids] -= np.fromiter(overlay.values(), dtype=np.float64, count=len(overlay))
+    return out
+
+
+def apply_penalties_f32(logits: np.ndarray, token_counts, presence: float = 0.0, frequency: float = 0.0,
+                        overlay=None) -> np.ndarray:
+    """The runtime's device twin ``mtplx/fast_sampling.py:42-81``
+    (``apply_penalties_mlx``): the same deltas computed in fp64, cast to fp32,
+    and added negated to the fp32 logits in fp32 (counts first, then the
+    overlay, each one rounding)."""
+    pres = float(np.clip(presence, PENALTY_MIN, PENALTY_MAX))
+    freq = float(np.clip(frequency, PENALTY_MIN, PENALTY_MAX))
+    counts_on = bool(token_counts) and (pres != 0.0 or freq != 0.0)
+    out = np.array(logits, dtype=np.float32, copy=True)
+    if counts_on:
+        ids = np.fromiter(token_counts.keys(), dtype=np.int64, count=len(token_counts))
+        c = np.fromiter(token_counts.values(), dtype=np.float64, count=len(token_counts))
+        out[ids] = out[ids] + (-(freq * c + pres * (c > 0.0)).astype(np.float32))
+    if overlay:
+        ids = np.fromiter(overlay.keys(), dtype=np.int64, count=len(overlay))
+        v = np.fromiter(overlay.values(), dtype=np.float64, count=len(overlay)).astype(np.float32)
+        out[ids] = out[ids] + (-v)
+    return out
 
 
 def softmax(logits: np.ndarray, temperature: float = 1.0) -> np.ndarray:
@@ -90,8 +139,11 @@ def apply_top_p_top_k(probs: np.ndarray, top_p: float = 1.0, top_k: int = 0) -> 
     return filtered / total
 
 
-def distribution_from_logits(logits: np.ndarray, config: SamplerConfig) -> np.ndarray:
-    """Dense law ``mtplx/sampling.py:259-276`` (penalties at their no-op default)."""
+def distribution_from_logits(logits: np.ndarray, config: SamplerConfig, token_counts=None, presence: float = 0.0,
+                             frequency: float = 0.0, overlay=None) -> np.ndarray:
+    """Dense law ``mtplx/sampling.py:259-276``: penalties (host law) on the raw
+    logits, softmax with temperature, then top-p / top-k."""
+    logits = apply_penalties(logits, token_counts, presence, frequency, overlay)
     return apply_top_p_top_k(softmax(logits, config.temperature), config.top_p, config.top_k)
 
 

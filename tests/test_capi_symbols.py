@@ -41,11 +41,14 @@ def test_size_queries_without_gpu(lib):
     lib.mtp_sampler_workspace_bytes.restype = ctypes.c_size_t
     lib.mtp_attn_workspace_bytes.restype = ctypes.c_size_t
     lib.mtp_qmv_workspace_bytes.restype = ctypes.c_size_t
-    assert lib.mtp_sampler_workspace_bytes(7, 151936) == 7 * 38 * 536
+    assert lib.mtp_sampler_workspace_bytes(7, 151936, 20) == (7 * 38 * 536 + 255) // 256 * 256
+    # wide laws (top_k 0 or > 64): per row an id/prob law and a residual area
+    row = ((16 + 4 * 151936 + 15) // 16 * 16 + 8 * 151936 + 255) // 256 * 256
+    assert lib.mtp_sampler_workspace_bytes(7, 151936, 0) == (7 * 38 * 536 + 255) // 256 * 256 + 2 * 7 * row
     assert lib.mtp_attn_workspace_bytes(8, 8, 32768, 0) == 8 * 8 * 32 * (32 * 128 + 64) * 4
-    # stream-K: two fp32 [8][64] partials per workgroup (one workgroup per CU,
-    # 256 when no device is visible, as here), then one arrival counter per
-    # 32-column tile (256-B aligned).
+    # tail split: two fp32 [8][64] partials per CU (256 when no device is
+    # visible, as here), then one arrival counter per 32-column tile
+    # (256-B aligned).
     counters = (17408 // 32 * 4 + 255) // 256 * 256
     assert lib.mtp_qmv_workspace_bytes(4, 17408, 5120, 0) == 2 * 256 * 8 * 64 * 4 + counters
 

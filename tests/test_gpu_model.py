@@ -6,7 +6,7 @@ import pytest
 import torch
 
 from oracle import sampler as S
-from oracle.model import route_topk, verify_forward
+from oracle.model import verify_forward
 from tests.gpu_util import assert_close
 from tests.model_util import model_params_numpy
 
@@ -17,10 +17,6 @@ def _run(cfg, B, L, starts, seed, moe_tokens=None):
     from mtplx_amd.verify_step import VerifyModel
     model = VerifyModel(cfg, device="cuda", seed=seed)
     model.allocate_cache(B, 320)
-    router = None
-    if cfg.n_experts:
-        model.synthetic_router_logits(B * L)
-        router = [route_topk(Lr.router_logits.cpu().numpy(), cfg.top_k) for Lr in model.layers]
     kc = [model.k_cache_standard(li).float().cpu().numpy().astype(np.float64) for li in range(cfg.layers)]
     vc = [model.v_cache_standard(li).float().cpu().numpy().astype(np.float64) for li in range(cfg.layers)]
     gen = torch.Generator(device="cuda").manual_seed(seed + 1)
@@ -28,7 +24,7 @@ def _run(cfg, B, L, starts, seed, moe_tokens=None):
     qs = torch.tensor(starts, dtype=torch.int32, device="cuda")
     logits = model.verify_logits(tokens, qs)
     torch.cuda.synchronize()
-    want = verify_forward(model_params_numpy(model), cfg, tokens.cpu().numpy(), np.array(starts), kc, vc, router)
+    want = verify_forward(model_params_numpy(model), cfg, tokens.cpu().numpy(), np.array(starts), kc, vc)
     return model, tokens, logits, want, kc, vc
 
 
@@ -36,12 +32,12 @@ def test_dense_verify_step_matches_oracle(gpu):
     from mtplx_amd.verify_step import DecoderConfig
     cfg = DecoderConfig(layers=2, hidden=512, ffn=1024, n_heads=8, n_kv_heads=2, head_dim=128, vocab=4096)
     model, tokens, logits, want, kc, vc = _run(cfg, 2, 4, [37, 200], 3)
-    assert_close(logits.cpu().numpy().astype(np.float64), want, rtol=3e-2, atol=3e-2, what="dense logits")
+    assert_close(logits.cpu().numpy().astype(np.float64), want, rtol=1e-2, atol=1e-2, what="dense logits")
     # the K/V rows the step wrote are the oracle's (RoPE'd k, raw v) within bf16 tolerance
     for li in range(cfg.layers):
         got_k = model.k_cache_standard(li).float().cpu().numpy()
         for b, s in enumerate([37, 200]):
-            assert_close(got_k[b, :, s:s + 4], kc[li][b, :, s:s + 4], rtol=2e-2, atol=2e-2, what="k rows")
+            assert_close(got_k[b, :, s:s + 4], kc[li][b, :, s:s + 4], rtol=1e-2, atol=1e-2, what="k rows")
     # accept/reject on the GPU logits is token-exact against the oracle law
     from mtplx_amd.sampling import SamplerConfig, spec_accept
     B, L = 2, 4
@@ -63,4 +59,26 @@ def test_moe_verify_step_matches_oracle(gpu):
     cfg = DecoderConfig(layers=2, hidden=512, ffn=0, n_heads=8, n_kv_heads=2, head_dim=128, vocab=2048,
                         n_experts=16, top_k=4, expert_ffn=256, shared_ffn=256)
     model, tokens, logits, want, kc, vc = _run(cfg, 2, 4, [10, 150], 7)
-    assert_close(logits.cpu().numpy().astype(np.float64), want, rtol=3e-2, atol=3e-2, what="moe logits")
+    assert_close(logits.cpu().numpy().astype(np.float64), want, rtol=1e-2, atol=1e-2, what="moe logits")
+
+
+def test_status_word_flags_bad_token_and_position(gpu):
+    """An out-of-vocabulary token and a K/V write past the cache capacity set
+    the forward's status word; check=True raises instead of returning logits
+    that look valid."""
+    from mtplx_amd import _lib
+    from mtplx_amd.verify_step import DecoderConfig, VerifyModel
+    cfg = DecoderConfig(layers=1, hidden=512, ffn=1024, n_heads=8, n_kv_heads=2, head_dim=128, vocab=1024)
+    model = VerifyModel(cfg, device="cuda", seed=4)
+    model.allocate_cache(1, 256)
+    ok = torch.tensor([[1, 2, 3, 4]], dtype=torch.int32, device="cuda")
+    model.verify_logits(ok, torch.tensor([10], dtype=torch.int32, device="cuda"), check=True)
+    assert int(model.status().item()) == 0
+    bad_tok = torch.tensor([[1, 2, cfg.vocab + 5, 4]], dtype=torch.int32, device="cuda")
+    with pytest.raises(_lib.MtpError):
+        model.verify_logits(bad_tok, torch.tensor([10], dtype=torch.int32, device="cuda"), check=True)
+    model.verify_logits(ok, torch.tensor([model.cap - 2], dtype=torch.int32, device="cuda"))
+    torch.cuda.synchronize()
+    assert int(model.status().item()) != 0
+    with pytest.raises(_lib.MtpError):
+        model.check_status()

@@ -1,0 +1,97 @@
+"""GPU parity of the composed verify step at the BASELINE shapes against the
+float64 oracle (``oracle.model.verify_forward``), at the north-star bf16 bar
+rtol = atol = 1e-2:
+
+* cfg3 width: two dense layers of the 27B shape (hidden 5120, SwiGLU 17408,
+  40/8 heads of 128, vocab 151936), one request, 4 verify rows at positions
+  4092..4095 of a 4096-token context;
+* cfg5 width: one MoE layer of the 125B-class shape (hidden 4096, 256
+  experts top-8 of FFN 1536 plus a shared expert, 32/4 heads, vocab 151936),
+  4 requests x 4 rows at 8k contexts, Zipf-skewed routing.
+
+The accept/reject on the produced logits is token-exact against the oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampler as S
+from oracle.model import verify_forward
+from tests.gpu_util import assert_close
+from tests.model_util import model_params_numpy
+
+pytestmark = pytest.mark.gpu
+
+
+def assert_rope_close(got, want, D=128, what="k rows"):
+    """RoPE'd rows: each rotate-half pair (d, d + D/2) is a rotation of the
+    bf16-rounded projection, so the error scales with the pair's norm, not
+    with the (possibly cancelled) component: |got - want| <= 1e-2 * |pair| + 1e-2."""
+    half = D // 2
+    r = np.sqrt(want[..., :half] ** 2 + want[..., half:] ** 2)
+    r = np.concatenate([r, r], axis=-1)
+    bad = np.abs(got - want) > 1e-2 + 1e-2 * r
+    if bad.any():
+        idx = np.argwhere(bad)[:5]
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outside 1e-2 of the pair norm; first "
+                             f"{idx.tolist()} got {got[tuple(idx[0])]} want {want[tuple(idx[0])]}")
+
+
+def _caches(model, layers):
+    kc = [model.k_cache_standard(li).float().cpu().numpy().astype(np.float64) for li in range(layers)]
+    vc = [model.v_cache_standard(li).float().cpu().numpy().astype(np.float64) for li in range(layers)]
+    return kc, vc
+
+
+def test_cfg3_width_two_layers_match_oracle(gpu):
+    from mtplx_amd.verify_step import DENSE_27B, VerifyModel
+    from dataclasses import replace
+    cfg = replace(DENSE_27B, layers=2)
+    model = VerifyModel(cfg, device="cuda", seed=17)
+    model.allocate_cache(1, 4096)
+    kc, vc = _caches(model, cfg.layers)
+    gen = torch.Generator(device="cuda").manual_seed(18)
+    tokens = torch.randint(0, cfg.vocab, (1, 4), device="cuda", dtype=torch.int32, generator=gen)
+    qs = torch.tensor([4092], dtype=torch.int32, device="cuda")
+    logits = model.verify_logits(tokens, qs, check=True)
+    got = logits.cpu().numpy().astype(np.float64)
+    want = verify_forward(model_params_numpy(model), cfg, tokens.cpu().numpy(), np.array([4092]), kc, vc)
+    assert_close(got, want, rtol=1e-2, atol=1e-2, what="cfg3-width logits")
+    for li in range(cfg.layers):
+        k = model.k_cache_standard(li).float().cpu().numpy()
+        v = model.v_cache_standard(li).float().cpu().numpy()
+        assert_rope_close(k[0, :, 4092:4096], kc[li][0, :, 4092:4096])
+        assert_close(v[0, :, 4092:4096], vc[li][0, :, 4092:4096], rtol=1e-2, atol=1e-2, what="v rows")
+    # accept/reject at the full vocabulary, token-exact against the oracle law
+    from mtplx_amd.sampling import SamplerConfig, spec_accept
+    draft = (logits[:3] + 0.5 * torch.randn((3, cfg.vocab), device="cuda", generator=gen)).contiguous()
+    u = torch.rand((1, 4), device="cuda", dtype=torch.float64, generator=gen)
+    res = spec_accept(logits.reshape(1, 4, -1), draft.reshape(1, 3, -1), tokens[:, 1:], u, SamplerConfig())
+    w = S.spec_accept(got.astype(np.float32), draft.cpu().numpy(), tokens[0, 1:].cpu().numpy(), u[0].cpu().numpy(),
+                      S.SamplerConfig())
+    assert res.tokens[0].cpu().numpy().tolist()[: len(w.tokens)] == w.tokens
+    assert int(res.n_accepted[0]) == w.n_accepted
+
+
+def test_cfg5_width_moe_layer_matches_oracle(gpu):
+    from mtplx_amd.verify_step import MOE_125B, VerifyModel
+    from dataclasses import replace
+    cfg = replace(MOE_125B, layers=1)
+    model = VerifyModel(cfg, device="cuda", seed=23)
+    B, L, ctx = 4, 4, 8192
+    model.allocate_cache(B, ctx)
+    kc, vc = _caches(model, cfg.layers)
+    gen = torch.Generator(device="cuda").manual_seed(24)
+    tokens = torch.randint(0, cfg.vocab, (B, L), device="cuda", dtype=torch.int32, generator=gen)
+    starts = [ctx - L, ctx - L - 100, ctx - L - 1000, 5000]
+    qs = torch.tensor(starts, dtype=torch.int32, device="cuda")
+    logits = model.verify_logits(tokens, qs, check=True)
+    got = logits.cpu().numpy().astype(np.float64)
+    routes = []
+    want = verify_forward(model_params_numpy(model), cfg, tokens.cpu().numpy(), np.array(starts), kc, vc, routes)
+    assert_close(got, want, rtol=1e-2, atol=1e-2, what="cfg5-width logits")
+    ids = routes[0][0]
+    # Zipf skew: a few experts take many of the 128 routed rows
+    counts = np.bincount(ids.reshape(-1), minlength=cfg.n_experts)
+    assert counts.max() >= 4 and (counts > 0).sum() < 128

@@ -48,34 +48,109 @@ def test_route_matches_oracle(gpu):
     wi, ww = route_topk(lg, 8)
     assert ids.cpu().numpy().tolist() == wi.tolist()
     assert np.allclose(w.cpu().numpy(), ww, atol=1e-6)
+    # strided logits ([T, E+1] router output) plus a per-expert skew, added in fp32
+    full = rng.normal(size=(16, 257)).astype(np.float32)
+    skew = (-1.1 * np.log(1.0 + rng.permutation(256))).astype(np.float32)
+    ids, w = route(torch.from_numpy(full).cuda(), 8, skew=torch.from_numpy(skew).cuda(), n_experts=256)
+    wi, ww = route_topk((full[:, :256] + skew[None, :]).astype(np.float64), 8)
+    assert ids.cpu().numpy().tolist() == wi.tolist()
+    assert np.allclose(w.cpu().numpy(), ww, atol=1e-6)
 
 
-def test_gathered_swiglu_down_and_combine(gpu):
-    from mtplx_amd.moe_sorted_gather import expert_sort, moe_combine, swiglu_rows, switch_linear
-    from mtplx_amd.quant import QuantizedLinear
-    rng = np.random.default_rng(3)
-    E, H, F, T, k = 12, 512, 256, 16, 4
+def test_segments_from_sorted_ids(gpu):
+    from mtplx_amd.moe_sorted_gather import segments
+    ids = np.array([0, 0, 3, 3, 3, 7, 9, 9], np.int32)
+    off, act = segments(torch.from_numpy(ids).cuda(), 10)
+    assert off.cpu().numpy().tolist() == OM.expert_offsets(ids, 10).tolist()
+    a = act.cpu().numpy()
+    assert a[0] == 4 and a[1:5].tolist() == [0, 3, 7, 9]
+    _, act = segments(torch.tensor([0, 2, 1], dtype=torch.int32, device="cuda"), 4)
+    assert int(act[0]) == -1
+    _, act = segments(torch.tensor([0, 4], dtype=torch.int32, device="cuda"), 4)
+    assert int(act[0]) == -1
+
+
+def _experts(rng, E, H, F):
     gu = make_affine4_weights(rng, E * 2 * F, H)
     gu = tuple(a.reshape(E, 2 * F, -1) for a in gu)
     dn = make_affine4_weights(rng, E * H, F)
     dn = tuple(a.reshape(E, H, -1) for a in dn)
+    return gu, dn
+
+
+def test_gathered_swiglu_down_and_combine(gpu):
+    """The ExpertSort fast path (what the verify step uses)."""
+    from mtplx_amd.moe_sorted_gather import expert_sort, moe_combine, swiglu_rows, switch_linear
+    from mtplx_amd.quant import QuantizedLinear
+    rng = np.random.default_rng(3)
+    E, H, F, T, k = 12, 512, 256, 16, 4
+    gu, dn = _experts(rng, E, H, F)
     x = randn_bf16(rng, (T, H))
     idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
     sc = rng.random((T, k)).astype(np.float32)
     es = expert_sort(torch.from_numpy(idx).cuda(), E)
     tgu = (u32(gu[0]), from_bits(gu[1]), from_bits(gu[2]))
-    h = swiglu_rows(x.reshape(T, 1, H), es, *tgu, group_size=64)
+    h = swiglu_rows(x.reshape(T, 1, H), es.row_map, *tgu, es.sorted_ids, group_size=64, bits=4, expert_sort=es)
     row_map, sorted_ids, inv, _ = OM.sort_rows(idx)
     want_h = OM.swiglu_rows(bits(x), row_map, sorted_ids, *gu, 64, bf16_storage=True)
     assert_close(bf16_values(h.reshape(-1, F)), want_h, what="swiglu rows")
     down = QuantizedLinear(u32(dn[0]), from_bits(dn[1]), from_bits(dn[2]))
-    y = switch_linear(down, h.reshape(-1, F), es)
+    y = switch_linear(down, h, es.sorted_ids, sorted_indices=True, expert_sort=es).reshape(-1, H)
     want_y = OM.gather_qmm_rows(bits(h.reshape(-1, F)), np.arange(T * k), sorted_ids, *dn, 64)
     assert_close(bf16_values(y), want_y, what="down rows")
-    out = moe_combine(y, es, torch.from_numpy(sc).cuda())
     yv = bf16_values(y)     # the combine is checked on the stored (bf16) expert outputs
-    want_out = (yv[inv.astype(np.int64)].reshape(T, k, H) * sc[:, :, None]).sum(axis=1)
-    assert_close(bf16_values(out), want_out, what="combine")
+    routed = (yv[inv.astype(np.int64)].reshape(T, k, H) * sc[:, :, None]).sum(axis=1)
+    out = moe_combine(y, es, torch.from_numpy(sc).cuda())
+    assert_close(bf16_values(out), routed, what="combine")
+    # gated shared expert + residual: h + bf16(bf16(routed) + bf16(sigmoid(g) * shared))
+    shared = randn_bf16(rng, (T, H))
+    resid = randn_bf16(rng, (T, H))
+    gates = rng.normal(size=(T, 3)).astype(np.float32)
+    out = moe_combine(y, es, torch.from_numpy(sc).cuda(), shared, shared_gate=torch.from_numpy(gates).cuda()[:, 1],
+                      resid=resid)
+    sg = 1.0 / (1.0 + np.exp(-gates[:, 1:2].astype(np.float64)))
+    from oracle.bf16 import round_to_bf16 as rb
+    want = rb(bf16_values(resid) + rb(rb(routed) + rb(sg * bf16_values(shared))))
+    assert_close(bf16_values(out), want, what="gated combine")
+
+
+def test_reference_call_sequence(gpu):
+    """The sorted chain exactly as ``mtplx/models/qwen4_exp.py:1565-1577`` calls
+    it: sort_rows -> swiglu_rows(tokens, row_map, w, s, b, idx, ...) ->
+    switch_linear(down, h, idx, sorted_indices=True) -> unsort (mlx-lm
+    _scatter_unsort) -> score-weighted sum, against the oracle's moe_forward."""
+    from mtplx_amd.moe_sorted_gather import sort_rows, swiglu_rows, switch_linear
+    from mtplx_amd.quant import QuantizedLinear
+    rng = np.random.default_rng(6)
+    E, H, F, T, k = 10, 256, 256, 12, 4
+    gu, dn = _experts(rng, E, H, F)
+    x = randn_bf16(rng, (T, H))
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    sc = rng.random((T, k)); sc /= sc.sum(axis=1, keepdims=True)
+    tokens, row_map, sidx, inv_order = sort_rows(x, torch.from_numpy(idx).cuda())
+    o_row_map, o_sorted, o_inv, _ = OM.sort_rows(idx)
+    assert row_map.cpu().numpy().astype(np.uint32).tolist() == o_row_map.tolist()
+    assert sidx.cpu().numpy().tolist() == o_sorted.astype(np.int64).tolist()
+    assert inv_order.cpu().numpy().tolist() == o_inv.astype(np.int64).tolist()
+    h = swiglu_rows(tokens, row_map, u32(gu[0]), from_bits(gu[1]), from_bits(gu[2]), sidx, group_size=64, bits=4,
+                    mode="affine")
+    assert tuple(h.shape) == (T * k, 1, F)
+    # each stored tensor against the oracle on the same (bf16) inputs
+    want_h = OM.swiglu_rows(bits(x), o_row_map, o_sorted, *gu, 64, bf16_storage=True)
+    assert_close(bf16_values(h.reshape(-1, F)), want_h, what="swiglu_rows")
+    down = QuantizedLinear(u32(dn[0]), from_bits(dn[1]), from_bits(dn[2]))
+    y = switch_linear(down, h, sidx, sorted_indices=True)
+    assert tuple(y.shape) == (T * k, 1, H)
+    want_y = OM.gather_qmm_rows(bits(h.reshape(-1, F)), np.arange(T * k), o_sorted, *dn, 64)
+    assert_close(bf16_values(y.reshape(-1, H)), want_y, what="switch_linear")
+    y_unsorted = y[inv_order.long()].reshape(T, k, 1, H).squeeze(-2)
+    # the unsort puts expert (t, j)'s output at flat row t*k + j
+    yv = bf16_values(y.reshape(-1, H))
+    assert np.array_equal(bf16_values(y_unsorted).reshape(T * k, H), yv[o_inv.astype(np.int64)])
+    # unsorted switch_linear returns rows in the caller's order
+    hs = h.reshape(-1, F)[inv_order.long()].contiguous()
+    y2 = switch_linear(down, hs, torch.from_numpy(idx).cuda().reshape(-1), sorted_indices=False)
+    assert torch.equal(y2.reshape(T * k, H), y_unsorted.reshape(T * k, H))
 
 
 def test_gather_qmm_contract(gpu):
@@ -91,3 +166,15 @@ def test_gather_qmm_contract(gpu):
                    torch.from_numpy(rhs).cuda(), group_size=64, bits=4)
     want = np.stack([OM.gather_qmm_rows(bits(x)[lhs[i]:lhs[i] + 1], [0], [rhs[i]], *w, 64)[0] for i in range(R)])
     assert_close(bf16_values(y), want, what="gather_qmm")
+    # mlx-lm SwitchGLU form: x [T,1,1,K] broadcast against indices [T,k] -> [T,k,1,N]
+    T, k = 5, 3
+    xs = randn_bf16(rng, (T, 1, 1, K))
+    ind = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    y = gather_qmm(xs, u32(w[0]), from_bits(w[1]), from_bits(w[2]), rhs_indices=torch.from_numpy(ind).cuda(),
+                   group_size=64, bits=4)
+    assert tuple(y.shape) == (T, k, 1, N)
+    xb = bits(xs.reshape(T, K))
+    for t in range(T):
+        for j in range(k):
+            want = OM.gather_qmm_rows(xb[t:t + 1], [0], [ind[t, j]], *w, 64)[0]
+            assert_close(bf16_values(y[t, j, 0]), want, what="switch-glu form")

@@ -113,6 +113,52 @@ def test_spec_accept_law_by_enumeration():
     assert np.allclose(law0, p[0], atol=3e-3)
 
 
+def _law_logits(*rows):
+    """Logit rows whose T=1 softmax is the given law exactly (log p; -inf for 0)."""
+    with np.errstate(divide="ignore"):
+        return np.log(np.array(rows, dtype=np.float64))
+
+
+_FULL = S.SamplerConfig(1.0, 1.0, 0)   # no top-k, no nucleus: the law is softmax(l)
+
+
+@pytest.mark.parametrize("u1,want", [(0.5, 0), (0.7, 1)])
+def test_spec_accept_reject_at_depth0_known_answer(u1, want):
+    """p0 = [.5,.3,.2,0], q0 = [.1,.1,.8,0], draft 2: a = .2/.8 = .25; u0 = .6
+    rejects; residual max(p-q,0) = [.4,.2] -> [2/3,1/3] over ids [0,1];
+    Generator.choice with u1 picks #{cdf <= u1}."""
+    tl = _law_logits([.5, .3, .2, 0], [.25, .25, .25, .25], [.25, .25, .25, .25])
+    dl = _law_logits([.1, .1, .8, 0], [.25, .25, .25, .25])
+    res = S.spec_accept(tl, dl, np.array([2, 1]), np.array([0.6, u1, 0.0]), _FULL)
+    assert res.n_accepted == 0 and res.uniforms_used == 2
+    assert res.tokens == [want]
+    assert np.isclose(res.accept_probs[0], 0.25) and len(res.accept_probs) == 1
+
+
+@pytest.mark.parametrize("u2,want", [(0.2, 2), (0.3, 3)])
+def test_spec_accept_reject_at_depth1_known_answer(u2, want):
+    """Depth 0 accepts (u0 = .2 <= a0 = .25); depth 1: p1 = [.1,.2,.3,.4],
+    q1 = [.4,.3,.2,.1], draft 0: a1 = .25, u1 = .9 rejects; residual
+    [0,0,.1,.3] -> [.25,.75] over ids [2,3], drawn with u2."""
+    tl = _law_logits([.5, .3, .2, 0], [.1, .2, .3, .4], [.25, .25, .25, .25])
+    dl = _law_logits([.1, .1, .8, 0], [.4, .3, .2, .1])
+    res = S.spec_accept(tl, dl, np.array([2, 0]), np.array([0.2, 0.9, u2]), _FULL)
+    assert res.n_accepted == 1 and res.uniforms_used == 3 and res.tokens == [2, want]
+    assert np.allclose(res.accept_probs, [0.25, 0.25])
+
+
+@pytest.mark.parametrize("u2,want", [(0.1, 0), (0.3, 1), (0.6, 2)])
+def test_spec_accept_all_accept_bonus_known_answer(u2, want):
+    """Every draft accepted (u = 0 <= a > 0): the bonus is
+    choice(law of target row K, u[K]); row K = [.25,.25,.5,0] has cdf
+    [.25,.5,1]."""
+    tl = _law_logits([.5, .3, .2, 0], [.1, .2, .3, .4], [.25, .25, .5, 0])
+    dl = _law_logits([.1, .1, .8, 0], [.4, .3, .2, .1])
+    res = S.spec_accept(tl, dl, np.array([2, 3]), np.array([0.0, 0.0, u2]), _FULL)
+    assert res.n_accepted == 2 and res.uniforms_used == 3 and res.tokens == [2, 3, want]
+    assert np.allclose(res.accept_probs, [0.25, 1.0])
+
+
 def test_spec_accept_uniform_consumption():
     cfg = S.SamplerConfig(0.6, 0.95, 20)
     rng = np.random.default_rng(9)
@@ -122,7 +168,48 @@ def test_spec_accept_uniform_consumption():
     # all-accept path: uniforms 0 accept everything -> bonus uses u[K]
     res = S.spec_accept(tl, dl, drafts, np.array([0.0] * K + [0.5]), cfg)
     assert res.n_accepted == K and res.uniforms_used == K + 1 and res.tokens[:K] == drafts.tolist()
-    # a reject at depth 0 consumes exactly two uniforms
-    res = S.spec_accept(tl, dl, drafts, np.array([1.0, 0.3, 0.0, 0.0]), cfg)
-    if res.accept_probs[0] < 1.0:
-        assert res.n_accepted == 0 and res.uniforms_used == 2 and len(res.tokens) == 1
+    # a draft outside the target's support has a = 0: u0 = 1 rejects it and
+    # exactly two uniforms are consumed
+    p0 = S.sparse_distribution(tl[0], cfg)
+    outside = next(t for t in range(V) if p0.probability(t) == 0.0)
+    res = S.spec_accept(tl, dl, np.array([outside] + drafts[1:].tolist()), np.array([1.0, 0.3, 0.0, 0.0]), cfg)
+    assert res.accept_probs[0] == 0.0
+    assert res.n_accepted == 0 and res.uniforms_used == 2 and len(res.tokens) == 1
+    assert res.tokens[0] == S.choice(S.residual(p0, S.sparse_distribution(dl[0], cfg)), 0.3)
+
+
+# -- penalties: tests/test_penalties.py:31-95 known answers -------------------
+
+_PEN = S.SamplerConfig(1.0, 1.0, 0)
+
+
+def test_presence_penalty_demotes_a_seen_token():
+    p = S.distribution_from_logits(np.array([5.0, 4.0, 0.0, 0.0]), _PEN, {0: 3}, presence=2.0)
+    assert int(np.argmax(p)) == 1
+
+
+def test_frequency_penalty_scales_with_count():
+    lg = np.array([5.0, 4.0, 0.0, 0.0])
+    assert int(np.argmax(S.distribution_from_logits(lg, _PEN, {0: 4}, frequency=0.5))) == 1
+    assert int(np.argmax(S.distribution_from_logits(lg, _PEN, {0: 1}, frequency=0.5))) == 0
+
+
+def test_zero_penalties_are_identical_and_clamped_range():
+    lg = np.array([5.0, 4.0, 3.0, 2.0, 1.0])
+    cfg = S.SamplerConfig(0.7, 0.9, 3)
+    assert np.array_equal(S.distribution_from_logits(lg, cfg),
+                          S.distribution_from_logits(lg, cfg, {0: 3, 1: 2}, 0.0, 0.0))
+    assert S.apply_penalties(lg, {0: 3}, 0.0, 0.0) is lg
+    # presence 100 clamps to 2: 5 -> 3 still above 2
+    assert int(np.argmax(S.distribution_from_logits(np.array([5.0, 2.0]), _PEN, {0: 1}, presence=100.0))) == 0
+
+
+def test_device_twin_matches_host_law():
+    raw = np.array([5.0, 4.0, 3.0, 1.0, 0.0])
+    counts = {0: 3, 2: 1}
+    host = S.apply_penalties(raw, counts, 1.5, 0.5)
+    twin = S.apply_penalties_f32(raw, counts, 1.5, 0.5)
+    assert twin.dtype == np.float32 and np.allclose(twin, host, atol=1e-5)
+    assert host.tolist() == [5.0 - 1.5 - 1.5, 4.0, 3.0 - 0.5 - 1.5, 1.0, 0.0]
+    ov = S.apply_penalties_f32(raw, None, 0.0, 0.0, {1: 0.25})
+    assert ov.tolist() == [5.0, 3.75, 3.0, 1.0, 0.0]
