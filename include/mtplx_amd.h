@@ -304,6 +304,19 @@ int mtp_spec_accept(const float* target_logits, const float* draft_logits, const
                     int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
                     size_t ws_bytes, void* stream);
 
+/* mtp_spec_accept without a workspace argument. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The workspace is a file-scope device array of 8 MiB per GPU, kept until the
+ * process ends; a call that would need more (mtp_sampler_workspace_bytes)
+ * returns MTP_ERR_UNSUPPORTED. It allocates nothing. Every call on one GPU
+ * shares that array: calls that overlap on a GPU race, so order them on one
+ * stream. */
+int mtp_spec_accept_noalloc(const float* target_logits, const float* draft_logits, const int32_t* draft_ids,
+                            const double* uniforms, int B, int K, int V, double temperature, int top_k, double top_p,
+                            int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status,
+                            void* stream);
+
 /* Per-row sparse law (ids ascending, fp64 probs, count) and optionally one
  * draw per row with uniforms[r]: mtplx/sampling.py:259 distribution_from_logits
  * + :342 sample_from_distribution; mtplx/fast_sampling.py:637

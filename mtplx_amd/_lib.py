@@ -44,6 +44,7 @@ SIGNATURES = {
     "mtp_embed_affine4": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp]),
     "mtp_sampler_workspace_bytes": (_sz, [_i, _i, _i]),
     "mtp_spec_accept": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mtp_spec_accept_noalloc": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp]),
     "mtp_sample_rows": (_i, [_vp, _i, _i, _d, _i, _d, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
     "mtp_apply_logit_deltas": (_i, [_vp, C.c_longlong, _i, _i, _vp, _vp, _vp, _i, _vp, _vp]),
     "mtp_probe_mfma_layout": (_i, [_vp, _vp]),

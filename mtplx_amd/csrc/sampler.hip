@@ -41,6 +41,8 @@
 
 #include <math.h>
 
+#include <mutex>
+
 namespace mtp {
 
 constexpr int kSampThreads = 512;
@@ -1363,6 +1365,69 @@ MTP_API int mtp_spec_accept(const float* target_logits, const float* draft_logit
                        pl.ksel, pl.greedy, temp, top_p, out_tokens, n_accepted, accept_probs, status);
   }
   return launch_check(who);
+}
+
+// ---- No-allocation variant --------------------------------------------------
+// For callers that cannot allocate (code under HIP graph capture, tight
+// serving loops, harnesses that forbid hipMalloc): mtp_spec_accept with its
+// workspace in a file-scope device array. Each GPU holds its own copy for the
+// life of the process; its address is looked up once per device
+// (hipGetSymbolAddress, with that device current) and cached. Nothing in the
+// sampler's workspace has to start at zero: every chunk partial, law and
+// residual area is written before it is read. Calls that overlap on one GPU
+// share the array and race; calls must be stream-ordered.
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+static int noalloc_scratch(void** out, const char* who) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("%s: hipGetDevice failed: %s", who, hipGetErrorString(e));
+    return MTP_ERR_HIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("%s: device %d outside the %d the scratch table covers", who, dev, kMaxDevices);
+    return MTP_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, dev, hipGetErrorString(e));
+      return MTP_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MTP_OK;
+}
+
+MTP_API int mtp_spec_accept_noalloc(const float* target_logits, const float* draft_logits, const int32_t* draft_ids,
+                                    const double* uniforms, int B, int K, int V, double temperature, int top_k,
+                                    double top_p, int32_t* out_tokens, int32_t* n_accepted, double* accept_probs,
+                                    int32_t* status, void* stream) {
+  const char* who = "mtp_spec_accept_noalloc";
+  if (B < 1 || K < 1 || V < 1 || top_k < 0) {
+    set_error("%s: need B>=1, K>=1, V>=1, top_k>=0", who);
+    return MTP_ERR_ARG;
+  }
+  const int greedy = !(temperature > 0.0);
+  const size_t need = mtp_sampler_workspace_bytes(B * (2 * K + 1), V, greedy ? 1 : top_k);
+  if (need > kNoAllocScratchBytes) {
+    set_error("%s: B=%d K=%d V=%d top_k=%d needs %zu B of scratch; the no-allocation entry point has %zu B "
+              "(use mtp_spec_accept with a workspace)", who, B, K, V, top_k, need, kNoAllocScratchBytes);
+    return MTP_ERR_UNSUPPORTED;
+  }
+  void* ws = nullptr;
+  const int rc = noalloc_scratch(&ws, who);
+  if (rc) return rc;
+  return mtp_spec_accept(target_logits, draft_logits, draft_ids, uniforms, B, K, V, temperature, top_k, top_p,
+                         out_tokens, n_accepted, accept_probs, status, ws, kNoAllocScratchBytes, stream);
 }
 
 MTP_API int mtp_sample_rows(const float* logits, int rows, int V, double temperature, int top_k, double top_p,
