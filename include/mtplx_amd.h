@@ -171,6 +171,35 @@ typedef struct mtp_qmv_args {
 } mtp_qmv_args;
 int mtp_qmv_affine4_ex(const mtp_qmv_args* args, void* stream);
 
+/* ---- 4-bit quantized matmul for 9..64 verify rows (MFMA) --------------------
+ * The continuous-batched ragged verify (M = sum_b (K_b + 1) rows, up to 64):
+ * each weight quad is read once and applied to all M rows on
+ * v_mfma_f32_32x32x16_bf16, x streaming through LDS by 256-k quads. Weights in
+ * the tile-major layout of mtp_pack_affine4 (w0; w1 = the up matrix of the
+ * pair); same arithmetic as mtp_qmv_affine4_ex (dequantised weights never
+ * rounded, fp32 accumulation). emode 0: y bf16 (or yf fp32 of the
+ * bf16-rounded value); 1: y = bf16(bf16(x W^T) + resid) (resid may alias y);
+ * 3: y = bf16(bf16(silu(bf16(x W0^T))) * bf16(x W1^T)). ldx/ldy <= 0 mean
+ * K/N; x rows 16-byte aligned. ws: mtp_qmm_workspace_bytes (256-byte aligned,
+ * zeroed once, then left to the library; calls sharing it stream-ordered),
+ * needed when the call splits leftover column groups by K.
+ * Replaces the M > 16 route of mtplx/nax_verify.py:754 (stock
+ * mx.quantized_matmul) and mtplx/nax_verify.py:690 nax_qmm_m16 for the
+ * batched verify lane (mtplx/batched_decode.py:338-395). */
+typedef struct mtp_qmm_args {
+  const void* x;
+  const void* w0;
+  const void* w1;
+  void* y;
+  float* yf;
+  const void* resid;
+  int M, N, K, group_size, ldx, ldy, emode;
+  void* ws;
+  size_t ws_bytes;
+} mtp_qmm_args;
+size_t mtp_qmm_workspace_bytes(int M, int N, int K, int dual);
+int mtp_qmm_affine4_mfma(const mtp_qmm_args* args, void* stream);
+
 /* ---- Ragged KV cache + attention -----------------------------------------
  * Cache layout [B, Hkv, cap, D] bf16 (mtplx/ragged_kv_cache.py:71).
  * Scatter: cache[b,h,write_start[b]+i,:] = new[b,h,i,:]

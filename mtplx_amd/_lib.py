@@ -59,6 +59,8 @@ SIGNATURES = {
     "mtp_pack_affine4": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mtp_pack_affine4_mf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mtp_qmv_affine4_ex": (_i, [_vp, _vp]),
+    "mtp_qmm_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "mtp_qmm_affine4_mfma": (_i, [_vp, _vp]),
     "mtp_attn_vt_workspace_bytes": (_sz, [_i, _i, _i]),
     "mtp_ragged_gqa_attn_rows_vt": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
     "mtp_rope_qkv_to_cache_vt": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _vp]),
@@ -99,6 +101,19 @@ def qmv_ex(stream, rope: dict | None = None, **fields) -> None:
         r = _fill(RopeOut(), rope)
         a.rope = C.pointer(r)
     call("mtp_qmv_affine4_ex", C.byref(a), stream)
+
+
+class QmmArgs(C.Structure):
+    """``mtp_qmm_args`` of include/mtplx_amd.h (same field order)."""
+
+    _fields_ = [(n, _vp) for n in ("x", "w0", "w1", "y", "yf", "resid")] + \
+               [(n, _i) for n in ("M", "N", "K", "group_size", "ldx", "ldy", "emode")] + \
+               [("ws", _vp), ("ws_bytes", C.c_size_t)]
+
+
+def qmm_mfma(stream, **fields) -> None:
+    """Call ``mtp_qmm_affine4_mfma``; tensor fields may be torch tensors or None."""
+    call("mtp_qmm_affine4_mfma", C.byref(_fill(QmmArgs(), fields)), stream)
 
 
 class MtpError(RuntimeError):

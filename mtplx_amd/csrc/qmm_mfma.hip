@@ -1,0 +1,438 @@
+// 4-bit affine quantized matmul for 9..64 verify rows (continuous-batched
+// ragged verify: M = sum of the requests' K_b + 1), gfx950.
+//
+//   y[m, n] = sum_k x[m, k] * (q[n, k] * s[n, k/gs] + b[n, k/gs])
+//
+// At these M all of x no longer fits in one workgroup's LDS (64 rows x 5120
+// k is 640 KB), so x streams through LDS quad by quad (256 k per step, a
+// double buffer of at most 32 KB each) while every weight quad is read from
+// HBM exactly once and applied to all M rows:
+//  * a workgroup of 4 waves owns a column group: 4 tiles of 32 columns (one
+//    per wave), or 2 column tiles x {gate, up} for the fused SwiGLU pair, so
+//    each staged x quad serves 128 weight columns;
+//  * x rows land in LDS with direct-to-LDS loads (no registers); each 16-byte
+//    chunk kc of row m sits at slot 32m + (kc ^ (m & 7)), so one wave load
+//    writes 1 KB contiguous and the A-operand reads of 8 consecutive rows hit
+//    8 different 16-byte bank groups;
+//  * the weights stream from the tile-major packed layout (mtp_pack_affine4)
+//    through a two-deep register ring, exactly as the skinny kernel reads
+//    them; nibbles become exact bf16 operands 128 + q with one AND-OR each;
+//  * v_mfma_f32_32x32x16_bf16 with A = x rows (one or two 32-row blocks), B =
+//    the lane's weight column; each 64-k group is finished on the VALU as
+//    acc += s * G + (b - 128 s) * sum(x_group) (group sums from LDS), so the
+//    dequantised weights are never rounded (the numerics of the skinny path);
+//  * groups left over after the last full round of workgroups are split by K
+//    over the idle CUs; their parts store fp32 sums, and the last part to
+//    arrive adds them in part order (deterministic) and runs the epilogue.
+// Epilogues: bf16 store (or fp32 of the bf16-rounded value), + residual,
+// and silu(gate) * up for the fused pair.
+#include "qmv_args.hpp"
+
+namespace mtp {
+
+constexpr int kQmWaves = 4;
+constexpr int kQmThreads = kQmWaves * 64;
+constexpr int kQmSlotsPerRow = 32;   // 16-byte chunks of one x row per quad (256 bf16)
+
+struct QmmRowsParams {
+  const uint16_t* x;
+  const uint32_t* w0;
+  const uint32_t* w1;      // up matrix of the fused pair
+  uint16_t* y;
+  float* yf;
+  const uint16_t* resid;
+  int M, N, K, ldx, ldy;
+  int Q;                   // quads (K / 256)
+  int ntiles;              // 32-column tiles
+  int full_groups;         // groups that run over all of K
+  int split;               // parts of each leftover group (1: none)
+  float* partial;          // [leftover groups][split][waves][R2*16][64]
+  uint32_t* counters;      // [leftover groups]
+};
+
+__device__ __forceinline__ int xslot(int m, int kc) { return m * kQmSlotsPerRow + (kc ^ (m & 7)); }
+
+// Direct-to-LDS loads of x[0:M, 256q : 256q + 256): wave instruction t
+// covers rows 2t and 2t + 1. A row past M (odd M) loads row M - 1 into a
+// slot row that is never an output.
+__device__ __forceinline__ void qm_stage(const QmmRowsParams& p, unsigned char* buf, int q, int wave, int lane) {
+  const int ninst = (p.M + 1) >> 1;
+  for (int t = wave; t < ninst; t += kQmWaves) {
+    const int m = 2 * t + (lane >> 5);
+    const int mr = m < p.M ? m : p.M - 1;
+    const int kc = (lane & 31) ^ (m & 7);
+    __builtin_amdgcn_global_load_lds((gptr_t)(p.x + (size_t)mr * p.ldx + 256 * q + 8 * kc),
+                                     (lptr_t)(buf + (size_t)t * 1024), 16, 0, 0);
+  }
+}
+
+static bool rows_aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+struct QmQuad {
+  uint4 w[4];
+  uint4 sb;
+};
+
+template <int R2, int EM>
+__global__ __launch_bounds__(kQmThreads) void qmm_rows_kernel(QmmRowsParams p) {
+  constexpr bool dual = EM == E_DUAL_SWIGLU;
+  constexpr int ROWS = 32 * R2;
+  constexpr int XBUF = ROWS * kQmSlotsPerRow * 16;   // bytes of one staged quad
+  // Dynamic LDS: two staged x quads, then their group sums [2][4][ROWS].
+  extern __shared__ __align__(16) unsigned char qm_lds[];
+  unsigned char* xbuf[2] = {qm_lds, qm_lds + XBUF};
+  float (*xs)[4][ROWS] = reinterpret_cast<float (*)[4][ROWS]>(qm_lds + 2 * XBUF);
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c32 = lane & 31, kq = lane >> 5;
+  const int M = p.M, Q = p.Q;
+
+  // Unit: a column group over all of K, or one K part of a leftover group.
+  int g, part = 0, q_lo = 0, q_n = Q;
+  const bool split = (int)blockIdx.x >= p.full_groups;
+  if (!split) {
+    g = blockIdx.x;
+  } else {
+    const int e = blockIdx.x - p.full_groups;
+    g = p.full_groups + e / p.split;
+    part = e % p.split;
+    q_lo = (part * Q) / p.split;
+    q_n = ((part + 1) * Q) / p.split - q_lo;
+  }
+  // This wave's tile (column tile ct of matrix mat).
+  const int ct = dual ? 2 * g + (wave & 1) : 4 * g + wave;
+  const int mat = dual ? (wave >> 1) : 0;
+  const bool has_tile = ct < p.ntiles;
+  const uint32_t* W = (mat ? p.w1 : p.w0) + (size_t)(has_tile ? ct : 0) * Q * kPackQuadWords;
+  const uint32_t* wl = W + lane * 4;
+  const uint32_t* sl = W + 1024 + c32 * 4;
+  const NibConsts nc = nib_consts();
+
+  auto load_quad = [&](QmQuad& r, int c) {
+    const int q = q_lo + (c < q_n ? c : q_n - 1);   // past the end: a valid block, never used
+    const size_t off = (size_t)q * kPackQuadWords;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) r.w[u] = *reinterpret_cast<const uint4*>(wl + off + 256 * u);
+    r.sb = *reinterpret_cast<const uint4*>(sl + off);
+  };
+
+  f32x16 acc[R2];
+#pragma unroll
+  for (int r2 = 0; r2 < R2; ++r2)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r2][r] = 0.f;
+
+  // A-operand LDS byte offsets of this lane, per row block: row 32 r2 + c32,
+  // chunk kc = 8u + 4 kq + ii of the quad.
+  int arow[R2];
+#pragma unroll
+  for (int r2 = 0; r2 < R2; ++r2) {
+    const int m = 32 * r2 + c32;
+    arow[r2] = m < M ? m : (M - 1);
+  }
+
+  auto compute = [&](const QmQuad& r, int buf) {
+    float sv[4], cb[4];
+    const uint32_t sw[2] = {r.sb.x, r.sb.y}, bw[2] = {r.sb.z, r.sb.w};
+    quad_scales<0>(sw, bw, sv, cb);   // the pack stores scales per 64-group for either group size
+    const unsigned char* xb = xbuf[buf];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t wv[4] = {r.w[u].x, r.w[u].y, r.w[u].z, r.w[u].w};
+      f32x16 G[R2];
+#pragma unroll
+      for (int r2 = 0; r2 < R2; ++r2)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) G[r2][i] = 0.f;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const bf16x8 b = nibbles_to_bf16(wv[ii], nc);
+        const int kc = 8 * u + 4 * kq + ii;
+#pragma unroll
+        for (int r2 = 0; r2 < R2; ++r2) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(xb + 16 * xslot(arow[r2], kc));
+          G[r2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, G[r2], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int r2 = 0; r2 < R2; ++r2) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float4 xv = *reinterpret_cast<const float4*>(&xs[buf][u][32 * r2 + 8 * j + 4 * kq]);
+          const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 4 * j + i;
+            acc[r2][r] = fmaf(sv[u], G[r2][r], fmaf(cb[u], xa[i], acc[r2][r]));
+          }
+        }
+      }
+    }
+  };
+
+  // Group sums of staged quad `buf`: thread t < 4M sums row t % M, group t / M.
+  auto group_sums = [&](int buf) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t one2 = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
+    for (int t = tid; t < 4 * M; t += kQmThreads) {
+      const int u = t / M, m = t - u * M;
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint4 c = *reinterpret_cast<const uint4*>(xbuf[buf] + 16 * xslot(m, 8 * u + j));
+        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, c.x), one2, s, false);
+        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, c.y), one2, s, false);
+        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, c.z), one2, s, false);
+        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, c.w), one2, s, false);
+      }
+      xs[buf][u][m] = s;
+    }
+  };
+
+  // Prologue: quad 0 of x, then the first two weight quads.
+  QmQuad ring0, ring1;
+  qm_stage(p, xbuf[0], q_lo, wave, lane);
+  load_quad(ring0, 0);
+  load_quad(ring1, 1);
+  // One step: quad c from ring slot `cur` and x buffer c & 1; refills `cur`
+  // with quad c + 2. At the wait only the newest ring slot (5 loads) may be
+  // outstanding: quad c's x and weights have landed.
+  auto step = [&](QmQuad& cur, int c) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(5));
+    lds_barrier();   // every wave's x loads of quad c are in LDS
+    group_sums(c & 1);
+    if (c + 1 < q_n) qm_stage(p, xbuf[(c + 1) & 1], q_lo + c + 1, wave, lane);
+    lds_barrier();   // group sums visible; buffer (c+1)&1 was last read before the first barrier
+    compute(cur, c & 1);
+    load_quad(cur, c + 2);
+  };
+  int c = 0;
+  do {
+    step(ring0, c);
+    if (c + 1 < q_n) step(ring1, c + 1);
+    c += 2;
+  } while (c < q_n);
+  __builtin_amdgcn_s_waitcnt(0);
+
+  // Output element of acc[r2][r]: row 32 r2 + 8 (r / 4) + 4 kq + r % 4,
+  // column 32 ct + c32.
+  auto row_of = [&](int r2, int r) { return 32 * r2 + 8 * (r >> 2) + 4 * kq + (r & 3); };
+
+  if (split) {
+    // This part's sums, device-coherent, in register order; the last part to
+    // arrive adds the parts in part order.
+    const int eg = g - p.full_groups;
+    float* mine = p.partial + (((size_t)eg * p.split + part) * kQmWaves + wave) * (R2 * 16 * 64);
+#pragma unroll
+    for (int r2 = 0; r2 < R2; ++r2)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        __hip_atomic_store(mine + (r2 * 16 + r) * 64 + lane, acc[r2][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned old = __hip_atomic_fetch_add(p.counters + eg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = old == (unsigned)(p.split - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+#pragma unroll
+    for (int r2 = 0; r2 < R2; ++r2)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r2][r] = 0.f;
+    for (int pp = 0; pp < p.split; ++pp) {
+      const float* src = p.partial + (((size_t)eg * p.split + pp) * kQmWaves + wave) * (R2 * 16 * 64);
+      float v[R2][16];
+#pragma unroll
+      for (int r2 = 0; r2 < R2; ++r2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          v[r2][r] = __hip_atomic_load(src + (r2 * 16 + r) * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int r2 = 0; r2 < R2; ++r2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r2][r] += v[r2][r];
+    }
+    if (tid == 0) __hip_atomic_store(p.counters + eg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  const int col = 32 * ct + c32;
+  if constexpr (dual) {
+    // The up waves hand their sums to the gate waves of the same columns.
+    float* ex = reinterpret_cast<float*>(xbuf[0]);   // [2 column tiles][R2*16][64]
+    __syncthreads();
+    if (mat == 1) {
+#pragma unroll
+      for (int r2 = 0; r2 < R2; ++r2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ex[((wave & 1) * R2 * 16 + r2 * 16 + r) * 64 + lane] = acc[r2][r];
+    }
+    __syncthreads();
+    if (mat == 0 && has_tile && col < p.N) {
+#pragma unroll
+      for (int r2 = 0; r2 < R2; ++r2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = row_of(r2, r);
+          if (m < M) {
+            const float up = ex[((wave & 1) * R2 * 16 + r2 * 16 + r) * 64 + lane];
+            const float gsl = round_bf(silu_f(round_bf(acc[r2][r])));
+            p.y[(size_t)m * p.ldy + col] = f2bf(gsl * round_bf(up));
+          }
+        }
+    }
+    return;
+  }
+  if (!has_tile || col >= p.N) return;
+#pragma unroll
+  for (int r2 = 0; r2 < R2; ++r2)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = row_of(r2, r);
+      if (m >= M) continue;
+      const size_t o = (size_t)m * p.ldy + col;
+      if (EM == E_RESID) {
+        p.y[o] = f2bf(round_bf(acc[r2][r]) + bf2f(p.resid[o]));
+      } else if (p.yf) {
+        p.yf[o] = round_bf(acc[r2][r]);
+      } else {
+        p.y[o] = f2bf(acc[r2][r]);
+      }
+    }
+}
+
+static size_t rows_lds_bytes(int R2) {
+  const size_t xbuf = (size_t)32 * R2 * kQmSlotsPerRow * 16;
+  return 2 * xbuf + (size_t)2 * 4 * 32 * R2 * sizeof(float);
+}
+
+struct RowsPlan {
+  int groups, full, split, leftover;
+};
+
+static RowsPlan rows_plan(int M, int N, int K, int dual) {
+  RowsPlan pl;
+  const int ntiles = cdiv(N, 32);
+  pl.groups = dual ? cdiv(ntiles, 2) : cdiv(ntiles, 4);
+  const int cus = device_cus();
+  const int Q = K >> 8;
+  const int R2 = M > 32 ? 2 : 1;
+  const int E = pl.groups % cus;
+  pl.full = pl.groups - E;
+  pl.split = 1;
+  pl.leftover = 0;
+  if (E > 0) {
+    int S = cus / E;
+    if (S > Q) S = Q;
+    // Partial sums cost 4 waves x R2 x 4 KB per part of each leftover group
+    // (written, then read once); keep them under half the group's weights.
+    const double wbytes = (double)E * 4 * Q * kPackQuadWords * 4;
+    const double per_part = (double)E * kQmWaves * R2 * 4096;
+    const int cap = (int)(0.5 * wbytes / per_part);
+    if (S > cap) S = cap;
+    if (S >= 2) {
+      pl.split = S;
+      pl.leftover = E;
+    } else {
+      pl.full = pl.groups;
+    }
+  }
+  return pl;
+}
+
+static size_t rows_partial_bytes(const RowsPlan& pl, int M) {
+  const int R2 = M > 32 ? 2 : 1;
+  return ((size_t)pl.leftover * pl.split * kQmWaves * R2 * 16 * 64 * sizeof(float) + 255) & ~(size_t)255;
+}
+
+}  // namespace mtp
+
+using namespace mtp;
+
+MTP_API size_t mtp_qmm_workspace_bytes(int M, int N, int K, int dual) {
+  if (M < 1 || M > 64 || N < 1 || K < 256 || K % 256) return 0;
+  const RowsPlan pl = rows_plan(M, N, K, dual);
+  return rows_partial_bytes(pl, M) + (((size_t)pl.leftover * 4 + 255) & ~(size_t)255);
+}
+
+MTP_API int mtp_qmm_affine4_mfma(const mtp_qmm_args* a, void* stream) {
+  const char* who = "mtp_qmm_affine4_mfma";
+  if (!a || !a->x || !a->w0 || (!a->y && !a->yf)) {
+    set_error("%s: null argument block, x, w0 or output", who);
+    return MTP_ERR_ARG;
+  }
+  const int M = a->M, N = a->N, K = a->K;
+  const int em = a->emode;
+  if (M < 1 || M > 64 || N < 1 || K < 256 || K % 256) {
+    set_error("%s: need 1 <= M <= 64, N >= 1, K a multiple of 256 (got M=%d N=%d K=%d)", who, M, N, K);
+    return MTP_ERR_ARG;
+  }
+  if (a->group_size != 64 && a->group_size != 128) {
+    set_error("%s: group_size %d unsupported (64 or 128)", who, a->group_size);
+    return MTP_ERR_UNSUPPORTED;
+  }
+  if (em != E_STORE && em != E_RESID && em != E_DUAL_SWIGLU) {
+    set_error("%s: emode %d unsupported (0 store, 1 residual, 3 SwiGLU pair)", who, em);
+    return MTP_ERR_UNSUPPORTED;
+  }
+  if ((em == E_DUAL_SWIGLU && (!a->w1 || !a->y)) || (em == E_RESID && (!a->resid || !a->y))) {
+    set_error("%s: emode %d needs %s", who, em, em == E_RESID ? "resid and y" : "w1 and y");
+    return MTP_ERR_ARG;
+  }
+  const int ldx = a->ldx > 0 ? a->ldx : K, ldy = a->ldy > 0 ? a->ldy : N;
+  if (ldx < K || ldy < N || !rows_aligned16(a->x) || (ldx % 8) || !rows_aligned16(a->w0) || (a->w1 && !rows_aligned16(a->w1))) {
+    set_error("%s: x rows must be 16-byte aligned (ldx %% 8 == 0), weights 16-byte aligned", who);
+    return MTP_ERR_ARG;
+  }
+  const int dual = em == E_DUAL_SWIGLU;
+  const RowsPlan pl = rows_plan(M, N, K, dual);
+  QmmRowsParams p = {};
+  p.x = (const uint16_t*)a->x;
+  p.w0 = (const uint32_t*)a->w0;
+  p.w1 = (const uint32_t*)a->w1;
+  p.y = (uint16_t*)a->y;
+  p.yf = a->yf;
+  p.resid = (const uint16_t*)a->resid;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.ldx = ldx;
+  p.ldy = ldy;
+  p.Q = K >> 8;
+  p.ntiles = cdiv(N, 32);
+  p.full_groups = pl.full;
+  p.split = pl.split;
+  if (pl.split > 1) {
+    const size_t need = mtp_qmm_workspace_bytes(M, N, K, dual);
+    if (!a->ws || a->ws_bytes < need || ((uintptr_t)a->ws & 255)) {
+      set_error("%s: a 256-byte aligned workspace of %zu B is needed (mtp_qmm_workspace_bytes), got %zu B", who, need,
+                a->ws_bytes);
+      return MTP_ERR_WORKSPACE;
+    }
+    p.partial = reinterpret_cast<float*>(a->ws);
+    p.counters = reinterpret_cast<uint32_t*>(reinterpret_cast<unsigned char*>(a->ws) + rows_partial_bytes(pl, M));
+  }
+  const int grid = pl.full + pl.leftover * pl.split;
+  hipStream_t st = (hipStream_t)stream;
+  // (the pack repeats a group-128 scale over its two 64-groups, so the kernel
+  // is the same for both group sizes). A failure of the attribute call
+  // surfaces as a launch error, checked below.
+#define MTP_ROWS(R2v, EMv)                                                                                \
+  do {                                                                                                    \
+    const size_t lds = rows_lds_bytes(R2v);                                                               \
+    auto k = qmm_rows_kernel<R2v, EMv>;                                                                   \
+    if (lds > 65536) (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                               (int)lds);                                                 \
+    hipLaunchKernelGGL(k, dim3(grid), dim3(kQmThreads), lds, st, p);                                      \
+  } while (0)
+  if (M > 32) {
+    if (em == E_STORE) MTP_ROWS(2, E_STORE); else if (em == E_RESID) MTP_ROWS(2, E_RESID); else MTP_ROWS(2, E_DUAL_SWIGLU);
+  } else {
+    if (em == E_STORE) MTP_ROWS(1, E_STORE); else if (em == E_RESID) MTP_ROWS(1, E_RESID); else MTP_ROWS(1, E_DUAL_SWIGLU);
+  }
+#undef MTP_ROWS
+  return launch_check(who);
+}

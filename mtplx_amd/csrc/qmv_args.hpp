@@ -47,3 +47,16 @@ int qmv_args_params(const mtp_qmv_args* a, QmmParams* out, const char* who);
 int qmm_check_args(int xm, int em, const QmmParams& p, const char* who);
 size_t stream_lds_bytes(int chunk_q, int M, int nw);
 }  // namespace mtp
+
+// mtp_qmm_affine4_mfma's argument block (the same layout as include/mtplx_amd.h).
+struct mtp_qmm_args {
+  const void* x;
+  const void* w0;
+  const void* w1;
+  void* y;
+  float* yf;
+  const void* resid;
+  int M, N, K, group_size, ldx, ldy, emode;
+  void* ws;
+  size_t ws_bytes;
+};
