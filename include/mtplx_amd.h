@@ -253,6 +253,44 @@ int mtp_rope_qkv_to_cache_vt(const void* qkv, const int32_t* q_start, const int3
                              void* k_cache, void* v_cache, int B, int L, int Hq, int Hkv, int D, int cap,
                              float rope_base, int32_t* status, void* stream);
 
+/* Ragged batches over the operand-major block cache, per-request capacities:
+ * the continuous-batched verify lane (mtplx/batched_decode.py:338-395,
+ * mtplx/ragged_kv_cache.py:201-277 with per-row q lengths). Request b has
+ * q_lens[b] query rows (<= Lmax) at positions q_start[b] + i; q is
+ * [B, Hq, Lmax, D]; its output rows are packed at row_off[b] + i of out
+ * [rows, Hq * D] (row_off NULL: b * Lmax + i). Its K/V live in blocks
+ * [kv_off[b], kv_off[b+1]) of k_blk / v_blk (4096 bf16 per 32-key block, the
+ * layout above; head h's nblk_b = (kv_off[b+1] - kv_off[b]) / Hkv blocks
+ * start at kv_off[b] + h * nblk_b); kv_off NULL means a uniform capacity cap.
+ * cap is the largest request capacity (a multiple of 32), total_cap the sum
+ * of the capacities (<= 0: B * cap), split_keys the keys per work unit (a
+ * multiple of 128; <= 0 picks about 1024 units over total_cap * Hkv).
+ * (Hq/Hkv) * Lmax <= 32, D = 128. */
+typedef struct mtp_attn_blocks_args {
+  const void* q;
+  const void* k_blk;
+  const void* v_blk;
+  const int32_t* q_start;
+  const int32_t* q_lens;
+  const int32_t* row_off;
+  const int32_t* kv_off;
+  void* out;
+  int B, Hq, Hkv, Lmax, D, cap, split_keys;
+  float scale;
+  long long total_cap;
+  void* ws;
+  size_t ws_bytes;
+} mtp_attn_blocks_args;
+size_t mtp_attn_blocks_workspace_bytes(int B, int Hkv, int cap, long long total_cap, int split_keys);
+int mtp_ragged_gqa_attn_blocks(const mtp_attn_blocks_args* args, void* stream);
+/* RoPE on packed ragged q|k|v rows [M, (Hq+2Hkv)*D] (row m of request b with
+ * row_off[b] <= m < row_off[b+1], position q_start[b] + m - row_off[b]):
+ * q -> q_out [B, Hq, Lmax, D], K/V into the blocks as above (kv_off NULL:
+ * uniform cap). Positions outside [0, capacity) are skipped and flag *status. */
+int mtp_rope_qkv_to_blocks(const void* qkv, int M, const int32_t* row_off, const int32_t* q_start,
+                           const int32_t* kv_off, void* q_out, void* k_blk, void* v_blk, int B, int Lmax, int Hq,
+                           int Hkv, int D, int cap, float rope_base, int32_t* status, void* stream);
+
 /* ---- Verify-step glue -------------------------------------------------------
  * RoPE (rotate-half, fp32 angles) on fused q|k|v rows [B*L, (Hq+2Hkv)*D] at
  * positions q_start[b]+i; q -> q_out [B,Hq,L,D], k/v written into the cache
@@ -332,6 +370,20 @@ int mtp_spec_accept(const float* target_logits, const float* draft_logits, const
                     const double* uniforms, int B, int K, int V, double temperature, int top_k, double top_p,
                     int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
                     size_t ws_bytes, void* stream);
+
+/* The same step for a ragged batch (the continuous-batched verify lane,
+ * mtplx/batched_decode.py:338-395): request b has depth K_b = k_lens[b]
+ * (1 <= K_b <= K_max); its target rows are target_logits rows
+ * t_off[b] .. t_off[b] + K_b (n_target rows in all) and its draft rows and
+ * draft ids are rows / entries d_off[b] .. d_off[b] + K_b - 1 (n_draft in
+ * all); uniforms [B, K_max+1] (request b consumes at most K_b + 1); outputs
+ * as above with K = K_max. Workspace: mtp_sampler_workspace_bytes(n_target +
+ * n_draft, V, top_k). */
+int mtp_spec_accept_ragged(const float* target_logits, int n_target, const float* draft_logits, int n_draft,
+                           const int32_t* t_off, const int32_t* d_off, const int32_t* k_lens, const int32_t* draft_ids,
+                           const double* uniforms, int B, int K_max, int V, double temperature, int top_k, double top_p,
+                           int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
+                           size_t ws_bytes, void* stream);
 
 /* mtp_spec_accept without a workspace argument. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under

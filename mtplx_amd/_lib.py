@@ -44,6 +44,8 @@ SIGNATURES = {
     "mtp_embed_affine4": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp]),
     "mtp_sampler_workspace_bytes": (_sz, [_i, _i, _i]),
     "mtp_spec_accept": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mtp_spec_accept_ragged": (_i, [_vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp,
+                                    _vp, _vp, _sz, _vp]),
     "mtp_spec_accept_noalloc": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp]),
     "mtp_sample_rows": (_i, [_vp, _i, _i, _d, _i, _d, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
     "mtp_apply_logit_deltas": (_i, [_vp, C.c_longlong, _i, _i, _vp, _vp, _vp, _i, _vp, _vp]),
@@ -61,6 +63,9 @@ SIGNATURES = {
     "mtp_qmv_affine4_ex": (_i, [_vp, _vp]),
     "mtp_qmm_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "mtp_qmm_affine4_mfma": (_i, [_vp, _vp]),
+    "mtp_attn_blocks_workspace_bytes": (_sz, [_i, _i, _i, C.c_longlong, _i]),
+    "mtp_ragged_gqa_attn_blocks": (_i, [_vp, _vp]),
+    "mtp_rope_qkv_to_blocks": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _vp]),
     "mtp_attn_vt_workspace_bytes": (_sz, [_i, _i, _i]),
     "mtp_ragged_gqa_attn_rows_vt": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
     "mtp_rope_qkv_to_cache_vt": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _vp]),
@@ -114,6 +119,19 @@ class QmmArgs(C.Structure):
 def qmm_mfma(stream, **fields) -> None:
     """Call ``mtp_qmm_affine4_mfma``; tensor fields may be torch tensors or None."""
     call("mtp_qmm_affine4_mfma", C.byref(_fill(QmmArgs(), fields)), stream)
+
+
+class AttnBlocksArgs(C.Structure):
+    """``mtp_attn_blocks_args`` of include/mtplx_amd.h (same field order)."""
+
+    _fields_ = [(n, _vp) for n in ("q", "k_blk", "v_blk", "q_start", "q_lens", "row_off", "kv_off", "out")] + \
+               [(n, _i) for n in ("B", "Hq", "Hkv", "Lmax", "D", "cap", "split_keys")] + \
+               [("scale", _f), ("total_cap", C.c_longlong), ("ws", _vp), ("ws_bytes", C.c_size_t)]
+
+
+def attn_blocks(stream, **fields) -> None:
+    """Call ``mtp_ragged_gqa_attn_blocks``; tensor fields may be torch tensors or None."""
+    call("mtp_ragged_gqa_attn_blocks", C.byref(_fill(AttnBlocksArgs(), fields)), stream)
 
 
 class MtpError(RuntimeError):

@@ -186,6 +186,34 @@ __global__ __launch_bounds__(kVtWaves * 64) void attn_vt_kernel(AttnParams p) {
   attn_vt_body<TPW, false>(p, (int)blockIdx.x, lds);
 }
 
+__global__ __launch_bounds__(kVtWaves * 64) void attn_vl_kernel(AttnParams p) {
+  __shared__ __align__(16) unsigned char lds[attn_vt_lds_bytes()];
+  attn_vl_body<false>(p, (int)blockIdx.x, lds);
+}
+
+// Keys per work unit of the block-layout entry point: about 1024 units over
+// the batch's summed capacity (total_cap * Hkv), at least 128 keys (one tile
+// per wave), at most 4096, a multiple of 128; then at most kMaxSplits splits
+// of the largest capacity.
+static int attn_blocks_plan(int Hkv, int cap, long long total_cap, int req, int* S, int* sk_out) {
+  int sk = req;
+  if (sk <= 0) {
+    const long long work = total_cap * Hkv;
+    sk = (int)((work + 1023) / 1024);
+    if (sk < 128) sk = 128;
+    if (sk > 4096) sk = 4096;
+  }
+  sk = ((sk + 127) / 128) * 128;
+  int s = cdiv(cap, sk);
+  if (s > kMaxSplits) {
+    sk = ((cdiv(cap, kMaxSplits) + 127) / 128) * 128;
+    s = cdiv(cap, sk);
+  }
+  *S = s;
+  *sk_out = sk;
+  return MTP_OK;
+}
+
 __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(AttnParams p) {
   __shared__ __align__(16) unsigned char lds[attn_merge_lds_bytes()];
   attn_merge_body<false>(p, (int)blockIdx.x, lds);
@@ -453,4 +481,61 @@ MTP_API int mtp_ragged_causal_mask(uint8_t* out, const int32_t* q_start, int B, 
   hipLaunchKernelGGL(ragged_mask_kernel, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t)stream, out, q_start, B,
                      q_len, key_len);
   return launch_check("mtp_ragged_causal_mask");
+}
+
+MTP_API size_t mtp_attn_blocks_workspace_bytes(int B, int Hkv, int cap, long long total_cap, int split_keys) {
+  if (B < 1 || Hkv < 1 || cap < 32) return 0;
+  int S, sk;
+  attn_blocks_plan(Hkv, cap, total_cap > 0 ? total_cap : (long long)B * cap, split_keys, &S, &sk);
+  const size_t units = (size_t)B * Hkv * S;
+  return units * 32 * kHD * sizeof(float) + units * 64 * sizeof(float);
+}
+
+MTP_API int mtp_ragged_gqa_attn_blocks(const mtp_attn_blocks_args* a, void* stream) {
+  const char* who = "mtp_ragged_gqa_attn_blocks";
+  if (!a || !a->q || !a->k_blk || !a->v_blk || !a->q_start || !a->out || a->B < 1 || a->Hq < 1 || a->Hkv < 1 ||
+      a->Lmax < 1 || a->cap < 32 || a->cap % 32) {
+    set_error("%s: bad arguments (cap a positive multiple of 32)", who);
+    return MTP_ERR_ARG;
+  }
+  if (a->D != kHD) {
+    set_error("%s: head_dim %d unsupported (128)", who, a->D);
+    return MTP_ERR_UNSUPPORTED;
+  }
+  if (a->Hq % a->Hkv || (a->Hq / a->Hkv) * a->Lmax > 32) {
+    set_error("%s: need Hq %% Hkv == 0 and (Hq/Hkv)*Lmax <= 32 (Hq=%d Hkv=%d Lmax=%d)", who, a->Hq, a->Hkv, a->Lmax);
+    return MTP_ERR_UNSUPPORTED;
+  }
+  AttnParams p{};
+  p.q = (const uint16_t*)a->q;
+  p.k = (const uint16_t*)a->k_blk;
+  p.v = (const uint16_t*)a->v_blk;
+  p.q_start = a->q_start;
+  p.q_lens = a->q_lens;
+  p.row_off = a->row_off;
+  p.kv_off = a->kv_off;
+  p.out = (uint16_t*)a->out;
+  p.B = a->B;
+  p.Hq = a->Hq;
+  p.Hkv = a->Hkv;
+  p.L = a->Lmax;
+  p.cap = a->cap;
+  p.out_rows = 1;
+  p.scale_log2 = a->scale * 1.4426950408889634f;
+  const long long total = a->total_cap > 0 ? a->total_cap : (long long)a->B * a->cap;
+  attn_blocks_plan(a->Hkv, a->cap, total, a->split_keys, &p.S, &p.split_keys);
+  const size_t need = mtp_attn_blocks_workspace_bytes(a->B, a->Hkv, a->cap, a->total_cap, a->split_keys);
+  if (!a->ws || a->ws_bytes < need) {
+    set_error("%s: workspace %zu < %zu (mtp_attn_blocks_workspace_bytes)", who, a->ws_bytes, need);
+    return MTP_ERR_WORKSPACE;
+  }
+  const size_t units = (size_t)a->B * a->Hkv * p.S;
+  p.part_o = (float*)a->ws;
+  p.part_ml = (float*)a->ws + units * 32 * kHD;
+  hipLaunchKernelGGL(attn_vl_kernel, dim3((unsigned)units), dim3(kVtWaves * 64), 0, (hipStream_t)stream, p);
+  int rc = launch_check(who);
+  if (rc) return rc;
+  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(a->B * a->Hkv * (a->Hq / a->Hkv) * a->Lmax)),
+                     dim3(kMergeThreads), 0, (hipStream_t)stream, p);
+  return launch_check(who);
 }

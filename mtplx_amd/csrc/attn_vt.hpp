@@ -6,6 +6,23 @@
 
 #include <stdlib.h>
 
+// mtp_ragged_gqa_attn_blocks' argument block (the layout of include/mtplx_amd.h).
+struct mtp_attn_blocks_args {
+  const void* q;
+  const void* k_blk;
+  const void* v_blk;
+  const int32_t* q_start;
+  const int32_t* q_lens;
+  const int32_t* row_off;
+  const int32_t* kv_off;
+  void* out;
+  int B, Hq, Hkv, Lmax, D, cap, split_keys;
+  float scale;
+  long long total_cap;
+  void* ws;
+  size_t ws_bytes;
+};
+
 namespace mtp {
 
 constexpr int kHD = 128;          // head dim
@@ -25,7 +42,25 @@ struct AttnParams {
   int B, Hq, Hkv, L, cap, S, split_keys;
   int out_rows;              // 1: out is [B, L, Hq, D] (rows feed the o projection)
   float scale_log2;          // softmax scale * log2(e)
+  // Ragged batches (the block-layout entry point): output row of request b's
+  // query i is row_off[b] + i (null: b * L + i); request b's K/V blocks are
+  // [kv_off[b], kv_off[b+1]), head h's nblk = (kv_off[b+1] - kv_off[b]) / Hkv
+  // of them starting at kv_off[b] + h * nblk (null: a uniform capacity cap).
+  const int32_t* row_off;
+  const int32_t* kv_off;
 };
+
+// Capacity (keys) of request b and the index of head h's first 32-key block.
+__device__ __forceinline__ int req_cap(const AttnParams& p, int b) {
+  return p.kv_off ? 32 * ((p.kv_off[b + 1] - p.kv_off[b]) / p.Hkv) : p.cap;
+}
+__device__ __forceinline__ size_t req_head_block(const AttnParams& p, int b, int h) {
+  if (p.kv_off) {
+    const int nb = (p.kv_off[b + 1] - p.kv_off[b]) / p.Hkv;
+    return (size_t)p.kv_off[b] + (size_t)h * nb;
+  }
+  return ((size_t)b * p.Hkv + h) * (size_t)(p.cap >> 5);
+}
 
 __device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
   return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
@@ -251,6 +286,204 @@ __device__ __forceinline__ void attn_vt_body(const AttnParams& p, const int unit
 
 
 
+// Unit = (request, kv head, split of split_keys keys) over per-request
+// capacities: the four waves take split_keys / 4 consecutive keys each and
+// walk them one 32-key tile at a time through a two-deep register ring (the
+// next tile's K and V^T operands in flight while this one is computed), then
+// merge in LDS in wave order as attn_vt_body does. split_keys is a multiple
+// of 128, so long contexts need few splits and few partials.
+template <bool WT>
+__device__ __forceinline__ void attn_vl_body(const AttnParams& p, const int unit, unsigned char* lds) {
+  constexpr int kOS = kVtOS;
+  float* s_o = reinterpret_cast<float*>(lds);   // [kVtWaves][32 * kOS]
+  float* s_m = s_o + kVtWaves * 32 * kOS;       // [kVtWaves][32]
+  float* s_l = s_m + kVtWaves * 32;             // [kVtWaves][32]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c32 = lane & 31;
+  const int h2 = lane >> 5;
+  const int s = unit % p.S;
+  const int bh = unit / p.S;
+  const int h = bh % p.Hkv;
+  const int b = bh / p.Hkv;
+  const int rep = p.Hq / p.Hkv;
+  const int qs = p.q_start[b];
+  const int L = p.q_lens ? p.q_lens[b] : p.L;
+  const int capb = req_cap(p, b);
+  const int kv_end = (qs + L < capb) ? qs + L : capb;
+  const int k0u = s * p.split_keys;
+  float* po = p.part_o + (size_t)unit * 32 * kHD;
+  float* pml = p.part_ml + (size_t)unit * 64;
+  if (k0u >= kv_end) {
+    if (tid < 32) {
+      st_f32<WT>(pml + 2 * tid, kNegBig);
+      st_f32<WT>(pml + 2 * tid + 1, 0.f);
+    }
+    return;   // uniform over the workgroup
+  }
+  const int wk = p.split_keys / kVtWaves;
+  const int k0 = k0u + wave * wk;
+  const int k1 = (k0 + wk < kv_end) ? k0 + wk : kv_end;
+
+  const int qcol = c32;
+  const int qr = qcol / p.L;
+  const int qi = qcol - qr * p.L;
+  const bool qvalid = (qr < rep) && (qi < L);
+  const int qbound = qs + qi;
+  f32x16 o[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) o[t] = f32x16{};
+  float m_run = kNegBig;
+  float l_run = 0.f;
+  bf16x8 qop[8];
+  {
+    const uint16_t* qrow = p.q + ((((size_t)b * p.Hq + h * rep + (qvalid ? qr : 0)) * p.L + (qvalid ? qi : 0)) * kHD);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint4 raw = qvalid ? *reinterpret_cast<const uint4*>(qrow + 64 * h2 + 8 * i) : make_uint4(0, 0, 0, 0);
+      qop[i] = __builtin_bit_cast(bf16x8, raw);
+    }
+  }
+  const size_t hb = req_head_block(p, b, h) * 4096;
+  const uint16_t* kbase = p.k + hb;
+  const uint16_t* vbase = p.v + hb;
+  // Tiles at or past k1 reload this wave's first block (valid memory, never used).
+  auto load_tile = [&](uint4 (&kr)[8], uint4 (&vr)[8], int kt) {
+    const size_t blk = (size_t)((kt < k1 ? kt : k0) >> 5) * 4096 + (size_t)lane * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kr[i] = *reinterpret_cast<const uint4*>(kbase + blk + i * 512);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vr[i] = *reinterpret_cast<const uint4*>(vbase + blk + i * 512);
+  };
+  auto tile = [&](const uint4 (&kr)[8], uint4 (&vr)[8], int kt) {
+    f32x16 st = {};
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kr[i]), qop[i], st, 0, 0, 0);
+    float sv[16];
+    float tmax = kNegBig;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kk = kt + 8 * (r >> 2) + 4 * h2 + (r & 3);
+      const bool ok = qvalid && kk < k1 && kk <= qbound;
+      sv[r] = ok ? st[r] * p.scale_log2 : -INFINITY;
+      tmax = fmaxf(tmax, sv[r]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float corr = exp2f(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sv[r] = exp2f(sv[r] - m_new);
+      psum += sv[r];
+    }
+    l_run = l_run * corr + psum;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+    if (kt + kTileKeys > k1) {   // keys past the end: zero V so stale cache bits cannot leak in
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int kbase_e = kt + 16 * jj + 4 * h2;   // slot e<4: kbase_e+e, e>=4: kbase_e+8+e-4
+        uint32_t msk[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int e0 = 2 * w, e1 = 2 * w + 1;
+          const int key0 = kbase_e + (e0 < 4 ? e0 : 8 + e0 - 4);
+          const int key1 = kbase_e + (e1 < 4 ? e1 : 8 + e1 - 4);
+          msk[w] = (key0 < k1 ? 0x0000ffffu : 0u) | (key1 < k1 ? 0xffff0000u : 0u);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          uint4& c = vr[2 * t + jj];
+          c.x &= msk[0];
+          c.y &= msk[1];
+          c.z &= msk[2];
+          c.w &= msk[3];
+        }
+      }
+    }
+    bf16x8 pop[2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      uint32_t pk[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) pk[t] = f2bf2(sv[8 * jj + 2 * t], sv[8 * jj + 2 * t + 1]);
+      pop[jj] = __builtin_bit_cast(bf16x8, pk);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vr[2 * t + jj]), pop[jj], o[t], 0,
+                                                        0, 0);
+  };
+  if (k0 < k1) {
+    uint4 ka[8], va[8], kb[8], vb[8];
+    load_tile(ka, va, k0);
+    load_tile(kb, vb, k0 + kTileKeys);
+    int kt = k0;
+    do {   // one exit, at the bottom; the second step is skipped by a uniform branch
+      tile(ka, va, kt);
+      load_tile(ka, va, kt + 2 * kTileKeys);
+      if (kt + kTileKeys < k1) {
+        tile(kb, vb, kt + kTileKeys);
+        load_tile(kb, vb, kt + 3 * kTileKeys);
+      }
+      kt += 2 * kTileKeys;
+    } while (kt < k1);
+  }
+
+  // Merge the four waves in LDS, wave order (deterministic), as attn_vt_body.
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (h2 == 0) {
+    s_m[wave * 32 + c32] = m_run;
+    s_l[wave * 32 + c32] = l_tot;
+  }
+  __syncthreads();
+  {
+    float mq = s_m[c32];
+#pragma unroll
+    for (int w = 1; w < kVtWaves; ++w) mq = fmaxf(mq, s_m[w * 32 + c32]);
+    const float sc = exp2f(m_run - mq);
+    float* so_w = s_o + wave * 32 * kOS;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<float4*>(&so_w[qcol * kOS + 32 * t + 8 * j + 4 * h2]) =
+            make_float4(o[t][4 * j] * sc, o[t][4 * j + 1] * sc, o[t][4 * j + 2] * sc, o[t][4 * j + 3] * sc);
+  }
+  __syncthreads();
+  for (int idx = 4 * tid; idx < 32 * kHD; idx += 4 * kVtWaves * 64) {
+    const int so = (idx / kHD) * kOS + (idx % kHD);
+    float4 v = *reinterpret_cast<const float4*>(&s_o[so]);
+#pragma unroll
+    for (int w = 1; w < kVtWaves; ++w) {
+      const float4 a = *reinterpret_cast<const float4*>(&s_o[w * 32 * kOS + so]);
+      v.x += a.x;
+      v.y += a.y;
+      v.z += a.z;
+      v.w += a.w;
+    }
+    *reinterpret_cast<float4*>(po + idx) = v;
+  }
+  if (tid < 32) {
+    float M = s_m[tid];
+#pragma unroll
+    for (int w = 1; w < kVtWaves; ++w) M = fmaxf(M, s_m[w * 32 + tid]);
+    float lsum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kVtWaves; ++w) lsum += s_l[w * 32 + tid] * exp2f(s_m[w * 32 + tid] - M);
+    pml[2 * tid] = M;
+    pml[2 * tid + 1] = lsum;
+  }
+}
+
 // Merge item = (request, kv head, query column), one per workgroup of
 // kMergeGroups x 128 threads: thread (g, d) sums column d over group g's
 // contiguous share of the splits, issuing all of its loads together (one
@@ -280,7 +513,8 @@ __device__ __forceinline__ void attn_merge_body(const AttnParams& p, const int i
   const int L = p.q_lens ? p.q_lens[b] : p.L;
   const int qr = q / p.L, qi = q - (q / p.L) * p.L;
   const int kv_end = p.q_start[b] + L;
-  int ns = cdiv(kv_end < p.cap ? kv_end : p.cap, p.split_keys);
+  const int capb = req_cap(p, b);
+  int ns = cdiv(kv_end < capb ? kv_end : capb, p.split_keys);
   if (ns > p.S) ns = p.S;
   const float* ml = p.part_ml + (size_t)bh * p.S * 64 + 2 * q;
   // This thread's partial-O loads go out first: they do not depend on the
@@ -339,8 +573,10 @@ __device__ __forceinline__ void attn_merge_body(const AttnParams& p, const int i
   for (int k = 1; k < kMergeGroups; ++k) tot += s_acc[k * 128 + d];
   const float lsum = s_red[1];
   const float val = (qi < L && lsum > 0.f) ? tot / lsum : 0.f;
-  const size_t oi = p.out_rows ? ((((size_t)b * p.L + qi) * p.Hq + h * rep + qr) * kHD + d)
+  const size_t orow = p.row_off ? (size_t)p.row_off[b] + qi : (size_t)b * p.L + qi;
+  const size_t oi = p.out_rows ? ((orow * p.Hq + h * rep + qr) * kHD + d)
                                : ((((size_t)b * p.Hq + h * rep + qr) * p.L + qi) * kHD + d);
+  if (p.row_off && qi >= L) return;   // packed rows: request b has only L of them
   st_u16<WT>(p.out + oi, f2bf(val));
 }
 

@@ -100,6 +100,67 @@ __global__ void rope_qkv_kernel(const uint16_t* qkv, const int32_t* q_start, con
   }
 }
 
+// Ragged rows into the operand-major block cache: packed row m belongs to
+// request b with row_off[b] <= m < row_off[b+1] (i = m - row_off[b], position
+// q_start[b] + i); q -> q_out [B, Hq, Lmax, D]; K/V into request b's blocks
+// (head h at kv_off[b] + h * nblk_b, nblk_b = (kv_off[b+1] - kv_off[b]) / Hkv;
+// kv_off null: a uniform capacity cap). D = 128.
+__global__ void rope_qkv_blocks_kernel(const uint16_t* qkv, const int32_t* row_off, const int32_t* q_start,
+                                       const int32_t* kv_off, uint16_t* q_out, uint16_t* kc, uint16_t* vc, int B,
+                                       int Lmax, int Hq, int Hkv, int D, int cap, float log2_base, int32_t* status) {
+  const int half = D / 2;
+  const int m = blockIdx.y;
+  int lo = 0, hi = B;   // the b with row_off[b] <= m < row_off[b+1]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (row_off[mid] <= m) lo = mid; else hi = mid;
+  }
+  const int b = lo;
+  const int i = m - row_off[b];
+  const int pos = q_start[b] + i;
+  const int nblk = kv_off ? (kv_off[b + 1] - kv_off[b]) / Hkv : cap / 32;
+  const int capb = 32 * nblk;
+  const size_t blk0 = kv_off ? (size_t)kv_off[b] : (size_t)b * Hkv * nblk;
+  const bool in_cap = pos >= 0 && pos < capb;
+  const int width = (Hq + 2 * Hkv) * D;
+  const uint16_t* row = qkv + (size_t)m * width;
+  const int nrot = (Hq + Hkv) * half;
+  for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < nrot + Hkv * D / 8; t += gridDim.x * blockDim.x) {
+    if (t < nrot) {
+      const int head = t / half;
+      const int j = t - head * half;
+      const uint16_t* src = row + head * D;
+      uint16_t o1, o2;
+      rope_pair(bf2f(src[j]), bf2f(src[j + half]), pos, j, D, log2_base, o1, o2);
+      if (head < Hq) {
+        uint16_t* dst = q_out + (((size_t)b * Hq + head) * Lmax + i) * D;
+        dst[j] = o1;
+        dst[j + half] = o2;
+      } else if (!in_cap) {
+        if (status) atomicOr(status, 1);
+      } else {
+        uint16_t* kh = kc + (blk0 + (size_t)(head - Hq) * nblk) * 4096;
+        kh[kblk_index(pos, j)] = o1;
+        kh[kblk_index(pos, j + half)] = o2;
+      }
+    } else if (!in_cap) {
+      if (status) atomicOr(status, 1);
+    } else {
+      const int e = (t - nrot) * 8;
+      const int head = e / D;
+      const int d = e - head * D;
+      const uint4 val = *reinterpret_cast<const uint4*>(row + (Hq + Hkv) * D + e);
+      uint16_t* vh = vc + (blk0 + (size_t)head * nblk) * 4096;
+      const uint32_t w4[4] = {val.x, val.y, val.z, val.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        vh[vblk_index(pos, d + 2 * u)] = (uint16_t)(w4[u] & 0xffff);
+        vh[vblk_index(pos, d + 2 * u + 1)] = (uint16_t)(w4[u] >> 16);
+      }
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const uint16_t* w, uint16_t* out, int H,
                                                       float eps) {
   const int m = blockIdx.x;
@@ -163,6 +224,23 @@ MTP_API int mtp_rope_qkv_to_cache_vt(const void* qkv, const int32_t* q_start, co
                                      float rope_base, int32_t* status, void* stream) {
   return rope_run(qkv, q_start, q_lens, q_out, k_cache, v_cache, B, L, Hq, Hkv, D, cap, rope_base, status, stream, 1,
                   "mtp_rope_qkv_to_cache_vt");
+}
+
+MTP_API int mtp_rope_qkv_to_blocks(const void* qkv, int M, const int32_t* row_off, const int32_t* q_start,
+                                   const int32_t* kv_off, void* q_out, void* k_blk, void* v_blk, int B, int Lmax,
+                                   int Hq, int Hkv, int D, int cap, float rope_base, int32_t* status, void* stream) {
+  const char* who = "mtp_rope_qkv_to_blocks";
+  if (!qkv || !row_off || !q_start || !q_out || !k_blk || !v_blk || M < 1 || B < 1 || Lmax < 1 || Hq < 1 ||
+      Hkv < 1 || D != 128 || !(rope_base > 1.f) || (!kv_off && (cap < 32 || cap % 32))) {
+    set_error("%s: bad arguments (D = 128; cap a multiple of 32 without kv_off)", who);
+    return MTP_ERR_ARG;
+  }
+  const int work = (Hq + Hkv) * (D / 2) + Hkv * D / 8;
+  dim3 grid(cdiv(work, 256), M);
+  hipLaunchKernelGGL(rope_qkv_blocks_kernel, grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t*)qkv, row_off,
+                     q_start, kv_off, (uint16_t*)q_out, (uint16_t*)k_blk, (uint16_t*)v_blk, B, Lmax, Hq, Hkv, D, cap,
+                     log2f(rope_base), status);
+  return launch_check(who);
 }
 
 MTP_API int mtp_rmsnorm(const void* x, const void* w, void* out, int M, int H, float eps, void* stream) {

@@ -386,6 +386,21 @@ __device__ void build_law(const ChunkPart* parts, int n_chunks, int ksel, int gr
   }
 }
 
+// Rows of request b: target rows t_off[b] .. t_off[b] + K_b, draft rows (and
+// draft ids) d_off[b] .. d_off[b] + K_b - 1, K_b = k_lens[b]; all null: the
+// uniform batch (K_b = K, t_off = b (K + 1), d_off = b K). Outputs keep the
+// uniform strides ([B, K+1] tokens, [B, K] accept probabilities, K = the
+// largest K_b).
+struct AcceptRows {
+  const int32_t* t_off;
+  const int32_t* d_off;
+  const int32_t* k_lens;
+  int nt;   // target rows in all (the draft rows follow them)
+};
+__device__ __forceinline__ int req_k(const AcceptRows& r, int b, int K) { return r.k_lens ? r.k_lens[b] : K; }
+__device__ __forceinline__ int req_t(const AcceptRows& r, int b, int K) { return r.t_off ? r.t_off[b] : b * (K + 1); }
+__device__ __forceinline__ int req_d(const AcceptRows& r, int b, int K) { return r.d_off ? r.d_off[b] : b * K; }
+
 __device__ double law_prob(const RowLaw& L, int tok) {
   for (int i = 0; i < L.n; ++i)
     if (L.ids[i] == tok) return L.probs[i];
@@ -419,9 +434,11 @@ __global__ __launch_bounds__(64) void accept_finish(const ChunkPart* __restrict_
                                                     int greedy, double temp, double top_p,
                                                     int32_t* __restrict__ out_tokens,
                                                     int32_t* __restrict__ n_accepted,
-                                                    double* __restrict__ accept_probs, int32_t* __restrict__ status) {
+                                                    double* __restrict__ accept_probs, int32_t* __restrict__ status,
+                                                    AcceptRows rr) {
   const int b = blockIdx.x;
   const int lane = threadIdx.x;
+  const int Kb = req_k(rr, b, K), tb = req_t(rr, b, K), db = req_d(rr, b, K);
   __shared__ RowLaw s_p, s_q;
   __shared__ uint64_t s_sel[kMaxTopK];
   __shared__ int s_done, s_ui, s_nacc;
@@ -435,25 +452,25 @@ __global__ __launch_bounds__(64) void accept_finish(const ChunkPart* __restrict_
   }
   __syncthreads();
   const double* u = uniforms + (size_t)b * (K + 1);
-  for (int d = 0; d <= K; ++d) {
-    build_law(tparts + ((size_t)b * (K + 1) + d) * n_chunks, n_chunks, ksel, greedy, temp, top_p, &s_p, s_sel);
+  for (int d = 0; d <= Kb; ++d) {
+    build_law(tparts + ((size_t)tb + d) * n_chunks, n_chunks, ksel, greedy, temp, top_p, &s_p, s_sel);
     __syncthreads();
-    if (d < K) {
-      build_law(dparts + ((size_t)b * K + d) * n_chunks, n_chunks, ksel, greedy, temp, top_p, &s_q, s_sel);
+    if (d < Kb) {
+      build_law(dparts + ((size_t)db + d) * n_chunks, n_chunks, ksel, greedy, temp, top_p, &s_q, s_sel);
       __syncthreads();
     }
     if (lane == 0) {
       int32_t* ot = out_tokens + (size_t)b * (K + 1);
-      if (s_p.nonfinite || (d < K && s_q.nonfinite)) {
+      if (s_p.nonfinite || (d < Kb && s_q.nonfinite)) {
         status[b] = 1;
         s_done = 1;
-      } else if (d == K) {
-        // all drafts accepted: bonus from row K
-        ot[K] = greedy ? s_p.ids[0] : law_choice(s_p.ids, s_p.probs, s_p.n, u[s_ui++]);
-        s_nacc = K;
+      } else if (d == Kb) {
+        // all drafts accepted: bonus from row K_b
+        ot[Kb] = greedy ? s_p.ids[0] : law_choice(s_p.ids, s_p.probs, s_p.n, u[s_ui++]);
+        s_nacc = Kb;
         s_done = 1;
       } else {
-        const int tok = draft_ids[(size_t)b * K + d];
+        const int tok = draft_ids[(size_t)db + d];
         const double p = law_prob(s_p, tok);
         const double q = law_prob(s_q, tok);
         double a;
@@ -670,7 +687,9 @@ __device__ int law_choice_wave(const int* ids, const double* p, int n, double u)
 // The accept loop of one request over its prebuilt laws (target rows 0..K,
 // draft rows 0..K-1); run by one whole wave. s_rid / s_rp: LDS scratch of
 // kMaxTopK entries for the residual law.
-__device__ void accept_loop_wave(const RowLaw* tl, const RowLaw* dl, int b, int K, int greedy,
+// Kb: this request's depth; K: the row stride of the outputs; db: the index
+// of its first draft id.
+__device__ void accept_loop_wave(const RowLaw* tl, const RowLaw* dl, int b, int Kb, int K, int db, int greedy,
                                  const int32_t* __restrict__ draft_ids, const double* __restrict__ uniforms,
                                  int32_t* __restrict__ out_tokens, int32_t* __restrict__ n_accepted,
                                  double* __restrict__ accept_probs, int32_t* __restrict__ status, int* s_rid,
@@ -681,20 +700,20 @@ __device__ void accept_loop_wave(const RowLaw* tl, const RowLaw* dl, int b, int 
   for (int d = lane; d < K; d += 64) accept_probs[(size_t)b * K + d] = -1.0;
   const double* u = uniforms + (size_t)b * (K + 1);
   int ui = 0, nacc = 0, bad = 0;
-  for (int d = 0; d <= K; ++d) {
+  for (int d = 0; d <= Kb; ++d) {
     const RowLaw& P = tl[d];
-    if (P.nonfinite || (d < K && dl[d].nonfinite)) {
+    if (P.nonfinite || (d < Kb && dl[d].nonfinite)) {
       bad = 1;
       break;
     }
-    if (d == K) {   // all drafts accepted: bonus from row K
+    if (d == Kb) {   // all drafts accepted: bonus from row K_b
       const int tok = greedy ? P.ids[0] : law_choice_wave(P.ids, P.probs, P.n, u[ui++]);
-      if (lane == 0) ot[K] = tok;
-      nacc = K;
+      if (lane == 0) ot[Kb] = tok;
+      nacc = Kb;
       break;
     }
     const RowLaw& Qd = dl[d];
-    const int tok = draft_ids[(size_t)b * K + d];
+    const int tok = draft_ids[(size_t)db + d];
     const double p = law_prob_wave(P, tok);
     const double q = law_prob_wave(Qd, tok);
     double a;
@@ -768,25 +787,27 @@ __global__ __launch_bounds__(1024) void accept_laws(const ChunkPart* __restrict_
                                                     int greedy, double temp, double top_p,
                                                     int32_t* __restrict__ out_tokens,
                                                     int32_t* __restrict__ n_accepted,
-                                                    double* __restrict__ accept_probs, int32_t* __restrict__ status) {
+                                                    double* __restrict__ accept_probs, int32_t* __restrict__ status,
+                                                    AcceptRows rr) {
   extern __shared__ __align__(16) unsigned char s_lds[];
   const int b = blockIdx.x;
   const int nwv = blockDim.x >> 6;
   const int wave = threadIdx.x >> 6;
-  const int nlaw = 2 * K + 1;
-  RowLaw* laws = reinterpret_cast<RowLaw*>(s_lds);
-  uint64_t* keys = reinterpret_cast<uint64_t*>(s_lds + (size_t)nlaw * sizeof(RowLaw)) + (size_t)wave * kLawKeys;
+  const int Kb = req_k(rr, b, K), tb = req_t(rr, b, K), db = req_d(rr, b, K);
+  const int nlaw = 2 * Kb + 1;
+  RowLaw* laws = reinterpret_cast<RowLaw*>(s_lds);   // sized for 2K + 1 laws
+  uint64_t* keys = reinterpret_cast<uint64_t*>(s_lds + (size_t)(2 * K + 1) * sizeof(RowLaw)) + (size_t)wave * kLawKeys;
   for (int li = wave; li < nlaw; li += nwv) {
-    const ChunkPart* rp = li <= K ? tparts + ((size_t)b * (K + 1) + li) * n_chunks
-                                  : dparts + ((size_t)b * K + (li - K - 1)) * n_chunks;
+    const ChunkPart* rp = li <= Kb ? tparts + ((size_t)tb + li) * n_chunks
+                                   : dparts + ((size_t)db + (li - Kb - 1)) * n_chunks;
     build_law_wave(rp, n_chunks, ksel, greedy, temp, top_p, &laws[li], keys);
   }
   __syncthreads();
   if (wave == 0) {   // the residual scratch reuses wave 0's key area
     double* s_rp = reinterpret_cast<double*>(keys);
     int* s_rid = reinterpret_cast<int*>(s_rp + kMaxTopK);
-    accept_loop_wave(laws, laws + K + 1, b, K, greedy, draft_ids, uniforms, out_tokens, n_accepted, accept_probs,
-                     status, s_rid, s_rp);
+    accept_loop_wave(laws, laws + Kb + 1, b, Kb, K, db, greedy, draft_ids, uniforms, out_tokens, n_accepted,
+                     accept_probs, status, s_rid, s_rp);
   }
 }
 
@@ -1166,9 +1187,11 @@ __global__ __launch_bounds__(kWideThreads) void wide_accept_kernel(
     const unsigned char* __restrict__ lawbuf, size_t row_bytes, int V, int B, int K,
     const int32_t* __restrict__ draft_ids, const double* __restrict__ uniforms, int32_t* __restrict__ out_tokens,
     int32_t* __restrict__ n_accepted, double* __restrict__ accept_probs, int32_t* __restrict__ status,
-    unsigned char* __restrict__ scratch) {
+    unsigned char* __restrict__ scratch, AcceptRows rr) {
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
+  const int Kb = req_k(rr, b, K), tb = req_t(rr, b, K), db = req_d(rr, b, K);
+  const int nt = rr.t_off ? rr.nt : B * (K + 1);
   __shared__ double s_d[kWideWaves];
   __shared__ double s_last, s_p, s_q;
   __shared__ uint32_t s_w[kWideWaves + 1];
@@ -1179,20 +1202,20 @@ __global__ __launch_bounds__(kWideThreads) void wide_accept_kernel(
   for (int d = tid; d < K; d += kWideThreads) accept_probs[(size_t)b * K + d] = -1.0;
   const double* u = uniforms + (size_t)b * (K + 1);
   int ui = 0, nacc = 0, bad = 0;
-  for (int d = 0; d <= K; ++d) {
-    const WideLaw P = wide_law(lawbuf, row_bytes, V, b * (K + 1) + d);
-    const WideLaw Q = d < K ? wide_law(lawbuf, row_bytes, V, B * (K + 1) + b * K + d) : P;
+  for (int d = 0; d <= Kb; ++d) {
+    const WideLaw P = wide_law(lawbuf, row_bytes, V, tb + d);
+    const WideLaw Q = d < Kb ? wide_law(lawbuf, row_bytes, V, nt + db + d) : P;
     if (P.nonfinite || Q.nonfinite) {
       bad = 1;
       break;
     }
-    if (d == K) {   // all drafts accepted: bonus from row K
+    if (d == Kb) {   // all drafts accepted: bonus from row K_b
       const int tok = block_choice(P.ids, P.probs, P.n, u[ui++], s_d, &s_last, s_w);
-      if (tid == 0) ot[K] = tok;
-      nacc = K;
+      if (tid == 0) ot[Kb] = tok;
+      nacc = Kb;
       break;
     }
-    const int tok = draft_ids[(size_t)b * K + d];
+    const int tok = draft_ids[(size_t)db + d];
     if (tid == 0) {
       s_p = wide_prob(P, tok);
       s_q = wide_prob(Q, tok);
@@ -1312,20 +1335,21 @@ MTP_API size_t mtp_sampler_workspace_bytes(int rows, int V, int top_k) {
   return n;
 }
 
-MTP_API int mtp_spec_accept(const float* target_logits, const float* draft_logits, const int32_t* draft_ids,
-                            const double* uniforms, int B, int K, int V, double temperature, int top_k,
-                            double top_p, int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status,
-                            void* ws, size_t ws_bytes, void* stream) {
-  const char* who = "mtp_spec_accept";
+// The accept step over nt target and nd draft rows (the uniform batch has
+// nt = B (K + 1), nd = B K and null offsets).
+static int spec_accept_run(const float* target_logits, const float* draft_logits, const int32_t* draft_ids,
+                           const double* uniforms, int B, int K, int V, double temperature, int top_k, double top_p,
+                           int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
+                           size_t ws_bytes, void* stream, AcceptRows rr, int nt, int nd, const char* who) {
   SamplerPlan pl;
   int rc = sampler_plan(V, top_k, temperature, &pl, who);
   if (rc) return rc;
-  if (B < 1 || K < 1 || !target_logits || !draft_logits || !draft_ids || !uniforms || !out_tokens ||
-      !n_accepted || !accept_probs || !status) {
+  if (B < 1 || K < 1 || nt < B || nd < 0 || !target_logits || (nd > 0 && !draft_logits) || !draft_ids || !uniforms ||
+      !out_tokens || !n_accepted || !accept_probs || !status) {
     set_error("%s: need B>=1, K>=1 and non-null buffers", who);
     return MTP_ERR_ARG;
   }
-  const int rows = B * (2 * K + 1);
+  const int rows = nt + nd;
   const size_t need = mtp_sampler_workspace_bytes(rows, V, pl.greedy ? 1 : top_k);
   if (!ws || ws_bytes < need) {
     set_error("%s: workspace %zu B < required %zu B", who, ws_bytes, need);
@@ -1334,20 +1358,23 @@ MTP_API int mtp_spec_accept(const float* target_logits, const float* draft_logit
   hipStream_t st = (hipStream_t)stream;
   const int n_chunks = pl.n_chunks;
   ChunkPart* tparts = reinterpret_cast<ChunkPart*>(ws);
-  ChunkPart* dparts = tparts + (size_t)B * (K + 1) * n_chunks;
+  ChunkPart* dparts = tparts + (size_t)nt * n_chunks;
   const double temp = pl.greedy ? 1.0 : temperature;
+  rr.nt = nt;
   // target rows then draft rows, one launch (dparts follows tparts)
   hipLaunchKernelGGL(vocab_partials, dim3(n_chunks, rows), dim3(kSampThreads), 0, st, target_logits,
-                     draft_logits, B * (K + 1), (long long)V, V, n_chunks, temp, pl.ksel, pl.greedy, tparts);
+                     draft_logits ? draft_logits : target_logits, nt, (long long)V, V, n_chunks, temp, pl.ksel,
+                     pl.greedy, tparts);
   if ((rc = launch_check(who))) return rc;
   if (pl.wide) {
     unsigned char* lawbuf = reinterpret_cast<unsigned char*>(ws) + parts_bytes(rows, V);
     const size_t rb = wide_row_bytes(V);
-    hipLaunchKernelGGL(wide_law_kernel, dim3(rows), dim3(kWideThreads), 0, st, target_logits, draft_logits,
-                       B * (K + 1), (long long)V, V, tparts, n_chunks, temp, pl.k_eff, top_p, lawbuf, rb);
+    hipLaunchKernelGGL(wide_law_kernel, dim3(rows), dim3(kWideThreads), 0, st, target_logits,
+                       draft_logits ? draft_logits : target_logits, nt, (long long)V, V, tparts, n_chunks, temp,
+                       pl.k_eff, top_p, lawbuf, rb);
     if ((rc = launch_check(who))) return rc;
     hipLaunchKernelGGL(wide_accept_kernel, dim3(B), dim3(kWideThreads), 0, st, lawbuf, rb, V, B, K, draft_ids,
-                       uniforms, out_tokens, n_accepted, accept_probs, status, lawbuf + (size_t)rows * rb);
+                       uniforms, out_tokens, n_accepted, accept_probs, status, lawbuf + (size_t)rows * rb, rr);
   } else if (n_chunks <= 64) {
     const int nwv = 2 * K + 1 < 16 ? 2 * K + 1 : 16;
     const size_t lds = accept_laws_lds(K, nwv);
@@ -1359,12 +1386,41 @@ MTP_API int mtp_spec_accept(const float* target_logits, const float* draft_logit
     if (lds > 65536) (void)hipFuncSetAttribute((const void*)accept_laws, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)lds);
     hipLaunchKernelGGL(accept_laws, dim3(B), dim3(nwv * 64), lds, st, tparts, dparts, n_chunks, draft_ids, uniforms,
-                       K, pl.ksel, pl.greedy, temp, top_p, out_tokens, n_accepted, accept_probs, status);
+                       K, pl.ksel, pl.greedy, temp, top_p, out_tokens, n_accepted, accept_probs, status, rr);
   } else {
     hipLaunchKernelGGL(accept_finish, dim3(B), dim3(64), 0, st, tparts, dparts, n_chunks, draft_ids, uniforms, K,
-                       pl.ksel, pl.greedy, temp, top_p, out_tokens, n_accepted, accept_probs, status);
+                       pl.ksel, pl.greedy, temp, top_p, out_tokens, n_accepted, accept_probs, status, rr);
   }
   return launch_check(who);
+}
+
+MTP_API int mtp_spec_accept(const float* target_logits, const float* draft_logits, const int32_t* draft_ids,
+                            const double* uniforms, int B, int K, int V, double temperature, int top_k,
+                            double top_p, int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status,
+                            void* ws, size_t ws_bytes, void* stream) {
+  if (B < 1 || K < 1) {
+    set_error("mtp_spec_accept: need B>=1, K>=1");
+    return MTP_ERR_ARG;
+  }
+  return spec_accept_run(target_logits, draft_logits, draft_ids, uniforms, B, K, V, temperature, top_k, top_p,
+                         out_tokens, n_accepted, accept_probs, status, ws, ws_bytes, stream, AcceptRows{}, B * (K + 1),
+                         B * K, "mtp_spec_accept");
+}
+
+MTP_API int mtp_spec_accept_ragged(const float* target_logits, int n_target, const float* draft_logits, int n_draft,
+                                   const int32_t* t_off, const int32_t* d_off, const int32_t* k_lens,
+                                   const int32_t* draft_ids, const double* uniforms, int B, int K_max, int V,
+                                   double temperature, int top_k, double top_p, int32_t* out_tokens,
+                                   int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
+                                   size_t ws_bytes, void* stream) {
+  if (!t_off || !d_off || !k_lens) {
+    set_error("mtp_spec_accept_ragged: t_off, d_off and k_lens are required");
+    return MTP_ERR_ARG;
+  }
+  AcceptRows rr{t_off, d_off, k_lens, n_target};
+  return spec_accept_run(target_logits, draft_logits, draft_ids, uniforms, B, K_max, V, temperature, top_k, top_p,
+                         out_tokens, n_accepted, accept_probs, status, ws, ws_bytes, stream, rr, n_target, n_draft,
+                         "mtp_spec_accept_ragged");
 }
 
 // ---- No-allocation variant --------------------------------------------------

@@ -273,8 +273,12 @@ def moe_combine(y_sorted: torch.Tensor, inv_order, route_weights: torch.Tensor, 
     gate_ld = 1
     if shared_gate is not None:
         gate_ld = int(shared_gate.stride(0)) if shared_gate.dim() > 0 else 1
-    _lib.call("mtp_moe_combine", y_sorted.contiguous().data_ptr(), inv.to(torch.int32).contiguous().data_ptr(),
-              w.data_ptr(), _lib.ptr(shared), _lib.ptr(shared_gate), gate_ld, _lib.ptr(resid), out.data_ptr(), T,
+    # Converted copies are bound to names so that each stays allocated until
+    # the call has been queued (a freed temporary's block can be handed to the
+    # next temporary in the same argument list).
+    ys = y_sorted.contiguous()
+    inv32 = inv.to(torch.int32).contiguous()
+    _lib.call("mtp_moe_combine", ys.data_ptr(), inv32.data_ptr(), w.data_ptr(), _lib.ptr(shared), _lib.ptr(shared_gate), gate_ld, _lib.ptr(resid), out.data_ptr(), T,
               top_k, H, _lib.stream_handle(y_sorted.device))
     return out
 

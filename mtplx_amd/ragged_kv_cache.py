@@ -166,8 +166,9 @@ class RaggedBatchKVCache:
         self._own_buffers()
         if self._status is None or self._status.device != keys.device:
             self._status = torch.zeros(1, dtype=torch.int32, device=keys.device)
-        _lib.call("mtp_kv_scatter", self.keys.data_ptr(), self.values.data_ptr(), keys.contiguous().data_ptr(),
-                  values.contiguous().data_ptr(), start.data_ptr(), B, H, int(self.keys.shape[2]), q, D,
+        kc, vc = keys.contiguous(), values.contiguous()   # named: both must stay allocated
+        _lib.call("mtp_kv_scatter", self.keys.data_ptr(), self.values.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                  start.data_ptr(), B, H, int(self.keys.shape[2]), q, D,
                   self._status.data_ptr(), _lib.stream_handle(keys.device))
         self.offsets = resulting.to(torch.int32)
         return self.keys, self.values
@@ -304,7 +305,8 @@ class RaggedBatchKVCache:
         B, H, _, D = (int(s) for s in self.keys.shape)
         st = _lib.stream_handle(self.keys.device)
         for cur, sn in ((self.keys, snap.keys), (self.values, snap.values)):
-            _lib.call("mtp_kv_restore_masked", cur.data_ptr(), sn.contiguous().data_ptr(), m8.data_ptr(), B, H, cap,
+            sn = sn.contiguous()
+            _lib.call("mtp_kv_restore_masked", cur.data_ptr(), sn.data_ptr(), m8.data_ptr(), B, H, cap,
                       int(sn.shape[2]), D, lo, hi, st)
 
 

@@ -281,3 +281,36 @@ def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_i
               float(config.temperature), int(config.top_k), float(config.top_p), out.data_ptr(), nacc.data_ptr(),
               ap.data_ptr(), st.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_handle(dev))
     return AcceptResult(out, nacc, ap, st)
+
+
+def spec_accept_ragged(target_rows: torch.Tensor, t_off: torch.Tensor, draft_rows: torch.Tensor, d_off: torch.Tensor,
+                       k_lens: torch.Tensor, draft_ids: torch.Tensor, uniforms: torch.Tensor,
+                       config: SamplerConfig) -> AcceptResult:
+    """Accept/reject for a ragged batch (per-request depths K_b, the
+    continuous-batched lane of ``mtplx/batched_decode.py:338-395``): request
+    b's K_b + 1 target rows start at row ``t_off[b]`` of ``target_rows``
+    ``[n_target, V]``, its K_b draft rows (and draft ids) at ``d_off[b]`` of
+    ``draft_rows`` ``[n_draft, V]`` / ``draft_ids`` ``[n_draft]``; uniforms
+    ``[B, K_max + 1]``. Outputs are ``[B, K_max + 1]`` tokens (-1 padded) and
+    ``[B, K_max]`` accept probabilities. No penalties on this lane."""
+    t = _rows(target_rows)
+    d = _rows(draft_rows)
+    dev = t.device
+    B = int(k_lens.numel())
+    K = int(uniforms.shape[-1]) - 1
+    V = int(t.shape[-1])
+    i32 = dict(device=dev, dtype=torch.int32)
+    to, do, kl = (x.to(**i32).contiguous() for x in (t_off, d_off, k_lens))
+    di = draft_ids.to(**i32).contiguous()
+    u = uniforms.to(device=dev, dtype=torch.float64).contiguous()
+    out = torch.empty((B, K + 1), **i32)
+    nacc = torch.empty(B, **i32)
+    ap = torch.empty((B, K), dtype=torch.float64, device=dev)
+    st = torch.empty(B, **i32)
+    nb = _lib.query("mtp_sampler_workspace_bytes", int(t.shape[0]) + int(d.shape[0]), V, int(config.top_k))
+    ws = _lib.WORKSPACES.get(nb, "sampler", dev)
+    _lib.call("mtp_spec_accept_ragged", t.data_ptr(), int(t.shape[0]), d.data_ptr(), int(d.shape[0]), to.data_ptr(),
+              do.data_ptr(), kl.data_ptr(), di.data_ptr(), u.data_ptr(), B, K, V, float(config.temperature),
+              int(config.top_k), float(config.top_p), out.data_ptr(), nacc.data_ptr(), ap.data_ptr(), st.data_ptr(),
+              ws.data_ptr(), ws.numel(), _lib.stream_handle(dev))
+    return AcceptResult(out, nacc, ap, st)

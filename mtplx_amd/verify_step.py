@@ -201,6 +201,48 @@ class VerifyModel:
         self.cap = cap
         self.batch = batch
 
+    def allocate_cache_blocks(self, capacities, *, fill_random: bool = True) -> None:
+        """A ragged cache for the continuous-batched lane: request b gets its
+        own capacity (rounded up to 32 keys) inside one packed buffer of
+        operand-major 32-key blocks per layer; ``kv_off`` int32 [B+1] holds
+        each request's first block (head h at kv_off[b] + h * nblk_b)."""
+        c = self.cfg
+        caps = [((int(x) + 31) // 32) * 32 for x in capacities]
+        offs = [0]
+        for cp in caps:
+            offs.append(offs[-1] + c.n_kv_heads * (cp // 32))
+        nblocks = offs[-1]
+        self.k_cache, self.v_cache = [], []
+        for _ in range(c.layers):
+            if fill_random:
+                k = torch.empty(nblocks * 4096, dtype=torch.bfloat16, device=self.device)
+                v = torch.empty_like(k)
+                step = 1 << 26   # fill in slices: bounded fp32 temporaries
+                for t in (k, v):
+                    for i in range(0, t.numel(), step):
+                        n = min(step, t.numel() - i)
+                        t[i:i + n] = torch.randn(n, generator=self.gen, device=self.device).to(torch.bfloat16)
+            else:
+                k = torch.zeros(nblocks * 4096, dtype=torch.bfloat16, device=self.device)
+                v = torch.zeros_like(k)
+            self.k_cache.append(k)
+            self.v_cache.append(v)
+        self.caps = caps
+        self.cap = max(caps)
+        self.total_cap = sum(caps)
+        self.batch = len(caps)
+        self.kv_off = torch.tensor(offs, dtype=torch.int32, device=self.device)
+        self._kv_off_host = offs
+
+    def cache_request(self, li: int, b: int, kind: str) -> torch.Tensor:
+        """Request b's K ("k") or V ("v") cache of layer li in the reference
+        layout [Hkv, cap_b, D] (from a block cache made by allocate_cache_blocks)."""
+        c = self.cfg
+        o0, o1 = self._kv_off_host[b], self._kv_off_host[b + 1]
+        buf = (self.k_cache if kind == "k" else self.v_cache)[li]
+        blk = buf[o0 * 4096:o1 * 4096].reshape(1, c.n_kv_heads, (o1 - o0) // c.n_kv_heads * 32, c.head_dim)
+        return kv_from_blocks(blk, kind)[0]
+
     # K and V caches are kept in the operand-major 32-key block layout
     # (include/mtplx_amd.h); these give the reference [B, Hkv, cap, D] view.
     def k_cache_standard(self, li: int) -> torch.Tensor:
@@ -364,6 +406,89 @@ class VerifyModel:
         qmv(st, x=sh_act, w0=W(L.shared_down), y0=shared, M=M, N=H, K=c.shared_ffn, group_size=gs, xmode=0,
             emode=0, packed=lay)
         moe_combine(ysorted, es, wts, shared, shared_gate=rl[:, E], resid=h, out=h)
+
+    def verify_logits_ragged(self, tokens: torch.Tensor, row_off: torch.Tensor, q_start: torch.Tensor,
+                             q_lens: torch.Tensor, Lmax: int, *, logits_out: torch.Tensor | None = None,
+                             check: bool = False) -> torch.Tensor:
+        """The continuous-batched verify forward (dense model, block cache from
+        :meth:`allocate_cache_blocks`): ``tokens`` int32 [M] packed request
+        after request, request b's ``q_lens[b]`` (<= ``Lmax``) rows at
+        ``row_off[b]`` (int32 [B+1]) and positions ``q_start[b] + i``. Every
+        projection runs on ``mtp_qmm_affine4_mfma`` (each weight quad read once
+        for all M <= 64 rows); RoPE writes K/V into the requests' blocks;
+        attention reads per-request capacities. Returns fp32 logits [M, V]."""
+        c = self.cfg
+        if c.n_experts:
+            raise NotImplementedError("the ragged lane serves the dense model")
+        M = int(tokens.numel())
+        B = int(q_start.numel())
+        dev = self.device
+        st = _lib.stream_handle(dev)
+        call = _lib.call
+        H, gs = c.hidden, c.group_size
+        status = torch.zeros(1, dtype=torch.int32, device=dev)
+        h = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+        xn = torch.empty_like(h)
+        tok = tokens.reshape(-1).to(torch.int32).contiguous()
+        call("mtp_embed_affine4", tok.data_ptr(), self.embed.weight.data_ptr(), self.embed.scales.data_ptr(),
+             self.embed.biases.data_ptr(), h.data_ptr(), M, H, c.vocab, gs, status.data_ptr(), st)
+        qkv = torch.empty((M, c.qkv_out), dtype=torch.bfloat16, device=dev)
+        qh = torch.empty((B, c.n_heads, Lmax, c.head_dim), dtype=torch.bfloat16, device=dev)
+        attn = torch.empty((M, c.n_heads * c.head_dim), dtype=torch.bfloat16, device=dev)
+        act = torch.empty((M, c.ffn), dtype=torch.bfloat16, device=dev)
+        ro = row_off.to(torch.int32).contiguous()
+        ql = q_lens.to(torch.int32).contiguous()
+        qmm_nb = max(_lib.query("mtp_qmm_workspace_bytes", M, n, k, d) for n, k, d in
+                     ((c.qkv_out, H, 0), (H, c.n_heads * c.head_dim, 0), (c.ffn, H, 1), (H, c.ffn, 0),
+                      (c.vocab, H, 0)))
+        qws = _lib.WORKSPACES.get(max(qmm_nb, 256), "qmm", dev)
+        anb = _lib.query("mtp_attn_blocks_workspace_bytes", B, c.n_kv_heads, self.cap, self.total_cap, 0)
+        aws = _lib.WORKSPACES.get(anb, "attn_blocks", dev)
+        scale = 1.0 / math.sqrt(c.head_dim)
+        eps = ctypes.c_float(c.rms_eps)
+
+        def mm(**kw):
+            _lib.qmm_mfma(st, M=M, group_size=gs, ws=qws, ws_bytes=qws.numel(), **kw)
+
+        def norm(x, w, out):
+            call("mtp_rmsnorm", x.data_ptr(), w.data_ptr(), out.data_ptr(), M, H, eps, st)
+
+        for li, L in enumerate(self.layers):
+            norm(h, L.in_norm, xn)
+            mm(x=xn, w0=L.qkv.packed, y=qkv, N=c.qkv_out, K=H, emode=0)
+            call("mtp_rope_qkv_to_blocks", qkv.data_ptr(), M, ro.data_ptr(), q_start.data_ptr(),
+                 self.kv_off.data_ptr(), qh.data_ptr(), self.k_cache[li].data_ptr(), self.v_cache[li].data_ptr(), B,
+                 Lmax, c.n_heads, c.n_kv_heads, c.head_dim, self.cap, ctypes.c_float(c.rope_theta),
+                 status.data_ptr(), st)
+            _lib.attn_blocks(st, q=qh, k_blk=self.k_cache[li], v_blk=self.v_cache[li], q_start=q_start, q_lens=ql,
+                             row_off=ro, kv_off=self.kv_off, out=attn, B=B, Hq=c.n_heads, Hkv=c.n_kv_heads, Lmax=Lmax,
+                             D=c.head_dim, cap=self.cap, split_keys=0, scale=scale, total_cap=self.total_cap, ws=aws,
+                             ws_bytes=aws.numel())
+            mm(x=attn, w0=L.o.packed, y=h, resid=h, N=H, K=c.n_heads * c.head_dim, emode=1)
+            norm(h, L.post_norm, xn)
+            mm(x=xn, w0=L.gate.packed, w1=L.up.packed, y=act, N=c.ffn, K=H, emode=3)
+            mm(x=act, w0=L.down.packed, y=h, resid=h, N=H, K=c.ffn, emode=1)
+        norm(h, self.final_norm, xn)
+        logits = logits_out if logits_out is not None else torch.empty((M, c.vocab), dtype=torch.float32, device=dev)
+        mm(x=xn, w0=self.lm_head.packed, yf=logits, N=c.vocab, K=H, emode=0)
+        self._status = status
+        if check:
+            self.check_status()
+        return logits
+
+    def verify_step_ragged(self, tokens: torch.Tensor, row_off: torch.Tensor, q_start: torch.Tensor,
+                           q_lens: torch.Tensor, Lmax: int, draft_logits: torch.Tensor, d_off: torch.Tensor,
+                           draft_index: torch.Tensor, uniforms: torch.Tensor, sampler: SamplerConfig = SamplerConfig()):
+        """Ragged forward, then accept/reject with per-request depths
+        K_b = q_lens[b] - 1: request b's draft ids are ``tokens[draft_index]``
+        entries d_off[b] .. d_off[b] + K_b - 1 (the rows after its primary) and
+        its draft rows the same rows of ``draft_logits``."""
+        from .sampling import spec_accept_ragged
+
+        logits = self.verify_logits_ragged(tokens, row_off, q_start, q_lens, Lmax)
+        self.last_logits = logits
+        drafts = tokens.reshape(-1)[draft_index]
+        return spec_accept_ragged(logits, row_off[:-1], draft_logits, d_off, q_lens - 1, drafts, uniforms, sampler)
 
     def verify_step(self, tokens: torch.Tensor, q_start: torch.Tensor, draft_logits: torch.Tensor,
                     uniforms: torch.Tensor, sampler: SamplerConfig = SamplerConfig()):

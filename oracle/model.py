@@ -59,26 +59,44 @@ def verify_forward(params: dict, cfg, tokens: np.ndarray, q_start: np.ndarray, k
     ``k_cache``/``v_cache`` are per-layer float64 arrays [B, Hkv, cap, D],
     updated in place at ``q_start[b] + i``. ``routes``, if a list, receives
     each MoE layer's ``(ids, weights)``."""
-    B, L = tokens.shape
-    M = B * L
+    tokens = np.asarray(tokens)
+    return verify_forward_ragged(params, cfg, list(tokens), q_start, k_cache, v_cache, routes)
+
+
+def verify_forward_ragged(params: dict, cfg, tokens: list, q_start, k_cache: list, v_cache: list,
+                          routes: list | None = None) -> np.ndarray:
+    """The same forward over a ragged batch: request b has ``len(tokens[b])``
+    rows at positions ``q_start[b] + i``; rows are packed request after
+    request (logits [sum_b L_b, V]). ``k_cache[li][b]`` is request b's
+    float64 [Hkv, cap_b, D] cache of layer li (a [B, Hkv, cap, D] array or a
+    list of per-request arrays), updated in place."""
     gs = cfg.group_size
     H, D, Hq, Hkv = cfg.hidden, cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    lens = [len(t) for t in tokens]
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    flat = np.concatenate([np.asarray(t).reshape(-1) for t in tokens])
+    M = int(offs[-1])
     emb = params["embed"]
     h = round_to_bf16(np.stack([dequantize_affine4(emb[0][t:t + 1], emb[1][t:t + 1], emb[2][t:t + 1], gs)[0]
-                                for t in tokens.reshape(-1)]))
-    pos = (np.asarray(q_start)[:, None] + np.arange(L)[None, :])  # [B, L]
+                                for t in flat]))
     for li, lay in enumerate(params["layers"]):
         xn = round_to_bf16(rmsnorm(h, lay["in_norm"], cfg.rms_eps))
-        qkv = round_to_bf16(qmm_affine4(xn, *lay["qkv"], gs)).reshape(B, L, Hq + 2 * Hkv, D)
-        q = round_to_bf16(rope_rotate_half(qkv[:, :, :Hq].transpose(0, 2, 1, 3), pos[:, None, :], cfg.rope_theta))
-        k = round_to_bf16(rope_rotate_half(qkv[:, :, Hq:Hq + Hkv].transpose(0, 2, 1, 3), pos[:, None, :],
-                                           cfg.rope_theta))
-        v = qkv[:, :, Hq + Hkv:].transpose(0, 2, 1, 3)
-        for b in range(B):
-            k_cache[li][b, :, q_start[b]:q_start[b] + L] = k[b]
-            v_cache[li][b, :, q_start[b]:q_start[b] + L] = v[b]
-        att = round_to_bf16(ragged_gqa_attention(q, k_cache[li], v_cache[li], q_start))   # [B, Hq, L, D]
-        att = att.transpose(0, 2, 1, 3).reshape(M, Hq * D)
+        qkv = round_to_bf16(qmm_affine4(xn, *lay["qkv"], gs)).reshape(M, Hq + 2 * Hkv, D)
+        att = np.zeros((M, Hq * D))
+        for b, L in enumerate(lens):
+            if L == 0:
+                continue
+            rows = slice(int(offs[b]), int(offs[b + 1]))
+            pos = int(q_start[b]) + np.arange(L)
+            blk = qkv[rows].transpose(1, 0, 2)                       # [heads, L, D]
+            q = round_to_bf16(rope_rotate_half(blk[:Hq], pos[None, :], cfg.rope_theta))
+            k = round_to_bf16(rope_rotate_half(blk[Hq:Hq + Hkv], pos[None, :], cfg.rope_theta))
+            v = blk[Hq + Hkv:]
+            kc, vc = k_cache[li][b], v_cache[li][b]
+            kc[:, pos[0]:pos[0] + L] = k
+            vc[:, pos[0]:pos[0] + L] = v
+            o = round_to_bf16(ragged_gqa_attention(q[None], kc[None], vc[None], [int(q_start[b])]))[0]
+            att[rows] = o.transpose(1, 0, 2).reshape(L, Hq * D)
         h = round_to_bf16(round_to_bf16(qmm_affine4(att, *lay["o"], gs)) + h)
         xn = round_to_bf16(rmsnorm(h, lay["post_norm"], cfg.rms_eps))
         if cfg.n_experts:

@@ -315,3 +315,31 @@ def test_moe_block_halves_are_both_added():
     assert np.array_equal(run(dict(lay, expert_down=zero_routed, shared_down=zero_shared)), want)
     assert not np.allclose(run(dict(lay, expert_down=zero_routed)), want)
     assert not np.allclose(run(dict(lay, shared_down=zero_shared)), want)
+
+
+def test_ragged_batch_equals_scalar_restatement_per_request():
+    """The ragged forward (requests of 1, 3 and 2 rows, capacities 8, 16 and
+    24, rows packed request after request) equals the scalar restatement run
+    on each request alone, so no row reads another request's tokens, cache
+    or positions."""
+    from oracle.model import verify_forward_ragged
+    cfg = _cfg(layers=1)
+    rng = np.random.default_rng(8)
+    params = _params(cfg, rng)
+    caps, lens, q_start = [8, 16, 24], [1, 3, 2], np.array([7, 2, 20])
+    kc = [[round_to_bf16(rng.normal(size=(cfg.n_kv_heads, c, cfg.head_dim))) for c in caps]]
+    vc = [[round_to_bf16(rng.normal(size=(cfg.n_kv_heads, c, cfg.head_dim))) for c in caps]]
+    kc2 = [[a.copy() for a in kc[0]]]
+    vc2 = [[a.copy() for a in vc[0]]]
+    tokens = [rng.integers(0, cfg.vocab, size=L) for L in lens]
+    got = verify_forward_ragged(params, cfg, tokens, q_start, kc, vc)
+    assert got.shape == (sum(lens), cfg.vocab)
+    r = 0
+    for b, L in enumerate(lens):
+        tb = tokens[b].reshape(1, L)
+        h = _embed_scalar(params, cfg, tb)
+        h = _layer_scalar(cfg, params["layers"][0], h, tb.shape, q_start[b:b + 1], kc2[0][b][None],
+                          vc2[0][b][None])
+        want = _head_scalar(params, cfg, h)
+        assert np.allclose(got[r:r + L], want, rtol=2 ** -7, atol=1e-9), b
+        r += L
