@@ -204,13 +204,13 @@ def roofline_qmv_cfg1(reps: int = 64, nsets: int = 8) -> dict:
             "frac": round(gbs / HBM_PEAK_GBS, 4), "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": byts}
 
 
-def mfma_qmv(M: int, reps: int = 64, nsets: int = 8) -> dict:
-    """The M >= 16 path (cfg4's ragged batches reach 64 rows, run as 32-row
-    launches): x [M,5120] . W [17408,5120] 4-bit g64, packed layout 1 with
-    R = M/2 accumulator rows, 8 rotating weight sets. All of x does not fit in
-    one workgroup's LDS at these M, so the kernel splits K (each workgroup
-    stages one part of x for a group of tiles; parts meet in the workspace).
-    Reported against the dense bf16 MFMA peak (2.5 PFLOP/s) and against HBM."""
+def qmm_rows(M: int, reps: int = 64, nsets: int = 8) -> dict:
+    """The M >= 16 path (cfg4's ragged batches reach 64 rows):
+    mtp_qmm_affine4_mfma, x [M,5120] . W [17408,5120] 4-bit g64 (packed
+    layout 1), each weight quad read once for all M rows on the 32x32x16
+    MFMA, x streamed through LDS; 8 rotating weight sets (400 MB > the
+    256 MB MALL). Launches replayed from a HIP graph (host set-up untimed).
+    Reported against the dense bf16 MFMA peak (2.5 PFLOP/s) and HBM."""
     import torch
 
     from mtplx_amd import _lib
@@ -223,47 +223,284 @@ def mfma_qmv(M: int, reps: int = 64, nsets: int = 8) -> dict:
         q.pack()
     x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-    ws = _lib.WORKSPACES.get(_lib.query("mtp_qmv_workspace_bytes", M, N, K, 0), "bench_mfma")
-    st = _lib.stream_handle()
+    ws = _lib.WORKSPACES.get(max(256, _lib.query("mtp_qmm_workspace_bytes", M, N, K, 0)), "bench_qmm")
+    gs_stream = torch.cuda.Stream()
 
     def launch(q):
-        _lib.qmv_ex(st, x=x, w0=q.packed, y0=y, M=M, N=N, K=K, group_size=gs, xmode=0, emode=0, packed=1, ws=ws,
-                    ws_bytes=ws.numel())
+        _lib.qmm_mfma(_lib.stream_handle(), x=x, w0=q.packed, y=y, M=M, N=N, K=K, group_size=gs, emode=0, ws=ws,
+                      ws_bytes=ws.numel())
 
-    for q in sets:
-        launch(q)
-    torch.cuda.synchronize()
-    # Graph replays: the launches' host-side set-up is not timed.
-    gs_stream = torch.cuda.Stream()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(gs_stream):
-        st = _lib.stream_handle()
         for q in sets:
             launch(q)
         gs_stream.synchronize()
         with torch.cuda.graph(graph, stream=gs_stream):
             for q in sets:
                 launch(q)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    rounds = max(1, reps // nsets)
-    with torch.cuda.stream(gs_stream):   # replay() and the events on one stream
-        graph.replay()
-        gs_stream.synchronize()
-        e0.record()
-        for _ in range(rounds):
-            graph.replay()
-        e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / (rounds * nsets)
+    us = _replay_us(graph, gs_stream, max(1, reps // nsets)) / nsets
     flops = 2.0 * M * N * K
     tfs = flops / us / 1e6
     byts = _qmv_bytes(M, N, K, gs)
-    return {"kernel": f"qmv_stream_kernel<NW=4,R={4 if M <= 8 else (8 if M <= 16 else 16)},X_PLAIN,E_STORE,packed> "
-                      "(mtp_qmv_affine4_ex, full K split)",
+    return {"kernel": f"qmm_rows_kernel<R2={1 if M <= 32 else 2},store> (mtp_qmm_affine4_mfma)",
             "rows": M, "avg_launch_us": round(us, 3), "achieved_tflops": round(tfs, 1),
             "frac_mfma_bf16": round(tfs / MFMA_BF16_PEAK_TFLOPS, 4), "achieved_gbs": round(byts / us / 1e3, 1),
             "frac_hbm": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def _replay_us(graph, stream, rounds: int) -> float:
+    """Average microseconds per replay of ``graph`` on ``stream`` (HIP events
+    recorded on that stream, one untimed replay first)."""
+    import torch
+
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        graph.replay()
+        stream.synchronize()
+        e0.record(stream)
+        for _ in range(rounds):
+            graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / rounds
+
+
+def _matrix_bytes(*qs) -> int:
+    return sum(t.numel() * t.element_size() for q in qs if q is not None for t in (q.weight, q.scales, q.biases))
+
+
+def _randn_bf16(n: int, gen, dev):
+    """n N(0,1) bf16 values, generated in slices (bounded fp32 temporaries)."""
+    import torch
+
+    out = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    step = 1 << 26
+    for i in range(0, n, step):
+        m = min(step, n - i)
+        out[i:i + m] = torch.randn(m, generator=gen, device=dev).to(torch.bfloat16)
+    return out
+
+
+def cfg4_ragged(model, steps: int = 5, warmup: int = 2, seed: int = 11) -> dict:
+    """BASELINE cfg4 on the same 27B-shaped weights: 16 requests, depths
+    U{1,2,3}, contexts log-uniform in [1k, 64k] (seeded), packed into one
+    ragged batch of M = sum(K_b + 1) rows; per-request capacities in one
+    block cache (each request's verify rows are its context's last rows).
+    One step = embedding -> 64 layers (RMSNorm, q|k|v on the rows kernel,
+    ragged RoPE + K/V write, block attention, o + residual, RMSNorm, gate/up
+    + SwiGLU, down + residual) -> norm + lm_head -> accept/reject with
+    per-request depths; launched eagerly. Algorithmic bytes per step: every
+    layer matrix and the lm_head once, each request's K/V (ctx_b keys x
+    Hkv x 128 x 2 x 2 B per layer) once, plus the M new K/V rows written."""
+    import numpy as np
+    import torch
+
+    from mtplx_amd.sampling import SamplerConfig
+
+    c = model.cfg
+    dev = model.device
+    rng = np.random.default_rng(seed)
+    B = 16
+    depths = rng.integers(1, 4, size=B)
+    ctx = np.exp(rng.uniform(np.log(1024), np.log(65536), size=B)).astype(np.int64)
+    lens = depths + 1
+    q_start = (ctx - lens).astype(np.int32)
+    row_off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    d_off = np.concatenate([[0], np.cumsum(depths)]).astype(np.int32)
+    draft_index = np.concatenate([np.arange(row_off[b] + 1, row_off[b + 1]) for b in range(B)]).astype(np.int64)
+    M, Lmax = int(row_off[-1]), int(lens.max())
+    model.allocate_cache_blocks(ctx)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+
+    def t(a, dtype=torch.int32):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(device=dev, dtype=dtype)
+
+    tokens = torch.randint(0, c.vocab, (M,), device=dev, dtype=torch.int32, generator=gen)
+    draft_logits = 3.0 * torch.randn((int(d_off[-1]), c.vocab), device=dev, generator=gen)
+    uniforms = torch.rand((B, 4), device=dev, dtype=torch.float64, generator=gen)
+    args = (tokens, t(row_off), t(q_start), t(lens), Lmax, draft_logits, t(d_off), t(draft_index, torch.int64),
+            uniforms, SamplerConfig(0.6, 0.95, 20))
+    for _ in range(warmup):
+        res = model.verify_step_ragged(*args)
+    torch.cuda.synchronize()
+    model.check_status()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        res = model.verify_step_ragged(*args)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    assert int(res.status.max().item()) == 0
+    kv_row = c.n_kv_heads * c.head_dim * 2 * 2
+    w_bytes = sum(_matrix_bytes(L.qkv, L.o, L.gate, L.up, L.down) for L in model.layers) + \
+        _matrix_bytes(model.lm_head)
+    kv_bytes = c.layers * (int(ctx.sum()) + M) * kv_row
+    mm_flops = 2.0 * M * sum(c.qkv_out * c.hidden + c.hidden * c.n_heads * c.head_dim + 3 * c.ffn * c.hidden
+                             for _ in range(c.layers)) + 2.0 * M * c.vocab * c.hidden
+    keys = sum(int(q_start[b]) * int(lens[b]) + int(lens[b]) * (int(lens[b]) + 1) // 2 for b in range(B))
+    at_flops = c.layers * 4.0 * c.n_heads * c.head_dim * keys
+    s = ms / 1e3
+    total = w_bytes + kv_bytes
+    return {"workload": "cfg4: 16 requests, depths U{1,2,3}, contexts log-uniform [1k, 64k] (seed %d), one ragged "
+                        "batch, 27B-shaped 4-bit dense decoder, eager launches" % seed,
+            "rows": M, "depths": depths.tolist(), "contexts": ctx.tolist(), "ms_per_step": round(ms, 4),
+            "verify_rows_per_s": round(M / s, 2), "weight_bytes": w_bytes, "kv_bytes": kv_bytes,
+            "achieved_gbs": round(total / s / 1e9, 1), "frac_hbm": round(total / s / 1e9 / HBM_PEAK_GBS, 4),
+            "achieved_tflops": round((mm_flops + at_flops) / s / 1e12, 2),
+            "frac_mfma_bf16": round((mm_flops + at_flops) / s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 5)}
+
+
+def cfg2_attention(nsets: int = 8, reps: int = 4, seed: int = 21) -> dict:
+    """BASELINE cfg2: 8 requests, KV lengths U[512, 32768] (seeded), 4 verify
+    rows each (the context's last 4 keys), 40/8 heads, head_dim 128, bf16.
+    Two kernels: the verify step's block attention (per-request capacities,
+    operand-major 32-key blocks) and the facade's split kernel over the
+    reference's contiguous [B, Hkv, cap, 128] cache. 8 rotating K/V sets
+    (> the 256 MB MALL) so every launch streams from HBM; achieved GB/s =
+    sum_b L_b x 4096 B (K and V of 8 heads x 128 x bf16) per launch."""
+    import numpy as np
+    import torch
+
+    from mtplx_amd import _lib
+
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(seed)
+    B, Hq, Hkv, D, L = 8, 40, 8, 128, 4
+    kv_len = rng.integers(512, 32769, size=B)
+    caps = ((kv_len + 31) // 32) * 32
+    q_start = (kv_len - L).astype(np.int32)
+    lens = np.full(B, L, np.int32)
+    row_off = (np.arange(B + 1) * L).astype(np.int32)
+    kv_off = np.concatenate([[0], np.cumsum(Hkv * (caps // 32))]).astype(np.int32)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+
+    def t(a):
+        return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(dev)
+
+    d_qs, d_lens, d_row, d_kv = t(q_start), t(lens), t(row_off), t(kv_off)
+    q = torch.randn((B, Hq, L, D), device=dev, generator=gen).to(torch.bfloat16)
+    algo = int(kv_len.sum()) * Hkv * D * 2 * 2
+    scale = 1.0 / np.sqrt(D)
+    out = {"workload": f"cfg2: 8 requests, KV lengths {kv_len.tolist()} (seed {seed}), 4 rows each, 40/8 heads",
+           "kv_bytes_per_launch": algo}
+
+    def timed(launch, n):
+        launch(0)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(n):
+            launch(i % nsets)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / n
+
+    # the verify step's block attention
+    nblk = int(kv_off[-1])
+    kb = [_randn_bf16(nblk * 4096, gen, dev) for _ in range(nsets)]
+    vb = [_randn_bf16(nblk * 4096, gen, dev) for _ in range(nsets)]
+    o = torch.empty((B * L, Hq * D), dtype=torch.bfloat16, device=dev)
+    nb = _lib.query("mtp_attn_blocks_workspace_bytes", B, Hkv, int(caps.max()), int(caps.sum()), 0)
+    ws = _lib.WORKSPACES.get(nb, "bench_attn_blocks", dev)
+    st = _lib.stream_handle(dev)
+
+    def blocks(i):
+        _lib.attn_blocks(st, q=q, k_blk=kb[i], v_blk=vb[i], q_start=d_qs, q_lens=d_lens, row_off=d_row, kv_off=d_kv,
+                         out=o, B=B, Hq=Hq, Hkv=Hkv, Lmax=L, D=D, cap=int(caps.max()), split_keys=0, scale=scale,
+                         total_cap=int(caps.sum()), ws=ws, ws_bytes=ws.numel())
+
+    us = timed(blocks, reps * nsets)
+    out["blocks"] = {"kernel": "attn_vl_kernel + attn_merge_kernel (mtp_ragged_gqa_attn_blocks)",
+                     "avg_launch_us": round(us, 3), "achieved_gbs": round(algo / us / 1e3, 1),
+                     "frac_hbm": round(algo / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del kb, vb
+    # the facade kernel over the reference's contiguous layout
+    cap = int(caps.max())
+    kc = [_randn_bf16(B * Hkv * cap * D, gen, dev).view(B, Hkv, cap, D) for _ in range(nsets)]
+    vc = [_randn_bf16(B * Hkv * cap * D, gen, dev).view(B, Hkv, cap, D) for _ in range(nsets)]
+    o2 = torch.empty((B, Hq, L, D), dtype=torch.bfloat16, device=dev)
+    nb = _lib.query("mtp_attn_workspace_bytes", B, Hkv, cap, 0)
+    ws2 = _lib.WORKSPACES.get(nb, "bench_attn", dev)
+
+    def split(i):
+        _lib.call("mtp_ragged_gqa_attn", q.data_ptr(), kc[i].data_ptr(), vc[i].data_ptr(), d_qs.data_ptr(),
+                  d_lens.data_ptr(), o2.data_ptr(), B, Hq, Hkv, L, D, cap, scale, 0, ws2.data_ptr(), ws2.numel(), st)
+
+    us = timed(split, reps * nsets)
+    out["contiguous"] = {"kernel": "attn_split_kernel + attn_merge_kernel (mtp_ragged_gqa_attn, ragged_sdpa)",
+                         "avg_launch_us": round(us, 3), "achieved_gbs": round(algo / us / 1e3, 1),
+                         "frac_hbm": round(algo / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del kc, vc
+    torch.cuda.empty_cache()
+    return out
+
+
+def cfg5_moe(steps: int = 5, warmup: int = 2, seed: int = 5) -> dict:
+    """BASELINE cfg5: the 125B-class MoE decoder (48 layers, hidden 4096,
+    256 experts top-8 + 1 gated shared expert, expert FFN 1536, 32/4 heads,
+    vocab 151936), random init, router skew Zipf(1.1), 4 requests x depth 3
+    (16 rows) at 8k context, experts sorted before the gathered matmuls.
+    Algorithmic bytes per step from the seeded routing: the distinct
+    (layer, expert) pairs the step routes to x one expert's gate/up + down
+    bytes, plus every dense matrix (q|k|v, o, router, shared expert) and the
+    lm_head once, plus the K/V read (8k keys x 4 heads x 128 x 2 x 2 B per
+    request and layer)."""
+    import torch
+
+    from mtplx_amd.sampling import SamplerConfig
+    from mtplx_amd.verify_step import MOE_125B, VerifyModel
+
+    dev = torch.device("cuda", 0)
+    c = MOE_125B
+    B, K, ctx = 4, 3, 8192
+    L = K + 1
+    model = VerifyModel(c, device=dev, seed=seed)
+    model.allocate_cache(B, ctx)
+    gen = torch.Generator(device=dev).manual_seed(seed + 1)
+    tokens = torch.randint(0, c.vocab, (B, L), device=dev, dtype=torch.int32, generator=gen)
+    q_start = torch.full((B,), ctx - L, dtype=torch.int32, device=dev)
+    draft_logits = (torch.randn((B, K, c.vocab), device=dev, generator=gen) * 3.0).contiguous()
+    uniforms = torch.rand((B, L), device=dev, dtype=torch.float64, generator=gen)
+    sampler = SamplerConfig(0.6, 0.95, 20)
+    model.route_log = []
+    res = model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)
+    torch.cuda.synchronize()
+    model.check_status()
+    distinct = [int(torch.unique(ids).numel()) for ids in model.route_log]
+    model.route_log = None
+    for _ in range(warmup):
+        res = model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        res = model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    assert int(res.status.max().item()) == 0
+    L0 = model.layers[0]
+    expert_bytes = (_matrix_bytes(L0.expert_gate_up) + _matrix_bytes(L0.expert_down)) // c.n_experts
+    dense = sum(_matrix_bytes(x.qkv, x.o, x.router, x.shared_gate, x.shared_up, x.shared_down)
+                for x in model.layers) + _matrix_bytes(model.lm_head)
+    kv = c.layers * B * ctx * c.n_kv_heads * c.head_dim * 2 * 2
+    total = sum(distinct) * expert_bytes + dense + kv
+    s = ms / 1e3
+    del model
+    torch.cuda.empty_cache()
+    return {"workload": "cfg5: 125B-class MoE decoder, 4 requests x depth 3 (16 rows), 8k context, Zipf(1.1) "
+                        "router skew, eager launches",
+            "rows": B * L, "ms_per_step": round(ms, 4), "verify_rows_per_s": round(B * L / s, 2),
+            "distinct_experts_per_layer_mean": round(sum(distinct) / len(distinct), 2),
+            "expert_bytes": expert_bytes, "bytes_per_step": total, "achieved_gbs": round(total / s / 1e9, 1),
+            "frac_hbm": round(total / s / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def cpu_baseline(layers: int, timeout_s: int = 300) -> dict | None:
@@ -336,6 +573,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--parts", default="",
+                    help="comma list of the extra measurements to run (cfg1,qmm,cfg4,cfg2,cfg5; default all)")
     ap.add_argument("--eager", action="store_true", help="launch kernel by kernel instead of one HIP graph per step")
     ap.add_argument("--profile-roofline", action="store_true",
                     help="only launch the roofline kernel (2 passes over the layers, eager) and a 256 MiB copy, "
@@ -401,11 +640,26 @@ def main() -> int:
     value = B * L / (ms / 1e3)
 
     roof = roofline_gate_up(model, B * L)
-    roof["cfg1_qmv"] = roofline_qmv_cfg1()
-    roof["m16_qmv"] = mfma_qmv(16)
-    roof["m32_qmv"] = mfma_qmv(32)
+    parts = set(args.parts.split(",")) if args.parts else {"cfg1", "qmm", "cfg4", "cfg2", "cfg5"}
+    if "cfg1" in parts:
+        roof["cfg1_qmv"] = roofline_qmv_cfg1()
+    if "qmm" in parts:
+        for m in (16, 32, 64):
+            roof[f"m{m}_qmm"] = qmm_rows(m)
+    others = {}
+    if not args.eager:
+        del cap
+    if "cfg4" in parts:
+        others["cfg4"] = cfg4_ragged(model)
+        print(f"cfg4 done: {others['cfg4']['ms_per_step']} ms/step", file=sys.stderr, flush=True)
     del model
     torch.cuda.empty_cache()
+    if "cfg2" in parts:
+        others["cfg2_attention"] = cfg2_attention()
+        print("cfg2 done", file=sys.stderr, flush=True)
+    if "cfg5" in parts:
+        others["cfg5"] = cfg5_moe()
+        print(f"cfg5 done: {others['cfg5']['ms_per_step']} ms/step", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu_baseline else cpu_baseline(cfg.layers)
 
     line = {
@@ -429,6 +683,7 @@ def main() -> int:
                    "launch": "eager" if args.eager else "hip_graph"},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "other_configs": others,
     }
     print(json.dumps(line), flush=True)
     return 0

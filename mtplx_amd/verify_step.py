@@ -57,6 +57,15 @@ class DecoderConfig:
     expert_ffn: int = 0
     shared_ffn: int = 0
     router_zipf_s: float = 1.1
+    # Weight recipe. False: every linear as the single-linear benchmark
+    # (nibbles U{0..15}, scales |N(0,0.02)|, biases N(0,0.01)). Its groups
+    # have mean 7.5 x scale, so each output column carries an offset common
+    # to all tokens; layer after layer the hidden rows become nearly the same
+    # vector and every token routes to the same top-k experts. True: centered
+    # groups (bias -7.5 x scale) with unit gain (scale std 1/sqrt(21.25 K),
+    # so an rms-1 input gives rms-1 outputs): hidden rows stay token-specific
+    # and routing follows the Zipf skew plus per-token spread.
+    centered_init: bool = False
 
     @property
     def qkv_out(self) -> int:
@@ -65,7 +74,7 @@ class DecoderConfig:
 
 DENSE_27B = DecoderConfig()
 MOE_125B = DecoderConfig(layers=48, hidden=4096, ffn=0, n_heads=32, n_kv_heads=4, n_experts=256, top_k=8,
-                         expert_ffn=1536, shared_ffn=1536)
+                         expert_ffn=1536, shared_ffn=1536, centered_init=True)
 
 
 def _norm_weight(n: int, gen, device) -> torch.Tensor:
@@ -136,35 +145,42 @@ class VerifyModel:
         self.gen = gen
         c = cfg
         gs = c.group_size
-        self.embed = QuantizedLinear.random(c.vocab, c.hidden, gs, generator=gen, device=device)
+
+        def lin(n, k, experts=None, gain=1.0):
+            if c.centered_init:
+                return QuantizedLinear.random(n, k, gs, generator=gen, device=device, experts=experts,
+                                              scale_std=gain / math.sqrt(21.25 * k), centered=True)
+            return QuantizedLinear.random(n, k, gs, generator=gen, device=device, experts=experts)
+
+        # embedding rows: rms ~1 under the centered recipe (gain sqrt(K))
+        self.embed = lin(c.vocab, c.hidden, gain=math.sqrt(c.hidden))
         self.layers: list[Layer] = []
         for _ in range(c.layers):
-            L = Layer(in_norm=_norm_weight(c.hidden, gen, device),
-                      qkv=QuantizedLinear.random(c.qkv_out, c.hidden, gs, generator=gen, device=device),
-                      o=QuantizedLinear.random(c.hidden, c.n_heads * c.head_dim, gs, generator=gen, device=device),
-                      post_norm=_norm_weight(c.hidden, gen, device))
+            L = Layer(in_norm=_norm_weight(c.hidden, gen, device), qkv=lin(c.qkv_out, c.hidden),
+                      o=lin(c.hidden, c.n_heads * c.head_dim), post_norm=_norm_weight(c.hidden, gen, device))
             if c.n_experts:
-                # Small router weights (logits ~ +-1) so the Zipf skew sets the
-                # experts' popularity; rank r (a per-layer permutation) gets
-                # -s * log(r).
+                # Zipf-skewed routing: rank r (a per-layer permutation) gets
+                # -s * log(r) added to the router logits; the router weights
+                # are zero-mean (centered groups) with a scale that gives the
+                # logits a per-token spread near the standard Gumbel's (std
+                # 1.28), the noise under which top-k of (skew + noise) draws
+                # experts with Zipf(s) popularity.
                 L.router = QuantizedLinear.random(c.n_experts + 1, c.hidden, gs, generator=gen, device=device,
-                                                  scale_std=0.002, bias_std=0.001)
+                                                  scale_std=0.0065, centered=True)
                 rank = torch.randperm(c.n_experts, generator=gen, device=device).to(torch.float32) + 1.0
                 L.router_skew = (-c.router_zipf_s * torch.log(rank)).contiguous()
-                L.expert_gate_up = QuantizedLinear.random(2 * c.expert_ffn, c.hidden, gs, generator=gen,
-                                                          device=device, experts=c.n_experts)
-                L.expert_down = QuantizedLinear.random(c.hidden, c.expert_ffn, gs, generator=gen, device=device,
-                                                       experts=c.n_experts)
-                L.shared_gate = QuantizedLinear.random(c.shared_ffn, c.hidden, gs, generator=gen, device=device)
-                L.shared_up = QuantizedLinear.random(c.shared_ffn, c.hidden, gs, generator=gen, device=device)
-                L.shared_down = QuantizedLinear.random(c.hidden, c.shared_ffn, gs, generator=gen, device=device)
+                L.expert_gate_up = lin(2 * c.expert_ffn, c.hidden, experts=c.n_experts)
+                L.expert_down = lin(c.hidden, c.expert_ffn, experts=c.n_experts)
+                L.shared_gate = lin(c.shared_ffn, c.hidden)
+                L.shared_up = lin(c.shared_ffn, c.hidden)
+                L.shared_down = lin(c.hidden, c.shared_ffn)
             else:
-                L.gate = QuantizedLinear.random(c.ffn, c.hidden, gs, generator=gen, device=device)
-                L.up = QuantizedLinear.random(c.ffn, c.hidden, gs, generator=gen, device=device)
-                L.down = QuantizedLinear.random(c.hidden, c.ffn, gs, generator=gen, device=device)
+                L.gate = lin(c.ffn, c.hidden)
+                L.up = lin(c.ffn, c.hidden)
+                L.down = lin(c.hidden, c.ffn)
             self.layers.append(L)
         self.final_norm = _norm_weight(c.hidden, gen, device)
-        self.lm_head = QuantizedLinear.random(c.vocab, c.hidden, gs, generator=gen, device=device)
+        self.lm_head = lin(c.vocab, c.hidden)
         # Tile-major copies for the streaming verify matmul (one pass at load
         # time), in layout 1 (any M) and layout 2 (M <= 4, 16x16x32 MFMA);
         # q|k|v also in RoPE tile order for the fused RoPE epilogue.
@@ -182,6 +198,9 @@ class VerifyModel:
         self.v_cache: list[torch.Tensor] = []
         self.cap = 0
         self._status: torch.Tensor | None = None
+        # A list here receives each MoE layer's routed expert ids (int32
+        # [M, top_k], on the device) as the forward runs; None records nothing.
+        self.route_log: list | None = None
 
     # -- cache ----------------------------------------------------------------
     def allocate_cache(self, batch: int, capacity: int, *, fill_random: bool = True) -> None:
@@ -377,6 +396,8 @@ class VerifyModel:
         wts = torch.empty((M, c.top_k), dtype=torch.float32, device=dev)
         call("mtp_moe_route", rl.data_ptr(), E + 1, L.router_skew.data_ptr(), M, E, c.top_k, ids.data_ptr(),
              wts.data_ptr(), st)
+        if self.route_log is not None:
+            self.route_log.append(ids)
         es = expert_sort(ids, E)
         R = M * c.top_k
         F = c.expert_ffn
