@@ -47,6 +47,26 @@ size_t mtp_qmv_workspace_bytes(int M, int N, int K, int dual);
 int mtp_qmv_affine4(const void* x, const void* w, const void* scales, const void* biases, void* y, int M, int N,
                     int K, int group_size, void* ws, size_t ws_bytes, void* stream);
 
+/* General affine quantized matmul for the formats the MFMA kernel does not
+ * take: bits 4 or 8, group_size 32, 64 or 128, any M >= 1 (launches of 8
+ * rows), K a multiple of 32 and of group_size, w 16-byte aligned. Weights
+ * uint32 [N, K*bits/32] (little-endian bit fields), scales/biases bf16
+ * [N, K/gs]; x bf16 [M, K]; output bf16 y or (y NULL) fp32 yf holding bf16
+ * values, [M, N]. fp32 accumulation, VALU (not the HBM-rate lane).
+ * Replaces: mtplx/verify_qmv.py:1377 stocklike_qmv8_matmul (8-bit verify
+ * rows, eligibility :1256), the group-32 routes of
+ * mtplx/kernels/qmv4_matmul.py:185 qmv4_matmul and
+ * mtplx/verify_crossrow.py:249 crossrow_qmm, and the mx.quantized_matmul
+ * fallback those lanes take on other shapes. */
+int mtp_qmv_affine(const void* x, const void* w, const void* scales, const void* biases, void* y, void* yf, int M,
+                   int N, int K, int group_size, int bits, void* stream);
+
+/* Activation chunk sums of the cross-row lane (mtplx/verify_crossrow.py:111
+ * make_chunk_sums): out[(kb*32 + lane)*8 + m] = sum over i < 16 of
+ * x[m, kb*512 + lane*16 + i] (fp32, index order), rows m >= M zero;
+ * 1 <= M <= 8, K a multiple of 512; out holds K/512*32*8 floats. */
+int mtp_chunk_sums(const void* x, int M, int K, float* out, void* stream);
+
 /* y = bf16(bf16(x @ W^T) + resid) — the residual add that follows o_proj and
  * down_proj in the verify forward (mlx-lm decoder layer `h + r`).
  * resid may alias y. ss_out (NULL = skip) receives, for each 32-column block

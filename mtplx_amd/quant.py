@@ -86,22 +86,25 @@ class QuantizedLinear:
     @classmethod
     def random(cls, out_features: int, in_features: int, group_size: int = 64, *, generator=None,
                device="cuda", scale_std: float = 0.02, bias_std: float = 0.01, experts: int | None = None,
-               centered: bool = False):
+               centered: bool = False, bits: int = 4):
         """Synthetic layer (random init): nibbles U{0..15}, scales |N(0,scale_std)|,
         biases N(0,bias_std), bf16 — the BASELINE weight recipe. ``experts``
         adds a leading expert axis (MoE switch layers). ``centered`` sets each
         group's bias to -7.5 x its scale instead, so the weights have zero
-        mean (no per-row offset in the outputs)."""
+        mean (no per-row offset in the outputs). ``bits`` 4 or 8 (uniform
+        fields, 32/bits per word)."""
+        if bits not in (4, 8):
+            raise ValueError("bits must be 4 or 8")
         lead = () if experts is None else (experts,)
-        w = torch.randint(-2 ** 31, 2 ** 31 - 1, lead + (out_features, in_features // 8), dtype=torch.int32,
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, lead + (out_features, in_features * bits // 32), dtype=torch.int32,
                           device=device, generator=generator)
         g = in_features // group_size
         s = (torch.randn(lead + (out_features, g), device=device, generator=generator) * scale_std).abs()
         b = torch.randn(lead + (out_features, g), device=device, generator=generator) * bias_std
         s = s.to(torch.bfloat16)
         if centered:
-            b = -7.5 * s.float()
-        return cls(w, s, b.to(torch.bfloat16), group_size=group_size)
+            b = -0.5 * ((1 << bits) - 1) * s.float()
+        return cls(w, s, b.to(torch.bfloat16), group_size=group_size, bits=bits)
 
 
 def rope_row_order(n_heads: int, head_dim: int) -> torch.Tensor:

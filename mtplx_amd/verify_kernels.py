@@ -5,9 +5,12 @@ Replaces the reference's verify qmm family (``mtplx/verify_kernels.py``:
 is what a :class:`~mtplx_amd.quant.QuantizedLinear` call runs
 (the ``mx.quantized_matmul(x, w, s, b, transpose=True)`` contract).
 
-Kernel: ``mtp_qmv_affine4`` — MFMA 32x32x16 bf16 with exact nibble operands,
-fp32 accumulation, one workgroup per 32 output columns (see ``csrc/qmv.hip``).
-Rows beyond 32 are processed in 32-row launches. There is no CPU path.
+Kernels: ``mtp_qmv_affine4`` for 4-bit groups of 64/128 with K % 256 == 0 —
+MFMA 32x32x16 bf16 with exact nibble operands, fp32 accumulation, one
+workgroup per 32 output columns (``csrc/qmv.hip``; rows beyond 32 in 32-row
+launches) — and ``mtp_qmv_affine`` for the other MLX affine packs (4- or
+8-bit, groups 32/64/128, K % 32 == 0; ``csrc/qmv_generic.hip``). There is no
+CPU path.
 """
 
 from __future__ import annotations
@@ -21,21 +24,26 @@ MAX_ROWS = 32
 
 def _check(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int,
            bits: int, mode: str) -> tuple[int, int]:
-    if mode != "affine" or bits != 4:
-        raise NotImplementedError(f"only 4-bit affine is on the gfx950 path (got {bits}-bit {mode})")
-    if group_size not in (64, 128):
-        raise NotImplementedError(f"group_size {group_size} not on the gfx950 path (64, 128)")
+    if mode != "affine" or bits not in (4, 8):
+        raise NotImplementedError(f"only 4- and 8-bit affine are on the gfx950 path (got {bits}-bit {mode})")
+    if group_size not in (32, 64, 128):
+        raise NotImplementedError(f"group_size {group_size} not on the gfx950 path (32, 64, 128)")
     if not x.is_cuda:
         raise RuntimeError("verify matmul needs a GPU tensor; there is no CPU path")
     if x.dtype != torch.bfloat16 or scales.dtype != torch.bfloat16 or biases.dtype != torch.bfloat16:
         raise TypeError("x, scales and biases must be bfloat16")
     n, kw = int(w.shape[-2]), int(w.shape[-1])
-    k = kw * 8
+    k = kw * 32 // bits
     if int(x.shape[-1]) != k:
         raise ValueError(f"x has K={int(x.shape[-1])}, weight packs K={k}")
-    if k % 256:
-        raise NotImplementedError(f"K={k} must be a multiple of 256 on the gfx950 path")
+    if k % 32 or k % group_size:
+        raise NotImplementedError(f"K={k} must be a multiple of 32 and of the group size on the gfx950 path")
     return n, k
+
+
+def fast_path(bits: int, group_size: int, k: int) -> bool:
+    """Whether the MFMA streaming kernel takes this pack (else the general one)."""
+    return int(bits) == 4 and int(group_size) in (64, 128) and int(k) % 256 == 0
 
 
 def vk_eligible_ksplit(m: int, K: int, N: int, bits: int, group_size: int, dtype) -> bool:
@@ -54,6 +62,10 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
     m = x2.shape[0]
     y = out if out is not None else torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
     st = _lib.stream_handle(x.device)
+    if not fast_path(bits, group_size, k):
+        _lib.call("mtp_qmv_affine", x2.data_ptr(), w.data_ptr(), scales.data_ptr(), biases.data_ptr(), y.data_ptr(),
+                  None, m, n, k, group_size, bits, st)
+        return y.reshape(*lead, n)
     for r0 in range(0, m, MAX_ROWS):
         r = min(MAX_ROWS, m - r0)
         _lib.call("mtp_qmv_affine4", x2[r0:].data_ptr(), w.data_ptr(), scales.data_ptr(), biases.data_ptr(),

@@ -133,11 +133,41 @@ def multi3_swiglu_down_qmv4_matmul(gate: torch.Tensor, up: torch.Tensor, module:
 
 
 def is_stocklike_qmv8_eligible(module: Any) -> bool:
-    """``mtplx/verify_qmv.py:1256``. 8-bit weights are outside this build's
-    4-bit verify path, so nothing is eligible."""
-    return False
+    """``mtplx/verify_qmv.py:1256``: an 8-bit affine QuantizedLinear with
+    biases, group 32/64/128, K % 256 == 0 and N % 8 == 0."""
+    if not isinstance(module, QuantizedLinear):
+        return False
+    if module.bits != 8 or module.group_size not in (32, 64, 128) or module.mode != "affine":
+        return False
+    if module.biases is None or module.weight.dim() != 2:
+        return False
+    k = int(module.weight.shape[1]) * 4
+    n = int(module.weight.shape[0])
+    return k % 256 == 0 and n % 8 == 0
 
 
 def stocklike_qmv8_matmul(x: torch.Tensor, module: Any) -> torch.Tensor:
-    """``mtplx/verify_qmv.py:1377``: ineligible -> ``module(x)`` as in the reference."""
-    return module(x)
+    """``mtplx/verify_qmv.py:1377``: 8-bit verify rows on ``mtp_qmv_affine``
+    (one batch of rows, bf16 x/scales/biases); anything else -> ``module(x)``
+    as in the reference."""
+    if not is_stocklike_qmv8_eligible(module):
+        return module(x)
+    if x.dim() < 2 or x.dtype != torch.bfloat16 or module.scales.dtype != x.dtype or \
+            module.biases.dtype != x.dtype:
+        return module(x)
+    k = int(x.shape[-1])
+    if k != int(module.weight.shape[1]) * 4:
+        return module(x)
+    lead = x.shape[:-2]
+    count = 1
+    for d in lead:
+        count *= int(d)
+    if count != 1:
+        return module(x)
+    m, n = int(x.shape[-2]), module.out_features
+    x2 = x.reshape(m, k).contiguous()
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    _lib.call("mtp_qmv_affine", x2.data_ptr(), module.weight.data_ptr(), module.scales.data_ptr(),
+              module.biases.data_ptr(), y.data_ptr(), None, m, n, k, module.group_size, 8,
+              _lib.stream_handle(x.device))
+    return _add_bias(y, module).reshape(*lead, m, n)

@@ -108,3 +108,69 @@ def make_affine4_weights(rng: np.random.Generator, n: int, k: int, group_size: i
     s = np.abs(rng.normal(0.0, scale_std, size=(n, k // group_size))).astype(np.float32)
     b = rng.normal(0.0, bias_std, size=(n, k // group_size)).astype(np.float32)
     return pack_affine4(q), f32_to_bf16_bits(s), f32_to_bf16_bits(b)
+
+
+# ---------------------------------------------------------------------------
+# Any power-of-two width (MLX affine quantization, mlx==0.32.2 as the
+# reference's pyproject.toml:36 pins; its verify lanes read 8-bit packs at
+# mtplx/verify_qmv.py:1256-1377 and group-32 packs at
+# mtplx/kernels/qmv4_matmul.py:158-176): a uint32 word holds 32/bits values,
+# value i in bits bits*i .. bits*i + bits - 1 (little-endian fields).
+
+def pack_affine(q: np.ndarray, bits: int) -> np.ndarray:
+    """uint ``[N, K]`` values in 0..2^bits-1 -> uint32 ``[N, K*bits/32]``."""
+    if bits not in (2, 4, 8):
+        raise ValueError("bits must be 2, 4 or 8")
+    vpw = 32 // bits
+    q = np.asarray(q)
+    if q.ndim != 2 or q.shape[1] % vpw:
+        raise ValueError(f"pack_affine expects [N, K] with K % {vpw} == 0")
+    if q.min(initial=0) < 0 or q.max(initial=0) > (1 << bits) - 1:
+        raise ValueError(f"values must lie in 0..{(1 << bits) - 1}")
+    q = q.astype(np.uint32).reshape(q.shape[0], -1, vpw)
+    shifts = (np.arange(vpw, dtype=np.uint32) * np.uint32(bits))[None, None, :]
+    return np.bitwise_or.reduce(q << shifts, axis=2).astype(np.uint32)
+
+
+def unpack_affine(w: np.ndarray, bits: int) -> np.ndarray:
+    """uint32 ``[N, K*bits/32]`` -> ``[N, K]`` values."""
+    vpw = 32 // bits
+    w = np.asarray(w, dtype=np.uint32)
+    shifts = (np.arange(vpw, dtype=np.uint32) * np.uint32(bits))[None, None, :]
+    q = (w[:, :, None] >> shifts) & np.uint32((1 << bits) - 1)
+    return q.reshape(w.shape[0], -1).astype(np.uint16 if bits > 8 else np.uint8)
+
+
+def qmm_affine(x: np.ndarray, w: np.ndarray, scales: np.ndarray, biases: np.ndarray, group_size: int,
+               bits: int) -> np.ndarray:
+    """``x @ dequant(W).T`` in float64 for ``bits``-wide affine weights."""
+    xf = _as_f64(x)
+    lead = xf.shape[:-1]
+    x2 = xf.reshape(-1, xf.shape[-1])
+    n = np.asarray(w).shape[0]
+    k = np.asarray(w).shape[1] * (32 // bits)
+    if x2.shape[1] != k:
+        raise ValueError(f"x has K={x2.shape[1]}, weight packs K={k}")
+    y = np.zeros((x2.shape[0], n), dtype=np.float64)
+    step = max(1, (1 << 22) // max(1, k))
+    for n0 in range(0, n, step):
+        sl = slice(n0, min(n, n0 + step))
+        q = unpack_affine(np.asarray(w)[sl], bits).astype(np.float64)
+        s = np.repeat(_as_f64(np.asarray(scales)[sl]), group_size, axis=1)
+        b = np.repeat(_as_f64(np.asarray(biases)[sl]), group_size, axis=1)
+        if s.shape != q.shape:
+            raise ValueError(f"scales {s.shape} do not match weights {q.shape} at group {group_size}")
+        y[:, sl] = x2 @ (q * s + b).T
+    return y.reshape(*lead, n)
+
+
+def make_affine_weights(rng: np.random.Generator, n: int, k: int, group_size: int, bits: int,
+                        scale_std: float = 0.02, bias_std: float = 0.01):
+    """Synthetic ``bits``-wide layer: values U{0..2^bits-1}, scales |N(0,
+    scale_std)|, biases N(0, bias_std), bf16. Returns ``(w, scales, biases)``."""
+    from .bf16 import f32_to_bf16_bits
+
+    q = rng.integers(0, 1 << bits, size=(n, k), dtype=np.uint16)
+    s = np.abs(rng.normal(0.0, scale_std, size=(n, k // group_size))).astype(np.float32)
+    b = rng.normal(0.0, bias_std, size=(n, k // group_size)).astype(np.float32)
+    return pack_affine(q, bits), f32_to_bf16_bits(s), f32_to_bf16_bits(b)
