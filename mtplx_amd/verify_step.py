@@ -93,6 +93,7 @@ class Layer:
     # MoE
     router: QuantizedLinear | None = None       # [E + 1, H]: E router rows, then the shared-expert gate row
     router_skew: torch.Tensor | None = None     # fp32 [E]: synthetic Zipf popularity added to the router logits
+                                                # (None: the logits as they are, as for loaded weights)
     expert_gate_up: QuantizedLinear | None = None   # [E, 2F, K/8] fused [gate | up]
     expert_down: QuantizedLinear | None = None      # [E, H, F/8]
     shared_gate: QuantizedLinear | None = None
@@ -181,6 +182,26 @@ class VerifyModel:
             self.layers.append(L)
         self.final_norm = _norm_weight(c.hidden, gen, device)
         self.lm_head = lin(c.vocab, c.hidden)
+        self._finish_init()
+
+    @classmethod
+    def from_weights(cls, cfg: DecoderConfig, embed: QuantizedLinear, layers: list[Layer], final_norm: torch.Tensor,
+                     lm_head: QuantizedLinear, *, device="cuda") -> "VerifyModel":
+        """A model over given weights (e.g. an MLX pack read by
+        :func:`mtplx_amd.mlx_pack.load_verify_model`) instead of random init."""
+        self = cls.__new__(cls)
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.gen = torch.Generator(device=self.device).manual_seed(0)
+        self.embed = embed
+        self.layers = layers
+        self.final_norm = final_norm
+        self.lm_head = lm_head
+        self._finish_init()
+        return self
+
+    def _finish_init(self) -> None:
+        c = self.cfg
         # Tile-major copies for the streaming verify matmul (one pass at load
         # time), in layout 1 (any M) and layout 2 (M <= 4, 16x16x32 MFMA);
         # q|k|v also in RoPE tile order for the fused RoPE epilogue.
@@ -394,7 +415,7 @@ class VerifyModel:
         qmv(st, x=xn, w0=Wr, yf=rl, M=M, N=E + 1, K=H, group_size=gs, xmode=0, emode=0, packed=lay)
         ids = torch.empty((M, c.top_k), dtype=torch.int32, device=dev)
         wts = torch.empty((M, c.top_k), dtype=torch.float32, device=dev)
-        call("mtp_moe_route", rl.data_ptr(), E + 1, L.router_skew.data_ptr(), M, E, c.top_k, ids.data_ptr(),
+        call("mtp_moe_route", rl.data_ptr(), E + 1, _lib.ptr(L.router_skew), M, E, c.top_k, ids.data_ptr(),
              wts.data_ptr(), st)
         if self.route_log is not None:
             self.route_log.append(ids)

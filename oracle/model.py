@@ -102,7 +102,10 @@ def verify_forward_ragged(params: dict, cfg, tokens: list, q_start, k_cache: lis
         if cfg.n_experts:
             E = cfg.n_experts
             rl = round_to_bf16(qmm_affine4(xn, *lay["router"], gs))          # [M, E + 1]
-            logits = (rl[:, :E].astype(np.float32) + np.asarray(lay["router_skew"], np.float32)[None, :])
+            skew = lay.get("router_skew")
+            logits = rl[:, :E].astype(np.float32)
+            if skew is not None:
+                logits = logits + np.asarray(skew, np.float32)[None, :]
             ids, wts = route_topk(logits.astype(np.float64), cfg.top_k)
             if routes is not None:
                 routes.append((ids, wts))

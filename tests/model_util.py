@@ -25,7 +25,7 @@ def model_params_numpy(model) -> dict:
         if L.gate is not None:
             d.update(gate=_ql(L.gate), up=_ql(L.up), down=_ql(L.down))
         else:
-            d.update(router=_ql(L.router), router_skew=L.router_skew.cpu().numpy().astype(np.float32),
+            d.update(router=_ql(L.router), router_skew=None if L.router_skew is None else L.router_skew.cpu().numpy().astype(np.float32),
                      expert_gate_up=_ql(L.expert_gate_up), expert_down=_ql(L.expert_down),
                      shared_gate=_ql(L.shared_gate), shared_up=_ql(L.shared_up), shared_down=_ql(L.shared_down))
         layers.append(d)
