@@ -161,6 +161,7 @@ typedef struct mtp_rope_out {
   int L, Hq, Hkv, D, cap, blocked;
   float rope_base;
 } mtp_rope_out;
+struct mtp_logits_topk;   /* emode 5's outputs, below */
 typedef struct mtp_qmv_args {
   const void* x;
   const void* x2;
@@ -188,8 +189,30 @@ typedef struct mtp_qmv_args {
    * the x_sums of a following xmode 3 call on y0. */
   const float* x_sums;
   float* y_sums;
+  const struct mtp_logits_topk* topk; /* emode 5 only */
 } mtp_qmv_args;
 int mtp_qmv_affine4_ex(const mtp_qmv_args* args, void* stream);
+
+/* emode 5 = the verify lm_head with the sampler's vocabulary reduction fused
+ * into its epilogue (mtplx/kernels/lm_head_topk.py:12-30 tile-local top-k,
+ * mtplx/kernels/logits_topk.py:1-12 logsumexp partials, fed to the accept
+ * step as mtplx/fast_sampling.py:407-451 feeds its candidates): yf receives
+ * the fp32 logits as emode 0 does, and parts the chunk partials of every
+ * row (the per-4096-id max and sum exp(l/T - max) in fp64, the non-finite
+ * flag and the top-k keys) exactly as mtp_spec_accept's first pass would
+ * compute them from those logits (keys and maxima bit-exact, sums in
+ * another fp64 order), so mtp_spec_accept_parts skips that pass for the
+ * target rows. Packed weights, 1 <= M <= 8, yf set; narrow laws only
+ * (temperature <= 0, or 1 <= top_k <= 64). Each workgroup covers 256
+ * consecutive ids; the last of a chunk's groups to arrive merges it. */
+typedef struct mtp_logits_topk {
+  void* parts;        /* chunk partials [M][ceil(N/4096)]: mtp_spec_accept_parts' workspace (its start) */
+  void* ws;           /* scratch of mtp_logits_topk_workspace_bytes(M, N), 256-byte aligned, zeroed once */
+  size_t ws_bytes;
+  double temperature; /* the sampler's (<= 0: greedy) */
+  int top_k;          /* the sampler's, 1..64 (ignored when greedy) */
+} mtp_logits_topk;
+size_t mtp_logits_topk_workspace_bytes(int M, int N);
 
 /* ---- 4-bit quantized matmul for 9..64 verify rows (MFMA) --------------------
  * The continuous-batched ragged verify (M = sum_b (K_b + 1) rows, up to 64):
@@ -387,6 +410,16 @@ int mtp_moe_combine(const void* y_sorted, const uint32_t* inv_order, const float
  * Workspace: mtp_sampler_workspace_bytes(B*(2K+1), V, top_k). */
 size_t mtp_sampler_workspace_bytes(int rows, int V, int top_k);
 int mtp_spec_accept(const float* target_logits, const float* draft_logits, const int32_t* draft_ids,
+                    const double* uniforms, int B, int K, int V, double temperature, int top_k, double top_p,
+                    int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
+                    size_t ws_bytes, void* stream);
+
+/* mtp_spec_accept with the target rows' chunk partials already in ws (from
+ * an emode-5 lm_head with the same temperature and top_k): only the draft
+ * rows are reduced here. Narrow laws only (MTP_ERR_UNSUPPORTED otherwise).
+ * No counterpart of its own in the reference: the fused path of
+ * mtplx/fast_sampling.py:407-451 that consumes lm_head top-k candidates. */
+int mtp_spec_accept_parts(const float* target_logits, const float* draft_logits, const int32_t* draft_ids,
                     const double* uniforms, int B, int K, int V, double temperature, int top_k, double top_p,
                     int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
                     size_t ws_bytes, void* stream);

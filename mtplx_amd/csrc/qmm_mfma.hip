@@ -355,7 +355,7 @@ using namespace mtp;
 MTP_API size_t mtp_qmm_workspace_bytes(int M, int N, int K, int dual) {
   if (M < 1 || M > 64 || N < 1 || K < 256 || K % 256) return 0;
   const RowsPlan pl = rows_plan(M, N, K, dual);
-  return rows_partial_bytes(pl, M) + (((size_t)pl.leftover * 4 + 255) & ~(size_t)255);
+  return pl.leftover ? kCounterBytes + rows_partial_bytes(pl, M) : 0;
 }
 
 MTP_API int mtp_qmm_affine4_mfma(const mtp_qmm_args* a, void* stream) {
@@ -412,8 +412,8 @@ MTP_API int mtp_qmm_affine4_mfma(const mtp_qmm_args* a, void* stream) {
                 a->ws_bytes);
       return MTP_ERR_WORKSPACE;
     }
-    p.partial = reinterpret_cast<float*>(a->ws);
-    p.counters = reinterpret_cast<uint32_t*>(reinterpret_cast<unsigned char*>(a->ws) + rows_partial_bytes(pl, M));
+    p.counters = reinterpret_cast<uint32_t*>(a->ws);   // the fixed counter area every shape shares
+    p.partial = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(a->ws) + kCounterBytes);
   }
   const int grid = pl.full + pl.leftover * pl.split;
   hipStream_t st = (hipStream_t)stream;

@@ -157,6 +157,20 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
                         const char* who, int schedule = 0) {
   const int rc = qmm_check(xm, em, p, who);
   if (rc != MTP_OK) return rc;
+  if (em == E_STORE_TOPK) {
+    Plan pl = make_plan(p.M, p.N, p.K);
+    if (!p.packed || p.M > 8 || !p.yf || !pl.resident || (xm != X_PLAIN && xm != X_RMSNORM) ||
+        (!p.topk_greedy && (p.topk_ksel < 1 || p.topk_ksel > kMaxTopK))) {
+      set_error("%s: emode 5 needs packed weights, M <= 8 with x in LDS, plain or RMSNorm x, fp32 logits (yf) and "
+                "a narrow law (temperature <= 0 or 1 <= top_k <= %d)", who, kMaxTopK);
+      return MTP_ERR_UNSUPPORTED;
+    }
+    p.chunk = pl.chunk;
+    p.n_blocks = pl.n_blocks;
+    pl.lds += (size_t)p.M * p.topk_tpw * 32 * sizeof(float);
+    qmv_launch_topk(xm, p, pl, st);
+    return launch_check(who);
+  }
   if (em == E_ROPE_QKV) {
     Plan pl = make_plan(p.M, p.N, p.K);
     if (!pl.resident) {
@@ -178,10 +192,11 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
       set_error("%s: workspace of %zu B (256-B aligned) needed, got %zu B", who, need, ws_bytes);
       return MTP_ERR_WORKSPACE;
     }
-    // Per-tile kernel with its leftover tiles split over all CUs.
+    // Per-tile kernel with its leftover tiles split over all CUs (counters:
+    // one per leftover tile, fewer than the CUs).
     p.tail_ok = 1;
-    p.partial = reinterpret_cast<float*>(ws);
-    p.counters = reinterpret_cast<uint32_t*>(reinterpret_cast<unsigned char*>(ws) + tail_counter_offset(device_cus()));
+    p.counters = reinterpret_cast<uint32_t*>(ws);
+    p.partial = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(ws) + kCounterBytes);
   }
   Plan pl = make_plan(p.M, p.N, p.K);
   if (p.packed && !pl.resident) {
@@ -190,18 +205,17 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
     // the parts meet through the workspace.
     const int S = full_split_parts(p.M, p.K, pl.nw);
     const size_t need = full_split_ws_bytes(p.M, p.N, p.K, pl.nw);
-    if (S < 2 || !ws || ws_bytes < need || ((uintptr_t)ws & 255)) {
+    if (S < 2 || !ws || ws_bytes < need || ((uintptr_t)ws & 255) || pl.n_blocks > kMaxCounters) {
       set_error("%s: packed weights with x too large for LDS (M=%d, K=%d) need a 256-B aligned workspace of %zu B "
-                "(mtp_qmv_workspace_bytes)", who, p.M, p.K, need);
+                "(mtp_qmv_workspace_bytes) and N <= %d", who, p.M, p.K, need, 32 * kMaxCounters);
       return ws ? MTP_ERR_WORKSPACE : MTP_ERR_UNSUPPORTED;
     }
     pl.split = S;
     pl.xq = cdiv(p.K >> 8, S);
     pl.lds = stream_lds(pl.xq, p.M, pl.nw);
     p.tail_ok = 1;
-    p.partial = reinterpret_cast<float*>(ws);
-    p.counters = reinterpret_cast<uint32_t*>(reinterpret_cast<unsigned char*>(ws) +
-                                             full_split_partial_bytes(p.M, p.N, p.K, pl.nw));
+    p.counters = reinterpret_cast<uint32_t*>(ws);   // one per tile
+    p.partial = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(ws) + kCounterBytes);
   }
   p.chunk = pl.chunk;
   launch_x(xm, em, p.gs == 64 ? 0 : 1, p, pl, st);
@@ -234,6 +248,11 @@ static QmmParams base_params(const void* x, const void* w, const void* s, const 
 using namespace mtp;
 
 MTP_API const char* mtp_last_error(void) { return g_err; }
+
+MTP_API size_t mtp_logits_topk_workspace_bytes(int M, int N) {
+  if (M < 1 || M > 8 || N < 1 || cdiv(N, kChunk) > kTopkMaxChunks) return 0;
+  return kTopkCounterBytes + topk_sub_bytes(M, N);
+}
 
 MTP_API size_t mtp_qmv_workspace_bytes(int M, int N, int K, int dual) {
   // Packed weights only: the tail split (fp32 partials of the tiles shared by
@@ -554,7 +573,8 @@ int qmv_args_params(const mtp_qmv_args* a, QmmParams* out, const char* who) {
     set_error("%s: null argument block", who);
     return MTP_ERR_ARG;
   }
-  if (a->xmode < 0 || a->xmode > 3 || a->emode < 0 || a->emode > 4 || (a->emode == E_ROPE_QKV && !a->rope)) {
+  if (a->xmode < 0 || a->xmode > 3 || a->emode < 0 || a->emode > 5 || (a->emode == E_ROPE_QKV && !a->rope) ||
+      (a->emode == E_STORE_TOPK && !a->topk)) {
     set_error("%s: xmode %d / emode %d out of range", who, a->xmode, a->emode);
     return MTP_ERR_ARG;
   }
@@ -590,6 +610,21 @@ int qmv_args_params(const mtp_qmv_args* a, QmmParams* out, const char* who) {
     p.rope_cap = r->cap;
     p.rope_blocked = r->blocked;
     p.rope_log2_base = r->rope_base > 1.f ? log2f(r->rope_base) : 0.f;
+  }
+  if (a->emode == E_STORE_TOPK) {
+    const mtp_logits_topk* t = a->topk;
+    p.topk_parts = t->parts;
+    p.topk_greedy = !(t->temperature > 0.0);
+    p.topk_temp = p.topk_greedy ? 1.0 : t->temperature;
+    p.topk_ksel = p.topk_greedy ? 1 : t->top_k;
+    p.topk_tpw = kTopkTilesPerGroup;
+    const size_t need = mtp_logits_topk_workspace_bytes(a->M, a->N);
+    if (!t->parts || !t->ws || t->ws_bytes < need || ((uintptr_t)t->ws & 255) || need == 0) {
+      set_error("%s: emode 5 needs chunk-partial output and a 256-B aligned scratch of %zu B", who, need);
+      return MTP_ERR_WORKSPACE;
+    }
+    p.topk_counters = reinterpret_cast<uint32_t*>(t->ws);   // fixed area first: shared by every shape
+    p.topk_sub = reinterpret_cast<unsigned char*>(t->ws) + kTopkCounterBytes;
   }
   *out = p;
   return MTP_OK;

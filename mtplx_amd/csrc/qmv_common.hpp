@@ -10,7 +10,7 @@ namespace mtp {
 // X_PRE: x comes with its per-32-column row sums (written by the producing
 // epilogue), so staging is the copy alone.
 enum XMode { X_PLAIN = 0, X_SWIGLU = 1, X_RMSNORM = 2, X_PRE = 3 };
-enum EMode { E_STORE = 0, E_RESID = 1, E_DUAL = 2, E_DUAL_SWIGLU = 3, E_ROPE_QKV = 4 };
+enum EMode { E_STORE = 0, E_RESID = 1, E_DUAL = 2, E_DUAL_SWIGLU = 3, E_ROPE_QKV = 4, E_STORE_TOPK = 5 };
 
 struct QmmParams {
   const uint16_t* x;       // activations [rows, ldx] (X_SWIGLU: gate)
@@ -63,6 +63,17 @@ struct QmmParams {
   int32_t* status;
   int rope_L, rope_Hq, rope_Hkv, rope_D, rope_cap, rope_blocked;
   float rope_log2_base;
+  // E_STORE_TOPK: fp32 logits (as E_STORE with yf) plus the sampler's chunk
+  // partials of every row. Workgroup vb takes the topk_tpw consecutive
+  // column tiles from vb * topk_tpw and writes the partial record of their
+  // ids (topk_sub [M][grid]); the last workgroup of each 4096-id chunk to
+  // arrive (topk_counters, one per chunk, left at zero) merges the chunk's
+  // records into topk_parts [M][n_chunks].
+  void* topk_sub;
+  void* topk_parts;
+  uint32_t* topk_counters;
+  double topk_temp;
+  int topk_ksel, topk_greedy, topk_tpw;
 };
 
 constexpr int kThreads = 256;
@@ -602,7 +613,7 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int
         fin[m * 64 + c] = in ? round_bf(v) : 0.f;
       }
       if (in) {
-        if (EM == E_STORE && p.yf)
+        if ((EM == E_STORE || EM == E_STORE_TOPK) && p.yf)
           st_f32<WT>(p.yf + o, round_bf(v));
         else
           st_u16<WT>(p.y0 + o, f2bf(v));
@@ -629,13 +640,18 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int
 
 int device_cus();
 
-// Tail-split workspace: fp32 partials of up to 8 rows x 64 values for two
-// parts per CU, then one self-resetting arrival counter per 32-column tile.
+// Every split-K workspace starts with one fixed area of arrival counters
+// (one per tile or tile group, each returned to zero by the call that used
+// it), and its partials follow. With the counters at one place for every
+// shape, one workspace serves calls of any shapes in turn: a call's partials
+// never land where another shape keeps its counters.
+constexpr size_t kCounterBytes = 65536;                 // 16384 counters
+constexpr int kMaxCounters = (int)(kCounterBytes / 4);
+// Tail split: fp32 partials of up to 8 rows x 64 values for two parts per CU.
 constexpr int kTailMaxRows = 8;
-inline size_t tail_counter_offset(int cus) { return (size_t)2 * cus * kTailMaxRows * 64 * sizeof(float); }
 inline size_t tail_workspace_bytes(int M, int N) {
   if (M < 1 || N < 1) return 0;
-  return tail_counter_offset(device_cus()) + ((size_t)cdiv(N, 32) * 4 + 255) / 256 * 256;
+  return kCounterBytes + (size_t)2 * device_cus() * kTailMaxRows * 64 * sizeof(float);
 }
 
 }  // namespace mtp

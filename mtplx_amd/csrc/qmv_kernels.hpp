@@ -537,7 +537,7 @@ static size_t full_split_partial_bytes(int M, int N, int K, int nw) {
   return (b + 255) / 256 * 256;
 }
 static size_t full_split_ws_bytes(int M, int N, int K, int nw) {
-  return full_split_partial_bytes(M, N, K, nw) + ((size_t)cdiv(N, 32) * 4 + 255) / 256 * 256;
+  return kCounterBytes + full_split_partial_bytes(M, N, K, nw);
 }
 
 
@@ -704,5 +704,17 @@ void qmv_launch_pre(int em, int gsh, const QmmParams& p, const Plan& pl, hipStre
 void qmv_launch_rmsnorm(int em, int gsh, const QmmParams& p, const Plan& pl, hipStream_t st);
 // q|k|v with the RoPE epilogue (x plain or RMSNorm).
 void qmv_launch_rope_qkv(int xm, const QmmParams& p, const Plan& pl, hipStream_t st);
+// Logits with the sampler's chunk partials (E_STORE_TOPK; x plain or RMSNorm).
+void qmv_launch_topk(int xm, const QmmParams& p, const Plan& pl, hipStream_t st);
+
+// E_STORE_TOPK: column tiles per workgroup (256 ids: 16 groups per 4096-id
+// chunk) and the scratch of the groups' partial records.
+constexpr int kTopkTilesPerGroup = 8;
+constexpr size_t kTopkCounterBytes = 4096;   // one counter per 4096-id chunk, first in the scratch
+constexpr int kTopkMaxChunks = (int)(kTopkCounterBytes / 4);
+inline size_t topk_sub_bytes(int M, int N) {
+  const size_t groups = (size_t)cdiv(cdiv(N, 32), kTopkTilesPerGroup);
+  return ((size_t)M * groups * sizeof(ChunkPart) + 255) & ~(size_t)255;
+}
 
 }  // namespace mtp

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "qmv_common.hpp"
+#include "sampler_common.hpp"
 
 #include <type_traits>
 
@@ -84,12 +85,13 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   // Tail split (packed weights only): workgroups from p.tail_first on each
   // take quads [q_lo, q_lo + q_n) of a leftover tile, one of tail_split
   // parts; the part that arrives last sums the parts in order and finishes.
-  const bool tail = PK && p.tail_split > 1 && vb >= p.tail_first;
+  constexpr bool kTopk = EM == E_STORE_TOPK;
+  const bool tail = !kTopk && PK && p.tail_split > 1 && vb >= p.tail_first;
   const bool full = tail && p.full_split;
-  // Tile stride between a workgroup's tiles: the grid, or the number of tile
-  // groups in the full split.
-  const int G = full ? vg / p.tail_split : vg;
-  int tile0 = vb, part = 0, q_lo = 0, q_n = Q;
+  // Tile stride between a workgroup's tiles: the grid, the number of tile
+  // groups in the full split, or 1 (E_STORE_TOPK: consecutive tiles).
+  const int G = kTopk ? 1 : (full ? vg / p.tail_split : vg);
+  int tile0 = kTopk ? vb * p.topk_tpw : vb, part = 0, q_lo = 0, q_n = Q;
   if (tail) {
     const int e = vb - p.tail_first;
     tile0 = p.tail_first + e / p.tail_split;
@@ -99,7 +101,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   }
   // A phase's grid can exceed its work (a persistent kernel keeps every CU):
   // workgroups without a tile only meet the barrier.
-  if (tail ? vb - p.tail_first >= (p.n_blocks - p.tail_first) * p.tail_split : vb >= p.n_blocks) {
+  if (tail ? vb - p.tail_first >= (p.n_blocks - p.tail_first) * p.tail_split : tile0 >= p.n_blocks) {
     if constexpr (kPhase) pre();
     return;
   }
@@ -111,6 +113,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   float* xs = reinterpret_cast<float*>(smem + xa_bytes(4 * QX, M));            // [QX*4][XSW]
   float* red = xs + QX * 4 * XSW;                                              // [NW][M][32]
   float* fin = red + NW * M * 32;                                              // [M][64]
+  float* topv = fin + M * 64;          // E_STORE_TOPK: [M][topk_tpw * 32] stored logits of this group
   __shared__ float s_inv_rms[32];
   __shared__ int s_last;
 
@@ -121,7 +124,9 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   const uint16_t* Bi = which ? p.b1 : p.b0;
   const int sgroups = p.K >> (6 + GSH);
   const int qw = (q_n > kw) ? cdiv(q_n - kw, KS) : 0;
-  const int ntiles = full ? cdiv(p.n_blocks - tile0, G) : ((PK && p.tail_split > 1) ? 1 : cdiv(p.n_blocks - vb, G));
+  const int ntiles = kTopk ? min(p.topk_tpw, p.n_blocks - tile0)
+                           : (full ? cdiv(p.n_blocks - tile0, G)
+                                   : ((PK && p.tail_split > 1) ? 1 : cdiv(p.n_blocks - vb, G)));
   const int nitems = ntiles * qw;
 
   // A operands: lanes of rows >= M repeat row c32 % M (their output rows
@@ -306,6 +311,10 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
     }
     qmm_epilogue<NW, EM, kPhase>(p, fin, nb, M, 0, (use_pre && j == 0) ? &pre_resid : nullptr,
                          (use_rpre && j == 0) ? &rope_pre : nullptr);
+    if constexpr (kTopk) {   // the stored values (bf16-rounded), for the group's partial
+      for (int idx = tid; idx < M * 32; idx += NT)
+        topv[(idx >> 5) * (p.topk_tpw * 32) + j * 32 + (idx & 31)] = fin[(idx >> 5) * 64 + (idx & 31)];
+    }
   };
 
   // Full split: after the last tile, wait once for all the part stores, then
@@ -336,6 +345,38 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
       }
       lds_barrier();   // s_lastv is rewritten by the next round
     }
+  };
+
+  // E_STORE_TOPK, after the group's tiles: one wave per row writes the
+  // partial record of the group's ids; the chunk's last group to arrive
+  // merges the chunk's records into its chunk partial and resets the counter.
+  auto topk_finish = [&](int sub, int nsub, int Mr, int t) {
+    lds_barrier();
+    const int span = p.topk_tpw * 32;               // ids per group (divides the 4096-id chunk)
+    const int id0 = sub * span;
+    const int spc = kChunk / span;                  // groups per chunk
+    const int chunk = sub / spc;
+    const int n_chunks = cdiv(p.N, kChunk);
+    ChunkPart* subs = reinterpret_cast<ChunkPart*>(p.topk_sub);
+    for (int m = wave; m < Mr; m += NW)
+      wave_sub_partial(topv + m * span, span, id0, p.N, p.topk_temp, p.topk_ksel, p.topk_greedy,
+                       subs + (size_t)m * nsub + sub);
+    __builtin_amdgcn_s_waitcnt(0);
+    lds_barrier();
+    const int first = chunk * spc;
+    const int nsc = (nsub - first) < spc ? (nsub - first) : spc;
+    if (t == 0) {
+      const unsigned old = __hip_atomic_fetch_add(p.topk_counters + chunk, 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+      s_last = (old == (unsigned)(nsc - 1)) ? 1 : 0;
+    }
+    lds_barrier();
+    if (!s_last) return;
+    ChunkPart* parts = reinterpret_cast<ChunkPart*>(p.topk_parts);
+    for (int m = wave; m < Mr; m += NW)
+      wave_merge_subs(subs + (size_t)m * nsub + first, nsc, p.topk_ksel, p.topk_greedy,
+                      parts + (size_t)m * n_chunks + chunk);
+    if (t == 0) __hip_atomic_store(p.topk_counters + chunk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
 
   // Prologue: the norm statistics, x straight into LDS, the norm weights
@@ -390,6 +431,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   if (qw == 0) {
     for (int j = 0; j < ntiles; ++j) finish(j);
     arrive_all();
+    if constexpr (kTopk) topk_finish(vb, vg, M, tid);
     return;
   }
   // One exit, at the bottom: a break after each step would be merged by the
@@ -417,6 +459,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
     }
   } while (i < nitems);
   arrive_all();
+  if constexpr (kTopk) topk_finish(vb, vg, M, tid);
 }
 
 }  // namespace mtp

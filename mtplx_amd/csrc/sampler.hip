@@ -38,6 +38,7 @@
 // added to the raw logits before any of this (mtp_apply_logit_deltas).
 // Deterministic: fixed reduction trees, no float atomics.
 #include "common.hpp"
+#include "sampler_common.hpp"
 
 #include <math.h>
 
@@ -45,88 +46,6 @@
 
 namespace mtp {
 
-constexpr int kSampThreads = 512;
-constexpr int kEPT = 8;                           // logits per thread per chunk
-constexpr int kChunk = kSampThreads * kEPT;       // 4096
-constexpr int kMaxTopK = 64;
-
-struct ChunkPart {
-  double m;             // max of l/T over the chunk (-inf if all -inf)
-  double s;             // sum exp(l/T - m)
-  int nonfinite;        // NaN or +inf seen
-  int pad;
-  uint64_t keys[kMaxTopK];
-};
-
-__device__ __forceinline__ uint32_t ordered_bits(float v) {
-  uint32_t u = __float_as_uint(v);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ float key_value(uint64_t key) {
-  uint32_t o = (uint32_t)(key >> 32);
-  uint32_t u = (o & 0x80000000u) ? (o & 0x7fffffffu) : ~o;
-  return __uint_as_float(u);
-}
-
-__device__ __forceinline__ int key_id(uint64_t key) { return (int)(~(uint32_t)key); }
-
-__device__ __forceinline__ uint64_t make_key(float v, int id) {
-  return ((uint64_t)ordered_bits(v) << 32) | (uint64_t)(~(uint32_t)id);
-}
-
-// Wave-uniform lane reads (v_readlane: the lane index must be uniform) and
-// DPP row steps, so the wave reductions below use no LDS permutes. Call them
-// from uniform control flow.
-__device__ __forceinline__ uint32_t rl32(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }
-__device__ __forceinline__ uint64_t rl64(uint64_t v, int l) {
-  return ((uint64_t)rl32((uint32_t)(v >> 32), l) << 32) | rl32((uint32_t)v, l);
-}
-__device__ __forceinline__ double rlf64(double v, int l) {
-  return __longlong_as_double((long long)rl64((uint64_t)__double_as_longlong(v), l));
-}
-__device__ __forceinline__ int rli(int v, int l) { return (int)rl32((uint32_t)v, l); }
-
-template <int CTRL>
-__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, false);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
-  return ((uint64_t)hi << 32) | lo;
-}
-template <int CTRL>
-__device__ __forceinline__ double dppf64(double v) {
-  return __longlong_as_double((long long)dpp64<CTRL>((uint64_t)__double_as_longlong(v)));
-}
-// Row (16-lane) steps: quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror.
-constexpr int kDppX1 = 0xB1, kDppX2 = 0x4E, kDppHalf = 0x141, kDppRow = 0x140;
-
-__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  v = umax64(v, dpp64<kDppX1>(v));
-  v = umax64(v, dpp64<kDppX2>(v));
-  v = umax64(v, dpp64<kDppHalf>(v));
-  v = umax64(v, dpp64<kDppRow>(v));
-  return umax64(umax64(rl64(v, 0), rl64(v, 16)), umax64(rl64(v, 32), rl64(v, 48)));
-}
-
-__device__ __forceinline__ double wave_max_f64(double v) {
-  v = fmax(v, dppf64<kDppX1>(v));
-  v = fmax(v, dppf64<kDppX2>(v));
-  v = fmax(v, dppf64<kDppHalf>(v));
-  v = fmax(v, dppf64<kDppRow>(v));
-  return fmax(fmax(rlf64(v, 0), rlf64(v, 16)), fmax(rlf64(v, 32), rlf64(v, 48)));
-}
-
-// Fixed tree: pairs, quads, eights, rows (each step commutative, so every
-// lane of a row holds the same sum), then the four rows.
-__device__ __forceinline__ double wave_sum_f64(double v) {
-  v += dppf64<kDppX1>(v);
-  v += dppf64<kDppX2>(v);
-  v += dppf64<kDppHalf>(v);
-  v += dppf64<kDppRow>(v);
-  return (rlf64(v, 0) + rlf64(v, 16)) + (rlf64(v, 32) + rlf64(v, 48));
-}
 
 // grid: (n_chunks, rows). logits row r at logits + r * ld.
 // Rows below nrows1 come from logits, the rest from logits2 (row - nrows1).
@@ -1340,10 +1259,16 @@ MTP_API size_t mtp_sampler_workspace_bytes(int rows, int V, int top_k) {
 static int spec_accept_run(const float* target_logits, const float* draft_logits, const int32_t* draft_ids,
                            const double* uniforms, int B, int K, int V, double temperature, int top_k, double top_p,
                            int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
-                           size_t ws_bytes, void* stream, AcceptRows rr, int nt, int nd, const char* who) {
+                           size_t ws_bytes, void* stream, AcceptRows rr, int nt, int nd, const char* who,
+                           bool target_ready = false) {
   SamplerPlan pl;
   int rc = sampler_plan(V, top_k, temperature, &pl, who);
   if (rc) return rc;
+  if (target_ready && pl.wide) {
+    set_error("%s: precomputed target partials serve narrow laws only (temperature <= 0 or 1 <= top_k <= %d)", who,
+              kMaxTopK);
+    return MTP_ERR_UNSUPPORTED;
+  }
   if (B < 1 || K < 1 || nt < B || nd < 0 || !target_logits || (nd > 0 && !draft_logits) || !draft_ids || !uniforms ||
       !out_tokens || !n_accepted || !accept_probs || !status) {
     set_error("%s: need B>=1, K>=1 and non-null buffers", who);
@@ -1361,11 +1286,19 @@ static int spec_accept_run(const float* target_logits, const float* draft_logits
   ChunkPart* dparts = tparts + (size_t)nt * n_chunks;
   const double temp = pl.greedy ? 1.0 : temperature;
   rr.nt = nt;
-  // target rows then draft rows, one launch (dparts follows tparts)
-  hipLaunchKernelGGL(vocab_partials, dim3(n_chunks, rows), dim3(kSampThreads), 0, st, target_logits,
-                     draft_logits ? draft_logits : target_logits, nt, (long long)V, V, n_chunks, temp, pl.ksel,
-                     pl.greedy, tparts);
-  if ((rc = launch_check(who))) return rc;
+  if (target_ready) {   // the target rows' partials are in ws already: the draft rows only
+    if (nd > 0) {
+      hipLaunchKernelGGL(vocab_partials, dim3(n_chunks, nd), dim3(kSampThreads), 0, st, draft_logits, draft_logits,
+                         nd, (long long)V, V, n_chunks, temp, pl.ksel, pl.greedy, dparts);
+      if ((rc = launch_check(who))) return rc;
+    }
+  } else {
+    // target rows then draft rows, one launch (dparts follows tparts)
+    hipLaunchKernelGGL(vocab_partials, dim3(n_chunks, rows), dim3(kSampThreads), 0, st, target_logits,
+                       draft_logits ? draft_logits : target_logits, nt, (long long)V, V, n_chunks, temp, pl.ksel,
+                       pl.greedy, tparts);
+    if ((rc = launch_check(who))) return rc;
+  }
   if (pl.wide) {
     unsigned char* lawbuf = reinterpret_cast<unsigned char*>(ws) + parts_bytes(rows, V);
     const size_t rb = wide_row_bytes(V);
@@ -1405,6 +1338,19 @@ MTP_API int mtp_spec_accept(const float* target_logits, const float* draft_logit
   return spec_accept_run(target_logits, draft_logits, draft_ids, uniforms, B, K, V, temperature, top_k, top_p,
                          out_tokens, n_accepted, accept_probs, status, ws, ws_bytes, stream, AcceptRows{}, B * (K + 1),
                          B * K, "mtp_spec_accept");
+}
+
+MTP_API int mtp_spec_accept_parts(const float* target_logits, const float* draft_logits, const int32_t* draft_ids,
+                                  const double* uniforms, int B, int K, int V, double temperature, int top_k,
+                                  double top_p, int32_t* out_tokens, int32_t* n_accepted, double* accept_probs,
+                                  int32_t* status, void* ws, size_t ws_bytes, void* stream) {
+  if (B < 1 || K < 1) {
+    set_error("mtp_spec_accept_parts: need B>=1, K>=1");
+    return MTP_ERR_ARG;
+  }
+  return spec_accept_run(target_logits, draft_logits, draft_ids, uniforms, B, K, V, temperature, top_k, top_p,
+                         out_tokens, n_accepted, accept_probs, status, ws, ws_bytes, stream, AcceptRows{}, B * (K + 1),
+                         B * K, "mtp_spec_accept_parts", true);
 }
 
 MTP_API int mtp_spec_accept_ragged(const float* target_logits, int n_target, const float* draft_logits, int n_draft,

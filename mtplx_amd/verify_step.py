@@ -36,7 +36,7 @@ import torch
 from . import _lib
 from .moe_sorted_gather import expert_sort, moe_combine
 from .quant import QuantizedLinear, rope_row_order
-from .sampling import SamplerConfig, spec_accept
+from .sampling import SamplerConfig, narrow_law, sampler_workspace, spec_accept
 
 
 @dataclass
@@ -307,11 +307,14 @@ class VerifyModel:
 
     # -- forward --------------------------------------------------------------
     def verify_logits(self, tokens: torch.Tensor, q_start: torch.Tensor, q_lens: torch.Tensor | None = None,
-                      *, logits_out: torch.Tensor | None = None, check: bool = False) -> torch.Tensor:
+                      *, logits_out: torch.Tensor | None = None, check: bool = False,
+                      topk: dict | None = None) -> torch.Tensor:
         """``tokens`` int32 ``[B, L]`` (GPU), ``q_start`` int32 ``[B]`` (GPU):
         writes K/V of the L rows at ``q_start[b] + i`` and returns fp32 logits ``[B*L, V]``.
         The device status word (:meth:`status`) flags invalid tokens or
-        positions; ``check=True`` synchronises and raises on it."""
+        positions; ``check=True`` synchronises and raises on it. ``topk``
+        (fields of ``mtp_logits_topk``, B*L <= 8): the lm_head also writes
+        the sampler's chunk partials of every row."""
         c = self.cfg
         B, Lq = (int(s) for s in tokens.shape)
         M = B * Lq
@@ -389,7 +392,7 @@ class VerifyModel:
                 ss_h = ss_b
         logits = logits_out if logits_out is not None else torch.empty((M, c.vocab), dtype=torch.float32, device=dev)
         qmv(st, x=h, x2=self.final_norm, ss_in=ss_h, eps=c.rms_eps, w0=W(self.lm_head), yf=logits, M=M,
-            N=c.vocab, K=H, group_size=gs, xmode=2, emode=0, packed=lay)
+            N=c.vocab, K=H, group_size=gs, xmode=2, emode=0 if topk is None else 5, packed=lay, topk=topk)
         self._status = status
         if check:
             self.check_status()
@@ -533,13 +536,27 @@ class VerifyModel:
         return spec_accept_ragged(logits, row_off[:-1], draft_logits, d_off, q_lens - 1, drafts, uniforms, sampler)
 
     def verify_step(self, tokens: torch.Tensor, q_start: torch.Tensor, draft_logits: torch.Tensor,
-                    uniforms: torch.Tensor, sampler: SamplerConfig = SamplerConfig()):
+                    uniforms: torch.Tensor, sampler: SamplerConfig = SamplerConfig(), *, fuse_topk: bool = True):
         """Forward the ``B x (K+1)`` verify rows, then accept/reject against the drafts
-        (``tokens[:, 1:]`` are the draft ids). Returns the device-side accept result."""
+        (``tokens[:, 1:]`` are the draft ids). Returns the device-side accept result.
+
+        With ``fuse_topk`` (and a narrow law, at most 8 rows) the lm_head
+        writes the target rows' chunk partials straight into the sampler's
+        workspace, so the accept step reduces only the draft rows."""
         B, L = (int(s) for s in tokens.shape)
-        logits = self.verify_logits(tokens, q_start)
+        K = L - 1
+        c = self.cfg
+        topk = None
+        if fuse_topk and B * L <= 8 and narrow_law(sampler, c.vocab):
+            sws = sampler_workspace(B, K, c.vocab, sampler, self.device)
+            nb = _lib.query("mtp_logits_topk_workspace_bytes", B * L, c.vocab)
+            tws = _lib.WORKSPACES.get(nb, "logits_topk", self.device)
+            topk = dict(parts=sws, ws=tws, ws_bytes=tws.numel(), temperature=float(sampler.temperature),
+                        top_k=int(sampler.top_k))
+        logits = self.verify_logits(tokens, q_start, topk=topk)
         self.last_logits = logits
-        return spec_accept(logits.reshape(B, L, -1), draft_logits, tokens[:, 1:].contiguous(), uniforms, sampler)
+        return spec_accept(logits.reshape(B, L, -1), draft_logits, tokens[:, 1:].contiguous(), uniforms, sampler,
+                           target_parts_ready=topk is not None)
 
 
 class CapturedVerifyStep:

@@ -46,11 +46,10 @@ def test_size_queries_without_gpu(lib):
     row = ((16 + 4 * 151936 + 15) // 16 * 16 + 8 * 151936 + 255) // 256 * 256
     assert lib.mtp_sampler_workspace_bytes(7, 151936, 0) == (7 * 38 * 536 + 255) // 256 * 256 + 2 * 7 * row
     assert lib.mtp_attn_workspace_bytes(8, 8, 32768, 0) == 8 * 8 * 32 * (32 * 128 + 64) * 4
-    # tail split: two fp32 [8][64] partials per CU (256 when no device is
-    # visible, as here), then one arrival counter per 32-column tile
-    # (256-B aligned).
-    counters = (17408 // 32 * 4 + 255) // 256 * 256
-    assert lib.mtp_qmv_workspace_bytes(4, 17408, 5120, 0) == 2 * 256 * 8 * 64 * 4 + counters
+    # tail split: a fixed 64 KiB area of arrival counters first (shared by
+    # every shape), then two fp32 [8][64] partials per CU (256 when no device
+    # is visible, as here).
+    assert lib.mtp_qmv_workspace_bytes(4, 17408, 5120, 0) == 65536 + 2 * 256 * 8 * 64 * 4
 
 
 def test_error_path_reports_message(lib):

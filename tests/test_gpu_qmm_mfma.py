@@ -92,8 +92,8 @@ def test_rows_kernel_matches_oracle(gpu, m, n, k, emode, gs):
     assert torch.equal(y.view(torch.int32) if fp32 else y.view(torch.int16),
                        y2.view(torch.int32) if fp32 else y2.view(torch.int16))
     if nb:
-        # the arrival counters sit in the workspace's last 256-byte block(s)
-        assert int(torch.count_nonzero(ws2[nb - 256: nb])) == 0
+        # the arrival counters sit in the workspace's first 64 KiB
+        assert int(torch.count_nonzero(ws2[:65536])) == 0
 
 
 @pytest.mark.parametrize("m", [16, 32])
@@ -132,3 +132,40 @@ def test_rows_kernel_needs_workspace_when_splitting(gpu):
     assert e.value.code == -3
     with pytest.raises(_lib.MtpError):
         _lib.qmm_mfma(_st(), x=x, w0=q0.pack(), y=y, M=65, N=n, K=k, group_size=64, emode=0)
+
+
+def test_one_workspace_serves_shapes_in_turn(gpu):
+    """Calls of different shapes alternate on one workspace (as the ragged
+    verify's projections do, layer after layer): every result repeats
+    bitwise, so no shape's partials land on another shape's counters."""
+    from mtplx_amd import _lib
+    g = torch.Generator(device="cuda").manual_seed(21)
+    shapes = [(45, 5120, 17408, 1), (45, 17408, 5120, 3), (45, 7168, 5120, 0), (45, 5120, 5120, 1)]
+    nb = max(_lib.query("mtp_qmm_workspace_bytes", m, n, k, 1 if e == 3 else 0) for m, n, k, e in shapes)
+    assert nb > 0
+    ws = torch.zeros(nb, dtype=torch.uint8, device="cuda")
+    runs = []
+    for m, n, k, e in shapes:
+        q0 = _layer(n, k, 64, g)
+        q1 = _layer(n, k, 64, g) if e == 3 else None
+        x = torch.randn((m, k), device="cuda", generator=g).to(torch.bfloat16)
+        r = torch.randn((m, n), device="cuda", generator=g).to(torch.bfloat16) if e == 1 else None
+        runs.append((m, n, k, e, q0, q1, x, r))
+
+    def call(m, n, k, e, q0, q1, x, r):
+        y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+        kw = dict(x=x, w0=q0.pack(), y=y, M=m, N=n, K=k, group_size=64, emode=e, ws=ws, ws_bytes=ws.numel())
+        if q1 is not None:
+            kw["w1"] = q1.pack()
+        if r is not None:
+            kw["resid"] = r
+        _lib.qmm_mfma(_st(), **kw)
+        return y
+
+    first = [call(*a) for a in runs]
+    second = [call(*a) for a in runs]
+    torch.cuda.synchronize()
+    for a, b in zip(first, second):
+        assert not torch.isnan(a.float()).any()
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert int(torch.count_nonzero(ws[:65536])) == 0

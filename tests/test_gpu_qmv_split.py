@@ -66,7 +66,7 @@ def test_full_split_matches_reference_layout_and_oracle(gpu, m, n, k, xmode, emo
     y1, y2 = run(1), run(1)
     assert torch.equal(y1.view(torch.int16), y2.view(torch.int16)), "full split not deterministic"
     nblk = (n + 31) // 32
-    cnt = ws[ws.numel() - (nblk * 4 + 255) // 256 * 256:][: 4 * nblk]
+    cnt = ws[: 4 * nblk]   # the counter area opens the workspace
     assert int(cnt.view(torch.int32).abs().sum().item()) == 0, "arrival counters not reset"
     a, b = bf16_values(y1), bf16_values(run(0))
     assert not np.isnan(a).any(), "unwritten outputs"
@@ -108,3 +108,38 @@ def test_full_split_needs_workspace(gpu):
     with pytest.raises(_lib.MtpError) as e:
         _lib.qmv_ex(_st(), x=x, w0=q.pack(), y0=y, M=m, N=n, K=k, group_size=64, packed=1)
     assert e.value.code == -2 and b"workspace" in str(e.value).encode()
+
+
+def test_one_workspace_serves_split_shapes_in_turn(gpu):
+    """Full-split and tail-split calls of different shapes alternate on one
+    workspace (as a verify forward's projections do, layer after layer):
+    every result repeats bitwise and the counter area ends at zero."""
+    from mtplx_amd import _lib
+    from mtplx_amd.quant import QuantizedLinear
+    g = torch.Generator(device="cuda").manual_seed(31)
+    shapes = [(16, 5120, 17408, 0), (16, 17408, 5120, 3), (16, 7168, 5120, 0), (4, 17408, 5120, 3),
+              (4, 5120, 17408, 0)]
+    nb = max(_lib.query("mtp_qmv_workspace_bytes", m, n, k, 1) for m, n, k, _ in shapes)
+    ws = torch.zeros(nb, dtype=torch.uint8, device="cuda")
+    runs = []
+    for m, n, k, e in shapes:
+        q0 = QuantizedLinear.random(n, k, 64, generator=g)
+        q1 = QuantizedLinear.random(n, k, 64, generator=g) if e == 3 else None
+        runs.append((m, n, k, e, q0, q1, torch.randn((m, k), device="cuda", generator=g).to(torch.bfloat16)))
+
+    def call(m, n, k, e, q0, q1, x):
+        y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+        kw = dict(x=x, w0=q0.pack(), y0=y, M=m, N=n, K=k, group_size=64, xmode=0, emode=e, packed=1, ws=ws,
+                  ws_bytes=ws.numel())
+        if q1 is not None:
+            kw["w1"] = q1.pack()
+        _lib.qmv_ex(_st(), **kw)
+        return y
+
+    first = [call(*a) for a in runs]
+    second = [call(*a) for a in runs]
+    torch.cuda.synchronize()
+    for a, b in zip(first, second):
+        assert not torch.isnan(a.float()).any()
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert int(torch.count_nonzero(ws[:65536])) == 0

@@ -69,7 +69,7 @@ def test_tail_split_matches_unsplit_and_oracle(gpu, m, n, k, xmode, emode):
     assert torch.equal(ss1, ss2)
     assert not torch.isnan(y1.float()).any(), "unwritten outputs"
     nblk = (n + 31) // 32
-    cnt = ws[ws.numel() - (nblk * 4 + 255) // 256 * 256:][: 4 * nblk]
+    cnt = ws[: 4 * nblk]   # the counter area opens the workspace
     assert int(cnt.view(torch.int32).abs().sum().item()) == 0, "arrival counters not reset"
     y0, _ = _run(q0, q1, x, nw, ssin, r, xmode, emode, m, n, k, None)
     a, b = bf16_values(y1), bf16_values(y0)
