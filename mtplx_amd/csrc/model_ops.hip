@@ -161,22 +161,68 @@ __global__ void rope_qkv_blocks_kernel(const uint16_t* qkv, const int32_t* row_o
   }
 }
 
+// One workgroup per row. Rows whose width is a multiple of 8 and at most
+// 8192 are read once, 16 bytes per load, and kept in registers between the
+// sum of squares and the scaled store; others take a strided loop.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const uint16_t* w, uint16_t* out, int H,
                                                       float eps) {
+  constexpr int kCh = 4;   // 8-value chunks per thread on the fast path
   const int m = blockIdx.x;
+  const int tid = threadIdx.x;
   const uint16_t* xr = x + (size_t)m * H;
+  uint16_t* orow = out + (size_t)m * H;
   __shared__ float red[4];
+  const bool fast = (H % 8) == 0 && H <= 256 * 8 * kCh;
   float ss = 0.f;
-  for (int k = threadIdx.x; k < H; k += 256) {
-    const float a = bf2f(xr[k]);
-    ss += a * a;
+  uint4 xv[kCh];
+  if (fast) {
+#pragma unroll
+    for (int c = 0; c < kCh; ++c) {
+      const int k = (tid + c * 256) * 8;
+      xv[c] = k < H ? *reinterpret_cast<const uint4*>(xr + k) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int c = 0; c < kCh; ++c) {
+      const uint32_t u[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a = __uint_as_float(u[j] << 16), b = __uint_as_float(u[j] & 0xffff0000u);
+        ss = fmaf(a, a, ss);
+        ss = fmaf(b, b, ss);
+      }
+    }
+  } else {
+    for (int k = tid; k < H; k += 256) {
+      const float a = bf2f(xr[k]);
+      ss += a * a;
+    }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   const float inv = rsqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)H + eps);
-  for (int k = threadIdx.x; k < H; k += 256) out[(size_t)m * H + k] = f2bf(bf2f(xr[k]) * inv * bf2f(w[k]));
+  if (fast) {
+#pragma unroll
+    for (int c = 0; c < kCh; ++c) {
+      const int k = (tid + c * 256) * 8;
+      if (k < H) {
+        const uint4 wv = *reinterpret_cast<const uint4*>(w + k);
+        const uint32_t u[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+        const uint32_t g[4] = {wv.x, wv.y, wv.z, wv.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a = __uint_as_float(u[j] << 16) * inv * __uint_as_float(g[j] << 16);
+          const float b = __uint_as_float(u[j] & 0xffff0000u) * inv * __uint_as_float(g[j] & 0xffff0000u);
+          o[j] = (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+        }
+        *reinterpret_cast<uint4*>(orow + k) = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  } else {
+    for (int k = tid; k < H; k += 256) orow[k] = f2bf(bf2f(xr[k]) * inv * bf2f(w[k]));
+  }
 }
 
 }  // namespace mtp
@@ -244,8 +290,8 @@ MTP_API int mtp_rope_qkv_to_blocks(const void* qkv, int M, const int32_t* row_of
 }
 
 MTP_API int mtp_rmsnorm(const void* x, const void* w, void* out, int M, int H, float eps, void* stream) {
-  if (!x || !w || !out || M < 1 || H < 1) {
-    set_error("mtp_rmsnorm: bad arguments");
+  if (!x || !w || !out || M < 1 || H < 1 || (H % 8 == 0 && (((uintptr_t)x | (uintptr_t)w | (uintptr_t)out) & 15))) {
+    set_error("mtp_rmsnorm: bad arguments (rows of a multiple of 8 need 16-byte aligned x, w, out)");
     return MTP_ERR_ARG;
   }
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)x,

@@ -47,18 +47,56 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t* i
     if (tid == 0) active[0] = -1;
     return;
   }
-  // Exclusive scan of counts (E <= 4096, one thread: small and fixed order).
-  if (tid == 0) {
-    int run = 0, na = 0;
-    for (int e = 0; e < E; ++e) {
-      const int c = s_cnt[e];
-      expert_off[e] = run;
-      if (c > 0) active[1 + na++] = e;
-      s_cnt[e] = run;
-      run += c;
+  // Exclusive scans of the counts and of the active flags (E <= 4096: each
+  // thread takes 4 consecutive experts; integer sums, so any order is exact).
+  {
+    constexpr int kPer = kMaxExperts / kSortThreads;   // 4
+    int c[kPer], rows = 0, acts = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = tid * kPer + j;
+      c[j] = e < E ? s_cnt[e] : 0;
+      rows += c[j];
+      acts += c[j] > 0;
     }
-    expert_off[E] = run;
-    active[0] = na;
+    // inclusive scans over the workgroup: waves by shuffles, then the wave totals
+    int ir = rows, ia = acts;
+    const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int r = __shfl_up(ir, off, 64), a = __shfl_up(ia, off, 64);
+      if (lane >= off) {
+        ir += r;
+        ia += a;
+      }
+    }
+    __shared__ int s_wr[kSortThreads / 64], s_wa[kSortThreads / 64];
+    if (lane == 63) {
+      s_wr[wave] = ir;
+      s_wa[wave] = ia;
+    }
+    __syncthreads();
+    int br = 0, ba = 0;
+    for (int w2 = 0; w2 < wave; ++w2) {
+      br += s_wr[w2];
+      ba += s_wa[w2];
+    }
+    int run = br + ir - rows, na = ba + ia - acts;   // exclusive prefix of this thread's first expert
+    __syncthreads();   // every thread has read its counts: s_cnt may take the offsets
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = tid * kPer + j;
+      if (e < E) {
+        expert_off[e] = run;
+        if (c[j] > 0) active[1 + na++] = e;
+        s_cnt[e] = run;
+        run += c[j];
+      }
+    }
+    if (tid == kSortThreads - 1) {
+      expert_off[E] = run;
+      active[0] = na;
+    }
   }
   __syncthreads();
   // Stable rank: earlier rows routed to the same expert.
@@ -73,14 +111,20 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t* i
   }
 }
 
-// One wave per token: top-k experts and renormalised softmax weights.
+// One wave per token: top-k experts and renormalised softmax weights. The
+// row (plus skew) is read once into LDS; the k rounds scan it there.
+constexpr int kRouteMaxE = 4096;
 __global__ __launch_bounds__(64) void moe_route_kernel(const float* logits, long long ld, const float* skew, int E,
                                                        int top_k, int32_t* ids, float* weights) {
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
-  const float* row = logits + (size_t)t * ld;
+  const float* grow = logits + (size_t)t * ld;
+  __shared__ float row[kRouteMaxE];
   __shared__ float s_val[64];
   __shared__ int s_id[64];
+  for (int e = lane; e < E; e += 64) row[e] = skew ? grow[e] + skew[e] : grow[e];
+  __syncthreads();
+  skew = nullptr;   // already added
   int taken_id = -1;
   float taken_val = INFINITY;
   for (int r = 0; r < top_k; ++r) {
@@ -218,8 +262,9 @@ MTP_API int mtp_moe_sort(const int32_t* topk_ids, int T, int top_k, int E, uint3
 MTP_API int mtp_moe_route(const float* logits, int ld, const float* skew, int T, int E, int top_k, int32_t* ids,
                           float* weights, void* stream) {
   if (ld <= 0) ld = E;
-  if (!logits || !ids || !weights || T < 1 || E < 1 || ld < E || top_k < 1 || top_k > 64 || top_k > E) {
-    set_error("mtp_moe_route: bad arguments (1 <= top_k <= min(64, E), ld >= E)");
+  if (!logits || !ids || !weights || T < 1 || E < 1 || E > kRouteMaxE || ld < E || top_k < 1 || top_k > 64 ||
+      top_k > E) {
+    set_error("mtp_moe_route: bad arguments (1 <= top_k <= min(64, E), E <= %d, ld >= E)", kRouteMaxE);
     return MTP_ERR_ARG;
   }
   hipLaunchKernelGGL(moe_route_kernel, dim3(T), dim3(64), 0, (hipStream_t)stream, logits, (long long)ld, skew, E,

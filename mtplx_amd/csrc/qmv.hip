@@ -38,21 +38,31 @@ void set_error(const char* fmt, ...) {
   va_end(ap);
 }
 
-// Expert-gathered launch: grid (column tiles, row tiles, expert slots).
+// Expert-gathered matmul: work items (active expert slot, row tile, column
+// tile) in slot-major order, taken grid-stride by a bounded grid. The number
+// of active experts is known only on the device; a grid over every expert
+// slot would dispatch mostly empty workgroups (e.g. 63 of 256 experts
+// active), while this one stops at the active items.
 template <int R, int XM, int EM, int GSH>
 __global__ __launch_bounds__(kThreads) void gather_qmm4_kernel(QmmParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
-  const int nb = blockIdx.x;
-  const int rt = blockIdx.y;
-  const int slot = blockIdx.z;
-  if (slot >= p.active[0]) return;
-  const int e = p.active[1 + slot];
-  const int r0 = p.expert_off[e] + 32 * rt;
-  const int r1 = p.expert_off[e + 1];
-  if (r0 >= r1) return;
-  const int M = min(32, r1 - r0);
-  qmm_body<4, R, XM, EM, GSH>(p, smem, nb, M, r0, (long long)e * p.w_estride, (long long)e * p.s_estride);
-  qmm_epilogue<4, EM>(p, fin_of(smem, 4), nb, M, r0);
+  const int per_slot = p.n_blocks * p.row_tiles;
+  const int items = p.active[0] * per_slot;
+  for (int w = blockIdx.x; w < items; w += gridDim.x) {
+    const int slot = w / per_slot;
+    const int rem = w - slot * per_slot;
+    const int rt = rem / p.n_blocks;
+    const int nb = rem - rt * p.n_blocks;
+    const int e = p.active[1 + slot];
+    const int r0 = p.expert_off[e] + 32 * rt;
+    const int r1 = p.expert_off[e + 1];
+    if (r0 < r1) {
+      const int M = min(32, r1 - r0);
+      qmm_body<4, R, XM, EM, GSH>(p, smem, nb, M, r0, (long long)e * p.w_estride, (long long)e * p.s_estride);
+      qmm_epilogue<4, EM>(p, fin_of(smem, 4), nb, M, r0);
+    }
+    __syncthreads();   // the next item restages LDS
+  }
 }
 
 int device_cus() {
@@ -437,7 +447,10 @@ MTP_API int mtp_gather_qmv_affine4(const void* x, const void* x2, const uint32_t
   }
   p.chunk = pl.chunk;
   pl.lds = lds_bytes(pl.chunk, mrows, 4);
-  dim3 grid(pl.n_blocks, p.row_tiles, E);
+  p.n_blocks = pl.n_blocks;
+  const long long all_items = (long long)pl.n_blocks * p.row_tiles * E;
+  const int cap = 4 * device_cus();   // a few resident workgroups per CU
+  dim3 grid((unsigned)(all_items < cap ? all_items : cap));
   hipStream_t st = (hipStream_t)stream;
 #define MTP_GATHER(RR, XMV, EMV)                                                                            \
   do {                                                                                                       \
