@@ -581,6 +581,8 @@ def main() -> int:
                          "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--profile-step", action="store_true",
                     help="only run one eager verify step and a 256 MiB copy, for rocprofv3 --pmc over every kernel")
+    ap.add_argument("--workload", choices=["cfg2", "cfg4", "cfg5"], default=None,
+                    help="only run that configuration's measurement (its sub-line, printed alone; for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the hot path is single-GPU); --gpus {args.gpus} is not supported",
@@ -596,6 +598,16 @@ def main() -> int:
     _lib.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.workload == "cfg2":
+        print(json.dumps(cfg2_attention()), flush=True)
+        return 0
+    if args.workload == "cfg5":
+        print(json.dumps(cfg5_moe(steps=args.steps, warmup=args.warmup)), flush=True)
+        return 0
+    if args.workload == "cfg4":
+        print(json.dumps(cfg4_ragged(VerifyModel(DENSE_27B, device=dev, seed=0), steps=args.steps,
+                                     warmup=args.warmup)), flush=True)
+        return 0
     cfg = DENSE_27B
     B, K = 1, 3
     L = K + 1
@@ -641,6 +653,7 @@ def main() -> int:
 
     roof = roofline_gate_up(model, B * L)
     parts = set(args.parts.split(",")) if args.parts else {"cfg1", "qmm", "cfg4", "cfg2", "cfg5"}
+    parts.discard("none")
     if "cfg1" in parts:
         roof["cfg1_qmv"] = roofline_qmv_cfg1()
     if "qmm" in parts:

@@ -46,7 +46,7 @@ SIGNATURES = {
     "mtp_embed_affine4": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp]),
     "mtp_sampler_workspace_bytes": (_sz, [_i, _i, _i]),
     "mtp_spec_accept": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
-    "mtp_spec_accept_parts": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mtp_spec_accept_parts": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "mtp_spec_accept_ragged": (_i, [_vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp,
                                     _vp, _vp, _sz, _vp]),
     "mtp_spec_accept_noalloc": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp]),
@@ -65,6 +65,7 @@ SIGNATURES = {
     "mtp_pack_affine4_mf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mtp_qmv_affine4_ex": (_i, [_vp, _vp]),
     "mtp_logits_topk_workspace_bytes": (_sz, [_i, _i]),
+    "mtp_logits_topk_parts_bytes": (_sz, [_i]),
     "mtp_qmm_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "mtp_qmm_affine4_mfma": (_i, [_vp, _vp]),
     "mtp_attn_blocks_workspace_bytes": (_sz, [_i, _i, _i, C.c_longlong, _i]),
@@ -87,7 +88,7 @@ class LogitsTopk(C.Structure):
     """``mtp_logits_topk`` of include/mtplx_amd.h (same field order)."""
 
     _fields_ = [("parts", _vp), ("ws", _vp), ("ws_bytes", C.c_size_t), ("temperature", C.c_double),
-                ("top_k", _i)]
+                ("top_k", _i), ("n_parts", _i)]
 
 
 class QmvArgs(C.Structure):
@@ -121,6 +122,8 @@ def qmv_ex(stream, rope: dict | None = None, topk: dict | None = None, **fields)
         t = _fill(LogitsTopk(), topk)
         a.topk = C.pointer(t)
     call("mtp_qmv_affine4_ex", C.byref(a), stream)
+    if t is not None:
+        topk["n_parts"] = int(t.n_parts)   # the records per row the call wrote
 
 
 class QmmArgs(C.Structure):

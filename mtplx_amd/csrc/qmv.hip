@@ -177,8 +177,12 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
     }
     p.chunk = pl.chunk;
     p.n_blocks = pl.n_blocks;
-    pl.lds += (size_t)p.M * p.topk_tpw * 32 * sizeof(float);
-    qmv_launch_topk(xm, p, pl, st);
+    const int parts = qmv_launch_topk(xm, p, pl, st);
+    if (parts < 0) {
+      set_error("%s: emode 5 needs at most 32 tiles per resident workgroup (N=%d)", who, p.N);
+      return MTP_ERR_UNSUPPORTED;
+    }
+    if (p.topk_nparts) *p.topk_nparts = parts;
     return launch_check(who);
   }
   if (em == E_ROPE_QKV) {
@@ -260,8 +264,13 @@ using namespace mtp;
 MTP_API const char* mtp_last_error(void) { return g_err; }
 
 MTP_API size_t mtp_logits_topk_workspace_bytes(int M, int N) {
-  if (M < 1 || M > 8 || N < 1 || cdiv(N, kChunk) > kTopkMaxChunks) return 0;
-  return kTopkCounterBytes + topk_sub_bytes(M, N);
+  if (M < 1 || M > 8 || N < 1) return 0;
+  return kTopkCounterBytes + topk_sub_bytes(M);
+}
+
+MTP_API size_t mtp_logits_topk_parts_bytes(int M) {
+  if (M < 1 || M > 8) return 0;
+  return (size_t)M * kTopkParts * sizeof(ChunkPart);
 }
 
 MTP_API size_t mtp_qmv_workspace_bytes(int M, int N, int K, int dual) {
@@ -625,12 +634,12 @@ int qmv_args_params(const mtp_qmv_args* a, QmmParams* out, const char* who) {
     p.rope_log2_base = r->rope_base > 1.f ? log2f(r->rope_base) : 0.f;
   }
   if (a->emode == E_STORE_TOPK) {
-    const mtp_logits_topk* t = a->topk;
+    mtp_logits_topk* t = a->topk;
     p.topk_parts = t->parts;
     p.topk_greedy = !(t->temperature > 0.0);
     p.topk_temp = p.topk_greedy ? 1.0 : t->temperature;
     p.topk_ksel = p.topk_greedy ? 1 : t->top_k;
-    p.topk_tpw = kTopkTilesPerGroup;
+    p.topk_nparts = &a->topk->n_parts;
     const size_t need = mtp_logits_topk_workspace_bytes(a->M, a->N);
     if (!t->parts || !t->ws || t->ws_bytes < need || ((uintptr_t)t->ws & 255) || need == 0) {
       set_error("%s: emode 5 needs chunk-partial output and a 256-B aligned scratch of %zu B", who, need);

@@ -21,6 +21,7 @@ struct mtp_logits_topk {
   size_t ws_bytes;
   double temperature;
   int top_k;
+  int n_parts;
 };
 
 struct mtp_qmv_args {
@@ -47,7 +48,7 @@ struct mtp_qmv_args {
   int schedule;
   const float* x_sums;
   float* y_sums;
-  const mtp_logits_topk* topk;
+  mtp_logits_topk* topk;
 };
 
 namespace mtp {

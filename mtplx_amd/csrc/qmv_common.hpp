@@ -63,17 +63,19 @@ struct QmmParams {
   int32_t* status;
   int rope_L, rope_Hq, rope_Hkv, rope_D, rope_cap, rope_blocked;
   float rope_log2_base;
-  // E_STORE_TOPK: fp32 logits (as E_STORE with yf) plus the sampler's chunk
-  // partials of every row. Workgroup vb takes the topk_tpw consecutive
-  // column tiles from vb * topk_tpw and writes the partial record of their
-  // ids (topk_sub [M][grid]); the last workgroup of each 4096-id chunk to
-  // arrive (topk_counters, one per chunk, left at zero) merges the chunk's
-  // records into topk_parts [M][n_chunks].
+  // E_STORE_TOPK: fp32 logits (as E_STORE with yf) plus the sampler's
+  // partial records of every row. The workgroups stream tiles as for
+  // E_STORE (vb, vb + grid, ...; at most topk_tpw each); each writes the
+  // record of its ids (topk_sub [M][grid]); consecutive sets of topk_wpg
+  // workgroups are merged by the last of each set to arrive (topk_counters,
+  // one per set, left at zero) into topk_parts [M][kTopkParts], one record
+  // per set.
   void* topk_sub;
   void* topk_parts;
   uint32_t* topk_counters;
   double topk_temp;
-  int topk_ksel, topk_greedy, topk_tpw;
+  int topk_ksel, topk_greedy, topk_tpw, topk_wpg;
+  int* topk_nparts;   // host: receives the records per row
 };
 
 constexpr int kThreads = 256;

@@ -88,10 +88,10 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   constexpr bool kTopk = EM == E_STORE_TOPK;
   const bool tail = !kTopk && PK && p.tail_split > 1 && vb >= p.tail_first;
   const bool full = tail && p.full_split;
-  // Tile stride between a workgroup's tiles: the grid, the number of tile
-  // groups in the full split, or 1 (E_STORE_TOPK: consecutive tiles).
-  const int G = kTopk ? 1 : (full ? vg / p.tail_split : vg);
-  int tile0 = kTopk ? vb * p.topk_tpw : vb, part = 0, q_lo = 0, q_n = Q;
+  // Tile stride between a workgroup's tiles: the grid, or the number of tile
+  // groups in the full split.
+  const int G = full ? vg / p.tail_split : vg;
+  int tile0 = vb, part = 0, q_lo = 0, q_n = Q;
   if (tail) {
     const int e = vb - p.tail_first;
     tile0 = p.tail_first + e / p.tail_split;
@@ -113,7 +113,14 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   float* xs = reinterpret_cast<float*>(smem + xa_bytes(4 * QX, M));            // [QX*4][XSW]
   float* red = xs + QX * 4 * XSW;                                              // [NW][M][32]
   float* fin = red + NW * M * 32;                                              // [M][64]
-  float* topv = fin + M * 64;          // E_STORE_TOPK: [M][topk_tpw * 32] stored logits of this group
+  float* topv = fin + M * 64;          // E_STORE_TOPK: [M][topk_tpw * 32] stored logits of this workgroup's tiles
+  // E_STORE_TOPK: per wave, the key lists of a chunk's groups while merging:
+  // in the staged-x area (free once the tiles are done) when it is large
+  // enough, else past topv (the host sizes LDS the same way).
+  const bool stage_in_xa = xa_bytes(4 * QX, M) >= (size_t)NW * kTopkStageKeys * sizeof(uint64_t);
+  uint64_t* topk_stage = (stage_in_xa ? reinterpret_cast<uint64_t*>(smem)
+                                      : reinterpret_cast<uint64_t*>(topv + M * p.topk_tpw * 32)) +
+                         (size_t)wave * kTopkStageKeys;
   __shared__ float s_inv_rms[32];
   __shared__ int s_last;
 
@@ -124,9 +131,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   const uint16_t* Bi = which ? p.b1 : p.b0;
   const int sgroups = p.K >> (6 + GSH);
   const int qw = (q_n > kw) ? cdiv(q_n - kw, KS) : 0;
-  const int ntiles = kTopk ? min(p.topk_tpw, p.n_blocks - tile0)
-                           : (full ? cdiv(p.n_blocks - tile0, G)
-                                   : ((PK && p.tail_split > 1) ? 1 : cdiv(p.n_blocks - vb, G)));
+  const int ntiles = full ? cdiv(p.n_blocks - tile0, G) : ((PK && p.tail_split > 1) ? 1 : cdiv(p.n_blocks - vb, G));
   const int nitems = ntiles * qw;
 
   // A operands: lanes of rows >= M repeat row c32 % M (their output rows
@@ -347,26 +352,24 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
     }
   };
 
-  // E_STORE_TOPK, after the group's tiles: one wave per row writes the
-  // partial record of the group's ids; the chunk's last group to arrive
-  // merges the chunk's records into its chunk partial and resets the counter.
-  auto topk_finish = [&](int sub, int nsub, int Mr, int t) {
+  // E_STORE_TOPK, after the workgroup's tiles (vb, vb + grid, ...): one wave
+  // per row writes the partial record of their ids; the workgroups form
+  // kTopkParts consecutive sets of topk_wpg, and the last of a set to arrive
+  // merges the set's records into the row's partial record of that set.
+  auto topk_finish = [&](int nt, int Mr, int t) {
     lds_barrier();
-    const int span = p.topk_tpw * 32;               // ids per group (divides the 4096-id chunk)
-    const int id0 = sub * span;
-    const int spc = kChunk / span;                  // groups per chunk
-    const int chunk = sub / spc;
-    const int n_chunks = cdiv(p.N, kChunk);
-    ChunkPart* subs = reinterpret_cast<ChunkPart*>(p.topk_sub);
+    const int span = p.topk_tpw * 32;
+    const int set = vb / p.topk_wpg;
+    ChunkPart* recs = reinterpret_cast<ChunkPart*>(p.topk_sub);
     for (int m = wave; m < Mr; m += NW)
-      wave_sub_partial(topv + m * span, span, id0, p.N, p.topk_temp, p.topk_ksel, p.topk_greedy,
-                       subs + (size_t)m * nsub + sub);
+      wave_sub_partial(topv + m * span, nt * 32, vb * 32, vg * 32, p.N, p.topk_temp, p.topk_ksel, p.topk_greedy,
+                       recs + (size_t)m * vg + vb);
     __builtin_amdgcn_s_waitcnt(0);
     lds_barrier();
-    const int first = chunk * spc;
-    const int nsc = (nsub - first) < spc ? (nsub - first) : spc;
+    const int first = set * p.topk_wpg;
+    const int nsc = (vg - first) < p.topk_wpg ? (vg - first) : p.topk_wpg;
     if (t == 0) {
-      const unsigned old = __hip_atomic_fetch_add(p.topk_counters + chunk, 1u, __ATOMIC_RELAXED,
+      const unsigned old = __hip_atomic_fetch_add(p.topk_counters + set, 1u, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT);
       s_last = (old == (unsigned)(nsc - 1)) ? 1 : 0;
     }
@@ -374,9 +377,9 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
     if (!s_last) return;
     ChunkPart* parts = reinterpret_cast<ChunkPart*>(p.topk_parts);
     for (int m = wave; m < Mr; m += NW)
-      wave_merge_subs(subs + (size_t)m * nsub + first, nsc, p.topk_ksel, p.topk_greedy,
-                      parts + (size_t)m * n_chunks + chunk);
-    if (t == 0) __hip_atomic_store(p.topk_counters + chunk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      wave_merge_subs(recs + (size_t)m * vg + first, nsc, p.topk_ksel, p.topk_greedy,
+                      parts + (size_t)m * kTopkParts + set, topk_stage);
+    if (t == 0) __hip_atomic_store(p.topk_counters + set, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
 
   // Prologue: the norm statistics, x straight into LDS, the norm weights
@@ -431,7 +434,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   if (qw == 0) {
     for (int j = 0; j < ntiles; ++j) finish(j);
     arrive_all();
-    if constexpr (kTopk) topk_finish(vb, vg, M, tid);
+    if constexpr (kTopk) topk_finish(ntiles, M, tid);
     return;
   }
   // One exit, at the bottom: a break after each step would be merged by the
@@ -459,7 +462,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
     }
   } while (i < nitems);
   arrive_all();
-  if constexpr (kTopk) topk_finish(vb, vg, M, tid);
+  if constexpr (kTopk) topk_finish(ntiles, M, tid);
 }
 
 }  // namespace mtp

@@ -699,7 +699,7 @@ __device__ void accept_loop_wave(const RowLaw* tl, const RowLaw* dl, int b, int 
 // One workgroup per request, one wave per law (2K+1 of them, up to 16 waves,
 // each wave taking every nwv-th law), then the accept loop on wave 0.
 // Dynamic LDS: laws [2K+1] then candidate keys [nwv][kLawKeys].
-__global__ __launch_bounds__(1024) void accept_laws(const ChunkPart* __restrict__ tparts,
+__global__ __launch_bounds__(1024) void accept_laws(const ChunkPart* __restrict__ tparts, int t_chunks,
                                                     const ChunkPart* __restrict__ dparts, int n_chunks,
                                                     const int32_t* __restrict__ draft_ids,
                                                     const double* __restrict__ uniforms, int K, int ksel,
@@ -717,9 +717,9 @@ __global__ __launch_bounds__(1024) void accept_laws(const ChunkPart* __restrict_
   RowLaw* laws = reinterpret_cast<RowLaw*>(s_lds);   // sized for 2K + 1 laws
   uint64_t* keys = reinterpret_cast<uint64_t*>(s_lds + (size_t)(2 * K + 1) * sizeof(RowLaw)) + (size_t)wave * kLawKeys;
   for (int li = wave; li < nlaw; li += nwv) {
-    const ChunkPart* rp = li <= Kb ? tparts + ((size_t)tb + li) * n_chunks
+    const ChunkPart* rp = li <= Kb ? tparts + ((size_t)tb + li) * t_chunks
                                    : dparts + ((size_t)db + (li - Kb - 1)) * n_chunks;
-    build_law_wave(rp, n_chunks, ksel, greedy, temp, top_p, &laws[li], keys);
+    build_law_wave(rp, li <= Kb ? t_chunks : n_chunks, ksel, greedy, temp, top_p, &laws[li], keys);
   }
   __syncthreads();
   if (wave == 0) {   // the residual scratch reuses wave 0's key area
@@ -1260,13 +1260,14 @@ static int spec_accept_run(const float* target_logits, const float* draft_logits
                            const double* uniforms, int B, int K, int V, double temperature, int top_k, double top_p,
                            int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
                            size_t ws_bytes, void* stream, AcceptRows rr, int nt, int nd, const char* who,
-                           bool target_ready = false) {
+                           const void* target_parts = nullptr, int t_parts = 0) {
+  const bool target_ready = target_parts != nullptr;
   SamplerPlan pl;
   int rc = sampler_plan(V, top_k, temperature, &pl, who);
   if (rc) return rc;
-  if (target_ready && pl.wide) {
-    set_error("%s: precomputed target partials serve narrow laws only (temperature <= 0 or 1 <= top_k <= %d)", who,
-              kMaxTopK);
+  if (target_ready && (pl.wide || t_parts < 1 || t_parts > 64 || pl.n_chunks > 64)) {
+    set_error("%s: precomputed target records serve narrow laws (temperature <= 0 or 1 <= top_k <= %d) with 1..64 "
+              "records per row and V <= 64 * 4096", who, kMaxTopK);
     return MTP_ERR_UNSUPPORTED;
   }
   if (B < 1 || K < 1 || nt < B || nd < 0 || !target_logits || (nd > 0 && !draft_logits) || !draft_ids || !uniforms ||
@@ -1284,6 +1285,8 @@ static int spec_accept_run(const float* target_logits, const float* draft_logits
   const int n_chunks = pl.n_chunks;
   ChunkPart* tparts = reinterpret_cast<ChunkPart*>(ws);
   ChunkPart* dparts = tparts + (size_t)nt * n_chunks;
+  const int t_chunks = target_ready ? t_parts : n_chunks;
+  const ChunkPart* tread = target_ready ? reinterpret_cast<const ChunkPart*>(target_parts) : tparts;
   const double temp = pl.greedy ? 1.0 : temperature;
   rr.nt = nt;
   if (target_ready) {   // the target rows' partials are in ws already: the draft rows only
@@ -1318,7 +1321,8 @@ static int spec_accept_run(const float* target_logits, const float* draft_logits
     // A failure here surfaces as a launch error, checked below.
     if (lds > 65536) (void)hipFuncSetAttribute((const void*)accept_laws, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)lds);
-    hipLaunchKernelGGL(accept_laws, dim3(B), dim3(nwv * 64), lds, st, tparts, dparts, n_chunks, draft_ids, uniforms,
+    hipLaunchKernelGGL(accept_laws, dim3(B), dim3(nwv * 64), lds, st, tread, t_chunks, dparts, n_chunks, draft_ids,
+                       uniforms,
                        K, pl.ksel, pl.greedy, temp, top_p, out_tokens, n_accepted, accept_probs, status, rr);
   } else {
     hipLaunchKernelGGL(accept_finish, dim3(B), dim3(64), 0, st, tparts, dparts, n_chunks, draft_ids, uniforms, K,
@@ -1340,17 +1344,19 @@ MTP_API int mtp_spec_accept(const float* target_logits, const float* draft_logit
                          B * K, "mtp_spec_accept");
 }
 
-MTP_API int mtp_spec_accept_parts(const float* target_logits, const float* draft_logits, const int32_t* draft_ids,
-                                  const double* uniforms, int B, int K, int V, double temperature, int top_k,
-                                  double top_p, int32_t* out_tokens, int32_t* n_accepted, double* accept_probs,
-                                  int32_t* status, void* ws, size_t ws_bytes, void* stream) {
-  if (B < 1 || K < 1) {
-    set_error("mtp_spec_accept_parts: need B>=1, K>=1");
+MTP_API int mtp_spec_accept_parts(const void* target_parts, int n_parts, const float* draft_logits,
+                                  const int32_t* draft_ids, const double* uniforms, int B, int K, int V,
+                                  double temperature, int top_k, double top_p, int32_t* out_tokens,
+                                  int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
+                                  size_t ws_bytes, void* stream) {
+  if (B < 1 || K < 1 || !target_parts) {
+    set_error("mtp_spec_accept_parts: need B>=1, K>=1 and the target records");
     return MTP_ERR_ARG;
   }
-  return spec_accept_run(target_logits, draft_logits, draft_ids, uniforms, B, K, V, temperature, top_k, top_p,
+  // target_logits is not read on this path: the draft logits stand in as a valid pointer
+  return spec_accept_run(draft_logits, draft_logits, draft_ids, uniforms, B, K, V, temperature, top_k, top_p,
                          out_tokens, n_accepted, accept_probs, status, ws, ws_bytes, stream, AcceptRows{}, B * (K + 1),
-                         B * K, "mtp_spec_accept_parts", true);
+                         B * K, "mtp_spec_accept_parts", target_parts, n_parts);
 }
 
 MTP_API int mtp_spec_accept_ragged(const float* target_logits, int n_target, const float* draft_logits, int n_draft,

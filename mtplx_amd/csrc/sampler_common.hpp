@@ -15,6 +15,8 @@ constexpr int kSampThreads = 512;
 constexpr int kEPT = 8;                           // logits per thread per chunk
 constexpr int kChunk = kSampThreads * kEPT;       // 4096
 constexpr int kMaxTopK = 64;
+constexpr int kTopkStageKeys = 16 * kMaxTopK;   // a merging wave's LDS: up to 16 lists of kMaxTopK keys
+constexpr int kTopkParts = 64;                   // partial records per row from the fused lm_head
 
 struct ChunkPart {
   double m;             // max of l/T over the chunk (-inf if all -inf)
@@ -108,29 +110,41 @@ __device__ __forceinline__ double ld_f64_agent(const double* p) {
   return __longlong_as_double((long long)ld_u64_agent(reinterpret_cast<const uint64_t*>(p)));
 }
 
-// One wave: the partial record of n <= 512 values vals[0..n) held in LDS
-// (id of vals[i] = id0 + i; ids >= V are outside the vocabulary), stored to
-// out with agent-scope stores. The sampler's per-chunk arithmetic on fewer
-// values: fp64 l/T, the maximum, sum exp(l/T - max), the non-finite flag,
-// and the top-ksel keys by repeated wave maxima over cached per-lane bests.
-__device__ inline void wave_sub_partial(const float* vals, int n, int id0, int V, double temp, int ksel, int greedy,
-                                        ChunkPart* out) {
+// One wave: the partial record of n <= 1024 values vals[0..n) held in LDS,
+// in 32-value tiles: value i has id id0 + (i / 32) * tstride + i % 32 (ids
+// >= V are outside the vocabulary). Stored to out with agent-scope stores.
+// The sampler's per-chunk arithmetic on another set of ids: fp64 l/T, the
+// maximum, sum exp(l/T - max), the non-finite flag, and the top-ksel keys by
+// repeated wave maxima over cached per-lane bests.
+__device__ inline void wave_sub_partial(const float* vals, int n, int id0, int tstride, int V, double temp,
+                                        int ksel, int greedy, ChunkPart* out) {
+  constexpr int kPer = 16;
   const int lane = threadIdx.x & 63;
-  float v[8];
-  double qv[8];
-  uint64_t keys[8];
+  float v[kPer];
+  double qv[kPer];
+  uint64_t keys[kPer];
+  bool ok[kPer];
+  const int ne = (n + 63) >> 6;   // slots holding any value (wave-uniform): the rest are skipped
   int nonfinite = 0;
   double mloc = -INFINITY;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int i = e * 64 + lane;
-    const int id = id0 + i;
-    const bool valid = i < n && id < V;
-    v[e] = valid ? vals[i] : -INFINITY;
-    if (valid && (isnan(v[e]) || (isinf(v[e]) && v[e] > 0))) nonfinite = 1;
-    qv[e] = greedy ? 0.0 : (double)v[e] / temp;
-    if (!greedy) mloc = fmax(mloc, qv[e]);
-    keys[e] = (valid && !isnan(v[e])) ? make_key(v[e], id) : 0ull;
+  for (int e = 0; e < kPer; ++e) {
+    ok[e] = false;
+    keys[e] = 0ull;
+    qv[e] = -INFINITY;
+    if (e < ne) {
+      const int i = e * 64 + lane;
+      const int id = id0 + (i >> 5) * tstride + (i & 31);
+      const bool valid = i < n && id < V;
+      ok[e] = valid;
+      v[e] = valid ? vals[i] : -INFINITY;
+      if (valid && (isnan(v[e]) || (isinf(v[e]) && v[e] > 0))) nonfinite = 1;
+      if (!greedy) {
+        qv[e] = (double)v[e] / temp;
+        mloc = fmax(mloc, qv[e]);
+      }
+      keys[e] = (valid && !isnan(v[e])) ? make_key(v[e], id) : 0ull;
+    }
   }
   double m = -INFINITY, s = 0.0;
   if (!greedy) {
@@ -138,23 +152,23 @@ __device__ inline void wave_sub_partial(const float* vals, int n, int id0, int V
     double sl = 0.0;
     if (m > -INFINITY) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (e * 64 + lane < n && id0 + e * 64 + lane < V) sl += exp(qv[e] - m);
+      for (int e = 0; e < kPer; ++e)
+        if (e < ne && ok[e]) sl += exp(qv[e] - m);
     }
     s = wave_sum_f64(sl);
   }
   const int nf = __any(nonfinite) ? 1 : 0;
   uint64_t best = 0ull;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) best = keys[e] > best ? keys[e] : best;
+  for (int e = 0; e < kPer; ++e) best = keys[e] > best ? keys[e] : best;
   for (int r = 0; r < ksel; ++r) {
     const uint64_t win = wave_max_u64(best);
     if (lane == 0) st_u64_agent(&out->keys[r], win);
     if (win != 0ull && best == win) {
       uint64_t nb = 0ull;
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (keys[e] < win && keys[e] > nb) nb = keys[e];
+      for (int e = 0; e < kPer; ++e)
+        if (e < ne && keys[e] < win && keys[e] > nb) nb = keys[e];
       best = nb;
     }
   }
@@ -168,12 +182,28 @@ __device__ inline void wave_sub_partial(const float* vals, int n, int id0, int V
 // One wave: merge n <= 16 partial records subs[0..n) (agent-scope loads) of
 // consecutive id ranges into the record out: the maximum of the maxima, the
 // sum of s_i exp(m_i - m) in record order, the OR of the flags, and the
-// top-ksel keys by a k-way merge of the sorted lists (lanes 0..n-1 hold the
-// list heads; a 16-lane DPP maximum picks the winner).
-__device__ inline void wave_merge_subs(const ChunkPart* subs, int n, int ksel, int greedy, ChunkPart* out) {
+// top-ksel keys by a k-way merge of the sorted lists. The lists are first
+// copied into the wave's LDS area stage (n * ksel keys, all loads in flight
+// at once), so the merge rounds read LDS (lanes 0..n-1 hold the list heads;
+// a 16-lane DPP maximum picks the winner).
+__device__ inline void wave_merge_subs(const ChunkPart* subs, int n, int ksel, int greedy, ChunkPart* out,
+                                       uint64_t* stage) {
   const int lane = threadIdx.x & 63;
+  for (int i = lane; i < n * ksel; i += 64) {
+    const int l = i / ksel;
+    stage[i] = ld_u64_agent(&subs[l].keys[i - l * ksel]);
+  }
+  double mi = -INFINITY, si = 0.0;
+  int nfi = 0;
+  if (lane < n) {
+    mi = ld_f64_agent(&subs[lane].m);
+    si = ld_f64_agent(&subs[lane].s);
+    nfi = __hip_atomic_load(&subs[lane].nonfinite, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
   int ptr = 0;
-  uint64_t h = lane < n ? ld_u64_agent(&subs[lane].keys[0]) : 0ull;
+  uint64_t h = lane < n ? stage[lane * ksel] : 0ull;
   for (int r = 0; r < ksel; ++r) {
     uint64_t w = h;
     w = umax64(w, dpp64<kDppX1>(w));
@@ -184,22 +214,24 @@ __device__ inline void wave_merge_subs(const ChunkPart* subs, int n, int ksel, i
     if (lane == 0) out->keys[r] = win;
     if (lane < n && win != 0ull && h == win) {
       ++ptr;
-      h = ptr < ksel ? ld_u64_agent(&subs[lane].keys[ptr]) : 0ull;
+      h = ptr < ksel ? stage[lane * ksel + ptr] : 0ull;
+    }
+  }
+  // maxima, flags and sums in record order (lanes 0..n-1 hold record lane)
+  double m = -INFINITY;
+  int nf = 0;
+  for (int i = 0; i < n; ++i) {
+    m = fmax(m, rlf64(mi, i));
+    nf |= rli(nfi, i);
+  }
+  double s = 0.0;
+  if (!greedy && m > -INFINITY) {
+    for (int i = 0; i < n; ++i) {
+      const double mm = rlf64(mi, i);
+      if (mm > -INFINITY) s += rlf64(si, i) * exp(mm - m);
     }
   }
   if (lane == 0) {
-    double m = -INFINITY, s = 0.0;
-    int nf = 0;
-    for (int i = 0; i < n; ++i) {
-      m = fmax(m, ld_f64_agent(&subs[i].m));
-      nf |= __hip_atomic_load(&subs[i].nonfinite, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (!greedy && m > -INFINITY) {
-      for (int i = 0; i < n; ++i) {
-        const double mi = ld_f64_agent(&subs[i].m);
-        if (mi > -INFINITY) s += ld_f64_agent(&subs[i].s) * exp(mi - m);
-      }
-    }
     out->m = m;
     out->s = s;
     out->nonfinite = nf;

@@ -250,7 +250,7 @@ def sampler_workspace(B: int, K: int, V: int, config: SamplerConfig, device) -> 
 
 def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_ids: torch.Tensor,
                 uniforms: torch.Tensor, config: SamplerConfig, *, token_counts=None,
-                penalty_overlay=None, target_parts_ready: bool = False) -> AcceptResult:
+                penalty_overlay=None, target_parts: tuple | None = None) -> AcceptResult:
     """Depth-K accept/reject with residual correction for ``B`` requests.
 
     ``target_logits`` ``[B, K+1, V]`` (verify rows), ``draft_logits`` ``[B, K, V]``,
@@ -264,9 +264,10 @@ def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_i
     (per-position prefix counts). ``penalty_overlay[b]``: one mapping for all
     of request b's rows, or a list of K+1 (one per depth).
 
-    ``target_parts_ready``: the target rows' chunk partials are already in
-    :func:`sampler_workspace` (an emode-5 lm_head wrote them with this
-    config); only the draft rows are reduced. Narrow laws, no penalties.
+    ``target_parts``: ``(records, n_parts)`` of the target rows from an
+    emode-5 lm_head with this config (``target_logits`` is then only used
+    for its shape); only the draft rows are reduced. Narrow laws, no
+    penalties.
     """
     B, K1, V = (int(s) for s in target_logits.shape)
     K = K1 - 1
@@ -276,7 +277,7 @@ def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_i
     di = draft_ids.to(device=dev, dtype=torch.int32).contiguous()
     pen = penalties_active(config, token_counts if not isinstance(token_counts, (list, tuple)) else any(token_counts),
                            penalty_overlay if not isinstance(penalty_overlay, (list, tuple)) else any(penalty_overlay))
-    if target_parts_ready and (pen or not narrow_law(config, V)):
+    if target_parts is not None and (pen or not narrow_law(config, V)):
         raise ValueError("precomputed target partials need a narrow law (greedy or 1 <= top_k <= 64) and no penalties")
     if pen:
         base = token_counts if isinstance(token_counts, (list, tuple)) else [token_counts] * B
@@ -298,7 +299,8 @@ def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_i
     ap = torch.empty((B, K), dtype=torch.float64, device=dev)
     st = torch.empty(B, dtype=torch.int32, device=dev)
     ws = sampler_workspace(B, K, V, config, dev)
-    _lib.call("mtp_spec_accept_parts" if target_parts_ready else "mtp_spec_accept", t.data_ptr(), d.data_ptr(),
+    head = (target_parts[0].data_ptr(), int(target_parts[1])) if target_parts is not None else (t.data_ptr(),)
+    _lib.call("mtp_spec_accept_parts" if target_parts is not None else "mtp_spec_accept", *head, d.data_ptr(),
               di.data_ptr(), u.data_ptr(), B, K, V,
               float(config.temperature), int(config.top_k), float(config.top_p), out.data_ptr(), nacc.data_ptr(),
               ap.data_ptr(), st.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_handle(dev))

@@ -36,7 +36,7 @@ import torch
 from . import _lib
 from .moe_sorted_gather import expert_sort, moe_combine
 from .quant import QuantizedLinear, rope_row_order
-from .sampling import SamplerConfig, narrow_law, sampler_workspace, spec_accept
+from .sampling import SamplerConfig, narrow_law, spec_accept
 
 
 @dataclass
@@ -536,27 +536,31 @@ class VerifyModel:
         return spec_accept_ragged(logits, row_off[:-1], draft_logits, d_off, q_lens - 1, drafts, uniforms, sampler)
 
     def verify_step(self, tokens: torch.Tensor, q_start: torch.Tensor, draft_logits: torch.Tensor,
-                    uniforms: torch.Tensor, sampler: SamplerConfig = SamplerConfig(), *, fuse_topk: bool = True):
+                    uniforms: torch.Tensor, sampler: SamplerConfig = SamplerConfig(), *, fuse_topk: bool = False):
         """Forward the ``B x (K+1)`` verify rows, then accept/reject against the drafts
         (``tokens[:, 1:]`` are the draft ids). Returns the device-side accept result.
 
         With ``fuse_topk`` (and a narrow law, at most 8 rows) the lm_head
-        writes the target rows' chunk partials straight into the sampler's
-        workspace, so the accept step reduces only the draft rows."""
+        writes the target rows' partial records itself, so the accept step
+        reduces only the draft rows. Same tokens and probabilities either
+        way; off by default because it is slower on MI355X for the 27B shape
+        (lm_head + reductions 150 us fused against 130 us unfused: the fused
+        kernel holds more registers, 3 waves per SIMD instead of 4)."""
         B, L = (int(s) for s in tokens.shape)
         K = L - 1
         c = self.cfg
         topk = None
         if fuse_topk and B * L <= 8 and narrow_law(sampler, c.vocab):
-            sws = sampler_workspace(B, K, c.vocab, sampler, self.device)
+            parts = _lib.WORKSPACES.get(_lib.query("mtp_logits_topk_parts_bytes", B * L), "logits_topk_parts",
+                                        self.device)
             nb = _lib.query("mtp_logits_topk_workspace_bytes", B * L, c.vocab)
             tws = _lib.WORKSPACES.get(nb, "logits_topk", self.device)
-            topk = dict(parts=sws, ws=tws, ws_bytes=tws.numel(), temperature=float(sampler.temperature),
+            topk = dict(parts=parts, ws=tws, ws_bytes=tws.numel(), temperature=float(sampler.temperature),
                         top_k=int(sampler.top_k))
         logits = self.verify_logits(tokens, q_start, topk=topk)
         self.last_logits = logits
         return spec_accept(logits.reshape(B, L, -1), draft_logits, tokens[:, 1:].contiguous(), uniforms, sampler,
-                           target_parts_ready=topk is not None)
+                           target_parts=None if topk is None else (topk["parts"], topk["n_parts"]))
 
 
 class CapturedVerifyStep:

@@ -3,11 +3,13 @@ into its epilogue (emode 5) and of the accept step that consumes it
 (``mtp_spec_accept_parts``).
 
 Bars: the fused call's fp32 logits bit-exact against the plain lm_head's;
-its chunk partials against the accept step's own first pass over those
-logits (``mtp_sample_rows`` writes the same records): top-k keys, maxima
-and non-finite flags bit-exact, the fp64 sums within 1e-12 relative (another
-summation order); the verify step with and without the fusion token-exact,
-accept probabilities within 1e-12; arrival counters back at zero."""
+its partial records, merged over each row on the host, against the accept
+step's own chunk records over those logits (``mtp_sample_rows`` writes them),
+merged the same way: the top-k keys, the maximum and the non-finite flag
+bit-exact, the fp64 total sum(exp(l/T - max)) within 1e-12 relative
+(another summation order); no id in two records of a row; the verify step
+with and without the fusion token-exact, accept probabilities within 1e-12;
+arrival counters back at zero."""
 
 import numpy as np
 import pytest
@@ -22,24 +24,38 @@ def _st():
     return torch.cuda.current_stream().cuda_stream
 
 
-def _parts(ws: torch.Tensor, rows: int, n_chunks: int) -> np.ndarray:
-    b = ws[: rows * n_chunks * PART.itemsize].cpu().numpy()
-    return b.view(PART).reshape(rows, n_chunks)
+def _parts(buf: torch.Tensor, rows: int, per_row: int, used: int) -> np.ndarray:
+    b = buf[: rows * per_row * PART.itemsize].cpu().numpy()
+    return b.view(PART).reshape(rows, per_row)[:, :used]
+
+
+def _merge(recs: np.ndarray, ksel: int, greedy: bool):
+    """One row's records -> (top-ksel keys, max, total sum, flag); key 0 is
+    an empty slot (never a valid key: its id field would be 2^32-1)."""
+    keys = recs["keys"][:, :ksel].reshape(-1)
+    keys = np.sort(keys[keys != 0])[::-1][:ksel]
+    nf = int(recs["nf"].max())
+    if greedy:
+        return keys, None, None, nf
+    m = float(recs["m"].max())
+    tot = float(sum(r["s"] * np.exp(r["m"] - m) for r in recs if r["s"] > 0))
+    return keys, m, tot, nf
 
 
 def _fused(q, layout, x, M, V, K, temp, top_k):
     from mtplx_amd import _lib
-    n_chunks = (V + 4095) // 4096
-    nb = _lib.query("mtp_sampler_workspace_bytes", M, V, top_k)
-    sws = torch.zeros(nb, dtype=torch.uint8, device="cuda")
+    pb = _lib.query("mtp_logits_topk_parts_bytes", M)
+    parts = torch.zeros(pb, dtype=torch.uint8, device="cuda")
     tb = _lib.query("mtp_logits_topk_workspace_bytes", M, V)
     tws = torch.zeros(tb, dtype=torch.uint8, device="cuda")
     logits = torch.full((M, V), float("nan"), dtype=torch.float32, device="cuda")
     w = q.pack(layout=layout)
-    _lib.qmv_ex(_st(), x=x, w0=w, yf=logits, M=M, N=V, K=K, group_size=64, xmode=0, emode=5, packed=layout,
-                topk=dict(parts=sws, ws=tws, ws_bytes=tws.numel(), temperature=temp, top_k=top_k))
+    tk = dict(parts=parts, ws=tws, ws_bytes=tws.numel(), temperature=temp, top_k=top_k)
+    _lib.qmv_ex(_st(), x=x, w0=w, yf=logits, M=M, N=V, K=K, group_size=64, xmode=0, emode=5, packed=layout, topk=tk)
     torch.cuda.synchronize()
-    return logits, _parts(sws, M, n_chunks), tws
+    n = tk["n_parts"]
+    assert 1 <= n <= 64
+    return logits, _parts(parts, M, 64, n), tws
 
 
 def _reference_parts(logits, M, V, temp, top_k):
@@ -56,7 +72,7 @@ def _reference_parts(logits, M, V, temp, top_k):
     _lib.call("mtp_sample_rows", logits.data_ptr(), M, V, temp, top_k, 1.0, u.data_ptr(), ids.data_ptr(),
               probs.data_ptr(), 64, cnt.data_ptr(), smp.data_ptr(), st.data_ptr(), ws.data_ptr(), ws.numel(), _st())
     torch.cuda.synchronize()
-    return _parts(ws, M, n_chunks)
+    return _parts(ws, M, n_chunks, n_chunks)
 
 
 @pytest.mark.parametrize("M,layout,V,K,temp,top_k", [
@@ -81,13 +97,20 @@ def test_fused_partials_match_first_pass(gpu, M, layout, V, K, temp, top_k):
     torch.cuda.synchronize()
     assert torch.equal(logits.view(torch.int32), plain.view(torch.int32))
     want = _reference_parts(plain, M, V, temp, top_k)
-    ksel = 1 if temp <= 0 else top_k
-    assert np.array_equal(got["keys"][:, :, :ksel], want["keys"][:, :, :ksel])
-    assert np.array_equal(got["m"], want["m"]) and np.array_equal(got["nf"], want["nf"])
-    if temp > 0:
-        assert np.allclose(got["s"], want["s"], rtol=1e-12, atol=0)
-    # the arrival counters (the scratch's first 4 KiB) are back at zero
-    assert int(torch.count_nonzero(tws[:4096])) == 0
+    greedy = temp <= 0
+    ksel = 1 if greedy else top_k
+    for r in range(M):
+        gk, gm, gs, gnf = _merge(got[r], ksel, greedy)
+        wk, wm, ws, wnf = _merge(want[r], ksel, greedy)
+        assert np.array_equal(gk, wk) and gnf == wnf, f"row {r}"
+        if not greedy:
+            assert gm == wm and abs(gs - ws) <= 1e-12 * ws, f"row {r}"
+        # the records' id sets are disjoint: no id appears in two records
+        k = got[r]["keys"][:, :ksel].reshape(-1)
+        k = k[k != 0]
+        assert len(np.unique(k & 0xFFFFFFFF)) == len(k), f"row {r}: an id in two records"
+    # the arrival counters (the scratch's first 256 bytes) are back at zero
+    assert int(torch.count_nonzero(tws[:256])) == 0
 
 
 def test_fused_lm_head_refuses_wide_laws_and_many_rows(gpu):
