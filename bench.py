@@ -267,7 +267,18 @@ def _replay_us(graph, stream, rounds: int) -> float:
 
 
 def _matrix_bytes(*qs) -> int:
-    return sum(t.numel() * t.element_size() for q in qs if q is not None for t in (q.weight, q.scales, q.biases))
+    """MLX-layout bytes of the layers (the packed copies hold the same bytes;
+    a layer whose source was released is counted from its shape)."""
+    total = 0
+    for q in qs:
+        if q is None:
+            continue
+        lead = 1
+        for d in q._shape[:-2]:
+            lead *= d
+        n, k = q.out_features, q.in_features
+        total += lead * (n * k * q.bits // 8 + 2 * n * (k // q.group_size) * 2)
+    return total
 
 
 def _randn_bf16(n: int, gen, dev):
@@ -472,6 +483,10 @@ def cfg5_moe(steps: int = 5, warmup: int = 2, seed: int = 5) -> dict:
     torch.cuda.synchronize()
     model.check_status()
     distinct = [int(torch.unique(ids).numel()) for ids in model.route_log]
+    counts = [torch.bincount(ids.reshape(-1).long(), minlength=c.n_experts) for ids in model.route_log]
+    few = sum(int(((n > 0) & (n <= 4)).sum()) for n in counts) / len(counts)
+    many = sum(int((n > 4).sum()) for n in counts) / len(counts)
+    rows_many = sum(int(n[n > 4].sum()) for n in counts) / len(counts)
     model.route_log = None
     for _ in range(warmup):
         res = model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)
@@ -499,6 +514,8 @@ def cfg5_moe(steps: int = 5, warmup: int = 2, seed: int = 5) -> dict:
                         "router skew, eager launches",
             "rows": B * L, "ms_per_step": round(ms, 4), "verify_rows_per_s": round(B * L / s, 2),
             "distinct_experts_per_layer_mean": round(sum(distinct) / len(distinct), 2),
+            "experts_with_1_to_4_rows_mean": round(few, 2), "experts_with_5_plus_rows_mean": round(many, 2),
+            "rows_in_5_plus_experts_mean": round(rows_many, 2),
             "expert_bytes": expert_bytes, "bytes_per_step": total, "achieved_gbs": round(total / s / 1e9, 1),
             "frac_hbm": round(total / s / 1e9 / HBM_PEAK_GBS, 4)}
 

@@ -382,6 +382,20 @@ int mtp_gather_qmv_affine4(const void* x, const void* x2, const uint32_t* row_ma
                            int group_size, int xmode, int emode, int rows_per_expert, void* ws, size_t ws_bytes,
                            void* stream);
 
+/* The same gathered matmul over the tile-major pack (mtp_pack_affine4) of
+ * the [E * rows_per_expert, K] expert matrix, x plain (gathered through
+ * row_map when given): emode 0 = store y [R, N], 3 = silu(x@Wg^T)*(x@Wu^T)
+ * with expert e's N gate rows at e * rows_per_expert and its N up rows next.
+ * Each workgroup streams several column tiles of one expert behind one
+ * staging of its rows (the dense verify kernels' body); experts with at most
+ * 4 rows and those with more run as two launches. N and rows_per_expert
+ * multiples of 32, K of 256, group size 64 or 128. Replaces the same
+ * reference calls as mtp_gather_qmv_affine4 (mtplx/moe_sorted_gather.py:241,
+ * :288; mtplx/models/qwen4_exp.py:1544-1577). */
+int mtp_gather_qmv_affine4_packed(const void* x, const uint32_t* row_map, const int32_t* expert_off,
+                                  const int32_t* active, const void* wp, void* y, int max_rows_per_expert, int E,
+                                  int N, int K, int group_size, int emode, int rows_per_expert, void* stream);
+
 /* Expert offsets int32 [E+1] and the active list [1+E] (as mtp_moe_sort
  * writes them) from ids already sorted ascending, the sorted_indices of the
  * reference entry points (mtplx/moe_sorted_gather.py:241 gather_qmm_rows,

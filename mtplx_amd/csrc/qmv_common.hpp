@@ -217,7 +217,8 @@ __device__ __forceinline__ void stage_x_issue(const QmmParams& p, uint4* xa, int
       int qd = kq0 + (c >> 5);
       if (qd >= Q) qd -= Q;
       const int k = 256 * qd + 8 * (c & 31);
-      __builtin_amdgcn_global_load_lds((gptr_t)(p.x + (size_t)m * p.ldx + k),
+      const size_t xr = p.rowmap ? (size_t)p.rowmap[m] : (size_t)m;   // gathered rows (MoE)
+      __builtin_amdgcn_global_load_lds((gptr_t)(p.x + xr * p.ldx + k),
                                        (lptr_t)(xa + (size_t)m * rstride + blk * 64), 16, 0, 0);
     }
   }

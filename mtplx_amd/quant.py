@@ -26,6 +26,7 @@ class QuantizedLinear:
         self.bias = bias
         self.packed: torch.Tensor | None = None         # layout 1 (any M)
         self.packed_mf16: torch.Tensor | None = None    # layout 2 (M <= 4)
+        self._shape = tuple(int(d) for d in self.weight.shape)   # kept when the source is released
 
     def pack(self, row_order: torch.Tensor | None = None, layout: int = 1) -> torch.Tensor:
         """Tile-major copy of the weights for the streaming kernel. ``layout``
@@ -41,13 +42,23 @@ class QuantizedLinear:
             raise ValueError(f"layout {layout} (1 or 2)")
         from . import _lib
 
-        if self.weight.dim() != 2 or self.bits != 4 or self.mode != "affine":
-            raise NotImplementedError("packing covers 2-D 4-bit affine layers")
-        n, k = self.out_features, self.in_features
+        if self.weight is None:
+            raise RuntimeError("the layer's source weights were released; only its cached packs remain")
+        experts = self.weight.dim() == 3
+        if self.weight.dim() not in (2, 3) or self.bits != 4 or self.mode != "affine":
+            raise NotImplementedError("packing covers 2-D (or expert-stacked 3-D) 4-bit affine layers")
+        if experts and (layout != 1 or row_order is not None or self.out_features % 32):
+            raise NotImplementedError("expert stacks pack in layout 1 only, with N a multiple of 32")
+        # An expert stack [E, N, K/8] packs as the [E*N, K] matrix: with N a
+        # multiple of 32 no tile straddles two experts, so expert e's tiles
+        # start at tile e * N / 32.
+        n, k = self.out_features * (self._shape[0] if experts else 1), self.in_features
         nbytes = _lib.query("mtp_pack_affine4_bytes", n, k)
         if nbytes == 0:
             raise NotImplementedError(f"cannot pack N={n} K={k} (K must be a multiple of 256)")
         w, s, b = self.weight, self.scales, self.biases
+        if experts:
+            w, s, b = w.reshape(n, -1), s.reshape(n, -1), b.reshape(n, -1)
         if row_order is not None:
             idx = row_order.to(device=w.device, dtype=torch.long)
             if idx.numel() != n:
@@ -63,13 +74,21 @@ class QuantizedLinear:
                 self.packed_mf16 = out
         return out
 
+    def release_source(self) -> None:
+        """Free the MLX-layout triple once the packs the caller needs are
+        cached (an expert stack of a large MoE is held only in its packed
+        copy). Calls that need the triple raise afterwards."""
+        if self.packed is None and self.packed_mf16 is None:
+            raise RuntimeError("pack the layer before releasing its source weights")
+        self.weight = self.scales = self.biases = None
+
     @property
     def in_features(self) -> int:
-        return int(self.weight.shape[-1]) * 32 // self.bits
+        return self._shape[-1] * 32 // self.bits
 
     @property
     def out_features(self) -> int:
-        return int(self.weight.shape[-2])
+        return self._shape[-2]
 
     def __contains__(self, name: str) -> bool:   # MLX-style `"bias" in module`
         return getattr(self, name, None) is not None
@@ -77,6 +96,8 @@ class QuantizedLinear:
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         from .verify_kernels import quantized_matmul
 
+        if self.weight is None:
+            raise RuntimeError("the layer's source weights were released; call the packed kernels directly")
         y = quantized_matmul(x, self.weight, self.scales, self.biases, group_size=self.group_size, bits=self.bits,
                              mode=self.mode)
         if self.bias is not None:

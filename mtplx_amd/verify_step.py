@@ -139,8 +139,9 @@ def kv_from_blocks(blk: torch.Tensor, kind: str) -> torch.Tensor:
 class VerifyModel:
     """Random-init weights of ``cfg`` resident in HBM plus a ragged KV cache."""
 
-    def __init__(self, cfg: DecoderConfig, *, device="cuda", seed: int = 0):
+    def __init__(self, cfg: DecoderConfig, *, device="cuda", seed: int = 0, keep_expert_source: bool = False):
         self.cfg = cfg
+        self.keep_expert_source = keep_expert_source
         self.device = torch.device(device)
         gen = torch.Generator(device=self.device).manual_seed(seed)
         self.gen = gen
@@ -186,11 +187,12 @@ class VerifyModel:
 
     @classmethod
     def from_weights(cls, cfg: DecoderConfig, embed: QuantizedLinear, layers: list[Layer], final_norm: torch.Tensor,
-                     lm_head: QuantizedLinear, *, device="cuda") -> "VerifyModel":
+                     lm_head: QuantizedLinear, *, device="cuda", keep_expert_source: bool = False) -> "VerifyModel":
         """A model over given weights (e.g. an MLX pack read by
         :func:`mtplx_amd.mlx_pack.load_verify_model`) instead of random init."""
         self = cls.__new__(cls)
         self.cfg = cfg
+        self.keep_expert_source = keep_expert_source
         self.device = torch.device(device)
         self.gen = torch.Generator(device=self.device).manual_seed(0)
         self.embed = embed
@@ -213,6 +215,14 @@ class VerifyModel:
                     q.pack(layout=2)
             L.qkv_rope = L.qkv.pack(rope_order)
             L.qkv_rope2 = L.qkv.pack(rope_order, layout=2)
+            # Expert stacks: layout 1 only, and (unless asked to keep it) the
+            # MLX-layout source is freed, so a 125B-class MoE holds its
+            # experts once (2.7 GB per layer at the cfg5 shape).
+            for q in (L.expert_gate_up, L.expert_down):
+                if q is not None:
+                    q.pack()
+                    if not self.keep_expert_source:
+                        q.release_source()
         self.lm_head.pack()
         self.lm_head.pack(layout=2)
         self.k_cache: list[torch.Tensor] = []
@@ -426,19 +436,14 @@ class VerifyModel:
         R = M * c.top_k
         F = c.expert_ffn
         hsorted = torch.empty((R, F), dtype=torch.bfloat16, device=dev)
-        gu = L.expert_gate_up
-        kw = int(gu.weight.shape[-1])
-        gk = int(gu.scales.shape[-1])
-        call("mtp_gather_qmv_affine4", xn.data_ptr(), None, es.row_map.data_ptr(), es.expert_off.data_ptr(),
-             es.active.data_ptr(), gu.weight.data_ptr(), gu.scales.data_ptr(), gu.biases.data_ptr(),
-             gu.weight.reshape(-1, kw)[F:].data_ptr(), gu.scales.reshape(-1, gk)[F:].data_ptr(),
-             gu.biases.reshape(-1, gk)[F:].data_ptr(), hsorted.data_ptr(), M, c.n_experts, F, H, gs, 0, 3, 2 * F,
-             None, 0, st)
+        # Routed experts over their packed stacks: gate|up + SwiGLU on the
+        # token rows gathered by row_map, then down on the sorted rows.
+        call("mtp_gather_qmv_affine4_packed", xn.data_ptr(), es.row_map.data_ptr(), es.expert_off.data_ptr(),
+             es.active.data_ptr(), L.expert_gate_up.packed.data_ptr(), hsorted.data_ptr(), M, E, F, H, gs, 3,
+             2 * F, st)
         ysorted = torch.empty((R, H), dtype=torch.bfloat16, device=dev)
-        dn = L.expert_down
-        call("mtp_gather_qmv_affine4", hsorted.data_ptr(), None, None, es.expert_off.data_ptr(),
-             es.active.data_ptr(), dn.weight.data_ptr(), dn.scales.data_ptr(), dn.biases.data_ptr(), None, None,
-             None, ysorted.data_ptr(), M, c.n_experts, H, F, gs, 0, 0, H, None, 0, st)
+        call("mtp_gather_qmv_affine4_packed", hsorted.data_ptr(), None, es.expert_off.data_ptr(),
+             es.active.data_ptr(), L.expert_down.packed.data_ptr(), ysorted.data_ptr(), M, E, H, F, gs, 0, H, st)
         # Shared expert (SwiGLU MLP) on the normalised rows, then one combine:
         # h = h + bf16(routed + bf16(sigmoid(gate) * shared)).
         def W(q):

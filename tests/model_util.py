@@ -15,6 +15,8 @@ def _vals(t: torch.Tensor) -> np.ndarray:
 def _ql(q):
     if q is None:
         return None
+    if q.weight is None:
+        raise ValueError("the layer's source weights were released: build the model with keep_expert_source=True")
     return (q.weight.detach().contiguous().cpu().numpy().view(np.uint32), _bits(q.scales), _bits(q.biases))
 
 

@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 
 def _run(cfg, B, L, starts, seed, moe_tokens=None):
     from mtplx_amd.verify_step import VerifyModel
-    model = VerifyModel(cfg, device="cuda", seed=seed)
+    model = VerifyModel(cfg, device="cuda", seed=seed, keep_expert_source=True)
     model.allocate_cache(B, 320)
     kc = [model.k_cache_standard(li).float().cpu().numpy().astype(np.float64) for li in range(cfg.layers)]
     vc = [model.v_cache_standard(li).float().cpu().numpy().astype(np.float64) for li in range(cfg.layers)]

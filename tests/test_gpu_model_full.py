@@ -89,7 +89,7 @@ def test_cfg5_width_moe_layer_matches_oracle(gpu):
     from mtplx_amd.verify_step import MOE_125B, VerifyModel
     from dataclasses import replace
     cfg = replace(MOE_125B, layers=1)
-    model = VerifyModel(cfg, device="cuda", seed=23)
+    model = VerifyModel(cfg, device="cuda", seed=23, keep_expert_source=True)
     B, L, ctx = 4, 4, 8192
     model.allocate_cache(B, ctx)
     kc, vc = _caches(model, cfg.layers)

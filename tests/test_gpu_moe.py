@@ -178,3 +178,79 @@ def test_gather_qmm_contract(gpu):
         for j in range(k):
             want = OM.gather_qmm_rows(xb[t:t + 1], [0], [ind[t, j]], *w, 64)[0]
             assert_close(bf16_values(y[t, j, 0]), want, what="switch-glu form")
+
+
+def _within_one_ulp(a, b, what):
+    """|a - b| <= one bf16 ulp of b (plus 1e-4 of the row's scale where a sum
+    cancels): the packed path sums the same products with the 8 k of each
+    MFMA operand in another order."""
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(b), 1e-30))) - 7)
+    bad = np.abs(a - b) > ulp + 1e-4 * np.abs(b).max(axis=1, keepdims=True)
+    assert not bad.any(), f"{what}: {int(bad.sum())} of {bad.size} beyond one ulp"
+
+
+@pytest.mark.parametrize("T,k,E,H,F,gs,zipf", [
+    (16, 8, 64, 1024, 512, 64, 1.1),   # cfg5-like: hot experts with all 16 rows, a tail of 1..4
+    (40, 4, 16, 512, 256, 64, 2.0),    # experts past 16 rows (several 16-row tiles)
+    (3, 2, 8, 512, 256, 128, 0.0),     # group 128, one or two rows per expert
+])
+def test_packed_expert_matmul(gpu, T, k, E, H, F, gs, zipf):
+    """mtp_gather_qmv_affine4_packed (the verify step's routed experts) against
+    the oracle's sorted chain (bf16 bar) and within one bf16 ulp of the
+    MLX-layout gather, for experts of every row class."""
+    from mtplx_amd import _lib
+    from mtplx_amd.moe_sorted_gather import expert_sort
+    from mtplx_amd.quant import QuantizedLinear
+    rng = np.random.default_rng(T * 100 + E)
+    gu = make_affine4_weights(rng, E * 2 * F, H, gs)
+    gu = tuple(a.reshape(E, 2 * F, -1) for a in gu)
+    dn = make_affine4_weights(rng, E * H, F, gs)
+    dn = tuple(a.reshape(E, H, -1) for a in dn)
+    x = randn_bf16(rng, (T, H))
+    p = np.exp(-zipf * np.log(np.arange(1, E + 1)))
+    p /= p.sum()
+    idx = np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)]).astype(np.int32)
+    es = expert_sort(torch.from_numpy(idx).cuda(), E)
+    counts = np.bincount(idx.reshape(-1), minlength=E)
+    qgu = QuantizedLinear(u32(gu[0]), from_bits(gu[1]), from_bits(gu[2]), group_size=gs)
+    qdn = QuantizedLinear(u32(dn[0]), from_bits(dn[1]), from_bits(dn[2]), group_size=gs)
+    st = torch.cuda.current_stream().cuda_stream
+    R = T * k
+    h = torch.full((R, F), float("nan"), dtype=torch.bfloat16, device="cuda")
+    _lib.call("mtp_gather_qmv_affine4_packed", x.data_ptr(), es.row_map.data_ptr(), es.expert_off.data_ptr(),
+              es.active.data_ptr(), qgu.pack().data_ptr(), h.data_ptr(), T, E, F, H, gs, 3, 2 * F, st)
+    y = torch.full((R, H), float("nan"), dtype=torch.bfloat16, device="cuda")
+    _lib.call("mtp_gather_qmv_affine4_packed", h.data_ptr(), None, es.expert_off.data_ptr(), es.active.data_ptr(),
+              qdn.pack().data_ptr(), y.data_ptr(), T, E, H, F, gs, 0, H, st)
+    # the MLX-layout gather on the same inputs
+    kw, gk = H // 8, H // gs
+    h0 = torch.full((R, F), float("nan"), dtype=torch.bfloat16, device="cuda")
+    _lib.call("mtp_gather_qmv_affine4", x.data_ptr(), None, es.row_map.data_ptr(), es.expert_off.data_ptr(),
+              es.active.data_ptr(), qgu.weight.data_ptr(), qgu.scales.data_ptr(), qgu.biases.data_ptr(),
+              qgu.weight.reshape(-1, kw)[F:].data_ptr(), qgu.scales.reshape(-1, gk)[F:].data_ptr(),
+              qgu.biases.reshape(-1, gk)[F:].data_ptr(), h0.data_ptr(), T, E, F, H, gs, 0, 3, 2 * F, None, 0, st)
+    y0 = torch.full((R, H), float("nan"), dtype=torch.bfloat16, device="cuda")
+    _lib.call("mtp_gather_qmv_affine4", h.data_ptr(), None, None, es.expert_off.data_ptr(), es.active.data_ptr(),
+              qdn.weight.data_ptr(), qdn.scales.data_ptr(), qdn.biases.data_ptr(), None, None, None, y0.data_ptr(),
+              T, E, H, F, gs, 0, 0, H, None, 0, st)
+    torch.cuda.synchronize()
+    assert counts.max() > (16 if T > 16 else 4) or zipf == 0.0   # the case reaches the row class it is for
+    row_map, sorted_ids, _, _ = OM.sort_rows(idx)
+    want_h = OM.swiglu_rows(bits(x), row_map, sorted_ids, *gu, gs, bf16_storage=True)
+    hv = bf16_values(h)
+    assert_close(hv, want_h, what=f"packed gate|up + SwiGLU T={T} E={E}")
+    _within_one_ulp(hv, bf16_values(h0), "packed vs MLX-layout gate|up")
+    want_y = OM.gather_qmm_rows(bits(h), np.arange(R), sorted_ids, *dn, gs)
+    yv = bf16_values(y)
+    assert_close(yv, want_y, what=f"packed down T={T} E={E}")
+    _within_one_ulp(yv, bf16_values(y0), "packed vs MLX-layout down")
+
+
+def test_packed_expert_matmul_refuses_bad_shapes(gpu):
+    from mtplx_amd import _lib
+    z = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    for N, K, rpe, em in ((48, 512, 48, 0), (64, 500, 64, 0), (64, 512, 64, 3), (64, 512, 64, 1)):
+        with pytest.raises(_lib.MtpError):
+            _lib.call("mtp_gather_qmv_affine4_packed", z.data_ptr(), None, z.data_ptr(), z.data_ptr(), z.data_ptr(),
+                      z.data_ptr(), 4, 2, N, K, 64, em, rpe, st)
