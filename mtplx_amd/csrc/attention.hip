@@ -186,9 +186,10 @@ __global__ __launch_bounds__(kVtWaves * 64) void attn_vt_kernel(AttnParams p) {
   attn_vt_body<TPW, false>(p, (int)blockIdx.x, lds);
 }
 
+template <int NRG>
 __global__ __launch_bounds__(kVtWaves * 64) void attn_vl_kernel(AttnParams p) {
   __shared__ __align__(16) unsigned char lds[attn_vt_lds_bytes()];
-  attn_vl_body<false>(p, (int)blockIdx.x, lds);
+  attn_vl_body<false, NRG>(p, (int)blockIdx.x, lds);
 }
 
 // Keys per work unit of the block-layout entry point: about 1024 units over
@@ -199,6 +200,8 @@ static int attn_blocks_plan(int Hkv, int cap, long long total_cap, int req, int*
   int sk = req;
   if (sk <= 0) {
     const long long work = total_cap * Hkv;
+    // 1024 units: 512-1024 measured within 2% on cfg2 and cfg4; 2048 and
+    // more slower (per-unit partials and ramp), 256 slower on cfg2.
     sk = (int)((work + 1023) / 1024);
     if (sk < 128) sk = 128;
     if (sk > 4096) sk = 4096;
@@ -532,7 +535,9 @@ MTP_API int mtp_ragged_gqa_attn_blocks(const mtp_attn_blocks_args* a, void* stre
   const size_t units = (size_t)a->B * a->Hkv * p.S;
   p.part_o = (float*)a->ws;
   p.part_ml = (float*)a->ws + units * 32 * kHD;
-  hipLaunchKernelGGL(attn_vl_kernel, dim3((unsigned)units), dim3(kVtWaves * 64), 0, (hipStream_t)stream, p);
+  // Two ring slots: three and four measured slower on cfg2 (122 and 129 us
+  // against 119 us per launch) and cfg4.
+  hipLaunchKernelGGL(attn_vl_kernel<2>, dim3((unsigned)units), dim3(kVtWaves * 64), 0, (hipStream_t)stream, p);
   int rc = launch_check(who);
   if (rc) return rc;
   hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(a->B * a->Hkv * (a->Hq / a->Hkv) * a->Lmax)),

@@ -292,7 +292,7 @@ __device__ __forceinline__ void attn_vt_body(const AttnParams& p, const int unit
 // next tile's K and V^T operands in flight while this one is computed), then
 // merge in LDS in wave order as attn_vt_body does. split_keys is a multiple
 // of 128, so long contexts need few splits and few partials.
-template <bool WT>
+template <bool WT, int NRG = 2>
 __device__ __forceinline__ void attn_vl_body(const AttnParams& p, const int unit, unsigned char* lds) {
   constexpr int kOS = kVtOS;
   float* s_o = reinterpret_cast<float*>(lds);   // [kVtWaves][32 * kOS]
@@ -348,9 +348,10 @@ __device__ __forceinline__ void attn_vl_body(const AttnParams& p, const int unit
   const size_t hb = req_head_block(p, b, h) * 4096;
   const uint16_t* kbase = p.k + hb;
   const uint16_t* vbase = p.v + hb;
-  // Tiles at or past k1 reload this wave's first block (valid memory, never used).
+  // Tiles at or past k1 reload this wave's last block (valid memory, still in
+  // L2 from the wave's own load of it; never used).
   auto load_tile = [&](uint4 (&kr)[8], uint4 (&vr)[8], int kt) {
-    const size_t blk = (size_t)((kt < k1 ? kt : k0) >> 5) * 4096 + (size_t)lane * 8;
+    const size_t blk = (size_t)((kt < k1 ? kt : k1 - 1) >> 5) * 4096 + (size_t)lane * 8;
 #pragma unroll
     for (int i = 0; i < 8; ++i) kr[i] = *reinterpret_cast<const uint4*>(kbase + blk + i * 512);
 #pragma unroll
@@ -423,18 +424,20 @@ __device__ __forceinline__ void attn_vl_body(const AttnParams& p, const int unit
                                                         0, 0);
   };
   if (k0 < k1) {
-    uint4 ka[8], va[8], kb[8], vb[8];
-    load_tile(ka, va, k0);
-    load_tile(kb, vb, k0 + kTileKeys);
+    // NRG-deep register ring of K and V^T tiles (slot i holds tile kt + 32 i).
+    uint4 kr[NRG][8], vr[NRG][8];
+#pragma unroll
+    for (int i = 0; i < NRG; ++i) load_tile(kr[i], vr[i], k0 + i * kTileKeys);
     int kt = k0;
-    do {   // one exit, at the bottom; the second step is skipped by a uniform branch
-      tile(ka, va, kt);
-      load_tile(ka, va, kt + 2 * kTileKeys);
-      if (kt + kTileKeys < k1) {
-        tile(kb, vb, kt + kTileKeys);
-        load_tile(kb, vb, kt + 3 * kTileKeys);
+    do {   // one exit, at the bottom; steps past the end are skipped by uniform branches
+#pragma unroll
+      for (int i = 0; i < NRG; ++i) {
+        if (i == 0 || kt + i * kTileKeys < k1) {
+          tile(kr[i], vr[i], kt + i * kTileKeys);
+          load_tile(kr[i], vr[i], kt + (i + NRG) * kTileKeys);
+        }
       }
-      kt += 2 * kTileKeys;
+      kt += NRG * kTileKeys;
     } while (kt < k1);
   }
 
