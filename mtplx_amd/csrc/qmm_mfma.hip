@@ -68,25 +68,36 @@ __device__ __forceinline__ void qm_stage(const QmmRowsParams& p, unsigned char* 
 
 static bool rows_aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
+static int env_int_rows(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return (v && *v) ? atoi(v) : dflt;
+}
+
 struct QmQuad {
   uint4 w[4];
   uint4 sb;
 };
 
-template <int R2, int EM>
-__global__ __launch_bounds__(kQmThreads) void qmm_rows_kernel(QmmRowsParams p) {
+// KH = 2: 8-wave workgroups whose two 4-wave halves take the two halves of
+// the unit's quads in the same steps (both quads staged behind the same
+// barriers), then add their sums in LDS in half order; two waves per SIMD
+// instead of one, with the same grid.
+template <int R2, int EM, int KH>
+__global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams p) {
   constexpr bool dual = EM == E_DUAL_SWIGLU;
   constexpr int ROWS = 32 * R2;
   constexpr int XBUF = ROWS * kQmSlotsPerRow * 16;   // bytes of one staged quad
-  // Dynamic LDS: two staged x quads, then their group sums [2][4][ROWS].
+  // Dynamic LDS: staged x quads [2][KH], then their group sums [2][KH][4][ROWS].
   extern __shared__ __align__(16) unsigned char qm_lds[];
-  unsigned char* xbuf[2] = {qm_lds, qm_lds + XBUF};
-  float (*xs)[4][ROWS] = reinterpret_cast<float (*)[4][ROWS]>(qm_lds + 2 * XBUF);
+  auto xbuf = [&](int b, int h) { return qm_lds + (size_t)(b * KH + h) * XBUF; };
+  float (*xs)[KH][4][ROWS] = reinterpret_cast<float (*)[KH][4][ROWS]>(qm_lds + 2 * KH * XBUF);
   __shared__ int s_last;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kh = wave / kQmWaves;   // K half of this wave
+  const int wt = wave % kQmWaves;   // the wave's tile slot in the group
   const int c32 = lane & 31, kq = lane >> 5;
   const int M = p.M, Q = p.Q;
 
@@ -102,9 +113,14 @@ __global__ __launch_bounds__(kQmThreads) void qmm_rows_kernel(QmmRowsParams p) {
     q_lo = (part * Q) / p.split;
     q_n = ((part + 1) * Q) / p.split - q_lo;
   }
+  // This half's quads [h_lo, h_lo + h_n); the steps run over the first half's count.
+  const int h0 = KH == 2 ? (q_n + 1) >> 1 : q_n;
+  const int h_lo = q_lo + (kh ? h0 : 0);
+  const int h_n = kh ? q_n - h0 : h0;
+  const int steps = h0;
   // This wave's tile (column tile ct of matrix mat).
-  const int ct = dual ? 2 * g + (wave & 1) : 4 * g + wave;
-  const int mat = dual ? (wave >> 1) : 0;
+  const int ct = dual ? 2 * g + (wt & 1) : 4 * g + wt;
+  const int mat = dual ? (wt >> 1) : 0;
   const bool has_tile = ct < p.ntiles;
   const uint32_t* W = (mat ? p.w1 : p.w0) + (size_t)(has_tile ? ct : 0) * Q * kPackQuadWords;
   const uint32_t* wl = W + lane * 4;
@@ -112,7 +128,8 @@ __global__ __launch_bounds__(kQmThreads) void qmm_rows_kernel(QmmRowsParams p) {
   const NibConsts nc = nib_consts();
 
   auto load_quad = [&](QmQuad& r, int c) {
-    const int q = q_lo + (c < q_n ? c : q_n - 1);   // past the end: a valid block, never used
+    // past the half's end (or an empty half): a valid block, never used
+    const int q = h_n > 0 ? h_lo + (c < h_n ? c : h_n - 1) : q_lo;
     const size_t off = (size_t)q * kPackQuadWords;
 #pragma unroll
     for (int u = 0; u < 4; ++u) r.w[u] = *reinterpret_cast<const uint4*>(wl + off + 256 * u);
@@ -138,7 +155,7 @@ __global__ __launch_bounds__(kQmThreads) void qmm_rows_kernel(QmmRowsParams p) {
     float sv[4], cb[4];
     const uint32_t sw[2] = {r.sb.x, r.sb.y}, bw[2] = {r.sb.z, r.sb.w};
     quad_scales<0>(sw, bw, sv, cb);   // the pack stores scales per 64-group for either group size
-    const unsigned char* xb = xbuf[buf];
+    const unsigned char* xb = xbuf(buf, kh);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const uint32_t wv[4] = {r.w[u].x, r.w[u].y, r.w[u].z, r.w[u].w};
@@ -161,7 +178,7 @@ __global__ __launch_bounds__(kQmThreads) void qmm_rows_kernel(QmmRowsParams p) {
       for (int r2 = 0; r2 < R2; ++r2) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float4 xv = *reinterpret_cast<const float4*>(&xs[buf][u][32 * r2 + 8 * j + 4 * kq]);
+          const float4 xv = *reinterpret_cast<const float4*>(&xs[buf][kh][u][32 * r2 + 8 * j + 4 * kq]);
           const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -173,49 +190,73 @@ __global__ __launch_bounds__(kQmThreads) void qmm_rows_kernel(QmmRowsParams p) {
     }
   };
 
-  // Group sums of staged quad `buf`: thread t < 4M sums row t % M, group t / M.
-  auto group_sums = [&](int buf) {
+  // Group sums of staged quad `buf` of each half: thread t < 4M of half h
+  // sums row t % M, group t / M.
+  auto group_sums = [&](int buf, int c) {
     typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     const bf16x2_t one2 = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
-    for (int t = tid; t < 4 * M; t += kQmThreads) {
+    const int h = tid / kQmThreads;
+    if (c >= (h ? q_n - h0 : h0)) return;   // this half has no quad c
+    for (int t = tid - h * kQmThreads; t < 4 * M; t += kQmThreads) {
       const int u = t / M, m = t - u * M;
       float s = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const uint4 c = *reinterpret_cast<const uint4*>(xbuf[buf] + 16 * xslot(m, 8 * u + j));
-        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, c.x), one2, s, false);
-        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, c.y), one2, s, false);
-        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, c.z), one2, s, false);
-        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, c.w), one2, s, false);
+        const uint4 cc = *reinterpret_cast<const uint4*>(xbuf(buf, h) + 16 * xslot(m, 8 * u + j));
+        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, cc.x), one2, s, false);
+        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, cc.y), one2, s, false);
+        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, cc.z), one2, s, false);
+        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, cc.w), one2, s, false);
       }
-      xs[buf][u][m] = s;
+      xs[buf][h][u][m] = s;
     }
   };
 
-  // Prologue: quad 0 of x, then the first two weight quads.
+  // Prologue: each half's quad 0 of x, then its first two weight quads.
   QmQuad ring0, ring1;
-  qm_stage(p, xbuf[0], q_lo, wave, lane);
+  if (h_n > 0) qm_stage(p, xbuf(0, kh), h_lo, wt, lane);
   load_quad(ring0, 0);
   load_quad(ring1, 1);
-  // One step: quad c from ring slot `cur` and x buffer c & 1; refills `cur`
-  // with quad c + 2. At the wait only the newest ring slot (5 loads) may be
-  // outstanding: quad c's x and weights have landed.
+  // One step: quad c of each half from ring slot `cur` and x buffer c & 1;
+  // refills `cur` with quad c + 2. At the wait only the newest ring slot (5
+  // loads) may be outstanding: this wave's x loads of quad c and its weights
+  // have landed.
   auto step = [&](QmQuad& cur, int c) {
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(5));
     lds_barrier();   // every wave's x loads of quad c are in LDS
-    group_sums(c & 1);
-    if (c + 1 < q_n) qm_stage(p, xbuf[(c + 1) & 1], q_lo + c + 1, wave, lane);
+    group_sums(c & 1, c);
+    if (c + 1 < h_n) qm_stage(p, xbuf((c + 1) & 1, kh), h_lo + c + 1, wt, lane);
     lds_barrier();   // group sums visible; buffer (c+1)&1 was last read before the first barrier
-    compute(cur, c & 1);
+    if (c < h_n) compute(cur, c & 1);
     load_quad(cur, c + 2);
   };
   int c = 0;
   do {
     step(ring0, c);
-    if (c + 1 < q_n) step(ring1, c + 1);
+    if (c + 1 < steps) step(ring1, c + 1);
     c += 2;
-  } while (c < q_n);
+  } while (c < steps);
   __builtin_amdgcn_s_waitcnt(0);
+
+  if constexpr (KH == 2) {
+    // The second half's sums join the first half's, in half order.
+    float* red = reinterpret_cast<float*>(qm_lds);   // [4 tile waves][R2*16][64]
+    __syncthreads();   // every wave is done with the staged x
+    if (kh == 1) {
+#pragma unroll
+      for (int r2 = 0; r2 < R2; ++r2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[(wt * R2 * 16 + r2 * 16 + r) * 64 + lane] = acc[r2][r];
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+      for (int r2 = 0; r2 < R2; ++r2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r2][r] += red[(wt * R2 * 16 + r2 * 16 + r) * 64 + lane];
+    }
+  }
+  const bool owner = kh == 0;   // the waves that hold the finished sums
 
   // Output element of acc[r2][r]: row 32 r2 + 8 (r / 4) + 4 kq + r % 4,
   // column 32 ct + c32.
@@ -225,12 +266,15 @@ __global__ __launch_bounds__(kQmThreads) void qmm_rows_kernel(QmmRowsParams p) {
     // This part's sums, device-coherent, in register order; the last part to
     // arrive adds the parts in part order.
     const int eg = g - p.full_groups;
-    float* mine = p.partial + (((size_t)eg * p.split + part) * kQmWaves + wave) * (R2 * 16 * 64);
+    float* mine = p.partial + (((size_t)eg * p.split + part) * kQmWaves + wt) * (R2 * 16 * 64);
+    if (owner) {
 #pragma unroll
-    for (int r2 = 0; r2 < R2; ++r2)
+      for (int r2 = 0; r2 < R2; ++r2)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        __hip_atomic_store(mine + (r2 * 16 + r) * 64 + lane, acc[r2][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int r = 0; r < 16; ++r)
+          __hip_atomic_store(mine + (r2 * 16 + r) * 64 + lane, acc[r2][r], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
@@ -239,22 +283,24 @@ __global__ __launch_bounds__(kQmThreads) void qmm_rows_kernel(QmmRowsParams p) {
     }
     __syncthreads();
     if (!s_last) return;
-#pragma unroll
-    for (int r2 = 0; r2 < R2; ++r2)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r2][r] = 0.f;
-    for (int pp = 0; pp < p.split; ++pp) {
-      const float* src = p.partial + (((size_t)eg * p.split + pp) * kQmWaves + wave) * (R2 * 16 * 64);
-      float v[R2][16];
+    if (owner) {
 #pragma unroll
       for (int r2 = 0; r2 < R2; ++r2)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          v[r2][r] = __hip_atomic_load(src + (r2 * 16 + r) * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int r = 0; r < 16; ++r) acc[r2][r] = 0.f;
+      for (int pp = 0; pp < p.split; ++pp) {
+        const float* src = p.partial + (((size_t)eg * p.split + pp) * kQmWaves + wt) * (R2 * 16 * 64);
+        float v[R2][16];
 #pragma unroll
-      for (int r2 = 0; r2 < R2; ++r2)
+        for (int r2 = 0; r2 < R2; ++r2)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r2][r] += v[r2][r];
+          for (int r = 0; r < 16; ++r)
+            v[r2][r] = __hip_atomic_load(src + (r2 * 16 + r) * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int r2 = 0; r2 < R2; ++r2)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[r2][r] += v[r2][r];
+      }
     }
     if (tid == 0) __hip_atomic_store(p.counters + eg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -262,23 +308,23 @@ __global__ __launch_bounds__(kQmThreads) void qmm_rows_kernel(QmmRowsParams p) {
   const int col = 32 * ct + c32;
   if constexpr (dual) {
     // The up waves hand their sums to the gate waves of the same columns.
-    float* ex = reinterpret_cast<float*>(xbuf[0]);   // [2 column tiles][R2*16][64]
+    float* ex = reinterpret_cast<float*>(qm_lds);   // [2 column tiles][R2*16][64]
     __syncthreads();
-    if (mat == 1) {
+    if (owner && mat == 1) {
 #pragma unroll
       for (int r2 = 0; r2 < R2; ++r2)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ex[((wave & 1) * R2 * 16 + r2 * 16 + r) * 64 + lane] = acc[r2][r];
+        for (int r = 0; r < 16; ++r) ex[((wt & 1) * R2 * 16 + r2 * 16 + r) * 64 + lane] = acc[r2][r];
     }
     __syncthreads();
-    if (mat == 0 && has_tile && col < p.N) {
+    if (owner && mat == 0 && has_tile && col < p.N) {
 #pragma unroll
       for (int r2 = 0; r2 < R2; ++r2)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int m = row_of(r2, r);
           if (m < M) {
-            const float up = ex[((wave & 1) * R2 * 16 + r2 * 16 + r) * 64 + lane];
+            const float up = ex[((wt & 1) * R2 * 16 + r2 * 16 + r) * 64 + lane];
             const float gsl = round_bf(silu_f(round_bf(acc[r2][r])));
             p.y[(size_t)m * p.ldy + col] = f2bf(gsl * round_bf(up));
           }
@@ -286,7 +332,7 @@ __global__ __launch_bounds__(kQmThreads) void qmm_rows_kernel(QmmRowsParams p) {
     }
     return;
   }
-  if (!has_tile || col >= p.N) return;
+  if (!owner || !has_tile || col >= p.N) return;
 #pragma unroll
   for (int r2 = 0; r2 < R2; ++r2)
 #pragma unroll
@@ -304,9 +350,11 @@ __global__ __launch_bounds__(kQmThreads) void qmm_rows_kernel(QmmRowsParams p) {
     }
 }
 
-static size_t rows_lds_bytes(int R2) {
+static size_t rows_lds_bytes(int R2, int KH) {
   const size_t xbuf = (size_t)32 * R2 * kQmSlotsPerRow * 16;
-  return 2 * xbuf + (size_t)2 * 4 * 32 * R2 * sizeof(float);
+  const size_t stage = 2 * KH * xbuf + (size_t)2 * KH * 4 * 32 * R2 * sizeof(float);
+  const size_t red = (size_t)kQmWaves * R2 * 16 * 64 * sizeof(float);   // the halves' reduction / the pair's exchange
+  return stage > red ? stage : red;
 }
 
 struct RowsPlan {
@@ -420,13 +468,27 @@ MTP_API int mtp_qmm_affine4_mfma(const mtp_qmm_args* a, void* stream) {
   // (the pack repeats a group-128 scale over its two 64-groups, so the kernel
   // is the same for both group sizes). A failure of the attribute call
   // surfaces as a launch error, checked below.
+  // Two K halves per workgroup (8 waves, one workgroup per CU by LDS at 64
+  // rows) when the grid fits on the CUs at once (q|k|v, o, down at cfg4:
+  // 20.8 -> 20.3, 27.6 -> 26.8, 41.1 -> 36.4 us); one (4 waves, two
+  // workgroups per CU) when it does not (gate|up 51 vs 57 us, lm_head 168
+  // vs 193 us with two halves).
+  const int kh_env = env_int_rows("MTPLX_AMD_QMM_HALVES", 0);
+  const int kh = kh_env == 1 || kh_env == 2 ? kh_env : (grid <= device_cus() ? 2 : 1);
 #define MTP_ROWS(R2v, EMv)                                                                                \
   do {                                                                                                    \
-    const size_t lds = rows_lds_bytes(R2v);                                                               \
-    auto k = qmm_rows_kernel<R2v, EMv>;                                                                   \
-    if (lds > 65536) (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, \
-                                               (int)lds);                                                 \
-    hipLaunchKernelGGL(k, dim3(grid), dim3(kQmThreads), lds, st, p);                                      \
+    const size_t lds = rows_lds_bytes(R2v, kh);                                                           \
+    if (kh == 2) {                                                                                        \
+      auto k = qmm_rows_kernel<R2v, EMv, 2>;                                                              \
+      if (lds > 65536) (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                                 (int)lds);                                               \
+      hipLaunchKernelGGL(k, dim3(grid), dim3(2 * kQmThreads), lds, st, p);                                \
+    } else {                                                                                              \
+      auto k = qmm_rows_kernel<R2v, EMv, 1>;                                                              \
+      if (lds > 65536) (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                                 (int)lds);                                               \
+      hipLaunchKernelGGL(k, dim3(grid), dim3(kQmThreads), lds, st, p);                                    \
+    }                                                                                                     \
   } while (0)
   if (M > 32) {
     if (em == E_STORE) MTP_ROWS(2, E_STORE); else if (em == E_RESID) MTP_ROWS(2, E_RESID); else MTP_ROWS(2, E_DUAL_SWIGLU);

@@ -33,3 +33,27 @@ def assert_close(got: np.ndarray, want: np.ndarray, rtol=1e-2, atol=1e-2, what="
         idx = np.argwhere(bad)[:5]
         raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outside rtol={rtol} atol={atol}; "
                              f"first {idx.tolist()} got {got[tuple(idx[0])]} want {want[tuple(idx[0])]}")
+
+
+def bf16_ulp(v: np.ndarray) -> np.ndarray:
+    """One bf16 ulp at |v| (8 significant bits)."""
+    return np.exp2(np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -126))) - 7)
+
+
+def assert_swiglu_close(got: np.ndarray, gate: np.ndarray, up: np.ndarray, want: np.ndarray, what=""):
+    """bf16(bf16(silu(bf16(gate))) * bf16(up)) outputs
+    (rtol = atol = 1e-2) plus one bf16 ulp of each rounded factor carried
+    through the product. Both sides round gate, silu and up to bf16 from
+    sums that differ in their last fp32 bits, so a value on a rounding
+    boundary may land one ulp apart; where silu is steep relative to its
+    value (its tail, gate < -4) and |up| is large, one ulp of gate moves the
+    product by several output ulps (gate -6, up -63: 0.023)."""
+    sig = 1.0 / (1.0 + np.exp(-gate))
+    s = gate * sig
+    ds = np.abs(sig * (1.0 + gate * (1.0 - sig)))
+    carry = np.abs(up) * (ds * bf16_ulp(gate) + bf16_ulp(s)) + np.abs(s) * bf16_ulp(up)
+    bad = np.abs(got - want) > 1e-2 + 1e-2 * np.abs(want) + carry
+    if bad.any():
+        idx = np.argwhere(bad)[:5]
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outside the bar; first {idx.tolist()} got "
+                             f"{got[tuple(idx[0])]} want {want[tuple(idx[0])]}")
