@@ -16,6 +16,7 @@
 //    sigmoid-gated shared expert and the residual: the block tail of
 //    mtplx/models/qwen4_exp.py:1438-1445 and :1544-1577.
 #include "common.hpp"
+#include "sampler_common.hpp"
 
 namespace mtp {
 
@@ -111,20 +112,66 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t* i
   }
 }
 
-// One wave per token: top-k experts and renormalised softmax weights. The
-// row (plus skew) is read once into LDS; the k rounds scan it there.
+// One wave per token: top-k experts and renormalised softmax weights.
+// Each candidate is the u64 key (order-preserving value bits << 32 | ~id),
+// so "value desc, id asc" is one unsigned max; -0 is folded into +0 first,
+// so equal values tie on the id as the float comparison does, and NaN never
+// wins (key 0). Up to kRouteRegE experts the keys stay in registers and
+// each of the k rounds is a DPP wave max; wider rows go through LDS.
 constexpr int kRouteMaxE = 4096;
+constexpr int kRouteRegE = 512;
+
+__device__ __forceinline__ uint64_t route_key(float v, int e) {
+  if (v != v) return 0ull;
+  return make_key(v + 0.0f, e);   // -0 + 0 = +0
+}
+
+__device__ __forceinline__ void route_finish(const float* s_val, const int* s_id, int t, int top_k, int32_t* ids,
+                                             float* weights) {
+  const float mx = s_val[0];
+  float sum = 0.f;
+  for (int r = 0; r < top_k; ++r) sum += __expf(s_val[r] - mx);
+  for (int r = 0; r < top_k; ++r) {
+    ids[(size_t)t * top_k + r] = s_id[r];
+    weights[(size_t)t * top_k + r] = __expf(s_val[r] - mx) / sum;
+  }
+}
+
 __global__ __launch_bounds__(64) void moe_route_kernel(const float* logits, long long ld, const float* skew, int E,
                                                        int top_k, int32_t* ids, float* weights) {
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
   const float* grow = logits + (size_t)t * ld;
-  __shared__ float row[kRouteMaxE];
   __shared__ float s_val[64];
   __shared__ int s_id[64];
+  if (E <= kRouteRegE) {
+    constexpr int kPer = kRouteRegE / 64;
+    uint64_t key[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int e = lane + 64 * i;
+      key[i] = e < E ? route_key(skew ? grow[e] + skew[e] : grow[e], e) : 0ull;
+    }
+    uint64_t taken = ~0ull;
+    for (int r = 0; r < top_k; ++r) {   // uniform: the DPP max needs every lane
+      uint64_t best = 0ull;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i)
+        if (key[i] < taken && key[i] > best) best = key[i];
+      best = wave_max_u64(best);
+      if (lane == 0) {
+        s_val[r] = best ? key_value(best) : -INFINITY;
+        s_id[r] = best ? key_id(best) : 0x7fffffff;
+      }
+      taken = best;
+    }
+    __syncthreads();
+    if (lane == 0) route_finish(s_val, s_id, t, top_k, ids, weights);
+    return;
+  }
+  __shared__ float row[kRouteMaxE];
   for (int e = lane; e < E; e += 64) row[e] = skew ? grow[e] + skew[e] : grow[e];
   __syncthreads();
-  skew = nullptr;   // already added
   int taken_id = -1;
   float taken_val = INFINITY;
   for (int r = 0; r < top_k; ++r) {
@@ -132,7 +179,7 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* logits, long
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     for (int e = lane; e < E; e += 64) {
-      const float v = skew ? row[e] + skew[e] : row[e];
+      const float v = row[e];
       const bool below = (v < taken_val) || (v == taken_val && e > taken_id);
       if (!below) continue;
       if (v > bv || (v == bv && e < bi)) {
@@ -157,15 +204,7 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* logits, long
     taken_id = bi;
   }
   __syncthreads();
-  if (lane == 0) {
-    const float mx = s_val[0];
-    float sum = 0.f;
-    for (int r = 0; r < top_k; ++r) sum += __expf(s_val[r] - mx);
-    for (int r = 0; r < top_k; ++r) {
-      ids[(size_t)t * top_k + r] = s_id[r];
-      weights[(size_t)t * top_k + r] = __expf(s_val[r] - mx) / sum;
-    }
-  }
+  if (lane == 0) route_finish(s_val, s_id, t, top_k, ids, weights);
 }
 
 // routed = bf16(sum_j w[t,j] * y_sorted[inv_order[t*k + j], :]);

@@ -55,6 +55,16 @@ def test_route_matches_oracle(gpu):
     wi, ww = route_topk((full[:, :256] + skew[None, :]).astype(np.float64), 8)
     assert ids.cpu().numpy().tolist() == wi.tolist()
     assert np.allclose(w.cpu().numpy(), ww, atol=1e-6)
+    # ties (repeated values, +0 and -0), the register path's widest row (512)
+    # and the LDS path (1000 experts), top_k up to 64
+    for E, k in ((512, 8), (300, 64), (1000, 10), (4096, 8)):
+        lg = rng.integers(-3, 4, size=(5, E)).astype(np.float32)
+        lg[0, ::7] = -0.0
+        lg[0, 1::7] = 0.0
+        ids, w = route(torch.from_numpy(lg).cuda(), k)
+        wi, ww = route_topk(lg, k)
+        assert ids.cpu().numpy().tolist() == wi.tolist(), (E, k)
+        assert np.allclose(w.cpu().numpy(), ww, atol=1e-6), (E, k)
 
 
 def test_segments_from_sorted_ids(gpu):
