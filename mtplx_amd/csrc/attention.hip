@@ -186,8 +186,10 @@ __global__ __launch_bounds__(kVtWaves * 64) void attn_vt_kernel(AttnParams p) {
   attn_vt_body<TPW, false>(p, (int)blockIdx.x, lds);
 }
 
+// Two waves per SIMD (256 registers; 280 unconstrained, one wave): cfg4
+// step 25.6-26.0 -> 25.2-25.5 ms, cfg2 within 2%.
 template <int NRG>
-__global__ __launch_bounds__(kVtWaves * 64) void attn_vl_kernel(AttnParams p) {
+__global__ __launch_bounds__(kVtWaves * 64, 2) void attn_vl_kernel(AttnParams p) {
   __shared__ __align__(16) unsigned char lds[attn_vt_lds_bytes()];
   attn_vl_body<false, NRG>(p, (int)blockIdx.x, lds);
 }
