@@ -194,6 +194,38 @@ __global__ __launch_bounds__(kVtWaves * 64, 2) void attn_vl_kernel(AttnParams p)
   attn_vl_body<false, NRG>(p, (int)blockIdx.x, lds);
 }
 
+// Balanced work over the per-request-capacity layout (attn_bal_body): one
+// round of workgroups, each streaming the same share of the batch's K and V.
+template <int NRG>
+__global__ __launch_bounds__(kVtWaves * 64, 2) void attn_bal_kernel(AttnParams p) {
+  __shared__ __align__(16) unsigned char lds[attn_bal_lds_bytes()];
+  attn_bal_body<false, NRG>(p, lds);
+}
+
+
+// Workgroups of the balanced kernel: one per CU (cfg2: 96.8 us at one per
+// CU, 99.0 at two, 109 at four, 118 at half the CUs), at most
+// (kMaxSplits - 2) * Hkv so that no head has more than kMaxSplits partials
+// (a head holds at most 1/Hkv of the tiles, so it meets at most G / Hkv + 2
+// workgroups). Partial slots: at most G - 1 plus one per head.
+static int attn_bal_grid(int Hkv) {
+  const long long g = device_cus();
+  const long long lim = (long long)(kMaxSplits - 2) * Hkv;
+  return (int)(g < lim ? g : lim);
+}
+static size_t attn_bal_ws_bytes(int B, int Hkv) {
+  const size_t slots = (size_t)attn_bal_grid(Hkv) + (size_t)B * Hkv;
+  return slots * 32 * kHD * sizeof(float) + slots * 64 * sizeof(float) + (size_t)2 * B * Hkv * sizeof(int32_t);
+}
+static bool attn_bal_enabled(int B, int split_keys) {
+  static int env = -1;
+  if (env < 0) {
+    const char* v = getenv("MTPLX_AMD_ATTN_BALANCED");
+    env = (v && *v) ? atoi(v) : 1;
+  }
+  return env != 0 && split_keys <= 0 && B <= kBalMaxReq;
+}
+
 // Keys per work unit of the block-layout entry point: about 1024 units over
 // the batch's summed capacity (total_cap * Hkv), at least 128 keys (one tile
 // per wave), at most 4096, a multiple of 128; then at most kMaxSplits splits
@@ -493,7 +525,10 @@ MTP_API size_t mtp_attn_blocks_workspace_bytes(int B, int Hkv, int cap, long lon
   int S, sk;
   attn_blocks_plan(Hkv, cap, total_cap > 0 ? total_cap : (long long)B * cap, split_keys, &S, &sk);
   const size_t units = (size_t)B * Hkv * S;
-  return units * 32 * kHD * sizeof(float) + units * 64 * sizeof(float);
+  const size_t unit_bytes = units * 32 * kHD * sizeof(float) + units * 64 * sizeof(float);
+  if (!attn_bal_enabled(B, split_keys)) return unit_bytes;
+  const size_t bal = attn_bal_ws_bytes(B, Hkv);
+  return bal > unit_bytes ? bal : unit_bytes;
 }
 
 MTP_API int mtp_ragged_gqa_attn_blocks(const mtp_attn_blocks_args* a, void* stream) {
@@ -528,6 +563,30 @@ MTP_API int mtp_ragged_gqa_attn_blocks(const mtp_attn_blocks_args* a, void* stre
   p.out_rows = 1;
   p.scale_log2 = a->scale * 1.4426950408889634f;
   const long long total = a->total_cap > 0 ? a->total_cap : (long long)a->B * a->cap;
+  if (attn_bal_enabled(a->B, a->split_keys)) {
+    // One round of workgroups with equal shares of the batch's tiles; the
+    // merge reads each head's partial slots from the table.
+    const int G = attn_bal_grid(a->Hkv);
+    const size_t need = attn_bal_ws_bytes(a->B, a->Hkv);
+    if (!a->ws || a->ws_bytes < need) {
+      set_error("%s: workspace %zu < %zu (mtp_attn_blocks_workspace_bytes)", who, a->ws_bytes, need);
+      return MTP_ERR_WORKSPACE;
+    }
+    const size_t slots = (size_t)G + (size_t)a->B * a->Hkv;
+    p.part_o = (float*)a->ws;
+    p.part_ml = (float*)a->ws + slots * 32 * kHD;
+    p.bal_tab = reinterpret_cast<int32_t*>((float*)a->ws + slots * (32 * kHD + 64));
+    p.S = 1;
+    p.split_keys = kTileKeys;
+    // One ring slot: 96.8 us on cfg2 against 128.2 with two (the deeper
+    // ring keeps twice the bytes in flight, which this HBM serves worse).
+    hipLaunchKernelGGL(attn_bal_kernel<1>, dim3((unsigned)G), dim3(kVtWaves * 64), 0, (hipStream_t)stream, p);
+    int rc = launch_check(who);
+    if (rc) return rc;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(a->B * a->Hkv * (a->Hq / a->Hkv) * a->Lmax)),
+                       dim3(kMergeThreads), 0, (hipStream_t)stream, p);
+    return launch_check(who);
+  }
   attn_blocks_plan(a->Hkv, a->cap, total, a->split_keys, &p.S, &p.split_keys);
   const size_t need = mtp_attn_blocks_workspace_bytes(a->B, a->Hkv, a->cap, a->total_cap, a->split_keys);
   if (!a->ws || a->ws_bytes < need) {
@@ -537,9 +596,9 @@ MTP_API int mtp_ragged_gqa_attn_blocks(const mtp_attn_blocks_args* a, void* stre
   const size_t units = (size_t)a->B * a->Hkv * p.S;
   p.part_o = (float*)a->ws;
   p.part_ml = (float*)a->ws + units * 32 * kHD;
-  // Two ring slots: three and four measured slower on cfg2 (122 and 129 us
-  // against 119 us per launch) and cfg4.
-  hipLaunchKernelGGL(attn_vl_kernel<2>, dim3((unsigned)units), dim3(kVtWaves * 64), 0, (hipStream_t)stream, p);
+  // One ring slot: 105.6 us on cfg2 against 123.1 with two (122 and 129 with
+  // three and four).
+  hipLaunchKernelGGL(attn_vl_kernel<1>, dim3((unsigned)units), dim3(kVtWaves * 64), 0, (hipStream_t)stream, p);
   int rc = launch_check(who);
   if (rc) return rc;
   hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(a->B * a->Hkv * (a->Hq / a->Hkv) * a->Lmax)),

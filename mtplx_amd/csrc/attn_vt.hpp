@@ -48,6 +48,9 @@ struct AttnParams {
   // of them starting at kv_off[b] + h * nblk (null: a uniform capacity cap).
   const int32_t* row_off;
   const int32_t* kv_off;
+  // Balanced work (attn_bal_body): per head (request-major), the first
+  // partial slot and the number of slots; null for the per-unit layout.
+  int32_t* bal_tab;
 };
 
 // Capacity (keys) of request b and the index of head h's first 32-key block.
@@ -152,12 +155,12 @@ __device__ __forceinline__ void attn_vt_body(const AttnParams& p, const int unit
       const size_t blk = (size_t)((kt < k1 ? kt : k0) >> 5) * 4096 + (size_t)lane * 8;
   #pragma unroll
       for (int i = 0; i < 8; ++i)
-        kr[tt][i] = kin ? *reinterpret_cast<const uint4*>(kbase + blk + i * 512) : make_uint4(0, 0, 0, 0);
+        kr[tt][i] = kin ? ld_stream(kbase + blk + i * 512) : make_uint4(0, 0, 0, 0);
   #pragma unroll
       for (int t = 0; t < 4; ++t)
   #pragma unroll
         for (int jj = 0; jj < 2; ++jj)
-          vr[tt][2 * t + jj] = *reinterpret_cast<const uint4*>(vbase + blk + (t * 2 + jj) * 512);
+          vr[tt][2 * t + jj] = ld_stream(vbase + blk + (t * 2 + jj) * 512);
     }
   #pragma unroll
     for (int tt = 0; tt < TPW; ++tt) {
@@ -286,14 +289,18 @@ __device__ __forceinline__ void attn_vt_body(const AttnParams& p, const int unit
 
 
 
-// Unit = (request, kv head, split of split_keys keys) over per-request
-// capacities: the four waves take split_keys / 4 consecutive keys each and
-// walk them one 32-key tile at a time through a two-deep register ring (the
-// next tile's K and V^T operands in flight while this one is computed), then
-// merge in LDS in wave order as attn_vt_body does. split_keys is a multiple
-// of 128, so long contexts need few splits and few partials.
-template <bool WT, int NRG = 2>
-__device__ __forceinline__ void attn_vl_body(const AttnParams& p, const int unit, unsigned char* lds) {
+// One (request b, kv head h) piece over per-request capacities: wave w of the
+// four attends keys [k0, k1) of its own (the caller's split of the piece),
+// one 32-key tile at a time through an NRG-deep register ring (the next
+// tiles' K and V^T operands in flight while this one is computed); the waves
+// then merge in LDS in wave order as attn_vt_body does and the workgroup
+// writes the piece's partial (o rows to po, (max, l) pairs to pml). qs, L:
+// the request's first query position and query count. A wave with k0 >= k1
+// contributes nothing. Every thread of the four waves must call it.
+template <bool WT, int NRG>
+__device__ __forceinline__ void attn_vl_piece(const AttnParams& p, const int b, const int h, const int qs,
+                                              const int L, const int k0, const int k1, float* po, float* pml,
+                                              unsigned char* lds) {
   constexpr int kOS = kVtOS;
   float* s_o = reinterpret_cast<float*>(lds);   // [kVtWaves][32 * kOS]
   float* s_m = s_o + kVtWaves * 32 * kOS;       // [kVtWaves][32]
@@ -303,29 +310,7 @@ __device__ __forceinline__ void attn_vl_body(const AttnParams& p, const int unit
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c32 = lane & 31;
   const int h2 = lane >> 5;
-  const int s = unit % p.S;
-  const int bh = unit / p.S;
-  const int h = bh % p.Hkv;
-  const int b = bh / p.Hkv;
   const int rep = p.Hq / p.Hkv;
-  const int qs = p.q_start[b];
-  const int L = p.q_lens ? p.q_lens[b] : p.L;
-  const int capb = req_cap(p, b);
-  const int kv_end = (qs + L < capb) ? qs + L : capb;
-  const int k0u = s * p.split_keys;
-  float* po = p.part_o + (size_t)unit * 32 * kHD;
-  float* pml = p.part_ml + (size_t)unit * 64;
-  if (k0u >= kv_end) {
-    if (tid < 32) {
-      st_f32<WT>(pml + 2 * tid, kNegBig);
-      st_f32<WT>(pml + 2 * tid + 1, 0.f);
-    }
-    return;   // uniform over the workgroup
-  }
-  const int wk = p.split_keys / kVtWaves;
-  const int k0 = k0u + wave * wk;
-  const int k1 = (k0 + wk < kv_end) ? k0 + wk : kv_end;
-
   const int qcol = c32;
   const int qr = qcol / p.L;
   const int qi = qcol - qr * p.L;
@@ -353,9 +338,9 @@ __device__ __forceinline__ void attn_vl_body(const AttnParams& p, const int unit
   auto load_tile = [&](uint4 (&kr)[8], uint4 (&vr)[8], int kt) {
     const size_t blk = (size_t)((kt < k1 ? kt : k1 - 1) >> 5) * 4096 + (size_t)lane * 8;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) kr[i] = *reinterpret_cast<const uint4*>(kbase + blk + i * 512);
+    for (int i = 0; i < 8; ++i) kr[i] = ld_stream(kbase + blk + i * 512);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vr[i] = *reinterpret_cast<const uint4*>(vbase + blk + i * 512);
+    for (int i = 0; i < 8; ++i) vr[i] = ld_stream(vbase + blk + i * 512);
   };
   auto tile = [&](const uint4 (&kr)[8], uint4 (&vr)[8], int kt) {
     f32x16 st = {};
@@ -487,6 +472,183 @@ __device__ __forceinline__ void attn_vl_body(const AttnParams& p, const int unit
   }
 }
 
+// Unit = (request, kv head, split of split_keys keys) over per-request
+// capacities: the four waves take split_keys / 4 consecutive keys each.
+// split_keys is a multiple of 128, so long contexts need few splits and few
+// partials.
+template <bool WT, int NRG = 2>
+__device__ __forceinline__ void attn_vl_body(const AttnParams& p, const int unit, unsigned char* lds) {
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int s = unit % p.S;
+  const int bh = unit / p.S;
+  const int h = bh % p.Hkv;
+  const int b = bh / p.Hkv;
+  const int qs = p.q_start[b];
+  const int L = p.q_lens ? p.q_lens[b] : p.L;
+  const int capb = req_cap(p, b);
+  const int kv_end = (qs + L < capb) ? qs + L : capb;
+  const int k0u = s * p.split_keys;
+  float* po = p.part_o + (size_t)unit * 32 * kHD;
+  float* pml = p.part_ml + (size_t)unit * 64;
+  if (k0u >= kv_end) {
+    if (tid < 32) {
+      st_f32<WT>(pml + 2 * tid, kNegBig);
+      st_f32<WT>(pml + 2 * tid + 1, 0.f);
+    }
+    return;   // uniform over the workgroup
+  }
+  const int wk = p.split_keys / kVtWaves;
+  const int k0 = k0u + wave * wk;
+  const int k1 = (k0 + wk < kv_end) ? k0 + wk : kv_end;
+  attn_vl_piece<WT, NRG>(p, b, h, qs, L, k0, k1, po, pml, lds);
+}
+
+// Balanced work for the per-request-capacity layout. The batch's 32-key
+// tiles are numbered request-major, then head, then position (each head of
+// request b has nt_b = ceil(kv_end_b / 32) tiles); workgroup w of G takes the
+// tiles [w T / G, (w+1) T / G) of the T in all, so every workgroup streams
+// the same share of K and V whatever the lengths. Its range falls into
+// pieces, one per head it touches; each piece is split over the four waves
+// by tiles and leaves one partial. Head bh's partials are the consecutive
+// slots from bal_base(bh), one per workgroup that touches it, in workgroup
+// order; the merge reads the (base, count) table that workgroup 0 writes.
+constexpr int kBalMaxReq = 256;   // requests the per-workgroup prefix table holds
+constexpr size_t attn_bal_lds_bytes() { return attn_vt_lds_bytes() + (size_t)3 * kBalMaxReq * sizeof(int); }
+
+// Workgroup owning global tile x (ranges [w T / G, (w+1) T / G)).
+__device__ __forceinline__ int bal_owner(long long x, long long T, int G) {
+  return (int)(((x + 1) * G - 1) / T);
+}
+
+// Tiles per head of request b (keys [0, kv_end) in 32-key tiles).
+__device__ __forceinline__ int bal_req_tiles(const AttnParams& p, int b) {
+  const int qs = p.q_start[b];
+  const int L = p.q_lens ? p.q_lens[b] : p.L;
+  const int capb = req_cap(p, b);
+  int kv_end = (qs + L < capb) ? qs + L : capb;
+  if (kv_end < 0) kv_end = 0;
+  return (kv_end + kTileKeys - 1) / kTileKeys;
+}
+
+// Slots (partials) of head (b, h) whose first global tile is P, nt tiles.
+__device__ __forceinline__ int bal_nparts(long long P, int nt, long long T, int G) {
+  return nt > 0 ? bal_owner(P + nt - 1, T, G) - bal_owner(P, T, G) + 1 : 0;
+}
+
+template <bool WT, int NRG = 2>
+__device__ __forceinline__ void attn_bal_body(const AttnParams& p, unsigned char* lds) {
+  int* s_nt = reinterpret_cast<int*>(lds + attn_vt_lds_bytes());   // [B] tiles per head of each request
+  int* s_pt = s_nt + kBalMaxReq;                                    // [B] first global tile of each request
+  int* s_ps = s_pt + kBalMaxReq;                                    // [B] first slot of each request
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = (int)gridDim.x, w = (int)blockIdx.x;
+  const int B = p.B, Hkv = p.Hkv;
+  // Tiles per request, then the request-major prefix sums (wave 0, 64
+  // requests at a time with a running carry).
+  for (int b = tid; b < B; b += kVtWaves * 64) s_nt[b] = bal_req_tiles(p, b);
+  __syncthreads();
+  if (wave == 0) {
+    int carry = 0;
+    for (int b0 = 0; b0 < B; b0 += 64) {
+      const int b = b0 + lane;
+      const int v = b < B ? Hkv * s_nt[b] : 0;
+      int incl = v;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += t;
+      }
+      if (b < B) s_pt[b] = carry + incl - v;
+      carry += __shfl(incl, 63, 64);
+    }
+  }
+  __syncthreads();
+  // Values read back from LDS are the same in every lane: readfirstlane
+  // keeps them (and the loop below) in scalar registers.
+  auto lds_int = [&](const int* a, int i) { return __builtin_amdgcn_readfirstlane(a[i]); };
+  const long long T = (long long)lds_int(s_pt, B - 1) + (long long)Hkv * lds_int(s_nt, B - 1);
+  if (T == 0) {   // no keys at all: every head has no partial
+    if (w == 0 && p.bal_tab)
+      for (int i = tid; i < 2 * B * Hkv; i += kVtWaves * 64) p.bal_tab[i] = 0;
+    return;
+  }
+  // Slot prefix: request b's heads take sum_h bal_nparts slots.
+  if (wave == 0) {
+    int carry = 0;
+    for (int b0 = 0; b0 < B; b0 += 64) {
+      const int b = b0 + lane;
+      int v = 0;
+      if (b < B)
+        for (int h = 0; h < Hkv; ++h) v += bal_nparts((long long)s_pt[b] + (long long)h * s_nt[b], s_nt[b], T, G);
+      int incl = v;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += t;
+      }
+      if (b < B) s_ps[b] = carry + incl - v;
+      carry += __shfl(incl, 63, 64);
+    }
+  }
+  __syncthreads();
+  // Workgroup 0 publishes each head's (first slot, slot count) for the merge.
+  if (w == 0 && p.bal_tab) {
+    for (int bh = tid; bh < B * Hkv; bh += kVtWaves * 64) {
+      const int b = bh / Hkv, h = bh - (bh / Hkv) * Hkv;
+      int base = s_ps[b];
+      for (int hh = 0; hh < h; ++hh) base += bal_nparts((long long)s_pt[b] + (long long)hh * s_nt[b], s_nt[b], T, G);
+      p.bal_tab[2 * bh] = base;
+      p.bal_tab[2 * bh + 1] = bal_nparts((long long)s_pt[b] + (long long)h * s_nt[b], s_nt[b], T, G);
+    }
+  }
+  const long long lo = (long long)w * T / G, hi = (long long)(w + 1) * T / G;
+  if (lo >= hi) return;   // uniform over the workgroup
+  // Request holding tile lo: the last b with s_pt[b] <= lo (binary search).
+  int b = 0;
+  {
+    int a = 0, z = B - 1;
+    while (a < z) {
+      const int m = (a + z + 1) >> 1;
+      if (lds_int(s_pt, m) <= lo) a = m; else z = m - 1;
+    }
+    b = a;
+  }
+  long long x = lo;
+  bool first = true;
+  while (x < hi) {
+    const int nt = lds_int(s_nt, b);
+    const long long pb = lds_int(s_pt, b);
+    if (nt == 0 || x >= pb + (long long)Hkv * nt) {   // past this request
+      ++b;
+      continue;
+    }
+    const int h = (int)((x - pb) / nt);
+    const long long P = pb + (long long)h * nt;   // head's first global tile
+    const int ta = (int)(x - P);
+    const int tb = (int)((hi < P + nt ? hi : P + nt) - P);
+    int slot = lds_int(s_ps, b);
+    for (int hh = 0; hh < h; ++hh) slot += bal_nparts(pb + (long long)hh * nt, nt, T, G);
+    slot += w - bal_owner(P, T, G);
+    const int qs = __builtin_amdgcn_readfirstlane(p.q_start[b]);
+    const int L = __builtin_amdgcn_readfirstlane(p.q_lens ? p.q_lens[b] : p.L);
+    const int capb = __builtin_amdgcn_readfirstlane(req_cap(p, b));
+    const int kv_end = (qs + L < capb) ? qs + L : capb;
+    // The four waves take consecutive shares of the piece's tiles.
+    const int n = tb - ta;
+    const int t0 = ta + (n * wave) / kVtWaves, t1 = ta + (n * (wave + 1)) / kVtWaves;
+    const int k0 = t0 * kTileKeys;
+    const int k1 = (t1 * kTileKeys < kv_end) ? t1 * kTileKeys : kv_end;
+    if (!first) __syncthreads();   // the previous piece's LDS reads are done
+    first = false;
+    attn_vl_piece<WT, NRG>(p, b, h, qs, L, k0, k1, p.part_o + (size_t)slot * 32 * kHD, p.part_ml + (size_t)slot * 64,
+                           lds);
+    x = P + tb;
+  }
+}
+
 // Merge item = (request, kv head, query column), one per workgroup of
 // kMergeGroups x 128 threads: thread (g, d) sums column d over group g's
 // contiguous share of the splits, issuing all of its loads together (one
@@ -517,13 +679,22 @@ __device__ __forceinline__ void attn_merge_body(const AttnParams& p, const int i
   const int qr = q / p.L, qi = q - (q / p.L) * p.L;
   const int kv_end = p.q_start[b] + L;
   const int capb = req_cap(p, b);
-  int ns = cdiv(kv_end < capb ? kv_end : capb, p.split_keys);
-  if (ns > p.S) ns = p.S;
-  const float* ml = p.part_ml + (size_t)bh * p.S * 64 + 2 * q;
+  // The head's partials: splits bh * S .. of the per-unit layout, or the
+  // balanced layout's slots from its table.
+  int ns, base;
+  if (p.bal_tab) {
+    base = p.bal_tab[2 * bh];
+    ns = p.bal_tab[2 * bh + 1];
+  } else {
+    base = bh * p.S;
+    ns = cdiv(kv_end < capb ? kv_end : capb, p.split_keys);
+    if (ns > p.S) ns = p.S;
+  }
+  const float* ml = p.part_ml + (size_t)base * 64 + 2 * q;
   // This thread's partial-O loads go out first: they do not depend on the
   // split weights, so the max / weight pass below overlaps their round trip.
   const int s0 = (g * ns) / kMergeGroups, s1 = ((g + 1) * ns) / kMergeGroups;
-  const float* po = p.part_o + ((size_t)bh * p.S * 32 + q) * kHD + d;
+  const float* po = p.part_o + ((size_t)base * 32 + q) * kHD + d;
   float v[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) v[i] = (s0 + i < s1) ? po[(size_t)(s0 + i) * 32 * kHD] : 0.f;

@@ -170,3 +170,61 @@ def test_cfg4_ragged_verify_step_matches_oracle(gpu):
         assert res.tokens[b].cpu().numpy().tolist()[: len(w.tokens)] == w.tokens, b
         assert (res.tokens[b, K + 1:].cpu().numpy() == -1).all()
         assert int(res.status[b]) == 0
+
+
+def _blocks_attention(ctx, lens, split_keys, seed, Hq=40, Hkv=8):
+    """Block attention over requests with contexts ``ctx`` (keys before the
+    new rows) and ``lens`` query rows; returns (output rows, inputs)."""
+    from mtplx_amd import _lib
+    D = 128
+    B = len(ctx)
+    lens = np.asarray(lens, np.int32)
+    q_start = np.asarray(ctx, np.int32)
+    caps = ((q_start + lens + 31) // 32) * 32
+    row_off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    Lmax = int(lens.max())
+    kv_off = np.concatenate([[0], np.cumsum(Hkv * (caps // 32))]).astype(np.int32)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    kb = torch.randn(int(kv_off[-1]) * 4096, device="cuda", generator=g).to(torch.bfloat16)
+    vb = torch.randn(int(kv_off[-1]) * 4096, device="cuda", generator=g).to(torch.bfloat16)
+    q = torch.randn((B, Hq, Lmax, D), device="cuda", generator=g).to(torch.bfloat16)
+    out = torch.full((int(row_off[-1]), Hq * D), float("nan"), dtype=torch.bfloat16, device="cuda")
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).cuda()  # noqa: E731
+    d_qs, d_lens, d_row, d_kv = t(q_start), t(lens), t(row_off), t(kv_off)
+    nb = _lib.query("mtp_attn_blocks_workspace_bytes", B, Hkv, int(caps.max()), int(caps.sum()), split_keys)
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    _lib.attn_blocks(_st(), q=q, k_blk=kb, v_blk=vb, q_start=d_qs, q_lens=d_lens, row_off=d_row, kv_off=d_kv,
+                     out=out, B=B, Hq=Hq, Hkv=Hkv, Lmax=Lmax, D=D, cap=int(caps.max()), split_keys=split_keys,
+                     scale=1.0 / np.sqrt(D), total_cap=int(caps.sum()), ws=ws, ws_bytes=ws.numel())
+    torch.cuda.synchronize()
+    return bf16_values(out), (q, kb, vb, q_start, lens, caps, row_off, kv_off)
+
+
+@pytest.mark.parametrize("case", ["long_among_short", "tiny_total", "single", "uniform"])
+@pytest.mark.parametrize("split_keys", [0, 1024])
+def test_block_attention_balanced_shapes(gpu, case, split_keys):
+    """split_keys 0 runs the balanced kernel (equal shares of all tiles per
+    workgroup, per-head partial slots); 1024 the per-unit kernel. Both
+    against the float64 oracle, request by request."""
+    from mtplx_amd.verify_step import kv_from_blocks
+    rng = np.random.default_rng(17)
+    if case == "long_among_short":
+        ctx = list(rng.integers(0, 97, size=11)) + [20000]
+        lens = list(rng.integers(1, 5, size=12))
+    elif case == "tiny_total":
+        ctx, lens = [3, 0], [2, 4]
+    elif case == "single":
+        ctx, lens = [30000], [4]
+    else:
+        ctx, lens = [4093] * 4, [3] * 4
+    Hq, Hkv, D = 40, 8, 128
+    got, (q, kb, vb, q_start, lens, caps, row_off, kv_off) = _blocks_attention(ctx, lens, split_keys, seed=23)
+    assert np.isfinite(got).all()
+    for b in range(len(ctx)):
+        o0, o1 = int(kv_off[b]), int(kv_off[b + 1])
+        kr = kv_from_blocks(kb[o0 * 4096:o1 * 4096].reshape(1, Hkv, int(caps[b]), D), "k").float().cpu().numpy()
+        vr = kv_from_blocks(vb[o0 * 4096:o1 * 4096].reshape(1, Hkv, int(caps[b]), D), "v").float().cpu().numpy()
+        L = int(lens[b])
+        want = A.ragged_gqa_attention(q[b:b + 1, :, :L].float().cpu().numpy(), kr, vr, [int(q_start[b])])[0]
+        rows = got[row_off[b]:row_off[b + 1]].reshape(L, Hq, D).transpose(1, 0, 2)
+        assert_close(rows, want, what=f"{case} request {b} (ctx {q_start[b] + L})")
