@@ -451,7 +451,7 @@ def cfg2_attention(nsets: int = 8, reps: int = 4, seed: int = 21) -> dict:
     return out
 
 
-def cfg5_moe(steps: int = 5, warmup: int = 2, seed: int = 5) -> dict:
+def cfg5_moe(steps: int = 5, warmup: int = 2, seed: int = 5, eager: bool = False) -> dict:
     """BASELINE cfg5: the 125B-class MoE decoder (48 layers, hidden 4096,
     256 experts top-8 + 1 gated shared expert, expert FFN 1536, 32/4 heads,
     vocab 151936), random init, router skew Zipf(1.1), 4 requests x depth 3
@@ -488,19 +488,34 @@ def cfg5_moe(steps: int = 5, warmup: int = 2, seed: int = 5) -> dict:
     many = sum(int((n > 4).sum()) for n in counts) / len(counts)
     rows_many = sum(int(n[n > 4].sum()) for n in counts) / len(counts)
     model.route_log = None
-    for _ in range(warmup):
-        res = model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
+    # The step (router, sort, both expert row classes, shared expert, combine)
+    # replayed from one HIP graph, as the cfg3 line; eager launches of its
+    # ~770 short kernels would add ~0.9 ms of host gaps per step.
+    from mtplx_amd.verify_step import CapturedVerifyStep
+    if eager:
+        cap = None
+        stream = torch.cuda.current_stream()
+
+        def step():
+            return model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)
+    else:
+        cap = CapturedVerifyStep(model, tokens, q_start, draft_logits, uniforms, sampler)
+        stream = cap.stream
+        step = cap.replay
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(steps):
-        res = model.verify_step(tokens, q_start, draft_logits, uniforms, sampler)
-    e1.record(stream)
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(steps):
+            res = step()
+        e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     assert int(res.status.max().item()) == 0
+    model.check_status()
     L0 = model.layers[0]
     expert_bytes = (_matrix_bytes(L0.expert_gate_up) + _matrix_bytes(L0.expert_down)) // c.n_experts
     dense = sum(_matrix_bytes(x.qkv, x.o, x.router, x.shared_gate, x.shared_up, x.shared_down)
@@ -508,10 +523,10 @@ def cfg5_moe(steps: int = 5, warmup: int = 2, seed: int = 5) -> dict:
     kv = c.layers * B * ctx * c.n_kv_heads * c.head_dim * 2 * 2
     total = sum(distinct) * expert_bytes + dense + kv
     s = ms / 1e3
-    del model
+    del cap, model
     torch.cuda.empty_cache()
     return {"workload": "cfg5: 125B-class MoE decoder, 4 requests x depth 3 (16 rows), 8k context, Zipf(1.1) "
-                        "router skew, eager launches",
+                        "router skew, " + ("eager launches" if eager else "launches replayed from one HIP graph"),
             "rows": B * L, "ms_per_step": round(ms, 4), "verify_rows_per_s": round(B * L / s, 2),
             "distinct_experts_per_layer_mean": round(sum(distinct) / len(distinct), 2),
             "experts_with_1_to_4_rows_mean": round(few, 2), "experts_with_5_plus_rows_mean": round(many, 2),
@@ -629,7 +644,7 @@ def main() -> int:
         print(json.dumps(cfg2_attention()), flush=True)
         return 0
     if args.workload == "cfg5":
-        print(json.dumps(cfg5_moe(steps=args.steps, warmup=args.warmup)), flush=True)
+        print(json.dumps(cfg5_moe(steps=args.steps, warmup=args.warmup, eager=args.eager)), flush=True)
         return 0
     if args.workload == "cfg4":
         print(json.dumps(cfg4_ragged(VerifyModel(DENSE_27B, device=dev, seed=0), steps=args.steps,
@@ -698,7 +713,7 @@ def main() -> int:
         others["cfg2_attention"] = cfg2_attention()
         print("cfg2 done", file=sys.stderr, flush=True)
     if "cfg5" in parts:
-        others["cfg5"] = cfg5_moe()
+        others["cfg5"] = cfg5_moe(eager=args.eager)
         print(f"cfg5 done: {others['cfg5']['ms_per_step']} ms/step", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu_baseline else cpu_baseline(cfg.layers)
 

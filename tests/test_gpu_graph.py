@@ -7,10 +7,18 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
-def test_captured_step_matches_eager_every_replay(gpu):
+@pytest.mark.parametrize("kind", ["dense", "moe"])
+def test_captured_step_matches_eager_every_replay(gpu, kind):
+    """dense: the cfg3-style layer; moe: router, expert sort, both routed
+    row classes (experts with 1-4 and with 5+ rows over 32 routed rows on 8
+    experts), shared expert and combine inside the captured step."""
     from mtplx_amd.sampling import SamplerConfig
     from mtplx_amd.verify_step import CapturedVerifyStep, DecoderConfig, VerifyModel
-    cfg = DecoderConfig(layers=2, hidden=512, ffn=1024, n_heads=8, n_kv_heads=2, head_dim=128, vocab=4096)
+    if kind == "dense":
+        cfg = DecoderConfig(layers=2, hidden=512, ffn=1024, n_heads=8, n_kv_heads=2, head_dim=128, vocab=4096)
+    else:
+        cfg = DecoderConfig(layers=2, hidden=512, ffn=0, n_heads=8, n_kv_heads=2, head_dim=128, vocab=4096,
+                            n_experts=8, top_k=4, expert_ffn=256, shared_ffn=256)
     model = VerifyModel(cfg, device="cuda", seed=21)
     B, L = 2, 4
     model.allocate_cache(B, 512)
