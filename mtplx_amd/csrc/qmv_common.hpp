@@ -650,8 +650,8 @@ int device_cus();
 // never land where another shape keeps its counters.
 constexpr size_t kCounterBytes = 65536;                 // 16384 counters
 constexpr int kMaxCounters = (int)(kCounterBytes / 4);
-// Tail split: fp32 partials of up to 8 rows x 64 values for two parts per CU.
-constexpr int kTailMaxRows = 8;
+// Tail split: fp32 partials of up to 16 rows x 64 values for two parts per CU.
+constexpr int kTailMaxRows = 16;
 inline size_t tail_workspace_bytes(int M, int N) {
   if (M < 1 || N < 1) return 0;
   return kCounterBytes + (size_t)2 * device_cus() * kTailMaxRows * 64 * sizeof(float);

@@ -565,7 +565,8 @@ static void launch_one(K k, const Plan& pl, int nt, hipStream_t st, const QmmPar
 // leftover tiles and E divides the CU count, the T - E full tiles run as
 // usual and every leftover tile is split by K into S = CUs / E parts, so the
 // last round puts exactly one part on every CU instead of a whole tile on E
-// of them. All T - E + CUs workgroups must be resident at once.
+// of them; with T <= CUs every tile is split into floor(CUs / T) parts. All
+// workgroups must be resident at once (one round).
 template <typename K>
 static bool tail_launch(K kernel, const Plan& pl, int nt, hipStream_t st, QmmParams q) {
   const int cus = device_cus();
@@ -588,16 +589,28 @@ static bool tail_launch(K kernel, const Plan& pl, int nt, hipStream_t st, QmmPar
     hipLaunchKernelGGL(kernel, dim3(groups * pl.split), dim3(nt), pl.lds, st, q);
     return true;
   }
-  if (T <= cus) return false;
-  const int E = T % cus;
-  if (E == 0 || cus % E) return false;
-  const int S = cus / E;
-  if (S < 2 || S > Q) return false;
+  // Fewer tiles than CUs (small N: the router, shared-expert and attention
+  // projections at M = 16): every tile is split by K into floor(CUs / T)
+  // parts (at most one per quad), so the launch keeps up to every CU busy
+  // instead of T of them.
+  int E, S, grid;
+  if (T <= cus) {
+    E = T;
+    S = cus / T;
+    if (S > Q) S = Q;
+    if (S < 2) return false;
+    grid = T * S;
+  } else {
+    E = T % cus;
+    if (E == 0 || cus % E) return false;
+    S = cus / E;
+    if (S < 2 || S > Q) return false;
+    grid = T - E + cus;
+  }
   if (pl.lds > 65536) (void)hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                 (int)pl.lds);
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, nt, pl.lds) != hipSuccess) return false;
-  const int grid = T - E + cus;
   if (grid > occ * cus) return false;
   q.tail_first = T - E;
   q.tail_split = S;
@@ -630,7 +643,7 @@ static void launch_rk(const QmmParams& q, const Plan& pl, hipStream_t st) {
       return;
     }
   }
-  if (q.packed && (R == 4 || pl.split > 1) && q.tail_ok &&
+  if (q.packed && (R <= 8 || pl.split > 1) && q.tail_ok &&
       tail_launch(qmv_stream_kernel<NW, R, XM, EM, 0, true>, pl, NW * 64, st, q))
     return;
   if constexpr (XM == X_PRE) {   // packed weights only (checked by the caller)

@@ -36,23 +36,33 @@ struct NoHook {
 };
 
 // Adds the S parts of one tile's fp32 sums [S][M*64] (device-coherent loads)
-// into fin, in part order. A thread's elements of one part are loaded
-// together (at most 8: M*64 <= 8 * threads), so the sum costs S round trips.
-template <int NT>
+// into fin, in part order. A thread's elements (at most 8: M*64 <= 8 *
+// threads) of up to 8 parts are loaded together, so the sum costs
+// ceil(S / 8) round trips (a tile split 16 ways, 2).
+// MAXN: the largest n the caller has (M <= 2R rows of 64 values).
+template <int NT, int MAXN>
 __device__ __forceinline__ void sum_parts(const float* p0, int S, int n, float* fin, int tid) {
-  static_assert(NT * 8 >= 32 * 64, "at most 8 elements per thread");
+  static_assert(NT * 8 >= MAXN, "at most 8 elements per thread");
+  constexpr int kE = (MAXN + NT - 1) / NT;   // elements per thread at n = MAXN
   float a[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) a[k] = 0.f;
-  for (int q = 0; q < S; ++q) {
-    float l[8];
+  for (int q0 = 0; q0 < S; q0 += 8) {
+    float l[8][kE];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int idx = tid + k * NT;
-      l[k] = idx < n ? __hip_atomic_load(p0 + (size_t)q * n + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-    }
+    for (int qq = 0; qq < 8; ++qq)
 #pragma unroll
-    for (int k = 0; k < 8; ++k) a[k] += l[k];
+      for (int k = 0; k < kE; ++k) {
+        const int idx = tid + k * NT;
+        l[qq][k] = (q0 + qq < S && idx < n)
+                       ? __hip_atomic_load(p0 + (size_t)(q0 + qq) * n + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                       : 0.f;
+      }
+#pragma unroll
+    for (int qq = 0; qq < 8; ++qq)
+      if (q0 + qq < S)
+#pragma unroll
+        for (int k = 0; k < kE; ++k) a[k] += l[qq][k];
   }
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
@@ -308,7 +318,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
       }
       lds_barrier();
       if (!s_last) return;
-      sum_parts<NT>(p.partial + (size_t)ti * p.tail_split * (M * 64), p.tail_split, M * 64, fin, tid);
+      sum_parts<NT, 2 * R * 64>(p.partial + (size_t)ti * p.tail_split * (M * 64), p.tail_split, M * 64, fin, tid);
       lds_barrier();
       qmm_epilogue<NW, EM, kPhase>(p, fin, nb, M, 0);
       if (tid == 0) __hip_atomic_store(p.counters + ti, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -342,7 +352,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
       for (int jj = 0; jj < jn; ++jj) {
         if (!s_lastv[jj]) continue;   // the same LDS value for every thread
         const int nb = tile0 + (j0 + jj) * G;
-        sum_parts<NT>(p.partial + (size_t)nb * p.tail_split * (M * 64), p.tail_split, M * 64, fin, tid);
+        sum_parts<NT, 2 * R * 64>(p.partial + (size_t)nb * p.tail_split * (M * 64), p.tail_split, M * 64, fin, tid);
         lds_barrier();
         qmm_epilogue<NW, EM, kPhase>(p, fin, nb, M, 0);
         if (tid == 0) __hip_atomic_store(p.counters + nb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

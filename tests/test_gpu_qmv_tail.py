@@ -45,6 +45,11 @@ CASES = [  # (M, N, K, xmode, emode): N/32 tiles = 512 + E, E | 256 on a 256-CU 
     (4, 18432, 2048, 0, 1),    # 576 tiles: 64 split 4 ways, residual + ss
     (2, 20480, 1024, 2, 0),    # 640 tiles: 128 split 2 ways
     (3, 17408, 2048, 0, 3),
+    # fewer tiles than CUs, every tile split floor(256 / T) ways (at most one part per quad):
+    (16, 257, 4096, 0, 0),     # router | shared gate of the MoE block: 9 tiles, 16 parts each
+    (16, 1536, 4096, 2, 3),    # shared expert gate/up + SwiGLU, fused norm: 48 tiles, 5 parts
+    (16, 4096, 1536, 0, 1),    # shared expert down + residual: 128 tiles, 2 parts
+    (4, 1024, 4096, 2, 0),     # 32 tiles, 8 parts
 ]
 
 
