@@ -143,8 +143,9 @@ int mtp_pack_affine4_mf16(const void* w, const void* scales, const void* biases,
  * (256-byte aligned, zeroed once before first use and then left to the
  * library; calls sharing one workspace must be stream-ordered). The per-tile
  * kernel then splits the leftover tiles of its last round by K over all CUs
- * (tiles mod CUs must divide the CU count; the parts are summed in a fixed
- * order). Without a workspace it runs unsplit. schedule must be 0.
+ * (tiles mod CUs must divide the CU count), or, with fewer tiles than CUs,
+ * every tile into floor(CUs / tiles) parts (M <= 16); the parts are summed in
+ * a fixed order. Without a workspace it runs unsplit. schedule must be 0.
  * emode 4 = q|k|v projection with RoPE and the cache write fused into the
  * epilogue (the work of mtp_rope_qkv_to_cache / _vt below, same rounding):
  * rope points at the outputs; y0 is unused; packed weights whose rows are in

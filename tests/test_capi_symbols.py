@@ -47,9 +47,9 @@ def test_size_queries_without_gpu(lib):
     assert lib.mtp_sampler_workspace_bytes(7, 151936, 0) == (7 * 38 * 536 + 255) // 256 * 256 + 2 * 7 * row
     assert lib.mtp_attn_workspace_bytes(8, 8, 32768, 0) == 8 * 8 * 32 * (32 * 128 + 64) * 4
     # tail split: a fixed 64 KiB area of arrival counters first (shared by
-    # every shape), then two fp32 [8][64] partials per CU (256 when no device
+    # every shape), then two fp32 [16][64] partials per CU (256 when no device
     # is visible, as here).
-    assert lib.mtp_qmv_workspace_bytes(4, 17408, 5120, 0) == 65536 + 2 * 256 * 8 * 64 * 4
+    assert lib.mtp_qmv_workspace_bytes(4, 17408, 5120, 0) == 65536 + 2 * 256 * 16 * 64 * 4
 
 
 def test_error_path_reports_message(lib):
