@@ -313,8 +313,10 @@ int mtp_rope_qkv_to_cache_vt(const void* qkv, const int32_t* q_start, const int3
  * start at kv_off[b] + h * nblk_b); kv_off NULL means a uniform capacity cap.
  * cap is the largest request capacity (a multiple of 32), total_cap the sum
  * of the capacities (<= 0: B * cap), split_keys the keys per work unit (a
- * multiple of 128; <= 0 picks about 1024 units over total_cap * Hkv).
- * (Hq/Hkv) * Lmax <= 32, D = 128. */
+ * multiple of 128). split_keys <= 0 (and B <= 256) gives balanced work
+ * instead: one workgroup per CU, each taking an equal share of all the
+ * batch's (request, head, 32-key tile) work up to each request's
+ * q_start + q_len, whatever the lengths. (Hq/Hkv) * Lmax <= 32, D = 128. */
 typedef struct mtp_attn_blocks_args {
   const void* q;
   const void* k_blk;
