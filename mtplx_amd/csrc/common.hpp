@@ -102,9 +102,11 @@ __host__ __device__ __forceinline__ size_t vblk_index(int key, int d) {
   return (size_t)(key >> 5) * 4096 + ((size_t)(t * 2 + jj) * 64 + h2 * 32 + c) * 8 + e;
 }
 
-// 16-byte load of data read once per launch (weights, KV blocks): the
-// non-temporal hint keeps these streams from displacing reused lines in the
-// caches, which measured 7-15% more streaming bandwidth on this GPU.
+// 16-byte load of data read once per launch (the attention's K/V blocks):
+// the non-temporal hint keeps the stream from displacing reused lines in the
+// caches (cfg2 attention 97-99 us against 107-110 us with plain loads). The
+// matmuls' weight quads use plain loads: non-temporal ones fetched ~6% more
+// bytes there for no gain in time.
 typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_stream(const void* p) {
   const u32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));

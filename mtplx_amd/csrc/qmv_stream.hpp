@@ -185,19 +185,19 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
       const size_t qoff = (size_t)(q_lo + (qw > 0 ? kw + KS * t_pf : 0)) * kPackQuadWords;
       const uint32_t* wp = wrow + qoff;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) qr.w[u] = ld_stream(wp + 256 * u);
-      const uint4 sb = ld_stream(reinterpret_cast<const uint32_t*>(srow) + qoff);
+      for (int u = 0; u < 4; ++u) qr.w[u] = *reinterpret_cast<const uint4*>(wp + 256 * u);
+      const uint4 sb = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(srow) + qoff);
       qr.s[0] = sb.x; qr.s[1] = sb.y;
       qr.b[0] = sb.z; qr.b[1] = sb.w;
       if (MF) {
-        const uint4 sb1 = ld_stream(reinterpret_cast<const uint32_t*>(srow) + qoff + 64);
+        const uint4 sb1 = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(srow) + qoff + 64);
         qr.s1[0] = sb1.x; qr.s1[MF ? 1 : 0] = sb1.y;
         qr.b1[0] = sb1.z; qr.b1[MF ? 1 : 0] = sb1.w;
       }
     } else {
       const uint32_t* wp = wrow + 32 * KS * t_pf;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) qr.w[u] = ld_stream(wp + 8 * u);
+      for (int u = 0; u < 4; ++u) qr.w[u] = *reinterpret_cast<const uint4*>(wp + 8 * u);
       if (GSH == 0) {
         const uint2 sv = *reinterpret_cast<const uint2*>(srow + 4 * KS * t_pf);
         const uint2 bv = *reinterpret_cast<const uint2*>(brow + 4 * KS * t_pf);
