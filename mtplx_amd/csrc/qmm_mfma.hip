@@ -82,7 +82,9 @@ struct QmQuad {
 // the unit's quads in the same steps (both quads staged behind the same
 // barriers), then add their sums in LDS in half order; two waves per SIMD
 // instead of one, with the same grid.
-template <int R2, int EM, int KH>
+// RGL: 8-row register groups of the last 32-row block that are finished
+// (rows past M need no group finish): 4, or 2 when M <= 32 (R2 - 1) + 16.
+template <int R2, int EM, int KH, int RGL = 4>
 __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams p) {
   constexpr bool dual = EM == E_DUAL_SWIGLU;
   constexpr int ROWS = 32 * R2;
@@ -178,6 +180,9 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
       for (int r2 = 0; r2 < R2; ++r2) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
+          // Rows 32 r2 + 8 j .. + 7 of register group j: groups past the
+          // last RGL of the last row block hold no output row (M <= 32 (R2 - 1) + 8 RGL).
+          if (r2 == R2 - 1 && j >= RGL) continue;
           const float4 xv = *reinterpret_cast<const float4*>(&xs[buf][kh][u][32 * r2 + 8 * j + 4 * kq]);
           const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
@@ -191,14 +196,17 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
   };
 
   // Group sums of staged quad `buf` of each half: thread t < 4M of half h
-  // sums row t % M, group t / M.
+  // sums row t % M, group t / M (4M <= the half's threads: one sum at most,
+  // its row and group fixed for the whole launch).
+  const int gs_t = tid % kQmThreads;
+  const int gs_u = gs_t / M, gs_m = gs_t - (gs_t / M) * M;
   auto group_sums = [&](int buf, int c) {
     typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     const bf16x2_t one2 = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
     const int h = tid / kQmThreads;
     if (c >= (h ? q_n - h0 : h0)) return;   // this half has no quad c
-    for (int t = tid - h * kQmThreads; t < 4 * M; t += kQmThreads) {
-      const int u = t / M, m = t - u * M;
+    if (gs_t < 4 * M) {
+      const int u = gs_u, m = gs_m;
       float s = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -475,25 +483,27 @@ MTP_API int mtp_qmm_affine4_mfma(const mtp_qmm_args* a, void* stream) {
   // vs 193 us with two halves).
   const int kh_env = env_int_rows("MTPLX_AMD_QMM_HALVES", 0);
   const int kh = kh_env == 1 || kh_env == 2 ? kh_env : (grid <= device_cus() ? 2 : 1);
-#define MTP_ROWS(R2v, EMv)                                                                                \
+#define MTP_ROWS(R2v, EMv, RGLv)                                                                          \
   do {                                                                                                    \
     const size_t lds = rows_lds_bytes(R2v, kh);                                                           \
     if (kh == 2) {                                                                                        \
-      auto k = qmm_rows_kernel<R2v, EMv, 2>;                                                              \
+      auto k = qmm_rows_kernel<R2v, EMv, 2, RGLv>;                                                        \
       if (lds > 65536) (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, \
                                                  (int)lds);                                               \
       hipLaunchKernelGGL(k, dim3(grid), dim3(2 * kQmThreads), lds, st, p);                                \
     } else {                                                                                              \
-      auto k = qmm_rows_kernel<R2v, EMv, 1>;                                                              \
+      auto k = qmm_rows_kernel<R2v, EMv, 1, RGLv>;                                                        \
       if (lds > 65536) (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, \
                                                  (int)lds);                                               \
       hipLaunchKernelGGL(k, dim3(grid), dim3(kQmThreads), lds, st, p);                                    \
     }                                                                                                     \
   } while (0)
-  if (M > 32) {
-    if (em == E_STORE) MTP_ROWS(2, E_STORE); else if (em == E_RESID) MTP_ROWS(2, E_RESID); else MTP_ROWS(2, E_DUAL_SWIGLU);
+  if (M > 48) {
+    if (em == E_STORE) MTP_ROWS(2, E_STORE, 4); else if (em == E_RESID) MTP_ROWS(2, E_RESID, 4); else MTP_ROWS(2, E_DUAL_SWIGLU, 4);
+  } else if (M > 32) {
+    if (em == E_STORE) MTP_ROWS(2, E_STORE, 2); else if (em == E_RESID) MTP_ROWS(2, E_RESID, 2); else MTP_ROWS(2, E_DUAL_SWIGLU, 2);
   } else {
-    if (em == E_STORE) MTP_ROWS(1, E_STORE); else if (em == E_RESID) MTP_ROWS(1, E_RESID); else MTP_ROWS(1, E_DUAL_SWIGLU);
+    if (em == E_STORE) MTP_ROWS(1, E_STORE, 4); else if (em == E_RESID) MTP_ROWS(1, E_RESID, 4); else MTP_ROWS(1, E_DUAL_SWIGLU, 4);
   }
 #undef MTP_ROWS
   return launch_check(who);

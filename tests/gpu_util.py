@@ -40,6 +40,19 @@ def bf16_ulp(v: np.ndarray) -> np.ndarray:
     return np.exp2(np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -126))) - 7)
 
 
+def assert_resid_close(got: np.ndarray, prod: np.ndarray, want: np.ndarray, what=""):
+    """bf16(bf16(x @ W) + resid) outputs: the north-star bar (rtol = atol =
+    1e-2) plus one bf16 ulp of the rounded product. Both sides round the
+    product to bf16 from sums that differ in their last fp32 bits, so it may
+    land one ulp apart; where the residual cancels much of the product, that
+    ulp is several ulps of the result (product -8.25, result -4.25: 0.0625)."""
+    bad = np.abs(got - want) > 1e-2 + 1e-2 * np.abs(want) + bf16_ulp(prod)
+    if bad.any():
+        idx = np.argwhere(bad)[:5]
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outside the bar; first {idx.tolist()} "
+                             f"got {got[tuple(idx[0])]} want {want[tuple(idx[0])]} product {prod[tuple(idx[0])]}")
+
+
 def assert_swiglu_close(got: np.ndarray, gate: np.ndarray, up: np.ndarray, want: np.ndarray, what=""):
     """bf16(bf16(silu(bf16(gate))) * bf16(up)) outputs
     (rtol = atol = 1e-2) plus one bf16 ulp of each rounded factor carried

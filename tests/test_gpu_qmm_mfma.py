@@ -20,7 +20,7 @@ import torch
 from oracle.bf16 import round_to_bf16
 from oracle.moe import silu
 from oracle.qmv import qmm_affine4
-from tests.gpu_util import assert_swiglu_close, assert_close, bf16_values, bits
+from tests.gpu_util import assert_resid_close, assert_swiglu_close, assert_close, bf16_values, bits
 
 pytestmark = pytest.mark.gpu
 
@@ -63,6 +63,8 @@ CASES = [  # m, n, k, emode, gs
     (48, 5120, 17408, 1, 64),    # down-shaped + residual (K split)
     (64, 2048, 5120, 3, 64),     # SwiGLU pair
     (33, 7168, 5120, 0, 64),     # q|k|v-shaped, odd rows
+    (45, 2048, 5120, 3, 64),     # SwiGLU pair at cfg4's 45 rows (rows 48..63 not finished)
+    (49, 5120, 5120, 1, 64),     # just past 48 rows: every row group finished
     (16, 5120, 5120, 1, 128),    # o-shaped, group 128
     (9, 1000, 2048, 0, 64),      # N not a multiple of 32
     (64, 151936 // 8, 5120, 2, 64),   # lm_head slice, fp32 out
@@ -90,6 +92,8 @@ def test_rows_kernel_matches_oracle(gpu, m, n, k, emode, gs):
         want = round_to_bf16(round_to_bf16(silu(a)) * up)
     if emode == 3:
         assert_swiglu_close(got, a, up, want, what=f"rows kernel m={m} n={n} k={k} SwiGLU")
+    elif emode == 1:
+        assert_resid_close(got, a, want, what=f"rows kernel m={m} n={n} k={k} + residual")
     else:
         assert_close(got, want, what=f"rows kernel m={m} n={n} k={k} e={emode}")
     # deterministic, counters returned to zero
