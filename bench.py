@@ -293,7 +293,7 @@ def _randn_bf16(n: int, gen, dev):
     return out
 
 
-def cfg4_ragged(model, steps: int = 5, warmup: int = 2, seed: int = 11) -> dict:
+def cfg4_ragged(model, steps: int = 5, warmup: int = 2, seed: int = 11, eager: bool = False) -> dict:
     """BASELINE cfg4 on the same 27B-shaped weights: 16 requests, depths
     U{1,2,3}, contexts log-uniform in [1k, 64k] (seeded), packed into one
     ragged batch of M = sum(K_b + 1) rows; per-request capacities in one
@@ -301,7 +301,8 @@ def cfg4_ragged(model, steps: int = 5, warmup: int = 2, seed: int = 11) -> dict:
     One step = embedding -> 64 layers (RMSNorm, q|k|v on the rows kernel,
     ragged RoPE + K/V write, block attention, o + residual, RMSNorm, gate/up
     + SwiGLU, down + residual) -> norm + lm_head -> accept/reject with
-    per-request depths; launched eagerly. Algorithmic bytes per step: every
+    per-request depths, replayed from one HIP graph (``eager``: launched
+    kernel by kernel). Algorithmic bytes per step: every
     layer matrix and the lm_head once, each request's K/V (ctx_b keys x
     Hkv x 128 x 2 x 2 B per layer) once, plus the M new K/V rows written."""
     import numpy as np
@@ -332,17 +333,27 @@ def cfg4_ragged(model, steps: int = 5, warmup: int = 2, seed: int = 11) -> dict:
     uniforms = torch.rand((B, 4), device=dev, dtype=torch.float64, generator=gen)
     args = (tokens, t(row_off), t(q_start), t(lens), Lmax, draft_logits, t(d_off), t(draft_index, torch.int64),
             uniforms, SamplerConfig(0.6, 0.95, 20))
-    for _ in range(warmup):
-        res = model.verify_step_ragged(*args)
-    torch.cuda.synchronize()
-    model.check_status()
-    stream = torch.cuda.current_stream()
+    from mtplx_amd.verify_step import CapturedRaggedVerifyStep
+    if eager:
+        stream = torch.cuda.current_stream()
+
+        def step():
+            return model.verify_step_ragged(*args)
+    else:
+        cap = CapturedRaggedVerifyStep(model, *args)
+        stream = cap.stream
+        step = cap.replay
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(steps):
-        res = model.verify_step_ragged(*args)
-    e1.record(stream)
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            res = step()
+        torch.cuda.synchronize()
+        model.check_status()
+        e0.record(stream)
+        for _ in range(steps):
+            res = step()
+        e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     assert int(res.status.max().item()) == 0
@@ -357,7 +368,8 @@ def cfg4_ragged(model, steps: int = 5, warmup: int = 2, seed: int = 11) -> dict:
     s = ms / 1e3
     total = w_bytes + kv_bytes
     return {"workload": "cfg4: 16 requests, depths U{1,2,3}, contexts log-uniform [1k, 64k] (seed %d), one ragged "
-                        "batch, 27B-shaped 4-bit dense decoder, eager launches" % seed,
+                        "batch, 27B-shaped 4-bit dense decoder, " % seed +
+                        ("eager launches" if eager else "launches replayed from one HIP graph"),
             "rows": M, "depths": depths.tolist(), "contexts": ctx.tolist(), "ms_per_step": round(ms, 4),
             "verify_rows_per_s": round(M / s, 2), "weight_bytes": w_bytes, "kv_bytes": kv_bytes,
             "achieved_gbs": round(total / s / 1e9, 1), "frac_hbm": round(total / s / 1e9 / HBM_PEAK_GBS, 4),
@@ -647,7 +659,7 @@ def main() -> int:
         print(json.dumps(cfg5_moe(steps=args.steps, warmup=args.warmup, eager=args.eager)), flush=True)
         return 0
     if args.workload == "cfg4":
-        print(json.dumps(cfg4_ragged(VerifyModel(DENSE_27B, device=dev, seed=0), steps=args.steps,
+        print(json.dumps(cfg4_ragged(VerifyModel(DENSE_27B, device=dev, seed=0), eager=args.eager, steps=args.steps,
                                      warmup=args.warmup)), flush=True)
         return 0
     cfg = DENSE_27B
@@ -705,7 +717,7 @@ def main() -> int:
     if not args.eager:
         del cap
     if "cfg4" in parts:
-        others["cfg4"] = cfg4_ragged(model)
+        others["cfg4"] = cfg4_ragged(model, eager=args.eager)
         print(f"cfg4 done: {others['cfg4']['ms_per_step']} ms/step", file=sys.stderr, flush=True)
     del model
     torch.cuda.empty_cache()

@@ -598,3 +598,33 @@ class CapturedVerifyStep:
         """Enqueue one step on the current stream's device; returns the (static) accept result."""
         self.graph.replay()
         return self.result
+
+
+class CapturedRaggedVerifyStep:
+    """``verify_step_ragged`` (embedding → layers → lm_head → accept/reject
+    with per-request depths) recorded once as a HIP graph, with the same
+    contract as :class:`CapturedVerifyStep`: the graph reads the tensors given
+    at capture time (update them in place between replays; the host-side
+    ``Lmax`` and the sampler configuration are fixed), and an eager warm-up on
+    the capture stream creates the workspaces first."""
+
+    def __init__(self, model: VerifyModel, tokens: torch.Tensor, row_off: torch.Tensor, q_start: torch.Tensor,
+                 q_lens: torch.Tensor, Lmax: int, draft_logits: torch.Tensor, d_off: torch.Tensor,
+                 draft_index: torch.Tensor, uniforms: torch.Tensor, sampler: SamplerConfig = SamplerConfig()):
+        self.model = model
+        self.args = (tokens, row_off, q_start, q_lens, Lmax, draft_logits, d_off, draft_index, uniforms, sampler)
+        self.stream = torch.cuda.Stream(device=model.device)
+        self.graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize(model.device)
+        with torch.cuda.stream(self.stream):
+            model.verify_step_ragged(*self.args)     # warm-up: workspaces
+        self.stream.synchronize()
+        with torch.cuda.graph(self.graph, stream=self.stream):
+            self.result = model.verify_step_ragged(*self.args)
+        self.logits = model.last_logits          # graph-owned output buffer
+        torch.cuda.synchronize(model.device)
+
+    def replay(self):
+        """Enqueue one step on the current stream's device; returns the (static) accept result."""
+        self.graph.replay()
+        return self.result
