@@ -18,9 +18,11 @@
 //    through a two-deep register ring, exactly as the skinny kernel reads
 //    them; nibbles become exact bf16 operands 128 + q with one AND-OR each;
 //  * v_mfma_f32_32x32x16_bf16 with A = x rows (one or two 32-row blocks), B =
-//    the lane's weight column; each 64-k group is finished on the VALU as
-//    acc += s * G + (b - 128 s) * sum(x_group) (group sums from LDS), so the
-//    dequantised weights are never rounded (the numerics of the skinny path);
+//    the lane's weight column; each 64-k group is finished as acc += s * G
+//    on the VALU, and the bias term (b - 128 s) * sum(x_group) of a quad's
+//    four groups as an fp32 MFMA over (group sums from LDS) x (b - 128 s), so
+//    the dequantised weights are never rounded (the numerics of the skinny
+//    path);
 //  * groups left over after the last full round of workgroups are split by K
 //    over the idle CUs; their parts store fp32 sums, and the last part to
 //    arrive adds them in part order (deterministic) and runs the epilogue.
@@ -158,6 +160,19 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
     const uint32_t sw[2] = {r.sb.x, r.sb.y}, bw[2] = {r.sb.z, r.sb.w};
     quad_scales<0>(sw, bw, sv, cb);   // the pack stores scales per 64-group for either group size
     const unsigned char* xb = xbuf(buf, kh);
+    // The bias term of the quad's four groups, sum_u (b_u - 128 s_u) * sum(x_u),
+    // is a (rows x 4) . (4 x 32 columns) product in fp32: two
+    // v_mfma_f32_32x32x2_f32 per row block, whose A operand of lane l is the
+    // group sum of row l % 32 for group 2p + l / 32, and B operand the lane's
+    // column's (b - 128 s) of the same group; same output layout as the
+    // bf16 MFMA, so it accumulates into acc directly.
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+      const float cbk = kq ? cb[2 * pp + 1] : cb[2 * pp];
+#pragma unroll
+      for (int r2 = 0; r2 < R2; ++r2)
+        acc[r2] = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[buf][kh][2 * pp + kq][32 * r2 + c32], cbk, acc[r2], 0, 0, 0);
+    }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const uint32_t wv[4] = {r.w[u].x, r.w[u].y, r.w[u].z, r.w[u].w};
@@ -183,12 +198,10 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
           // Rows 32 r2 + 8 j .. + 7 of register group j: groups past the
           // last RGL of the last row block hold no output row (M <= 32 (R2 - 1) + 8 RGL).
           if (r2 == R2 - 1 && j >= RGL) continue;
-          const float4 xv = *reinterpret_cast<const float4*>(&xs[buf][kh][u][32 * r2 + 8 * j + 4 * kq]);
-          const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = 4 * j + i;
-            acc[r2][r] = fmaf(sv[u], G[r2][r], fmaf(cb[u], xa[i], acc[r2][r]));
+            acc[r2][r] = fmaf(sv[u], G[r2][r], acc[r2][r]);
           }
         }
       }
