@@ -256,6 +256,25 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(AttnParams p)
   attn_merge_body<false>(p, (int)blockIdx.x, lds);
 }
 
+__global__ __launch_bounds__(kMergeHeadThreads) void attn_merge_head_kernel(AttnParams p) {
+  attn_merge_head_body<false>(p, (int)blockIdx.x);
+}
+
+// The split merge: one workgroup per (request, kv head) with all its query
+// columns when the batch has many heads (ragged batches, a few partials per
+// head), else one per (request, kv head, query column) (few heads with many
+// partials each: the cfg3 step's 8 heads x 32 splits). MTPLX_AMD_ATTN_MERGE_HEAD=0
+// keeps the per-column form everywhere.
+constexpr int kMergeHeadMinHeads = 64;
+static void launch_merge(const AttnParams& p, int B, int Hq, int Hkv, int L, hipStream_t st) {
+  const char* v = getenv("MTPLX_AMD_ATTN_MERGE_HEAD");
+  const bool off = v && *v && atoi(v) == 0;
+  if (!off && B * Hkv >= kMergeHeadMinHeads)
+    hipLaunchKernelGGL(attn_merge_head_kernel, dim3((unsigned)(B * Hkv)), dim3(kMergeHeadThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * Hkv * (Hq / Hkv) * L)), dim3(kMergeThreads), 0, st, p);
+}
+
 // Split length: ~2048 work units over the whole capacity (ragged rows leave
 // the units past their length empty), 64..4096 keys, a multiple of the tile.
 static int attn_plan(int B, int Hkv, int cap, int split_keys_req, int* S, int* split_keys) {
@@ -399,7 +418,7 @@ static int attn_run(const void* q, const void* k, const void* v, const int32_t* 
   hipLaunchKernelGGL(attn_split_kernel, dim3((unsigned)units), dim3(64), 0, st, p);
   int rc = launch_check(who);
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(B * Hkv * (Hq / Hkv) * L), dim3(kMergeThreads), 0, st, p);
+  launch_merge(p, B, Hq, Hkv, L, st);
   return launch_check(who);
 }
 
@@ -474,8 +493,7 @@ MTP_API int mtp_ragged_gqa_attn_rows_vt(const void* q, const void* k, const void
     hipLaunchKernelGGL(attn_vt_kernel<2>, dim3((unsigned)units), dim3(kVtWaves * 64), 0, (hipStream_t)stream, p);
   int rc = launch_check(who);
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * Hkv * (Hq / Hkv) * L)), dim3(kMergeThreads), 0,
-                     (hipStream_t)stream, p);
+  launch_merge(p, B, Hq, Hkv, L, (hipStream_t)stream);
   return launch_check(who);
 }
 
@@ -583,8 +601,7 @@ MTP_API int mtp_ragged_gqa_attn_blocks(const mtp_attn_blocks_args* a, void* stre
     hipLaunchKernelGGL(attn_bal_kernel<1>, dim3((unsigned)G), dim3(kVtWaves * 64), 0, (hipStream_t)stream, p);
     int rc = launch_check(who);
     if (rc) return rc;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(a->B * a->Hkv * (a->Hq / a->Hkv) * a->Lmax)),
-                       dim3(kMergeThreads), 0, (hipStream_t)stream, p);
+    launch_merge(p, a->B, a->Hq, a->Hkv, a->Lmax, (hipStream_t)stream);
     return launch_check(who);
   }
   attn_blocks_plan(a->Hkv, a->cap, total, a->split_keys, &p.S, &p.split_keys);
@@ -601,7 +618,6 @@ MTP_API int mtp_ragged_gqa_attn_blocks(const mtp_attn_blocks_args* a, void* stre
   hipLaunchKernelGGL(attn_vl_kernel<1>, dim3((unsigned)units), dim3(kVtWaves * 64), 0, (hipStream_t)stream, p);
   int rc = launch_check(who);
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(a->B * a->Hkv * (a->Hq / a->Hkv) * a->Lmax)),
-                     dim3(kMergeThreads), 0, (hipStream_t)stream, p);
+  launch_merge(p, a->B, a->Hq, a->Hkv, a->Lmax, (hipStream_t)stream);
   return launch_check(who);
 }

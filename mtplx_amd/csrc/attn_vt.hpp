@@ -754,6 +754,92 @@ __device__ __forceinline__ void attn_merge_body(const AttnParams& p, const int i
   st_u16<WT>(p.out + oi, f2bf(val));
 }
 
+// Merge item = one (request, kv head) with all its query columns, for
+// batches with many heads and few partials each (ragged batches): thread t of
+// kMergeHeadThreads takes column t / 8 and 16 consecutive d, and walks the
+// head's partials kMergeHeadBatch at a time with every load of a batch in
+// flight together (index clamped into the head's slots, so they issue back
+// to back), the running max rescaled between batches; fixed order, so the
+// result is deterministic.
+constexpr int kMergeHeadThreads = 256;
+constexpr int kMergeHeadBatch = 8;
+
+template <bool WT>
+__device__ __forceinline__ void attn_merge_head_body(const AttnParams& p, const int bh) {
+  const int tid = threadIdx.x;
+  const int rep = p.Hq / p.Hkv;
+  const int rows = rep * p.L;
+  const int q = tid >> 3;
+  const int d0 = (tid & 7) * 16;
+  if (q >= rows) return;
+  const int h = bh % p.Hkv;
+  const int b = bh / p.Hkv;
+  const int L = p.q_lens ? p.q_lens[b] : p.L;
+  const int qr = q / p.L, qi = q - (q / p.L) * p.L;
+  if (p.row_off && qi >= L) return;   // packed rows: request b has only L of them
+  int ns, base;
+  if (p.bal_tab) {
+    base = p.bal_tab[2 * bh];
+    ns = p.bal_tab[2 * bh + 1];
+  } else {
+    const int kv_end = p.q_start[b] + L;
+    const int capb = req_cap(p, b);
+    base = bh * p.S;
+    ns = cdiv(kv_end < capb ? kv_end : capb, p.split_keys);
+    if (ns > p.S) ns = p.S;
+  }
+  float M = kNegBig, lsum = 0.f;
+  float acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  for (int s0 = 0; s0 < ns; s0 += kMergeHeadBatch) {   // ns == 0 (no keys): zeros out
+    float4 v[kMergeHeadBatch][4];
+    float2 ml[kMergeHeadBatch];
+#pragma unroll
+    for (int j = 0; j < kMergeHeadBatch; ++j) {
+      const int sj = base + (s0 + j < ns ? s0 + j : ns - 1);
+      const float* src = p.part_o + ((size_t)sj * 32 + q) * kHD + d0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[j][c] = *reinterpret_cast<const float4*>(src + 4 * c);
+      ml[j] = *reinterpret_cast<const float2*>(p.part_ml + (size_t)sj * 64 + 2 * q);
+    }
+#pragma unroll
+    for (int j = 0; j < kMergeHeadBatch; ++j)
+      if (s0 + j >= ns) ml[j] = make_float2(kNegBig, 0.f);   // past the head's slots (uniform)
+    float mb = M;
+#pragma unroll
+    for (int j = 0; j < kMergeHeadBatch; ++j) mb = fmaxf(mb, ml[j].x);
+    const float cr = exp2f(M - mb);
+    M = mb;
+    lsum *= cr;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] *= cr;
+#pragma unroll
+    for (int j = 0; j < kMergeHeadBatch; ++j) {
+      if (s0 + j >= ns) continue;   // uniform: its values are another slot's
+      const float w = exp2f(ml[j].x - M);
+      lsum += __fmul_rn(ml[j].y, w);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        acc[4 * c] += v[j][c].x * w;
+        acc[4 * c + 1] += v[j][c].y * w;
+        acc[4 * c + 2] += v[j][c].z * w;
+        acc[4 * c + 3] += v[j][c].w * w;
+      }
+    }
+  }
+  const bool live = qi < L && lsum > 0.f;
+  uint32_t pk[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) pk[i] = pack_bf2(live ? acc[2 * i] / lsum : 0.f, live ? acc[2 * i + 1] / lsum : 0.f);
+  const size_t orow = p.row_off ? (size_t)p.row_off[b] + qi : (size_t)b * p.L + qi;
+  const size_t oi = p.out_rows ? ((orow * p.Hq + h * rep + qr) * kHD + d0)
+                               : ((((size_t)b * p.Hq + h * rep + qr) * p.L + qi) * kHD + d0);
+  uint4* dst = reinterpret_cast<uint4*>(p.out + oi);
+  dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+}
+
 // Tiles per wave: one (more workgroups, shorter chains) while that keeps the
 // partials to merge within kMaxSplits per (request, kv head), else two.
 inline int attn_vt_plan(int cap, int* S, int* tpw) {

@@ -202,11 +202,17 @@ def _blocks_attention(ctx, lens, split_keys, seed, Hq=40, Hkv=8):
 
 @pytest.mark.parametrize("case", ["long_among_short", "tiny_total", "single", "uniform"])
 @pytest.mark.parametrize("split_keys", [0, 1024])
-def test_block_attention_balanced_shapes(gpu, case, split_keys):
+@pytest.mark.parametrize("merge", ["auto", "column"])
+def test_block_attention_balanced_shapes(gpu, case, split_keys, merge, monkeypatch):
     """split_keys 0 runs the balanced kernel (equal shares of all tiles per
     workgroup, per-head partial slots); 1024 the per-unit kernel. Both
-    against the float64 oracle, request by request."""
+    against the float64 oracle, request by request. merge "auto" merges the
+    partials per (request, kv head) when the batch has 64 heads or more
+    (long_among_short: 96), "column" per (request, kv head, query column)
+    everywhere."""
     from mtplx_amd.verify_step import kv_from_blocks
+    if merge == "column":
+        monkeypatch.setenv("MTPLX_AMD_ATTN_MERGE_HEAD", "0")
     rng = np.random.default_rng(17)
     if case == "long_among_short":
         ctx = list(rng.integers(0, 97, size=11)) + [20000]
