@@ -438,7 +438,7 @@ def cfg2_attention(nsets: int = 8, reps: int = 4, seed: int = 21) -> dict:
                          total_cap=int(caps.sum()), ws=ws, ws_bytes=ws.numel())
 
     us = timed(blocks, reps * nsets)
-    out["blocks"] = {"kernel": "attn_bal_kernel + attn_merge_kernel (mtp_ragged_gqa_attn_blocks)",
+    out["blocks"] = {"kernel": "attn_bal_kernel + attn_merge_head_kernel (mtp_ragged_gqa_attn_blocks)",
                      "avg_launch_us": round(us, 3), "achieved_gbs": round(algo / us / 1e3, 1),
                      "frac_hbm": round(algo / us / 1e3 / HBM_PEAK_GBS, 4)}
     del kb, vb
@@ -455,7 +455,7 @@ def cfg2_attention(nsets: int = 8, reps: int = 4, seed: int = 21) -> dict:
                   d_lens.data_ptr(), o2.data_ptr(), B, Hq, Hkv, L, D, cap, scale, 0, ws2.data_ptr(), ws2.numel(), st)
 
     us = timed(split, reps * nsets)
-    out["contiguous"] = {"kernel": "attn_split_kernel + attn_merge_kernel (mtp_ragged_gqa_attn, ragged_sdpa)",
+    out["contiguous"] = {"kernel": "attn_split_kernel + attn_merge_head_kernel (mtp_ragged_gqa_attn, ragged_sdpa)",
                          "avg_launch_us": round(us, 3), "achieved_gbs": round(algo / us / 1e3, 1),
                          "frac_hbm": round(algo / us / 1e3 / HBM_PEAK_GBS, 4)}
     del kc, vc
