@@ -23,8 +23,22 @@
 namespace mtp {
 
 
+// The V tile sits in LDS in its natural layout (key-major, rows padded to
+// kVrowStride elements = 288 B, so the four rows one transposing read spans
+// fall in distinct banks). ds_read_b64_tr_b16 returns, to lane i of each
+// 16-lane group, element i % 4 of the 4 consecutive bf16 loaded by lane
+// 4 e + i / 4, as its slot e (e = 0..3). Lane j of the group therefore
+// addresses row key0 + j / 4, columns d0 + 4 (j % 4): lane i receives
+// V[key0 + e][d0 + i] in slot e, a V^T MFMA operand's four keys.
+constexpr int kVrowStride = kHD + 16;
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v4i16_t lds_read_tr16(const uint16_t* a) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)(a));
+}
+
 __global__ __launch_bounds__(64) void attn_split_kernel(AttnParams p) {
-  __shared__ __align__(16) uint16_t vt[kHD * kVtStride];
+  __shared__ __align__(16) uint16_t ktile[kTileKeys * kVrowStride];
+  __shared__ __align__(16) uint16_t vtile[kTileKeys * kVrowStride];
   const int lane = threadIdx.x;
   const int c32 = lane & 31;
   const int h2 = lane >> 5;
@@ -81,34 +95,36 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnParams p) {
   const uint16_t* vbase = p.v + ((size_t)b * p.Hkv + h) * (size_t)p.cap * kHD;
 
   for (int kt = k0; kt < k1; kt += kTileKeys) {
-    const int key = kt + c32;
-    const bool kin = key < k1;
-    const uint16_t* krow = kbase + (size_t)(kin ? key : kt) * kHD + 64 * h2;
-    const uint16_t* vrow = vbase + (size_t)(kin ? key : kt) * kHD + 64 * h2;
-    uint4 kr[8], vr[8];
+    // The 8 KB K and V tiles with contiguous loads (instruction i: bytes
+    // 1024 i + 16 lane, i.e. key 4 i + lane / 16, d 8 (lane % 16)); keys past
+    // k1 read as zero (stale cache bits cannot leak into P V).
+    uint4 kc[8], vc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      kr[i] = kin ? *reinterpret_cast<const uint4*>(krow + 8 * i) : make_uint4(0, 0, 0, 0);
-      vr[i] = kin ? *reinterpret_cast<const uint4*>(vrow + 8 * i) : make_uint4(0, 0, 0, 0);
+      const int key = kt + 4 * i + (lane >> 4);
+      const bool kin = key < k1;
+      const size_t off = (size_t)(kin ? key : kt) * kHD + 8 * (lane & 15);
+      kc[i] = kin ? ld_stream(kbase + off) : make_uint4(0, 0, 0, 0);
+      vc[i] = kin ? ld_stream(vbase + off) : make_uint4(0, 0, 0, 0);
     }
+    __syncthreads();   // the previous tile's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int o = (4 * i + (lane >> 4)) * kVrowStride + 8 * (lane & 15);
+      *reinterpret_cast<uint4*>(ktile + o) = kc[i];
+      *reinterpret_cast<uint4*>(vtile + o) = vc[i];
+    }
+    __syncthreads();
+    // K operands: lane (key c32, half h2) takes d 64 h2 + 8 i .. + 7 of MFMA i.
+    uint4 kr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kr[i] = *reinterpret_cast<const uint4*>(ktile + c32 * kVrowStride + 64 * h2 + 8 * i);
     // S^T[key][q]
     f32x16 st = {};
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kr[i]), qop[i], st, 0, 0, 0);
 
-    // V^T tile into LDS: vt[d][key].
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t w4[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int d = 64 * h2 + 8 * i + 2 * t;
-        vt[d * kVtStride + c32] = (uint16_t)(w4[t] & 0xffff);
-        vt[(d + 1) * kVtStride + c32] = (uint16_t)(w4[t] >> 16);
-      }
-    }
 
     // Scale, mask, tile max for column q (this lane's 16 keys + lane^32's).
     float sv[16];
@@ -145,20 +161,21 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnParams p) {
       for (int t = 0; t < 4; ++t) pk[t] = pack_bf2(sv[8 * jj + 2 * t], sv[8 * jj + 2 * t + 1]);
       pop[jj] = __builtin_bit_cast(bf16x8, pk);
     }
-    __syncthreads();
     // O^T[d][q] += V^T[d][keys] P^T[keys][q]; slot e of lane (d, h2) in step j
-    // is key 16j + (e<4 ? 4*h2+e : 8+4*h2+e-4).
+    // is key 16j + (e<4 ? 4*h2+e : 8+4*h2+e-4): two transposing reads, keys
+    // 16j + 4 h2 + {0..3} and 16j + 8 + 4 h2 + {0..3}, for d = 32t + lane % 32.
+    const int gj = lane & 15;
+    const uint16_t* vlane = vtile + (4 * h2 + (gj >> 2)) * kVrowStride + 16 * ((lane >> 4) & 1) + 4 * (gj & 3);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const uint16_t* vd = vt + (32 * t + c32) * kVtStride;
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        uint16_t e8[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          e8[e] = vd[16 * jj + 4 * h2 + e];
-          e8[4 + e] = vd[16 * jj + 8 + 4 * h2 + e];
-        }
+        const v4i16_t lo = lds_read_tr16(vlane + 16 * jj * kVrowStride + 32 * t);
+        const v4i16_t hi = lds_read_tr16(vlane + (16 * jj + 8) * kVrowStride + 32 * t);
+        const uint4 e8 = make_uint4((uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16),
+                                    (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16),
+                                    (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16),
+                                    (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16));
         o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, e8), pop[jj], o[t], 0, 0, 0);
       }
     }
