@@ -63,6 +63,10 @@ def install_nax_qlinear_patch() -> dict:
             k = int(x.shape[-1])
             m = x.numel() // max(k, 1)
             if vk_eligible_ksplit(m, k, self.out_features, self.bits, self.group_size, x.dtype):
+                from .verify_qmv import packed_matmul
+                y = packed_matmul(x, self)   # a module packed once streams its tile-major copy
+                if y is not None:
+                    return y
                 y = quantized_matmul(x, self.weight, self.scales, self.biases, group_size=self.group_size,
                                      bits=self.bits)
                 return y + self.bias if self.bias is not None else y

@@ -19,7 +19,29 @@ from .quant import QuantizedLinear
 
 def _affine4(module: Any) -> bool:
     return (isinstance(module, QuantizedLinear) and module.bits == 4 and module.group_size in (64, 128)
-            and module.mode == "affine" and module.biases is not None)
+            and module.mode == "affine"
+            and (module.biases is not None or module.packed is not None or module.packed_mf16 is not None))
+
+
+def _packed(module: QuantizedLinear, m: int) -> tuple[torch.Tensor, int] | None:
+    """The module's cached tile-major pack for ``m`` rows: layout 2 (the
+    16x16x32 MFMA form) at up to 4 rows when cached, else layout 1, or None.
+    A module packed once (``module.pack()``) reads its weights as 1 KB
+    contiguous runs per wave load (cfg1 shape: 17.2 us against 25.5 us on the
+    MLX layout, whose per-lane row reads scatter), so the facade takes the
+    pack whenever it is there and the MLX triple otherwise."""
+    if m <= 4 and module.packed_mf16 is not None:
+        return module.packed_mf16, 2
+    if module.packed is not None:
+        return module.packed, 1
+    return None
+
+
+def _qmv_packed(stream, m: int, n: int, k: int, **kw) -> None:
+    """mtp_qmv_affine4_ex on packed weights with this stream's split-K workspace."""
+    dev = kw["x"].device
+    ws = _lib.WORKSPACES.get(max(256, _lib.query("mtp_qmv_workspace_bytes", m, n, 1, 1)), "verify_qmv", dev)
+    _lib.qmv_ex(stream, M=m, N=n, K=k, ws=ws, ws_bytes=ws.numel(), **kw)
 
 
 def is_multi3_qmv4_eligible(module: Any) -> bool:
@@ -35,7 +57,7 @@ def is_smalln_pair_qmv4_eligible(left: Any, right: Any) -> bool:
     """``mtplx/verify_qmv.py:36``: two equal-shape tiny-N (48) affine int4 linears."""
     if not (_affine4(left) and _affine4(right)):
         return False
-    if left.group_size != right.group_size or left.weight.shape != right.weight.shape:
+    if left.group_size != right.group_size or left._shape != right._shape:
         return False
     return left.in_features % 512 == 0 and left.out_features == 48
 
@@ -43,7 +65,7 @@ def is_smalln_pair_qmv4_eligible(left: Any, right: Any) -> bool:
 def _rows(x: torch.Tensor, module: QuantizedLinear) -> tuple[torch.Tensor, tuple] | None:
     if x.dim() < 2 or x.dtype != torch.bfloat16 or not x.is_cuda:
         return None
-    if module.scales.dtype != x.dtype or module.biases.dtype != x.dtype:
+    if module.scales is not None and (module.scales.dtype != x.dtype or module.biases.dtype != x.dtype):
         return None
     k = int(x.shape[-1])
     if k != module.in_features:
@@ -61,18 +83,41 @@ def _add_bias(y: torch.Tensor, module: QuantizedLinear) -> torch.Tensor:
     return y + module.bias if module.bias is not None else y
 
 
+def packed_matmul(x: torch.Tensor, module: QuantizedLinear) -> torch.Tensor | None:
+    """``x @ module.weight.T`` on the module's cached pack (up to 32 bf16
+    rows on the GPU), or None when there is no pack or x does not qualify.
+    Never falls back to ``module(x)``, so a patched ``__call__`` may use it."""
+    r = _rows(x, module)
+    if r is None:
+        return None
+    x2, lead = r
+    m, k = (int(d) for d in x2.shape)
+    pk = _packed(module, m)
+    if pk is None:
+        return None
+    n = module.out_features
+    y = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    _qmv_packed(_lib.stream_handle(x.device), m, n, k, x=x2, w0=pk[0], y0=y, group_size=module.group_size,
+                xmode=0, emode=0, packed=pk[1])
+    return _add_bias(y, module).reshape(*lead, n)
+
+
 def multi3_qmv4_matmul(x: torch.Tensor, module: QuantizedLinear) -> torch.Tensor:
     """``x @ module.weight.T`` on the verify kernel (``mtplx/verify_qmv.py:194``)."""
     if not is_multi3_qmv4_eligible(module):
         return module(x)
+    y = packed_matmul(x, module)
+    if y is not None:
+        return y
     r = _rows(x, module)
-    if r is None:
+    if r is None or module.weight is None:
         return module(x)
     x2, lead = r
     n = module.out_features
-    y = torch.empty((x2.shape[0], n), dtype=x.dtype, device=x.device)
+    m, k = (int(d) for d in x2.shape)
+    y = torch.empty((m, n), dtype=x.dtype, device=x.device)
     _lib.call("mtp_qmv_affine4", x2.data_ptr(), module.weight.data_ptr(), module.scales.data_ptr(),
-              module.biases.data_ptr(), y.data_ptr(), x2.shape[0], n, x2.shape[1], module.group_size, None, 0,
+              module.biases.data_ptr(), y.data_ptr(), m, n, k, module.group_size, None, 0,
               _lib.stream_handle(x.device))
     return _add_bias(y, module).reshape(*lead, n)
 
@@ -92,19 +137,27 @@ def multi3_dual_qmv4_matmul(x: torch.Tensor, gate_module: QuantizedLinear, up_mo
                             _pair_checked: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
     """Gate/up projections in one launch (``mtplx/verify_qmv.py:614``)."""
     ok = _pair_checked or (is_multi3_qmv4_eligible(gate_module) and is_multi3_qmv4_eligible(up_module)
-                           and gate_module.weight.shape == up_module.weight.shape
+                           and gate_module._shape == up_module._shape
                            and gate_module.group_size == up_module.group_size)
     r = _rows(x, gate_module) if ok else None
     if r is None:
         return gate_module(x), up_module(x)
     x2, lead = r
     n = gate_module.out_features
-    y0 = torch.empty((x2.shape[0], n), dtype=x.dtype, device=x.device)
+    m, k = (int(d) for d in x2.shape)
+    y0 = torch.empty((m, n), dtype=x.dtype, device=x.device)
     y1 = torch.empty_like(y0)
-    _lib.call("mtp_qmv_affine4_dual", x2.data_ptr(), gate_module.weight.data_ptr(), gate_module.scales.data_ptr(),
-              gate_module.biases.data_ptr(), up_module.weight.data_ptr(), up_module.scales.data_ptr(),
-              up_module.biases.data_ptr(), y0.data_ptr(), y1.data_ptr(), x2.shape[0], n, x2.shape[1],
-              gate_module.group_size, 0, None, 0, _lib.stream_handle(x.device))
+    pg, pu = _packed(gate_module, m), _packed(up_module, m)
+    if pg is not None and pu is not None and pg[1] == pu[1]:
+        _qmv_packed(_lib.stream_handle(x.device), m, n, k, x=x2, w0=pg[0], w1=pu[0], y0=y0, y1=y1,
+                    group_size=gate_module.group_size, xmode=0, emode=2, packed=pg[1])
+    elif gate_module.weight is None or up_module.weight is None:
+        return gate_module(x), up_module(x)
+    else:
+        _lib.call("mtp_qmv_affine4_dual", x2.data_ptr(), gate_module.weight.data_ptr(),
+                  gate_module.scales.data_ptr(), gate_module.biases.data_ptr(), up_module.weight.data_ptr(),
+                  up_module.scales.data_ptr(), up_module.biases.data_ptr(), y0.data_ptr(), y1.data_ptr(), m, n, k,
+                  gate_module.group_size, 0, None, 0, _lib.stream_handle(x.device))
     return _add_bias(y0, gate_module).reshape(*lead, n), _add_bias(y1, up_module).reshape(*lead, n)
 
 
@@ -125,10 +178,18 @@ def multi3_swiglu_down_qmv4_matmul(gate: torch.Tensor, up: torch.Tensor, module:
     g2, lead = r
     u2 = up.reshape(g2.shape).contiguous()
     n = module.out_features
-    y = torch.empty((g2.shape[0], n), dtype=gate.dtype, device=gate.device)
-    _lib.call("mtp_qmv_affine4_swiglu_in", g2.data_ptr(), u2.data_ptr(), module.weight.data_ptr(),
-              module.scales.data_ptr(), module.biases.data_ptr(), None, y.data_ptr(), g2.shape[0], n, g2.shape[1],
-              module.group_size, None, 0, _lib.stream_handle(gate.device))
+    m, k = (int(d) for d in g2.shape)
+    y = torch.empty((m, n), dtype=gate.dtype, device=gate.device)
+    pk = _packed(module, m)
+    if pk is not None:
+        _qmv_packed(_lib.stream_handle(gate.device), m, n, k, x=g2, x2=u2, w0=pk[0], y0=y,
+                    group_size=module.group_size, xmode=1, emode=0, packed=pk[1])
+    elif module.weight is None:
+        return fallback()
+    else:
+        _lib.call("mtp_qmv_affine4_swiglu_in", g2.data_ptr(), u2.data_ptr(), module.weight.data_ptr(),
+                  module.scales.data_ptr(), module.biases.data_ptr(), None, y.data_ptr(), m, n, k,
+                  module.group_size, None, 0, _lib.stream_handle(gate.device))
     return _add_bias(y, module).reshape(*lead, n)
 
 

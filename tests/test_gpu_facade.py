@@ -53,6 +53,33 @@ def test_verify_qmv_surface(gpu):
     assert yl.shape == (4, 48) and yr.shape == (4, 48)
 
 
+@pytest.mark.parametrize("m", [4, 8])
+def test_verify_qmv_surface_on_packed_modules(gpu, m):
+    """Modules packed once (layouts 1 and 2) take the tile-major kernels
+    through the same facade calls, also after their MLX triples are released;
+    the oracle is computed from the triples before the release. m = 4 runs
+    layout 2 (16x16x32 MFMA), m = 8 layout 1."""
+    from oracle.bf16 import f32_to_bf16_bits, round_to_bf16
+    from mtplx_amd import verify_qmv as V
+    rng = np.random.default_rng(10 + m)
+    q, g, u, d = _ql(1024, 2048, 11), _ql(1024, 2048, 12), _ql(1024, 2048, 13), _ql(2048, 1024, 14)
+    ref = {name: _np(mod) for name, mod in (("q", q), ("g", g), ("u", u), ("d", d))}
+    for mod in (q, g, u, d):
+        mod.pack()
+        mod.pack(layout=2)
+        mod.release_source()
+    x = randn_bf16(rng, (m, 2048))
+    xb = bits(x)
+    assert_close(bf16_values(V.multi3_qmv4_matmul(x, q)), qmm_affine4(xb, *ref["q"], 64), what=f"packed m={m}")
+    yg, yu = V.multi3_dual_qmv4_matmul(x, g, u)
+    assert_close(bf16_values(yg), qmm_affine4(xb, *ref["g"], 64), what=f"packed dual gate m={m}")
+    assert_close(bf16_values(yu), qmm_affine4(xb, *ref["u"], 64), what=f"packed dual up m={m}")
+    gate, up = randn_bf16(rng, (m, 1024)), randn_bf16(rng, (m, 1024))
+    act = round_to_bf16(round_to_bf16(silu(bf16_values(gate))) * bf16_values(up))
+    assert_close(bf16_values(V.multi3_swiglu_down_qmv4_matmul(gate, up, d)),
+                 qmm_affine4(f32_to_bf16_bits(act.astype(np.float32)), *ref["d"], 64), what=f"packed swiglu down m={m}")
+
+
 def test_nax_patch_routes_and_counts(gpu):
     from mtplx_amd import nax_verify
     from mtplx_amd.quant import QuantizedLinear
@@ -63,6 +90,15 @@ def test_nax_patch_routes_and_counts(gpu):
     try:
         assert getattr(QuantizedLinear.__call__, "_mtplx_amd_patch", False)
         assert_close(bf16_values(q(x)), qmm_affine4(bits(x), *_np(q), 64), what="patched call")
+        # a packed module (source released) takes its pack through the patch;
+        # K = 768 is not a multiple of 512 (no verify_qmv route), so only the
+        # pack serves it
+        q2 = _ql(256, 768, 8)
+        ref = _np(q2)
+        q2.pack()
+        q2.release_source()
+        x2 = randn_bf16(rng, (4, 768))
+        assert_close(bf16_values(q2(x2)), qmm_affine4(bits(x2), *ref, 64), what="patched call on a pack")
     finally:
         nax_verify.uninstall_nax_qlinear_patch()
 
