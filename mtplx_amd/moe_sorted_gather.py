@@ -121,6 +121,23 @@ def sort_rows(x: torch.Tensor, indices: torch.Tensor, n_experts: int | None = No
     return tokens, es.row_map, es.sorted_ids, es.inv_order
 
 
+def _gather_packed(x, es: ExpertSort, rowmap, packed, n_out, group_size, max_rows):
+    """The sorted rows through an expert stack's tile-major pack (layout 1,
+    ``QuantizedLinear.pack()``), on the verify step's packed-expert kernel."""
+    R = int(es.row_map.numel())
+    K = int(x.shape[-1])
+    y = torch.empty((R, n_out), dtype=torch.bfloat16, device=x.device)
+    _lib.call("mtp_gather_qmv_affine4_packed", x.data_ptr(), _lib.ptr(rowmap), es.expert_off.data_ptr(),
+              es.active.data_ptr(), packed.data_ptr(), y.data_ptr(), max_rows, es.n_experts, n_out, K, group_size, 0,
+              n_out, _lib.stream_handle(x.device))
+    return y
+
+
+def _packable(module, N: int, K: int) -> bool:
+    return (getattr(module, "packed", None) is not None and N % 32 == 0 and K % 256 == 0
+            and int(module.group_size) in (64, 128))
+
+
 def _gather(x, x2, es: ExpertSort, rowmap, w, scales, biases, w1, s1, b1, n_out, xmode, emode, rows_per_expert,
             group_size, max_rows):
     R = int(es.row_map.numel())
@@ -189,20 +206,29 @@ def switch_linear(module: Any, x: torch.Tensor, indices: torch.Tensor, *, sorted
     ``scales``, ``biases``, ``group_size``, ``bits``, ``mode``. Unsorted indices
     are sorted on the GPU and the result returned in the caller's order."""
     _check_quant(getattr(module, "bits", 4), getattr(module, "mode", "affine"))
-    E, N = int(module.weight.shape[0]), int(module.weight.shape[-2])
+    shape = getattr(module, "_shape", None) or tuple(module.weight.shape)
+    E, N = int(shape[0]), int(shape[-2])
     lead = x.shape[:-1]
     x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    K = int(x2.shape[-1])
     ids = indices.reshape(-1)
     if int(ids.numel()) != int(x2.shape[0]):
         raise ValueError(f"switch_linear: {x2.shape[0]} rows but {ids.numel()} expert indices")
+    # An expert stack packed once (QuantizedLinear.pack()) streams its
+    # tile-major copy, also after its MLX triple is released.
+    packed = _packable(module, N, K) and x2.dtype == torch.bfloat16
+
+    def run(es, rowmap):
+        if packed:
+            return _gather_packed(x2, es, rowmap, module.packed, N, int(module.group_size), int(x2.shape[0]))
+        return _gather(x2, None, es, rowmap, module.weight, module.scales, module.biases, None, None, None, N, 0, 0,
+                       N, int(module.group_size), int(x2.shape[0]))
+
     if sorted_indices:
         es = expert_sort if expert_sort is not None else _sorted_rows(ids, E)
-        y = _gather(x2, None, es, None, module.weight, module.scales, module.biases, None, None, None, N, 0, 0, N,
-                    int(module.group_size), int(x2.shape[0]))
-        return y.reshape(*lead, N)
+        return run(es, None).reshape(*lead, N)
     es = _expert_sort(ids.reshape(-1, 1), E)
-    y = _gather(x2, None, es, es.row_map, module.weight, module.scales, module.biases, None, None, None, N, 0, 0, N,
-                int(module.group_size), int(x2.shape[0]))
+    y = run(es, es.row_map)
     return y[es.inv_order.long()].reshape(*lead, N)
 
 

@@ -161,6 +161,14 @@ def test_reference_call_sequence(gpu):
     hs = h.reshape(-1, F)[inv_order.long()].contiguous()
     y2 = switch_linear(down, hs, torch.from_numpy(idx).cuda().reshape(-1), sorted_indices=False)
     assert torch.equal(y2.reshape(T * k, H), y_unsorted.reshape(T * k, H))
+    # the same stack packed once (its MLX triple released) runs on the
+    # packed-expert kernel, sorted and unsorted, against the same oracle
+    down.pack()
+    down.release_source()
+    yp = switch_linear(down, h, sidx, sorted_indices=True)
+    assert_close(bf16_values(yp.reshape(-1, H)), want_y, what="switch_linear on a pack")
+    yp2 = switch_linear(down, hs, torch.from_numpy(idx).cuda().reshape(-1), sorted_indices=False)
+    assert torch.equal(yp2.reshape(T * k, H), yp[inv_order.long()].reshape(T * k, H))
 
 
 def test_gather_qmm_contract(gpu):
