@@ -47,6 +47,12 @@ size_t mtp_qmv_workspace_bytes(int M, int N, int K, int dual);
 int mtp_qmv_affine4(const void* x, const void* w, const void* scales, const void* biases, void* y, int M, int N,
                     int K, int group_size, void* ws, size_t ws_bytes, void* stream);
 
+/* 1 when the RoPE epilogue (emode 4 of mtp_qmv_affine4_ex) takes M rows of a
+ * K-wide x into an N-wide q|k|v projection (M <= 16, all of x in LDS), else
+ * 0. No reference counterpart: it tells the fused verify step whether the
+ * q|k|v projection can write RoPE'd rows and the K/V cache itself. */
+int mtp_qmv_rope_fusable(int M, int N, int K);
+
 /* General affine quantized matmul for the formats the MFMA kernel does not
  * take: bits 4 or 8, group_size 32, 64 or 128, any M >= 1 (launches of 8
  * rows), K a multiple of 32 and of group_size, w 16-byte aligned. Weights

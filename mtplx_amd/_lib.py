@@ -24,6 +24,7 @@ _sz = C.c_size_t
 SIGNATURES = {
     "mtp_last_error": (C.c_char_p, []),
     "mtp_qmv_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "mtp_qmv_rope_fusable": (_i, [_i, _i, _i]),
     "mtp_qmv_affine4": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "mtp_qmv_affine": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "mtp_chunk_sums": (_i, [_vp, _i, _i, _vp, _vp]),

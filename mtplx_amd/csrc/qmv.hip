@@ -150,11 +150,11 @@ static int qmm_check(int xm, int em, const QmmParams& p, const char* who) {
   }
   if (em == E_ROPE_QKV) {
     const int D = p.rope_D;
-    if (!p.packed || p.M > 8 || (xm != X_PLAIN && xm != X_RMSNORM) || !p.q_start || !p.q_out || !p.k_cache ||
+    if (!p.packed || p.M > 16 || (xm != X_PLAIN && xm != X_RMSNORM) || !p.q_start || !p.q_out || !p.k_cache ||
         !p.v_cache || D < 32 || D % 32 || p.rope_L < 1 || p.M % p.rope_L || p.rope_Hq < 1 || p.rope_Hkv < 1 ||
         p.N != (p.rope_Hq + 2 * p.rope_Hkv) * D || p.rope_cap < 1 || !(p.rope_log2_base > 0.f) ||
         (p.rope_blocked && (p.rope_cap % 32 || D != 128))) {
-      set_error("%s: RoPE epilogue needs packed weights in RoPE tile order, M<=8 (a multiple of L), plain or "
+      set_error("%s: RoPE epilogue needs packed weights in RoPE tile order, M<=16 (a multiple of L), plain or "
                 "RMSNorm x, N=(Hq+2Hkv)*D with D%%32==0, base>1, non-null q_start/q_out/caches "
                 "(blocked caches: D=128, cap%%32==0)", who);
       return MTP_ERR_ARG;
@@ -271,6 +271,12 @@ MTP_API size_t mtp_logits_topk_workspace_bytes(int M, int N) {
 MTP_API size_t mtp_logits_topk_parts_bytes(int M) {
   if (M < 1 || M > 8) return 0;
   return (size_t)M * kTopkParts * sizeof(ChunkPart);
+}
+
+MTP_API int mtp_qmv_rope_fusable(int M, int N, int K) {
+  // The RoPE epilogue (emode 4) takes up to 16 rows with all of x in LDS.
+  if (M < 1 || M > 16 || N < 1 || K < 256 || K % 256) return 0;
+  return make_plan(M, N, K).resident ? 1 : 0;
 }
 
 MTP_API size_t mtp_qmv_workspace_bytes(int M, int N, int K, int dual) {

@@ -689,7 +689,7 @@ static void launch_e(int em, const QmmParams& p, const Plan& pl, hipStream_t st)
 }
 
 
-// q|k|v with the RoPE epilogue: packed weights, R = 4 (M <= 8) only.
+// q|k|v with the RoPE epilogue: packed weights, R = 4 (M <= 8) or 8 (M <= 16).
 template <int XM>
 static void launch_rope(const QmmParams& q, const Plan& pl, hipStream_t st) {
   if (q.packed == 2) {
@@ -702,6 +702,11 @@ static void launch_rope(const QmmParams& q, const Plan& pl, hipStream_t st) {
       launch_one(qmv_stream_kernel<4, 4, XM, E_ROPE_QKV, 0, true, true, 1>, pl, 4 * 64, st, q);
     else
       launch_one(qmv_stream_kernel<4, 4, XM, E_ROPE_QKV, 0, true, true, 2>, pl, 4 * 64, st, q);
+  } else if (q.M > 8) {   // 9..16 rows: R = 8 (layout 1)
+    if (pl.nw == 8)
+      launch_one(qmv_stream_kernel<8, 8, XM, E_ROPE_QKV, 0, true>, pl, 8 * 64, st, q);
+    else
+      launch_one(qmv_stream_kernel<4, 8, XM, E_ROPE_QKV, 0, true>, pl, 4 * 64, st, q);
   } else if (pl.nw == 8) {
     launch_one(qmv_stream_kernel<8, 4, XM, E_ROPE_QKV, 0, true>, pl, 8 * 64, st, q);
   } else {

@@ -365,7 +365,8 @@ class VerifyModel:
         def qmv(stream, **kw):
             _lib.qmv_ex(stream, ws=qws, ws_bytes=qws.numel(), **kw)
 
-        fused_rope = M <= 8   # the RoPE epilogue covers up to 8 rows
+        # The RoPE epilogue covers up to 16 rows with all of x in LDS.
+        fused_rope = bool(_lib.query("mtp_qmv_rope_fusable", M, c.qkv_out, H))
         lay = 2 if M <= 4 else 1   # layout 2: the 16x16x32 MFMA form for up to 4 rows
 
         def W(q):

@@ -24,7 +24,20 @@ CASES = [  # B, L, Hq, Hkv, D, K, xmode, blocked, cap, starts, lens
     (2, 3, 4, 1, 128, 256, 0, 0, 256, [7, 0], None),
     (1, 6, 6, 2, 64, 768, 2, 0, 256, [100], [5]),           # D = 64
     (8, 1, 4, 2, 128, 1024, 0, 1, 256, [0, 1, 2, 31, 32, 63, 200, 255], None),
+    (4, 4, 32, 4, 128, 4096, 2, 1, 8192, [8000, 100, 5000, 3], None),   # 16 rows: the cfg5 step's shape
+    (2, 8, 8, 2, 128, 512, 2, 1, 256, [200, 10], [8, 5]),              # 16 rows, ragged
 ]
+
+
+@pytest.mark.gpu
+def test_rope_fusable_query(gpu):
+    """The fused form takes up to 16 rows with all of x in LDS: the cfg5
+    width (K = 4096) at 16 rows, not the 27B width (K = 5120)."""
+    from mtplx_amd import _lib
+    assert _lib.query("mtp_qmv_rope_fusable", 4, 7168, 5120) == 1
+    assert _lib.query("mtp_qmv_rope_fusable", 16, 5120, 4096) == 1
+    assert _lib.query("mtp_qmv_rope_fusable", 16, 7168, 5120) == 0
+    assert _lib.query("mtp_qmv_rope_fusable", 17, 5120, 4096) == 0
 
 
 @pytest.mark.gpu
