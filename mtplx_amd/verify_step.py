@@ -11,9 +11,10 @@ Per layer the kernels are:
   1. ``mtp_qmv_affine4_ex`` emode 4  input RMSNorm fused into the q|k|v matmul,
                                      whose epilogue applies RoPE at per-request
                                      offsets and writes K/V into the cache
-                                     (M > 8: the q|k|v matmul, then
+                                     (where the epilogue does not fit: the q|k|v matmul, then
                                      ``mtp_rope_qkv_to_cache_vt``)
-  3. ``mtp_ragged_gqa_attn_rows_vt`` ragged GQA attention (split-KV + merge)
+  3. ``mtp_ragged_gqa_attn_rows_vt`` ragged GQA attention (split-KV + merge; the balanced
+     ``mtp_ragged_gqa_attn_blocks`` for long total contexts)
   4. ``mtp_qmv_affine4_residual``    o_proj + residual add
   5. ``mtp_qmv_affine4_rmsnorm_dual`` post-attention RMSNorm + gate/up + SwiGLU
   6. ``mtp_qmv_affine4_residual``    down_proj + residual add
@@ -355,6 +356,14 @@ class VerifyModel:
         act_sums = torch.empty(((ffn + 31) // 32) * 32, dtype=torch.float32, device=dev)
         nb = _lib.query("mtp_attn_vt_workspace_bytes", B, c.n_kv_heads, self.cap)
         aws = _lib.WORKSPACES.get(nb, "attn", dev)
+        # Long total contexts (B * Hkv * cap >= 65536 key-heads: cfg5's 4 x 4 x
+        # 8k) run the balanced block attention (one workgroup per CU, equal
+        # shares of all tiles): cfg5 13.84 -> 13.70 ms per step. The cfg3 step
+        # (1 x 8 x 4k) keeps the split kernel (4.95 against 5.34 ms).
+        balanced = B * c.n_kv_heads * self.cap >= 65536
+        if balanced:
+            bnb = _lib.query("mtp_attn_blocks_workspace_bytes", B, c.n_kv_heads, self.cap, 0, 0)
+            bws = _lib.WORKSPACES.get(bnb, "attn_blocks", dev)
         scale = 1.0 / math.sqrt(c.head_dim)
         ql = None if q_lens is None else q_lens.to(torch.int32).contiguous()
         # Per-tile streaming kernel with a workspace: its leftover tiles (e.g.
@@ -386,9 +395,15 @@ class VerifyModel:
                 call("mtp_rope_qkv_to_cache_vt", qkv.data_ptr(), q_start.data_ptr(), _lib.ptr(ql), qh.data_ptr(),
                      self.k_cache[li].data_ptr(), self.v_cache[li].data_ptr(), B, Lq, c.n_heads, c.n_kv_heads,
                      c.head_dim, self.cap, ctypes.c_float(c.rope_theta), status.data_ptr(), st)
-            call("mtp_ragged_gqa_attn_rows_vt", qh.data_ptr(), self.k_cache[li].data_ptr(),
-                 self.v_cache[li].data_ptr(), q_start.data_ptr(), _lib.ptr(ql), attn.data_ptr(), B, c.n_heads,
-                 c.n_kv_heads, Lq, c.head_dim, self.cap, ctypes.c_float(scale), aws.data_ptr(), aws.numel(), st)
+            if balanced:
+                _lib.attn_blocks(st, q=qh, k_blk=self.k_cache[li], v_blk=self.v_cache[li], q_start=q_start, q_lens=ql,
+                                 row_off=None, kv_off=None, out=attn, B=B, Hq=c.n_heads, Hkv=c.n_kv_heads, Lmax=Lq,
+                                 D=c.head_dim, cap=self.cap, split_keys=0, scale=scale, total_cap=0, ws=bws,
+                                 ws_bytes=bws.numel())
+            else:
+                call("mtp_ragged_gqa_attn_rows_vt", qh.data_ptr(), self.k_cache[li].data_ptr(),
+                     self.v_cache[li].data_ptr(), q_start.data_ptr(), _lib.ptr(ql), attn.data_ptr(), B, c.n_heads,
+                     c.n_kv_heads, Lq, c.head_dim, self.cap, ctypes.c_float(scale), aws.data_ptr(), aws.numel(), st)
             qmv(st, x=attn, w0=W(L.o), resid=h, y0=h, ss_out=ss_a, M=M, N=H, K=c.n_heads * c.head_dim,
                 group_size=gs, xmode=0, emode=1, packed=lay)
             ss_h = ss_a
