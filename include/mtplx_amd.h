@@ -73,6 +73,15 @@ int mtp_qmv_affine(const void* x, const void* w, const void* scales, const void*
  * 1 <= M <= 8, K a multiple of 512; out holds K/512*32*8 floats. */
 int mtp_chunk_sums(const void* x, int M, int K, float* out, void* stream);
 
+/* The cross-row lane's matmul with its precomputed chunk sums
+ * (mtplx/verify_crossrow.py:249 crossrow_qmm(..., xsums=make_chunk_sums(x))):
+ * 4-bit affine, group 32 or 64, 1 <= M <= 8, K a multiple of 512; x bf16
+ * [M, K], xsums the mtp_chunk_sums table of x; y bf16 [M, N]. Each 32-k
+ * block's bias term b * sum(x) reads its sum from the table (two 16-value
+ * slices) instead of re-summing the staged x; otherwise as mtp_qmv_affine. */
+int mtp_crossrow_qmm(const void* x, const float* xsums, const void* w, const void* scales, const void* biases,
+                     void* y, int M, int N, int K, int group_size, void* stream);
+
 /* y = bf16(bf16(x @ W^T) + resid) — the residual add that follows o_proj and
  * down_proj in the verify forward (mlx-lm decoder layer `h + r`).
  * resid may alias y. ss_out (NULL = skip) receives, for each 32-column block
@@ -460,8 +469,11 @@ int mtp_spec_accept_parts(const void* target_parts, int n_parts, const float* dr
  * t_off[b] .. t_off[b] + K_b (n_target rows in all) and its draft rows and
  * draft ids are rows / entries d_off[b] .. d_off[b] + K_b - 1 (n_draft in
  * all); uniforms [B, K_max+1] (request b consumes at most K_b + 1); outputs
- * as above with K = K_max. Workspace: mtp_sampler_workspace_bytes(n_target +
- * n_draft, V, top_k). */
+ * as above with K = K_max. A request whose rows fall outside the buffers
+ * (K_b < 0 or K_b > K_max, t_off[b] + K_b >= n_target, d_off[b] + K_b >
+ * n_draft, or a negative offset) is checked on the device and skipped: its
+ * status is 2, its tokens and accept probabilities -1, n_accepted 0.
+ * Workspace: mtp_sampler_workspace_bytes(n_target + n_draft, V, top_k). */
 int mtp_spec_accept_ragged(const float* target_logits, int n_target, const float* draft_logits, int n_draft,
                            const int32_t* t_off, const int32_t* d_off, const int32_t* k_lens, const int32_t* draft_ids,
                            const double* uniforms, int B, int K_max, int V, double temperature, int top_k, double top_p,

@@ -281,12 +281,15 @@ __global__ __launch_bounds__(kMergeHeadThreads) void attn_merge_head_kernel(Attn
 // columns when the batch has many heads (ragged batches, a few partials per
 // head), else one per (request, kv head, query column) (few heads with many
 // partials each: the cfg3 step's 8 heads x 32 splits). MTPLX_AMD_ATTN_MERGE_HEAD=0
-// keeps the per-column form everywhere.
+// keeps the per-column form everywhere. ``per_head`` forces the per-head
+// form whatever the batch: a caller-given split length uses it, so a
+// request's merged output depends only on its own keys and the split length,
+// never on the other requests in the batch (the two forms round differently).
 constexpr int kMergeHeadMinHeads = 64;
-static void launch_merge(const AttnParams& p, int B, int Hq, int Hkv, int L, hipStream_t st) {
+static void launch_merge(const AttnParams& p, int B, int Hq, int Hkv, int L, hipStream_t st, bool per_head = false) {
   const char* v = getenv("MTPLX_AMD_ATTN_MERGE_HEAD");
   const bool off = v && *v && atoi(v) == 0;
-  if (!off && B * Hkv >= kMergeHeadMinHeads)
+  if (per_head || (!off && B * Hkv >= kMergeHeadMinHeads))
     hipLaunchKernelGGL(attn_merge_head_kernel, dim3((unsigned)(B * Hkv)), dim3(kMergeHeadThreads), 0, st, p);
   else
     hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * Hkv * (Hq / Hkv) * L)), dim3(kMergeThreads), 0, st, p);
@@ -635,6 +638,7 @@ MTP_API int mtp_ragged_gqa_attn_blocks(const mtp_attn_blocks_args* a, void* stre
   hipLaunchKernelGGL(attn_vl_kernel<1>, dim3((unsigned)units), dim3(kVtWaves * 64), 0, (hipStream_t)stream, p);
   int rc = launch_check(who);
   if (rc) return rc;
-  launch_merge(p, a->B, a->Hq, a->Hkv, a->Lmax, (hipStream_t)stream);
+  // A given split length: the per-head merge in every batch (batch-invariant rows).
+  launch_merge(p, a->B, a->Hq, a->Hkv, a->Lmax, (hipStream_t)stream, a->split_keys > 0);
   return launch_check(who);
 }

@@ -45,6 +45,15 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t* i
   }
   __syncthreads();
   if (s_bad) {
+    // An id outside [0, E): flag it and leave outputs that index only inside
+    // their buffers (identity order, empty expert ranges), so a consumer that
+    // does not check the flag reads valid rows and runs no expert.
+    for (int i = tid; i < R; i += kSortThreads) {
+      row_map[i] = (uint32_t)(i / top_k);
+      sorted_ids[i] = 0;
+      inv_order[i] = (uint32_t)i;
+    }
+    for (int e = tid; e <= E; e += kSortThreads) expert_off[e] = 0;
     if (tid == 0) active[0] = -1;
     return;
   }
@@ -245,7 +254,8 @@ __global__ __launch_bounds__(kSortThreads) void moe_segments_kernel(const int32_
     if (e < 0 || e >= E || (i > 0 && sorted_ids[i - 1] > e)) s_bad = 1;
   }
   __syncthreads();
-  if (s_bad) {
+  if (s_bad) {   // empty expert ranges: a consumer that does not check the flag runs no expert
+    for (int e = tid; e <= E; e += kSortThreads) expert_off[e] = 0;
     if (tid == 0) active[0] = -1;
     return;
   }

@@ -388,7 +388,12 @@ static RowsPlan rows_plan(int M, int N, int K, int dual) {
   pl.groups = dual ? cdiv(ntiles, 2) : cdiv(ntiles, 4);
   const int cus = device_cus();
   const int Q = K >> 8;
-  const int R2 = M > 32 ? 2 : 1;
+  // The plan depends on N, K and the CU count only, never on M: a row's
+  // sums then run in the same order (same K parts, same part sums) at any M,
+  // so a request's outputs are bit-identical alone and inside a batch. The
+  // partial-sum cap below is sized for the 64-row partials.
+  (void)M;
+  const int R2 = 2;
   const int E = pl.groups % cus;
   pl.full = pl.groups - E;
   pl.split = 1;

@@ -33,6 +33,11 @@ struct GenericArgs {
   const uint16_t* b;
   uint16_t* y;
   float* yf;
+  // Optional chunk-sum table of the cross-row lane (mtp_chunk_sums layout:
+  // [(kb*32 + lane)*8 + m] = sum of x[m, kb*512 + lane*16 .. +16)); when
+  // given, each 32-k block sum is read from it (two 16-value slices) instead
+  // of being summed from the staged x.
+  const float* xsums;
   int M, N, K, gs, ldx, ldy;
 };
 
@@ -69,9 +74,14 @@ __global__ __launch_bounds__(256) void qmv_generic_kernel(GenericArgs a) {
     __syncthreads();
     for (int i = tid; i < M * nblk; i += 256) {
       const int m = i / nblk, blk = i - m * nblk;
-      const float* xp = &xs[m][blk * 33];
       float t = 0.f;
-      for (int j = 0; j < 32; ++j) t += xp[j];
+      if (a.xsums) {   // k0 is a multiple of 512: chunk kb = k0 / 512, slices 2 blk and 2 blk + 1
+        const float* cs = a.xsums + ((size_t)(k0 >> 9) * 32 + 2 * blk) * 8 + m;
+        t = cs[0] + cs[8];
+      } else {
+        const float* xp = &xs[m][blk * 33];
+        for (int j = 0; j < 32; ++j) t += xp[j];
+      }
       xsum[m][blk] = t;
     }
     __syncthreads();
@@ -151,9 +161,9 @@ __global__ __launch_bounds__(256) void chunk_sums_kernel(const uint16_t* x, int 
 
 using namespace mtp;
 
-MTP_API int mtp_qmv_affine(const void* x, const void* w, const void* scales, const void* biases, void* y, void* yf,
-                           int M, int N, int K, int group_size, int bits, void* stream) {
-  const char* who = "mtp_qmv_affine";
+static int qmv_affine_run(const void* x, const float* xsums, const void* w, const void* scales, const void* biases,
+                          void* y, void* yf, int M, int N, int K, int group_size, int bits, void* stream,
+                          const char* who) {
   if (!x || !w || !scales || !biases || (!y && !yf) || M < 1 || N < 1 || K < 32 || K % 32) {
     set_error("%s: bad arguments (non-null x/w/scales/biases/output, M, N >= 1, K a positive multiple of 32)", who);
     return MTP_ERR_ARG;
@@ -180,6 +190,7 @@ MTP_API int mtp_qmv_affine(const void* x, const void* w, const void* scales, con
     a.b = (const uint16_t*)biases;
     a.y = y ? (uint16_t*)y + (size_t)r0 * N : nullptr;
     a.yf = yf ? (float*)yf + (size_t)r0 * N : nullptr;
+    a.xsums = xsums;   // (M <= 8 when given: one launch)
     a.M = (M - r0) < kGenRows ? (M - r0) : kGenRows;
     a.N = N;
     a.K = K;
@@ -194,6 +205,26 @@ MTP_API int mtp_qmv_affine(const void* x, const void* w, const void* scales, con
     if (rc) return rc;
   }
   return MTP_OK;
+}
+
+MTP_API int mtp_qmv_affine(const void* x, const void* w, const void* scales, const void* biases, void* y, void* yf,
+                           int M, int N, int K, int group_size, int bits, void* stream) {
+  return qmv_affine_run(x, nullptr, w, scales, biases, y, yf, M, N, K, group_size, bits, stream, "mtp_qmv_affine");
+}
+
+MTP_API int mtp_crossrow_qmm(const void* x, const float* xsums, const void* w, const void* scales,
+                             const void* biases, void* y, int M, int N, int K, int group_size, void* stream) {
+  const char* who = "mtp_crossrow_qmm";
+  if (!xsums || M < 1 || M > kGenRows || K < 512 || K % 512) {
+    set_error("%s: need the chunk-sum table (mtp_chunk_sums), 1 <= M <= %d and K a positive multiple of 512", who,
+              kGenRows);
+    return MTP_ERR_ARG;
+  }
+  if (group_size != 32 && group_size != 64) {
+    set_error("%s: group_size %d unsupported (the cross-row lane takes 32 or 64)", who, group_size);
+    return MTP_ERR_UNSUPPORTED;
+  }
+  return qmv_affine_run(x, xsums, w, scales, biases, y, nullptr, M, N, K, group_size, 4, stream, who);
 }
 
 MTP_API int mtp_chunk_sums(const void* x, int M, int K, float* out, void* stream) {

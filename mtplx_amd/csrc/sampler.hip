@@ -315,10 +315,31 @@ struct AcceptRows {
   const int32_t* d_off;
   const int32_t* k_lens;
   int nt;   // target rows in all (the draft rows follow them)
+  int nd;   // draft rows (and draft ids) in all
 };
 __device__ __forceinline__ int req_k(const AcceptRows& r, int b, int K) { return r.k_lens ? r.k_lens[b] : K; }
 __device__ __forceinline__ int req_t(const AcceptRows& r, int b, int K) { return r.t_off ? r.t_off[b] : b * (K + 1); }
 __device__ __forceinline__ int req_d(const AcceptRows& r, int b, int K) { return r.d_off ? r.d_off[b] : b * K; }
+
+// Whether request b's rows lie inside the buffers: 0 <= K_b <= K, its K_b + 1
+// target rows inside the nt target rows and its K_b draft rows inside the nd
+// draft rows. The offsets of a ragged batch are device data the host never
+// reads, so every accept kernel checks them before touching a row: a request
+// that fails gets status 2, tokens and accept probabilities -1 and no accepted
+// drafts, and nothing of it is read or written past its own output rows.
+__device__ __forceinline__ bool req_in_bounds(const AcceptRows& r, int Kb, int tb, int db, int K) {
+  return Kb >= 0 && Kb <= K && tb >= 0 && (long long)tb + Kb < (long long)r.nt && db >= 0 &&
+         (long long)db + Kb <= (long long)r.nd;
+}
+
+// Outputs of a request whose rows fail req_in_bounds (one thread writes them).
+__device__ __forceinline__ void req_reject(int b, int K, int32_t* out_tokens, int32_t* n_accepted,
+                                           double* accept_probs, int32_t* status) {
+  for (int d = 0; d <= K; ++d) out_tokens[(size_t)b * (K + 1) + d] = -1;
+  for (int d = 0; d < K; ++d) accept_probs[(size_t)b * K + d] = -1.0;
+  n_accepted[b] = 0;
+  status[b] = 2;
+}
 
 __device__ double law_prob(const RowLaw& L, int tok) {
   for (int i = 0; i < L.n; ++i)
@@ -358,6 +379,10 @@ __global__ __launch_bounds__(64) void accept_finish(const ChunkPart* __restrict_
   const int b = blockIdx.x;
   const int lane = threadIdx.x;
   const int Kb = req_k(rr, b, K), tb = req_t(rr, b, K), db = req_d(rr, b, K);
+  if (!req_in_bounds(rr, Kb, tb, db, K)) {   // uniform over the block
+    if (lane == 0) req_reject(b, K, out_tokens, n_accepted, accept_probs, status);
+    return;
+  }
   __shared__ RowLaw s_p, s_q;
   __shared__ uint64_t s_sel[kMaxTopK];
   __shared__ int s_done, s_ui, s_nacc;
@@ -713,6 +738,10 @@ __global__ __launch_bounds__(1024) void accept_laws(const ChunkPart* __restrict_
   const int nwv = blockDim.x >> 6;
   const int wave = threadIdx.x >> 6;
   const int Kb = req_k(rr, b, K), tb = req_t(rr, b, K), db = req_d(rr, b, K);
+  if (!req_in_bounds(rr, Kb, tb, db, K)) {   // uniform over the block
+    if (threadIdx.x == 0) req_reject(b, K, out_tokens, n_accepted, accept_probs, status);
+    return;
+  }
   const int nlaw = 2 * Kb + 1;
   RowLaw* laws = reinterpret_cast<RowLaw*>(s_lds);   // sized for 2K + 1 laws
   uint64_t* keys = reinterpret_cast<uint64_t*>(s_lds + (size_t)(2 * K + 1) * sizeof(RowLaw)) + (size_t)wave * kLawKeys;
@@ -1110,6 +1139,10 @@ __global__ __launch_bounds__(kWideThreads) void wide_accept_kernel(
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const int Kb = req_k(rr, b, K), tb = req_t(rr, b, K), db = req_d(rr, b, K);
+  if (!req_in_bounds(rr, Kb, tb, db, K)) {   // uniform over the block
+    if (tid == 0) req_reject(b, K, out_tokens, n_accepted, accept_probs, status);
+    return;
+  }
   const int nt = rr.t_off ? rr.nt : B * (K + 1);
   __shared__ double s_d[kWideWaves];
   __shared__ double s_last, s_p, s_q;
@@ -1289,6 +1322,7 @@ static int spec_accept_run(const float* target_logits, const float* draft_logits
   const ChunkPart* tread = target_ready ? reinterpret_cast<const ChunkPart*>(target_parts) : tparts;
   const double temp = pl.greedy ? 1.0 : temperature;
   rr.nt = nt;
+  rr.nd = nd;
   if (target_ready) {   // the target rows' partials are in ws already: the draft rows only
     if (nd > 0) {
       hipLaunchKernelGGL(vocab_partials, dim3(n_chunks, nd), dim3(kSampThreads), 0, st, draft_logits, draft_logits,
@@ -1369,7 +1403,7 @@ MTP_API int mtp_spec_accept_ragged(const float* target_logits, int n_target, con
     set_error("mtp_spec_accept_ragged: t_off, d_off and k_lens are required");
     return MTP_ERR_ARG;
   }
-  AcceptRows rr{t_off, d_off, k_lens, n_target};
+  AcceptRows rr{t_off, d_off, k_lens, n_target, n_draft};
   return spec_accept_run(target_logits, draft_logits, draft_ids, uniforms, B, K_max, V, temperature, top_k, top_p,
                          out_tokens, n_accepted, accept_probs, status, ws, ws_bytes, stream, rr, n_target, n_draft,
                          "mtp_spec_accept_ragged");

@@ -19,10 +19,19 @@ Mapping onto :class:`~mtplx_amd.verify_step.VerifyModel` (exact: rows are
 independent, so stacking quantized rows changes no value): q|k|v rows are
 stacked into one projection; each expert's gate and up rows into one
 ``[E, 2F, K/8]`` pack; the router's E rows and the shared-expert gate's row
-into one ``[E+1, H]`` projection. Tensors the verify forward has no use for
-are refused (``strict``), except the MTP draft head (``mtp.*``), which the
-verify step does not run. Reading is CPU-only; :func:`load_verify_model`
-moves the weights to the GPU and packs them there.
+into one ``[E+1, H]`` projection.
+
+Tensors the verify forward does not read are refused unless they cannot change
+its logits: the MTP draft head (``mtp.*``) is always skipped, and with
+``strict=False`` so are rotary ``inv_freq`` buffers and a multimodal pack's
+vision tower and projector. Anything else left over (e.g. Qwen3's per-head
+``q_norm``/``k_norm``, projection biases) is part of the decoder's math that
+this forward does not apply, so it is refused whatever ``strict`` says.
+
+Shards are opened lazily (``safetensors.safe_open``) and read one layer at a
+time: :func:`load_verify_model` uploads and packs each layer on the GPU before
+reading the next, so host memory holds one layer's tensors (plus the
+embedding and lm_head), not the whole pack.
 """
 
 from __future__ import annotations
@@ -79,13 +88,52 @@ def shard_files(path: Path) -> list[Path]:
     return files
 
 
-def read_tensors(path: Path) -> dict[str, torch.Tensor]:
-    from safetensors.torch import load_file
+class LazyTensors:
+    """Read-only mapping name -> CPU tensor over a pack's shards; a tensor is
+    read from its shard when it is looked up, not before."""
 
-    out: dict[str, torch.Tensor] = {}
-    for f in shard_files(path):
-        out.update(load_file(str(f), device="cpu"))
-    return out
+    def __init__(self, files: list[Path]):
+        from safetensors import safe_open
+
+        self._handles = []
+        self._where: dict[str, Any] = {}
+        for f in files:
+            h = safe_open(str(f), framework="pt", device="cpu")
+            self._handles.append(h)
+            for k in h.keys():
+                self._where[k] = h
+
+    def __contains__(self, key: str) -> bool:
+        return key in self._where
+
+    def __getitem__(self, key: str) -> torch.Tensor:
+        h = self._where.get(key)
+        if h is None:
+            raise KeyError(key)
+        return h.get_tensor(key)
+
+    def __iter__(self):
+        return iter(self._where)
+
+    def keys(self):
+        return self._where.keys()
+
+
+def read_tensors(path: Path) -> LazyTensors:
+    return LazyTensors(shard_files(path))
+
+
+# Names a verify forward may skip without changing its logits (strict=False):
+# rotary frequency buffers (the forward computes its own from rope_theta) and
+# the vision side of a multimodal pack (the verify rows are text tokens).
+_IGNORABLE_PARTS = ("rotary_emb.inv_freq",)
+_IGNORABLE_PREFIXES = ("vision_tower.", "visual.", "model.visual.", "multi_modal_projector.", "model.vision_tower.",
+                       "model.multi_modal_projector.")
+
+
+def _ignorable(key: str, outer: str) -> bool:
+    k = key[len(outer):] if outer and key.startswith(outer) else key
+    return any(p in k for p in _IGNORABLE_PARTS) or any(k.startswith(p) for p in _IGNORABLE_PREFIXES)
 
 
 def decoder_config(config: dict) -> DecoderConfig:
@@ -169,10 +217,11 @@ def _stack(parts_list, dim: int):
     return tuple(torch.cat([p[i] for p in parts_list], dim=dim) for i in range(3)) + (parts_list[0][3],)
 
 
-def read_mlx_pack(path, *, strict: bool = True) -> tuple[DecoderConfig, dict]:
-    """Parse a pack on the CPU: (config, weights in the verify model's
-    structure as CPU tensors: ``embed``/``lm_head``/per-layer triples
-    ``(weight int32, scales, biases, group_size)``, norm weights)."""
+def _walk(path, strict: bool, on_layer=None) -> tuple[DecoderConfig, dict]:
+    """Parse a pack on the CPU into the verify model's structure. Each layer's
+    dict (norm weights and triples ``(weight int32, scales, biases,
+    group_size)``) goes to ``on_layer(i, layer)`` as soon as it is read, whose
+    return value is kept in its place (``None``: the layer dict itself)."""
     path = Path(path)
     config = json.loads((path / "config.json").read_text())
     cfg = decoder_config(config)
@@ -182,8 +231,18 @@ def read_mlx_pack(path, *, strict: bool = True) -> tuple[DecoderConfig, dict]:
         raise PackError("no embed_tokens.weight in the pack")
     prefix = emb_keys[0][: -len("embed_tokens.weight")]          # e.g. "model."
     outer = prefix[: -len("model.")] if prefix.endswith("model.") else ""
+    # Refuse leftovers before reading any weight: names are all it takes.
     r = _Reader(tensors, quantization(config), outer, cfg.group_size)
     m = prefix[len(outer):]
+    expected = _expected_names(cfg, outer + m, outer, config)
+    left = sorted(k for k in tensors.keys() if k not in expected and not k.startswith(outer + "mtp."))
+    math = [k for k in left if not _ignorable(k, outer)]
+    if math:
+        raise PackError(f"{len(math)} tensors change the decoder's math but the verify forward does not apply them, "
+                        f"e.g. {math[:4]}")
+    if strict and left:
+        raise PackError(f"{len(left)} tensors the verify forward does not use, e.g. {left[:4]} (strict=False "
+                        "ignores rotary buffers and a vision tower)")
     out: dict[str, Any] = {"embed": r.triple(m + "embed_tokens"), "layers": []}
     for i in range(cfg.layers):
         p = f"{m}layers.{i}."
@@ -199,13 +258,16 @@ def read_mlx_pack(path, *, strict: bool = True) -> tuple[DecoderConfig, dict]:
             lay["router"] = _stack([router, sgate], 0)
             g, u = r.triple(p + "mlp.switch_mlp.gate_proj"), r.triple(p + "mlp.switch_mlp.up_proj")
             lay["expert_gate_up"] = _stack([g, u], 1)
+            del g, u
             lay["expert_down"] = r.triple(p + "mlp.switch_mlp.down_proj")
             for n in ("gate", "up", "down"):
                 lay[f"shared_{n}"] = r.triple(p + f"mlp.shared_expert.{n}_proj")
         else:
             for n in ("gate", "up", "down"):
                 lay[n] = r.triple(p + f"mlp.{n}_proj")
-        out["layers"].append(lay)
+        kept = on_layer(i, lay) if on_layer is not None else None
+        out["layers"].append(lay if kept is None else kept)
+        del lay
     out["final_norm"] = r.norm(m + "norm")
     if (outer + "lm_head.weight") in tensors:
         out["lm_head"] = r.triple("lm_head")
@@ -213,26 +275,57 @@ def read_mlx_pack(path, *, strict: bool = True) -> tuple[DecoderConfig, dict]:
         out["lm_head"] = out["embed"]
     else:
         raise PackError("no lm_head and the embeddings are not tied")
-    left = sorted(k for k in tensors if k not in r.used and not k.startswith(outer + "mtp."))
-    if strict and left:
-        raise PackError(f"{len(left)} tensors the verify forward does not use, e.g. {left[:4]} (strict=False "
-                        "ignores them)")
     return cfg, out
+
+
+def _expected_names(cfg: DecoderConfig, m: str, outer: str, config: dict) -> set[str]:
+    """Every tensor name the verify forward reads from a pack of ``cfg``."""
+    names: set[str] = set()
+
+    def tri(n):
+        names.update(n + x for x in (".weight", ".scales", ".biases"))
+
+    tri(m + "embed_tokens")
+    for i in range(cfg.layers):
+        p = f"{m}layers.{i}."
+        names.update({p + "input_layernorm.weight", p + "post_attention_layernorm.weight"})
+        for n in ("q", "k", "v", "o"):
+            tri(p + f"self_attn.{n}_proj")
+        if cfg.n_experts:
+            tri(p + "mlp.gate")
+            tri(p + "mlp.shared_expert_gate")
+            for n in ("gate", "up", "down"):
+                tri(p + f"mlp.switch_mlp.{n}_proj")
+                tri(p + f"mlp.shared_expert.{n}_proj")
+        else:
+            for n in ("gate", "up", "down"):
+                tri(p + f"mlp.{n}_proj")
+    names.add(m + "norm.weight")
+    tri(outer + "lm_head")
+    return names
+
+
+def read_mlx_pack(path, *, strict: bool = True) -> tuple[DecoderConfig, dict]:
+    """Parse a pack on the CPU: (config, weights in the verify model's
+    structure as CPU tensors: ``embed``/``lm_head``/per-layer triples
+    ``(weight int32, scales, biases, group_size)``, norm weights)."""
+    return _walk(path, strict)
 
 
 def load_verify_model(path, *, device="cuda", strict: bool = True) -> VerifyModel:
     """A :class:`VerifyModel` over the pack's weights (on ``device``, packed
     for the streaming kernels; routing without the synthetic skew)."""
-    cfg, w = read_mlx_pack(path, strict=strict)
-    layers = []
-    for lw in w["layers"]:
+    def upload(i, lw):
         L = Layer(in_norm=lw["in_norm"].to(device), qkv=_ql(lw["qkv"], device), o=_ql(lw["o"], device),
                   post_norm=lw["post_norm"].to(device))
         for name in ("gate", "up", "down", "router", "expert_gate_up", "expert_down", "shared_gate", "shared_up",
                      "shared_down"):
             if name in lw:
                 setattr(L, name, _ql(lw[name], device))
-        layers.append(L)
+        return L   # the CPU copies of this layer are dropped here
+
+    cfg, w = _walk(path, strict, upload)
+    layers = w["layers"]
     embed = _ql(w["embed"], device)
     lm_head = embed if w["lm_head"] is w["embed"] else _ql(w["lm_head"], device)
     return VerifyModel.from_weights(cfg, embed, layers, w["final_norm"].to(device), lm_head, device=device)

@@ -63,9 +63,16 @@ class ExpertSort:
     sorted_ids: torch.Tensor   # [R] expert of sorted row i (ascending)
     inv_order: torch.Tensor    # [R] sorted position of flat row j
     expert_off: torch.Tensor   # int32 [E+1]
-    active: torch.Tensor       # int32 [1+E]: count, then active experts
+    active: torch.Tensor       # int32 [1+E]: count, then active experts; count -1: invalid ids
     top_k: int
     n_experts: int
+
+    def check(self) -> None:
+        """Raise ``ValueError`` if the sort flagged its ids (an id outside
+        ``[0, n_experts)``, or a descent where ascending ids were promised).
+        Synchronises with the device; the sort itself never does."""
+        if int(self.active[0].item()) < 0:
+            raise ValueError(f"expert ids outside [0, {self.n_experts}) or not ascending")
 
 
 def expert_sort(indices: torch.Tensor, n_experts: int) -> ExpertSort:
@@ -102,20 +109,27 @@ def segments(sorted_ids: torch.Tensor, n_experts: int) -> tuple[torch.Tensor, to
 
 def _sorted_rows(rhs_indices: torch.Tensor, n_experts: int, top_k: int = 1) -> ExpertSort:
     """An :class:`ExpertSort` view of rows whose expert ids are already sorted
-    (the ``sorted_indices=True`` contract); raises on unsorted or out-of-range ids."""
+    (the ``sorted_indices=True`` contract). No host synchronisation: ids that
+    do not ascend inside ``[0, n_experts)`` are flagged on the device
+    (``ExpertSort.check``) and the gathered matmul then runs no expert, so its
+    (zero-filled) output stays zero."""
     ids = rhs_indices.reshape(-1).to(torch.int32).contiguous()
     off, active = segments(ids, n_experts)
-    if int(active[0].item()) < 0:
-        raise ValueError(f"sorted indices must ascend within [0, {n_experts})")
     R = int(ids.numel())
     ar = torch.arange(R, dtype=torch.int32, device=ids.device)
     return ExpertSort(ar, ids, ar, off, active, top_k, n_experts)
 
 
+SORT_MAX_EXPERTS = 4096   # the single-workgroup counting sort's bound (mtp_moe_sort)
+
+
 def sort_rows(x: torch.Tensor, indices: torch.Tensor, n_experts: int | None = None):
     """``(tokens [n,1,K], row_map, sorted_indices, inv_order)`` exactly as
-    ``mtplx/moe_sorted_gather.py:221-238`` (stable sort of the flattened ids)."""
-    E = int(n_experts) if n_experts is not None else int(indices.max().item()) + 1
+    ``mtplx/moe_sorted_gather.py:221-238`` (stable sort of the flattened ids).
+    Without ``n_experts`` the sort counts over ``SORT_MAX_EXPERTS`` bins, so
+    the call never waits on the device; an id outside that range is flagged
+    on the device and leaves the identity order."""
+    E = int(n_experts) if n_experts is not None else SORT_MAX_EXPERTS
     es = expert_sort(indices, E)
     tokens = x.reshape(-1, 1, x.shape[-1])
     return tokens, es.row_map, es.sorted_ids, es.inv_order
@@ -126,7 +140,7 @@ def _gather_packed(x, es: ExpertSort, rowmap, packed, n_out, group_size, max_row
     ``QuantizedLinear.pack()``), on the verify step's packed-expert kernel."""
     R = int(es.row_map.numel())
     K = int(x.shape[-1])
-    y = torch.empty((R, n_out), dtype=torch.bfloat16, device=x.device)
+    y = torch.zeros((R, n_out), dtype=torch.bfloat16, device=x.device)   # flagged sort: zeros
     _lib.call("mtp_gather_qmv_affine4_packed", x.data_ptr(), _lib.ptr(rowmap), es.expert_off.data_ptr(),
               es.active.data_ptr(), packed.data_ptr(), y.data_ptr(), max_rows, es.n_experts, n_out, K, group_size, 0,
               n_out, _lib.stream_handle(x.device))
@@ -142,7 +156,8 @@ def _gather(x, x2, es: ExpertSort, rowmap, w, scales, biases, w1, s1, b1, n_out,
             group_size, max_rows):
     R = int(es.row_map.numel())
     K = int(x.shape[-1])
-    y = torch.empty((R, n_out), dtype=torch.bfloat16, device=x.device)
+    # zero-filled: rows of a flagged sort (no expert runs) read as zeros
+    y = torch.zeros((R, n_out), dtype=torch.bfloat16, device=x.device)
     ptr = _lib.ptr
     _lib.call("mtp_gather_qmv_affine4", x.data_ptr(), ptr(x2), ptr(rowmap), es.expert_off.data_ptr(),
               es.active.data_ptr(), w.data_ptr(), scales.data_ptr(), biases.data_ptr(), ptr(w1), ptr(s1), ptr(b1),
@@ -323,3 +338,187 @@ def route(router_logits: torch.Tensor, top_k: int, skew: torch.Tensor | None = N
     _lib.call("mtp_moe_route", lg.data_ptr(), int(lg.stride(0)), _lib.ptr(sk), T, E, top_k, ids.data_ptr(),
               wts.data_ptr(), _lib.stream_handle(lg.device))
     return ids, wts
+
+
+# ---------------------------------------------------------------------------
+# The mlx-lm switch layers the reference patches (``mlx_lm.models.switch_layers``
+# ``QuantizedSwitchLinear`` / ``SwitchGLU`` / ``SwiGLU``), restated on torch
+# tensors with their call contracts, and the reference's idempotent patches
+# of them (``mtplx/moe_sorted_gather.py:359-481``).
+
+_GUARD_MARK = "_mtplx_switch_linear_guard"
+_GLU_MARK = "_mtplx_switch_glu_rows"
+# Routed rows from which the sorted chain runs on the row-map kernel (the
+# caller regime's threshold, ``mtplx/models/qwen4_exp.py:1548``; the
+# reference's Apple kernel needs 4096+, ``kernels/moe_sorted_gather_nax.py:86``).
+SWITCH_GLU_MIN_ROWS = 64
+
+
+def _silu(x: torch.Tensor) -> torch.Tensor:
+    return torch.nn.functional.silu(x)
+
+
+class SwiGLU:
+    """``activation(x, gate) = silu(gate) * x`` (mlx-lm's SwiGLU)."""
+
+    def __call__(self, x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        return _silu(gate) * x
+
+
+class QuantizedSwitchLinear:
+    """Expert-stacked 4-bit affine projection: ``weight`` ``[E, N, K/8]``,
+    ``scales`` / ``biases`` ``[E, N, K/gs]``. ``module(x, indices,
+    sorted_indices=False)`` is ``gather_qmm(x, w, s, b, rhs_indices=indices,
+    transpose=True)`` (+ the expert's bias row), mlx-lm's contract."""
+
+    def __init__(self, weight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int = 64,
+                 bits: int = 4, mode: str = "affine", bias: torch.Tensor | None = None):
+        self.weight = weight.view(torch.int32) if weight.dtype == torch.uint32 else weight
+        self.scales = scales
+        self.biases = biases
+        self.group_size = int(group_size)
+        self.bits = int(bits)
+        self.mode = mode
+        self.bias = bias
+        self.packed = None
+        self._shape = tuple(int(d) for d in self.weight.shape)
+        self.training = False
+
+    def __contains__(self, name: str) -> bool:
+        return getattr(self, name, None) is not None
+
+    def __call__(self, x: torch.Tensor, indices: torch.Tensor, sorted_indices: bool = False) -> torch.Tensor:
+        y = gather_qmm(x, self.weight, self.scales, self.biases, rhs_indices=indices, transpose=True,
+                       group_size=self.group_size, bits=self.bits, mode=self.mode, sorted_indices=sorted_indices)
+        if self.bias is not None:
+            y = y + self.bias[indices.long()].unsqueeze(-2)
+        return y
+
+
+class SwitchGLU:
+    """mlx-lm's ``SwitchGLU``: ``down(activation(up(x), gate(x)))`` per routed
+    expert; from 64 routed rows the rows are expert-sorted first and the
+    result unsorted (``_gather_sort`` / ``_scatter_unsort``)."""
+
+    def __init__(self, gate_proj: QuantizedSwitchLinear, up_proj: QuantizedSwitchLinear,
+                 down_proj: QuantizedSwitchLinear, activation=None):
+        self.gate_proj, self.up_proj, self.down_proj = gate_proj, up_proj, down_proj
+        self.activation = activation if activation is not None else SwiGLU()
+        self.training = False
+
+    def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        x = x.unsqueeze(-2).unsqueeze(-2)                     # [..., 1, 1, D]
+        do_sort = int(indices.numel()) >= 64
+        idx, inv = indices, None
+        if do_sort:
+            top_k = int(indices.shape[-1])
+            flat = indices.reshape(-1)
+            es = expert_sort(flat.reshape(-1, 1), int(self.gate_proj._shape[0]))
+            rows = x.reshape(-1, 1, int(x.shape[-1]))
+            # sorting [R, 1] ids: row_map is the flat position, whose token row is position // top_k
+            x = rows[es.row_map.long() // top_k]
+            idx, inv = es.sorted_ids, es.inv_order
+        x_up = self.up_proj(x, idx, sorted_indices=do_sort)
+        x_gate = self.gate_proj(x, idx, sorted_indices=do_sort)
+        y = self.down_proj(self.activation(x_up, x_gate), idx, sorted_indices=do_sort)
+        if do_sort:
+            y = y[inv.long()].reshape(*indices.shape, *y.shape[-2:])
+        return y.squeeze(-2)
+
+
+def install_switch_linear_guard(cls=None) -> bool:
+    """The reference's row-pad guard around the quantized switch linear's
+    ``__call__`` (``mtplx/moe_sorted_gather.py:359-397``). It is a no-op
+    wherever :func:`guard_active` is false, which is everywhere here (the
+    gfx950 gathers count rows in 32 bits), so nothing is installed and False
+    is returned, as the reference does off its affected MLX releases. Where
+    the guard were active it wraps ``cls.__call__`` once (marker attribute)."""
+    if not guard_active():
+        return False
+    cls = QuantizedSwitchLinear if cls is None else cls
+    current = cls.__call__
+    if getattr(current, _GUARD_MARK, False):
+        return True
+
+    def guarded_call(self, x, indices, sorted_indices=False):
+        if sorted_indices:
+            pad = pad_rows(int(indices.shape[0]))
+            if pad:
+                rows = int(indices.shape[0])
+                xp = torch.cat([x, x[-1:].expand(pad, *x.shape[1:])], 0)
+                ip = torch.cat([indices, indices[-1:].expand(pad)], 0)
+                _STATS["padded_calls"] += 1
+                _STATS["padded_rows"] += pad
+                return current(self, xp, ip, sorted_indices=True)[:rows]
+        return current(self, x, indices, sorted_indices=sorted_indices)
+
+    setattr(guarded_call, _GUARD_MARK, True)
+    cls.__call__ = guarded_call
+    return True
+
+
+def _glu_projections(module: Any):
+    """The gate and up projections of a quantized ``SwitchGLU`` with the
+    SwiGLU activation and no bias (same group size and bits), else None."""
+    if type(getattr(module, "activation", None)) is not SwiGLU:
+        return None
+    gate, up = getattr(module, "gate_proj", None), getattr(module, "up_proj", None)
+    for proj in (gate, up):
+        if not isinstance(proj, QuantizedSwitchLinear) or proj.bias is not None or proj.mode != "affine" or \
+                proj.weight is None:
+            return None
+    if gate.group_size != up.group_size or gate.bits != up.bits or gate.bits != 4 or gate._shape != up._shape:
+        return None
+    return gate, up
+
+
+def switch_glu_rows(module: Any, x: torch.Tensor, indices: torch.Tensor, original) -> torch.Tensor:
+    """``SwitchGLU.__call__`` with its sorted regime on the row-map kernel
+    (``mtplx/moe_sorted_gather.py:420``): the rows are sorted as the stock
+    call sorts them, the gate and up gathers and ``silu(gate) * up`` run as
+    one kernel reading each token row in place through the sort's row map
+    (``mtp_gather_qmv_affine4`` emode 3 over the separate gate and up
+    stacks), then the down projection with sorted indices and the unsort.
+    Training, fewer than ``SWITCH_GLU_MIN_ROWS`` routed rows, another
+    activation or layout run ``original``."""
+    if getattr(module, "training", False) or int(indices.numel()) < SWITCH_GLU_MIN_ROWS:
+        return original(module, x, indices)
+    projections = _glu_projections(module)
+    if projections is None or x.dtype != torch.bfloat16 or not x.is_cuda:
+        return original(module, x, indices)
+    gate, up = projections
+    E, F = int(gate._shape[0]), int(gate._shape[1])
+    K = int(x.shape[-1])
+    if K % 256 or int(gate.group_size) not in (64, 128):
+        return original(module, x, indices)
+    top_k = int(indices.shape[-1])
+    es = expert_sort(indices.reshape(-1, top_k), E)
+    rows = x.reshape(-1, K).contiguous()
+    R = int(es.row_map.numel())
+    h = _gather(rows, None, es, es.row_map, gate.weight, gate.scales, gate.biases, up.weight, up.scales, up.biases,
+                F, 0, 3, F, int(gate.group_size), R)
+    y = module.down_proj(h.reshape(R, 1, F), es.sorted_ids, sorted_indices=True)
+    y = y[es.inv_order.long()]
+    return y.reshape(*indices.shape, *y.shape[-2:]).squeeze(-2)
+
+
+def install_switch_glu_rows(cls=None) -> bool:
+    """Route ``SwitchGLU.__call__`` through :func:`switch_glu_rows`
+    (``mtplx/moe_sorted_gather.py:458-481``): wraps the class's current call
+    once (marker attribute ``_mtplx_switch_glu_rows``), so a second install
+    is a no-op. Returns whether it is installed."""
+    from . import _lib
+
+    _lib.load()   # the row-map kernel lives in the HIP library; raises when it is missing
+    cls = SwitchGLU if cls is None else cls
+    current = cls.__call__
+    if getattr(current, _GLU_MARK, False):
+        return True
+
+    def rows_call(self, x, indices):
+        return switch_glu_rows(self, x, indices, current)
+
+    setattr(rows_call, _GLU_MARK, True)
+    rows_call.__wrapped__ = current
+    cls.__call__ = rows_call
+    return True

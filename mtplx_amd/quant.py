@@ -94,10 +94,18 @@ class QuantizedLinear:
         return getattr(self, name, None) is not None
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        """``x @ W.T (+ bias)``: on the layer's tile-major packs when it has
+        them (past 32 rows the layout-1 pack, made here on first use), else
+        on the MLX triple."""
         from .verify_kernels import quantized_matmul
+        from .verify_qmv import packed_matmul
 
+        y = packed_matmul(x, self)
+        if y is not None:
+            return y
         if self.weight is None:
-            raise RuntimeError("the layer's source weights were released; call the packed kernels directly")
+            raise RuntimeError("the layer's source weights were released and its packs do not serve this call "
+                               "(bf16 rows on the GPU with K equal to the layer's in_features)")
         y = quantized_matmul(x, self.weight, self.scales, self.biases, group_size=self.group_size, bits=self.bits,
                              mode=self.mode)
         if self.bias is not None:

@@ -5,10 +5,11 @@
 
 ``make_chunk_sums`` fills the reference's table layout on the GPU
 (``mtp_chunk_sums``: per 512-k block and lane, the 16-value slice sum of
-each row, stride 8). ``crossrow_qmm`` checks a given table's size and then
-runs the verify matmul, which forms its group sums while staging x: the
-result is the same with or without the table, as in the reference, where
-the table reproduces the kernel's own accumulation order.
+each row, stride 8). ``crossrow_qmm`` with a table runs ``mtp_crossrow_qmm``,
+whose 32-k block finishes read their activation sums from the table (two
+slices per block) instead of re-summing the staged x; without one it runs
+the verify matmul, which forms the sums while staging x. Both meet the same
+oracle bar; the two sum orders differ only in fp32 rounding.
 """
 
 from __future__ import annotations
@@ -50,6 +51,20 @@ def crossrow_qmm(x: torch.Tensor, w_q: torch.Tensor, scales: torch.Tensor, biase
                  group_size: int, xsums: torch.Tensor | None = None) -> torch.Tensor:
     """M-row affine-4 matmul ``[m, n]`` (bf16), optional chunk-sum table."""
     m, k = int(x.shape[-2]), int(x.shape[-1])
-    if xsums is not None and int(xsums.numel()) != (k // _BLOCK) * 32 * _SUMS_STRIDE:
+    if xsums is None:
+        return quantized_matmul(x.reshape(m, k), w_q, scales, biases, group_size=int(group_size), bits=4)
+    if int(xsums.numel()) != (k // _BLOCK) * 32 * _SUMS_STRIDE:
         raise ValueError(f"xsums has {int(xsums.numel())} entries, K={k} needs {(k // _BLOCK) * 32 * _SUMS_STRIDE}")
-    return quantized_matmul(x.reshape(m, k), w_q, scales, biases, group_size=int(group_size), bits=4)
+    if xsums.dtype != torch.float32 or not xsums.is_cuda or m > _SUMS_STRIDE:
+        raise ValueError("xsums must be the fp32 GPU table of make_chunk_sums (at most 8 rows)")
+    if x.dtype != torch.bfloat16 or scales.dtype != torch.bfloat16 or biases.dtype != torch.bfloat16:
+        raise TypeError("x, scales and biases must be bfloat16")
+    n = int(w_q.shape[-2])
+    if int(w_q.shape[-1]) * 8 != k:
+        raise ValueError(f"x has K={k}, the 4-bit weight packs K={int(w_q.shape[-1]) * 8}")
+    x2 = x.reshape(m, k).contiguous()
+    xs = xsums.contiguous()
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    _lib.call("mtp_crossrow_qmm", x2.data_ptr(), xs.data_ptr(), w_q.data_ptr(), scales.data_ptr(), biases.data_ptr(),
+              y.data_ptr(), m, n, k, int(group_size), _lib.stream_handle(x.device))
+    return y

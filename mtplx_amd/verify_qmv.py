@@ -3,8 +3,10 @@
 Same function names, arguments and fallback convention as the reference:
 an ineligible call returns ``module(x)`` — here the general gfx950 matmul of
 :class:`~mtplx_amd.quant.QuantizedLinear` — and never raises on shape. The
-reference's fixed-M probes (M=3 "multi3", M=4 pair) are generalised to any
-M <= 32 rows, which is what the verify forward produces (M = B*(K+1)).
+reference's fixed-M probes (M=3 "multi3", M=4 pair) are generalised to every
+verify-row count M = sum_b (K_b + 1): up to 32 rows on the streaming kernel,
+more on the 9..64-row MFMA kernel over the module's layout-1 pack (packed on
+first use and kept on the module; 64-row launches past 64 rows).
 """
 
 from __future__ import annotations
@@ -15,6 +17,7 @@ import torch
 
 from . import _lib
 from .quant import QuantizedLinear
+from .verify_kernels import STREAM_ROWS, fast_path, quantized_matmul, rows_matmul
 
 
 def _affine4(module: Any) -> bool:
@@ -74,7 +77,7 @@ def _rows(x: torch.Tensor, module: QuantizedLinear) -> tuple[torch.Tensor, tuple
     m = 1
     for d in lead:
         m *= int(d)
-    if m > 32:
+    if m < 1:
         return None
     return x.reshape(m, k).contiguous(), lead
 
@@ -83,19 +86,32 @@ def _add_bias(y: torch.Tensor, module: QuantizedLinear) -> torch.Tensor:
     return y + module.bias if module.bias is not None else y
 
 
-def packed_matmul(x: torch.Tensor, module: QuantizedLinear) -> torch.Tensor | None:
-    """``x @ module.weight.T`` on the module's cached pack (up to 32 bf16
-    rows on the GPU), or None when there is no pack or x does not qualify.
+def packed_matmul(x: torch.Tensor, module: QuantizedLinear, *, exact: bool = False) -> torch.Tensor | None:
+    """``x @ module.weight.T`` on the module's cached pack (bf16 rows on the
+    GPU), or None when there is no suitable pack or x does not qualify. Up to
+    32 rows stream the pack on ``mtp_qmv_affine4_ex``; more rows (or
+    ``exact``: every M, the row-invariant greedy lane) run
+    ``mtp_qmm_affine4_mfma`` on the layout-1 pack. A module with an MLX
+    triple but no layout-1 pack gets one here when the MFMA kernel needs it.
     Never falls back to ``module(x)``, so a patched ``__call__`` may use it."""
+    if len(module._shape) != 2:   # expert stacks go through switch_linear
+        return None
     r = _rows(x, module)
     if r is None:
         return None
     x2, lead = r
     m, k = (int(d) for d in x2.shape)
+    n = module.out_features
+    if m > STREAM_ROWS or exact:
+        if module.packed is None:
+            if module.weight is None or not fast_path(module.bits, module.group_size, k):
+                return None
+            module.pack()
+        y = rows_matmul(x2, module.packed, n, module.group_size)
+        return _add_bias(y, module).reshape(*lead, n)
     pk = _packed(module, m)
     if pk is None:
         return None
-    n = module.out_features
     y = torch.empty((m, n), dtype=x.dtype, device=x.device)
     _qmv_packed(_lib.stream_handle(x.device), m, n, k, x=x2, w0=pk[0], y0=y, group_size=module.group_size,
                 xmode=0, emode=0, packed=pk[1])
@@ -114,11 +130,7 @@ def multi3_qmv4_matmul(x: torch.Tensor, module: QuantizedLinear) -> torch.Tensor
         return module(x)
     x2, lead = r
     n = module.out_features
-    m, k = (int(d) for d in x2.shape)
-    y = torch.empty((m, n), dtype=x.dtype, device=x.device)
-    _lib.call("mtp_qmv_affine4", x2.data_ptr(), module.weight.data_ptr(), module.scales.data_ptr(),
-              module.biases.data_ptr(), y.data_ptr(), m, n, k, module.group_size, None, 0,
-              _lib.stream_handle(x.device))
+    y = quantized_matmul(x2, module.weight, module.scales, module.biases, group_size=module.group_size, bits=4)
     return _add_bias(y, module).reshape(*lead, n)
 
 
@@ -140,7 +152,8 @@ def multi3_dual_qmv4_matmul(x: torch.Tensor, gate_module: QuantizedLinear, up_mo
                            and gate_module._shape == up_module._shape
                            and gate_module.group_size == up_module.group_size)
     r = _rows(x, gate_module) if ok else None
-    if r is None:
+    if r is None or int(r[0].shape[0]) > STREAM_ROWS:
+        # past 32 rows: one MFMA launch per projection (no two-output form there)
         return gate_module(x), up_module(x)
     x2, lead = r
     n = gate_module.out_features
@@ -173,7 +186,7 @@ def multi3_swiglu_down_qmv4_matmul(gate: torch.Tensor, up: torch.Tensor, module:
     if gate.shape != up.shape or not is_multi3_qmv4_eligible(module):
         return fallback()
     r = _rows(gate, module)
-    if r is None or up.dtype != gate.dtype:
+    if r is None or up.dtype != gate.dtype or int(r[0].shape[0]) > STREAM_ROWS:
         return fallback()
     g2, lead = r
     u2 = up.reshape(g2.shape).contiguous()

@@ -37,7 +37,19 @@ import torch
 from . import _lib
 from .moe_sorted_gather import expert_sort, moe_combine
 from .quant import QuantizedLinear, rope_row_order
+from .attention_context import exact_lane_counts, exact_t0_guard_armed, exact_verify_required
 from .sampling import SamplerConfig, narrow_law, spec_accept
+
+# Keys per attention work unit on the exact lane: a fixed split length (a
+# multiple of 128) makes each request's partials and merge independent of the
+# rest of the batch; 1024 keeps at most 256 splits up to 256k-key contexts.
+EXACT_SPLIT_KEYS = 1024
+
+
+def _exact_lane(sampler: SamplerConfig) -> bool:
+    """Greedy verify forwards (or any forward inside ``exact_verify(True)``)
+    take the exact lane while the guard is armed."""
+    return exact_verify_required() or (not float(sampler.temperature) > 0.0 and exact_t0_guard_armed())
 
 
 @dataclass
@@ -319,16 +331,31 @@ class VerifyModel:
     # -- forward --------------------------------------------------------------
     def verify_logits(self, tokens: torch.Tensor, q_start: torch.Tensor, q_lens: torch.Tensor | None = None,
                       *, logits_out: torch.Tensor | None = None, check: bool = False,
-                      topk: dict | None = None) -> torch.Tensor:
+                      topk: dict | None = None, exact: bool = False, layer_log: list | None = None) -> torch.Tensor:
         """``tokens`` int32 ``[B, L]`` (GPU), ``q_start`` int32 ``[B]`` (GPU):
         writes K/V of the L rows at ``q_start[b] + i`` and returns fp32 logits ``[B*L, V]``.
         The device status word (:meth:`status`) flags invalid tokens or
         positions; ``check=True`` synchronises and raises on it. ``topk``
         (fields of ``mtp_logits_topk``, B*L <= 8): the lm_head also writes
-        the sampler's chunk partials of every row."""
+        the sampler's chunk partials of every row. ``exact``: the exact lane
+        (:meth:`verify_logits_ragged` with ``exact=True`` over this uniform
+        cache), whose rows do not depend on B or L. ``layer_log``: a list
+        that receives a copy of the hidden rows (bf16 ``[B*L, H]``) entering
+        every layer and the final norm (layers + 1 entries)."""
         c = self.cfg
         B, Lq = (int(s) for s in tokens.shape)
         M = B * Lq
+        if exact:
+            if topk is not None or c.n_experts:
+                raise ValueError("the exact lane serves the dense model without the fused lm_head records")
+            dev = self.device
+            nblk = self.cap // 32
+            kv_off = torch.arange(B + 1, dtype=torch.int32, device=dev) * (c.n_kv_heads * nblk)
+            row_off = torch.arange(B + 1, dtype=torch.int32, device=dev) * Lq
+            ql = torch.full((B,), Lq, dtype=torch.int32, device=dev) if q_lens is None else q_lens
+            return self._ragged_forward(tokens.reshape(-1), row_off, q_start, ql, Lq, kv_off, B * self.cap,
+                                        logits_out=logits_out, check=check, split_keys=EXACT_SPLIT_KEYS,
+                                        layer_log=layer_log)
         dev = self.device
         st = _lib.stream_handle(dev)
         gs = c.group_size
@@ -382,6 +409,8 @@ class VerifyModel:
             return q.packed_mf16 if lay == 2 else q.packed
 
         for li, L in enumerate(self.layers):
+            if layer_log is not None:
+                layer_log.append(h.clone())
             xin = dict(x=h, x2=L.in_norm, xmode=2)   # input RMSNorm fused into the staging
             if fused_rope:
                 rope = dict(q_start=q_start, q_lens=ql, q_out=qh, k_cache=self.k_cache[li], v_cache=self.v_cache[li],
@@ -416,6 +445,8 @@ class VerifyModel:
                 qmv(st, x=act, x_sums=act_sums, w0=W(L.down), resid=h, y0=h, ss_out=ss_b, M=M, N=H, K=c.ffn,
                     group_size=gs, xmode=3, emode=1, packed=lay)
                 ss_h = ss_b
+        if layer_log is not None:
+            layer_log.append(h.clone())
         logits = logits_out if logits_out is not None else torch.empty((M, c.vocab), dtype=torch.float32, device=dev)
         qmv(st, x=h, x2=self.final_norm, ss_in=ss_h, eps=c.rms_eps, w0=W(self.lm_head), yf=logits, M=M,
             N=c.vocab, K=H, group_size=gs, xmode=2, emode=0 if topk is None else 5, packed=lay, topk=topk)
@@ -475,19 +506,38 @@ class VerifyModel:
 
     def verify_logits_ragged(self, tokens: torch.Tensor, row_off: torch.Tensor, q_start: torch.Tensor,
                              q_lens: torch.Tensor, Lmax: int, *, logits_out: torch.Tensor | None = None,
-                             check: bool = False) -> torch.Tensor:
+                             check: bool = False, exact: bool = False, layer_log: list | None = None) -> torch.Tensor:
         """The continuous-batched verify forward (dense model, block cache from
         :meth:`allocate_cache_blocks`): ``tokens`` int32 [M] packed request
         after request, request b's ``q_lens[b]`` (<= ``Lmax``) rows at
         ``row_off[b]`` (int32 [B+1]) and positions ``q_start[b] + i``. Every
         projection runs on ``mtp_qmm_affine4_mfma`` (each weight quad read once
         for all M <= 64 rows); RoPE writes K/V into the requests' blocks;
-        attention reads per-request capacities. Returns fp32 logits [M, V]."""
+        attention reads per-request capacities. Returns fp32 logits [M, V].
+
+        ``exact``: the exact lane. The matmul's K split never depends on M,
+        and attention runs ``EXACT_SPLIT_KEYS``-key units with the per-head
+        merge instead of the balanced kernel (whose shares depend on the
+        whole batch), so each request's logits are bit-identical to those of
+        the same rows verified alone (any L, any batch)."""
+        return self._ragged_forward(tokens, row_off, q_start, q_lens, Lmax, self.kv_off, self.total_cap,
+                                    logits_out=logits_out, check=check,
+                                    split_keys=EXACT_SPLIT_KEYS if exact else 0, layer_log=layer_log)
+
+    def _ragged_forward(self, tokens: torch.Tensor, row_off: torch.Tensor, q_start: torch.Tensor,
+                        q_lens: torch.Tensor, Lmax: int, kv_off: torch.Tensor, total_cap: int, *,
+                        logits_out: torch.Tensor | None, check: bool, split_keys: int,
+                        layer_log: list | None) -> torch.Tensor:
+        """The ragged forward over a block cache described by ``kv_off``
+        (int32 [B+1], first block of each request) and ``total_cap`` (summed
+        capacities); ``split_keys`` 0 = balanced attention."""
         c = self.cfg
         if c.n_experts:
             raise NotImplementedError("the ragged lane serves the dense model")
         M = int(tokens.numel())
         B = int(q_start.numel())
+        if M > 64:
+            raise ValueError(f"the ragged lane takes at most 64 rows (got {M})")
         dev = self.device
         st = _lib.stream_handle(dev)
         call = _lib.call
@@ -508,7 +558,7 @@ class VerifyModel:
                      ((c.qkv_out, H, 0), (H, c.n_heads * c.head_dim, 0), (c.ffn, H, 1), (H, c.ffn, 0),
                       (c.vocab, H, 0)))
         qws = _lib.WORKSPACES.get(max(qmm_nb, 256), "qmm", dev)
-        anb = _lib.query("mtp_attn_blocks_workspace_bytes", B, c.n_kv_heads, self.cap, self.total_cap, 0)
+        anb = _lib.query("mtp_attn_blocks_workspace_bytes", B, c.n_kv_heads, self.cap, total_cap, split_keys)
         aws = _lib.WORKSPACES.get(anb, "attn_blocks", dev)
         scale = 1.0 / math.sqrt(c.head_dim)
         eps = ctypes.c_float(c.rms_eps)
@@ -519,21 +569,26 @@ class VerifyModel:
         def norm(x, w, out):
             call("mtp_rmsnorm", x.data_ptr(), w.data_ptr(), out.data_ptr(), M, H, eps, st)
 
+        kvo = kv_off.to(torch.int32).contiguous()
         for li, L in enumerate(self.layers):
+            if layer_log is not None:
+                layer_log.append(h.clone())
             norm(h, L.in_norm, xn)
             mm(x=xn, w0=L.qkv.packed, y=qkv, N=c.qkv_out, K=H, emode=0)
             call("mtp_rope_qkv_to_blocks", qkv.data_ptr(), M, ro.data_ptr(), q_start.data_ptr(),
-                 self.kv_off.data_ptr(), qh.data_ptr(), self.k_cache[li].data_ptr(), self.v_cache[li].data_ptr(), B,
+                 kvo.data_ptr(), qh.data_ptr(), self.k_cache[li].data_ptr(), self.v_cache[li].data_ptr(), B,
                  Lmax, c.n_heads, c.n_kv_heads, c.head_dim, self.cap, ctypes.c_float(c.rope_theta),
                  status.data_ptr(), st)
             _lib.attn_blocks(st, q=qh, k_blk=self.k_cache[li], v_blk=self.v_cache[li], q_start=q_start, q_lens=ql,
-                             row_off=ro, kv_off=self.kv_off, out=attn, B=B, Hq=c.n_heads, Hkv=c.n_kv_heads, Lmax=Lmax,
-                             D=c.head_dim, cap=self.cap, split_keys=0, scale=scale, total_cap=self.total_cap, ws=aws,
-                             ws_bytes=aws.numel())
+                             row_off=ro, kv_off=kvo, out=attn, B=B, Hq=c.n_heads, Hkv=c.n_kv_heads, Lmax=Lmax,
+                             D=c.head_dim, cap=self.cap, split_keys=split_keys, scale=scale, total_cap=total_cap,
+                             ws=aws, ws_bytes=aws.numel())
             mm(x=attn, w0=L.o.packed, y=h, resid=h, N=H, K=c.n_heads * c.head_dim, emode=1)
             norm(h, L.post_norm, xn)
             mm(x=xn, w0=L.gate.packed, w1=L.up.packed, y=act, N=c.ffn, K=H, emode=3)
             mm(x=act, w0=L.down.packed, y=h, resid=h, N=H, K=c.ffn, emode=1)
+        if layer_log is not None:
+            layer_log.append(h.clone())
         norm(h, self.final_norm, xn)
         logits = logits_out if logits_out is not None else torch.empty((M, c.vocab), dtype=torch.float32, device=dev)
         mm(x=xn, w0=self.lm_head.packed, yf=logits, N=c.vocab, K=H, emode=0)
@@ -551,7 +606,13 @@ class VerifyModel:
         its draft rows the same rows of ``draft_logits``."""
         from .sampling import spec_accept_ragged
 
-        logits = self.verify_logits_ragged(tokens, row_off, q_start, q_lens, Lmax)
+        if int(uniforms.shape[-1]) < int(Lmax) or int(uniforms.shape[0]) != int(q_start.numel()):
+            raise ValueError(f"uniforms must be [B, >= Lmax] = [{int(q_start.numel())}, >= {int(Lmax)}] "
+                             f"(got {list(uniforms.shape)}): request b consumes up to q_lens[b] of its row")
+        exact = _exact_lane(sampler)
+        if exact:
+            exact_lane_counts["verify_step_ragged"] += 1
+        logits = self.verify_logits_ragged(tokens, row_off, q_start, q_lens, Lmax, exact=exact)
         self.last_logits = logits
         drafts = tokens.reshape(-1)[draft_index]
         return spec_accept_ragged(logits, row_off[:-1], draft_logits, d_off, q_lens - 1, drafts, uniforms, sampler)
@@ -571,6 +632,14 @@ class VerifyModel:
         K = L - 1
         c = self.cfg
         topk = None
+        if _exact_lane(sampler) and not c.n_experts:
+            # Greedy verify: the exact lane, whose rows do not depend on the
+            # batch (the argmax the autoregressive decode of the same rows picks).
+            exact_lane_counts["verify_step"] += 1
+            logits = self.verify_logits(tokens, q_start, exact=True)
+            self.last_logits = logits
+            return spec_accept(logits.reshape(B, L, -1), draft_logits, tokens[:, 1:].contiguous(), uniforms,
+                               sampler)
         if fuse_topk and B * L <= 8 and narrow_law(sampler, c.vocab):
             parts = _lib.WORKSPACES.get(_lib.query("mtp_logits_topk_parts_bytes", B * L), "logits_topk_parts",
                                         self.device)

@@ -16,6 +16,10 @@ k; routed rows go through the sorted SwiGLU chain; the shared expert is
 ``sigmoid(gate) * shared_mlp(x)``; the block output ``routed + shared`` is
 added to the residual stream.
 
+``decoder_layer`` is the one-layer restatement both forwards run; a test
+can feed it the GPU's own hidden rows (teacher forcing) to hold every layer
+of a deep model to the bar separately.
+
 Parity pins (tests/test_oracle_model.py): a zero-layer model equals a
 closed form of norm + lm_head over the embedding rows; a layer whose o and
 down projections are zero leaves the residual stream unchanged, so its
@@ -70,60 +74,90 @@ def verify_forward_ragged(params: dict, cfg, tokens: list, q_start, k_cache: lis
     request (logits [sum_b L_b, V]). ``k_cache[li][b]`` is request b's
     float64 [Hkv, cap_b, D] cache of layer li (a [B, Hkv, cap, D] array or a
     list of per-request arrays), updated in place."""
+    lens = [len(t) for t in tokens]
+    flat = np.concatenate([np.asarray(t).reshape(-1) for t in tokens])
+    h = embed_rows(params, cfg, flat)
+    for li, lay in enumerate(params["layers"]):
+        h = decoder_layer(lay, cfg, h, lens, q_start, k_cache[li], v_cache[li], routes)
+    return final_logits(params, cfg, h)
+
+
+def embed_rows(params: dict, cfg, flat_tokens) -> np.ndarray:
+    """Embedding rows (bf16 values) of the flattened tokens."""
+    gs = cfg.group_size
+    emb = params["embed"]
+    return round_to_bf16(np.stack([dequantize_affine4(emb[0][t:t + 1], emb[1][t:t + 1], emb[2][t:t + 1], gs)[0]
+                                   for t in np.asarray(flat_tokens).reshape(-1)]))
+
+
+def final_logits(params: dict, cfg, h: np.ndarray) -> np.ndarray:
+    """Final RMSNorm and lm_head of the hidden rows (bf16 values)."""
+    xn = round_to_bf16(rmsnorm(h, params["final_norm"], cfg.rms_eps))
+    return round_to_bf16(qmm_affine4(xn, *params["lm_head"], cfg.group_size))
+
+
+def decoder_layer(lay: dict, cfg, h: np.ndarray, lens, q_start, k_cache_layer, v_cache_layer,
+                  routes: list | None = None, trace: dict | None = None) -> np.ndarray:
+    """One decoder layer on the packed rows ``h`` [sum(lens), H] (bf16
+    values): request b's ``lens[b]`` rows at positions ``q_start[b] + i``.
+    ``k_cache_layer[b]`` / ``v_cache_layer[b]`` are request b's float64
+    [Hkv, cap_b, D] caches of this layer, updated in place. Returns the
+    layer's output rows (bf16 values). ``trace``, if a dict, receives the
+    two rounded block outputs added to the residual stream: ``"attn_out"``
+    (the o projection) and ``"mlp_out"`` (down projection, or routed +
+    shared for an MoE layer)."""
     gs = cfg.group_size
     H, D, Hq, Hkv = cfg.hidden, cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
-    lens = [len(t) for t in tokens]
     offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
-    flat = np.concatenate([np.asarray(t).reshape(-1) for t in tokens])
     M = int(offs[-1])
-    emb = params["embed"]
-    h = round_to_bf16(np.stack([dequantize_affine4(emb[0][t:t + 1], emb[1][t:t + 1], emb[2][t:t + 1], gs)[0]
-                                for t in flat]))
-    for li, lay in enumerate(params["layers"]):
-        xn = round_to_bf16(rmsnorm(h, lay["in_norm"], cfg.rms_eps))
-        qkv = round_to_bf16(qmm_affine4(xn, *lay["qkv"], gs)).reshape(M, Hq + 2 * Hkv, D)
-        att = np.zeros((M, Hq * D))
-        for b, L in enumerate(lens):
-            if L == 0:
-                continue
-            rows = slice(int(offs[b]), int(offs[b + 1]))
-            pos = int(q_start[b]) + np.arange(L)
-            blk = qkv[rows].transpose(1, 0, 2)                       # [heads, L, D]
-            q = round_to_bf16(rope_rotate_half(blk[:Hq], pos[None, :], cfg.rope_theta))
-            k = round_to_bf16(rope_rotate_half(blk[Hq:Hq + Hkv], pos[None, :], cfg.rope_theta))
-            v = blk[Hq + Hkv:]
-            kc, vc = k_cache[li][b], v_cache[li][b]
-            kc[:, pos[0]:pos[0] + L] = k
-            vc[:, pos[0]:pos[0] + L] = v
-            o = round_to_bf16(ragged_gqa_attention(q[None], kc[None], vc[None], [int(q_start[b])]))[0]
-            att[rows] = o.transpose(1, 0, 2).reshape(L, Hq * D)
-        h = round_to_bf16(round_to_bf16(qmm_affine4(att, *lay["o"], gs)) + h)
-        xn = round_to_bf16(rmsnorm(h, lay["post_norm"], cfg.rms_eps))
-        if cfg.n_experts:
-            E = cfg.n_experts
-            rl = round_to_bf16(qmm_affine4(xn, *lay["router"], gs))          # [M, E + 1]
-            skew = lay.get("router_skew")
-            logits = rl[:, :E].astype(np.float32)
-            if skew is not None:
-                logits = logits + np.asarray(skew, np.float32)[None, :]
-            ids, wts = route_topk(logits.astype(np.float64), cfg.top_k)
-            if routes is not None:
-                routes.append((ids, wts))
-            routed = round_to_bf16(moe_forward(xn, ids, wts, lay["expert_gate_up"], lay["expert_down"], gs))
-            sg = round_to_bf16(qmm_affine4(xn, *lay["shared_gate"], gs))
-            su = round_to_bf16(qmm_affine4(xn, *lay["shared_up"], gs))
-            sa = round_to_bf16(round_to_bf16(silu(sg)) * su)
-            sd = round_to_bf16(qmm_affine4(sa, *lay["shared_down"], gs))
-            gate = 1.0 / (1.0 + np.exp(-rl[:, E]))
-            shared = round_to_bf16(gate[:, None] * sd)
-            h = round_to_bf16(h + round_to_bf16(routed + shared))
-        else:
-            g = round_to_bf16(qmm_affine4(xn, *lay["gate"], gs))
-            u = round_to_bf16(qmm_affine4(xn, *lay["up"], gs))
-            a = round_to_bf16(round_to_bf16(silu(g)) * u)
-            h = round_to_bf16(round_to_bf16(qmm_affine4(a, *lay["down"], gs)) + h)
-    xn = round_to_bf16(rmsnorm(h, params["final_norm"], cfg.rms_eps))
-    return round_to_bf16(qmm_affine4(xn, *params["lm_head"], gs))
+    h = np.asarray(h, dtype=np.float64)
+    xn = round_to_bf16(rmsnorm(h, lay["in_norm"], cfg.rms_eps))
+    qkv = round_to_bf16(qmm_affine4(xn, *lay["qkv"], gs)).reshape(M, Hq + 2 * Hkv, D)
+    att = np.zeros((M, Hq * D))
+    for b, L in enumerate(lens):
+        if L == 0:
+            continue
+        rows = slice(int(offs[b]), int(offs[b + 1]))
+        pos = int(q_start[b]) + np.arange(L)
+        blk = qkv[rows].transpose(1, 0, 2)                       # [heads, L, D]
+        q = round_to_bf16(rope_rotate_half(blk[:Hq], pos[None, :], cfg.rope_theta))
+        k = round_to_bf16(rope_rotate_half(blk[Hq:Hq + Hkv], pos[None, :], cfg.rope_theta))
+        v = blk[Hq + Hkv:]
+        kc, vc = k_cache_layer[b], v_cache_layer[b]
+        kc[:, pos[0]:pos[0] + L] = k
+        vc[:, pos[0]:pos[0] + L] = v
+        o = round_to_bf16(ragged_gqa_attention(q[None], kc[None], vc[None], [int(q_start[b])]))[0]
+        att[rows] = o.transpose(1, 0, 2).reshape(L, Hq * D)
+    o_out = round_to_bf16(qmm_affine4(att, *lay["o"], gs))
+    h = round_to_bf16(o_out + h)
+    xn = round_to_bf16(rmsnorm(h, lay["post_norm"], cfg.rms_eps))
+    if cfg.n_experts:
+        E = cfg.n_experts
+        rl = round_to_bf16(qmm_affine4(xn, *lay["router"], gs))          # [M, E + 1]
+        skew = lay.get("router_skew")
+        logits = rl[:, :E].astype(np.float32)
+        if skew is not None:
+            logits = logits + np.asarray(skew, np.float32)[None, :]
+        ids, wts = route_topk(logits.astype(np.float64), cfg.top_k)
+        if routes is not None:
+            routes.append((ids, wts))
+        routed = round_to_bf16(moe_forward(xn, ids, wts, lay["expert_gate_up"], lay["expert_down"], gs))
+        sg = round_to_bf16(qmm_affine4(xn, *lay["shared_gate"], gs))
+        su = round_to_bf16(qmm_affine4(xn, *lay["shared_up"], gs))
+        sa = round_to_bf16(round_to_bf16(silu(sg)) * su)
+        sd = round_to_bf16(qmm_affine4(sa, *lay["shared_down"], gs))
+        gate = 1.0 / (1.0 + np.exp(-rl[:, E]))
+        shared = round_to_bf16(gate[:, None] * sd)
+        mlp_out = round_to_bf16(routed + shared)
+    else:
+        g = round_to_bf16(qmm_affine4(xn, *lay["gate"], gs))
+        u = round_to_bf16(qmm_affine4(xn, *lay["up"], gs))
+        a = round_to_bf16(round_to_bf16(silu(g)) * u)
+        mlp_out = round_to_bf16(qmm_affine4(a, *lay["down"], gs))
+    if trace is not None:
+        trace["attn_out"] = o_out
+        trace["mlp_out"] = mlp_out
+    return round_to_bf16(h + mlp_out)
 
 
 def route_topk(logits: np.ndarray, top_k: int):

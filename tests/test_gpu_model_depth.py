@@ -1,0 +1,213 @@
+"""Full-depth parity of the composed verify step against the float64 oracle.
+
+* cfg3: the whole 64-layer 27B-shaped step (hidden 5120, SwiGLU 17408, 40/8
+  heads, vocab 151936; one request, 4 rows at positions 4092..4095).
+* cfg5: two layers of the 125B-class MoE shape (4 requests x 4 rows at 8k).
+
+Each layer is held to the north-star bar on its own by teacher forcing: the
+oracle's ``decoder_layer`` takes the GPU's own bf16 rows entering the layer
+(``VerifyModel.verify_logits(layer_log=...)``) and must give the rows the
+GPU stored after it within rtol = atol = 1e-2, plus one bf16 ulp of each of
+the two rounded block outputs added to the residual stream (both sides
+round the same products to bf16 from sums that differ in their last fp32
+bits, so a product on a rounding boundary lands one ulp apart; where the
+residual cancels it, that ulp is several ulps of the result). The RoPE'd
+K rows and the V rows each layer writes are held to the same bar. The final
+norm + lm_head is held to 1e-2 on the GPU's last rows.
+
+End to end, the oracle runs the whole forward from the tokens, and
+acceptance on the GPU's logits must be token-exact against the oracle's
+acceptance on its own logits, with each row's logits within a relative L2
+error of 1e-2. For the 64-layer dense step the logits must also meet
+rtol = atol = 1e-2 except where two values one bf16 ulp apart straddle the
+bar. The test prints, per layer, the share of stored elements equal to the
+oracle's and the share within one bf16 ulp of each rounding that forms them.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampler as S
+from oracle.model import decoder_layer, embed_rows, final_logits
+from tests.gpu_util import assert_close, bf16_ulp, bf16_values
+from tests.model_util import model_params_numpy
+
+pytestmark = pytest.mark.gpu
+
+
+def _ulps(got: np.ndarray, want: np.ndarray) -> np.ndarray:
+    return np.abs(got - want) / bf16_ulp(want)
+
+
+def assert_layer_close(got, want, trace, what):
+    """rtol = atol = 1e-2 plus one bf16 ulp of each rounded block output."""
+    allow = 1e-2 + 1e-2 * np.abs(want) + bf16_ulp(trace["attn_out"]) + bf16_ulp(trace["mlp_out"])
+    bad = np.abs(got - want) > allow
+    if bad.any():
+        idx = np.argwhere(bad)[:5]
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outside the bar; first {idx.tolist()} "
+                             f"got {got[tuple(idx[0])]} want {want[tuple(idx[0])]}")
+
+
+def assert_rope_close(got, want, D=128, what="k rows"):
+    half = D // 2
+    r = np.sqrt(want[..., :half] ** 2 + want[..., half:] ** 2)
+    r = np.concatenate([r, r], axis=-1)
+    bad = np.abs(got - want) > 1e-2 + 1e-2 * r
+    if bad.any():
+        idx = np.argwhere(bad)[:5]
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outside 1e-2 of the pair norm; first "
+                             f"{idx.tolist()}")
+
+
+def _flips(got, want, tr) -> str:
+    """How much of a layer's output difference one-ulp rounding flips explain:
+    the share of elements equal, and within one bf16 ulp of each of the three
+    roundings that form them (the residual sum and the two block outputs)."""
+    d = np.abs(got - want)
+    one = bf16_ulp(want) + bf16_ulp(tr["attn_out"]) + bf16_ulp(tr["mlp_out"])
+    return (f"equal {np.mean(d == 0):.4f}, within one ulp of each rounding {np.mean(d <= one):.5f} "
+            f"(max {float((d / one).max()):.2f} of that)")
+
+
+def _hist(u: np.ndarray) -> str:
+    n = u.size
+    return (f"0 ulp {np.mean(u == 0):.4f}, <=1 ulp {np.mean(u <= 1):.5f}, >1 ulp {int((u > 1).sum())}/{n}, "
+            f"max {u.max():.2f}")
+
+
+def _teacher_forced(model, cfg, params, hs, starts, L, tag):
+    """Every layer of the model against the oracle layer fed the GPU's rows."""
+    B = len(starts)
+    for li in range(cfg.layers):
+        kc = model.k_cache_standard(li).float().cpu().numpy().astype(np.float64)
+        vc = model.v_cache_standard(li).float().cpu().numpy().astype(np.float64)
+        gk = np.stack([kc[b, :, s:s + L] for b, s in enumerate(starts)])
+        gv = np.stack([vc[b, :, s:s + L] for b, s in enumerate(starts)])
+        tr = {}
+        want = decoder_layer(params["layers"][li], cfg, hs[li], [L] * B, starts, list(kc), list(vc), trace=tr)
+        assert_layer_close(hs[li + 1], want, tr, f"{tag} layer {li} (teacher-forced)")
+        assert_rope_close(gk, np.stack([kc[b, :, s:s + L] for b, s in enumerate(starts)]), what=f"{tag} k rows {li}")
+        assert_close(gv, np.stack([vc[b, :, s:s + L] for b, s in enumerate(starts)]), what=f"{tag} v rows {li}")
+        if li % 8 == 0 or li == cfg.layers - 1:
+            print(f"{tag} layer {li}: h vs teacher-forced oracle: {_flips(hs[li + 1], want, tr)}", flush=True)
+        del kc, vc
+
+
+def _oracle_forward(params, cfg, tokens, starts, kc, vc, tag, routes=None):
+    """``oracle.model.verify_forward`` layer by layer, printing progress."""
+    lens = [len(t) for t in tokens]
+    h = embed_rows(params, cfg, np.concatenate([np.asarray(t).reshape(-1) for t in tokens]))
+    for li, lay in enumerate(params["layers"]):
+        h = decoder_layer(lay, cfg, h, lens, starts, kc[li], vc[li], routes)
+        if li % 8 == 7:
+            print(f"{tag}: oracle forward through layer {li}", flush=True)
+    return final_logits(params, cfg, h)
+
+
+@pytest.mark.timeout(900)
+def test_cfg3_full_depth(gpu):
+    from mtplx_amd.sampling import SamplerConfig, spec_accept
+    from mtplx_amd.verify_step import DENSE_27B, VerifyModel
+    cfg = DENSE_27B
+    model = VerifyModel(cfg, device="cuda", seed=17)
+    model.allocate_cache(1, 4096)
+    # the cache before the step: positions 4092.. are overwritten by the step
+    kc0 = [model.k_cache_standard(li)[:, :, :4092].float().cpu().numpy() for li in range(cfg.layers)]
+    vc0 = [model.v_cache_standard(li)[:, :, :4092].float().cpu().numpy() for li in range(cfg.layers)]
+    gen = torch.Generator(device="cuda").manual_seed(18)
+    tokens = torch.randint(0, cfg.vocab, (1, 4), device="cuda", dtype=torch.int32, generator=gen)
+    qs = torch.tensor([4092], dtype=torch.int32, device="cuda")
+    log = []
+    logits = model.verify_logits(tokens, qs, check=True, layer_log=log)
+    got = logits.cpu().numpy().astype(np.float64)
+    hs = [bf16_values(t) for t in log]
+    assert len(hs) == cfg.layers + 1
+    params = model_params_numpy(model)
+    _teacher_forced(model, cfg, params, hs, [4092], 4, "cfg3")
+    tf = final_logits(params, cfg, hs[-1])
+    assert_close(got, tf, what="cfg3 logits on the GPU's last rows")
+    print(f"cfg3 logits vs teacher-forced lm_head: {_hist(_ulps(got, tf))}", flush=True)
+    # end to end: the oracle's own 64-layer forward from the tokens
+    kc = [np.concatenate([k, np.zeros((1, cfg.n_kv_heads, 4, cfg.head_dim), np.float32)], axis=2).astype(np.float64)
+          for k in kc0]
+    vc = [np.concatenate([v, np.zeros((1, cfg.n_kv_heads, 4, cfg.head_dim), np.float32)], axis=2).astype(np.float64)
+          for v in vc0]
+    del kc0, vc0
+    want = _oracle_forward(params, cfg, list(tokens.cpu().numpy()), [4092], kc, vc, "cfg3")
+    u = _ulps(got, want)
+    rel = np.sqrt(((got - want) ** 2).sum(axis=1)) / np.sqrt((want ** 2).sum(axis=1))
+    print(f"cfg3 end-to-end logits (64 layers): {_hist(u)}; per-row relative L2 {rel.tolist()}", flush=True)
+    over = np.abs(got - want) > 1e-2 + 1e-2 * np.abs(want)
+    # the bar, except where two sides one bf16 ulp apart straddle it
+    assert (u[over] <= 1.0).all(), f"{int((u[over] > 1).sum())} logits beyond the bar by more than one ulp"
+    assert (rel <= 1e-2).all()
+    # accept/reject: GPU on its logits, token-exact against the oracle on its own
+    draft = (logits[:3] + 0.5 * torch.randn((3, cfg.vocab), device="cuda", generator=gen)).contiguous()
+    for seed in range(4):
+        g2 = torch.Generator(device="cuda").manual_seed(100 + seed)
+        uni = torch.rand((1, 4), device="cuda", dtype=torch.float64, generator=g2)
+        res = spec_accept(logits.reshape(1, 4, -1), draft.reshape(1, 3, -1), tokens[:, 1:], uni, SamplerConfig())
+        w = S.spec_accept(want.astype(np.float32), draft.cpu().numpy(), tokens[0, 1:].cpu().numpy(),
+                          uni[0].cpu().numpy(), S.SamplerConfig())
+        assert res.tokens[0].cpu().numpy().tolist()[: len(w.tokens)] == w.tokens, seed
+        assert int(res.n_accepted[0]) == w.n_accepted
+
+
+@pytest.mark.timeout(900)
+def test_cfg5_two_layers_depth(gpu):
+    from dataclasses import replace
+
+    from mtplx_amd.verify_step import MOE_125B, VerifyModel
+    cfg = replace(MOE_125B, layers=2)
+    model = VerifyModel(cfg, device="cuda", seed=23, keep_expert_source=True)
+    B, L, ctx = 4, 4, 8192
+    model.allocate_cache(B, ctx)
+    kc0 = [model.k_cache_standard(li).float().cpu().numpy().astype(np.float64) for li in range(cfg.layers)]
+    vc0 = [model.v_cache_standard(li).float().cpu().numpy().astype(np.float64) for li in range(cfg.layers)]
+    gen = torch.Generator(device="cuda").manual_seed(24)
+    tokens = torch.randint(0, cfg.vocab, (B, L), device="cuda", dtype=torch.int32, generator=gen)
+    starts = [ctx - L, ctx - L - 100, ctx - L - 1000, 5000]
+    qs = torch.tensor(starts, dtype=torch.int32, device="cuda")
+    model.route_log = []
+    log = []
+    logits = model.verify_logits(tokens, qs, check=True, layer_log=log)
+    got = logits.cpu().numpy().astype(np.float64)
+    hs = [bf16_values(t) for t in log]
+    params = model_params_numpy(model)
+    _teacher_forced(model, cfg, params, hs, starts, L, "cfg5")
+    tf = final_logits(params, cfg, hs[-1])
+    assert_close(got, tf, what="cfg5 logits on the GPU's last rows")
+    print(f"cfg5 logits vs teacher-forced lm_head: {_hist(_ulps(got, tf))}", flush=True)
+    routes = []
+    want = _oracle_forward(params, cfg, list(tokens.cpu().numpy()), starts, kc0, vc0, "cfg5", routes)
+    for li in range(cfg.layers):
+        assert np.array_equal(np.sort(model.route_log[li].cpu().numpy(), axis=1), np.sort(routes[li][0], axis=1))
+        # Zipf skew with per-token spread: a few experts take many of the 128
+        # routed rows, and tokens do not all share one top-8
+        counts = np.bincount(routes[li][0].reshape(-1), minlength=cfg.n_experts)
+        assert counts.max() >= 4 and 24 <= (counts > 0).sum() < 128
+    u = _ulps(got, want)
+    rel = np.sqrt(((got - want) ** 2).sum(axis=1)) / np.sqrt((want ** 2).sum(axis=1))
+    print(f"cfg5 end-to-end logits (2 layers): {_hist(u)}; max per-row relative L2 {rel.max():.5f}", flush=True)
+    over = np.abs(got - want) > 1e-2 + 1e-2 * np.abs(want)
+    d = np.abs(got - want)
+    print(f"cfg5 end-to-end: {int(over.sum())} of {over.size} beyond rtol=atol=1e-2 (max excess "
+          f"{float((d - 1e-2 - 1e-2 * np.abs(want)).max()):.4f}); |diff| rms {float(np.sqrt((d ** 2).mean())):.5f}",
+          flush=True)
+    assert (rel <= 1e-2).all()
+    # accept/reject on every request: GPU on its logits, token-exact against the oracle on its own
+    from mtplx_amd.sampling import SamplerConfig, spec_accept
+    lg = logits.reshape(B, L, -1)
+    draft = (lg[:, :L - 1] + 0.5 * torch.randn((B, L - 1, cfg.vocab), device="cuda", generator=gen)).contiguous()
+    wt = want.reshape(B, L, -1).astype(np.float32)
+    for seed in range(4):
+        g2 = torch.Generator(device="cuda").manual_seed(200 + seed)
+        uni = torch.rand((B, L), device="cuda", dtype=torch.float64, generator=g2)
+        res = spec_accept(lg, draft, tokens[:, 1:], uni, SamplerConfig())
+        for b in range(B):
+            w = S.spec_accept(wt[b], draft[b].cpu().numpy(), tokens[b, 1:].cpu().numpy(), uni[b].cpu().numpy(),
+                              S.SamplerConfig())
+            assert res.tokens[b].cpu().numpy().tolist()[: len(w.tokens)] == w.tokens, (seed, b)
+            assert int(res.n_accepted[b]) == w.n_accepted

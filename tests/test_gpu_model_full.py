@@ -1,26 +1,12 @@
 """GPU parity of the composed verify step at the BASELINE shapes against the
 float64 oracle (``oracle.model.verify_forward``), at the north-star bf16 bar
-rtol = atol = 1e-2:
+rtol = atol = 1e-2: two dense layers of the 27B shape (hidden 5120, SwiGLU
+17408, 40/8 heads of 128, vocab 151936), one request, 4 verify rows at
+positions 4092..4095 of a 4096-token context, with the K/V rows each layer
+writes and token-exact accept/reject on the produced logits.
 
-* cfg3 width: two dense layers of the 27B shape (hidden 5120, SwiGLU 17408,
-  40/8 heads of 128, vocab 151936), one request, 4 verify rows at positions
-  4092..4095 of a 4096-token context;
-* cfg5 width: one MoE layer of the 125B-class shape (hidden 4096, 256
-  experts top-8 of FFN 1536 plus a shared expert, 32/4 heads, vocab 151936),
-  4 requests x 4 rows at 8k contexts, Zipf-skewed routing. This model uses
-  the centered unit-gain weight recipe (so tokens route to different
-  experts), under which the logits have rms ~1 and the GPU-vs-oracle
-  difference is bf16 rounding noise of rms 0.003-0.005 (about one bf16 ulp
-  at the logits' scale: the two sides accumulate in fp32 and float64 and
-  round the same stored tensors to bf16, so roundings near a boundary go
-  opposite ways and propagate at unit gain). Its 3-sigma tails pass 0.01 on
-  ~0.05% of the elements (measured on this seed: 1203 of 2.4M fail atol
-  1e-2, 22 fail 1.5e-2, none 2e-2), so the bar is rtol 1e-2 with atol 2e-2
-  (five bf16 ulps at rms 1), plus a
-  relative L2 error <= 1e-2 on every row, and the routed expert ids equal
-  the oracle's exactly.
-
-The accept/reject on the produced logits is token-exact against the oracle.
+The full 64-layer step and the MoE shape are held to the bar layer by layer
+in ``test_gpu_model_depth.py``.
 """
 
 import numpy as np
@@ -83,32 +69,3 @@ def test_cfg3_width_two_layers_match_oracle(gpu):
                       S.SamplerConfig())
     assert res.tokens[0].cpu().numpy().tolist()[: len(w.tokens)] == w.tokens
     assert int(res.n_accepted[0]) == w.n_accepted
-
-
-def test_cfg5_width_moe_layer_matches_oracle(gpu):
-    from mtplx_amd.verify_step import MOE_125B, VerifyModel
-    from dataclasses import replace
-    cfg = replace(MOE_125B, layers=1)
-    model = VerifyModel(cfg, device="cuda", seed=23, keep_expert_source=True)
-    B, L, ctx = 4, 4, 8192
-    model.allocate_cache(B, ctx)
-    kc, vc = _caches(model, cfg.layers)
-    gen = torch.Generator(device="cuda").manual_seed(24)
-    tokens = torch.randint(0, cfg.vocab, (B, L), device="cuda", dtype=torch.int32, generator=gen)
-    starts = [ctx - L, ctx - L - 100, ctx - L - 1000, 5000]
-    qs = torch.tensor(starts, dtype=torch.int32, device="cuda")
-    model.route_log = []
-    logits = model.verify_logits(tokens, qs, check=True)
-    got = logits.cpu().numpy().astype(np.float64)
-    gpu_ids = model.route_log[0].cpu().numpy()
-    routes = []
-    want = verify_forward(model_params_numpy(model), cfg, tokens.cpu().numpy(), np.array(starts), kc, vc, routes)
-    ids = routes[0][0]
-    assert np.array_equal(np.sort(gpu_ids, axis=1), np.sort(ids, axis=1)), "routed expert ids differ"
-    assert_close(got, want, rtol=1e-2, atol=2e-2, what="cfg5-width logits")
-    rel = np.sqrt(((got - want) ** 2).sum(axis=1)) / np.sqrt((want ** 2).sum(axis=1))
-    assert (rel <= 1e-2).all(), rel
-    # Zipf skew with per-token spread: a few experts take many of the 128
-    # routed rows, and tokens do not all share one top-8
-    counts = np.bincount(ids.reshape(-1), minlength=cfg.n_experts)
-    assert counts.max() >= 4 and 24 <= (counts > 0).sum() < 128

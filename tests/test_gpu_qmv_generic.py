@@ -169,9 +169,13 @@ def test_crossrow_surface(gpu):
         q, (w, s, bb) = _layer(rng, n, k, gs, 4)
         y0 = crossrow_qmm(x, q.weight, q.scales, q.biases, group_size=gs)
         y1 = crossrow_qmm(x, q.weight, q.scales, q.biases, group_size=gs, xsums=t)
+        # the table is what the bias term reads: an all-zero table drops it
+        y2 = crossrow_qmm(x, q.weight, q.scales, q.biases, group_size=gs, xsums=torch.zeros_like(t))
         torch.cuda.synchronize()
-        assert torch.equal(y0, y1)
         want_y = round_to_bf16(qmm_affine(bits(x), w, s, bb, gs, 4))
         assert_close(bf16_values(y0), want_y, what=f"crossrow g{gs}")
+        assert_close(bf16_values(y1), want_y, what=f"crossrow g{gs} with the chunk-sum table")
+        want_nb = round_to_bf16(qmm_affine(bits(x), w, s, np.zeros_like(bb), gs, 4))
+        assert_close(bf16_values(y2), want_nb, what=f"crossrow g{gs} with a zero table")
     with pytest.raises(ValueError):
         crossrow_qmm(x, q.weight, q.scales, q.biases, group_size=64, xsums=t[:-8])

@@ -250,3 +250,86 @@ def test_spec_accept_greedy_lane(gpu):
     assert nacc.tolist() == [3, 1, 3, 3]
     assert out[1, :2].tolist() == [drafts[1, 0], target[1, 1].argmax()]
     assert out[0].tolist() == [*drafts[0].tolist(), int(target[0, K].argmax())]
+
+
+def _spec_ragged(target_rows, draft_rows, t_off, d_off, k_lens, drafts, uniforms, cfg):
+    """mtp_spec_accept_ragged through the facade on host arrays."""
+    from mtplx_amd.sampling import SamplerConfig, spec_accept_ragged
+    c = SamplerConfig(cfg.temperature, cfg.top_p, cfg.top_k)
+    cu = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a).astype(dt)).cuda()   # noqa: E731
+    res = spec_accept_ragged(cu(target_rows, np.float32), cu(t_off, np.int32), cu(draft_rows, np.float32),
+                             cu(d_off, np.int32), cu(k_lens, np.int32), cu(drafts, np.int32), cu(uniforms, np.float64), c)
+    torch.cuda.synchronize()
+    return (res.tokens.cpu().numpy(), res.n_accepted.cpu().numpy(), res.accept_probs.cpu().numpy(),
+            res.status.cpu().numpy())
+
+
+def _ragged_case(rng, V, k_lens, scale=3.0, corr=0.5):
+    """Packed target rows (K_b + 1 per request) and draft rows (K_b per request)."""
+    t_off = np.concatenate([[0], np.cumsum(np.asarray(k_lens) + 1)])
+    d_off = np.concatenate([[0], np.cumsum(k_lens)])
+    target = rng.normal(0, scale, (int(t_off[-1]), V)).astype(np.float32)
+    draft = np.concatenate([target[t_off[b]:t_off[b] + k] + rng.normal(0, corr, (k, V))
+                            for b, k in enumerate(k_lens)]).astype(np.float32)
+    return target, draft, t_off, d_off
+
+
+def test_spec_accept_ragged_out_of_range_request(gpu):
+    """A request whose depth or offsets point outside the buffers is skipped
+    on the device with status 2 (tokens -1, nothing accepted); the other
+    requests are token-exact against the oracle."""
+    cfg = S.SamplerConfig(0.6, 0.95, 20)
+    rng = np.random.default_rng(77)
+    V = 4096
+    k_lens = [3, 2, 1, 3]
+    target, draft, t_off, d_off = _ragged_case(rng, V, k_lens)
+    drafts = np.concatenate([S.sample_rows(draft[d_off[b]:d_off[b] + k], rng.random(k), cfg)
+                             for b, k in enumerate(k_lens)]).astype(np.int32)
+    uniforms = rng.random((len(k_lens), 4))
+    bad_k = np.array(k_lens, np.int32)
+    bad_k[1] = 7                                   # deeper than K_max = 3
+    bad_t = t_off[:-1].copy()
+    bad_t[2] = int(t_off[-1]) - 1                  # its 2 target rows run past n_target
+    bad_d = d_off[:-1].copy()
+    bad_d[3] = -1                                  # negative draft offset
+    for kl, to, do, hit in ((bad_k, t_off[:-1], d_off[:-1], 1), (np.array(k_lens, np.int32), bad_t, d_off[:-1], 2),
+                            (np.array(k_lens, np.int32), t_off[:-1], bad_d, 3)):
+        out, nacc, ap, st = _spec_ragged(target, draft, to, do, kl, drafts, uniforms, cfg)
+        assert st[hit] == 2 and nacc[hit] == 0 and (out[hit] == -1).all() and (ap[hit] == -1).all()
+        for b, k in enumerate(k_lens):
+            if b == hit:
+                continue
+            assert st[b] == 0
+            want = S.spec_accept(target[t_off[b]:t_off[b] + k + 1], draft[d_off[b]:d_off[b] + k],
+                                 drafts[d_off[b]:d_off[b] + k], uniforms[b], cfg)
+            assert int(nacc[b]) == want.n_accepted and out[b, : len(want.tokens)].tolist() == want.tokens
+
+
+def test_spec_accept_greedy_lane_ragged(gpu):
+    """The greedy lane over a ragged batch: each request accepts its drafts
+    while they equal the target argmax, corrects with the argmax at the first
+    mismatch, and takes the argmax of row K_b as its bonus."""
+    cfg = S.SamplerConfig(0.0, 1.0, 0)
+    rng = np.random.default_rng(19)
+    V = 5000
+    k_lens = [3, 1, 2, 3, 1]
+    target, draft, t_off, d_off = _ragged_case(rng, V, k_lens, scale=1.0, corr=0.0)
+    drafts = np.concatenate([target[t_off[b]:t_off[b] + k].argmax(axis=1) for b, k in enumerate(k_lens)])
+    drafts[d_off[3] + 1] = (drafts[d_off[3] + 1] + 1) % V      # request 3 rejects at depth 1
+    drafts[d_off[1]] = (drafts[d_off[1]] + 3) % V              # request 1 rejects at depth 0
+    out, nacc, ap, st = _spec_ragged(target, draft, t_off[:-1], d_off[:-1], np.array(k_lens), drafts,
+                                     np.zeros((len(k_lens), 4)), cfg)
+    assert (st == 0).all()
+    assert nacc.tolist() == [3, 0, 2, 1, 1]
+    for b, k in enumerate(k_lens):
+        arg = target[t_off[b]:t_off[b] + k + 1].argmax(axis=1)
+        want = []
+        for d in range(k + 1):
+            if d == k or drafts[d_off[b] + d] != arg[d]:
+                want.append(int(arg[d]))
+                break
+            want.append(int(drafts[d_off[b] + d]))
+        assert out[b, : len(want)].tolist() == want, b
+        assert (out[b, len(want):] == -1).all()
+    assert out[3, :2].tolist() == [drafts[d_off[3]], int(target[t_off[3] + 1].argmax())]
+    assert out[0, 3] == int(target[t_off[0] + 3].argmax())

@@ -71,7 +71,18 @@ def test_refusals(tmp_path):
                                    "mtp.fc.weight": torch.ones(4, dtype=torch.bfloat16)})
     with pytest.raises(PackError, match="q_norm"):
         read_mlx_pack(d)
-    read_mlx_pack(d, strict=False)                     # mtp.* is always ignored
+    with pytest.raises(PackError, match="change the decoder's math"):
+        read_mlx_pack(d, strict=False)                 # per-head q/k norms change the logits: always refused
+    d = tmp_path / "r"; d.mkdir()
+    write_pack(d, layers=1, extra={"model.layers.0.self_attn.rotary_emb.inv_freq": torch.ones(64),
+                                   "mtp.fc.weight": torch.ones(4, dtype=torch.bfloat16)})
+    with pytest.raises(PackError, match="inv_freq"):
+        read_mlx_pack(d)                               # strict: every unused tensor but mtp.* is refused
+    read_mlx_pack(d, strict=False)                     # rotary buffers and mtp.* cannot change the logits
+    d = tmp_path / "s"; d.mkdir()
+    write_pack(d, layers=1, extra={"model.layers.0.self_attn.q_proj.bias": torch.ones(512, dtype=torch.bfloat16)})
+    with pytest.raises(PackError):
+        read_mlx_pack(d, strict=False)                 # projection biases: refused
     d = tmp_path / "b"; d.mkdir()
     write_pack(d, layers=1, config_extra={"quantization": {"group_size": 64, "bits": 4,
                                                            "model.layers.0.mlp.down_proj": {"bits": 8}}})
