@@ -12,7 +12,9 @@ The MoE layer follows the reference's verify call of the sparse block
 ``:1544-1577``): router logits (bf16, a quantized projection whose last row
 is the shared-expert gate) plus the synthetic per-expert Zipf skew pick the
 top-k experts (value desc, id asc) with softmax weights renormalised over the
-k; routed rows go through the sorted SwiGLU chain; the shared expert is
+k; routed rows go through the sorted SwiGLU chain, stored as bf16 where
+the reference's chain stores them (gate|up product, silu, SwiGLU rows, each
+expert's down rows); the shared expert is
 ``sigmoid(gate) * shared_mlp(x)``; the block output ``routed + shared`` is
 added to the residual stream.
 
@@ -141,7 +143,8 @@ def decoder_layer(lay: dict, cfg, h: np.ndarray, lens, q_start, k_cache_layer, v
         ids, wts = route_topk(logits.astype(np.float64), cfg.top_k)
         if routes is not None:
             routes.append((ids, wts))
-        routed = round_to_bf16(moe_forward(xn, ids, wts, lay["expert_gate_up"], lay["expert_down"], gs))
+        routed = round_to_bf16(moe_forward(xn, ids, wts, lay["expert_gate_up"], lay["expert_down"], gs,
+                                           bf16_storage=True))
         sg = round_to_bf16(qmm_affine4(xn, *lay["shared_gate"], gs))
         su = round_to_bf16(qmm_affine4(xn, *lay["shared_up"], gs))
         sa = round_to_bf16(round_to_bf16(silu(sg)) * su)

@@ -76,15 +76,24 @@ def swiglu_rows(x, row_map, sorted_ids, w, scales, biases, group_size: int, bf16
     return round_to_bf16(round_to_bf16(silu(gu[:, :half])) * gu[:, half:])
 
 
-def moe_forward(x, indices, route_weights, gate_up, down, group_size: int) -> np.ndarray:
+def moe_forward(x, indices, route_weights, gate_up, down, group_size: int, bf16_storage: bool = False) -> np.ndarray:
     """Routed experts of one token block: sort -> SwiGLU rows -> down rows ->
     unsort -> score-weighted sum over top_k. ``gate_up``/``down`` are
-    ``(w, scales, biases)`` triples with a leading expert axis."""
+    ``(w, scales, biases)`` triples with a leading expert axis.
+
+    ``bf16_storage`` rounds where the reference's sorted chain stores bf16
+    tensors: the gathered gate|up product, ``silu(gate)`` and the SwiGLU rows
+    (``swiglu_rows``, ``mtplx/moe_sorted_gather.py:322-328``) and each
+    expert's down-projection rows, which the block then weights and sums
+    (``mtplx/models/qwen4_exp.py:1565-1577``, ``:1438-1441``)."""
     xf = _as_f64(x)
     T, top_k = np.asarray(indices).shape
     row_map, sorted_ids, inv_order, _ = sort_rows(indices)
-    h = swiglu_rows(xf, row_map, sorted_ids, *gate_up, group_size)
+    h = swiglu_rows(xf, row_map, sorted_ids, *gate_up, group_size, bf16_storage=bf16_storage)
     y_sorted = gather_qmm_rows(h, np.arange(len(row_map)), sorted_ids, *down, group_size)
+    if bf16_storage:
+        from .bf16 import round_to_bf16
+        y_sorted = round_to_bf16(y_sorted)
     y = y_sorted[inv_order.astype(np.int64)].reshape(T, top_k, -1)
     return (y * np.asarray(route_weights, dtype=np.float64)[:, :, None]).sum(axis=1)
 

@@ -195,9 +195,9 @@ def _layer_scalar(cfg, lay, h, tokens_shape, q_start, kc, vc):
         ex = [np.exp(score[e] - score[chosen[0]]) for e in chosen]
         routed = np.zeros(H)
         for j, e in enumerate(chosen):
-            gu = _matvec_scalar(tuple(a[e] for a in lay["expert_gate_up"]), x)
-            hh = np.array([_silu(gu[f]) * gu[F + f] for f in range(F)])
-            y = _matvec_scalar(tuple(a[e] for a in lay["expert_down"]), hh)
+            gu = [_rb(v) for v in _matvec_scalar(tuple(a[e] for a in lay["expert_gate_up"]), x)]
+            hh = np.array([_rb(_rb(_silu(gu[f])) * gu[F + f]) for f in range(F)])
+            y = np.array([_rb(v) for v in _matvec_scalar(tuple(a[e] for a in lay["expert_down"]), hh)])
             routed += (ex[j] / sum(ex)) * y
         sg = _matvec_scalar(lay["shared_gate"], x)
         su = _matvec_scalar(lay["shared_up"], x)
