@@ -10,7 +10,8 @@ Prints one JSON line. ``value`` = verify rows/s = B*(K+1)/t_step. The
 ``roofline`` object times the step's dominant kernel (the fused norm+gate/up
 quantized matmul, one launch per layer's weights, so no launch re-reads
 cached weights) with HIP events on the stream it runs on; ``cpu_baseline``
-times the float64 NumPy oracle on a bounded sample of the same step.
+times an fp32 NumPy/BLAS port of the same step (weights dequantised ahead of
+time) on a bounded sample.
 """
 
 from __future__ import annotations
@@ -167,8 +168,12 @@ def _gate_up_launcher(model, M, x, ss, y, ysum):
 
 
 def roofline_qmv_cfg1(reps: int = 64, nsets: int = 8) -> dict:
-    """BASELINE cfg1 qmv (x [4,5120] . W [17408,5120] 4-bit g64), 8 rotating weight
-    sets (400 MB > 256 MB MALL) so every launch streams from HBM."""
+    """BASELINE cfg1 qmv (x [4,5120] . W [17408,5120] 4-bit g64) on the verify
+    step's own path: packed layout 2 (the 16x16x32 MFMA form for 4 rows), the
+    tail split over all CUs with the step's shared workspace, launches
+    replayed from a HIP graph; 8 rotating weight sets (400 MB > the 256 MB
+    MALL) so every launch streams from HBM. Timed with HIP events on the
+    replay stream."""
     import torch
 
     from mtplx_amd import _lib
@@ -178,30 +183,68 @@ def roofline_qmv_cfg1(reps: int = 64, nsets: int = 8) -> dict:
     gen = torch.Generator(device="cuda").manual_seed(1)
     sets = [QuantizedLinear.random(N, K, gs, generator=gen) for _ in range(nsets)]
     for q in sets:
-        q.pack()
+        q.pack(layout=2)
+        q.release_source()
     x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-    st = _lib.stream_handle()
+    ws = _lib.WORKSPACES.get(_lib.query("mtp_qmv_workspace_bytes", M, N, K, 1), "bench_cfg1")
+    stream = torch.cuda.Stream()
 
     def launch(q):
-        _lib.qmv_ex(st, x=x, w0=q.packed, y0=y, M=M, N=N, K=K, group_size=gs, xmode=0, emode=0, packed=1)
+        _lib.qmv_ex(_lib.stream_handle(), x=x, w0=q.packed_mf16, y0=y, M=M, N=N, K=K, group_size=gs, xmode=0,
+                    emode=0, packed=2, ws=ws, ws_bytes=ws.numel())
 
-    for q in sets:
-        launch(q)
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(reps):
-        launch(sets[i % nsets])
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / reps
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        for q in sets:
+            launch(q)
+        stream.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            for q in sets:
+                launch(q)
+    us = _replay_us(graph, stream, max(1, reps // nsets)) / nsets
     byts = _qmv_bytes(M, N, K, gs)
     gbs = byts / us / 1e3
-    return {"kernel": "qmv_stream_kernel<NW=4,R=4,X_PLAIN,E_STORE,packed> (mtp_qmv_affine4_ex)",
-            "achieved": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": byts}
+    return {"kernel": "qmv_stream_kernel<NW=4,R=4,X_PLAIN,E_STORE,packed,MF> (mtp_qmv_affine4_ex, packed layout 2, "
+                      "tail split, graph replay)",
+            "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "avg_launch_us": round(us, 3),
+            "algorithmic_bytes_per_launch": byts, "target_us_at_70pct": round(byts / (0.7 * HBM_PEAK_GBS) / 1e3, 2)}
+
+
+def accept_leg_cfg1(reps: int = 64, nsets: int = 64) -> dict:
+    """BASELINE cfg1's accept leg: rejection sampling with residual
+    correction for 3 drafts over fp32 logits, target [4, 151936] and draft
+    [3, 151936] ~N(0, 3), temperature 0.6, top-k 20, top-p 0.95, seeded
+    uniforms (``mtp_spec_accept``: ``vocab_partials`` over the 7 rows, then
+    ``accept_laws``). 64 rotating logit sets (272 MB > the 256 MB MALL),
+    launches replayed from a HIP graph, HIP events on the replay stream.
+    Algorithmic bytes: the 7 logit rows read once (4,254,208 B)."""
+    import torch
+
+    from mtplx_amd.sampling import SamplerConfig, spec_accept
+
+    B, K, V = 1, 3, 151936
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    tl = [(torch.randn((B, K + 1, V), device="cuda", generator=gen) * 3.0) for _ in range(nsets)]
+    dl = [(t[:, :K] + 0.5 * torch.randn((B, K, V), device="cuda", generator=gen)).contiguous() for t in tl]
+    ids = torch.randint(0, V, (B, K), device="cuda", dtype=torch.int32, generator=gen)
+    u = torch.rand((B, K + 1), device="cuda", dtype=torch.float64, generator=gen)
+    cfg = SamplerConfig(0.6, 0.95, 20)
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        for i in range(nsets):
+            res = spec_accept(tl[i], dl[i], ids, u, cfg)
+        stream.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(nsets):
+                res = spec_accept(tl[i], dl[i], ids, u, cfg)
+    us = _replay_us(graph, stream, max(1, reps // nsets)) / nsets
+    assert int(res.status.max().item()) == 0
+    byts = (2 * K + 1) * B * V * 4
+    return {"kernels": "vocab_partials + accept_laws (mtp_spec_accept)", "rows": "target [4,151936] + draft [3,151936]",
+            "avg_step_us": round(us, 3), "algorithmic_bytes": byts, "achieved_gbs": round(byts / us / 1e3, 1),
+            "frac_hbm": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
 def qmm_rows(M: int, reps: int = 64, nsets: int = 8) -> dict:
@@ -554,8 +597,8 @@ def cpu_threads() -> int:
 
 
 def cpu_baseline(layers: int, timeout_s: int = 300) -> dict | None:
-    """Float64 NumPy oracle on a bounded sample in a child process, its BLAS
-    on cpu_threads() threads."""
+    """The CPU port on a bounded sample in a child process, its BLAS on
+    cpu_threads() threads."""
     t = str(cpu_threads())
     env = dict(os.environ, OMP_NUM_THREADS=t, OPENBLAS_NUM_THREADS=t, MKL_NUM_THREADS=t)
     cmd = [sys.executable, "-c", f"import sys; sys.path.insert(0, {ROOT!r}); import bench; bench._cpu_child({layers})"]
@@ -571,39 +614,66 @@ def cpu_baseline(layers: int, timeout_s: int = 300) -> dict | None:
 
 
 def _cpu_child(layers: int) -> None:
-    """Three passes of one decoder layer (a few seconds each here), 1/4 of
-    the lm_head and the sampler on the oracle, extrapolated to the full
-    depth-3 verify step of the 27B shape (every layer has the same shapes,
-    so one layer's weights serve each pass)."""
+    """A CPU port of the depth-3 verify step of the 27B shape in fp32 with
+    the weights dequantised ahead of time (untimed; a CPU serving the model
+    would hold them so): per layer RMSNorm, q|k|v, RoPE, GQA attention over
+    the 4096-token cache, o, RMSNorm, gate/up + SwiGLU, down, every matmul a
+    multithreaded fp32 BLAS product; then 1/4 of the lm_head and the
+    sampler's accept step (the fp64 oracle). Three passes of one layer (every
+    layer has the same shapes) are timed and extrapolated to the step."""
     import numpy as np
 
-    from oracle import attention as A
     from oracle import sampler as S
-    from oracle.moe import silu
-    from oracle.qmv import make_affine4_weights, qmm_affine4
+    from oracle.qmv import dequantize_affine4, make_affine4_weights
 
     SAMPLE_LAYERS, LM_PART = 3, 4
     rng = np.random.default_rng(0)
     M, H, F, Hq, Hkv, D, V, ctx = 4, 5120, 17408, 40, 8, 128, 151936, 4096
-    lay = {n: make_affine4_weights(rng, o, i) for n, o, i in
-           [("qkv", (Hq + 2 * Hkv) * D, H), ("o", H, Hq * D), ("g", F, H), ("u", F, H), ("d", H, F)]}
-    lm = make_affine4_weights(rng, V // LM_PART, H)
-    k = rng.standard_normal((1, Hkv, ctx, D)).astype(np.float32)
-    v = rng.standard_normal((1, Hkv, ctx, D)).astype(np.float32)
-    h = rng.standard_normal((M, H))
+    rep = Hq // Hkv
+
+    def deq(n, k):
+        return dequantize_affine4(*make_affine4_weights(rng, n, k), 64).astype(np.float32)
+
+    W = {n: deq(o, i) for n, o, i in
+         [("qkv", (Hq + 2 * Hkv) * D, H), ("o", H, Hq * D), ("g", F, H), ("u", F, H), ("d", H, F)]}
+    lm = deq(V // LM_PART, H)
+    kc = rng.standard_normal((Hkv, ctx, D)).astype(np.float32)
+    vc = rng.standard_normal((Hkv, ctx, D)).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    h = rng.standard_normal((M, H)).astype(np.float32)
+    pos = np.arange(ctx - M, ctx, dtype=np.float32)
+    inv = (1.0e6 ** (-(np.arange(D // 2, dtype=np.float32) * 2.0) / D)).astype(np.float32)
+    cos, sin = np.cos(pos[:, None] * inv), np.sin(pos[:, None] * inv)
+    mask = np.where(np.arange(ctx)[None, :] <= (ctx - M + np.arange(M))[:, None], 0.0, -np.inf).astype(np.float32)
+
+    def norm(x):
+        return x / np.sqrt((x * x).mean(axis=1, keepdims=True) + 1e-6) * nw
+
+    def rope(x):   # [M, heads, D]
+        x1, x2 = x[..., : D // 2], x[..., D // 2:]
+        c, s_ = cos[:, None, :], sin[:, None, :]
+        return np.concatenate([x1 * c - x2 * s_, x1 * s_ + x2 * c], axis=-1)
+
     t0 = time.perf_counter()
     for _ in range(SAMPLE_LAYERS):
-        xn = h / np.sqrt((h ** 2).mean(axis=1, keepdims=True) + 1e-6)
-        qkv = qmm_affine4(xn, *lay["qkv"], 64)
-        q = qkv[:, : Hq * D].reshape(M, Hq, D).transpose(1, 0, 2)[None]
-        att = A.ragged_gqa_attention(q, k, v, [ctx - M])
-        h = h + qmm_affine4(att[0].transpose(1, 0, 2).reshape(M, Hq * D), *lay["o"], 64)
-        xn = h / np.sqrt((h ** 2).mean(axis=1, keepdims=True) + 1e-6)
-        a = silu(qmm_affine4(xn, *lay["g"], 64)) * qmm_affine4(xn, *lay["u"], 64)
-        h = h + qmm_affine4(a, *lay["d"], 64)
+        qkv = (norm(h) @ W["qkv"].T).reshape(M, Hq + 2 * Hkv, D)
+        q, k, v = rope(qkv[:, :Hq]), rope(qkv[:, Hq:Hq + Hkv]), qkv[:, Hq + Hkv:]
+        kc[:, ctx - M:] = k.transpose(1, 0, 2)
+        vc[:, ctx - M:] = v.transpose(1, 0, 2)
+        att = np.empty((M, Hq, D), np.float32)
+        for g in range(Hkv):
+            qg = q[:, g * rep:(g + 1) * rep].transpose(1, 0, 2).reshape(rep * M, D)
+            sc = (qg @ kc[g].T) / np.float32(np.sqrt(D)) + np.tile(mask, (rep, 1))
+            p = np.exp(sc - sc.max(axis=1, keepdims=True))
+            o = (p @ vc[g]) / p.sum(axis=1, keepdims=True)
+            att[:, g * rep:(g + 1) * rep] = o.reshape(rep, M, D).transpose(1, 0, 2)
+        h = h + att.reshape(M, Hq * D) @ W["o"].T
+        xn = norm(h)
+        gt, up = xn @ W["g"].T, xn @ W["u"].T
+        h = h + (gt / (1.0 + np.exp(-gt)) * up) @ W["d"].T
     t_layer = (time.perf_counter() - t0) / SAMPLE_LAYERS
     t0 = time.perf_counter()
-    qmm_affine4(xn, *lm, 64)
+    norm(h) @ lm.T
     t_lm = (time.perf_counter() - t0) * LM_PART
     logits = rng.normal(0, 3, (7, V))
     t0 = time.perf_counter()
@@ -612,11 +682,11 @@ def _cpu_child(layers: int) -> None:
     t_step = layers * t_layer + t_lm + t_acc
     threads = int(os.environ.get("OPENBLAS_NUM_THREADS", "1"))
     print(json.dumps({"value": round(M / t_step, 4), "unit": "verify rows/s", "cores": threads, "kind": "port",
-                      "sample": f"float64 NumPy oracle, BLAS on {threads} threads (dequantisation and the "
-                                f"sampler single-threaded): {SAMPLE_LAYERS} passes of one decoder layer "
-                                f"({t_layer:.2f} s each; the step has {layers}) + 1/{LM_PART} of lm_head "
-                                f"({t_lm / LM_PART:.2f} s) + accept ({t_acc:.3f} s), extrapolated to the "
-                                f"full step ({t_step:.1f} s)",
+                      "sample": f"fp32 NumPy/BLAS port on {threads} threads, weights dequantised ahead of time "
+                                f"(untimed): {SAMPLE_LAYERS} passes of one 27B-shaped decoder layer at 4096 context "
+                                f"({t_layer * 1e3:.1f} ms each; the step has {layers}) + 1/{LM_PART} of lm_head "
+                                f"({t_lm / LM_PART * 1e3:.1f} ms) + the fp64 oracle's accept step "
+                                f"({t_acc * 1e3:.1f} ms), extrapolated to the full step ({t_step * 1e3:.0f} ms)",
                       "host_cpu_count": os.cpu_count()}))
 
 
@@ -635,7 +705,7 @@ def main() -> int:
                          "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--profile-step", action="store_true",
                     help="only run one eager verify step and a 256 MiB copy, for rocprofv3 --pmc over every kernel")
-    ap.add_argument("--workload", choices=["cfg2", "cfg4", "cfg5"], default=None,
+    ap.add_argument("--workload", choices=["cfg1", "cfg2", "cfg4", "cfg5"], default=None,
                     help="only run that configuration's measurement (its sub-line, printed alone; for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -652,6 +722,9 @@ def main() -> int:
     _lib.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.workload == "cfg1":
+        print(json.dumps({"cfg1_qmv": roofline_qmv_cfg1(), "cfg1_accept": accept_leg_cfg1()}), flush=True)
+        return 0
     if args.workload == "cfg2":
         print(json.dumps(cfg2_attention()), flush=True)
         return 0
@@ -710,6 +783,7 @@ def main() -> int:
     parts.discard("none")
     if "cfg1" in parts:
         roof["cfg1_qmv"] = roofline_qmv_cfg1()
+        roof["cfg1_accept"] = accept_leg_cfg1()
     if "qmm" in parts:
         for m in (16, 32, 64):
             roof[f"m{m}_qmm"] = qmm_rows(m)

@@ -255,7 +255,9 @@ __device__ __forceinline__ void attn_vt_body(const AttnParams& p, const int unit
   }
   __syncthreads();
   if (!act) return;
-  for (int idx = 4 * tid; idx < 32 * kHD; idx += 4 * kVtWaves * 64) {
+  // Only the live query columns (rep * L of the 32): the merge reads no others.
+  const int live = rep * p.L;
+  for (int idx = 4 * tid; idx < live * kHD; idx += 4 * kVtWaves * 64) {
     const int so = (idx / kHD) * kOS + (idx % kHD);
     float4 v = *reinterpret_cast<const float4*>(&s_o[so]);
 #pragma unroll
@@ -447,7 +449,9 @@ __device__ __forceinline__ void attn_vl_piece(const AttnParams& p, const int b, 
             make_float4(o[t][4 * j] * sc, o[t][4 * j + 1] * sc, o[t][4 * j + 2] * sc, o[t][4 * j + 3] * sc);
   }
   __syncthreads();
-  for (int idx = 4 * tid; idx < 32 * kHD; idx += 4 * kVtWaves * 64) {
+  // Only the live query columns (rep * L of the 32): the merge reads no others.
+  const int live = (p.Hq / p.Hkv) * p.L;
+  for (int idx = 4 * tid; idx < live * kHD; idx += 4 * kVtWaves * 64) {
     const int so = (idx / kHD) * kOS + (idx % kHD);
     float4 v = *reinterpret_cast<const float4*>(&s_o[so]);
 #pragma unroll

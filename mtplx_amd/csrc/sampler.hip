@@ -16,9 +16,9 @@
 //     4096-logit chunk once (coalesced), and emits the chunk's fp64 max of
 //     l/T, fp64 sum exp(l/T - max), a non-finite flag, and its top-k keys.
 //     A key is (order-preserving float bits << 32) | ~id, so one u64 max is
-//     "value desc, id asc". Top-k: each wave selects from its 512 logits
-//     with per-thread cached bests (each round only the winning thread
-//     rescans its 8 registers), then wave 0 merges the eight sorted lists.
+//     "value desc, id asc". Top-k: a radix select finds the k-th largest key
+//     eight bits at a time (LDS digit histograms); the keys at or above it
+//     are gathered and one wave sorts them (bitonic across its 64 lanes).
 //     Target and draft rows go through one launch.
 //  2. accept_laws: one workgroup per request, one wave per row law: merges
 //     the row's chunks (max/sum-exp combine in fixed chunk order, top-k as a
@@ -81,7 +81,6 @@ __global__ __launch_bounds__(kSampThreads) void vocab_partials(const float* __re
     if (!greedy) mloc = fmax(mloc, qv[e]);
   }
   __shared__ double s_red[NWV];
-  __shared__ uint64_t s_wkey[NWV][kMaxTopK];
   __shared__ int s_nf[NWV];
 
   double mchunk = -INFINITY, schunk = 0.0;
@@ -110,46 +109,121 @@ __global__ __launch_bounds__(kSampThreads) void vocab_partials(const float* __re
     if (lane == 0) s_nf[wave] = nf;
   }
 
-  // Top-k: each wave selects the top ksel of its own 512 logits (cached
-  // per-thread bests, no barriers), then wave 0 merges the NWV sorted lists.
+  // Top-k by radix select: the ksel-th largest key K* of the chunk is found
+  // eight bits at a time from the top (an LDS histogram of the next digit
+  // among the keys that share the digits found so far; wave 0 finds the digit
+  // holding rank r from the top), stopping as soon as the boundary digit's
+  // keys all belong to the top ksel. Keys are distinct (the id is part of
+  // the key), so the selected set is exact; its at most 64 keys are then
+  // gathered in LDS and sorted descending by one wave (bitonic over 64 lanes).
   uint64_t keys[kEPT];
 #pragma unroll
   for (int e = 0; e < kEPT; ++e) {
     const int id = base + e * kSampThreads + tid;
     keys[e] = (id < V && !isnan(v[e])) ? make_key(v[e], id) : 0ull;
   }
-  uint64_t best = 0ull;
+  __shared__ int s_hist[256];
+  __shared__ uint64_t s_sel[kMaxTopK];
+  __shared__ int s_rank, s_cnt, s_nsel, s_nvalid;
+  __shared__ uint64_t s_prefix;
+  {
+    int nv = 0;
 #pragma unroll
-  for (int e = 0; e < kEPT; ++e) best = keys[e] > best ? keys[e] : best;
-
-  for (int r = 0; r < ksel; ++r) {
-    const uint64_t win = wave_max_u64(best);
-    if (lane == 0) s_wkey[wave][r] = win;
-    if (win != 0ull && best == win) {
-      uint64_t nb = 0ull;
+    for (int e = 0; e < kEPT; ++e) nv += keys[e] != 0ull;
+    if (tid == 0) {
+      s_nvalid = 0;
+      s_nsel = 0;
+    }
+    __syncthreads();
+    if (nv) atomicAdd(&s_nvalid, nv);
+  }
+  __syncthreads();
+  const int nvalid = s_nvalid;
+  // Keys >= thr are selected; with at most ksel valid keys, all of them.
+  uint64_t thr = 1ull;
+  if (nvalid > ksel) {
+    uint64_t prefix = 0ull;
+    int rank = ksel;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+      for (int i = tid; i < 256; i += kSampThreads) s_hist[i] = 0;
+      __syncthreads();
+      const uint64_t hi_mask = shift == 56 ? 0ull : ~((1ull << (shift + 8)) - 1ull);
 #pragma unroll
       for (int e = 0; e < kEPT; ++e)
-        if (keys[e] < win && keys[e] > nb) nb = keys[e];
-      best = nb;
+        if (keys[e] != 0ull && (keys[e] & hi_mask) == prefix) atomicAdd(&s_hist[(keys[e] >> shift) & 255u], 1);
+      __syncthreads();
+      if (wave == 0) {
+        // lane l holds digits 255 - 4l .. 252 - 4l (descending); the
+        // inclusive prefix over lanes counts the keys at or above each block
+        int c[4], tot = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          c[j] = s_hist[255 - 4 * lane - j];
+          tot += c[j];
+        }
+        int incl = tot;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int y = __shfl_up(incl, o, 64);
+          if (lane >= o) incl += y;
+        }
+        const int above = incl - tot;
+        if (above < rank && rank <= incl) {   // exactly one lane holds the rank
+          int d = 0, a = above, cnt = 0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (cnt == 0 && a + c[j] >= rank) {
+              d = 255 - 4 * lane - j;
+              cnt = c[j];
+            } else if (cnt == 0) {
+              a += c[j];
+            }
+          }
+          s_prefix = prefix | ((uint64_t)d << shift);
+          s_rank = rank - a;
+          s_cnt = cnt;
+        }
+      }
+      __syncthreads();
+      // (wave 0 rewrites these only after the next pass's two barriers,
+      // which every thread reaches after reading them here)
+      prefix = s_prefix;
+      rank = s_rank;
+      const int cnt = s_cnt;
+      if (cnt == rank || shift == 0) {
+        // every key under the boundary prefix is in (cnt == rank), or the
+        // prefix is the full key K* itself: select the keys >= prefix
+        thr = prefix;
+        break;
+      }
     }
   }
+  // Gather the selected keys (at most ksel <= 64), then sort them descending.
+#pragma unroll
+  for (int e = 0; e < kEPT; ++e)
+    if (keys[e] != 0ull && keys[e] >= thr) {
+      const int at = atomicAdd(&s_nsel, 1);
+      if (at < kMaxTopK) s_sel[at] = keys[e];   // at most ksel <= kMaxTopK by construction
+    }
   __syncthreads();
   if (wave != 0) return;
   ChunkPart* out = parts + (size_t)row * n_chunks + chunk;
-  int ptr = 0;
-  uint64_t h = lane < NWV ? s_wkey[lane][0] : 0ull;
-  for (int r = 0; r < ksel; ++r) {
-    uint64_t w = h;   // max over lanes 0..7 (NWV = 8)
-    w = umax64(w, dpp64<kDppX1>(w));
-    w = umax64(w, dpp64<kDppX2>(w));
-    w = umax64(w, dpp64<kDppHalf>(w));
-    const uint64_t win = rl64(w, 0);
-    if (lane == 0) out->keys[r] = win;
-    if (lane < NWV && win != 0ull && h == win) {
-      ++ptr;
-      h = ptr < ksel ? s_wkey[lane][ptr] : 0ull;
+  const int nsel = s_nsel < kMaxTopK ? s_nsel : kMaxTopK;
+  uint64_t kv = lane < nsel ? s_sel[lane] : 0ull;
+  // bitonic sort of 64 keys across the wave, descending
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(kv >> 32), stride, 64) << 32) |
+                         (uint32_t)__shfl_xor((int)(uint32_t)kv, stride, 64);
+      const bool lower = (lane & stride) == 0;
+      const bool desc = (lane & size) == 0;   // the last pass (size 64) orders all 64 descending
+      const bool take_max = lower == desc;
+      kv = take_max ? (kv > o ? kv : o) : (kv < o ? kv : o);
     }
   }
+  if (lane < ksel) out->keys[lane] = kv;
   if (lane == 0) {
     int nf = 0;
 #pragma unroll
