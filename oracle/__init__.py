@@ -1,7 +1,7 @@
 """CPU oracle for the speculative-verify hot path — TEST INFRASTRUCTURE ONLY.
 
-This package restates, in NumPy float64 (and plain C under ``oracle/c``), the
-algorithms of the reference's verify path:
+This package restates, in NumPy float64, the algorithms of the reference's
+verify path:
 
 * ``qmv``      4-bit affine group-wise quantized matmul
                (``mtplx/verify_kernels.py:69-88``, ``:372``; ``mtplx/verify_qmv.py:58-191``)
@@ -14,7 +14,8 @@ algorithms of the reference's verify path:
                (``mtplx/ragged_kv_cache.py:201-496``)
 * ``moe``      expert sort, gathered quantized matmul, SwiGLU, unsort
                (``mtplx/moe_sorted_gather.py:170-328``, ``mtplx/models/qwen4_exp.py:1544-1577``)
-* ``model``    one verify step of a dense decoder built from the above.
+* ``model``    one verify step of a dense or MoE decoder built from the above
+               (``decoder_layer`` is the one-layer restatement both use).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
 leg may import it, and only as the checker. The product package
