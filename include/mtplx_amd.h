@@ -414,6 +414,17 @@ int mtp_gather_qmv_affine4_packed(const void* x, const uint32_t* row_map, const 
                                   const int32_t* active, const void* wp, void* y, int max_rows_per_expert, int E,
                                   int N, int K, int group_size, int emode, int rows_per_expert, void* stream);
 
+/* mtp_gather_qmv_affine4_packed for one row class of experts: row_class 1
+ * runs only the experts with 1-4 rows, 2 only those with 5 or more, 0 both
+ * (the call above). Each class is a launch of its own, so a caller can put
+ * them on two streams and run them side by side (the 5+-row class is latency
+ * bound at cfg5). Same arguments otherwise; the same rows of y are written
+ * as by the call above. Replaces the same reference call sites. */
+int mtp_gather_qmv_affine4_packed_rows(const void* x, const uint32_t* row_map, const int32_t* expert_off,
+                                       const int32_t* active, const void* wp, void* y, int max_rows_per_expert, int E,
+                                       int N, int K, int group_size, int emode, int rows_per_expert, int row_class,
+                                       void* stream);
+
 /* Expert offsets int32 [E+1] and the active list [1+E] (as mtp_moe_sort
  * writes them) from ids already sorted ascending, the sorted_indices of the
  * reference entry points (mtplx/moe_sorted_gather.py:241 gather_qmm_rows,

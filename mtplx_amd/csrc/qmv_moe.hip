@@ -139,8 +139,10 @@ static int moe_launch(const QmmParams& p, const MoeUnits& mu, int rows_lds, hipS
   return MTP_OK;
 }
 
+// row_class: 0 both launches, 1 only the experts with 1-4 rows, 2 only those
+// with more (two streams can then run the classes side by side).
 template <int EM>
-static int moe_launch_classes(const QmmParams& p, MoeUnits mu, int max_rows, hipStream_t st) {
+static int moe_launch_classes(const QmmParams& p, MoeUnits mu, int max_rows, hipStream_t st, int row_class) {
   // rows <= 4: one row tile, LDS for four rows
   mu.rows_tile = 4;
   mu.row_tiles = 1;
@@ -149,8 +151,11 @@ static int moe_launch_classes(const QmmParams& p, MoeUnits mu, int max_rows, hip
   // six tiles per unit: graph-free cfg5 steps measured 14.3 ms at 4-6,
   // 14.7 at 8, 15.0 at 10 and 16.0 with one unit per CU
   mu.tpu = env_int("MTPLX_AMD_MOE_TILES_SMALL", 6);
-  int rc = moe_launch<4, 4, EM>(p, mu, 4, st);
-  if (rc != MTP_OK || max_rows <= 4) return rc;
+  if (row_class != 2) {
+    const int rc = moe_launch<4, 4, EM>(p, mu, 4, st);
+    if (rc != MTP_OK) return rc;
+  }
+  if (max_rows <= 4 || row_class == 1) return MTP_OK;
   // rows >= 5: 16-row tiles (the rows of an expert past 16 in further
   // tiles). 8-row tiles on 4-wave workgroups measured the same at cfg5.
   mu.rows_tile = 16;
@@ -168,11 +173,13 @@ using namespace mtp;
 // Packed form of mtp_gather_qmv_affine4: wp is mtp_pack_affine4 of the
 // [E * rows_per_expert, K] matrix (expert e's rows at e * rows_per_expert;
 // for the fused pair its N gate rows then its N up rows).
-MTP_API int mtp_gather_qmv_affine4_packed(const void* x, const uint32_t* rowmap, const int32_t* expert_off,
-                                          const int32_t* active, const void* wp, void* y, int max_rows_per_expert,
-                                          int E, int N, int K, int group_size, int emode, int rows_per_expert,
-                                          void* stream) {
-  const char* who = "mtp_gather_qmv_affine4_packed";
+static int gather_packed_run(const void* x, const uint32_t* rowmap, const int32_t* expert_off, const int32_t* active,
+                             const void* wp, void* y, int max_rows_per_expert, int E, int N, int K, int group_size,
+                             int emode, int rows_per_expert, int row_class, void* stream, const char* who) {
+  if (row_class < 0 || row_class > 2) {
+    set_error("%s: row_class %d (0 all experts, 1 those with 1-4 rows, 2 those with more)", who, row_class);
+    return MTP_ERR_ARG;
+  }
   if (!x || !expert_off || !active || !wp || !y || max_rows_per_expert < 1 || max_rows_per_expert > 32767 || E < 1 ||
       E > 65535 || N < 32 || K < 256) {
     set_error("%s: bad arguments", who);
@@ -221,12 +228,28 @@ MTP_API int mtp_gather_qmv_affine4_packed(const void* x, const uint32_t* rowmap,
   hipStream_t st = (hipStream_t)stream;
   int rc;
   if (emode == E_DUAL_SWIGLU)
-    rc = moe_launch_classes<E_DUAL_SWIGLU>(p, mu, max_rows_per_expert, st);
+    rc = moe_launch_classes<E_DUAL_SWIGLU>(p, mu, max_rows_per_expert, st, row_class);
   else
-    rc = moe_launch_classes<E_STORE>(p, mu, max_rows_per_expert, st);
+    rc = moe_launch_classes<E_STORE>(p, mu, max_rows_per_expert, st, row_class);
   if (rc != MTP_OK) {
     set_error("%s: K=%d needs more LDS than a workgroup has", who, K);
     return rc;
   }
   return launch_check(who);
+}
+
+MTP_API int mtp_gather_qmv_affine4_packed(const void* x, const uint32_t* rowmap, const int32_t* expert_off,
+                                          const int32_t* active, const void* wp, void* y, int max_rows_per_expert,
+                                          int E, int N, int K, int group_size, int emode, int rows_per_expert,
+                                          void* stream) {
+  return gather_packed_run(x, rowmap, expert_off, active, wp, y, max_rows_per_expert, E, N, K, group_size, emode,
+                           rows_per_expert, 0, stream, "mtp_gather_qmv_affine4_packed");
+}
+
+MTP_API int mtp_gather_qmv_affine4_packed_rows(const void* x, const uint32_t* rowmap, const int32_t* expert_off,
+                                               const int32_t* active, const void* wp, void* y,
+                                               int max_rows_per_expert, int E, int N, int K, int group_size, int emode,
+                                               int rows_per_expert, int row_class, void* stream) {
+  return gather_packed_run(x, rowmap, expert_off, active, wp, y, max_rows_per_expert, E, N, K, group_size, emode,
+                           rows_per_expert, row_class, stream, "mtp_gather_qmv_affine4_packed_rows");
 }

@@ -30,6 +30,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 from dataclasses import dataclass
 
 import torch
@@ -44,6 +45,18 @@ from .sampling import SamplerConfig, narrow_law, spec_accept
 # multiple of 128) makes each request's partials and merge independent of the
 # rest of the batch; 1024 keeps at most 256 splits up to 256k-key contexts.
 EXACT_SPLIT_KEYS = 1024
+
+
+# MoE layers run the 5+-row experts and the shared expert on a second stream
+# beside the 1-4-row experts (MTPLX_AMD_MOE_SIDE_STREAM=0: one stream).
+MOE_SIDE_STREAM = (os.environ.get("MTPLX_AMD_MOE_SIDE_STREAM") or "1").strip() not in {"0", "false", "off", "no"}
+
+
+def qmv_ws_bytes(M: int, c: "DecoderConfig") -> int:
+    """Split-K workspace of the streaming matmul for every projection of the step."""
+    ffn = c.expert_ffn if c.n_experts else c.ffn
+    ns = (c.qkv_out, c.hidden, ffn, c.vocab) + ((c.shared_ffn, c.n_experts + 1) if c.n_experts else ())
+    return max(_lib.query("mtp_qmv_workspace_bytes", M, n, 1, 1) for n in ns)
 
 
 def _exact_lane(sampler: SamplerConfig) -> bool:
@@ -238,6 +251,7 @@ class VerifyModel:
                         q.release_source()
         self.lm_head.pack()
         self.lm_head.pack(layout=2)
+        self._side = None
         self.k_cache: list[torch.Tensor] = []
         self.v_cache: list[torch.Tensor] = []
         self.cap = 0
@@ -245,6 +259,12 @@ class VerifyModel:
         # A list here receives each MoE layer's routed expert ids (int32
         # [M, top_k], on the device) as the forward runs; None records nothing.
         self.route_log: list | None = None
+
+    def _side_stream(self) -> torch.Stream:
+        """The model's second stream (default priority), made on first use."""
+        if self._side is None:
+            self._side = torch.cuda.Stream(device=self.device)
+        return self._side
 
     # -- cache ----------------------------------------------------------------
     def allocate_cache(self, batch: int, capacity: int, *, fill_random: bool = True) -> None:
@@ -395,8 +415,7 @@ class VerifyModel:
         ql = None if q_lens is None else q_lens.to(torch.int32).contiguous()
         # Per-tile streaming kernel with a workspace: its leftover tiles (e.g.
         # the last 32 of gate/up's 544 on 256 CUs) are split by K over all CUs.
-        qmv_nb = max(_lib.query("mtp_qmv_workspace_bytes", M, n, 1, 1) for n in (c.qkv_out, H, ffn, c.vocab))
-        qws = _lib.WORKSPACES.get(qmv_nb, "qmv", dev)
+        qws = _lib.WORKSPACES.get(qmv_ws_bytes(M, c), "qmv", dev)
 
         def qmv(stream, **kw):
             _lib.qmv_ex(stream, ws=qws, ws_bytes=qws.numel(), **kw)
@@ -483,25 +502,58 @@ class VerifyModel:
         R = M * c.top_k
         F = c.expert_ffn
         hsorted = torch.empty((R, F), dtype=torch.bfloat16, device=dev)
-        # Routed experts over their packed stacks: gate|up + SwiGLU on the
-        # token rows gathered by row_map, then down on the sorted rows.
-        call("mtp_gather_qmv_affine4_packed", xn.data_ptr(), es.row_map.data_ptr(), es.expert_off.data_ptr(),
-             es.active.data_ptr(), L.expert_gate_up.packed.data_ptr(), hsorted.data_ptr(), M, E, F, H, gs, 3,
-             2 * F, st)
         ysorted = torch.empty((R, H), dtype=torch.bfloat16, device=dev)
-        call("mtp_gather_qmv_affine4_packed", hsorted.data_ptr(), None, es.expert_off.data_ptr(),
-             es.active.data_ptr(), L.expert_down.packed.data_ptr(), ysorted.data_ptr(), M, E, H, F, gs, 0, H, st)
+
+        # Routed experts over their packed stacks: gate|up + SwiGLU on the
+        # token rows gathered by row_map, then down on the sorted rows; one
+        # launch per row class (experts with 1-4 rows, with more).
+        def experts(row_class, stream):
+            call("mtp_gather_qmv_affine4_packed_rows", xn.data_ptr(), es.row_map.data_ptr(), es.expert_off.data_ptr(),
+                 es.active.data_ptr(), L.expert_gate_up.packed.data_ptr(), hsorted.data_ptr(), M, E, F, H, gs, 3,
+                 2 * F, row_class, stream)
+            call("mtp_gather_qmv_affine4_packed_rows", hsorted.data_ptr(), None, es.expert_off.data_ptr(),
+                 es.active.data_ptr(), L.expert_down.packed.data_ptr(), ysorted.data_ptr(), M, E, H, F, gs, 0, H,
+                 row_class, stream)
+
         # Shared expert (SwiGLU MLP) on the normalised rows, then one combine:
         # h = h + bf16(routed + bf16(sigmoid(gate) * shared)).
         def W(q):
             return q.packed_mf16 if lay == 2 else q.packed
 
         sh_act = torch.empty((M, c.shared_ffn), dtype=torch.bfloat16, device=dev)
-        qmv(st, x=xn, w0=W(L.shared_gate), w1=W(L.shared_up), y0=sh_act, M=M, N=c.shared_ffn, K=H, group_size=gs,
-            xmode=0, emode=3, packed=lay)
         shared = torch.empty_like(h)
-        qmv(st, x=sh_act, w0=W(L.shared_down), y0=shared, M=M, N=H, K=c.shared_ffn, group_size=gs, xmode=0,
-            emode=0, packed=lay)
+
+        def shared_expert(stream, run):
+            run(stream, x=xn, w0=W(L.shared_gate), w1=W(L.shared_up), y0=sh_act, M=M, N=c.shared_ffn, K=H,
+                group_size=gs, xmode=0, emode=3, packed=lay)
+            run(stream, x=sh_act, w0=W(L.shared_down), y0=shared, M=M, N=H, K=c.shared_ffn, group_size=gs, xmode=0,
+                emode=0, packed=lay)
+
+        side = self._side_stream() if MOE_SIDE_STREAM else None
+        if side is None:
+            experts(0, st)
+            shared_expert(st, qmv)
+        else:
+            # The latency-bound work (the 5+-row experts, the shared expert)
+            # on a second stream beside the 1-4-row experts, which stream
+            # most of the bytes; the combine waits for both.
+            main = torch.cuda.current_stream(dev)
+            fork = torch.cuda.Event()
+            fork.record(main)
+            side.wait_event(fork)
+            with torch.cuda.stream(side):
+                sst = side.cuda_stream
+                sws = _lib.WORKSPACES.get(qmv_ws_bytes(M, c), "qmv_side", dev)
+
+                def side_qmv(stream, **kw):
+                    _lib.qmv_ex(stream, ws=sws, ws_bytes=sws.numel(), **kw)
+
+                experts(2, sst)
+                shared_expert(sst, side_qmv)
+                join = torch.cuda.Event()
+                join.record(side)
+            experts(1, st)
+            main.wait_event(join)
         moe_combine(ysorted, es, wts, shared, shared_gate=rl[:, E], resid=h, out=h)
 
     def verify_logits_ragged(self, tokens: torch.Tensor, row_off: torch.Tensor, q_start: torch.Tensor,
