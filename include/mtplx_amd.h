@@ -440,6 +440,13 @@ int mtp_moe_segments(const int32_t* sorted_ids, int R, int E, int32_t* expert_of
 int mtp_moe_combine(const void* y_sorted, const uint32_t* inv_order, const float* route_w, const void* shared,
                     const float* shared_gate, int gate_ld, const void* resid, void* out, int T, int top_k, int H,
                     void* stream);
+/* mtp_moe_combine that also writes the sums of squares of out's stored
+ * values, ss_out[j * 32 + t] over 32-column block j (H % 32 == 0, T <= 32):
+ * the statistics the next layer's fused input RMSNorm reads, as the dense
+ * residual epilogues write them. */
+int mtp_moe_combine_ss(const void* y_sorted, const uint32_t* inv_order, const float* route_w, const void* shared,
+                       const float* shared_gate, int gate_ld, const void* resid, void* out, float* ss_out, int T,
+                       int top_k, int H, void* stream);
 
 /* ---- Exact speculative accept / reject ------------------------------------
  * target_logits fp32 [B*(K+1), V] (row K of each request = bonus row),

@@ -64,6 +64,7 @@ SIGNATURES = {
     "mtp_moe_route": (_i, [_vp, _i, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "mtp_moe_segments": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "mtp_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp]),
+    "mtp_moe_combine_ss": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mtp_pack_affine4_bytes": (_sz, [_i, _i]),
     "mtp_pack_affine4": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mtp_pack_affine4_mf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),

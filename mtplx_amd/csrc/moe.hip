@@ -220,12 +220,19 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* logits, long
 // sh = bf16(sigmoid(gate[t]) * shared[t, :]) (no gate: shared itself);
 // out[t, :] = bf16(resid[t, :] + bf16(routed + sh)) (no resid: the block output).
 // Each stored tensor of the reference chain is rounded where it stores it.
-__global__ void moe_combine_kernel(const uint16_t* y_sorted, const uint32_t* inv_order, const float* w,
-                                   const uint16_t* shared, const float* gate, long long gate_ld,
-                                   const uint16_t* resid, uint16_t* out, int T, int k, int H) {
+// One column per thread (grid.x * 256 >= H). ss_out (H % 32 == 0, T <= 32):
+// per 32-column block j, ss_out[j * 32 + t] = the sum of the squared stored
+// values in column order (the residual epilogue's statistics, read by the
+// next fused RMSNorm).
+constexpr int kCombineThreads = 256;
+__global__ __launch_bounds__(kCombineThreads) void moe_combine_kernel(
+    const uint16_t* y_sorted, const uint32_t* inv_order, const float* w, const uint16_t* shared, const float* gate,
+    long long gate_ld, const uint16_t* resid, uint16_t* out, float* ss_out, int T, int k, int H) {
   const int t = blockIdx.y;
+  const int h = blockIdx.x * kCombineThreads + threadIdx.x;
   const float sg = gate ? 1.0f / (1.0f + __expf(-gate[(size_t)t * gate_ld])) : 1.0f;
-  for (int h = blockIdx.x * blockDim.x + threadIdx.x; h < H; h += gridDim.x * blockDim.x) {
+  float stored = 0.f;
+  if (h < H) {
     float acc = 0.f;
     for (int j = 0; j < k; ++j) {
       const uint32_t r = inv_order[(size_t)t * k + j];
@@ -238,6 +245,18 @@ __global__ void moe_combine_kernel(const uint16_t* y_sorted, const uint32_t* inv
     }
     if (resid) v = bf2f(resid[(size_t)t * H + h]) + v;
     out[(size_t)t * H + h] = f2bf(v);
+    stored = round_bf(v);
+  }
+  if (ss_out) {   // uniform over the grid
+    __shared__ float s_sq[kCombineThreads];
+    s_sq[threadIdx.x] = stored * stored;
+    __syncthreads();
+    const int j = blockIdx.x * (kCombineThreads / 32) + (int)threadIdx.x;
+    if (threadIdx.x < kCombineThreads / 32 && j * 32 < H) {
+      float a = 0.f;
+      for (int c = 0; c < 32; ++c) a += s_sq[threadIdx.x * 32 + c];
+      ss_out[(size_t)j * 32 + t] = a;
+    }
   }
 }
 
@@ -332,17 +351,35 @@ MTP_API int mtp_moe_segments(const int32_t* sorted_ids, int R, int E, int32_t* e
   return launch_check("mtp_moe_segments");
 }
 
+static int moe_combine_run(const void* y_sorted, const uint32_t* inv_order, const float* route_w, const void* shared,
+                           const float* shared_gate, int gate_ld, const void* resid, void* out, float* ss_out, int T,
+                           int top_k, int H, void* stream, const char* who) {
+  if (!y_sorted || !inv_order || !route_w || !out || T < 1 || top_k < 1 || H < 1 ||
+      (shared_gate && (!shared || gate_ld < 1))) {
+    set_error("%s: bad arguments", who);
+    return MTP_ERR_ARG;
+  }
+  if (ss_out && (H % 32 || T > 32)) {
+    set_error("%s: the sums of squares need H %% 32 == 0 and T <= 32 (got H=%d T=%d)", who, H, T);
+    return MTP_ERR_ARG;
+  }
+  dim3 grid(cdiv(H, kCombineThreads), T);
+  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(kCombineThreads), 0, (hipStream_t)stream,
+                     (const uint16_t*)y_sorted, inv_order, route_w, (const uint16_t*)shared, shared_gate,
+                     (long long)gate_ld, (const uint16_t*)resid, (uint16_t*)out, ss_out, T, top_k, H);
+  return launch_check(who);
+}
+
 MTP_API int mtp_moe_combine(const void* y_sorted, const uint32_t* inv_order, const float* route_w,
                             const void* shared, const float* shared_gate, int gate_ld, const void* resid, void* out,
                             int T, int top_k, int H, void* stream) {
-  if (!y_sorted || !inv_order || !route_w || !out || T < 1 || top_k < 1 || H < 1 ||
-      (shared_gate && (!shared || gate_ld < 1))) {
-    set_error("mtp_moe_combine: bad arguments");
-    return MTP_ERR_ARG;
-  }
-  dim3 grid(cdiv(H, 256), T);
-  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t*)y_sorted,
-                     inv_order, route_w, (const uint16_t*)shared, shared_gate, (long long)gate_ld,
-                     (const uint16_t*)resid, (uint16_t*)out, T, top_k, H);
-  return launch_check("mtp_moe_combine");
+  return moe_combine_run(y_sorted, inv_order, route_w, shared, shared_gate, gate_ld, resid, out, nullptr, T, top_k, H,
+                         stream, "mtp_moe_combine");
+}
+
+MTP_API int mtp_moe_combine_ss(const void* y_sorted, const uint32_t* inv_order, const float* route_w,
+                               const void* shared, const float* shared_gate, int gate_ld, const void* resid, void* out,
+                               float* ss_out, int T, int top_k, int H, void* stream) {
+  return moe_combine_run(y_sorted, inv_order, route_w, shared, shared_gate, gate_ld, resid, out, ss_out, T, top_k, H,
+                         stream, "mtp_moe_combine_ss");
 }

@@ -295,12 +295,13 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
 
 def moe_combine(y_sorted: torch.Tensor, inv_order, route_weights: torch.Tensor, shared: torch.Tensor | None = None,
                 *, shared_gate: torch.Tensor | None = None, resid: torch.Tensor | None = None,
-                out: torch.Tensor | None = None) -> torch.Tensor:
+                out: torch.Tensor | None = None, ss_out: torch.Tensor | None = None) -> torch.Tensor:
     """The sparse block's tail (``mtplx/models/qwen4_exp.py:1438-1445``, the
     unsort of ``:1544-1577``): ``bf16(sum_j w[t,j] * y_sorted[inv_order[t*k+j]])``
     plus ``sigmoid(shared_gate[t]) * shared[t]`` (``shared_gate``: fp32 ``[T]``
     or a strided column), plus ``resid`` when given. ``inv_order`` is the
-    tensor or an :class:`ExpertSort`."""
+    tensor or an :class:`ExpertSort`. ``ss_out`` (fp32, ``H`` entries, T <= 32):
+    each 32-column block's sums of squares of the output rows, ``[H/32][32]``."""
     if isinstance(inv_order, ExpertSort):
         inv, top_k = inv_order.inv_order, inv_order.top_k
     else:
@@ -319,8 +320,16 @@ def moe_combine(y_sorted: torch.Tensor, inv_order, route_weights: torch.Tensor, 
     # next temporary in the same argument list).
     ys = y_sorted.contiguous()
     inv32 = inv.to(torch.int32).contiguous()
-    _lib.call("mtp_moe_combine", ys.data_ptr(), inv32.data_ptr(), w.data_ptr(), _lib.ptr(shared), _lib.ptr(shared_gate), gate_ld, _lib.ptr(resid), out.data_ptr(), T,
-              top_k, H, _lib.stream_handle(y_sorted.device))
+    if ss_out is not None:
+        if ss_out.dtype != torch.float32 or ss_out.numel() < H or not ss_out.is_contiguous():
+            raise ValueError(f"ss_out must be a contiguous fp32 tensor of at least {H} entries")
+        _lib.call("mtp_moe_combine_ss", ys.data_ptr(), inv32.data_ptr(), w.data_ptr(), _lib.ptr(shared),
+                  _lib.ptr(shared_gate), gate_ld, _lib.ptr(resid), out.data_ptr(), ss_out.data_ptr(), T, top_k, H,
+                  _lib.stream_handle(y_sorted.device))
+        return out
+    _lib.call("mtp_moe_combine", ys.data_ptr(), inv32.data_ptr(), w.data_ptr(), _lib.ptr(shared),
+              _lib.ptr(shared_gate), gate_ld, _lib.ptr(resid), out.data_ptr(), T, top_k, H,
+              _lib.stream_handle(y_sorted.device))
     return out
 
 

@@ -272,3 +272,33 @@ def test_packed_expert_matmul_refuses_bad_shapes(gpu):
         with pytest.raises(_lib.MtpError):
             _lib.call("mtp_gather_qmv_affine4_packed", z.data_ptr(), None, z.data_ptr(), z.data_ptr(), z.data_ptr(),
                       z.data_ptr(), 4, 2, N, K, 64, em, rpe, st)
+
+
+def test_combine_sums_of_squares(gpu):
+    """mtp_moe_combine_ss: the same rows as mtp_moe_combine and, per 32-column
+    block, the fp32 sum of the squared stored values in column order (the
+    residual epilogue's statistics), bit for bit."""
+    from mtplx_amd.moe_sorted_gather import expert_sort, moe_combine
+    rng = np.random.default_rng(9)
+    T, k, E, H = 16, 8, 64, 4096
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    es = expert_sort(torch.from_numpy(idx).cuda(), E)
+    y = randn_bf16(rng, (T * k, H))
+    sc = torch.from_numpy(rng.random((T, k)).astype(np.float32)).cuda()
+    shared = randn_bf16(rng, (T, H))
+    resid = randn_bf16(rng, (T, H))
+    gate = torch.from_numpy(rng.normal(size=(T, 2)).astype(np.float32)).cuda()[:, 1]
+    ss = torch.full((H,), float("nan"), dtype=torch.float32, device="cuda")
+    out = moe_combine(y, es, sc, shared, shared_gate=gate, resid=resid, ss_out=ss)
+    out0 = moe_combine(y, es, sc, shared, shared_gate=gate, resid=resid)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out0.view(torch.int16))
+    v = bf16_values(out).astype(np.float32).reshape(T, H // 32, 32)
+    acc = np.zeros((T, H // 32), np.float32)
+    for c in range(32):   # sequential fp32 sums; bf16 squares are exact in fp32
+        acc = acc + v[:, :, c] * v[:, :, c]
+    got = ss.reshape(H // 32, 32).cpu().numpy()
+    assert np.array_equal(got[:, :T], acc.T)
+    from mtplx_amd import _lib
+    with pytest.raises(_lib.MtpError):   # H % 32 != 0: no whole 32-column blocks
+        moe_combine(y[:, :3984], es, sc, ss_out=torch.empty(3984, device="cuda"))
