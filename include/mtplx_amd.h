@@ -177,7 +177,6 @@ typedef struct mtp_rope_out {
   int L, Hq, Hkv, D, cap, blocked;
   float rope_base;
 } mtp_rope_out;
-struct mtp_logits_topk;   /* emode 5's outputs, below */
 typedef struct mtp_qmv_args {
   const void* x;
   const void* x2;
@@ -205,35 +204,9 @@ typedef struct mtp_qmv_args {
    * the x_sums of a following xmode 3 call on y0. */
   const float* x_sums;
   float* y_sums;
-  const struct mtp_logits_topk* topk; /* emode 5 only */
 } mtp_qmv_args;
 int mtp_qmv_affine4_ex(const mtp_qmv_args* args, void* stream);
 
-/* emode 5 = the verify lm_head with the sampler's vocabulary reduction fused
- * into its epilogue (mtplx/kernels/lm_head_topk.py:12-30 tile-local top-k,
- * mtplx/kernels/logits_topk.py:1-12 logsumexp partials, fed to the accept
- * step as mtplx/fast_sampling.py:407-451 feeds its candidates). yf receives
- * the fp32 logits as emode 0 does; parts receives, for every row, n_parts
- * (<= 64, written back into the struct) partial records of the sampler's
- * reduction over disjoint id sets covering the vocabulary: each the fp64
- * max and sum exp(l/T - max), the non-finite flag and the top-k keys
- * (value desc, id asc). The law built from them equals the one
- * mtp_spec_accept builds from the logits (the same candidates and maximum;
- * the sums in another fp64 order), so mtp_spec_accept_parts skips the
- * target rows' pass over the logits. Each workgroup streams its tiles as
- * emode 0 does and records its ids; sets of up to 16 workgroups are merged
- * by the last to arrive. Packed weights, 1 <= M <= 8, yf set; narrow laws
- * only (temperature <= 0, or 1 <= top_k <= 64). */
-typedef struct mtp_logits_topk {
-  void* parts;        /* [M][64] records: mtp_logits_topk_parts_bytes(M) */
-  void* ws;           /* scratch of mtp_logits_topk_workspace_bytes(M, N), 256-byte aligned, zeroed once */
-  size_t ws_bytes;
-  double temperature; /* the sampler's (<= 0: greedy) */
-  int top_k;          /* the sampler's, 1..64 (ignored when greedy) */
-  int n_parts;        /* out: records per row, for mtp_spec_accept_parts */
-} mtp_logits_topk;
-size_t mtp_logits_topk_workspace_bytes(int M, int N);
-size_t mtp_logits_topk_parts_bytes(int M);
 
 /* ---- 4-bit quantized matmul for 9..64 verify rows (MFMA) --------------------
  * The continuous-batched ragged verify (M = sum_b (K_b + 1) rows, up to 64):
@@ -469,17 +442,6 @@ int mtp_spec_accept(const float* target_logits, const float* draft_logits, const
                     int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
                     size_t ws_bytes, void* stream);
 
-/* mtp_spec_accept with the target rows' reduction already done: target_parts
- * holds n_parts records per target row (row b*(K+1)+d), as an emode-5 lm_head
- * writes them with the same temperature and top_k; only the draft rows are
- * reduced here (ws as for mtp_spec_accept). Narrow laws only
- * (MTP_ERR_UNSUPPORTED otherwise). No counterpart of its own in the
- * reference: the consumer of lm_head candidates in the fused path of
- * mtplx/fast_sampling.py:407-451. */
-int mtp_spec_accept_parts(const void* target_parts, int n_parts, const float* draft_logits,
-                          const int32_t* draft_ids, const double* uniforms, int B, int K, int V, double temperature,
-                          int top_k, double top_p, int32_t* out_tokens, int32_t* n_accepted, double* accept_probs,
-                          int32_t* status, void* ws, size_t ws_bytes, void* stream);
 
 /* The same step for a ragged batch (the continuous-batched verify lane,
  * mtplx/batched_decode.py:338-395): request b has depth K_b = k_lens[b]

@@ -48,7 +48,6 @@ SIGNATURES = {
     "mtp_embed_affine4": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp]),
     "mtp_sampler_workspace_bytes": (_sz, [_i, _i, _i]),
     "mtp_spec_accept": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
-    "mtp_spec_accept_parts": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "mtp_spec_accept_ragged": (_i, [_vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp,
                                     _vp, _vp, _sz, _vp]),
     "mtp_spec_accept_noalloc": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _d, _i, _d, _vp, _vp, _vp, _vp, _vp]),
@@ -69,8 +68,6 @@ SIGNATURES = {
     "mtp_pack_affine4": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mtp_pack_affine4_mf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mtp_qmv_affine4_ex": (_i, [_vp, _vp]),
-    "mtp_logits_topk_workspace_bytes": (_sz, [_i, _i]),
-    "mtp_logits_topk_parts_bytes": (_sz, [_i]),
     "mtp_qmm_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "mtp_qmm_affine4_mfma": (_i, [_vp, _vp]),
     "mtp_attn_blocks_workspace_bytes": (_sz, [_i, _i, _i, C.c_longlong, _i]),
@@ -89,13 +86,6 @@ class RopeOut(C.Structure):
                [(n, _i) for n in ("L", "Hq", "Hkv", "D", "cap", "blocked")] + [("rope_base", _f)]
 
 
-class LogitsTopk(C.Structure):
-    """``mtp_logits_topk`` of include/mtplx_amd.h (same field order)."""
-
-    _fields_ = [("parts", _vp), ("ws", _vp), ("ws_bytes", C.c_size_t), ("temperature", C.c_double),
-                ("top_k", _i), ("n_parts", _i)]
-
-
 class QmvArgs(C.Structure):
     """``mtp_qmv_args`` of include/mtplx_amd.h (same field order)."""
 
@@ -103,7 +93,7 @@ class QmvArgs(C.Structure):
                                    "resid", "ss_out")] + [("eps", _f)] + \
                [(n, _i) for n in ("M", "N", "K", "group_size", "ldx", "ldy", "xmode", "emode", "packed")] + \
                [("ws", _vp), ("ws_bytes", C.c_size_t), ("rope", C.POINTER(RopeOut)), ("schedule", _i)] + \
-               [(n, _vp) for n in ("x_sums", "y_sums")] + [("topk", C.POINTER(LogitsTopk))]
+               [(n, _vp) for n in ("x_sums", "y_sums")]
 
 
 def _fill(struct, fields: dict):
@@ -114,21 +104,15 @@ def _fill(struct, fields: dict):
     return struct
 
 
-def qmv_ex(stream, rope: dict | None = None, topk: dict | None = None, **fields) -> None:
+def qmv_ex(stream, rope: dict | None = None, **fields) -> None:
     """Call ``mtp_qmv_affine4_ex``; tensor fields may be torch tensors or None.
-    ``rope``: fields of ``mtp_rope_out`` (emode 4); ``topk``: fields of
-    ``mtp_logits_topk`` (emode 5)."""
+    ``rope``: fields of ``mtp_rope_out`` (emode 4)."""
     a = _fill(QmvArgs(), fields)
-    r = t = None
+    r = None
     if rope is not None:
         r = _fill(RopeOut(), rope)
         a.rope = C.pointer(r)
-    if topk is not None:
-        t = _fill(LogitsTopk(), topk)
-        a.topk = C.pointer(t)
     call("mtp_qmv_affine4_ex", C.byref(a), stream)
-    if t is not None:
-        topk["n_parts"] = int(t.n_parts)   # the records per row the call wrote
 
 
 class QmmArgs(C.Structure):

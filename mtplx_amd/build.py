@@ -18,7 +18,7 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmtplx_amd.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["qmv.hip", "qmv_xplain.hip", "qmv_xswiglu.hip", "qmv_xpre.hip", "qmv_xrmsnorm.hip", "qmv_rope.hip", "qmv_topk.hip",
+SOURCES = ["qmv.hip", "qmv_xplain.hip", "qmv_xswiglu.hip", "qmv_xpre.hip", "qmv_xrmsnorm.hip", "qmv_rope.hip",
            "qmv_moe.hip", "qmv_generic.hip", "qmm_mfma.hip", "sampler.hip", "attention.hip", "model_ops.hip", "moe.hip"]
 
 # Packed fp32 VALU instructions are disabled for every device pass: some

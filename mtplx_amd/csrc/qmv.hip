@@ -167,24 +167,6 @@ static int qmm_dispatch(int xm, int em, QmmParams p, void* ws, size_t ws_bytes, 
                         const char* who, int schedule = 0) {
   const int rc = qmm_check(xm, em, p, who);
   if (rc != MTP_OK) return rc;
-  if (em == E_STORE_TOPK) {
-    Plan pl = make_plan(p.M, p.N, p.K);
-    if (!p.packed || p.M > 8 || !p.yf || !pl.resident || (xm != X_PLAIN && xm != X_RMSNORM) ||
-        (!p.topk_greedy && (p.topk_ksel < 1 || p.topk_ksel > kMaxTopK))) {
-      set_error("%s: emode 5 needs packed weights, M <= 8 with x in LDS, plain or RMSNorm x, fp32 logits (yf) and "
-                "a narrow law (temperature <= 0 or 1 <= top_k <= %d)", who, kMaxTopK);
-      return MTP_ERR_UNSUPPORTED;
-    }
-    p.chunk = pl.chunk;
-    p.n_blocks = pl.n_blocks;
-    const int parts = qmv_launch_topk(xm, p, pl, st);
-    if (parts < 0) {
-      set_error("%s: emode 5 needs at most 32 tiles per resident workgroup (N=%d)", who, p.N);
-      return MTP_ERR_UNSUPPORTED;
-    }
-    if (p.topk_nparts) *p.topk_nparts = parts;
-    return launch_check(who);
-  }
   if (em == E_ROPE_QKV) {
     Plan pl = make_plan(p.M, p.N, p.K);
     if (!pl.resident) {
@@ -262,16 +244,6 @@ static QmmParams base_params(const void* x, const void* w, const void* s, const 
 using namespace mtp;
 
 MTP_API const char* mtp_last_error(void) { return g_err; }
-
-MTP_API size_t mtp_logits_topk_workspace_bytes(int M, int N) {
-  if (M < 1 || M > 8 || N < 1) return 0;
-  return kTopkCounterBytes + topk_sub_bytes(M);
-}
-
-MTP_API size_t mtp_logits_topk_parts_bytes(int M) {
-  if (M < 1 || M > 8) return 0;
-  return (size_t)M * kTopkParts * sizeof(ChunkPart);
-}
 
 MTP_API int mtp_qmv_rope_fusable(int M, int N, int K) {
   // The RoPE epilogue (emode 4) takes up to 16 rows with all of x in LDS.
@@ -601,8 +573,7 @@ int qmv_args_params(const mtp_qmv_args* a, QmmParams* out, const char* who) {
     set_error("%s: null argument block", who);
     return MTP_ERR_ARG;
   }
-  if (a->xmode < 0 || a->xmode > 3 || a->emode < 0 || a->emode > 5 || (a->emode == E_ROPE_QKV && !a->rope) ||
-      (a->emode == E_STORE_TOPK && !a->topk)) {
+  if (a->xmode < 0 || a->xmode > 3 || a->emode < 0 || a->emode > 4 || (a->emode == E_ROPE_QKV && !a->rope)) {
     set_error("%s: xmode %d / emode %d out of range", who, a->xmode, a->emode);
     return MTP_ERR_ARG;
   }
@@ -638,21 +609,6 @@ int qmv_args_params(const mtp_qmv_args* a, QmmParams* out, const char* who) {
     p.rope_cap = r->cap;
     p.rope_blocked = r->blocked;
     p.rope_log2_base = r->rope_base > 1.f ? log2f(r->rope_base) : 0.f;
-  }
-  if (a->emode == E_STORE_TOPK) {
-    mtp_logits_topk* t = a->topk;
-    p.topk_parts = t->parts;
-    p.topk_greedy = !(t->temperature > 0.0);
-    p.topk_temp = p.topk_greedy ? 1.0 : t->temperature;
-    p.topk_ksel = p.topk_greedy ? 1 : t->top_k;
-    p.topk_nparts = &a->topk->n_parts;
-    const size_t need = mtp_logits_topk_workspace_bytes(a->M, a->N);
-    if (!t->parts || !t->ws || t->ws_bytes < need || ((uintptr_t)t->ws & 255) || need == 0) {
-      set_error("%s: emode 5 needs chunk-partial output and a 256-B aligned scratch of %zu B", who, need);
-      return MTP_ERR_WORKSPACE;
-    }
-    p.topk_counters = reinterpret_cast<uint32_t*>(t->ws);   // fixed area first: shared by every shape
-    p.topk_sub = reinterpret_cast<unsigned char*>(t->ws) + kTopkCounterBytes;
   }
   *out = p;
   return MTP_OK;

@@ -15,15 +15,6 @@ struct mtp_rope_out {
   float rope_base;
 };
 
-struct mtp_logits_topk {
-  void* parts;
-  void* ws;
-  size_t ws_bytes;
-  double temperature;
-  int top_k;
-  int n_parts;
-};
-
 struct mtp_qmv_args {
   const void* x;
   const void* x2;
@@ -48,7 +39,6 @@ struct mtp_qmv_args {
   int schedule;
   const float* x_sums;
   float* y_sums;
-  mtp_logits_topk* topk;
 };
 
 namespace mtp {

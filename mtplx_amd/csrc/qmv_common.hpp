@@ -10,7 +10,7 @@ namespace mtp {
 // X_PRE: x comes with its per-32-column row sums (written by the producing
 // epilogue), so staging is the copy alone.
 enum XMode { X_PLAIN = 0, X_SWIGLU = 1, X_RMSNORM = 2, X_PRE = 3 };
-enum EMode { E_STORE = 0, E_RESID = 1, E_DUAL = 2, E_DUAL_SWIGLU = 3, E_ROPE_QKV = 4, E_STORE_TOPK = 5 };
+enum EMode { E_STORE = 0, E_RESID = 1, E_DUAL = 2, E_DUAL_SWIGLU = 3, E_ROPE_QKV = 4 };
 
 struct QmmParams {
   const uint16_t* x;       // activations [rows, ldx] (X_SWIGLU: gate)
@@ -63,19 +63,6 @@ struct QmmParams {
   int32_t* status;
   int rope_L, rope_Hq, rope_Hkv, rope_D, rope_cap, rope_blocked;
   float rope_log2_base;
-  // E_STORE_TOPK: fp32 logits (as E_STORE with yf) plus the sampler's
-  // partial records of every row. The workgroups stream tiles as for
-  // E_STORE (vb, vb + grid, ...; at most topk_tpw each); each writes the
-  // record of its ids (topk_sub [M][grid]); consecutive sets of topk_wpg
-  // workgroups are merged by the last of each set to arrive (topk_counters,
-  // one per set, left at zero) into topk_parts [M][kTopkParts], one record
-  // per set.
-  void* topk_sub;
-  void* topk_parts;
-  uint32_t* topk_counters;
-  double topk_temp;
-  int topk_ksel, topk_greedy, topk_tpw, topk_wpg;
-  int* topk_nparts;   // host: receives the records per row
 };
 
 constexpr int kThreads = 256;
@@ -616,7 +603,7 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, float* fin, int
         fin[m * 64 + c] = in ? round_bf(v) : 0.f;
       }
       if (in) {
-        if ((EM == E_STORE || EM == E_STORE_TOPK) && p.yf)
+        if (EM == E_STORE && p.yf)
           st_f32<WT>(p.yf + o, round_bf(v));
         else
           st_u16<WT>(p.y0 + o, f2bf(v));

@@ -722,13 +722,5 @@ void qmv_launch_pre(int em, int gsh, const QmmParams& p, const Plan& pl, hipStre
 void qmv_launch_rmsnorm(int em, int gsh, const QmmParams& p, const Plan& pl, hipStream_t st);
 // q|k|v with the RoPE epilogue (x plain or RMSNorm).
 void qmv_launch_rope_qkv(int xm, const QmmParams& p, const Plan& pl, hipStream_t st);
-// Logits with the sampler's partial records (E_STORE_TOPK; x plain or
-// RMSNorm); returns the records per row, or -1.
-int qmv_launch_topk(int xm, const QmmParams& p, const Plan& pl, hipStream_t st);
-
-// E_STORE_TOPK scratch: one counter per set first (a fixed area), then the
-// workgroups' records [M][grid <= 1024].
-constexpr size_t kTopkCounterBytes = 256;
-inline size_t topk_sub_bytes(int M) { return (size_t)M * 1024 * sizeof(ChunkPart); }
 
 }  // namespace mtp

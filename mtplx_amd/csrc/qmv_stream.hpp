@@ -4,7 +4,6 @@
 #pragma once
 
 #include "qmv_common.hpp"
-#include "sampler_common.hpp"
 
 #include <type_traits>
 
@@ -95,8 +94,7 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   // Tail split (packed weights only): workgroups from p.tail_first on each
   // take quads [q_lo, q_lo + q_n) of a leftover tile, one of tail_split
   // parts; the part that arrives last sums the parts in order and finishes.
-  constexpr bool kTopk = EM == E_STORE_TOPK;
-  const bool tail = !kTopk && PK && p.tail_split > 1 && vb >= p.tail_first;
+  const bool tail = PK && p.tail_split > 1 && vb >= p.tail_first;
   const bool full = tail && p.full_split;
   // Tile stride between a workgroup's tiles: the grid, or the number of tile
   // groups in the full split.
@@ -123,14 +121,6 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   float* xs = reinterpret_cast<float*>(smem + xa_bytes(4 * QX, M));            // [QX*4][XSW]
   float* red = xs + QX * 4 * XSW;                                              // [NW][M][32]
   float* fin = red + NW * M * 32;                                              // [M][64]
-  float* topv = fin + M * 64;          // E_STORE_TOPK: [M][topk_tpw * 32] stored logits of this workgroup's tiles
-  // E_STORE_TOPK: per wave, the key lists of a chunk's groups while merging:
-  // in the staged-x area (free once the tiles are done) when it is large
-  // enough, else past topv (the host sizes LDS the same way).
-  const bool stage_in_xa = xa_bytes(4 * QX, M) >= (size_t)NW * kTopkStageKeys * sizeof(uint64_t);
-  uint64_t* topk_stage = (stage_in_xa ? reinterpret_cast<uint64_t*>(smem)
-                                      : reinterpret_cast<uint64_t*>(topv + M * p.topk_tpw * 32)) +
-                         (size_t)wave * kTopkStageKeys;
   __shared__ float s_inv_rms[32];
   __shared__ int s_last;
 
@@ -326,10 +316,6 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
     }
     qmm_epilogue<NW, EM, kPhase>(p, fin, nb, M, 0, (use_pre && j == 0) ? &pre_resid : nullptr,
                          (use_rpre && j == 0) ? &rope_pre : nullptr);
-    if constexpr (kTopk) {   // the stored values (bf16-rounded), for the group's partial
-      for (int idx = tid; idx < M * 32; idx += NT)
-        topv[(idx >> 5) * (p.topk_tpw * 32) + j * 32 + (idx & 31)] = fin[(idx >> 5) * 64 + (idx & 31)];
-    }
   };
 
   // Full split: after the last tile, wait once for all the part stores, then
@@ -360,36 +346,6 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
       }
       lds_barrier();   // s_lastv is rewritten by the next round
     }
-  };
-
-  // E_STORE_TOPK, after the workgroup's tiles (vb, vb + grid, ...): one wave
-  // per row writes the partial record of their ids; the workgroups form
-  // kTopkParts consecutive sets of topk_wpg, and the last of a set to arrive
-  // merges the set's records into the row's partial record of that set.
-  auto topk_finish = [&](int nt, int Mr, int t) {
-    lds_barrier();
-    const int span = p.topk_tpw * 32;
-    const int set = vb / p.topk_wpg;
-    ChunkPart* recs = reinterpret_cast<ChunkPart*>(p.topk_sub);
-    for (int m = wave; m < Mr; m += NW)
-      wave_sub_partial(topv + m * span, nt * 32, vb * 32, vg * 32, p.N, p.topk_temp, p.topk_ksel, p.topk_greedy,
-                       recs + (size_t)m * vg + vb);
-    __builtin_amdgcn_s_waitcnt(0);
-    lds_barrier();
-    const int first = set * p.topk_wpg;
-    const int nsc = (vg - first) < p.topk_wpg ? (vg - first) : p.topk_wpg;
-    if (t == 0) {
-      const unsigned old = __hip_atomic_fetch_add(p.topk_counters + set, 1u, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-      s_last = (old == (unsigned)(nsc - 1)) ? 1 : 0;
-    }
-    lds_barrier();
-    if (!s_last) return;
-    ChunkPart* parts = reinterpret_cast<ChunkPart*>(p.topk_parts);
-    for (int m = wave; m < Mr; m += NW)
-      wave_merge_subs(recs + (size_t)m * vg + first, nsc, p.topk_ksel, p.topk_greedy,
-                      parts + (size_t)m * kTopkParts + set, topk_stage);
-    if (t == 0) __hip_atomic_store(p.topk_counters + set, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
 
   // Prologue: the norm statistics, x straight into LDS, the norm weights
@@ -444,7 +400,6 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   if (qw == 0) {
     for (int j = 0; j < ntiles; ++j) finish(j);
     arrive_all();
-    if constexpr (kTopk) topk_finish(ntiles, M, tid);
     return;
   }
   // One exit, at the bottom: a break after each step would be merged by the
@@ -472,7 +427,6 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
     }
   } while (i < nitems);
   arrive_all();
-  if constexpr (kTopk) topk_finish(ntiles, M, tid);
 }
 
 }  // namespace mtp

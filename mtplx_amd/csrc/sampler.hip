@@ -1366,17 +1366,10 @@ MTP_API size_t mtp_sampler_workspace_bytes(int rows, int V, int top_k) {
 static int spec_accept_run(const float* target_logits, const float* draft_logits, const int32_t* draft_ids,
                            const double* uniforms, int B, int K, int V, double temperature, int top_k, double top_p,
                            int32_t* out_tokens, int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
-                           size_t ws_bytes, void* stream, AcceptRows rr, int nt, int nd, const char* who,
-                           const void* target_parts = nullptr, int t_parts = 0) {
-  const bool target_ready = target_parts != nullptr;
+                           size_t ws_bytes, void* stream, AcceptRows rr, int nt, int nd, const char* who) {
   SamplerPlan pl;
   int rc = sampler_plan(V, top_k, temperature, &pl, who);
   if (rc) return rc;
-  if (target_ready && (pl.wide || t_parts < 1 || t_parts > 64 || pl.n_chunks > 64)) {
-    set_error("%s: precomputed target records serve narrow laws (temperature <= 0 or 1 <= top_k <= %d) with 1..64 "
-              "records per row and V <= 64 * 4096", who, kMaxTopK);
-    return MTP_ERR_UNSUPPORTED;
-  }
   if (B < 1 || K < 1 || nt < B || nd < 0 || !target_logits || (nd > 0 && !draft_logits) || !draft_ids || !uniforms ||
       !out_tokens || !n_accepted || !accept_probs || !status) {
     set_error("%s: need B>=1, K>=1 and non-null buffers", who);
@@ -1392,24 +1385,14 @@ static int spec_accept_run(const float* target_logits, const float* draft_logits
   const int n_chunks = pl.n_chunks;
   ChunkPart* tparts = reinterpret_cast<ChunkPart*>(ws);
   ChunkPart* dparts = tparts + (size_t)nt * n_chunks;
-  const int t_chunks = target_ready ? t_parts : n_chunks;
-  const ChunkPart* tread = target_ready ? reinterpret_cast<const ChunkPart*>(target_parts) : tparts;
   const double temp = pl.greedy ? 1.0 : temperature;
   rr.nt = nt;
   rr.nd = nd;
-  if (target_ready) {   // the target rows' partials are in ws already: the draft rows only
-    if (nd > 0) {
-      hipLaunchKernelGGL(vocab_partials, dim3(n_chunks, nd), dim3(kSampThreads), 0, st, draft_logits, draft_logits,
-                         nd, (long long)V, V, n_chunks, temp, pl.ksel, pl.greedy, dparts);
-      if ((rc = launch_check(who))) return rc;
-    }
-  } else {
-    // target rows then draft rows, one launch (dparts follows tparts)
-    hipLaunchKernelGGL(vocab_partials, dim3(n_chunks, rows), dim3(kSampThreads), 0, st, target_logits,
-                       draft_logits ? draft_logits : target_logits, nt, (long long)V, V, n_chunks, temp, pl.ksel,
-                       pl.greedy, tparts);
-    if ((rc = launch_check(who))) return rc;
-  }
+  // target rows then draft rows, one launch (dparts follows tparts)
+  hipLaunchKernelGGL(vocab_partials, dim3(n_chunks, rows), dim3(kSampThreads), 0, st, target_logits,
+                     draft_logits ? draft_logits : target_logits, nt, (long long)V, V, n_chunks, temp, pl.ksel,
+                     pl.greedy, tparts);
+  if ((rc = launch_check(who))) return rc;
   if (pl.wide) {
     unsigned char* lawbuf = reinterpret_cast<unsigned char*>(ws) + parts_bytes(rows, V);
     const size_t rb = wide_row_bytes(V);
@@ -1429,7 +1412,7 @@ static int spec_accept_run(const float* target_logits, const float* draft_logits
     // A failure here surfaces as a launch error, checked below.
     if (lds > 65536) (void)hipFuncSetAttribute((const void*)accept_laws, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)lds);
-    hipLaunchKernelGGL(accept_laws, dim3(B), dim3(nwv * 64), lds, st, tread, t_chunks, dparts, n_chunks, draft_ids,
+    hipLaunchKernelGGL(accept_laws, dim3(B), dim3(nwv * 64), lds, st, tparts, n_chunks, dparts, n_chunks, draft_ids,
                        uniforms,
                        K, pl.ksel, pl.greedy, temp, top_p, out_tokens, n_accepted, accept_probs, status, rr);
   } else {
@@ -1450,21 +1433,6 @@ MTP_API int mtp_spec_accept(const float* target_logits, const float* draft_logit
   return spec_accept_run(target_logits, draft_logits, draft_ids, uniforms, B, K, V, temperature, top_k, top_p,
                          out_tokens, n_accepted, accept_probs, status, ws, ws_bytes, stream, AcceptRows{}, B * (K + 1),
                          B * K, "mtp_spec_accept");
-}
-
-MTP_API int mtp_spec_accept_parts(const void* target_parts, int n_parts, const float* draft_logits,
-                                  const int32_t* draft_ids, const double* uniforms, int B, int K, int V,
-                                  double temperature, int top_k, double top_p, int32_t* out_tokens,
-                                  int32_t* n_accepted, double* accept_probs, int32_t* status, void* ws,
-                                  size_t ws_bytes, void* stream) {
-  if (B < 1 || K < 1 || !target_parts) {
-    set_error("mtp_spec_accept_parts: need B>=1, K>=1 and the target records");
-    return MTP_ERR_ARG;
-  }
-  // target_logits is not read on this path: the draft logits stand in as a valid pointer
-  return spec_accept_run(draft_logits, draft_logits, draft_ids, uniforms, B, K, V, temperature, top_k, top_p,
-                         out_tokens, n_accepted, accept_probs, status, ws, ws_bytes, stream, AcceptRows{}, B * (K + 1),
-                         B * K, "mtp_spec_accept_parts", target_parts, n_parts);
 }
 
 MTP_API int mtp_spec_accept_ragged(const float* target_logits, int n_target, const float* draft_logits, int n_draft,

@@ -233,24 +233,15 @@ def _position_counts(base, drafts_b, K):
     return out
 
 
-def narrow_law(config: SamplerConfig, vocab: int) -> bool:
-    """Whether the law's support is bounded by 64 ids (greedy, or
-    1 <= top_k <= 64): the laws whose target reduction an lm_head can fuse."""
-    greedy = not (float(config.temperature) > 0.0)
-    k = int(config.top_k)
-    return greedy or (k > 0 and min(k, int(vocab)) <= 64)
-
-
 def sampler_workspace(B: int, K: int, V: int, config: SamplerConfig, device) -> torch.Tensor:
-    """The accept step's workspace (its first bytes: the target rows' chunk
-    partials, which an emode-5 lm_head may fill ahead of the step)."""
+    """The accept step's workspace (the rows' chunk partials, then the laws)."""
     nb = _lib.query("mtp_sampler_workspace_bytes", B * (2 * K + 1), V, int(config.top_k))
     return _lib.WORKSPACES.get(nb, "sampler", device)
 
 
 def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_ids: torch.Tensor,
                 uniforms: torch.Tensor, config: SamplerConfig, *, token_counts=None,
-                penalty_overlay=None, target_parts: tuple | None = None) -> AcceptResult:
+                penalty_overlay=None) -> AcceptResult:
     """Depth-K accept/reject with residual correction for ``B`` requests.
 
     ``target_logits`` ``[B, K+1, V]`` (verify rows), ``draft_logits`` ``[B, K, V]``,
@@ -263,11 +254,6 @@ def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_i
     request b are penalised with those counts plus ``draft_ids[b, :d]``
     (per-position prefix counts). ``penalty_overlay[b]``: one mapping for all
     of request b's rows, or a list of K+1 (one per depth).
-
-    ``target_parts``: ``(records, n_parts)`` of the target rows from an
-    emode-5 lm_head with this config (``target_logits`` is then only used
-    for its shape); only the draft rows are reduced. Narrow laws, no
-    penalties.
     """
     B, K1, V = (int(s) for s in target_logits.shape)
     K = K1 - 1
@@ -277,8 +263,6 @@ def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_i
     di = draft_ids.to(device=dev, dtype=torch.int32).contiguous()
     pen = penalties_active(config, token_counts if not isinstance(token_counts, (list, tuple)) else any(token_counts),
                            penalty_overlay if not isinstance(penalty_overlay, (list, tuple)) else any(penalty_overlay))
-    if target_parts is not None and (pen or not narrow_law(config, V)):
-        raise ValueError("precomputed target partials need a narrow law (greedy or 1 <= top_k <= 64) and no penalties")
     if pen:
         base = token_counts if isinstance(token_counts, (list, tuple)) else [token_counts] * B
         ovl = penalty_overlay if isinstance(penalty_overlay, (list, tuple)) else [penalty_overlay] * B
@@ -299,9 +283,7 @@ def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_i
     ap = torch.empty((B, K), dtype=torch.float64, device=dev)
     st = torch.empty(B, dtype=torch.int32, device=dev)
     ws = sampler_workspace(B, K, V, config, dev)
-    head = (target_parts[0].data_ptr(), int(target_parts[1])) if target_parts is not None else (t.data_ptr(),)
-    _lib.call("mtp_spec_accept_parts" if target_parts is not None else "mtp_spec_accept", *head, d.data_ptr(),
-              di.data_ptr(), u.data_ptr(), B, K, V,
+    _lib.call("mtp_spec_accept", t.data_ptr(), d.data_ptr(), di.data_ptr(), u.data_ptr(), B, K, V,
               float(config.temperature), int(config.top_k), float(config.top_p), out.data_ptr(), nacc.data_ptr(),
               ap.data_ptr(), st.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_handle(dev))
     return AcceptResult(out, nacc, ap, st)

@@ -39,7 +39,7 @@ from . import _lib
 from .moe_sorted_gather import expert_sort, moe_combine
 from .quant import QuantizedLinear, rope_row_order
 from .attention_context import exact_lane_counts, exact_t0_guard_armed, exact_verify_required
-from .sampling import SamplerConfig, narrow_law, spec_accept
+from .sampling import SamplerConfig, spec_accept
 
 # Keys per attention work unit on the exact lane: a fixed split length (a
 # multiple of 128) makes each request's partials and merge independent of the
@@ -351,13 +351,11 @@ class VerifyModel:
     # -- forward --------------------------------------------------------------
     def verify_logits(self, tokens: torch.Tensor, q_start: torch.Tensor, q_lens: torch.Tensor | None = None,
                       *, logits_out: torch.Tensor | None = None, check: bool = False,
-                      topk: dict | None = None, exact: bool = False, layer_log: list | None = None) -> torch.Tensor:
+                      exact: bool = False, layer_log: list | None = None) -> torch.Tensor:
         """``tokens`` int32 ``[B, L]`` (GPU), ``q_start`` int32 ``[B]`` (GPU):
         writes K/V of the L rows at ``q_start[b] + i`` and returns fp32 logits ``[B*L, V]``.
         The device status word (:meth:`status`) flags invalid tokens or
-        positions; ``check=True`` synchronises and raises on it. ``topk``
-        (fields of ``mtp_logits_topk``, B*L <= 8): the lm_head also writes
-        the sampler's chunk partials of every row. ``exact``: the exact lane
+        positions; ``check=True`` synchronises and raises on it. ``exact``: the exact lane
         (:meth:`verify_logits_ragged` with ``exact=True`` over this uniform
         cache), whose rows do not depend on B or L. ``layer_log``: a list
         that receives a copy of the hidden rows (bf16 ``[B*L, H]``) entering
@@ -366,8 +364,8 @@ class VerifyModel:
         B, Lq = (int(s) for s in tokens.shape)
         M = B * Lq
         if exact:
-            if topk is not None or c.n_experts:
-                raise ValueError("the exact lane serves the dense model without the fused lm_head records")
+            if c.n_experts:
+                raise ValueError("the exact lane serves the dense model")
             dev = self.device
             nblk = self.cap // 32
             kv_off = torch.arange(B + 1, dtype=torch.int32, device=dev) * (c.n_kv_heads * nblk)
@@ -468,7 +466,7 @@ class VerifyModel:
             layer_log.append(h.clone())
         logits = logits_out if logits_out is not None else torch.empty((M, c.vocab), dtype=torch.float32, device=dev)
         qmv(st, x=h, x2=self.final_norm, ss_in=ss_h, eps=c.rms_eps, w0=W(self.lm_head), yf=logits, M=M,
-            N=c.vocab, K=H, group_size=gs, xmode=2, emode=0 if topk is None else 5, packed=lay, topk=topk)
+            N=c.vocab, K=H, group_size=gs, xmode=2, emode=0, packed=lay)
         self._status = status
         if check:
             self.check_status()
@@ -671,20 +669,12 @@ class VerifyModel:
         return spec_accept_ragged(logits, row_off[:-1], draft_logits, d_off, q_lens - 1, drafts, uniforms, sampler)
 
     def verify_step(self, tokens: torch.Tensor, q_start: torch.Tensor, draft_logits: torch.Tensor,
-                    uniforms: torch.Tensor, sampler: SamplerConfig = SamplerConfig(), *, fuse_topk: bool = False):
+                    uniforms: torch.Tensor, sampler: SamplerConfig = SamplerConfig()):
         """Forward the ``B x (K+1)`` verify rows, then accept/reject against the drafts
-        (``tokens[:, 1:]`` are the draft ids). Returns the device-side accept result.
-
-        With ``fuse_topk`` (and a narrow law, at most 8 rows) the lm_head
-        writes the target rows' partial records itself, so the accept step
-        reduces only the draft rows. Same tokens and probabilities either
-        way; off by default because it is slower on MI355X for the 27B shape
-        (lm_head + reductions 150 us fused against 130 us unfused: the fused
-        kernel holds more registers, 3 waves per SIMD instead of 4)."""
+        (``tokens[:, 1:]`` are the draft ids). Returns the device-side accept result."""
         B, L = (int(s) for s in tokens.shape)
         K = L - 1
         c = self.cfg
-        topk = None
         if _exact_lane(sampler) and not c.n_experts:
             # Greedy verify: the exact lane, whose rows do not depend on the
             # batch (the argmax the autoregressive decode of the same rows picks).
@@ -693,17 +683,9 @@ class VerifyModel:
             self.last_logits = logits
             return spec_accept(logits.reshape(B, L, -1), draft_logits, tokens[:, 1:].contiguous(), uniforms,
                                sampler)
-        if fuse_topk and B * L <= 8 and narrow_law(sampler, c.vocab):
-            parts = _lib.WORKSPACES.get(_lib.query("mtp_logits_topk_parts_bytes", B * L), "logits_topk_parts",
-                                        self.device)
-            nb = _lib.query("mtp_logits_topk_workspace_bytes", B * L, c.vocab)
-            tws = _lib.WORKSPACES.get(nb, "logits_topk", self.device)
-            topk = dict(parts=parts, ws=tws, ws_bytes=tws.numel(), temperature=float(sampler.temperature),
-                        top_k=int(sampler.top_k))
-        logits = self.verify_logits(tokens, q_start, topk=topk)
+        logits = self.verify_logits(tokens, q_start)
         self.last_logits = logits
-        return spec_accept(logits.reshape(B, L, -1), draft_logits, tokens[:, 1:].contiguous(), uniforms, sampler,
-                           target_parts=None if topk is None else (topk["parts"], topk["n_parts"]))
+        return spec_accept(logits.reshape(B, L, -1), draft_logits, tokens[:, 1:].contiguous(), uniforms, sampler)
 
 
 class CapturedVerifyStep:
