@@ -255,7 +255,7 @@ __device__ double np_sum_small(const double* a, int n) {
 
 // np_sum_small of n <= 64 values in LDS, run by a whole wave (same order:
 // lanes 0..7 hold the 8 strided accumulators); the result is uniform.
-__device__ double np_sum_wave(const double* a, int n) {
+__device__ __forceinline__ double np_sum_wave(const double* a, int n) {
   const int lane = threadIdx.x & 63;
   if (n < 8) {
     double r = 0.0;
@@ -567,42 +567,13 @@ constexpr int kLawKeys = 768;   // staged candidate keys per wave (38 chunks x 2
 
 __device__ __forceinline__ void wave_sync_lds() { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup"); }
 
-__device__ void build_law_wave(const ChunkPart* parts, int n_chunks, int ksel, int greedy, double temp, double top_p,
-                               RowLaw* law, uint64_t* s_keys) {
+// Top-k of the chunks' sorted key lists (list c at kp + c * kstride; lane c
+// holds list c's head h0 and next h1): k rounds of wave maxima. Returns the
+// lane's winner (lane r: the r-th largest key). Templated on the pointer so
+// that the staged case reads LDS (ds loads), not generic memory.
+template <typename KeyPtr>
+__device__ __forceinline__ uint64_t merge_sorted_lists(KeyPtr kp, int kstride, bool own, int ksel) {
   const int lane = threadIdx.x & 63;
-  const bool own = lane < n_chunks;
-  double m = -INFINITY, sc = 0.0;
-  int nf = 0;
-  if (own) {
-    m = parts[lane].m;
-    sc = parts[lane].s;
-    nf = parts[lane].nonfinite;
-  }
-  // Candidate keys: staged in LDS when they fit, else read in place.
-  const int ncand = n_chunks * ksel;
-  const uint64_t* kp;
-  int kstride;
-  if (ncand <= kLawKeys) {
-    for (int i = lane; i < ncand; i += 64) {
-      const int c = i / ksel;
-      s_keys[i] = parts[c].keys[i - c * ksel];
-    }
-    wave_sync_lds();
-    kp = s_keys;
-    kstride = ksel;
-  } else {
-    kp = parts[0].keys;
-    kstride = (int)(sizeof(ChunkPart) / sizeof(uint64_t));
-  }
-  // fp64 max / sum-exp combine, the sum in chunk order.
-  const double M = wave_max_f64(m);
-  nf = __any(nf) ? 1 : 0;
-  double S = 0.0;
-  if (!greedy) {
-    const double term = (own && m > -INFINITY) ? sc * exp(m - M) : 0.0;
-    for (int c = 0; c < n_chunks; ++c) S += rlf64(term, c);
-  }
-  // Top-k: k-way merge of the sorted chunk lists; head h0 and next h1 per lane.
   uint64_t h0 = 0ull, h1 = 0ull;
   int ptr = 0;
   if (own) {
@@ -620,6 +591,58 @@ __device__ void build_law_wave(const ChunkPart* parts, int n_chunks, int ksel, i
       h1 = ptr + 1 < ksel ? kp[(size_t)lane * kstride + ptr + 1] : 0ull;
     }
   }
+  return mysel;
+}
+
+__device__ __forceinline__ void build_law_wave(const ChunkPart* parts, int n_chunks, int ksel, int greedy,
+                                               double temp, double top_p, RowLaw* law, uint64_t* s_keys) {
+  const int lane = threadIdx.x & 63;
+  const bool own = lane < n_chunks;
+  double m = -INFINITY, sc = 0.0;
+  int nf = 0;
+  if (own) {
+    m = parts[lane].m;
+    sc = parts[lane].s;
+    nf = parts[lane].nonfinite;
+  }
+  // Candidate keys: staged in LDS when they fit (their loads issued with the
+  // statistics' loads above, one round trip for both), else read in place.
+  const int ncand = n_chunks * ksel;
+  const bool staged = ncand <= kLawKeys;
+  if (staged) {
+    // All of the lane's loads in flight at once, then the LDS stores. Key i
+    // is key i % ksel of chunk i / ksel; (c, r) follow i in steps of 64.
+    constexpr int kPer = kLawKeys / 64;
+    uint64_t kv[kPer];
+    int c = lane / ksel, r = lane - (lane / ksel) * ksel;
+    const int dc = 64 / ksel, dr = 64 - (64 / ksel) * ksel;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      kv[j] = lane + 64 * j < ncand ? parts[c].keys[r] : 0ull;
+      c += dc;
+      r += dr;
+      if (r >= ksel) {
+        r -= ksel;
+        ++c;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+      if (lane + 64 * j < ncand) s_keys[lane + 64 * j] = kv[j];
+    wave_sync_lds();
+  }
+  // fp64 max / sum-exp combine, the sum in chunk order.
+  const double M = wave_max_f64(m);
+  nf = __any(nf) ? 1 : 0;
+  double S = 0.0;
+  if (!greedy) {
+    const double term = (own && m > -INFINITY) ? sc * exp(m - M) : 0.0;
+    for (int c = 0; c < n_chunks; ++c) S += rlf64(term, c);
+  }
+  // The k-way merge of the sorted chunk lists.
+  const uint64_t mysel = staged ? merge_sorted_lists(s_keys, ksel, own, ksel)
+                                : merge_sorted_lists(parts[0].keys, (int)(sizeof(ChunkPart) / sizeof(uint64_t)), own,
+                                                     ksel);
   const uint64_t sel0 = rl64(mysel, 0);
   const int nonfinite = nf || !(greedy || (isfinite(S) && S > 0.0));
   if (nonfinite || greedy) {
@@ -680,7 +703,7 @@ __device__ void build_law_wave(const ChunkPart* parts, int n_chunks, int ksel, i
 }
 
 // Probability of tok under law L (0 if absent); whole wave, uniform result.
-__device__ double law_prob_wave(const RowLaw& L, int tok) {
+__device__ __forceinline__ double law_prob_wave(const RowLaw& L, int tok) {
   const int lane = threadIdx.x & 63;
   const uint64_t hit = __ballot(lane < L.n && L.ids[lane] == tok);
   return hit ? L.probs[__ffsll((unsigned long long)hit) - 1] : 0.0;
@@ -688,7 +711,7 @@ __device__ double law_prob_wave(const RowLaw& L, int tok) {
 
 // Generator.choice(ids, p) given its uniform (n <= 64, arrays in LDS); whole
 // wave. cdf = cumsum(p) / cdf[-1] in order; idx = #{cdf <= u}, at most n-1.
-__device__ int law_choice_wave(const int* ids, const double* p, int n, double u) {
+__device__ __forceinline__ int law_choice_wave(const int* ids, const double* p, int n, double u) {
   const int lane = threadIdx.x & 63;
   const double pv = lane < n ? p[lane] : 0.0;
   double run = 0.0, mine = 0.0;
@@ -707,7 +730,7 @@ __device__ int law_choice_wave(const int* ids, const double* p, int n, double u)
 // kMaxTopK entries for the residual law.
 // Kb: this request's depth; K: the row stride of the outputs; db: the index
 // of its first draft id.
-__device__ void accept_loop_wave(const RowLaw* tl, const RowLaw* dl, int b, int Kb, int K, int db, int greedy,
+__device__ __forceinline__ void accept_loop_wave(const RowLaw* tl, const RowLaw* dl, int b, int Kb, int K, int db, int greedy,
                                  const int32_t* __restrict__ draft_ids, const double* __restrict__ uniforms,
                                  int32_t* __restrict__ out_tokens, int32_t* __restrict__ n_accepted,
                                  double* __restrict__ accept_probs, int32_t* __restrict__ status, int* s_rid,
@@ -755,15 +778,20 @@ __device__ void accept_loop_wave(const RowLaw* tl, const RowLaw* dl, int b, int 
       // Residual max(p - q, 0) over the union of supports, ids ascending:
       // an id outside P's support has p = 0 and a zero residual, so the
       // positive residuals are P's entries in P's (ascending) order.
-      int myid = 0;
-      double r = 0.0;
-      if (lane < P.n) {
-        myid = P.ids[lane];
-        double qv = 0.0;
-        for (int j = 0; j < Qd.n; ++j)
-          if (Qd.ids[j] == myid) qv = Qd.probs[j];
-        r = fmax(P.probs[lane] - qv, 0.0);
+      // q of each of P's ids: lane j holds Q's entry j; a ballot per id of P
+      // finds its lane (ids are unique in a law), no LDS scan per lane.
+      const int pn = __builtin_amdgcn_readfirstlane(P.n);
+      const int qid = lane < Qd.n ? Qd.ids[lane] : -1;
+      const double qp = lane < Qd.n ? Qd.probs[lane] : 0.0;
+      const int myid = lane < pn ? P.ids[lane] : -2;
+      double qv = 0.0;
+      for (int i = 0; i < pn; ++i) {
+        const uint64_t hit = __ballot(qid == rli(myid, i));
+        const double v = hit ? rlf64(qp, __ffsll((unsigned long long)hit) - 1) : 0.0;
+        if (lane == i) qv = v;
       }
+      double r = 0.0;
+      if (lane < pn) r = fmax(P.probs[lane] - qv, 0.0);
       const bool keep = lane < P.n && r > 0.0 && isfinite(r);
       const uint64_t km = __ballot(keep);
       const int n = __popcll(km);

@@ -67,12 +67,27 @@ constexpr int kDppX1 = 0xB1, kDppX2 = 0x4E, kDppHalf = 0x141, kDppRow = 0x140;
 
 __device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
+__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v, uint32_t w) { return v > w ? v : w; }
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = dpp_max_u32(v, dpp32<kDppX1>(v));
+  v = dpp_max_u32(v, dpp32<kDppX2>(v));
+  v = dpp_max_u32(v, dpp32<kDppHalf>(v));
+  v = dpp_max_u32(v, dpp32<kDppRow>(v));
+  return dpp_max_u32(dpp_max_u32(rl32(v, 0), rl32(v, 16)), dpp_max_u32(rl32(v, 32), rl32(v, 48)));
+}
+
+// The u64 maximum as two 32-bit ones: the high words, then the low words of
+// the lanes holding the maximal high word (lexicographic, so the same value
+// as a 64-bit reduction, with single-instruction DPP steps).
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  v = umax64(v, dpp64<kDppX1>(v));
-  v = umax64(v, dpp64<kDppX2>(v));
-  v = umax64(v, dpp64<kDppHalf>(v));
-  v = umax64(v, dpp64<kDppRow>(v));
-  return umax64(umax64(rl64(v, 0), rl64(v, 16)), umax64(rl64(v, 32), rl64(v, 48)));
+  const uint32_t hi = (uint32_t)(v >> 32);
+  const uint32_t mh = wave_max_u32(hi);
+  const uint32_t ml = wave_max_u32(hi == mh ? (uint32_t)v : 0u);
+  return ((uint64_t)mh << 32) | ml;
 }
 
 __device__ __forceinline__ double wave_max_f64(double v) {
