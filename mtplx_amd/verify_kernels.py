@@ -10,10 +10,12 @@ the fixed-M entry points ``vk_eligible_m4`` / ``vk_eligible_m6`` :222-228,
 
 Kernels, by rows M (4-bit groups of 64/128 with K % 256 == 0):
 
-* M <= 32: ``mtp_qmv_affine4`` (MFMA 32x32x16 bf16 with exact nibble
-  operands, fp32 accumulation, one workgroup per 32 output columns) on the
-  MLX layout, or ``mtp_qmv_affine4_ex`` on a tile-major pack when the
-  caller has one;
+* M <= 32: ``mtp_qmv_affine4_ex`` (the streaming kernel: 1 KB contiguous
+  weight loads per wave, the leftover tiles split by K over all CUs) on a
+  tile-major pack of the triple, layout 2 (the 16x16x32 MFMA form) up to 4
+  rows and layout 1 beyond, packed once and kept like the M > 32 pack
+  (cfg1 shape: 15.7 against 25.5 us for ``mtp_qmv_affine4`` on the MLX
+  layout, which runs when ``MTPLX_AMD_PACK_CACHE=0``);
 * M > 32: ``mtp_qmm_affine4_mfma`` (each weight quad read once for 64 rows)
   on the layout-1 tile-major pack, in 64-row launches. A raw MLX triple is
   packed once and the pack kept, keyed by the weight tensor (a verify
@@ -92,8 +94,8 @@ def vk_eligible_m6(m: int, K: int, N: int, bits: int, group_size: int, dtype) ->
 
 # -- tile-major packs of raw MLX triples --------------------------------------
 
-# id(weight tensor) -> (weakref to it, version, scales ptr, biases ptr, group size, pack). Keyed by
-# identity (a tensor's == is elementwise); an entry goes when its weight tensor is collected.
+# (id(weight tensor), layout) -> (weakref to it, version, scales ptr, biases ptr, group size, pack).
+# Keyed by identity (a tensor's == is elementwise); entries go when their weight tensor is collected.
 _PACKS: dict = {}
 
 
@@ -101,14 +103,12 @@ def _pack_cache_enabled() -> bool:
     return (os.environ.get("MTPLX_AMD_PACK_CACHE") or "1").strip() not in {"0", "false", "off", "no"}
 
 
-def layout1_pack(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int) -> torch.Tensor:
-    """The layout-1 tile-major copy (``mtp_pack_affine4``) of a 4-bit MLX
-    triple ``[N, K/8]``. Kept per weight tensor while the tensor lives and its
-    version counter, scales and biases are unchanged (unless
-    ``MTPLX_AMD_PACK_CACHE=0``, which packs into a temporary every call)."""
+def _cached_pack(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int,
+                 layout: int) -> torch.Tensor:
     key_ok = _pack_cache_enabled()
+    key = (id(w), layout)
     if key_ok:
-        hit = _PACKS.get(id(w))
+        hit = _PACKS.get(key)
         if hit is not None:
             ref, ver, sp, bp, gs, pack = hit
             if ref() is w and ver == w._version and sp == scales.data_ptr() and bp == biases.data_ptr() and \
@@ -120,14 +120,28 @@ def layout1_pack(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, gr
         raise NotImplementedError(f"cannot pack N={n} K={k} (K must be a multiple of 256)")
     wc, sc, bc = w.contiguous(), scales.contiguous(), biases.contiguous()
     out = torch.empty(nbytes // 4, dtype=torch.int32, device=w.device)
-    _lib.call("mtp_pack_affine4", wc.data_ptr(), sc.data_ptr(), bc.data_ptr(), out.data_ptr(), n, k, int(group_size),
-              _lib.stream_handle(w.device))
+    _lib.call("mtp_pack_affine4" if layout == 1 else "mtp_pack_affine4_mf16", wc.data_ptr(), sc.data_ptr(),
+              bc.data_ptr(), out.data_ptr(), n, k, int(group_size), _lib.stream_handle(w.device))
     if key_ok:
-        key = id(w)
         if key not in _PACKS:
             weakref.finalize(w, _PACKS.pop, key, None)
         _PACKS[key] = (weakref.ref(w), w._version, scales.data_ptr(), biases.data_ptr(), int(group_size), out)
     return out
+
+
+def layout1_pack(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int) -> torch.Tensor:
+    """The layout-1 tile-major copy (``mtp_pack_affine4``) of a 4-bit MLX
+    triple ``[N, K/8]``. Kept per weight tensor while the tensor lives and its
+    version counter, scales and biases are unchanged (unless
+    ``MTPLX_AMD_PACK_CACHE=0``, which packs into a temporary every call)."""
+    return _cached_pack(w, scales, biases, group_size, 1)
+
+
+def layout2_pack(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int) -> torch.Tensor:
+    """The layout-2 copy (``mtp_pack_affine4_mf16``, the 16x16x32 MFMA order
+    for up to 4 rows) of a 4-bit MLX triple, kept as :func:`layout1_pack`
+    keeps its own."""
+    return _cached_pack(w, scales, biases, group_size, 2)
 
 
 def rows_matmul(x2: torch.Tensor, pack: torch.Tensor, n: int, group_size: int,
@@ -166,8 +180,16 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
         y = rows_matmul(x2, layout1_pack(w, scales, biases, group_size), n, group_size, out)
         return y.reshape(*lead, n)
     y = out if out is not None else torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
-    _lib.call("mtp_qmv_affine4", x2.data_ptr(), w.data_ptr(), scales.data_ptr(), biases.data_ptr(), y.data_ptr(), m, n,
-              k, group_size, None, 0, _lib.stream_handle(x.device))
+    st = _lib.stream_handle(x.device)
+    if not _pack_cache_enabled():   # no copy kept: the MLX layout in place
+        _lib.call("mtp_qmv_affine4", x2.data_ptr(), w.data_ptr(), scales.data_ptr(), biases.data_ptr(), y.data_ptr(),
+                  m, n, k, group_size, None, 0, st)
+        return y.reshape(*lead, n)
+    lay = 2 if m <= 4 else 1
+    pack = layout2_pack(w, scales, biases, group_size) if lay == 2 else layout1_pack(w, scales, biases, group_size)
+    ws = _lib.WORKSPACES.get(max(256, _lib.query("mtp_qmv_workspace_bytes", m, n, k, 1)), "verify_qmv", x.device)
+    _lib.qmv_ex(st, x=x2, w0=pack, y0=y, M=m, N=n, K=k, group_size=int(group_size), xmode=0, emode=0, packed=lay,
+                ws=ws, ws_bytes=ws.numel())
     return y.reshape(*lead, n)
 
 

@@ -17,7 +17,7 @@ import torch
 
 from . import _lib
 from .quant import QuantizedLinear
-from .verify_kernels import STREAM_ROWS, fast_path, quantized_matmul, rows_matmul
+from .verify_kernels import STREAM_ROWS, _pack_cache_enabled, fast_path, quantized_matmul, rows_matmul
 
 
 def _affine4(module: Any) -> bool:
@@ -27,23 +27,30 @@ def _affine4(module: Any) -> bool:
 
 
 def _packed(module: QuantizedLinear, m: int) -> tuple[torch.Tensor, int] | None:
-    """The module's cached tile-major pack for ``m`` rows: layout 2 (the
-    16x16x32 MFMA form) at up to 4 rows when cached, else layout 1, or None.
-    A module packed once (``module.pack()``) reads its weights as 1 KB
-    contiguous runs per wave load (cfg1 shape: 17.2 us against 25.5 us on the
-    MLX layout, whose per-lane row reads scatter), so the facade takes the
-    pack whenever it is there and the MLX triple otherwise."""
+    """The module's tile-major pack for ``m`` rows: layout 2 (the 16x16x32
+    MFMA form) at up to 4 rows, else layout 1, or None. A pack reads the
+    weights as 1 KB contiguous runs per wave load (cfg1 shape: 15.7 us
+    against 25.5 us on the MLX layout, whose per-lane row reads scatter), so
+    a module that still holds its MLX triple is packed for the layout on its
+    first call and keeps it (unless ``MTPLX_AMD_PACK_CACHE=0``); a released
+    module serves the layout it has."""
     if m <= 4 and module.packed_mf16 is not None:
         return module.packed_mf16, 2
+    can_pack = module.weight is not None and fast_path(module.bits, module.group_size, module.in_features) and \
+        _pack_cache_enabled()
+    if m <= 4 and can_pack:
+        return module.pack(layout=2), 2
     if module.packed is not None:
         return module.packed, 1
+    if can_pack:
+        return module.pack(), 1
     return None
 
 
 def _qmv_packed(stream, m: int, n: int, k: int, **kw) -> None:
     """mtp_qmv_affine4_ex on packed weights with this stream's split-K workspace."""
     dev = kw["x"].device
-    ws = _lib.WORKSPACES.get(max(256, _lib.query("mtp_qmv_workspace_bytes", m, n, 1, 1)), "verify_qmv", dev)
+    ws = _lib.WORKSPACES.get(max(256, _lib.query("mtp_qmv_workspace_bytes", m, n, k, 1)), "verify_qmv", dev)
     _lib.qmv_ex(stream, M=m, N=n, K=k, ws=ws, ws_bytes=ws.numel(), **kw)
 
 

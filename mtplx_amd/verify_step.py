@@ -53,10 +53,14 @@ MOE_SIDE_STREAM = (os.environ.get("MTPLX_AMD_MOE_SIDE_STREAM") or "1").strip() n
 
 
 def qmv_ws_bytes(M: int, c: "DecoderConfig") -> int:
-    """Split-K workspace of the streaming matmul for every projection of the step."""
+    """Split-K workspace of the streaming matmul for every projection of the
+    step (the tail split's, or the full split's where x does not fit in LDS)."""
     ffn = c.expert_ffn if c.n_experts else c.ffn
-    ns = (c.qkv_out, c.hidden, ffn, c.vocab) + ((c.shared_ffn, c.n_experts + 1) if c.n_experts else ())
-    return max(_lib.query("mtp_qmv_workspace_bytes", M, n, 1, 1) for n in ns)
+    H = c.hidden
+    nk = [(c.qkv_out, H), (H, c.n_heads * c.head_dim), (ffn, H), (H, ffn), (c.vocab, H)]
+    if c.n_experts:
+        nk += [(c.shared_ffn, H), (H, c.shared_ffn), (c.n_experts + 1, H)]
+    return max(_lib.query("mtp_qmv_workspace_bytes", M, n, k, 1) for n, k in nk)
 
 
 def _exact_lane(sampler: SamplerConfig) -> bool:
