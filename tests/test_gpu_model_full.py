@@ -71,21 +71,24 @@ def test_cfg3_width_two_layers_match_oracle(gpu):
     assert int(res.n_accepted[0]) == w.n_accepted
 
 
-def test_cfg3_width_sixteen_rows_full_split(gpu):
-    """4 requests x 4 rows (M = 16) at the 27B width: 16 rows of x at hidden
-    5120 do not fit in one workgroup's LDS, so the uniform step's streaming
-    matmuls take the full K split, sized by the step's workspace query with
-    each projection's real K. One layer against the oracle at the bar."""
+@pytest.mark.parametrize("B,L", [(4, 4), (8, 4), (3, 1), (5, 2)])
+def test_cfg3_width_uniform_batches(gpu, B, L):
+    """B requests x L rows on the uniform cache at the 27B width, one layer
+    against the oracle at the bar. From 16 rows on, x at hidden 5120 does not
+    fit in one workgroup's LDS, so the streaming matmuls take the full K split
+    (sized by the step's workspace query with each projection's real K) and
+    q|k|v runs without the fused RoPE epilogue; M = 3 and 10 cover row
+    counts off the tile multiples."""
     from mtplx_amd.verify_step import DENSE_27B, VerifyModel
     from dataclasses import replace
     cfg = replace(DENSE_27B, layers=1)
-    model = VerifyModel(cfg, device="cuda", seed=19)
-    model.allocate_cache(4, 2048)
+    model = VerifyModel(cfg, device="cuda", seed=19 + B)
+    model.allocate_cache(B, 2048)
     kc, vc = _caches(model, cfg.layers)
-    gen = torch.Generator(device="cuda").manual_seed(20)
-    tokens = torch.randint(0, cfg.vocab, (4, 4), device="cuda", dtype=torch.int32, generator=gen)
-    qs_np = np.array([2044, 100, 1500, 7])
+    gen = torch.Generator(device="cuda").manual_seed(20 + B)
+    tokens = torch.randint(0, cfg.vocab, (B, L), device="cuda", dtype=torch.int32, generator=gen)
+    qs_np = np.random.default_rng(B).integers(0, 2048 - L, B)
     qs = torch.from_numpy(qs_np.astype(np.int32)).cuda()
     logits = model.verify_logits(tokens, qs, check=True)
     want = verify_forward(model_params_numpy(model), cfg, tokens.cpu().numpy(), qs_np, kc, vc)
-    assert_close(logits.cpu().numpy().astype(np.float64), want, rtol=1e-2, atol=1e-2, what="M=16 logits")
+    assert_close(logits.cpu().numpy().astype(np.float64), want, rtol=1e-2, atol=1e-2, what=f"B={B} L={L} logits")
