@@ -458,8 +458,9 @@ class VerifyModel:
                 group_size=gs, xmode=0, emode=1, packed=lay)
             ss_h = ss_a
             if c.n_experts:
-                self._moe_block(L, h, M, st, qmv, lay, ss_b)
-                ss_h = ss_b
+                # (the statistics' layout holds up to 32 rows)
+                ss_h = ss_b if M <= 32 else None
+                self._moe_block(L, h, M, st, qmv, lay, ss_h)
             else:
                 qmv(st, x=h, x2=L.post_norm, ss_in=ss_h, eps=c.rms_eps, w0=W(L.gate), w1=W(L.up), y0=act,
                     y_sums=act_sums, M=M, N=c.ffn, K=H, group_size=gs, xmode=2, emode=3, packed=lay)
@@ -476,12 +477,13 @@ class VerifyModel:
             self.check_status()
         return logits
 
-    def _moe_block(self, L: Layer, h: torch.Tensor, M: int, st: int, qmv, lay: int, ss_out: torch.Tensor) -> None:
+    def _moe_block(self, L: Layer, h: torch.Tensor, M: int, st: int, qmv, lay: int,
+                   ss_out: torch.Tensor | None) -> None:
         """The sparse block on the post-attention norm of ``h``, added to ``h``
         in place: routed experts through the sorted chain
         (``mtplx/models/qwen4_exp.py:1544-1577``) plus the sigmoid-gated shared
         expert (``:1438-1445``). The combine writes the output rows' sums of
-        squares to ``ss_out`` for the next fused RMSNorm."""
+        squares to ``ss_out`` (when given) for the next fused RMSNorm."""
         c = self.cfg
         call = _lib.call
         gs = c.group_size

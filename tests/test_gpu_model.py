@@ -54,12 +54,16 @@ def test_dense_verify_step_matches_oracle(gpu):
         assert int(res.n_accepted[b]) == w.n_accepted
 
 
-def test_moe_verify_step_matches_oracle(gpu):
+@pytest.mark.parametrize("B,L", [(2, 4), (1, 1), (3, 3), (8, 4)])
+def test_moe_verify_step_matches_oracle(gpu, B, L):
+    """The MoE block at 1 to 32 rows (the sort, both expert row classes on two
+    streams, the combine and its statistics for the next layer's norm)."""
     from mtplx_amd.verify_step import DecoderConfig
     cfg = DecoderConfig(layers=2, hidden=512, ffn=0, n_heads=8, n_kv_heads=2, head_dim=128, vocab=2048,
                         n_experts=16, top_k=4, expert_ffn=256, shared_ffn=256)
-    model, tokens, logits, want, kc, vc = _run(cfg, 2, 4, [10, 150], 7)
-    assert_close(logits.cpu().numpy().astype(np.float64), want, rtol=1e-2, atol=1e-2, what="moe logits")
+    starts = [int(v) for v in np.random.default_rng(B * 10 + L).integers(0, 320 - L, B)]
+    model, tokens, logits, want, kc, vc = _run(cfg, B, L, starts, 7)
+    assert_close(logits.cpu().numpy().astype(np.float64), want, rtol=1e-2, atol=1e-2, what=f"moe logits B={B} L={L}")
 
 
 def test_status_word_flags_bad_token_and_position(gpu):
