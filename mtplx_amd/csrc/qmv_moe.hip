@@ -148,9 +148,12 @@ static int moe_launch_classes(const QmmParams& p, MoeUnits mu, int max_rows, hip
   mu.row_tiles = 1;
   mu.m_lo = 1;
   mu.m_hi = 4;
-  // six tiles per unit: graph-free cfg5 steps measured 14.3 ms at 4-6,
-  // 14.7 at 8, 15.0 at 10 and 16.0 with one unit per CU
-  mu.tpu = env_int("MTPLX_AMD_MOE_TILES_SMALL", 6);
+  // gate|up: six tiles per unit (graph-free cfg5 steps measured 14.3 ms at
+  // 4-6, 14.7 at 8, 15.0 at 10 and 16.0 with one unit per CU). down, whose
+  // tiles are 4x smaller at K = 1536: twelve (cfg5 graph steps with the side
+  // stream 12.67-12.69 ms against 12.73-12.76 at six, 12.93-12.96 at nine,
+  // 12.99 at eighteen).
+  mu.tpu = EM == E_STORE ? env_int("MTPLX_AMD_MOE_TILES_SMALL_DOWN", 12) : env_int("MTPLX_AMD_MOE_TILES_SMALL", 6);
   if (row_class != 2) {
     const int rc = moe_launch<4, 4, EM>(p, mu, 4, st);
     if (rc != MTP_OK) return rc;
