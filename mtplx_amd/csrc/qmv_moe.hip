@@ -165,7 +165,10 @@ static int moe_launch_classes(const QmmParams& p, MoeUnits mu, int max_rows, hip
   mu.row_tiles = cdiv(max_rows, 16);
   mu.m_lo = 5;
   mu.m_hi = INT_MAX;
-  mu.tpu = env_int("MTPLX_AMD_MOE_TILES_LARGE", 0);
+  // three tiles per unit (cfg5 graph steps with the side stream: 12.42-12.43
+  // ms at three, 12.43-12.47 at four, 12.59 at five, 12.67-12.69 with about
+  // one unit per CU, 13.0 at eight)
+  mu.tpu = env_int("MTPLX_AMD_MOE_TILES_LARGE", 3);
   return moe_launch<8, 8, EM>(p, mu, 16, st);
 }
 
