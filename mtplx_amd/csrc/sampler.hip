@@ -127,15 +127,16 @@ __global__ __launch_bounds__(kSampThreads) void vocab_partials(const float* __re
   __shared__ int s_rank, s_cnt, s_nsel, s_nvalid;
   __shared__ uint64_t s_prefix;
   {
+    // valid keys: a ballot count per key slot, one LDS add per wave
     int nv = 0;
 #pragma unroll
-    for (int e = 0; e < kEPT; ++e) nv += keys[e] != 0ull;
+    for (int e = 0; e < kEPT; ++e) nv += __popcll(__ballot(keys[e] != 0ull));
     if (tid == 0) {
       s_nvalid = 0;
       s_nsel = 0;
     }
     __syncthreads();
-    if (nv) atomicAdd(&s_nvalid, nv);
+    if (lane == 0 && nv) atomicAdd(&s_nvalid, nv);
   }
   __syncthreads();
   const int nvalid = s_nvalid;
