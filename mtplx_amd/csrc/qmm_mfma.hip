@@ -11,9 +11,9 @@
 //    per wave), or 2 column tiles x {gate, up} for the fused SwiGLU pair, so
 //    each staged x quad serves 128 weight columns;
 //  * x rows land in LDS with direct-to-LDS loads (no registers); each 16-byte
-//    chunk kc of row m sits at slot 32m + (kc ^ (m & 7)), so one wave load
-//    writes 1 KB contiguous and the A-operand reads of 8 consecutive rows hit
-//    8 different 16-byte bank groups;
+//    chunk kc of row m sits at slot 32m + (kc ^ (m & 15)), so one wave load
+//    writes 1 KB contiguous and the A-operand reads of 16 consecutive rows
+//    hit 16 different 16-byte bank groups;
 //  * the weights stream from the tile-major packed layout (mtp_pack_affine4)
 //    through a two-deep register ring, exactly as the skinny kernel reads
 //    them; nibbles become exact bf16 operands 128 + q with one AND-OR each;
@@ -52,7 +52,7 @@ struct QmmRowsParams {
   uint32_t* counters;      // [leftover groups]
 };
 
-__device__ __forceinline__ int xslot(int m, int kc) { return m * kQmSlotsPerRow + (kc ^ (m & 7)); }
+__device__ __forceinline__ int xslot(int m, int kc) { return m * kQmSlotsPerRow + (kc ^ (m & 15)); }
 
 // Direct-to-LDS loads of x[0:M, 256q : 256q + 256): wave instruction t
 // covers rows 2t and 2t + 1. A row past M (odd M) loads row M - 1 into a
@@ -62,7 +62,7 @@ __device__ __forceinline__ void qm_stage(const QmmRowsParams& p, unsigned char* 
   for (int t = wave; t < ninst; t += kQmWaves) {
     const int m = 2 * t + (lane >> 5);
     const int mr = m < p.M ? m : p.M - 1;
-    const int kc = (lane & 31) ^ (m & 7);
+    const int kc = (lane & 31) ^ (m & 15);
     __builtin_amdgcn_global_load_lds((gptr_t)(p.x + (size_t)mr * p.ldx + 256 * q + 8 * kc),
                                      (lptr_t)(buf + (size_t)t * 1024), 16, 0, 0);
   }
