@@ -210,20 +210,7 @@ __global__ __launch_bounds__(kSampThreads) void vocab_partials(const float* __re
   if (wave != 0) return;
   ChunkPart* out = parts + (size_t)row * n_chunks + chunk;
   const int nsel = s_nsel < kMaxTopK ? s_nsel : kMaxTopK;
-  uint64_t kv = lane < nsel ? s_sel[lane] : 0ull;
-  // bitonic sort of 64 keys across the wave, descending
-#pragma unroll
-  for (int size = 2; size <= 64; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(kv >> 32), stride, 64) << 32) |
-                         (uint32_t)__shfl_xor((int)(uint32_t)kv, stride, 64);
-      const bool lower = (lane & stride) == 0;
-      const bool desc = (lane & size) == 0;   // the last pass (size 64) orders all 64 descending
-      const bool take_max = lower == desc;
-      kv = take_max ? (kv > o ? kv : o) : (kv < o ? kv : o);
-    }
-  }
+  const uint64_t kv = wave_sort_desc_u64(lane < nsel ? s_sel[lane] : 0ull);
   if (lane < ksel) out->keys[lane] = kv;
   if (lane == 0) {
     int nf = 0;

@@ -80,14 +80,36 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return dpp_max_u32(dpp_max_u32(rl32(v, 0), rl32(v, 16)), dpp_max_u32(rl32(v, 32), rl32(v, 48)));
 }
 
-// The u64 maximum as two 32-bit ones: the high words, then the low words of
-// the lanes holding the maximal high word (lexicographic, so the same value
-// as a 64-bit reduction, with single-instruction DPP steps).
+// The u64 maximum as 32-bit ones: the high words, then, when more than one
+// lane holds the maximal high word, the low words of those lanes
+// (lexicographic, so the same value as a 64-bit reduction, with
+// single-instruction DPP steps). A single holder's key is read directly.
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   const uint32_t hi = (uint32_t)(v >> 32);
   const uint32_t mh = wave_max_u32(hi);
+  const uint64_t at = __ballot(hi == mh);
+  if (__popcll(at) == 1) return ((uint64_t)mh << 32) | rl32((uint32_t)v, __ffsll((unsigned long long)at) - 1);
   const uint32_t ml = wave_max_u32(hi == mh ? (uint32_t)v : 0u);
   return ((uint64_t)mh << 32) | ml;
+}
+
+// Bitonic sort of one key per lane across the wave, descending (lane 0 the
+// largest). Call from uniform control flow.
+__device__ __forceinline__ uint64_t wave_sort_desc_u64(uint64_t kv) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(kv >> 32), stride, 64) << 32) |
+                         (uint32_t)__shfl_xor((int)(uint32_t)kv, stride, 64);
+      const bool lower = (lane & stride) == 0;
+      const bool desc = (lane & size) == 0;   // the last pass (size 64) orders all 64 descending
+      const bool take_max = lower == desc;
+      kv = take_max ? (kv > o ? kv : o) : (kv < o ? kv : o);
+    }
+  }
+  return kv;
 }
 
 __device__ __forceinline__ double wave_max_f64(double v) {

@@ -72,6 +72,38 @@ def test_sparse_law_and_draws_match_oracle(gpu, V, cfg):
         assert int(smp[r]) == S.choice(want, u[r]), r
 
 
+@pytest.mark.parametrize("case", ["k20", "k64", "ties", "one_chunk"])
+def test_narrow_top_k_selection_paths(gpu, case):
+    """The narrow law's top k is a k-way merge of the chunks' sorted lists,
+    one wave maximum of the list heads per round (high words first, the low
+    words only when several heads share the maximal high word). Cases: plain
+    k = 20 over 38 chunks, k = 64, 20 equal values spread over 10 chunks (the
+    id decides every round), one chunk with every key selected; ids and draws
+    exact, against the oracle."""
+    rng = np.random.default_rng(11)
+    V, k, rows = 151936, 20, 4
+    if case == "one_chunk":
+        V, k = 50, 50          # top_k = V: one chunk, every key selected
+    logits = rng.normal(0, 3, (rows, V)).astype(np.float32)
+    if case == "k64":
+        k = 64
+    elif case == "ties":
+        # 20 equal top values spread over 10 chunks, two each: the id decides
+        for c in range(10):
+            logits[:, 4096 * (3 * c + 1) + 7 * c] = 20.0
+            logits[:, 4096 * (3 * c + 1) + 7 * c + 1000] = 20.0
+    cfg = S.SamplerConfig(0.6, 0.95, k)
+    u = rng.random(rows)
+    ids, probs, cnt, smp, st = _sample_rows(logits, cfg, u)
+    assert (st == 0).all()
+    for r in range(rows):
+        want = S.sparse_distribution(logits[r], cfg)
+        n = int(cnt[r])
+        assert ids[r, :n].tolist() == want.ids.tolist(), (case, r)
+        assert np.allclose(probs[r, :n], want.probs, rtol=0, atol=1e-9), (case, r)
+        assert int(smp[r]) == S.choice(want, u[r]), (case, r)
+
+
 def test_wide_law_tie_group_cut(gpu):
     """A tie group straddling the top-k cut keeps its lowest ids, and one
     straddling the nucleus cut is cut inside the group (same mass each)."""
