@@ -718,8 +718,10 @@ __device__ __forceinline__ int law_choice_wave(const int* ids, const double* p, 
 // kMaxTopK entries for the residual law.
 // Kb: this request's depth; K: the row stride of the outputs; db: the index
 // of its first draft id.
-__device__ __forceinline__ void accept_loop_wave(const RowLaw* tl, const RowLaw* dl, int b, int Kb, int K, int db, int greedy,
-                                 const int32_t* __restrict__ draft_ids, const double* __restrict__ uniforms,
+// tok_l / u_l: lane d holds draft token d and uniform d of the request
+// (loaded at kernel start, so the chain reads registers, not memory).
+__device__ __forceinline__ void accept_loop_wave(const RowLaw* tl, const RowLaw* dl, int b, int Kb, int K, int greedy,
+                                 int tok_l, double u_l,
                                  int32_t* __restrict__ out_tokens, int32_t* __restrict__ n_accepted,
                                  double* __restrict__ accept_probs, int32_t* __restrict__ status, int* s_rid,
                                  double* s_rp) {
@@ -727,7 +729,6 @@ __device__ __forceinline__ void accept_loop_wave(const RowLaw* tl, const RowLaw*
   int32_t* ot = out_tokens + (size_t)b * (K + 1);
   for (int d = lane; d <= K; d += 64) ot[d] = -1;
   for (int d = lane; d < K; d += 64) accept_probs[(size_t)b * K + d] = -1.0;
-  const double* u = uniforms + (size_t)b * (K + 1);
   int ui = 0, nacc = 0, bad = 0;
   for (int d = 0; d <= Kb; ++d) {
     const RowLaw& P = tl[d];
@@ -736,13 +737,13 @@ __device__ __forceinline__ void accept_loop_wave(const RowLaw* tl, const RowLaw*
       break;
     }
     if (d == Kb) {   // all drafts accepted: bonus from row K_b
-      const int tok = greedy ? P.ids[0] : law_choice_wave(P.ids, P.probs, P.n, u[ui++]);
+      const int tok = greedy ? P.ids[0] : law_choice_wave(P.ids, P.probs, P.n, rlf64(u_l, ui++));
       if (lane == 0) ot[Kb] = tok;
       nacc = Kb;
       break;
     }
     const RowLaw& Qd = dl[d];
-    const int tok = draft_ids[(size_t)db + d];
+    const int tok = rli(tok_l, d);
     const double p = law_prob_wave(P, tok);
     const double q = law_prob_wave(Qd, tok);
     double a;
@@ -752,7 +753,7 @@ __device__ __forceinline__ void accept_loop_wave(const RowLaw* tl, const RowLaw*
       a = acc ? 1.0 : 0.0;
     } else {
       a = (q <= 0.0) ? (p > 0.0 ? 1.0 : 0.0) : fmin(1.0, p / q);
-      acc = u[ui++] <= a;
+      acc = rlf64(u_l, ui++) <= a;
     }
     if (lane == 0) accept_probs[(size_t)b * K + d] = a;
     if (acc) {
@@ -791,14 +792,14 @@ __device__ __forceinline__ void accept_loop_wave(const RowLaw* tl, const RowLaw*
       wave_sync_lds();
       const double tot = np_sum_wave(s_rp, n);
       if (n == 0 || !(isfinite(tot) && tot > 0.0)) {
-        corr = law_choice_wave(P.ids, P.probs, P.n, u[ui++]);
+        corr = law_choice_wave(P.ids, P.probs, P.n, rlf64(u_l, ui++));
       } else {
         if (lane < n) s_rp[lane] = s_rp[lane] / tot;
         wave_sync_lds();
         const double t2 = np_sum_wave(s_rp, n);
         if (lane < n) s_rp[lane] = s_rp[lane] / t2;
         wave_sync_lds();
-        corr = law_choice_wave(s_rid, s_rp, n, u[ui++]);
+        corr = law_choice_wave(s_rid, s_rp, n, rlf64(u_l, ui++));
       }
     }
     if (lane == 0) ot[d] = corr;
@@ -832,6 +833,14 @@ __global__ __launch_bounds__(1024) void accept_laws(const ChunkPart* __restrict_
     if (threadIdx.x == 0) req_reject(b, K, out_tokens, n_accepted, accept_probs, status);
     return;
   }
+  // The accept chain's inputs, loaded now (K + 1 <= 64: the host's bound).
+  double u_l = 0.0;
+  int tok_l = -1;
+  if (wave == 0) {
+    const int lane = threadIdx.x & 63;
+    if (lane <= Kb) u_l = uniforms[(size_t)b * (K + 1) + lane];
+    if (lane < Kb) tok_l = draft_ids[(size_t)db + lane];
+  }
   const int nlaw = 2 * Kb + 1;
   RowLaw* laws = reinterpret_cast<RowLaw*>(s_lds);   // sized for 2K + 1 laws
   uint64_t* keys = reinterpret_cast<uint64_t*>(s_lds + (size_t)(2 * K + 1) * sizeof(RowLaw)) + (size_t)wave * kLawKeys;
@@ -844,8 +853,8 @@ __global__ __launch_bounds__(1024) void accept_laws(const ChunkPart* __restrict_
   if (wave == 0) {   // the residual scratch reuses wave 0's key area
     double* s_rp = reinterpret_cast<double*>(keys);
     int* s_rid = reinterpret_cast<int*>(s_rp + kMaxTopK);
-    accept_loop_wave(laws, laws + Kb + 1, b, Kb, K, db, greedy, draft_ids, uniforms, out_tokens, n_accepted,
-                     accept_probs, status, s_rid, s_rp);
+    accept_loop_wave(laws, laws + Kb + 1, b, Kb, K, greedy, tok_l, u_l, out_tokens, n_accepted, accept_probs,
+                     status, s_rid, s_rp);
   }
 }
 
@@ -1421,7 +1430,7 @@ static int spec_accept_run(const float* target_logits, const float* draft_logits
   } else if (n_chunks <= 64) {
     const int nwv = 2 * K + 1 < 16 ? 2 * K + 1 : 16;
     const size_t lds = accept_laws_lds(K, nwv);
-    if (lds > 160 * 1024) {
+    if (lds > 160 * 1024 || K + 1 > 64) {   // (the LDS bound alone keeps K <= 41)
       set_error("%s: K=%d needs %zu B of LDS", who, K, lds);
       return MTP_ERR_UNSUPPORTED;
     }
