@@ -297,12 +297,13 @@ __device__ __forceinline__ void attn_vt_body(const AttnParams& p, const int unit
 // tiles' K and V^T operands in flight while this one is computed); the waves
 // then merge in LDS in wave order as attn_vt_body does and the workgroup
 // writes the piece's partial (o rows to po, (max, l) pairs to pml). qs, L:
-// the request's first query position and query count. A wave with k0 >= k1
+// the request's first query position and query count; hblk: the first
+// 32-key block of head (b, h) (req_head_block). A wave with k0 >= k1
 // contributes nothing. Every thread of the four waves must call it.
 template <bool WT, int NRG>
 __device__ __forceinline__ void attn_vl_piece(const AttnParams& p, const int b, const int h, const int qs,
-                                              const int L, const int k0, const int k1, float* po, float* pml,
-                                              unsigned char* lds) {
+                                              const int L, const int k0, const int k1, const size_t hblk,
+                                              float* po, float* pml, unsigned char* lds) {
   constexpr int kOS = kVtOS;
   float* s_o = reinterpret_cast<float*>(lds);   // [kVtWaves][32 * kOS]
   float* s_m = s_o + kVtWaves * 32 * kOS;       // [kVtWaves][32]
@@ -332,7 +333,7 @@ __device__ __forceinline__ void attn_vl_piece(const AttnParams& p, const int b, 
       qop[i] = __builtin_bit_cast(bf16x8, raw);
     }
   }
-  const size_t hb = req_head_block(p, b, h) * 4096;
+  const size_t hb = hblk * 4096;
   const uint16_t* kbase = p.k + hb;
   const uint16_t* vbase = p.v + hb;
   // Tiles at or past k1 reload this wave's last block (valid memory, still in
@@ -505,7 +506,7 @@ __device__ __forceinline__ void attn_vl_body(const AttnParams& p, const int unit
   const int wk = p.split_keys / kVtWaves;
   const int k0 = k0u + wave * wk;
   const int k1 = (k0 + wk < kv_end) ? k0 + wk : kv_end;
-  attn_vl_piece<WT, NRG>(p, b, h, qs, L, k0, k1, po, pml, lds);
+  attn_vl_piece<WT, NRG>(p, b, h, qs, L, k0, k1, req_head_block(p, b, h), po, pml, lds);
 }
 
 // Balanced work for the per-request-capacity layout. The batch's 32-key
@@ -518,21 +519,14 @@ __device__ __forceinline__ void attn_vl_body(const AttnParams& p, const int unit
 // slots from bal_base(bh), one per workgroup that touches it, in workgroup
 // order; the merge reads the (base, count) table that workgroup 0 writes.
 constexpr int kBalMaxReq = 256;   // requests the per-workgroup prefix table holds
-constexpr size_t attn_bal_lds_bytes() { return attn_vt_lds_bytes() + (size_t)3 * kBalMaxReq * sizeof(int); }
+constexpr int kBalReqArrays = 8;   // per-request values the prologue keeps in LDS (ints)
+constexpr size_t attn_bal_lds_bytes() {
+  return attn_vt_lds_bytes() + (size_t)kBalReqArrays * kBalMaxReq * sizeof(int);
+}
 
 // Workgroup owning global tile x (ranges [w T / G, (w+1) T / G)).
 __device__ __forceinline__ int bal_owner(long long x, long long T, int G) {
   return (int)(((x + 1) * G - 1) / T);
-}
-
-// Tiles per head of request b (keys [0, kv_end) in 32-key tiles).
-__device__ __forceinline__ int bal_req_tiles(const AttnParams& p, int b) {
-  const int qs = p.q_start[b];
-  const int L = p.q_lens ? p.q_lens[b] : p.L;
-  const int capb = req_cap(p, b);
-  int kv_end = (qs + L < capb) ? qs + L : capb;
-  if (kv_end < 0) kv_end = 0;
-  return (kv_end + kTileKeys - 1) / kTileKeys;
 }
 
 // Slots (partials) of head (b, h) whose first global tile is P, nt tiles.
@@ -545,14 +539,39 @@ __device__ __forceinline__ void attn_bal_body(const AttnParams& p, unsigned char
   int* s_nt = reinterpret_cast<int*>(lds + attn_vt_lds_bytes());   // [B] tiles per head of each request
   int* s_pt = s_nt + kBalMaxReq;                                    // [B] first global tile of each request
   int* s_ps = s_pt + kBalMaxReq;                                    // [B] first slot of each request
+  int* s_qs = s_ps + kBalMaxReq;                                    // [B] first query position
+  int* s_ql = s_qs + kBalMaxReq;                                    // [B] query rows
+  int* s_ke = s_ql + kBalMaxReq;                                    // [B] keys [0, kv_end) attended
+  int* s_hb = s_ke + kBalMaxReq;                                    // [2B] head 0's first block, blocks per head
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = (int)gridDim.x, w = (int)blockIdx.x;
   const int B = p.B, Hkv = p.Hkv;
-  // Tiles per request, then the request-major prefix sums (wave 0, 64
-  // requests at a time with a running carry).
-  for (int b = tid; b < B; b += kVtWaves * 64) s_nt[b] = bal_req_tiles(p, b);
+  // Each request's values, read from memory once (every load of a thread
+  // issued together) and kept in LDS for the pieces below; then the tiles
+  // per request and the request-major prefix sums (wave 0, 64 requests at a
+  // time with a running carry).
+  for (int b = tid; b < B; b += kVtWaves * 64) {
+    const int qs = p.q_start[b];
+    const int L = p.q_lens ? p.q_lens[b] : p.L;
+    int blk0, nbh;   // req_head_block(p, b, 0) and the blocks per head (req_cap / 32)
+    if (p.kv_off) {
+      blk0 = p.kv_off[b];
+      nbh = (p.kv_off[b + 1] - blk0) / Hkv;
+    } else {
+      nbh = p.cap >> 5;
+      blk0 = b * Hkv * nbh;
+    }
+    int kv_end = (qs + L < 32 * nbh) ? qs + L : 32 * nbh;
+    if (kv_end < 0) kv_end = 0;
+    s_nt[b] = (kv_end + kTileKeys - 1) / kTileKeys;
+    s_qs[b] = qs;
+    s_ql[b] = L;
+    s_ke[b] = kv_end;
+    s_hb[2 * b] = blk0;
+    s_hb[2 * b + 1] = nbh;
+  }
   __syncthreads();
   if (wave == 0) {
     int carry = 0;
@@ -629,17 +648,17 @@ __device__ __forceinline__ void attn_bal_body(const AttnParams& p, unsigned char
       ++b;
       continue;
     }
-    const int h = (int)((x - pb) / nt);
+    const int h = (int)(x - pb) / nt;   // x - pb < Hkv * nt
     const long long P = pb + (long long)h * nt;   // head's first global tile
     const int ta = (int)(x - P);
     const int tb = (int)((hi < P + nt ? hi : P + nt) - P);
     int slot = lds_int(s_ps, b);
     for (int hh = 0; hh < h; ++hh) slot += bal_nparts(pb + (long long)hh * nt, nt, T, G);
     slot += w - bal_owner(P, T, G);
-    const int qs = __builtin_amdgcn_readfirstlane(p.q_start[b]);
-    const int L = __builtin_amdgcn_readfirstlane(p.q_lens ? p.q_lens[b] : p.L);
-    const int capb = __builtin_amdgcn_readfirstlane(req_cap(p, b));
-    const int kv_end = (qs + L < capb) ? qs + L : capb;
+    const int qs = lds_int(s_qs, b);
+    const int L = lds_int(s_ql, b);
+    const int kv_end = lds_int(s_ke, b);
+    const size_t hblk = (size_t)lds_int(s_hb, 2 * b) + (size_t)h * lds_int(s_hb, 2 * b + 1);
     // The four waves take consecutive shares of the piece's tiles.
     const int n = tb - ta;
     const int t0 = ta + (n * wave) / kVtWaves, t1 = ta + (n * (wave + 1)) / kVtWaves;
@@ -647,8 +666,8 @@ __device__ __forceinline__ void attn_bal_body(const AttnParams& p, unsigned char
     const int k1 = (t1 * kTileKeys < kv_end) ? t1 * kTileKeys : kv_end;
     if (!first) __syncthreads();   // the previous piece's LDS reads are done
     first = false;
-    attn_vl_piece<WT, NRG>(p, b, h, qs, L, k0, k1, p.part_o + (size_t)slot * 32 * kHD, p.part_ml + (size_t)slot * 64,
-                           lds);
+    attn_vl_piece<WT, NRG>(p, b, h, qs, L, k0, k1, hblk, p.part_o + (size_t)slot * 32 * kHD,
+                           p.part_ml + (size_t)slot * 64, lds);
     x = P + tb;
   }
 }
