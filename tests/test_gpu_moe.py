@@ -211,6 +211,7 @@ def _within_one_ulp(a, b, what):
     (16, 8, 64, 1024, 512, 64, 1.1),   # cfg5-like: hot experts with all 16 rows, a tail of 1..4
     (40, 4, 16, 512, 256, 64, 2.0),    # experts past 16 rows (several 16-row tiles)
     (3, 2, 8, 512, 256, 128, 0.0),     # group 128, one or two rows per expert
+    (32, 8, 64, 512, 256, 64, 50.0),   # every token on the same 8 experts (32 rows each), 56 experts idle
 ])
 def test_packed_expert_matmul(gpu, T, k, E, H, F, gs, zipf):
     """mtp_gather_qmv_affine4_packed (the verify step's routed experts) against

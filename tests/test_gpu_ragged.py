@@ -200,7 +200,7 @@ def _blocks_attention(ctx, lens, split_keys, seed, Hq=40, Hkv=8):
     return bf16_values(out), (q, kb, vb, q_start, lens, caps, row_off, kv_off)
 
 
-@pytest.mark.parametrize("case", ["long_among_short", "tiny_total", "single", "uniform"])
+@pytest.mark.parametrize("case", ["long_among_short", "tiny_total", "single", "uniform", "many"])
 @pytest.mark.parametrize("split_keys", [0, 1024])
 @pytest.mark.parametrize("merge", ["auto", "column"])
 def test_block_attention_balanced_shapes(gpu, case, split_keys, merge, monkeypatch):
@@ -221,6 +221,9 @@ def test_block_attention_balanced_shapes(gpu, case, split_keys, merge, monkeypat
         ctx, lens = [3, 0], [2, 4]
     elif case == "single":
         ctx, lens = [30000], [4]
+    elif case == "many":   # 130 requests: the prologue's request scans run in three rounds of 64
+        ctx = list(rng.integers(0, 400, size=130))
+        lens = list(rng.integers(1, 5, size=130))
     else:
         ctx, lens = [4093] * 4, [3] * 4
     Hq, Hkv, D = 40, 8, 128
