@@ -55,11 +55,12 @@ struct QmmRowsParams {
 __device__ __forceinline__ int xslot(int m, int kc) { return m * kQmSlotsPerRow + (kc ^ (m & 15)); }
 
 // Direct-to-LDS loads of x[0:M, 256q : 256q + 256): wave instruction t
-// covers rows 2t and 2t + 1. A row past M (odd M) loads row M - 1 into a
-// slot row that is never an output.
-__device__ __forceinline__ void qm_stage(const QmmRowsParams& p, unsigned char* buf, int q, int wave, int lane) {
+// covers rows 2t and 2t + 1, instructions spread over nw waves. A row past M
+// (odd M) loads row M - 1 into a slot row that is never an output.
+__device__ __forceinline__ void qm_stage(const QmmRowsParams& p, unsigned char* buf, int q, int wave, int nw,
+                                         int lane) {
   const int ninst = (p.M + 1) >> 1;
-  for (int t = wave; t < ninst; t += kQmWaves) {
+  for (int t = wave; t < ninst; t += nw) {
     const int m = 2 * t + (lane >> 5);
     const int mr = m < p.M ? m : p.M - 1;
     const int kc = (lane & 31) ^ (m & 15);
@@ -86,10 +87,17 @@ struct QmQuad {
 // instead of one, with the same grid.
 // RGL: 8-row register groups of the last 32-row block that are finished
 // (rows past M need no group finish): 4, or 2 when M <= 32 (R2 - 1) + 16.
-template <int R2, int EM, int KH, int RGL = 4>
-__global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams p) {
+// RS = 2 (with R2 = 2): twice the waves, each computing one of the two
+// 32-row blocks of its tile (both read the tile's weights; the second read
+// hits L2). Every output element sees the same operations in the same
+// order as with RS = 1; the waves per SIMD double, which hides more of each
+// wave's waits.
+template <int R2, int EM, int KH, int RGL = 4, int RS = 1>
+__global__ __launch_bounds__(kQmThreads * KH * RS, RS == 2 ? 4 : 1) void qmm_rows_kernel(QmmRowsParams p) {
+  static_assert(RS == 1 || (RS == 2 && R2 == 2), "row split: two 32-row blocks");
   constexpr bool dual = EM == E_DUAL_SWIGLU;
   constexpr int ROWS = 32 * R2;
+  constexpr int NR2 = R2 / RS;   // row blocks per wave
   constexpr int XBUF = ROWS * kQmSlotsPerRow * 16;   // bytes of one staged quad
   // Dynamic LDS: staged x quads [2][KH], then their group sums [2][KH][4][ROWS].
   extern __shared__ __align__(16) unsigned char qm_lds[];
@@ -100,8 +108,11 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kh = wave / kQmWaves;   // K half of this wave
-  const int wt = wave % kQmWaves;   // the wave's tile slot in the group
+  const int rs = wave / (kQmWaves * KH);         // row-block share of this wave
+  const int wk = wave - rs * (kQmWaves * KH);
+  const int kh = wk / kQmWaves;                  // K half of this wave
+  const int wt = wk % kQmWaves;                  // the wave's tile slot in the group
+  const int rb0 = rs * NR2;                      // first 32-row block of this wave
   const int c32 = lane & 31, kq = lane >> 5;
   const int M = p.M, Q = p.Q;
 
@@ -140,18 +151,19 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
     r.sb = *reinterpret_cast<const uint4*>(sl + off);
   };
 
-  f32x16 acc[R2];
+  // acc[r2]: row block rb0 + r2.
+  f32x16 acc[NR2];
 #pragma unroll
-  for (int r2 = 0; r2 < R2; ++r2)
+  for (int r2 = 0; r2 < NR2; ++r2)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r2][r] = 0.f;
 
-  // A-operand LDS byte offsets of this lane, per row block: row 32 r2 + c32,
-  // chunk kc = 8u + 4 kq + ii of the quad.
-  int arow[R2];
+  // A-operand rows of this lane, per row block: row 32 (rb0 + r2) + c32
+  // (chunk kc = 8u + 4 kq + ii of the quad).
+  int arow[NR2];
 #pragma unroll
-  for (int r2 = 0; r2 < R2; ++r2) {
-    const int m = 32 * r2 + c32;
+  for (int r2 = 0; r2 < NR2; ++r2) {
+    const int m = 32 * (rb0 + r2) + c32;
     arow[r2] = m < M ? m : (M - 1);
   }
 
@@ -170,15 +182,16 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
     for (int pp = 0; pp < 2; ++pp) {
       const float cbk = kq ? cb[2 * pp + 1] : cb[2 * pp];
 #pragma unroll
-      for (int r2 = 0; r2 < R2; ++r2)
-        acc[r2] = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[buf][kh][2 * pp + kq][32 * r2 + c32], cbk, acc[r2], 0, 0, 0);
+      for (int r2 = 0; r2 < NR2; ++r2)
+        acc[r2] = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[buf][kh][2 * pp + kq][32 * (rb0 + r2) + c32], cbk, acc[r2],
+                                                       0, 0, 0);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const uint32_t wv[4] = {r.w[u].x, r.w[u].y, r.w[u].z, r.w[u].w};
-      f32x16 G[R2];
+      f32x16 G[NR2];
 #pragma unroll
-      for (int r2 = 0; r2 < R2; ++r2)
+      for (int r2 = 0; r2 < NR2; ++r2)
 #pragma unroll
         for (int i = 0; i < 16; ++i) G[r2][i] = 0.f;
 #pragma unroll
@@ -186,18 +199,18 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
         const bf16x8 b = nibbles_to_bf16(wv[ii], nc);
         const int kc = 8 * u + 4 * kq + ii;
 #pragma unroll
-        for (int r2 = 0; r2 < R2; ++r2) {
+        for (int r2 = 0; r2 < NR2; ++r2) {
           const bf16x8 a = *reinterpret_cast<const bf16x8*>(xb + 16 * xslot(arow[r2], kc));
           G[r2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, G[r2], 0, 0, 0);
         }
       }
 #pragma unroll
-      for (int r2 = 0; r2 < R2; ++r2) {
+      for (int r2 = 0; r2 < NR2; ++r2) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          // Rows 32 r2 + 8 j .. + 7 of register group j: groups past the
-          // last RGL of the last row block hold no output row (M <= 32 (R2 - 1) + 8 RGL).
-          if (r2 == R2 - 1 && j >= RGL) continue;
+          // Rows 32 (rb0 + r2) + 8 j .. + 7 of register group j: groups past
+          // the last RGL of the last row block hold no output row (M <= 32 (R2 - 1) + 8 RGL).
+          if (rb0 + r2 == R2 - 1 && j >= RGL) continue;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = 4 * j + i;
@@ -209,14 +222,16 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
   };
 
   // Group sums of staged quad `buf` of each half: thread t < 4M of half h
-  // sums row t % M, group t / M (4M <= the half's threads: one sum at most,
-  // its row and group fixed for the whole launch).
+  // (among the waves of row share 0) sums row t % M, group t / M (4M <= the
+  // half's threads: one sum at most, its row and group fixed for the whole
+  // launch).
   const int gs_t = tid % kQmThreads;
   const int gs_u = gs_t / M, gs_m = gs_t - (gs_t / M) * M;
   auto group_sums = [&](int buf, int c) {
     typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     const bf16x2_t one2 = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
-    const int h = tid / kQmThreads;
+    const int h = kh;
+    if (rs != 0) return;
     if (c >= (h ? q_n - h0 : h0)) return;   // this half has no quad c
     if (gs_t < 4 * M) {
       const int u = gs_u, m = gs_m;
@@ -235,7 +250,8 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
 
   // Prologue: each half's quad 0 of x, then its first two weight quads.
   QmQuad ring0, ring1;
-  if (h_n > 0) qm_stage(p, xbuf(0, kh), h_lo, wt, lane);
+  const int sw = rs * kQmWaves + wt;   // this wave's index among its half's RS * 4 staging waves
+  if (h_n > 0) qm_stage(p, xbuf(0, kh), h_lo, sw, kQmWaves * RS, lane);
   load_quad(ring0, 0);
   load_quad(ring1, 1);
   // One step: quad c of each half from ring slot `cur` and x buffer c & 1;
@@ -246,7 +262,7 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(5));
     lds_barrier();   // every wave's x loads of quad c are in LDS
     group_sums(c & 1, c);
-    if (c + 1 < h_n) qm_stage(p, xbuf((c + 1) & 1, kh), h_lo + c + 1, wt, lane);
+    if (c + 1 < h_n) qm_stage(p, xbuf((c + 1) & 1, kh), h_lo + c + 1, sw, kQmWaves * RS, lane);
     lds_barrier();   // group sums visible; buffer (c+1)&1 was last read before the first barrier
     if (c < h_n) compute(cur, c & 1);
     load_quad(cur, c + 2);
@@ -265,23 +281,23 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
     __syncthreads();   // every wave is done with the staged x
     if (kh == 1) {
 #pragma unroll
-      for (int r2 = 0; r2 < R2; ++r2)
+      for (int r2 = 0; r2 < NR2; ++r2)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) red[(wt * R2 * 16 + r2 * 16 + r) * 64 + lane] = acc[r2][r];
+        for (int r = 0; r < 16; ++r) red[(wt * R2 * 16 + (rb0 + r2) * 16 + r) * 64 + lane] = acc[r2][r];
     }
     __syncthreads();
     if (kh == 0) {
 #pragma unroll
-      for (int r2 = 0; r2 < R2; ++r2)
+      for (int r2 = 0; r2 < NR2; ++r2)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r2][r] += red[(wt * R2 * 16 + r2 * 16 + r) * 64 + lane];
+        for (int r = 0; r < 16; ++r) acc[r2][r] += red[(wt * R2 * 16 + (rb0 + r2) * 16 + r) * 64 + lane];
     }
   }
   const bool owner = kh == 0;   // the waves that hold the finished sums
 
-  // Output element of acc[r2][r]: row 32 r2 + 8 (r / 4) + 4 kq + r % 4,
+  // Output element of acc[r2][r]: row 32 (rb0 + r2) + 8 (r / 4) + 4 kq + r % 4,
   // column 32 ct + c32.
-  auto row_of = [&](int r2, int r) { return 32 * r2 + 8 * (r >> 2) + 4 * kq + (r & 3); };
+  auto row_of = [&](int r2, int r) { return 32 * (rb0 + r2) + 8 * (r >> 2) + 4 * kq + (r & 3); };
 
   if (split) {
     // This part's sums, device-coherent, in register order; the last part to
@@ -290,10 +306,10 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
     float* mine = p.partial + (((size_t)eg * p.split + part) * kQmWaves + wt) * (R2 * 16 * 64);
     if (owner) {
 #pragma unroll
-      for (int r2 = 0; r2 < R2; ++r2)
+      for (int r2 = 0; r2 < NR2; ++r2)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          __hip_atomic_store(mine + (r2 * 16 + r) * 64 + lane, acc[r2][r], __ATOMIC_RELAXED,
+          __hip_atomic_store(mine + ((rb0 + r2) * 16 + r) * 64 + lane, acc[r2][r], __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -306,19 +322,20 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
     if (!s_last) return;
     if (owner) {
 #pragma unroll
-      for (int r2 = 0; r2 < R2; ++r2)
+      for (int r2 = 0; r2 < NR2; ++r2)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r2][r] = 0.f;
       for (int pp = 0; pp < p.split; ++pp) {
         const float* src = p.partial + (((size_t)eg * p.split + pp) * kQmWaves + wt) * (R2 * 16 * 64);
-        float v[R2][16];
+        float v[NR2][16];
 #pragma unroll
-        for (int r2 = 0; r2 < R2; ++r2)
+        for (int r2 = 0; r2 < NR2; ++r2)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            v[r2][r] = __hip_atomic_load(src + (r2 * 16 + r) * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            v[r2][r] = __hip_atomic_load(src + ((rb0 + r2) * 16 + r) * 64 + lane, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
-        for (int r2 = 0; r2 < R2; ++r2)
+        for (int r2 = 0; r2 < NR2; ++r2)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[r2][r] += v[r2][r];
       }
@@ -333,19 +350,19 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
     __syncthreads();
     if (owner && mat == 1) {
 #pragma unroll
-      for (int r2 = 0; r2 < R2; ++r2)
+      for (int r2 = 0; r2 < NR2; ++r2)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ex[((wt & 1) * R2 * 16 + r2 * 16 + r) * 64 + lane] = acc[r2][r];
+        for (int r = 0; r < 16; ++r) ex[((wt & 1) * R2 * 16 + (rb0 + r2) * 16 + r) * 64 + lane] = acc[r2][r];
     }
     __syncthreads();
     if (owner && mat == 0 && has_tile && col < p.N) {
 #pragma unroll
-      for (int r2 = 0; r2 < R2; ++r2)
+      for (int r2 = 0; r2 < NR2; ++r2)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int m = row_of(r2, r);
           if (m < M) {
-            const float up = ex[((wt & 1) * R2 * 16 + r2 * 16 + r) * 64 + lane];
+            const float up = ex[((wt & 1) * R2 * 16 + (rb0 + r2) * 16 + r) * 64 + lane];
             const float gsl = round_bf(silu_f(round_bf(acc[r2][r])));
             p.y[(size_t)m * p.ldy + col] = f2bf(gsl * round_bf(up));
           }
@@ -355,7 +372,7 @@ __global__ __launch_bounds__(kQmThreads * KH) void qmm_rows_kernel(QmmRowsParams
   }
   if (!owner || !has_tile || col >= p.N) return;
 #pragma unroll
-  for (int r2 = 0; r2 < R2; ++r2)
+  for (int r2 = 0; r2 < NR2; ++r2)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int m = row_of(r2, r);
@@ -376,6 +393,31 @@ static size_t rows_lds_bytes(int R2, int KH) {
   const size_t stage = 2 * KH * xbuf + (size_t)2 * KH * 4 * 32 * R2 * sizeof(float);
   const size_t red = (size_t)kQmWaves * R2 * 16 * 64 * sizeof(float);   // the halves' reduction / the pair's exchange
   return stage > red ? stage : red;
+}
+
+// One launch of qmm_rows_kernel: KH K halves per workgroup, and with two row
+// blocks (R2 = 2) optionally one row block per wave (RS = 2). A failure of
+// the attribute call surfaces as a launch error, checked by the caller.
+template <int R2, int EM, int RGL>
+static void launch_rows(const QmmRowsParams& p, int grid, int kh, int rsplit, hipStream_t st) {
+  const size_t lds = rows_lds_bytes(R2, kh);
+  auto go = [&](auto kern, int threads) {
+    if (lds > 65536) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(threads), lds, st, p);
+  };
+  if constexpr (R2 == 2) {
+    if (rsplit) {
+      if (kh == 2)
+        go(qmm_rows_kernel<2, EM, 2, RGL, 2>, 4 * kQmThreads);
+      else
+        go(qmm_rows_kernel<2, EM, 1, RGL, 2>, 2 * kQmThreads);
+      return;
+    }
+  }
+  if (kh == 2)
+    go(qmm_rows_kernel<R2, EM, 2, RGL>, 2 * kQmThreads);
+  else
+    go(qmm_rows_kernel<R2, EM, 1, RGL>, kQmThreads);
 }
 
 struct RowsPlan {
@@ -501,28 +543,21 @@ MTP_API int mtp_qmm_affine4_mfma(const mtp_qmm_args* a, void* stream) {
   // vs 193 us with two halves).
   const int kh_env = env_int_rows("MTPLX_AMD_QMM_HALVES", 0);
   const int kh = kh_env == 1 || kh_env == 2 ? kh_env : (grid <= device_cus() ? 2 : 1);
-#define MTP_ROWS(R2v, EMv, RGLv)                                                                          \
-  do {                                                                                                    \
-    const size_t lds = rows_lds_bytes(R2v, kh);                                                           \
-    if (kh == 2) {                                                                                        \
-      auto k = qmm_rows_kernel<R2v, EMv, 2, RGLv>;                                                        \
-      if (lds > 65536) (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, \
-                                                 (int)lds);                                               \
-      hipLaunchKernelGGL(k, dim3(grid), dim3(2 * kQmThreads), lds, st, p);                                \
-    } else {                                                                                              \
-      auto k = qmm_rows_kernel<R2v, EMv, 1, RGLv>;                                                        \
-      if (lds > 65536) (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, \
-                                                 (int)lds);                                               \
-      hipLaunchKernelGGL(k, dim3(grid), dim3(kQmThreads), lds, st, p);                                    \
-    }                                                                                                     \
-  } while (0)
+  // Past 32 rows each wave takes one 32-row block (MTPLX_AMD_QMM_ROWSPLIT=0:
+  // both blocks per wave).
+  const int rsplit = env_int_rows("MTPLX_AMD_QMM_ROWSPLIT", 1) != 0;
   if (M > 48) {
-    if (em == E_STORE) MTP_ROWS(2, E_STORE, 4); else if (em == E_RESID) MTP_ROWS(2, E_RESID, 4); else MTP_ROWS(2, E_DUAL_SWIGLU, 4);
+    if (em == E_STORE) launch_rows<2, E_STORE, 4>(p, grid, kh, rsplit, st);
+    else if (em == E_RESID) launch_rows<2, E_RESID, 4>(p, grid, kh, rsplit, st);
+    else launch_rows<2, E_DUAL_SWIGLU, 4>(p, grid, kh, rsplit, st);
   } else if (M > 32) {
-    if (em == E_STORE) MTP_ROWS(2, E_STORE, 2); else if (em == E_RESID) MTP_ROWS(2, E_RESID, 2); else MTP_ROWS(2, E_DUAL_SWIGLU, 2);
+    if (em == E_STORE) launch_rows<2, E_STORE, 2>(p, grid, kh, rsplit, st);
+    else if (em == E_RESID) launch_rows<2, E_RESID, 2>(p, grid, kh, rsplit, st);
+    else launch_rows<2, E_DUAL_SWIGLU, 2>(p, grid, kh, rsplit, st);
   } else {
-    if (em == E_STORE) MTP_ROWS(1, E_STORE, 4); else if (em == E_RESID) MTP_ROWS(1, E_RESID, 4); else MTP_ROWS(1, E_DUAL_SWIGLU, 4);
+    if (em == E_STORE) launch_rows<1, E_STORE, 4>(p, grid, kh, 0, st);
+    else if (em == E_RESID) launch_rows<1, E_RESID, 4>(p, grid, kh, 0, st);
+    else launch_rows<1, E_DUAL_SWIGLU, 4>(p, grid, kh, 0, st);
   }
-#undef MTP_ROWS
   return launch_check(who);
 }
