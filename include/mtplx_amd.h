@@ -137,7 +137,7 @@ int mtp_qmv_affine4_rmsnorm_dual(const void* x, const void* norm_w, const float*
 size_t mtp_pack_affine4_bytes(int N, int K);
 int mtp_pack_affine4(const void* w, const void* scales, const void* biases, void* out, int N, int K, int group_size,
                      void* stream);
-/* Layout 2, the same size, for M <= 4 on the 16x16x32 MFMA (packed = 2 in
+/* Layout 2, the same size, for M <= 16 on the 16x16x32 MFMA (packed = 2 in
  * mtp_qmv_args): in block (t, q), load u = 64-group u of the quad, and lane l
  * gets word jj = 2kk + h = word 8u + 4kk + l/16 of row 32t + 16h + l%16;
  * nibble order and the scale/bias words as in layout 1. No reference
@@ -152,7 +152,7 @@ int mtp_pack_affine4_mf16(const void* w, const void* scales, const void* biases,
  * emode: 0 = store (y0 bf16, or yf fp32 when set), 1 = + resid (ss_out
  * optional), 2 = two outputs (w1 -> y1), 3 = silu(x@W0^T)*(x@W1^T).
  * packed = 1: w0/w1 come from mtp_pack_affine4 (s0/b0/s1/b1 unused);
- * packed = 2: from mtp_pack_affine4_mf16, M <= 4 only (16x16x32 MFMA).
+ * packed = 2: from mtp_pack_affine4_mf16, M <= 16 only (16x16x32 MFMA).
  * ldx/ldy <= 0 mean K/N.
  * ws/ws_bytes: with packed weights, a workspace of mtp_qmv_workspace_bytes
  * (256-byte aligned, zeroed once before first use and then left to the

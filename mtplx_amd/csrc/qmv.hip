@@ -144,8 +144,8 @@ static int qmm_check(int xm, int em, const QmmParams& p, const char* who) {
     set_error("%s: packed=%d (0 = MLX layout, 1, 2 = packed layouts)", who, p.packed);
     return MTP_ERR_ARG;
   }
-  if (p.packed == 2 && p.M > 4) {
-    set_error("%s: packed layout 2 (16x16x32) serves M <= 4 only (M=%d)", who, p.M);
+  if (p.packed == 2 && p.M > 16) {
+    set_error("%s: packed layout 2 (16x16x32) serves M <= 16 only (M=%d)", who, p.M);
     return MTP_ERR_UNSUPPORTED;
   }
   if (em == E_ROPE_QKV) {

@@ -493,6 +493,33 @@ __device__ __forceinline__ void quad_mma16(const unsigned char* lds, uint32_t a0
   }
 }
 
+// The same quad on up to 16 rows (x row m at A row m): lane l's output
+// register i is row 4(l/16) + i of columns l%16 (t0) and 16 + l%16 (t1), and
+// its four rows' group sums are one float4 at x_off + g * xsw * 4.
+__device__ __forceinline__ void quad_mma16x16(const unsigned char* lds, uint32_t a0, uint32_t a1, uint32_t x_off,
+                                              int xsw, const uint4 (&w)[4], const float (&s0)[4],
+                                              const float (&cb0)[4], const float (&s1)[4], const float (&cb1)[4],
+                                              NibConsts nc, float (&t0)[4], float (&t1)[4]) {
+  typedef float f32x4_t __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const bf16x8 A0 = *reinterpret_cast<const bf16x8*>(lds + a0 + g * 128);
+    const bf16x8 A1 = *reinterpret_cast<const bf16x8*>(lds + a1 + g * 128);
+    f32x4_t G0 = {}, G1 = {};
+    G0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, nibbles_to_bf16(w[g].x, nc), G0, 0, 0, 0);
+    G1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, nibbles_to_bf16(w[g].y, nc), G1, 0, 0, 0);
+    G0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, nibbles_to_bf16(w[g].z, nc), G0, 0, 0, 0);
+    G1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, nibbles_to_bf16(w[g].w, nc), G1, 0, 0, 0);
+    const float4 xv = *reinterpret_cast<const float4*>(lds + x_off + g * xsw * 4);
+    const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      t0[i] = fmaf(s0[g], G0[i], fmaf(cb0[g], xa[i], t0[i]));
+      t1[i] = fmaf(s1[g], G1[i], fmaf(cb1[g], xa[i], t1[i]));
+    }
+  }
+}
+
 // Second producer input of the chunk at (row offset xo, column k): the up
 // half for SwiGLU, the norm weight for RMSNorm, nothing otherwise.
 template <int XM>

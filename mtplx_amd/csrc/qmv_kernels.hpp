@@ -474,7 +474,10 @@ static int env_int(const char* name, int dflt) {
   return (v && *v) ? atoi(v) : dflt;
 }
 
-static int r_of(int M) { return M <= 8 ? 4 : (M <= 16 ? 8 : 16); }
+// Group-sum rows (2R) the LDS plan reserves: 5..8 rows get R = 8's, which
+// the 16x16x32 form (layout 2) uses there (the 32x32x16 form's R = 4 needs
+// less), so one plan serves both layouts.
+static int r_of(int M) { return M <= 4 ? 4 : (M <= 16 ? 8 : 16); }
 
 // LDS of the gathered (chunked) kernel: staged x per quad (4 groups x
 // (8*M*16 B + 32 floats)); the K-split reduction reuses the same area.
@@ -626,20 +629,21 @@ static bool mf_short_ring(const QmmParams& q, int nw, int em) {
   return cdiv(q.K >> 8, ks) <= 3;
 }
 
-template <int NW, int XM, int EM, int NRT>
+// R = 4: up to 4 rows; R = 8: up to 16 rows (quad_mma16x16).
+template <int NW, int R, int XM, int EM, int NRT>
 static void launch_mf(const QmmParams& q, const Plan& pl, hipStream_t st) {
-  if (!(q.tail_ok && tail_launch(qmv_stream_kernel<NW, 4, XM, EM, 0, true, true, NRT>, pl, NW * 64, st, q)))
-    launch_one(qmv_stream_kernel<NW, 4, XM, EM, 0, true, true, NRT>, pl, NW * 64, st, q);
+  if (!(q.tail_ok && tail_launch(qmv_stream_kernel<NW, R, XM, EM, 0, true, true, NRT>, pl, NW * 64, st, q)))
+    launch_one(qmv_stream_kernel<NW, R, XM, EM, 0, true, true, NRT>, pl, NW * 64, st, q);
 }
 
 template <int NW, int R, int XM, int EM, int GSH>
 static void launch_rk(const QmmParams& q, const Plan& pl, hipStream_t st) {
-  if constexpr (R == 4) {
-    if (q.packed == 2) {   // 16x16x32 layout, M <= 4 (checked by the caller)
+  if constexpr (R == 4 || R == 8) {
+    if (q.packed == 2) {   // 16x16x32 layout: M <= 4 at R = 4, M <= 16 at R = 8 (checked by the caller)
       if (mf_short_ring(q, NW, EM))
-        launch_mf<NW, XM, EM, 1>(q, pl, st);
+        launch_mf<NW, R, XM, EM, 1>(q, pl, st);
       else
-        launch_mf<NW, XM, EM, 2>(q, pl, st);
+        launch_mf<NW, R, XM, EM, 2>(q, pl, st);
       return;
     }
   }
@@ -662,7 +666,7 @@ template <int NW, int XM, int EM, int GSH>
 static void launch_n(const QmmParams& p, const Plan& pl, hipStream_t st) {
   QmmParams q = p;
   q.n_blocks = pl.n_blocks;
-  if (p.M <= 8)
+  if (p.M <= (p.packed == 2 ? 4 : 8))
     launch_rk<NW, 4, XM, EM, GSH>(q, pl, st);
   else if (p.M <= 16)
     launch_rk<NW, 8, XM, EM, GSH>(q, pl, st);
@@ -689,10 +693,21 @@ static void launch_e(int em, const QmmParams& p, const Plan& pl, hipStream_t st)
 }
 
 
-// q|k|v with the RoPE epilogue: packed weights, R = 4 (M <= 8) or 8 (M <= 16).
+// q|k|v with the RoPE epilogue: packed weights, R = 4 (M <= 8) or 8 (M <= 16);
+// layout 2: R = 4 up to 4 rows, R = 8 (16x16x32 on 16 rows) up to 16.
 template <int XM>
 static void launch_rope(const QmmParams& q, const Plan& pl, hipStream_t st) {
-  if (q.packed == 2) {
+  if (q.packed == 2 && q.M > 4) {
+    const bool sh = mf_short_ring(q, pl.nw, E_ROPE_QKV);
+    if (pl.nw == 8 && sh)
+      launch_one(qmv_stream_kernel<8, 8, XM, E_ROPE_QKV, 0, true, true, 1>, pl, 8 * 64, st, q);
+    else if (pl.nw == 8)
+      launch_one(qmv_stream_kernel<8, 8, XM, E_ROPE_QKV, 0, true, true, 2>, pl, 8 * 64, st, q);
+    else if (sh)
+      launch_one(qmv_stream_kernel<4, 8, XM, E_ROPE_QKV, 0, true, true, 1>, pl, 4 * 64, st, q);
+    else
+      launch_one(qmv_stream_kernel<4, 8, XM, E_ROPE_QKV, 0, true, true, 2>, pl, 4 * 64, st, q);
+  } else if (q.packed == 2) {
     const bool sh = mf_short_ring(q, pl.nw, E_ROPE_QKV);
     if (pl.nw == 8 && sh)
       launch_one(qmv_stream_kernel<8, 4, XM, E_ROPE_QKV, 0, true, true, 1>, pl, 8 * 64, st, q);

@@ -18,9 +18,11 @@ namespace mtp {
 // stay in flight). Lanes whose A-operand row is past M read a zero block in
 // LDS instead of branching.
 //
-// MF (packed layout 2, M <= 4): the quads run on v_mfma_f32_16x16x32_bf16
-// (quad_mma16): half the MFMA cycles of the 32x32x16 form for these 4 rows
-// and a quarter of the group-finish FMAs. Staging and epilogues are shared.
+// MF (packed layout 2, M <= 4 with R = 4, M <= 16 with R = 8): the quads run
+// on v_mfma_f32_16x16x32_bf16 (quad_mma16 / quad_mma16x16): half the MFMA
+// cycles of the 32x32x16 form, whose 32 A rows these row counts half fill,
+// and at 4 rows a quarter of the group-finish FMAs. Staging and epilogues are
+// shared.
 //
 // The body takes its block index vb and grid size vg as arguments so a
 // persistent kernel can run it as one phase of several. ``pre`` is called
@@ -83,6 +85,8 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   constexpr int KS = dual ? NW / 2 : NW;
   constexpr int XSW = 2 * R;
   constexpr int NR = NRT;
+  constexpr bool MF16 = MF && R == 8;   // up to 16 rows on the 16x16x32 form
+  static_assert(!MF || R == 4 || R == 8, "the 16x16x32 form takes R = 4 (4 rows) or 8 (16 rows)");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar loop control
@@ -214,10 +218,13 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
   // MF: A row 4m holds x row m, read by lanes with (l%16) = 4m (the other
   // lanes of each four read a valid row too; their outputs are unused).
-  const int mf_arow = ((lane & 15) >> 2) < M ? ((lane & 15) >> 2) : 0;
+  // MF16: A row m holds x row m (rows past M read row 0, outputs unused), and
+  // lane l's group sums are those of rows 4(l/16) .. + 3 (zero past M).
+  const int mf_arow = MF16 ? ((lane & 15) < M ? (lane & 15) : 0) : (((lane & 15) >> 2) < M ? ((lane & 15) >> 2) : 0);
   const uint32_t mf_a0 = (uint32_t)xa_index(0, mf_arow, M, rstride, 0, lane >> 4) * 16;
   const uint32_t mf_a1 = (uint32_t)xa_index(1, mf_arow, M, rstride, 0, lane >> 4) * 16;
-  const uint32_t mf_x = (uint32_t)((unsigned char*)xs - smem) + 4 * ((lane >> 4) < M ? (lane >> 4) : 0);
+  const uint32_t mf_x = (uint32_t)((unsigned char*)xs - smem) +
+                        (MF16 ? 16 * (lane >> 4) : 4 * ((lane >> 4) < M ? (lane >> 4) : 0));
 
   auto compute = [&](const QuadRegs& cr, int t) {
     const int gq = 4 * (kw + t * KS);
@@ -227,8 +234,15 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
       float sv1[4], cb1[4];
       const uint32_t s1w[2] = {cr.s1[0], cr.s1[MF ? 1 : 0]}, b1w[2] = {cr.b1[0], cr.b1[MF ? 1 : 0]};
       quad_scales<0>(s1w, b1w, sv1, cb1);
-      quad_mma16(smem, mf_a0 + (uint32_t)gq * 128, mf_a1 + (uint32_t)gq * 128, mf_x + (uint32_t)gq * (XSW * 4), XSW,
-                 cr.w, sv, cb, sv1, cb1, nc, acc[0], acc[1]);
+      if constexpr (MF16) {
+        float (&t0)[4] = *reinterpret_cast<float (*)[4]>(&acc[0]);
+        float (&t1)[4] = *reinterpret_cast<float (*)[4]>(&acc[MF16 ? 4 : 0]);
+        quad_mma16x16(smem, mf_a0 + (uint32_t)gq * 128, mf_a1 + (uint32_t)gq * 128,
+                      mf_x + (uint32_t)gq * (XSW * 4), XSW, cr.w, sv, cb, sv1, cb1, nc, t0, t1);
+      } else {
+        quad_mma16(smem, mf_a0 + (uint32_t)gq * 128, mf_a1 + (uint32_t)gq * 128, mf_x + (uint32_t)gq * (XSW * 4),
+                   XSW, cr.w, sv, cb, sv1, cb1, nc, acc[0], acc[1]);
+      }
     } else {
       quad_mma<R>(smem, a_lane + (uint32_t)gq * 128, x_lane + (uint32_t)gq * (XSW * 4), cr.w, sv, cb, nc, acc);
     }
@@ -258,7 +272,19 @@ __device__ __forceinline__ void qmv_stream_body(const QmmParams& p, const int vb
     const int nb = tile0 + j * G;
     const bool valid = nb * 32 + c32 < p.N;
     lds_barrier();
-    if constexpr (MF) {   // lane l: row l/16, columns l%16 and 16 + l%16
+    if constexpr (MF16) {   // lane l: rows 4(l/16) + i, columns l%16 (acc[i]) and 16 + l%16 (acc[4 + i])
+      const int c = lane & 15;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = 4 * (lane >> 4) + i;
+        if (m < M) {
+          red[(wave * M + m) * 32 + c] = (nb * 32 + c < p.N) ? acc[i] : 0.f;
+          red[(wave * M + m) * 32 + 16 + c] = (nb * 32 + 16 + c < p.N) ? acc[4 + i] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    } else if constexpr (MF) {   // lane l: row l/16, columns l%16 and 16 + l%16
       const int m = lane >> 4, c = lane & 15;
       if (m < M) {
         red[(wave * M + m) * 32 + c] = (nb * 32 + c < p.N) ? acc[0] : 0.f;

@@ -25,12 +25,12 @@ class QuantizedLinear:
         self.mode = mode
         self.bias = bias
         self.packed: torch.Tensor | None = None         # layout 1 (any M)
-        self.packed_mf16: torch.Tensor | None = None    # layout 2 (M <= 4)
+        self.packed_mf16: torch.Tensor | None = None    # layout 2 (M <= 16)
         self._shape = tuple(int(d) for d in self.weight.shape)   # kept when the source is released
 
     def pack(self, row_order: torch.Tensor | None = None, layout: int = 1) -> torch.Tensor:
         """Tile-major copy of the weights for the streaming kernel. ``layout``
-        1 serves any M (``packed=1``); 2 is the 16x16x32-MFMA order for M <= 4
+        1 serves any M (``packed=1``); 2 is the 16x16x32-MFMA order for M <= 16
         (``packed=2``). Without ``row_order`` each layout is made once and
         cached; with it, packed row i is original row ``row_order[i]`` (e.g.
         :func:`rope_row_order`)."""

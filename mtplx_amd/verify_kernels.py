@@ -12,7 +12,7 @@ Kernels, by rows M (4-bit groups of 64/128 with K % 256 == 0):
 
 * M <= 32: ``mtp_qmv_affine4_ex`` (the streaming kernel: 1 KB contiguous
   weight loads per wave, the leftover tiles split by K over all CUs) on a
-  tile-major pack of the triple, layout 2 (the 16x16x32 MFMA form) up to 4
+  tile-major pack of the triple, layout 2 (the 16x16x32 MFMA form) up to 16
   rows and layout 1 beyond, packed once and kept like the M > 32 pack
   (cfg1 shape: 15.7 against 25.5 us for ``mtp_qmv_affine4`` on the MLX
   layout, which runs when ``MTPLX_AMD_PACK_CACHE=0``);
@@ -139,7 +139,7 @@ def layout1_pack(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, gr
 
 def layout2_pack(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int) -> torch.Tensor:
     """The layout-2 copy (``mtp_pack_affine4_mf16``, the 16x16x32 MFMA order
-    for up to 4 rows) of a 4-bit MLX triple, kept as :func:`layout1_pack`
+    for up to 16 rows) of a 4-bit MLX triple, kept as :func:`layout1_pack`
     keeps its own."""
     return _cached_pack(w, scales, biases, group_size, 2)
 
@@ -185,7 +185,7 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
         _lib.call("mtp_qmv_affine4", x2.data_ptr(), w.data_ptr(), scales.data_ptr(), biases.data_ptr(), y.data_ptr(),
                   m, n, k, group_size, None, 0, st)
         return y.reshape(*lead, n)
-    lay = 2 if m <= 4 else 1
+    lay = 2 if m <= 16 else 1
     pack = layout2_pack(w, scales, biases, group_size) if lay == 2 else layout1_pack(w, scales, biases, group_size)
     ws = _lib.WORKSPACES.get(max(256, _lib.query("mtp_qmv_workspace_bytes", m, n, k, 1)), "verify_qmv", x.device)
     _lib.qmv_ex(st, x=x2, w0=pack, y0=y, M=m, N=n, K=k, group_size=int(group_size), xmode=0, emode=0, packed=lay,

@@ -28,17 +28,17 @@ def _affine4(module: Any) -> bool:
 
 def _packed(module: QuantizedLinear, m: int) -> tuple[torch.Tensor, int] | None:
     """The module's tile-major pack for ``m`` rows: layout 2 (the 16x16x32
-    MFMA form) at up to 4 rows, else layout 1, or None. A pack reads the
+    MFMA form) at up to 16 rows, else layout 1, or None. A pack reads the
     weights as 1 KB contiguous runs per wave load (cfg1 shape: 15.7 us
     against 25.5 us on the MLX layout, whose per-lane row reads scatter), so
     a module that still holds its MLX triple is packed for the layout on its
     first call and keeps it (unless ``MTPLX_AMD_PACK_CACHE=0``); a released
     module serves the layout it has."""
-    if m <= 4 and module.packed_mf16 is not None:
+    if m <= 16 and module.packed_mf16 is not None:
         return module.packed_mf16, 2
     can_pack = module.weight is not None and fast_path(module.bits, module.group_size, module.in_features) and \
         _pack_cache_enabled()
-    if m <= 4 and can_pack:
+    if m <= 16 and can_pack:
         return module.pack(layout=2), 2
     if module.packed is not None:
         return module.packed, 1

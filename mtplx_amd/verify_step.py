@@ -50,6 +50,10 @@ EXACT_SPLIT_KEYS = 1024
 # MoE layers run the 5+-row experts and the shared expert on a second stream
 # beside the 1-4-row experts (MTPLX_AMD_MOE_SIDE_STREAM=0: one stream).
 MOE_SIDE_STREAM = (os.environ.get("MTPLX_AMD_MOE_SIDE_STREAM") or "1").strip() not in {"0", "false", "off", "no"}
+# Rows up to which the dense projections take packed layout 2 (the
+# 16x16x32 MFMA form, at most 16; MTPLX_AMD_LAYOUT2_ROWS=4 keeps 5..16 rows on
+# layout 1's 32x32x16 form).
+LAYOUT2_ROWS = min(16, int(os.environ.get("MTPLX_AMD_LAYOUT2_ROWS") or "16"))
 
 
 def qmv_ws_bytes(M: int, c: "DecoderConfig") -> int:
@@ -235,7 +239,7 @@ class VerifyModel:
     def _finish_init(self) -> None:
         c = self.cfg
         # Tile-major copies for the streaming verify matmul (one pass at load
-        # time), in layout 1 (any M) and layout 2 (M <= 4, 16x16x32 MFMA);
+        # time), in layout 1 (any M) and layout 2 (M <= 16, 16x16x32 MFMA);
         # q|k|v also in RoPE tile order for the fused RoPE epilogue.
         rope_order = rope_row_order(c.n_heads + 2 * c.n_kv_heads, c.head_dim)
         for L in self.layers:
@@ -424,7 +428,7 @@ class VerifyModel:
 
         # The RoPE epilogue covers up to 16 rows with all of x in LDS.
         fused_rope = bool(_lib.query("mtp_qmv_rope_fusable", M, c.qkv_out, H))
-        lay = 2 if M <= 4 else 1   # layout 2: the 16x16x32 MFMA form for up to 4 rows
+        lay = 2 if M <= LAYOUT2_ROWS else 1   # layout 2: the 16x16x32 MFMA form for up to 16 rows
 
         def W(q):
             return q.packed_mf16 if lay == 2 else q.packed

@@ -1,4 +1,5 @@
-"""GPU parity: packed layout 2 and its 16x16x32-MFMA quad (M <= 4).
+"""GPU parity: packed layout 2 and its 16x16x32-MFMA quads (M <= 4, and up
+to 16 rows with x row m at A row m).
 
 The layout is pinned bit-for-bit by a NumPy restatement. The matmul computes
 the same per-group sums as layout 1, with the MFMA summing each 32-k step in
@@ -62,6 +63,14 @@ CASES = [  # m, n, k, xmode, emode, use_ws
     (3, 300, 768, 2, 0, False),
     (2, 640, 512, 0, 3, False),
     (4, 151936 // 8, 5120, 2, 0, True),
+    # 5..16 rows: every A row a row of x, four output rows per lane
+    (16, 4096, 4096, 2, 3, True),     # cfg5-width fused norm + gate/up + SwiGLU, tail split
+    (16, 4096, 4096, 0, 1, True),     # cfg5-width o_proj + residual
+    (9, 4096, 1536, 0, 1, False),     # down width of an expert, 9 rows
+    (5, 300, 768, 2, 0, False),
+    (12, 640, 512, 0, 3, False),
+    (16, 1000, 1024, 0, 0, False),
+    (8, 5120, 17408, 0, 0, True),     # x beyond LDS: full K split
 ]
 
 
@@ -117,24 +126,26 @@ def test_layout2_matches_layout1_and_oracle(gpu, m, n, k, xmode, emode, use_ws):
         assert_close(a, want, what=f"layout 2 M={m} N={n} K={k} x{xmode} e{emode}")
 
 
-def test_layout2_rope_epilogue_and_limits(gpu):
+@pytest.mark.parametrize("B", [1, 4])
+def test_layout2_rope_epilogue_and_limits(gpu, B):
     """The RoPE epilogue on layout 2 equals the layout-2 q|k|v matmul plus the
-    RoPE writer, bit for bit; M > 4 is refused."""
+    RoPE writer, bit for bit, at 4 rows and at 16 (4 requests); M > 16 is
+    refused."""
     from mtplx_amd import _lib
     from mtplx_amd.quant import QuantizedLinear, rope_row_order
-    B, L, Hq, Hkv, D, K, cap = 1, 4, 8, 2, 128, 1024, 256
+    L, Hq, Hkv, D, K, cap = 4, 8, 2, 128, 1024, 256
     M, N = B * L, (Hq + 2 * Hkv) * D
     g = torch.Generator(device="cuda").manual_seed(3)
     q = QuantizedLinear.random(N, K, 64, generator=g)
     x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
     nw = (1 + 0.1 * torch.randn(K, device="cuda", generator=g)).to(torch.bfloat16)
-    qs = torch.tensor([100], dtype=torch.int32, device="cuda")
+    qs = torch.tensor([100 + 7 * b for b in range(B)], dtype=torch.int32, device="cuda")
 
     def bufs():
         return (torch.zeros((B, Hq, L, D), dtype=torch.bfloat16, device="cuda"),
                 torch.zeros((B, Hkv, cap, D), dtype=torch.bfloat16, device="cuda"),
                 torch.zeros((B, Hkv, cap, D), dtype=torch.bfloat16, device="cuda"),
-                torch.zeros(1, dtype=torch.int32, device="cuda"))
+                torch.zeros(B, dtype=torch.int32, device="cuda"))
     qo0, kc0, vc0, st0 = bufs()
     qkv = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     _lib.qmv_ex(_st(), x=x, x2=nw, eps=1e-6, w0=q.pack(layout=2), y0=qkv, M=M, N=N, K=K, group_size=64, xmode=2,
@@ -150,8 +161,8 @@ def test_layout2_rope_epilogue_and_limits(gpu):
     assert torch.equal(qo0.view(torch.int16), qo1.view(torch.int16))
     assert torch.equal(kc0.view(torch.int16), kc1.view(torch.int16))
     assert torch.equal(vc0.view(torch.int16), vc1.view(torch.int16))
-    x8 = torch.zeros((8, K), dtype=torch.bfloat16, device="cuda")
-    y8 = torch.empty((8, N), dtype=torch.bfloat16, device="cuda")
+    x17 = torch.zeros((17, K), dtype=torch.bfloat16, device="cuda")
+    y17 = torch.empty((17, N), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(_lib.MtpError) as e:
-        _lib.qmv_ex(_st(), x=x8, w0=q.pack(layout=2), y0=y8, M=8, N=N, K=K, group_size=64, packed=2)
+        _lib.qmv_ex(_st(), x=x17, w0=q.pack(layout=2), y0=y17, M=17, N=N, K=K, group_size=64, packed=2)
     assert e.value.code == -2
