@@ -398,6 +398,17 @@ int mtp_gather_qmv_affine4_packed_rows(const void* x, const uint32_t* row_map, c
                                        int N, int K, int group_size, int emode, int rows_per_expert, int row_class,
                                        void* stream);
 
+/* mtp_gather_qmv_affine4_packed_rows over the layout-2 pack
+ * (mtp_pack_affine4_mf16) of the same [E * rows_per_expert, K] matrix: the
+ * 16x16x32 MFMA quads, in the 4-row form for the 1-4-row class and the
+ * 16-row form for 16-row tiles. Same arguments and outputs. Replaces the same
+ * reference call sites (mtplx/moe_sorted_gather.py:241, :288;
+ * mtplx/models/qwen4_exp.py:1544-1577). */
+int mtp_gather_qmv_affine4_packed_mf16(const void* x, const uint32_t* row_map, const int32_t* expert_off,
+                                       const int32_t* active, const void* wp, void* y, int max_rows_per_expert, int E,
+                                       int N, int K, int group_size, int emode, int rows_per_expert, int row_class,
+                                       void* stream);
+
 /* Expert offsets int32 [E+1] and the active list [1+E] (as mtp_moe_sort
  * writes them) from ids already sorted ascending, the sorted_indices of the
  * reference entry points (mtplx/moe_sorted_gather.py:241 gather_qmm_rows,

@@ -60,6 +60,7 @@ SIGNATURES = {
                                     _i, _i, _i, _i, _vp, _sz, _vp]),
     "mtp_gather_qmv_affine4_packed": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
     "mtp_gather_qmv_affine4_packed_rows": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "mtp_gather_qmv_affine4_packed_mf16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp]),
     "mtp_moe_route": (_i, [_vp, _i, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "mtp_moe_segments": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "mtp_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp]),

@@ -15,7 +15,9 @@
 // Experts are split into two launches by their row count, because LDS (all
 // of a row tile's x) sets the occupancy: rows <= 4 run with R = 4 and LDS
 // for four rows (four 4-wave workgroups per CU at K = 4096); rows >= 5 run
-// 16-row tiles with R = 8 and 8-wave workgroups. Each workgroup first lists
+// 16-row tiles with R = 8 and 8-wave workgroups. The stack is packed in
+// layout 1 (32x32x16 quads) or layout 2 (16x16x32 quads: the 4-row form for
+// the first class, the 16-row form for the second). Each workgroup first lists
 // its class's experts in LDS from the device's active list (one parallel
 // pass), sizes the units so that about one round of them covers the grid,
 // then takes units grid-stride.
@@ -39,7 +41,7 @@ constexpr int kMoeList = 512;   // experts of a class listed in LDS (more: read 
 
 // The pack holds each 64-k group's scale and bias (group 128 repeats them),
 // so the body runs with GSH = 0 for either group size.
-template <int NW, int R, int EM, int NRT>
+template <int NW, int R, int EM, int NRT, bool MF>
 __global__ __launch_bounds__(NW * 64) void moe_stream_kernel(QmmParams p, MoeUnits mu) {
   constexpr int NT = NW * 64;
   // This class's experts, in active-list order: (e | rows << 16, first row).
@@ -122,14 +124,14 @@ __global__ __launch_bounds__(NW * 64) void moe_stream_kernel(QmmParams p, MoeUni
     q.w0 = p.w0 + e * mu.w_estride;
     if (EM == E_DUAL_SWIGLU) q.w1 = q.w0 + mu.w1_off;
     q.y0 = p.y0 + (size_t)(e0 + t0) * p.ldy;
-    qmv_stream_body<NW, R, X_PLAIN, EM, 0, true, false, NRT>(q, r, S, NoHook{});
+    qmv_stream_body<NW, R, X_PLAIN, EM, 0, true, MF, NRT>(q, r, S, NoHook{});
     __syncthreads();   // the next unit restages LDS
   }
 }
 
-template <int NW, int R, int EM>
+template <int NW, int R, int EM, bool MF>
 static int moe_launch(const QmmParams& p, const MoeUnits& mu, int rows_lds, hipStream_t st) {
-  auto k = moe_stream_kernel<NW, R, EM, 2>;
+  auto k = moe_stream_kernel<NW, R, EM, 2, MF>;
   const size_t lds = stream_lds(p.K >> 8, rows_lds, NW);
   if (lds + 2 * kMoeList * sizeof(int) + 512 > kLdsMax) return MTP_ERR_UNSUPPORTED;   // + the static expert list
   if (lds > 65536) (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -141,7 +143,7 @@ static int moe_launch(const QmmParams& p, const MoeUnits& mu, int rows_lds, hipS
 
 // row_class: 0 both launches, 1 only the experts with 1-4 rows, 2 only those
 // with more (two streams can then run the classes side by side).
-template <int EM>
+template <int EM, bool MF>
 static int moe_launch_classes(const QmmParams& p, MoeUnits mu, int max_rows, hipStream_t st, int row_class) {
   // rows <= 4: one row tile, LDS for four rows
   mu.rows_tile = 4;
@@ -155,7 +157,7 @@ static int moe_launch_classes(const QmmParams& p, MoeUnits mu, int max_rows, hip
   // 12.99 at eighteen).
   mu.tpu = EM == E_STORE ? env_int("MTPLX_AMD_MOE_TILES_SMALL_DOWN", 12) : env_int("MTPLX_AMD_MOE_TILES_SMALL", 6);
   if (row_class != 2) {
-    const int rc = moe_launch<4, 4, EM>(p, mu, 4, st);
+    const int rc = moe_launch<4, 4, EM, MF>(p, mu, 4, st);
     if (rc != MTP_OK) return rc;
   }
   if (max_rows <= 4 || row_class == 1) return MTP_OK;
@@ -169,19 +171,21 @@ static int moe_launch_classes(const QmmParams& p, MoeUnits mu, int max_rows, hip
   // ms at three, 12.43-12.47 at four, 12.59 at five, 12.67-12.69 with about
   // one unit per CU, 13.0 at eight)
   mu.tpu = env_int("MTPLX_AMD_MOE_TILES_LARGE", 3);
-  return moe_launch<8, 8, EM>(p, mu, 16, st);
+  return moe_launch<8, 8, EM, MF>(p, mu, 16, st);
 }
 
 }  // namespace mtp
 
 using namespace mtp;
 
-// Packed form of mtp_gather_qmv_affine4: wp is mtp_pack_affine4 of the
-// [E * rows_per_expert, K] matrix (expert e's rows at e * rows_per_expert;
-// for the fused pair its N gate rows then its N up rows).
+// Packed form of mtp_gather_qmv_affine4: wp is mtp_pack_affine4 (layout 1)
+// or mtp_pack_affine4_mf16 (layout 2) of the [E * rows_per_expert, K] matrix
+// (expert e's rows at e * rows_per_expert; for the fused pair its N gate rows
+// then its N up rows).
 static int gather_packed_run(const void* x, const uint32_t* rowmap, const int32_t* expert_off, const int32_t* active,
                              const void* wp, void* y, int max_rows_per_expert, int E, int N, int K, int group_size,
-                             int emode, int rows_per_expert, int row_class, void* stream, const char* who) {
+                             int emode, int rows_per_expert, int row_class, int layout, void* stream,
+                             const char* who) {
   if (row_class < 0 || row_class > 2) {
     set_error("%s: row_class %d (0 all experts, 1 those with 1-4 rows, 2 those with more)", who, row_class);
     return MTP_ERR_ARG;
@@ -223,7 +227,7 @@ static int gather_packed_run(const void* x, const uint32_t* rowmap, const int32_
   p.ldx = K;
   p.ldy = N;
   p.eps = 1e-6f;
-  p.packed = 1;
+  p.packed = layout;
   p.n_blocks = N / 32;
   p.tail_split = 1;
   MoeUnits mu = {};
@@ -234,9 +238,11 @@ static int gather_packed_run(const void* x, const uint32_t* rowmap, const int32_
   hipStream_t st = (hipStream_t)stream;
   int rc;
   if (emode == E_DUAL_SWIGLU)
-    rc = moe_launch_classes<E_DUAL_SWIGLU>(p, mu, max_rows_per_expert, st, row_class);
+    rc = layout == 2 ? moe_launch_classes<E_DUAL_SWIGLU, true>(p, mu, max_rows_per_expert, st, row_class)
+                     : moe_launch_classes<E_DUAL_SWIGLU, false>(p, mu, max_rows_per_expert, st, row_class);
   else
-    rc = moe_launch_classes<E_STORE>(p, mu, max_rows_per_expert, st, row_class);
+    rc = layout == 2 ? moe_launch_classes<E_STORE, true>(p, mu, max_rows_per_expert, st, row_class)
+                     : moe_launch_classes<E_STORE, false>(p, mu, max_rows_per_expert, st, row_class);
   if (rc != MTP_OK) {
     set_error("%s: K=%d needs more LDS than a workgroup has", who, K);
     return rc;
@@ -249,7 +255,7 @@ MTP_API int mtp_gather_qmv_affine4_packed(const void* x, const uint32_t* rowmap,
                                           int E, int N, int K, int group_size, int emode, int rows_per_expert,
                                           void* stream) {
   return gather_packed_run(x, rowmap, expert_off, active, wp, y, max_rows_per_expert, E, N, K, group_size, emode,
-                           rows_per_expert, 0, stream, "mtp_gather_qmv_affine4_packed");
+                           rows_per_expert, 0, 1, stream, "mtp_gather_qmv_affine4_packed");
 }
 
 MTP_API int mtp_gather_qmv_affine4_packed_rows(const void* x, const uint32_t* rowmap, const int32_t* expert_off,
@@ -257,5 +263,13 @@ MTP_API int mtp_gather_qmv_affine4_packed_rows(const void* x, const uint32_t* ro
                                                int max_rows_per_expert, int E, int N, int K, int group_size, int emode,
                                                int rows_per_expert, int row_class, void* stream) {
   return gather_packed_run(x, rowmap, expert_off, active, wp, y, max_rows_per_expert, E, N, K, group_size, emode,
-                           rows_per_expert, row_class, stream, "mtp_gather_qmv_affine4_packed_rows");
+                           rows_per_expert, row_class, 1, stream, "mtp_gather_qmv_affine4_packed_rows");
+}
+
+MTP_API int mtp_gather_qmv_affine4_packed_mf16(const void* x, const uint32_t* rowmap, const int32_t* expert_off,
+                                               const int32_t* active, const void* wp, void* y,
+                                               int max_rows_per_expert, int E, int N, int K, int group_size, int emode,
+                                               int rows_per_expert, int row_class, void* stream) {
+  return gather_packed_run(x, rowmap, expert_off, active, wp, y, max_rows_per_expert, E, N, K, group_size, emode,
+                           rows_per_expert, row_class, 2, stream, "mtp_gather_qmv_affine4_packed_mf16");
 }

@@ -47,8 +47,8 @@ class QuantizedLinear:
         experts = self.weight.dim() == 3
         if self.weight.dim() not in (2, 3) or self.bits != 4 or self.mode != "affine":
             raise NotImplementedError("packing covers 2-D (or expert-stacked 3-D) 4-bit affine layers")
-        if experts and (layout != 1 or row_order is not None or self.out_features % 32):
-            raise NotImplementedError("expert stacks pack in layout 1 only, with N a multiple of 32")
+        if experts and (row_order is not None or self.out_features % 32):
+            raise NotImplementedError("expert stacks pack without a row order, with N a multiple of 32")
         # An expert stack [E, N, K/8] packs as the [E*N, K] matrix: with N a
         # multiple of 32 no tile straddles two experts, so expert e's tiles
         # start at tile e * N / 32.

@@ -54,6 +54,9 @@ MOE_SIDE_STREAM = (os.environ.get("MTPLX_AMD_MOE_SIDE_STREAM") or "1").strip() n
 # 16x16x32 MFMA form, at most 16; MTPLX_AMD_LAYOUT2_ROWS=4 keeps 5..16 rows on
 # layout 1's 32x32x16 form).
 LAYOUT2_ROWS = min(16, int(os.environ.get("MTPLX_AMD_LAYOUT2_ROWS") or "16"))
+# Packed layout of the routed expert stacks: 2 (16x16x32 quads, the default)
+# or 1 (MTPLX_AMD_MOE_LAYOUT=1: 32x32x16 quads). One layout is kept.
+MOE_LAYOUT = 1 if (os.environ.get("MTPLX_AMD_MOE_LAYOUT") or "2").strip() == "1" else 2
 
 
 def qmv_ws_bytes(M: int, c: "DecoderConfig") -> int:
@@ -249,12 +252,12 @@ class VerifyModel:
                     q.pack(layout=2)
             L.qkv_rope = L.qkv.pack(rope_order)
             L.qkv_rope2 = L.qkv.pack(rope_order, layout=2)
-            # Expert stacks: layout 1 only, and (unless asked to keep it) the
-            # MLX-layout source is freed, so a 125B-class MoE holds its
-            # experts once (2.7 GB per layer at the cfg5 shape).
+            # Expert stacks: one packed layout (MOE_LAYOUT), and (unless asked
+            # to keep it) the MLX-layout source is freed, so a 125B-class MoE
+            # holds its experts once (2.7 GB per layer at the cfg5 shape).
             for q in (L.expert_gate_up, L.expert_down):
                 if q is not None:
-                    q.pack()
+                    q.pack(layout=MOE_LAYOUT)
                     if not self.keep_expert_source:
                         q.release_source()
         self.lm_head.pack()
@@ -516,13 +519,16 @@ class VerifyModel:
         # Routed experts over their packed stacks: gate|up + SwiGLU on the
         # token rows gathered by row_map, then down on the sorted rows; one
         # launch per row class (experts with 1-4 rows, with more).
+        gfn = "mtp_gather_qmv_affine4_packed_mf16" if MOE_LAYOUT == 2 else "mtp_gather_qmv_affine4_packed_rows"
+
+        def EW(q):
+            return q.packed_mf16 if MOE_LAYOUT == 2 else q.packed
+
         def experts(row_class, stream):
-            call("mtp_gather_qmv_affine4_packed_rows", xn.data_ptr(), es.row_map.data_ptr(), es.expert_off.data_ptr(),
-                 es.active.data_ptr(), L.expert_gate_up.packed.data_ptr(), hsorted.data_ptr(), M, E, F, H, gs, 3,
-                 2 * F, row_class, stream)
-            call("mtp_gather_qmv_affine4_packed_rows", hsorted.data_ptr(), None, es.expert_off.data_ptr(),
-                 es.active.data_ptr(), L.expert_down.packed.data_ptr(), ysorted.data_ptr(), M, E, H, F, gs, 0, H,
-                 row_class, stream)
+            call(gfn, xn.data_ptr(), es.row_map.data_ptr(), es.expert_off.data_ptr(), es.active.data_ptr(),
+                 EW(L.expert_gate_up).data_ptr(), hsorted.data_ptr(), M, E, F, H, gs, 3, 2 * F, row_class, stream)
+            call(gfn, hsorted.data_ptr(), None, es.expert_off.data_ptr(), es.active.data_ptr(),
+                 EW(L.expert_down).data_ptr(), ysorted.data_ptr(), M, E, H, F, gs, 0, H, row_class, stream)
 
         # Shared expert (SwiGLU MLP) on the normalised rows, then one combine:
         # h = h + bf16(routed + bf16(sigmoid(gate) * shared)).

@@ -198,13 +198,15 @@ def test_gather_qmm_contract(gpu):
             assert_close(bf16_values(y[t, j, 0]), want, what="switch-glu form")
 
 
-def _within_one_ulp(a, b, what):
-    """|a - b| <= one bf16 ulp of b (plus 1e-4 of the row's scale where a sum
-    cancels): the packed path sums the same products with the 8 k of each
-    MFMA operand in another order."""
+def _within_one_ulp(a, b, what, ulps=1):
+    """|a - b| <= ``ulps`` bf16 ulps of b (plus 1e-4 of the row's scale where
+    a sum cancels): the packed path sums the same products with the k of each
+    MFMA operand in another order. One ulp for a rounded sum; two through
+    SwiGLU, which rounds the gate and the up sum (each one ulp apart at most)
+    and then their product."""
     ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(b), 1e-30))) - 7)
-    bad = np.abs(a - b) > ulp + 1e-4 * np.abs(b).max(axis=1, keepdims=True)
-    assert not bad.any(), f"{what}: {int(bad.sum())} of {bad.size} beyond one ulp"
+    bad = np.abs(a - b) > ulps * ulp + 1e-4 * np.abs(b).max(axis=1, keepdims=True)
+    assert not bad.any(), f"{what}: {int(bad.sum())} of {bad.size} beyond {ulps} ulp"
 
 
 @pytest.mark.parametrize("T,k,E,H,F,gs,zipf", [
@@ -216,7 +218,9 @@ def _within_one_ulp(a, b, what):
 def test_packed_expert_matmul(gpu, T, k, E, H, F, gs, zipf):
     """mtp_gather_qmv_affine4_packed (the verify step's routed experts) against
     the oracle's sorted chain (bf16 bar) and within one bf16 ulp of the
-    MLX-layout gather, for experts of every row class."""
+    MLX-layout gather, for experts of every row class; the layout-2 entry
+    (mtp_gather_qmv_affine4_packed_mf16) against the same bar and within one
+    ulp of layout 1."""
     from mtplx_amd import _lib
     from mtplx_amd.moe_sorted_gather import expert_sort
     from mtplx_amd.quant import QuantizedLinear
@@ -263,6 +267,24 @@ def test_packed_expert_matmul(gpu, T, k, E, H, F, gs, zipf):
     yv = bf16_values(y)
     assert_close(yv, want_y, what=f"packed down T={T} E={E}")
     _within_one_ulp(yv, bf16_values(y0), "packed vs MLX-layout down")
+    # layout 2 (16x16x32 quads: the 4-row form for 1-4-row experts, the
+    # 16-row form for 16-row tiles), each class on its own launch
+    h2 = torch.full((R, F), float("nan"), dtype=torch.bfloat16, device="cuda")
+    y2 = torch.full((R, H), float("nan"), dtype=torch.bfloat16, device="cuda")
+    for row_class in (1, 2):
+        _lib.call("mtp_gather_qmv_affine4_packed_mf16", x.data_ptr(), es.row_map.data_ptr(), es.expert_off.data_ptr(),
+                  es.active.data_ptr(), qgu.pack(layout=2).data_ptr(), h2.data_ptr(), T, E, F, H, gs, 3, 2 * F,
+                  row_class, st)
+    for row_class in (1, 2):
+        _lib.call("mtp_gather_qmv_affine4_packed_mf16", h.data_ptr(), None, es.expert_off.data_ptr(),
+                  es.active.data_ptr(), qdn.pack(layout=2).data_ptr(), y2.data_ptr(), T, E, H, F, gs, 0, H, row_class,
+                  st)
+    torch.cuda.synchronize()
+    h2v, y2v = bf16_values(h2), bf16_values(y2)
+    assert_close(h2v, want_h, what=f"layout-2 gate|up + SwiGLU T={T} E={E}")
+    _within_one_ulp(h2v, hv, "layout 2 vs layout 1 gate|up + SwiGLU", ulps=2)
+    assert_close(y2v, want_y, what=f"layout-2 down T={T} E={E}")
+    _within_one_ulp(y2v, yv, "layout 2 vs layout 1 down")
 
 
 def test_packed_expert_matmul_refuses_bad_shapes(gpu):
