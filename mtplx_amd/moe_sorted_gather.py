@@ -135,20 +135,31 @@ def sort_rows(x: torch.Tensor, indices: torch.Tensor, n_experts: int | None = No
     return tokens, es.row_map, es.sorted_ids, es.inv_order
 
 
-def _gather_packed(x, es: ExpertSort, rowmap, packed, n_out, group_size, max_rows):
-    """The sorted rows through an expert stack's tile-major pack (layout 1,
-    ``QuantizedLinear.pack()``), on the verify step's packed-expert kernel."""
+def _stack_pack(module) -> tuple[torch.Tensor, str] | None:
+    """An expert stack's tile-major pack and the packed-expert entry point
+    that reads it: layout 1 (``QuantizedLinear.pack()``) or layout 2
+    (``pack(layout=2)``, what the verify step keeps), or None."""
+    if getattr(module, "packed", None) is not None:
+        return module.packed, "mtp_gather_qmv_affine4_packed_rows"
+    if getattr(module, "packed_mf16", None) is not None:
+        return module.packed_mf16, "mtp_gather_qmv_affine4_packed_mf16"
+    return None
+
+
+def _gather_packed(x, es: ExpertSort, rowmap, module, n_out, group_size, max_rows):
+    """The sorted rows through an expert stack's tile-major pack, on the
+    verify step's packed-expert kernels (both row classes)."""
+    pack, fn = _stack_pack(module)
     R = int(es.row_map.numel())
     K = int(x.shape[-1])
     y = torch.zeros((R, n_out), dtype=torch.bfloat16, device=x.device)   # flagged sort: zeros
-    _lib.call("mtp_gather_qmv_affine4_packed", x.data_ptr(), _lib.ptr(rowmap), es.expert_off.data_ptr(),
-              es.active.data_ptr(), packed.data_ptr(), y.data_ptr(), max_rows, es.n_experts, n_out, K, group_size, 0,
-              n_out, _lib.stream_handle(x.device))
+    _lib.call(fn, x.data_ptr(), _lib.ptr(rowmap), es.expert_off.data_ptr(), es.active.data_ptr(), pack.data_ptr(),
+              y.data_ptr(), max_rows, es.n_experts, n_out, K, group_size, 0, n_out, 0, _lib.stream_handle(x.device))
     return y
 
 
 def _packable(module, N: int, K: int) -> bool:
-    return (getattr(module, "packed", None) is not None and N % 32 == 0 and K % 256 == 0
+    return (_stack_pack(module) is not None and N % 32 == 0 and K % 256 == 0
             and int(module.group_size) in (64, 128))
 
 
@@ -235,7 +246,7 @@ def switch_linear(module: Any, x: torch.Tensor, indices: torch.Tensor, *, sorted
 
     def run(es, rowmap):
         if packed:
-            return _gather_packed(x2, es, rowmap, module.packed, N, int(module.group_size), int(x2.shape[0]))
+            return _gather_packed(x2, es, rowmap, module, N, int(module.group_size), int(x2.shape[0]))
         return _gather(x2, None, es, rowmap, module.weight, module.scales, module.biases, None, None, None, N, 0, 0,
                        N, int(module.group_size), int(x2.shape[0]))
 

@@ -169,6 +169,12 @@ def test_reference_call_sequence(gpu):
     assert_close(bf16_values(yp.reshape(-1, H)), want_y, what="switch_linear on a pack")
     yp2 = switch_linear(down, hs, torch.from_numpy(idx).cuda().reshape(-1), sorted_indices=False)
     assert torch.equal(yp2.reshape(T * k, H), yp[inv_order.long()].reshape(T * k, H))
+    # and a stack held only in layout 2 (as the verify step keeps its experts)
+    down2 = QuantizedLinear(u32(dn[0]), from_bits(dn[1]), from_bits(dn[2]))
+    down2.pack(layout=2)
+    down2.release_source()
+    yq = switch_linear(down2, h, sidx, sorted_indices=True)
+    assert_close(bf16_values(yq.reshape(-1, H)), want_y, what="switch_linear on a layout-2 pack")
 
 
 def test_gather_qmm_contract(gpu):
