@@ -524,14 +524,24 @@ constexpr size_t attn_bal_lds_bytes() {
   return attn_vt_lds_bytes() + (size_t)kBalReqArrays * kBalMaxReq * sizeof(int);
 }
 
-// Workgroup owning global tile x (ranges [w T / G, (w+1) T / G)).
-__device__ __forceinline__ int bal_owner(long long x, long long T, int G) {
-  return (int)(((x + 1) * G - 1) / T);
-}
+// The balanced split of T tiles over the first G workgroups of the grid,
+// G = min(grid, T): workgroup w takes tiles [lo(w), lo(w + 1)),
+// lo(w) = floor(w T / G). With G <= T every one of them gets a tile, so no
+// workgroup inside a head's range of slots is empty and the merge reads only
+// written partials (with more workgroups than tiles, empty ones in the middle
+// of a head's range would leave slots holding stale partials).
+struct BalSplit {
+  long long T;
+  int G;
+  __device__ BalSplit(long long T_, int grid) : T(T_), G((long long)grid < T_ ? grid : (int)T_) {}
+  __device__ long long lo(int w) const { return (long long)w * T / G; }
+  // Workgroup owning tile x: the largest w with lo(w) <= x.
+  __device__ int owner(long long x) const { return (int)(((x + 1) * G - 1) / T); }
+};
 
 // Slots (partials) of head (b, h) whose first global tile is P, nt tiles.
-__device__ __forceinline__ int bal_nparts(long long P, int nt, long long T, int G) {
-  return nt > 0 ? bal_owner(P + nt - 1, T, G) - bal_owner(P, T, G) + 1 : 0;
+__device__ __forceinline__ int bal_nparts(long long P, int nt, const BalSplit& bs) {
+  return nt > 0 ? bs.owner(P + nt - 1) - bs.owner(P) + 1 : 0;
 }
 
 template <bool WT, int NRG = 2>
@@ -593,6 +603,7 @@ __device__ __forceinline__ void attn_bal_body(const AttnParams& p, unsigned char
   // keeps them (and the loop below) in scalar registers.
   auto lds_int = [&](const int* a, int i) { return __builtin_amdgcn_readfirstlane(a[i]); };
   const long long T = (long long)lds_int(s_pt, B - 1) + (long long)Hkv * lds_int(s_nt, B - 1);
+  const BalSplit bs(T, G);
   if (T == 0) {   // no keys at all: every head has no partial
     if (w == 0 && p.bal_tab)
       for (int i = tid; i < 2 * B * Hkv; i += kVtWaves * 64) p.bal_tab[i] = 0;
@@ -605,7 +616,7 @@ __device__ __forceinline__ void attn_bal_body(const AttnParams& p, unsigned char
       const int b = b0 + lane;
       int v = 0;
       if (b < B)
-        for (int h = 0; h < Hkv; ++h) v += bal_nparts((long long)s_pt[b] + (long long)h * s_nt[b], s_nt[b], T, G);
+        for (int h = 0; h < Hkv; ++h) v += bal_nparts((long long)s_pt[b] + (long long)h * s_nt[b], s_nt[b], bs);
       int incl = v;
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
@@ -622,13 +633,14 @@ __device__ __forceinline__ void attn_bal_body(const AttnParams& p, unsigned char
     for (int bh = tid; bh < B * Hkv; bh += kVtWaves * 64) {
       const int b = bh / Hkv, h = bh - (bh / Hkv) * Hkv;
       int base = s_ps[b];
-      for (int hh = 0; hh < h; ++hh) base += bal_nparts((long long)s_pt[b] + (long long)hh * s_nt[b], s_nt[b], T, G);
+      for (int hh = 0; hh < h; ++hh) base += bal_nparts((long long)s_pt[b] + (long long)hh * s_nt[b], s_nt[b], bs);
       p.bal_tab[2 * bh] = base;
-      p.bal_tab[2 * bh + 1] = bal_nparts((long long)s_pt[b] + (long long)h * s_nt[b], s_nt[b], T, G);
+      p.bal_tab[2 * bh + 1] = bal_nparts((long long)s_pt[b] + (long long)h * s_nt[b], s_nt[b], bs);
     }
   }
-  const long long lo = (long long)w * T / G, hi = (long long)(w + 1) * T / G;
-  if (lo >= hi) return;   // uniform over the workgroup
+  if (w >= bs.G) return;   // past the split's workgroups (fewer tiles than the grid)
+  const long long lo = bs.lo(w), hi = bs.lo(w + 1);
+  if (lo >= hi) return;     // (not reached: each of the split's workgroups has a tile)
   // Request holding tile lo: the last b with s_pt[b] <= lo (binary search).
   int b = 0;
   {
@@ -653,8 +665,8 @@ __device__ __forceinline__ void attn_bal_body(const AttnParams& p, unsigned char
     const int ta = (int)(x - P);
     const int tb = (int)((hi < P + nt ? hi : P + nt) - P);
     int slot = lds_int(s_ps, b);
-    for (int hh = 0; hh < h; ++hh) slot += bal_nparts(pb + (long long)hh * nt, nt, T, G);
-    slot += w - bal_owner(P, T, G);
+    for (int hh = 0; hh < h; ++hh) slot += bal_nparts(pb + (long long)hh * nt, nt, bs);
+    slot += w - bs.owner(P);
     const int qs = lds_int(s_qs, b);
     const int L = lds_int(s_ql, b);
     const int kv_end = lds_int(s_ke, b);

@@ -172,9 +172,11 @@ def test_cfg4_ragged_verify_step_matches_oracle(gpu):
         assert int(res.status[b]) == 0
 
 
-def _blocks_attention(ctx, lens, split_keys, seed, Hq=40, Hkv=8):
+def _blocks_attention(ctx, lens, split_keys, seed, Hq=40, Hkv=8, ws_fill=None):
     """Block attention over requests with contexts ``ctx`` (keys before the
-    new rows) and ``lens`` query rows; returns (output rows, inputs)."""
+    new rows) and ``lens`` query rows; returns (output rows, inputs).
+    ``ws_fill``: a float every word of the workspace holds beforehand (stale
+    partials that must never be read)."""
     from mtplx_amd import _lib
     D = 128
     B = len(ctx)
@@ -193,6 +195,8 @@ def _blocks_attention(ctx, lens, split_keys, seed, Hq=40, Hkv=8):
     d_qs, d_lens, d_row, d_kv = t(q_start), t(lens), t(row_off), t(kv_off)
     nb = _lib.query("mtp_attn_blocks_workspace_bytes", B, Hkv, int(caps.max()), int(caps.sum()), split_keys)
     ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    if ws_fill is not None:
+        ws.view(torch.float32)[: nb // 4].fill_(ws_fill)
     _lib.attn_blocks(_st(), q=q, k_blk=kb, v_blk=vb, q_start=d_qs, q_lens=d_lens, row_off=d_row, kv_off=d_kv,
                      out=out, B=B, Hq=Hq, Hkv=Hkv, Lmax=Lmax, D=D, cap=int(caps.max()), split_keys=split_keys,
                      scale=1.0 / np.sqrt(D), total_cap=int(caps.sum()), ws=ws, ws_bytes=ws.numel())
@@ -200,7 +204,7 @@ def _blocks_attention(ctx, lens, split_keys, seed, Hq=40, Hkv=8):
     return bf16_values(out), (q, kb, vb, q_start, lens, caps, row_off, kv_off)
 
 
-@pytest.mark.parametrize("case", ["long_among_short", "tiny_total", "single", "uniform", "many"])
+@pytest.mark.parametrize("case", ["long_among_short", "tiny_total", "single", "uniform", "many", "short_multi_tile"])
 @pytest.mark.parametrize("split_keys", [0, 1024])
 @pytest.mark.parametrize("merge", ["auto", "column"])
 def test_block_attention_balanced_shapes(gpu, case, split_keys, merge, monkeypatch):
@@ -224,10 +228,15 @@ def test_block_attention_balanced_shapes(gpu, case, split_keys, merge, monkeypat
     elif case == "many":   # 130 requests: the prologue's request scans run in three rounds of 64
         ctx = list(rng.integers(0, 400, size=130))
         lens = list(rng.integers(1, 5, size=130))
+    elif case == "short_multi_tile":   # fewer tiles (72) than workgroups, several per head
+        ctx, lens = [60, 200], [4, 2]
     else:
         ctx, lens = [4093] * 4, [3] * 4
     Hq, Hkv, D = 40, 8, 128
-    got, (q, kb, vb, q_start, lens, caps, row_off, kv_off) = _blocks_attention(ctx, lens, split_keys, seed=23)
+    # every workspace word 1e4 beforehand: a partial slot the merge reads but
+    # no workgroup wrote would dominate the merged rows
+    got, (q, kb, vb, q_start, lens, caps, row_off, kv_off) = _blocks_attention(ctx, lens, split_keys, seed=23,
+                                                                             ws_fill=1e4)
     assert np.isfinite(got).all()
     for b in range(len(ctx)):
         o0, o1 = int(kv_off[b]), int(kv_off[b + 1])
