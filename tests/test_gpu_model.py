@@ -13,10 +13,10 @@ from tests.model_util import model_params_numpy
 pytestmark = pytest.mark.gpu
 
 
-def _run(cfg, B, L, starts, seed, moe_tokens=None):
+def _run(cfg, B, L, starts, seed, moe_tokens=None, cap=320):
     from mtplx_amd.verify_step import VerifyModel
     model = VerifyModel(cfg, device="cuda", seed=seed, keep_expert_source=True)
-    model.allocate_cache(B, 320)
+    model.allocate_cache(B, cap)
     kc = [model.k_cache_standard(li).float().cpu().numpy().astype(np.float64) for li in range(cfg.layers)]
     vc = [model.v_cache_standard(li).float().cpu().numpy().astype(np.float64) for li in range(cfg.layers)]
     gen = torch.Generator(device="cuda").manual_seed(seed + 1)
@@ -64,6 +64,21 @@ def test_moe_verify_step_matches_oracle(gpu, B, L):
     starts = [int(v) for v in np.random.default_rng(B * 10 + L).integers(0, 320 - L, B)]
     model, tokens, logits, want, kc, vc = _run(cfg, B, L, starts, 7)
     assert_close(logits.cpu().numpy().astype(np.float64), want, rtol=1e-2, atol=1e-2, what=f"moe logits B={B} L={L}")
+
+
+def test_moe_verify_step_balanced_attention_short_contexts(gpu):
+    """A cache large enough for the balanced attention (B * Hkv * cap >= 65536
+    key-heads) holding short contexts: fewer 32-key tiles than workgroups,
+    several per head (the split then runs over as many workgroups as tiles)."""
+    from mtplx_amd.verify_step import DecoderConfig
+    cfg = DecoderConfig(layers=2, hidden=512, ffn=0, n_heads=8, n_kv_heads=2, head_dim=128, vocab=2048,
+                        n_experts=16, top_k=4, expert_ffn=256, shared_ffn=256)
+    B, L = 8, 4
+    starts = [int(v) for v in np.random.default_rng(3).integers(20, 300, B)]
+    model, tokens, logits, want, kc, vc = _run(cfg, B, L, starts, 9, cap=4096)
+    assert B * cfg.n_kv_heads * model.cap >= 65536
+    assert_close(logits.cpu().numpy().astype(np.float64), want, rtol=1e-2, atol=1e-2,
+                 what="moe logits, balanced attention over short contexts")
 
 
 def test_status_word_flags_bad_token_and_position(gpu):
