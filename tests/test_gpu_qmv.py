@@ -236,11 +236,12 @@ def test_pack_layout_bit_exact(gpu, n, k, gs):
 @pytest.mark.parametrize("m,n,k,gs,xmode,emode", [
     (4, 17408, 5120, 64, 0, 0), (4, 7168, 5120, 64, 2, 0), (4, 5120, 17408, 64, 0, 1),
     (4, 1536, 2048, 64, 2, 3), (4, 300, 1024, 128, 0, 0), (8, 600, 1024, 64, 2, 3), (16, 256, 512, 64, 0, 1),
-    (4, 151936 // 8, 5120, 64, 2, 0)])
+    (4, 151936 // 8, 5120, 64, 2, 0), (16, 512, 1024, 64, 0, 2), (12, 640, 1024, 64, 1, 0), (3, 640, 1024, 64, 1, 2)])
 def test_packed_path_matches_unpacked(gpu, m, n, k, gs, xmode, emode):
-    """The tile-major path computes the same sums as the reference-layout path
-    with the 8 k of each MFMA operand in another order, so outputs agree to
-    one bf16 ulp (and both meet the oracle bar)."""
+    """The tile-major paths (layout 1, and layout 2 up to 16 rows) compute the
+    same sums as the reference-layout path with the k of each MFMA operand in
+    another order, so outputs agree to one bf16 ulp (and both meet the oracle
+    bar); xmode 1 (silu(x) * x2) and emode 2 (two outputs) included."""
     from mtplx_amd import _lib
     from mtplx_amd.quant import QuantizedLinear
     g = torch.Generator(device="cuda").manual_seed(m * 1000 + n)
@@ -248,30 +249,35 @@ def test_packed_path_matches_unpacked(gpu, m, n, k, gs, xmode, emode):
     q1 = QuantizedLinear.random(n, k, gs, generator=g)
     x = torch.randn((m, k), device="cuda", generator=g).to(torch.bfloat16)
     nw = (1 + 0.1 * torch.randn(k, device="cuda", generator=g)).to(torch.bfloat16)
+    up = torch.randn((m, k), device="cuda", generator=g).to(torch.bfloat16)
     r = torch.randn((m, n), device="cuda", generator=g).to(torch.bfloat16)
     st = _stream()
     outs = []
-    for packed in (0, 1):
+    layouts = (0, 1, 2) if m <= 16 else (0, 1)
+    for packed in layouts:
         y0 = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
         y1 = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
         ss = torch.zeros(((n + 31) // 32) * 32, dtype=torch.float32, device="cuda")
-        kw = dict(x=x, x2=nw if xmode == 2 else None, eps=1e-6, M=m, N=n, K=k, group_size=gs, xmode=xmode,
+        kw = dict(x=x, x2=nw if xmode == 2 else (up if xmode == 1 else None), eps=1e-6, M=m, N=n, K=k,
+                  group_size=gs, xmode=xmode,
                   emode=emode, packed=packed, y0=y0, y1=y1 if emode == 2 else None,
                   resid=r if emode == 1 else None, ss_out=ss if emode == 1 else None)
         if packed:
-            kw.update(w0=q0.pack(), w1=q1.pack() if emode >= 2 else None)
+            kw.update(w0=q0.pack(layout=packed), w1=q1.pack(layout=packed) if emode >= 2 else None)
         else:
             kw.update(w0=q0.weight, s0=q0.scales, b0=q0.biases, w1=q1.weight if emode >= 2 else None,
                       s1=q1.scales if emode >= 2 else None, b1=q1.biases if emode >= 2 else None)
         _lib.qmv_ex(st, **kw)
         torch.cuda.synchronize()
-        outs.append((y0.clone(), ss.clone()))
-    a, b = bf16_values(outs[1][0]), bf16_values(outs[0][0])
-    tol = np.maximum(np.abs(a), np.abs(b)) * 2.0 ** -7 + 1e-4 * np.abs(b).max()
-    assert (np.abs(a - b) <= tol).all(), np.abs(a - b).max()
-    if emode == 1:
-        assert torch.allclose(outs[0][1], outs[1][1], rtol=1e-3, atol=1e-3)
-    assert not torch.isnan(outs[1][0].float()).any()
+        outs.append((y0.clone(), ss.clone(), y1.clone()))
+    for i in range(1, len(layouts)):
+        for j in ((0, 2) if emode == 2 else (0,)):
+            a, b = bf16_values(outs[i][j]), bf16_values(outs[0][j])
+            tol = np.maximum(np.abs(a), np.abs(b)) * 2.0 ** -7 + 1e-4 * np.abs(b).max()
+            assert (np.abs(a - b) <= tol).all(), (layouts[i], j, np.abs(a - b).max())
+        if emode == 1:
+            assert torch.allclose(outs[0][1], outs[i][1], rtol=1e-3, atol=1e-3)
+        assert not torch.isnan(outs[i][0].float()).any()
     if xmode == 0 and emode == 0 and n * k <= 4_000_000:
         want = qmm_affine4(bits(x), *(t.cpu().numpy().view(np.uint32) if i == 0 else bits(t)
                                        for i, t in enumerate((q0.weight, q0.scales, q0.biases))), gs)
