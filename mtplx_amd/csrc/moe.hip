@@ -109,15 +109,40 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t* i
     }
   }
   __syncthreads();
-  // Stable rank: earlier rows routed to the same expert.
-  for (int i = tid; i < R; i += kSortThreads) {
-    const int e = s_ids[i];
-    int rank = 0;
-    for (int j = 0; j < i; ++j) rank += (s_ids[j] == e);
-    const int pos = s_cnt[e] + rank;
-    row_map[pos] = (uint32_t)(i / top_k);
-    sorted_ids[pos] = (uint32_t)e;
-    inv_order[i] = (uint32_t)pos;
+  // Stable positions, 64 rows (one wave) at a time in row order: within a
+  // wave the rows routed to the same expert are matched by ballots over the
+  // id's bits, and each group's first lane takes the group's run of positions
+  // from the expert's running offset (s_cnt); the rounds run in row order,
+  // one workgroup barrier each, so earlier rows always come first.
+  const int lane = tid & 63, wave = tid >> 6;
+  for (int c0 = 0; c0 < R; c0 += kSortThreads) {
+    const int i = c0 + tid;
+    const bool valid = i < R;
+    const int e = valid ? s_ids[i] : 0;
+    unsigned long long m = __ballot(valid);
+    for (int b = 0; (1 << b) < E; ++b) {   // uniform
+      const bool bit = ((e >> b) & 1) != 0;
+      const unsigned long long bal = __ballot(valid && bit);
+      m &= bit ? bal : ~bal;
+    }
+    if (!valid) m = 0ull;
+    const int leader = m ? __ffsll(m) - 1 : lane;
+    int base = 0;
+    const int nwav = (R - c0 + 63) >> 6 < kSortThreads / 64 ? (R - c0 + 63) >> 6 : kSortThreads / 64;
+    for (int w = 0; w < nwav; ++w) {
+      if (wave == w && valid && lane == leader) {
+        base = s_cnt[e];
+        s_cnt[e] = base + __popcll(m);
+      }
+      __syncthreads();
+    }
+    base = __shfl(base, leader, 64);
+    if (valid) {
+      const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
+      row_map[pos] = (uint32_t)(i / top_k);
+      sorted_ids[pos] = (uint32_t)e;
+      inv_order[i] = (uint32_t)pos;
+    }
   }
 }
 

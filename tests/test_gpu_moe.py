@@ -13,7 +13,8 @@ from tests.gpu_util import assert_close, bf16_values, bits, from_bits, randn_bf1
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("T,k,E", [(16, 8, 256), (4, 2, 8), (64, 8, 128), (1, 1, 4), (200, 10, 300)])
+@pytest.mark.parametrize("T,k,E", [(16, 8, 256), (4, 2, 8), (64, 8, 128), (1, 1, 4), (200, 10, 300),
+                                    (1024, 8, 4096), (333, 2, 2)])
 def test_expert_sort_bit_exact(gpu, T, k, E):
     from mtplx_amd.moe_sorted_gather import expert_sort
     rng = np.random.default_rng(T * k + E)
