@@ -67,14 +67,17 @@ __host__ __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) 
 // theta = pos * 2^(-(2d/D) * log2(base)); outputs rounded to bf16. Shared by
 // the standalone RoPE kernel and the fused q|k|v matmul epilogue so both
 // round identically.
+// The products and sums below use explicitly rounded operations, so no
+// kernel's contraction choices change them: every writer and epilogue (and
+// the precomputed angle table) produce the same bits for the same inputs.
 __device__ __forceinline__ void rope_angle(int pos, int d, int D, float log2_base, float& sn, float& cs) {
-  const float inv_freq = exp2f(-((float)(2 * d) / (float)D) * log2_base);
-  const float theta = (float)pos * inv_freq;
+  const float inv_freq = exp2f(__fmul_rn(-((float)(2 * d) / (float)D), log2_base));
+  const float theta = __fmul_rn((float)pos, inv_freq);
   sincosf(theta, &sn, &cs);
 }
 __device__ __forceinline__ void rope_apply(float x1, float x2, float sn, float cs, uint16_t& o1, uint16_t& o2) {
-  o1 = f2bf(x1 * cs - x2 * sn);
-  o2 = f2bf(x1 * sn + x2 * cs);
+  o1 = f2bf(__fmaf_rn(x1, cs, -__fmul_rn(x2, sn)));
+  o2 = f2bf(__fmaf_rn(x1, sn, __fmul_rn(x2, cs)));
 }
 __device__ __forceinline__ void rope_pair(float x1, float x2, int pos, int d, int D, float log2_base, uint16_t& o1,
                                           uint16_t& o2) {
