@@ -7,18 +7,21 @@ This is the forward the reference runs on ``[primary, d1..dK]``
 64 layers, hidden 5120, SwiGLU 17408, 40/8 heads of 128, RMSNorm, RoPE 1e6,
 vocab 151936, every linear 4-bit affine g64, bf16 KV cache) or its MoE variant.
 
-Per layer the kernels are:
-  1. ``mtp_qmv_affine4_ex`` emode 4  input RMSNorm fused into the q|k|v matmul,
-                                     whose epilogue applies RoPE at per-request
-                                     offsets and writes K/V into the cache
-                                     (where the epilogue does not fit: the q|k|v matmul, then
-                                     ``mtp_rope_qkv_to_cache_vt``)
-  3. ``mtp_ragged_gqa_attn_rows_vt`` ragged GQA attention (split-KV + merge; the balanced
-     ``mtp_ragged_gqa_attn_blocks`` for long total contexts)
-  4. ``mtp_qmv_affine4_residual``    o_proj + residual add
-  5. ``mtp_qmv_affine4_rmsnorm_dual`` post-attention RMSNorm + gate/up + SwiGLU
-  6. ``mtp_qmv_affine4_residual``    down_proj + residual add
-  (MoE layers replace 5-6 with RMSNorm → router projection (its last row
+Per layer the kernels are (every matmul is ``mtp_qmv_affine4_ex`` on the
+layer's packed weights; the mode names the fused work):
+  1. xmode 2, emode 4   input RMSNorm fused into the q|k|v matmul, whose
+                        epilogue applies RoPE at per-request offsets and
+                        writes K/V into the cache (where the epilogue does not
+                        fit: the q|k|v matmul, then ``mtp_rope_qkv_to_cache_vt``)
+  2. ``mtp_ragged_gqa_attn_rows_vt``  ragged GQA attention (split-KV + merge;
+                        the balanced ``mtp_ragged_gqa_attn_blocks`` for long
+                        total contexts)
+  3. emode 1            o_proj + residual add (``mtp_qmv_affine4_residual``'s work)
+  4. xmode 2, emode 3   post-attention RMSNorm + gate/up + SwiGLU
+                        (``mtp_qmv_affine4_rmsnorm_dual``'s work)
+  5. xmode 3, emode 1   down_proj + residual add, the row sums of its input
+                        handed over by step 4
+  (MoE layers replace 4-5 with RMSNorm → router projection (its last row
   is the shared-expert gate) → top-k route → expert sort → gathered SwiGLU →
   gathered down, the shared expert's SwiGLU MLP, and one combine: residual +
   routed + sigmoid(gate) * shared, ``mtplx/models/qwen4_exp.py:1416-1445``.)
