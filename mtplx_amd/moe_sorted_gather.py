@@ -9,7 +9,10 @@ gfx950 kernels count rows in 32 bits, so ``guard_active()`` is False and
 
 GPU work: ``mtp_moe_sort`` (stable counting sort + expert offsets + active
 list) and ``mtp_gather_qmv_affine4`` (rows read in place through the row map,
-one column of workgroups per active expert, optional fused SwiGLU).
+one column of workgroups per active expert, optional fused SwiGLU); expert
+stacks packed once (``QuantizedLinear.pack``) run
+``mtp_gather_qmv_affine4_packed_rows`` (layout 1) or
+``mtp_gather_qmv_affine4_packed_mf16`` (layout 2) instead.
 """
 
 from __future__ import annotations
